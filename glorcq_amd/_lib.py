@@ -1,0 +1,98 @@
+"""ctypes binding of libglorcq_hip.so (the C ABI declared in include/glorcq_hip.h).
+
+The library is loaded after torch so both share one HIP runtime in the process
+(torch ships libamdhip64.so.7 with the same SONAME the library links against).
+Loading never touches the GPU, so symbol checks run on hosts without one.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (load torch's HIP runtime first)
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libglorcq_hip.so"
+
+_c_int = ctypes.c_int
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+
+# name -> (restype, argtypes); must match include/glorcq_hip.h exactly.
+SIGNATURES = {
+    "glq_version": (_c_int, []),
+    "glq_last_error": (ctypes.c_char_p, []),
+    "glq_gemv_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "glq_gemv_lora": (_c_int, [
+        _vp, _i64, _i64, _i64,          # x, M, K, N
+        _vp, _c_int, _vp, _vp,          # codes, bits, scales, zeros
+        _i64, _c_int,                   # group, sym
+        _vp, _vp, _i64, _vp,            # U, SV, rank, xU
+        _vp, _vp,                       # bias, y
+        _vp, _i64, _vp,                 # workspace, bytes, stream
+    ]),
+    "glq_gemv_lora_batched": (_c_int, [
+        _i64, _vp, _i64,                # items, x, x_stride
+        _i64, _i64, _i64,               # M, K, N
+        _vp, _i64, _c_int,              # codes, codes_stride, bits
+        _vp, _vp, _i64,                 # scales, zeros, sz_stride
+        _i64, _c_int,                   # group, sym
+        _vp, _i64, _vp, _i64, _i64,     # U, u_stride, SV, sv_stride, rank
+        _vp, _i64,                      # xU, xu_stride
+        _vp, _i64,                      # bias, bias_stride
+        _vp, _i64,                      # y, y_stride
+        _vp, _i64, _vp,                 # workspace, bytes, stream
+    ]),
+    "glq_workspace_status": (_c_int, [_vp, ctypes.POINTER(ctypes.c_int32), _vp]),
+    "glq_workspace_reset": (_c_int, [_vp, _i64, _vp]),
+    "glq_unpack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _c_int, _vp, _vp]),
+    "glq_dequant_weight": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp, _i64, _c_int, _vp, _vp]),
+    "glq_pack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp]),
+}
+
+_lib = None
+_load_error: str | None = None
+
+
+def load(path: str | os.PathLike | None = None):
+    """Returns the loaded library (cached); raises RuntimeError if missing."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        _load_error = f"{p} not built (run `python -m glorcq_amd.build`)"
+        raise RuntimeError(_load_error)
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def available() -> bool:
+    try:
+        load()
+        return True
+    except (RuntimeError, OSError):
+        return False
+
+
+def check(rc: int, what: str) -> None:
+    """Raises RuntimeError with the library's message for a nonzero return."""
+    if rc != 0:
+        msg = _lib.glq_last_error().decode(errors="replace") if _lib else "?"
+        raise RuntimeError(f"{what}: {msg} (code {rc})")
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None for None)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device=None) -> int:
+    """hipStream_t of torch's current stream on `device`."""
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,208 @@
+// Packed-code codec kernels: pack, unpack and exact fp16 dequantization, plus
+// the library's error state and workspace utilities.
+//
+// Bit layout (the reference's LSB-first convention, inference/kernels/
+// __init__.py:113-118 and inference/quantized_linear.py:115-146, widened from
+// uint8 to int32 words): code k of row n is bits [b*(k%cpw), b*(k%cpw)+b) of
+// word n*(K/cpw) + k/cpw, cpw = 32/b codes per word.
+
+#include <hip/hip_fp16.h>
+#include <string.h>
+
+#include "glq_internal.h"
+
+namespace glq {
+
+static thread_local char g_err[512] = {0};
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_err[0] = 0; }
+
+// One thread per packed word: emits cpw codes.
+template <int BITS>
+__global__ void unpack_kernel(const uint32_t* __restrict__ codes, int64_t words,
+                              int sym, int32_t* __restrict__ out) {
+  constexpr int CPW = 32 / BITS;
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (w >= words) return;
+  uint32_t v = codes[w];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    int32_t q = (int32_t)((v >> (BITS * c)) & MASK);
+    if (sym && q >= (1 << (BITS - 1))) q -= (1 << BITS);
+    out[w * CPW + c] = q;
+  }
+}
+
+// One thread per packed word: emits cpw fp16 weights, each rounded exactly as
+// the reference's fp16 dequant loop does: fp16(fp16(q - z) * s) (sym: q * s).
+template <int BITS>
+__global__ void dequant_kernel(const uint32_t* __restrict__ codes, int64_t N,
+                               int64_t K, const __half* __restrict__ scales,
+                               const __half* __restrict__ zeros, int64_t group,
+                               int sym, __half* __restrict__ W) {
+  constexpr int CPW = 32 / BITS;
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  const int64_t kw = K / CPW;
+  int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (w >= N * kw) return;
+  const int64_t n = w / kw;
+  const int64_t k0 = (w % kw) * CPW;
+  const int64_t G = K / group;
+  uint32_t v = codes[w];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int64_t k = k0 + c;
+    const int64_t g = k / group;
+    int32_t q = (int32_t)((v >> (BITS * c)) & MASK);
+    __half s = scales[n * G + g];
+    __half wq;
+    if (sym) {
+      if (q >= (1 << (BITS - 1))) q -= (1 << BITS);
+      wq = __hmul(__int2half_rn(q), s);
+    } else {
+      wq = __hmul(__hsub(__int2half_rn(q), zeros[n * G + g]), s);
+    }
+    W[n * K + k] = wq;
+  }
+}
+
+// One thread per output word.
+template <int BITS>
+__global__ void pack_kernel(const int32_t* __restrict__ q, int64_t words,
+                            uint32_t* __restrict__ codes) {
+  constexpr int CPW = 32 / BITS;
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (w >= words) return;
+  uint32_t v = 0;
+#pragma unroll
+  for (int c = 0; c < CPW; ++c)
+    v |= ((uint32_t)q[w * CPW + c] & MASK) << (BITS * c);
+  codes[w] = v;
+}
+
+__global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+}  // namespace glq
+
+using namespace glq;
+
+static int check_codec_shape(int64_t N, int64_t K, int bits) {
+  GLQ_CHECK(bits == 2 || bits == 4, "bits must be 2 or 4 (got %d)", bits);
+  GLQ_CHECK(N >= 0 && K >= 0, "negative shape N=%lld K=%lld", (long long)N,
+            (long long)K);
+  GLQ_CHECK(K % (32 / bits) == 0,
+            "K=%lld must be a multiple of %d for %d-bit codes", (long long)K,
+            32 / bits, bits);
+  return GLQ_OK;
+}
+
+extern "C" {
+
+int glq_version(void) { return 100; }
+
+const char* glq_last_error(void) { return g_err; }
+
+int glq_unpack_codes(const int32_t* codes, int64_t N, int64_t K, int bits,
+                     int sym, int32_t* out, void* stream) {
+  clear_error();
+  int rc = check_codec_shape(N, K, bits);
+  if (rc) return rc;
+  const int64_t words = N * K / (32 / bits);
+  if (words == 0) return GLQ_OK;
+  GLQ_CHECK(codes && out, "null pointer");
+  const int bs = 256;
+  const dim3 grid((unsigned)((words + bs - 1) / bs));
+  hipStream_t s = (hipStream_t)stream;
+  if (bits == 2)
+    unpack_kernel<2><<<grid, bs, 0, s>>>((const uint32_t*)codes, words, sym, out);
+  else
+    unpack_kernel<4><<<grid, bs, 0, s>>>((const uint32_t*)codes, words, sym, out);
+  GLQ_LAUNCH_CHECK("unpack_kernel");
+  return GLQ_OK;
+}
+
+int glq_dequant_weight(const int32_t* codes, int64_t N, int64_t K, int bits,
+                       const void* scales, const void* zeros, int64_t group,
+                       int sym, void* W, void* stream) {
+  clear_error();
+  int rc = check_codec_shape(N, K, bits);
+  if (rc) return rc;
+  GLQ_CHECK(group > 0 && K % group == 0,
+            "K=%lld must be a multiple of group=%lld", (long long)K,
+            (long long)group);
+  const int64_t words = N * K / (32 / bits);
+  if (words == 0) return GLQ_OK;
+  GLQ_CHECK(codes && scales && W && (sym || zeros), "null pointer");
+  const int bs = 256;
+  const dim3 grid((unsigned)((words + bs - 1) / bs));
+  hipStream_t s = (hipStream_t)stream;
+  if (bits == 2)
+    dequant_kernel<2><<<grid, bs, 0, s>>>((const uint32_t*)codes, N, K,
+                                          (const __half*)scales,
+                                          (const __half*)zeros, group, sym,
+                                          (__half*)W);
+  else
+    dequant_kernel<4><<<grid, bs, 0, s>>>((const uint32_t*)codes, N, K,
+                                          (const __half*)scales,
+                                          (const __half*)zeros, group, sym,
+                                          (__half*)W);
+  GLQ_LAUNCH_CHECK("dequant_kernel");
+  return GLQ_OK;
+}
+
+int glq_pack_codes(const int32_t* q, int64_t N, int64_t K, int bits,
+                   int32_t* codes, void* stream) {
+  clear_error();
+  int rc = check_codec_shape(N, K, bits);
+  if (rc) return rc;
+  const int64_t words = N * K / (32 / bits);
+  if (words == 0) return GLQ_OK;
+  GLQ_CHECK(q && codes, "null pointer");
+  const int bs = 256;
+  const dim3 grid((unsigned)((words + bs - 1) / bs));
+  hipStream_t s = (hipStream_t)stream;
+  if (bits == 2)
+    pack_kernel<2><<<grid, bs, 0, s>>>(q, words, (uint32_t*)codes);
+  else
+    pack_kernel<4><<<grid, bs, 0, s>>>(q, words, (uint32_t*)codes);
+  GLQ_LAUNCH_CHECK("pack_kernel");
+  return GLQ_OK;
+}
+
+int glq_workspace_status(const void* workspace, int32_t* status,
+                         void* stream) {
+  clear_error();
+  GLQ_CHECK(workspace && status, "null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  GLQ_HIP(hipMemcpyAsync(status, (const uint32_t*)workspace + kCtrError,
+                         sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  GLQ_HIP(hipStreamSynchronize(s));
+  return GLQ_OK;
+}
+
+int glq_workspace_reset(void* workspace, int64_t workspace_bytes,
+                        void* stream) {
+  clear_error();
+  GLQ_CHECK(workspace, "null workspace");
+  GLQ_CHECK(workspace_bytes >= 4 * kCtrDone, "workspace too small");
+  const int64_t n = workspace_bytes / 4;
+  const int bs = 256;
+  fill_u32_kernel<<<dim3((unsigned)((n + bs - 1) / bs)), bs, 0,
+                    (hipStream_t)stream>>>((uint32_t*)workspace, n);
+  GLQ_LAUNCH_CHECK("fill_u32_kernel");
+  return GLQ_OK;
+}
+
+}  // extern "C"

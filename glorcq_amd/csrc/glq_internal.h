@@ -1,0 +1,58 @@
+// Internal helpers shared by the HIP translation units of libglorcq_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/glorcq_hip.h"
+
+namespace glq {
+
+// Per-thread message of the last failed entry point.
+void set_error(const char* fmt, ...);
+void clear_error();
+
+}  // namespace glq
+
+// Argument check: records the message and returns GLQ_ERR_INVALID from the
+// enclosing C entry point (the analogue of TORCH_CHECK in the reference host
+// code, inference/kernels/gptq_matmul.cu:232-267).
+#define GLQ_CHECK(cond, ...)            \
+  do {                                  \
+    if (!(cond)) {                      \
+      glq::set_error(__VA_ARGS__);      \
+      return GLQ_ERR_INVALID;           \
+    }                                   \
+  } while (0)
+
+// HIP call check.
+#define GLQ_HIP(call)                                                       \
+  do {                                                                      \
+    hipError_t e_ = (call);                                                 \
+    if (e_ != hipSuccess) {                                                 \
+      glq::set_error("%s failed: %s", #call, hipGetErrorString(e_));        \
+      return GLQ_ERR_HIP;                                                   \
+    }                                                                       \
+  } while (0)
+
+// Launch check after every kernel launch (the reference has none).
+#define GLQ_LAUNCH_CHECK(name)                                              \
+  do {                                                                      \
+    hipError_t e_ = hipGetLastError();                                      \
+    if (e_ != hipSuccess) {                                                 \
+      glq::set_error("launch of %s failed: %s", name, hipGetErrorString(e_)); \
+      return GLQ_ERR_HIP;                                                   \
+    }                                                                       \
+  } while (0)
+
+// Workspace header layout (32-bit words).  The counters are zero between
+// launches: every launch that uses them resets them before it ends.
+namespace glq {
+constexpr int kCtrTicket = 0;   // next job ticket
+constexpr int kCtrExit = 1;     // workgroups that finished
+constexpr int kCtrError = 2;    // sticky error word (nonzero = wait timed out)
+constexpr int kCtrDone = 64;    // per-item count of finished low-rank producers
+inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+}  // namespace glq

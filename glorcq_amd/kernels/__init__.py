@@ -1,0 +1,290 @@
+"""Operator boundary: Python entry points over the gfx950 HIP library.
+
+Mirrors the reference's `inference.kernels` module (inference/kernels/
+__init__.py) so host code keeps its call sites:
+
+  is_gptq_cuda_available()            __init__.py:55
+  is_cuda_available()                 __init__.py:39   (TurboQuant codec: not built)
+  gptq_dequant_matmul_fused(...)      __init__.py:284-346
+  _unpack_indices_2bit(...)           __init__.py:113-118
+
+plus the packed-format entry points this build adds:
+
+  packed_dequant_matmul_fused(...)    fused dequant-GEMV/GEMM + low-rank + bias
+  packed_dequant_matmul_batched(...)  many independent problems, one launch
+  unpack_codes / dequant_weight / pack_codes_device   bit-exact codec checks
+
+Error contract: argument problems raise RuntimeError (the reference's
+TORCH_CHECK -> RuntimeError).  Unlike the reference there is no silent
+fallback: if the HIP library is missing or a launch fails the call raises, so
+a result always comes from the HIP kernels.
+"""
+
+from __future__ import annotations
+
+import logging
+
+import torch
+
+from .. import _lib
+from ..format import pack_codes
+
+logger = logging.getLogger(__name__)
+
+# workspace cache: (device index, stream handle) -> uint8 tensor (zeroed once;
+# every launch leaves its counters zeroed)
+_workspaces: dict = {}
+
+GEMV_MAX_M = 16
+
+
+def is_gptq_cuda_available() -> bool:
+    """True when the HIP library is built and a GPU is visible."""
+    return _lib.available() and torch.cuda.is_available()
+
+
+def is_cuda_available() -> bool:
+    """TurboQuant (codebook) kernels are not part of this build."""
+    return False
+
+
+def _require(t: torch.Tensor, name: str, dtype=None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise RuntimeError(f"{name} must be a tensor")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor (glorcq_amd runs on the GPU only)")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {dtype} (got {t.dtype})")
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Zeroed workspace for the current stream of `device`, grown on demand.
+
+    Launches on one stream run in order, and each leaves the counters zero, so
+    the buffer is reused; different streams get different buffers.
+    """
+    lib = _lib.load()
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (idx, _lib.stream_handle(dev))
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, 1 << 16)
+        if ws is not None:
+            size = max(size, 2 * ws.numel())
+        ws = torch.zeros(size, dtype=torch.uint8, device=dev)
+        _workspaces[key] = ws
+    del lib
+    return ws
+
+
+def workspace_status(ws: torch.Tensor) -> int:
+    """Sticky error word of a workspace (0 = every low-rank wait completed)."""
+    import ctypes
+
+    lib = _lib.load()
+    out = ctypes.c_int32(0)
+    _lib.check(lib.glq_workspace_status(ws.data_ptr(), ctypes.byref(out),
+                                        _lib.stream_handle(ws.device)), "glq_workspace_status")
+    return int(out.value)
+
+
+def packed_dequant_matmul_fused(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
+                                zeros: torch.Tensor | None, bits: int, groupsize: int,
+                                sym: bool = False, U: torch.Tensor | None = None,
+                                SV: torch.Tensor | None = None,
+                                precomputed_xU: torch.Tensor | None = None,
+                                bias: torch.Tensor | None = None,
+                                out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = dequant(codes) x + (x U) SV^T + bias, fp16 (M, N), one HIP launch.
+
+    x (M, K) fp16; codes (N, K*bits/32) int32; scales/zeros (N, K/groupsize)
+    fp16; U (K, r) fp16; SV (N, r) fp16; precomputed_xU (M, r) fp16 replaces
+    x U (the cluster-shared hook of GLoRCQLinear.forward,
+    inference/quantized_linear.py:286-345); bias (N,) fp16.
+    """
+    lib = _lib.load()
+    _require(x, "x", torch.float16)
+    _require(codes, "codes", torch.int32)
+    _require(scales, "scales", torch.float16)
+    if not sym:
+        if zeros is None:
+            raise RuntimeError("zeros required for asymmetric codes")
+        _require(zeros, "zeros", torch.float16)
+    if x.dim() != 2:
+        raise RuntimeError("x must be 2-D (M, K)")
+    M, K = x.shape
+    N = codes.shape[0]
+    if codes.shape[1] * (32 // bits) != K:
+        raise RuntimeError(f"codes shape {tuple(codes.shape)} does not match K={K} at {bits} bits")
+    if scales.shape != (N, K // groupsize):
+        raise RuntimeError(f"scales shape {tuple(scales.shape)} != ({N}, {K // groupsize})")
+    rank = 0
+    if SV is not None:
+        _require(SV, "SV", torch.float16)
+        rank = SV.shape[1]
+        if SV.shape[0] != N:
+            raise RuntimeError("SV must be (N, r)")
+        if precomputed_xU is not None:
+            _require(precomputed_xU, "precomputed_xU", torch.float16)
+            if precomputed_xU.shape != (M, rank):
+                raise RuntimeError("precomputed_xU must be (M, r)")
+        elif U is None:
+            raise RuntimeError("LoRA needs U or precomputed_xU")
+        else:
+            _require(U, "U", torch.float16)
+            if U.shape != (K, rank):
+                raise RuntimeError("U must be (K, r)")
+    if bias is not None:
+        _require(bias, "bias", torch.float16)
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.float16, device=x.device)
+    else:
+        _require(out, "out", torch.float16)
+        if out.shape != (M, N):
+            raise RuntimeError("out must be (M, N)")
+    if M == 0 or N == 0:
+        return out
+    stream = _lib.stream_handle(x.device)
+    for m0 in range(0, M, GEMV_MAX_M):
+        m1 = min(M, m0 + GEMV_MAX_M)
+        mb = m1 - m0
+        nbytes = lib.glq_gemv_workspace_bytes(1, mb, K, N, rank if precomputed_xU is None else 0)
+        ws = workspace(x.device, nbytes)
+        xu = None if precomputed_xU is None else precomputed_xU[m0:m1]
+        rc = lib.glq_gemv_lora(
+            x[m0:m1].data_ptr(), mb, K, N, codes.data_ptr(), bits, scales.data_ptr(),
+            _lib.ptr(zeros), groupsize, int(bool(sym)),
+            _lib.ptr(U if precomputed_xU is None else None), _lib.ptr(SV), rank,
+            _lib.ptr(xu), _lib.ptr(bias), out[m0:m1].data_ptr(),
+            ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, "glq_gemv_lora")
+    return out
+
+
+def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
+                                  zeros: torch.Tensor | None, bits: int, groupsize: int,
+                                  sym: bool = False, U: torch.Tensor | None = None,
+                                  SV: torch.Tensor | None = None,
+                                  bias: torch.Tensor | None = None,
+                                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """E independent problems in one launch: x (E, M, K), codes (E, N, Kw),
+    scales/zeros (E, N, G), U (E, K, r), SV (E, N, r), bias (E, N) -> (E, M, N).
+
+    The packed-format counterpart of turbo_dequant_grouped_gemv_fused
+    (inference/kernels/__init__.py:242-278), with the low-rank term fused.
+    """
+    lib = _lib.load()
+    _require(x, "x", torch.float16)
+    _require(codes, "codes", torch.int32)
+    _require(scales, "scales", torch.float16)
+    if not sym:
+        _require(zeros, "zeros", torch.float16)
+    E, M, K = x.shape
+    N = codes.shape[1]
+    if codes.shape[0] != E or codes.shape[2] * (32 // bits) != K:
+        raise RuntimeError("codes must be (E, N, K*bits/32)")
+    if M > GEMV_MAX_M:
+        raise RuntimeError(f"batched GEMV takes M <= {GEMV_MAX_M}")
+    rank = 0
+    if SV is not None:
+        _require(SV, "SV", torch.float16)
+        _require(U, "U", torch.float16)
+        rank = SV.shape[2]
+    if bias is not None:
+        _require(bias, "bias", torch.float16)
+    if out is None:
+        out = torch.empty(E, M, N, dtype=torch.float16, device=x.device)
+    if E == 0 or M == 0 or N == 0:
+        return out
+    nbytes = lib.glq_gemv_workspace_bytes(E, M, K, N, rank)
+    ws = workspace(x.device, nbytes)
+    rc = lib.glq_gemv_lora_batched(
+        E, x.data_ptr(), M * K, M, K, N, codes.data_ptr(), codes.shape[1] * codes.shape[2],
+        bits, scales.data_ptr(), _lib.ptr(zeros), scales.shape[1] * scales.shape[2],
+        groupsize, int(bool(sym)), _lib.ptr(U), K * rank, _lib.ptr(SV), N * rank, rank,
+        None, 0, _lib.ptr(bias), N, out.data_ptr(), M * N, ws.data_ptr(), ws.numel(),
+        _lib.stream_handle(x.device))
+    _lib.check(rc, "glq_gemv_lora_batched")
+    return out
+
+
+def gptq_dequant_matmul_fused(x, qweight_int, scales, zeros, groupsize, sym=False,
+                              lora_USV=None, bits: int | None = None):
+    """Reference signature (inference/kernels/__init__.py:284): unpacked (N, K)
+    integer codes, fp16 scales/zeros, optional (U, S, V) low-rank tuple ->
+    fp16 (B, N).
+
+    The reference casts the (N, K) int32 codes to int8 on every call; here they
+    are packed on the device instead (4-bit container unless `bits` is given,
+    which holds any code width <= 4).  Keep weights packed (GLoRCQLinear) to
+    avoid the per-call pack.
+    """
+    b = 4 if bits is None else bits
+    if b not in (2, 4):
+        b = 4 if b < 4 else b
+    if b > 4:
+        raise RuntimeError(f"{bits}-bit codes are not supported (2 or 4)")
+    codes = pack_codes_device(qweight_int.to(torch.int32).contiguous(), b)
+    xh = x.to(torch.float16).contiguous()
+    U = SV = None
+    if lora_USV is not None:
+        U_, S_, V_ = lora_USV
+        U = U_.to(torch.float16).contiguous()
+        SV = (V_.float() * S_.float().unsqueeze(0)).to(torch.float16).contiguous()
+    return packed_dequant_matmul_fused(xh, codes, scales.contiguous(),
+                                       None if zeros is None else zeros.contiguous(),
+                                       b, groupsize, sym, U=U, SV=SV)
+
+
+def pack_codes_device(q: torch.Tensor, bits: int) -> torch.Tensor:
+    """(N, K) int32 codes on the GPU -> packed (N, K*bits/32) int32 (HIP kernel)."""
+    lib = _lib.load()
+    _require(q, "q", torch.int32)
+    N, K = q.shape
+    out = torch.empty(N, K * bits // 32, dtype=torch.int32, device=q.device)
+    _lib.check(lib.glq_pack_codes(q.data_ptr(), N, K, bits, out.data_ptr(),
+                                  _lib.stream_handle(q.device)), "glq_pack_codes")
+    return out
+
+
+def unpack_codes(codes: torch.Tensor, bits: int, K: int, sym: bool = False) -> torch.Tensor:
+    """Packed (N, K*bits/32) int32 -> (N, K) int32 codes (HIP kernel)."""
+    lib = _lib.load()
+    _require(codes, "codes", torch.int32)
+    N = codes.shape[0]
+    out = torch.empty(N, K, dtype=torch.int32, device=codes.device)
+    _lib.check(lib.glq_unpack_codes(codes.data_ptr(), N, K, bits, int(bool(sym)), out.data_ptr(),
+                                    _lib.stream_handle(codes.device)), "glq_unpack_codes")
+    return out
+
+
+def dequant_weight(codes: torch.Tensor, bits: int, K: int, scales: torch.Tensor,
+                   zeros: torch.Tensor | None, groupsize: int, sym: bool = False) -> torch.Tensor:
+    """fp16 W (N, K) = fp16(fp16(q - z) * s) (HIP kernel; bit-exact with the
+    reference's fp16 dequant loop, inference/quantized_linear.py:271-284)."""
+    lib = _lib.load()
+    _require(codes, "codes", torch.int32)
+    _require(scales, "scales", torch.float16)
+    N = codes.shape[0]
+    out = torch.empty(N, K, dtype=torch.float16, device=codes.device)
+    _lib.check(lib.glq_dequant_weight(codes.data_ptr(), N, K, bits, scales.data_ptr(),
+                                      _lib.ptr(zeros), groupsize, int(bool(sym)), out.data_ptr(),
+                                      _lib.stream_handle(codes.device)), "glq_dequant_weight")
+    return out
+
+
+def _unpack_indices_2bit(packed: torch.Tensor, K: int) -> torch.Tensor:
+    """Reference helper (inference/kernels/__init__.py:113-118): (N, K/4) uint8 ->
+    (N, K) long, LSB-first.  Host-side format utility (not a compute path)."""
+    shifts = torch.tensor([0, 2, 4, 6], device=packed.device, dtype=torch.uint8)
+    return ((packed.unsqueeze(-1) >> shifts) & 0x3).reshape(packed.shape[0], -1)[:, :K].long()
+
+
+__all__ = [
+    "is_gptq_cuda_available", "is_cuda_available", "packed_dequant_matmul_fused",
+    "packed_dequant_matmul_batched", "gptq_dequant_matmul_fused", "unpack_codes",
+    "dequant_weight", "pack_codes_device", "pack_codes", "workspace", "workspace_status",
+]

@@ -1,0 +1,146 @@
+/*
+ * glorcq_hip.h — C ABI of the MI355X (gfx950) GLoRCQ hot-path library.
+ *
+ * The library computes the fused "dequantize + GEMV/GEMM + low-rank
+ * correction" that a GLoRCQ quantized linear layer runs for every projection:
+ *
+ *     y[m, n] = sum_k W[n, k] * x[m, k]  +  sum_j a[m, j] * SV[n, j]  + bias[n]
+ *     W[n, k] = s[n, k/g] * (q[n, k] - z[n, k/g])       (asymmetric)
+ *     W[n, k] = s[n, k/g] * q_signed[n, k]              (symmetric)
+ *     a[m, j] = sum_k x[m, k] * U[k, j]                 (or a caller-supplied a)
+ *
+ * Data format (device memory, all row-major, little-endian):
+ *   codes   int32 (N, K*bits/32): b-bit codes packed LSB-first along K; code k
+ *           of row n sits in word k/(32/b) at bit offset b*(k % (32/b)).
+ *           Symmetric codes are stored as b-bit two's complement.
+ *   scales  fp16 (N, K/g)     zeros fp16 (N, K/g) (ignored when sym != 0)
+ *   U       fp16 (K, r)       input-side low-rank factor (shared per cluster)
+ *   SV      fp16 (N, r)       output-side low-rank factor with S fused in
+ *   x       fp16 (M, K)       y fp16 (M, N)      bias fp16 (N) or NULL
+ *
+ * Reference interface replaced (nicyyyy/GLoRCQ):
+ *   inference/kernels/__init__.py:284-346  gptq_dequant_matmul_fused
+ *   inference/kernels/gptq_matmul.cu:223-315 gptq_dequant_matmul_cuda (host)
+ *   inference/quantized_linear.py:286-355   GLoRCQLinear.forward (+ LoRA add)
+ *
+ * Conventions: every pointer argument is a device pointer unless stated; every
+ * entry point launches on the given HIP stream (`stream`, a hipStream_t passed
+ * as void*; NULL = default stream), never synchronizes, never allocates device
+ * memory, and returns 0 on success or a nonzero GLQ_ERR_* code.  The message
+ * of the last failure on the calling thread is available from
+ * glq_last_error().  Empty work (M == 0 or N == 0) is a successful no-op.
+ */
+#ifndef GLORCQ_HIP_H
+#define GLORCQ_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GLQ_OK 0
+#define GLQ_ERR_INVALID 1   /* argument check failed (the TORCH_CHECK analogue) */
+#define GLQ_ERR_HIP 2       /* a HIP runtime call or kernel launch failed       */
+#define GLQ_ERR_WORKSPACE 3 /* workspace too small or in a bad state            */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int glq_version(void);
+
+/* Message of the last error raised on the calling thread ("" if none). */
+const char* glq_last_error(void);
+
+/*
+ * Bytes of workspace glq_gemv_lora / glq_gemv_lora_batched need for `items`
+ * independent problems of shape (M, K, N, rank).  The workspace must be zeroed
+ * once before first use (hipMemset); every launch leaves its counters zeroed on
+ * exit, so one workspace can be reused by consecutive launches on ONE stream.
+ * Launches that overlap in time (different streams) need different workspaces.
+ */
+int64_t glq_gemv_workspace_bytes(int64_t items, int64_t M, int64_t K,
+                                 int64_t N, int64_t rank);
+
+/*
+ * Fused dequant-GEMV + low-rank correction, 1 <= M <= 16 (decode).
+ * Replaces gptq_dequant_matmul_fused (inference/kernels/__init__.py:284) and
+ * the LoRA tail of GLoRCQLinear.forward (inference/quantized_linear.py:338-349).
+ *   bits      2 or 4;  group % 128 == 0;  K % group == 0
+ *   U, SV     may be NULL (no correction) ; rank % 8 == 0, rank <= 512
+ *   xU        optional precomputed a = x*U (M, rank) fp16 (cluster-shared
+ *             x*U, the `precomputed_xU` hook of quantized_linear.py:286); when
+ *             given, U is not read.
+ *   bias      optional (N) fp16
+ *   workspace device buffer of glq_gemv_workspace_bytes(1, M, K, N, rank)
+ */
+int glq_gemv_lora(const void* x, int64_t M, int64_t K, int64_t N,
+                  const int32_t* codes, int bits, const void* scales,
+                  const void* zeros, int64_t group, int sym, const void* U,
+                  const void* SV, int64_t rank, const void* xU,
+                  const void* bias, void* y, void* workspace,
+                  int64_t workspace_bytes, void* stream);
+
+/*
+ * Batched form: `items` independent problems of one shape in ONE launch, item
+ * i reading codes + i*codes_stride (int32 elements), scales/zeros + i*sz_stride,
+ * U + i*u_stride, SV + i*sv_stride, bias + i*bias_stride, x + i*x_stride,
+ * xU + i*xu_stride and writing y + i*y_stride (fp16 elements).  This is the
+ * grouped expert GEMV of the reference's graph-mode MoE step
+ * (turbo_dequant_grouped_gemv, inference/kernels/__init__.py:242-278), in the
+ * packed group-quantized format.
+ */
+int glq_gemv_lora_batched(int64_t items, const void* x, int64_t x_stride,
+                          int64_t M, int64_t K, int64_t N,
+                          const int32_t* codes, int64_t codes_stride, int bits,
+                          const void* scales, const void* zeros,
+                          int64_t sz_stride, int64_t group, int sym,
+                          const void* U, int64_t u_stride, const void* SV,
+                          int64_t sv_stride, int64_t rank, const void* xU,
+                          int64_t xu_stride, const void* bias,
+                          int64_t bias_stride, void* y, int64_t y_stride,
+                          void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
+/*
+ * Reads the sticky error word of a workspace into *status (host pointer) with
+ * a synchronous copy on `stream` (0 = no kernel-side error seen; nonzero =
+ * a consumer gave up waiting for its low-rank producers).  Debug/test use.
+ */
+int glq_workspace_status(const void* workspace, int32_t* status, void* stream);
+
+/* Zeroes a workspace (counters and error word) with a fill kernel. */
+int glq_workspace_reset(void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Debug: unpack codes (N, K*bits/32) int32 -> (N, K) int32.  Codes are
+ * returned unsigned (0..2^b-1), or sign-extended when sym != 0.
+ * Replaces _unpack_indices (inference/quantized_linear.py:115-146) and
+ * _unpack_indices_2bit (inference/kernels/__init__.py:113-118) for the packed
+ * int32 container.
+ */
+int glq_unpack_codes(const int32_t* codes, int64_t N, int64_t K, int bits,
+                     int sym, int32_t* out, void* stream);
+
+/*
+ * Debug: dequantize to fp16 W (N, K), bit-exactly fp16(fp16(q - z) * s)
+ * (sym: fp16(q * s)), i.e. GLoRCQLinear._dequant_gptq
+ * (inference/quantized_linear.py:271-284).
+ */
+int glq_dequant_weight(const int32_t* codes, int64_t N, int64_t K, int bits,
+                       const void* scales, const void* zeros, int64_t group,
+                       int sym, void* W, void* stream);
+
+/*
+ * Packs (N, K) int32 codes into the int32 container on the device (load-time
+ * helper; values are masked to b bits, so two's-complement symmetric codes
+ * pack directly).  Replaces the per-call int32->int8 cast of the reference
+ * (inference/kernels/__init__.py:305-309) with a one-time pack.
+ */
+int glq_pack_codes(const int32_t* q, int64_t N, int64_t K, int bits,
+                   int32_t* codes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GLORCQ_HIP_H */

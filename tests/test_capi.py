@@ -1,0 +1,100 @@
+"""The C ABI library loads and exports every symbol include/glorcq_hip.h declares
+(no compute calls: runs without a GPU), and the host-side checks of the
+boundary behave like the reference's TORCH_CHECK contract."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from glorcq_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "glorcq_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(glq_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for need in ["glq_gemv_lora", "glq_gemv_lora_batched", "glq_unpack_codes",
+                 "glq_dequant_weight", "glq_pack_codes", "glq_last_error"]:
+        assert need in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_symbols():
+        assert hasattr(lib, name), f"{name} declared but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_exported_symbols_are_c_linkage():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (glq_\w+)$", out, flags=re.M))
+    assert set(declared_symbols()) <= exported
+
+
+def test_version_and_workspace_sizes(lib):
+    assert lib.glq_version() >= 100
+    a = lib.glq_gemv_workspace_bytes(1, 1, 2048, 1408, 64)
+    b = lib.glq_gemv_workspace_bytes(4, 1, 2048, 1408, 64)
+    assert 0 < a < b
+    assert lib.glq_gemv_workspace_bytes(1, 1, 2048, 1408, 0) < a
+    assert lib.glq_gemv_workspace_bytes(-1, 1, 1, 1, 1) == -1
+
+
+def test_argument_checks_raise_before_any_launch(lib):
+    """Invalid arguments are rejected on the host (no device pointer is
+    touched), mirroring gptq_matmul.cu:232-267; empty work is a no-op
+    (gptq_matmul.cu:271-276)."""
+    nul = None
+    # bits
+    rc = lib.glq_gemv_lora(1 << 12, 1, 2048, 1408, 1 << 12, 3, 1 << 12, 1 << 12, 128, 0,
+                           nul, nul, 0, nul, nul, 1 << 12, 1 << 12, 1 << 20, nul)
+    assert rc == 1 and b"bits" in lib.glq_last_error()
+    # M > 16
+    rc = lib.glq_gemv_lora(1 << 12, 17, 2048, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 128, 0,
+                           nul, nul, 0, nul, nul, 1 << 12, 1 << 12, 1 << 20, nul)
+    assert rc == 1 and b"M" in lib.glq_last_error()
+    # group not multiple of 128
+    rc = lib.glq_gemv_lora(1 << 12, 1, 2048, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 64, 0,
+                           nul, nul, 0, nul, nul, 1 << 12, 1 << 12, 1 << 20, nul)
+    assert rc == 1 and b"group" in lib.glq_last_error()
+    # workspace too small
+    rc = lib.glq_gemv_lora(1 << 12, 1, 2048, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 128, 0,
+                           1 << 12, 1 << 12, 64, nul, nul, 1 << 12, 1 << 12, 16, nul)
+    assert rc == 1 and b"workspace" in lib.glq_last_error()
+    # misaligned x
+    rc = lib.glq_gemv_lora((1 << 12) + 2, 1, 2048, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 128, 0,
+                           nul, nul, 0, nul, nul, 1 << 12, 1 << 12, 1 << 20, nul)
+    assert rc == 1 and b"aligned" in lib.glq_last_error()
+    # empty work: success, nothing launched
+    assert lib.glq_gemv_lora(nul, 0, 2048, 1408, nul, 2, nul, nul, 128, 0, nul, nul, 0, nul,
+                             nul, nul, nul, 0, nul) == 0
+    assert lib.glq_unpack_codes(nul, 0, 64, 2, 0, nul, nul) == 0
+    assert lib.glq_unpack_codes(nul, 4, 63, 2, 0, nul, nul) == 1
+
+
+def test_python_boundary_rejects_cpu_tensors():
+    import torch
+
+    from glorcq_amd import kernels
+
+    x = torch.zeros(1, 128, dtype=torch.float16)
+    codes = torch.zeros(16, 8, dtype=torch.int32)
+    s = torch.zeros(16, 1, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        kernels.packed_dequant_matmul_fused(x, codes, s, s, 2, 128)
+    assert kernels.is_cuda_available() is False

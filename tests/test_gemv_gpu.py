@@ -1,0 +1,245 @@
+"""GPU parity of the fused dequant-GEMV + low-rank kernels against the CPU oracle.
+
+Bars (north star): unpacked codes and dequantized fp16 weights bit-exact;
+outputs |y - y_oracle| <= 1e-3 + 1e-2 |y_oracle| against the reference's fp16
+CPU fallback restated in oracle/glorcq_oracle.py.  Every call goes through the
+C ABI (libglorcq_hip.so) via glorcq_amd.kernels.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from glorcq_amd import format as fmt
+from glorcq_amd import kernels as K_
+from oracle import glorcq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-2, 1e-3
+
+
+def to(p, dev):
+    return {k: getattr(p, k).to(dev) for k in ("codes", "scales", "zeros", "U", "SV", "x")}
+
+
+def oracle_y(p, x=None, lora=True, xu=None, bias=None):
+    x = p.x if x is None else x
+    return O.linear_forward_fp16(x, p.q, p.scales, p.zeros, p.group, p.sym,
+                                 U=p.U if lora else None, SV=p.SV if lora else None,
+                                 precomputed_xU=xu, bias=bias)
+
+
+def assert_parity(y, ref, what):
+    y = y.float().cpu()
+    ref = ref.float().cpu()
+    err = (y - ref).abs()
+    bad = err > ATOL + RTOL * ref.abs()
+    assert not bool(bad.any()), (f"{what}: {int(bad.sum())} of {bad.numel()} outside bar, "
+                                 f"max err {err.max().item():.3e}")
+
+
+# ----------------------------------------------------------- codec (exact) --
+@pytest.mark.parametrize("bits,sym", [(2, False), (4, False), (2, True), (4, True)])
+def test_unpack_bit_exact(gpu, bits, sym):
+    g = torch.Generator().manual_seed(bits * 10 + sym)
+    words = torch.randint(-(2**31), 2**31 - 1, (257, 96), generator=g, dtype=torch.int64)
+    words = words.to(torch.int32)
+    K = 96 * 32 // bits
+    got = K_.unpack_codes(words.to(gpu), bits, K, sym).cpu().numpy()
+    assert np.array_equal(got, O.unpack_codes(words.numpy(), bits, K, sym))
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_pack_device_matches_oracle(gpu, bits):
+    g = torch.Generator().manual_seed(21)
+    q = torch.randint(-(1 << (bits - 1)), 1 << bits, (64, 512), generator=g, dtype=torch.int32)
+    got = K_.pack_codes_device(q.to(gpu), bits).cpu().numpy()
+    assert np.array_equal(got, O.pack_codes(q.numpy(), bits))
+
+
+@pytest.mark.parametrize("bits,sym,intz", [(2, False, True), (4, False, True), (2, True, True),
+                                           (4, True, True), (2, False, False), (4, False, False)])
+def test_dequant_bit_exact(gpu, bits, sym, intz):
+    p = fmt.make_linear(1024, 160, bits=bits, group=128, seed=31 + bits, sym=sym)
+    zeros = p.zeros
+    if not intz:  # the reference kernel tests' non-integer zero-points
+        g = torch.Generator().manual_seed(77)
+        zeros = (torch.randn(p.zeros.shape, generator=g) * 0.5).half()
+    W = K_.dequant_weight(p.codes.to(gpu), bits, 1024, p.scales.to(gpu),
+                          None if sym else zeros.to(gpu), 128, sym).cpu()
+    ref = O.dequant_fp16(p.q, p.scales, zeros, 128, sym)
+    assert np.array_equal(W.numpy().view(np.uint16), ref.numpy().view(np.uint16))
+
+
+# ------------------------------------------------------ fused GEMV + LoRA ---
+def test_config0_exact_inputs(gpu):
+    """K=2048, N=1408, 2-bit, g=128, r=64, M=1, seed 0."""
+    p = fmt.make_linear(2048, 1408, bits=2, group=128, rank=64, M=1, seed=0)
+    d = to(p, gpu)
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], 2, 128,
+                                       U=d["U"], SV=d["SV"])
+    torch.cuda.synchronize()
+    assert y.shape == (1, 1408) and y.dtype == torch.float16
+    assert_parity(y, oracle_y(p), "config0")
+    assert K_.workspace_status(K_.workspace(gpu, 0)) == 0
+
+
+SHAPES = [  # (name, K, N, bits) — Qwen1.5-MoE-A2.7B projections (config 1) + more
+    ("expert gate/up 2b", 2048, 1408, 2),
+    ("expert down 2b", 1408, 2048, 2),
+    ("attn q/k/v/o 4b", 2048, 2048, 4),
+    ("shared gate/up 4b", 2048, 5632, 4),
+    ("shared down 4b", 5632, 2048, 4),
+]
+
+
+@pytest.mark.parametrize("name,K,N,bits", SHAPES)
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+def test_shapes_batch_sweep(gpu, name, K, N, bits, M):
+    p = fmt.make_linear(K, N, bits=bits, group=128, rank=64, M=M, seed=K + N + M)
+    d = to(p, gpu)
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], bits, 128,
+                                       U=d["U"], SV=d["SV"])
+    assert_parity(y, oracle_y(p), f"{name} M={M}")
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_no_lora_and_bias(gpu, bits):
+    p = fmt.make_linear(1024, 320, bits=bits, rank=64, M=3, seed=5)
+    d = to(p, gpu)
+    bias = (torch.randn(320, generator=torch.Generator().manual_seed(1)) * 0.1).half()
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], bits, 128,
+                                       bias=bias.to(gpu))
+    assert_parity(y, oracle_y(p, lora=False, bias=bias), "no-lora+bias")
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], bits, 128,
+                                       U=d["U"], SV=d["SV"], bias=bias.to(gpu))
+    assert_parity(y, oracle_y(p, bias=bias), "lora+bias")
+
+
+def test_precomputed_xu(gpu):
+    """Cluster-shared x*U hook (quantized_linear.py:286-345)."""
+    p = fmt.make_linear(2048, 1408, bits=2, rank=64, M=4, seed=8)
+    d = to(p, gpu)
+    xu = (p.x @ p.U)
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], 2, 128,
+                                       SV=d["SV"], precomputed_xU=xu.to(gpu))
+    assert_parity(y, oracle_y(p, xu=xu), "precomputed xU")
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_sym(gpu, bits):
+    p = fmt.make_linear(2048, 512, bits=bits, rank=64, M=1, seed=12, sym=True)
+    d = to(p, gpu)
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], None, bits, 128,
+                                       sym=True, U=d["U"], SV=d["SV"])
+    assert_parity(y, oracle_y(p), "sym")
+
+
+def test_noninteger_zeros(gpu):
+    p = fmt.make_linear(2048, 256, bits=2, rank=64, M=2, seed=13)
+    p.zeros = (torch.randn(p.zeros.shape, generator=torch.Generator().manual_seed(3)) * 0.5).half()
+    d = to(p, gpu)
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], 2, 128,
+                                       U=d["U"], SV=d["SV"])
+    assert_parity(y, oracle_y(p), "non-integer zeros")
+
+
+@pytest.mark.parametrize("K,N,M,group,rank", [
+    (128, 16, 1, 128, 8),      # smallest legal problem
+    (256, 1000, 5, 256, 40),   # ragged N, group 256, rank not a multiple of 32
+    (14336, 4096, 1, 128, 64),  # Mixtral down_proj K (the reference's smem overflow case)
+    (14336, 512, 2, 128, 64),
+    (4096, 14336, 1, 128, 128),
+    (2048, 64, 16, 128, 512),  # max rank
+])
+def test_edge_shapes(gpu, K, N, M, group, rank):
+    p = fmt.make_linear(K, N, bits=2, group=group, rank=rank, M=M, seed=K + N)
+    d = to(p, gpu)
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], 2, group,
+                                       U=d["U"], SV=d["SV"])
+    assert_parity(y, oracle_y(p), f"K={K} N={N} M={M}")
+
+
+def test_empty_batch(gpu):
+    """B=0 returns shape (0, N) (test_kernels_qwen.py:151-154)."""
+    p = fmt.make_linear(2048, 1408, bits=2, M=1, seed=0)
+    d = to(p, gpu)
+    y = K_.packed_dequant_matmul_fused(d["x"][:0], d["codes"], d["scales"], d["zeros"], 2, 128,
+                                       U=d["U"], SV=d["SV"])
+    assert y.shape == (0, 1408)
+    torch.zeros(1, device=gpu)
+    torch.cuda.synchronize()
+
+
+def test_m_above_16_blocks(gpu):
+    p = fmt.make_linear(1024, 256, bits=4, rank=64, M=40, seed=14)
+    d = to(p, gpu)
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], 4, 128,
+                                       U=d["U"], SV=d["SV"])
+    assert_parity(y, oracle_y(p), "M=40")
+
+
+def test_repeat_calls_reuse_workspace(gpu):
+    """Counters self-reset: consecutive launches on one stream agree exactly."""
+    p = fmt.make_linear(2048, 1408, bits=2, rank=64, M=1, seed=0)
+    d = to(p, gpu)
+    ys = [K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], 2, 128,
+                                         U=d["U"], SV=d["SV"]) for _ in range(5)]
+    torch.cuda.synchronize()
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
+    assert K_.workspace_status(K_.workspace(gpu, 0)) == 0
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_batched_items(gpu, bits):
+    E, M, K, N, r = 6, 2, 2048, 1408, 64
+    ps = [fmt.make_linear(K, N, bits=bits, rank=r, M=M, seed=100 + e) for e in range(E)]
+    st = lambda k: torch.stack([getattr(p, k) for p in ps]).to(gpu)  # noqa: E731
+    y = K_.packed_dequant_matmul_batched(st("x"), st("codes"), st("scales"), st("zeros"), bits,
+                                         128, U=st("U"), SV=st("SV"))
+    for e, p in enumerate(ps):
+        assert_parity(y[e], oracle_y(p), f"item {e}")
+
+
+def test_reference_signature_unpacked_codes(gpu):
+    """gptq_dequant_matmul_fused with the reference's (N, K) int32 codes and an
+    (U, S, V) low-rank tuple."""
+    p = fmt.make_linear(2048, 512, bits=2, rank=64, M=1, seed=15)
+    g = torch.Generator().manual_seed(2)
+    S = torch.rand(64, generator=g).half()
+    V = p.SV  # (N, r)
+    y = K_.gptq_dequant_matmul_fused(p.x.to(gpu), p.q.to(gpu), p.scales.to(gpu),
+                                     p.zeros.to(gpu), 128, False,
+                                     lora_USV=(p.U.to(gpu), S.to(gpu), V.to(gpu)))
+    SV = (V.float() * S.float()[None]).half()
+    ref = O.linear_forward_fp16(p.x, p.q, p.scales, p.zeros, 128, U=p.U, SV=SV)
+    assert_parity(y, ref, "reference signature")
+
+
+def test_graph_capture_replays(gpu):
+    """The fused call captured in a HIP graph: every replay, with eager work
+    between replays, matches the eager result."""
+    p = fmt.make_linear(2048, 1408, bits=2, rank=64, M=1, seed=0)
+    d = to(p, gpu)
+    out = torch.empty(1, 1408, dtype=torch.float16, device=gpu)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], 2, 128,
+                                       U=d["U"], SV=d["SV"], out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], 2, 128,
+                                       U=d["U"], SV=d["SV"], out=out)
+    for i in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        _ = (d["x"].float() * 2).sum().item()  # eager work between replays
