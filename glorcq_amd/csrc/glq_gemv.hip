@@ -68,7 +68,8 @@ struct GemvArgs {
   int tiles;    // consumer jobs per item
   int kw;       // int32 words per weight row
   int rpad;     // rank rounded up to 32
-  int xstride;  // halves per token row of staged x in LDS
+  int kp;       // codes per K-phase staged in LDS (multiple of group)
+  int xstride;  // halves per token row of staged x in LDS (kp + 8)
   int apad;     // halves per token row of staged a in LDS
   unsigned* ctr;
   float* apart;  // (items, P, M, rpad)
@@ -232,90 +233,27 @@ __device__ void gemv_consumer(const GemvArgs& a, int item, int tile,
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, kb = lane >> 4;
   const int M = a.M, K = a.K, N = a.N, G = a.G;
-  const int nch = K >> 7;
+  const int KP = a.kp;        // codes per K-phase (multiple of the group size)
+  const int ncp = KP >> 7;    // 128-code chunks per phase
+  const int cpg = a.group >> 7;  // chunks per quantization group
+  const int gp = KP / a.group;   // groups per phase
   const int r0 = tile * R;
 
-  const LdsLayout L = lds_layout(M, K, G, T, a.xstride, a.apad);
-  __half* xs = (__half*)(smem + L.xs);      // M x xstride, permuted x
-  float* xsum = (float*)(smem + L.xsum);    // M x nch
-  float* xbias = (float*)(smem + L.xbias);  // M x nch
-  float* s_l = (float*)(smem + L.s);        // G x R scales
-  float* z_l = (float*)(smem + L.z);        // G x R zero-points
+  const LdsLayout L = lds_layout(M, KP, gp, T, a.xstride, a.apad);
+  __half* xs = (__half*)(smem + L.xs);      // M x xstride, permuted x of the phase
+  float* xsum = (float*)(smem + L.xsum);    // M x ncp
+  float* xbias = (float*)(smem + L.xbias);  // M x ncp
+  float* s_l = (float*)(smem + L.s);        // gp x R scales
+  float* z_l = (float*)(smem + L.z);        // gp x R zero-points
   f32x4* red = (f32x4*)(smem + L.red);      // 4 x T x 64 partial tiles
   __half* a_l = (__half*)(smem + L.a);      // M x apad low-rank factor a
 
   const __half* X = a.x + (int64_t)item * a.x_es;
-
-  // ---- stage x (permuted to operand order) and its per-chunk sums ----
-  {
-    const int nb = K >> 4;  // 16-code blocks per token row
-    const int total = M * nb;
-    for (int base = 0; base < total; base += 256) {
-      const int idx = base + tid;
-      const bool v = idx < total;
-      float s = 0.f, sb = 0.f;
-      int m = 0, blk = 0;
-      if (v) {
-        m = idx / nb;
-        blk = idx - m * nb;
-        const f16x8* src = (const f16x8*)(X + (int64_t)m * K + blk * 16);
-        f16x8 in0 = src[0], in1 = src[1];
-        _Float16 in[16], o[16];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          in[c] = in0[c];
-          in[8 + c] = in1[c];
-        }
-#pragma unroll
-        for (int pos = 0; pos < 16; ++pos) {
-          o[pos] = in[perm_src<BITS>(pos)];
-          const float f = (float)o[pos];
-          s += f;
-          sb += code_bias<BITS>(pos) * f;
-        }
-        f16x8 o0, o1;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          o0[c] = o[c];
-          o1[c] = o[8 + c];
-        }
-        f16x8* dst = (f16x8*)(xs + (int64_t)m * a.xstride + blk * 16);
-        dst[0] = o0;
-        dst[1] = o1;
-      }
-      // 8 consecutive blocks form one 128-code chunk (nb % 8 == 0).
-      s += __shfl_xor(s, 1);
-      s += __shfl_xor(s, 2);
-      s += __shfl_xor(s, 4);
-      sb += __shfl_xor(sb, 1);
-      sb += __shfl_xor(sb, 2);
-      sb += __shfl_xor(sb, 4);
-      if (v && (idx & 7) == 0) {
-        xsum[m * nch + (blk >> 3)] = s;
-        xbias[m * nch + (blk >> 3)] = sb;
-      }
-    }
-  }
-  // ---- stage scales / zero-points of this tile, transposed to [g][row] ----
-  {
-    const __half* S = a.scales + (int64_t)item * a.sz_es;
-    const __half* Z = a.zeros + (int64_t)item * a.sz_es;
-    const float zsym = (float)(1 << (BITS - 1));
-    for (int idx = tid; idx < R * G; idx += 256) {
-      const int row = idx / G, g = idx - row * G;
-      const int n = min(r0 + row, N - 1);
-      s_l[g * R + row] = __half2float(S[(int64_t)n * G + g]);
-      z_l[g * R + row] = a.sym ? zsym : __half2float(Z[(int64_t)n * G + g]);
-    }
-  }
-  __syncthreads();
-
-  // ---- main loop: this wave's share of the K chunks ----
+  const __half* S = a.scales + (int64_t)item * a.sz_es;
+  const __half* Z = a.zeros + (int64_t)item * a.sz_es;
   const uint32_t* C = a.codes + (int64_t)item * a.codes_es;
   const uint32_t xor_mask = a.sym ? (BITS == 2 ? 0xAAAAAAAAu : 0x88888888u) : 0u;
   const bool mv = li < M;
-  const int c_begin = (wave * nch) >> 2, c_end = ((wave + 1) * nch) >> 2;
-  const int cpg = a.group >> 7;  // chunks per quantization group
   int64_t roff[T];
 #pragma unroll
   for (int t = 0; t < T; ++t)
@@ -324,58 +262,130 @@ __device__ void gemv_consumer(const GemvArgs& a, int item, int tile,
 #pragma unroll
   for (int t = 0; t < T; ++t) yacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int ch = c_begin; ch < c_end; ++ch) {
-    uint32_t wv[T][BITS];
+  for (int k0 = 0; k0 < K; k0 += KP) {
+    const int kl = min(KP, K - k0);  // codes in this phase
+    const int nchl = kl >> 7;
+    // ---- stage x (permuted to operand order) and its per-chunk sums ----
+    {
+      const int nb = kl >> 4;  // 16-code blocks per token row in this phase
+      const int total = M * nb;
+      for (int base = 0; base < total; base += 256) {
+        const int idx = base + tid;
+        const bool v = idx < total;
+        float s = 0.f, sb = 0.f;
+        int m = 0, blk = 0;
+        if (v) {
+          m = idx / nb;
+          blk = idx - m * nb;
+          const f16x8* src = (const f16x8*)(X + (int64_t)m * K + k0 + blk * 16);
+          f16x8 in0 = src[0], in1 = src[1];
+          _Float16 in[16], o[16];
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-      const uint32_t* p = C + roff[t] + ch * (4 * BITS);
-      if constexpr (BITS == 2) {
-        const u32x2 q = *(const u32x2*)p;
-        wv[t][0] = q.x;
-        wv[t][1] = q.y;
-      } else {
-        const u32x4 q = *(const u32x4*)p;
-        wv[t][0] = q.x;
-        wv[t][1] = q.y;
-        wv[t][2] = q.z;
-        wv[t][3] = q.w;
+          for (int c = 0; c < 8; ++c) {
+            in[c] = in0[c];
+            in[8 + c] = in1[c];
+          }
+#pragma unroll
+          for (int pos = 0; pos < 16; ++pos) {
+            o[pos] = in[perm_src<BITS>(pos)];
+            const float f = (float)o[pos];
+            s += f;
+            sb += code_bias<BITS>(pos) * f;
+          }
+          f16x8 o0, o1;
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            o0[c] = o[c];
+            o1[c] = o[8 + c];
+          }
+          f16x8* dst = (f16x8*)(xs + (int64_t)m * a.xstride + blk * 16);
+          dst[0] = o0;
+          dst[1] = o1;
+        }
+        // 8 consecutive blocks form one 128-code chunk (nb % 8 == 0).
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        s += __shfl_xor(s, 4);
+        sb += __shfl_xor(sb, 1);
+        sb += __shfl_xor(sb, 2);
+        sb += __shfl_xor(sb, 4);
+        if (v && (idx & 7) == 0) {
+          xsum[m * ncp + (blk >> 3)] = s;
+          xbias[m * ncp + (blk >> 3)] = sb;
+        }
       }
     }
-    f16x8 bx[4];
-    float c1 = 0.f, c2 = 0.f;
-    if (mv) {
-      const f16x8* xp = (const f16x8*)(xs + (int64_t)li * a.xstride + ch * 128 + kb * 32);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bx[j] = xp[j];
-      c1 = xbias[li * nch + ch];
-      c2 = xsum[li * nch + ch];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bx[j] = f16x8{};
+    // ---- stage this phase's scales / zero-points, transposed to [g][row] ----
+    {
+      const int g0 = k0 / a.group;
+      const int gl = kl / a.group;
+      const float zsym = (float)(1 << (BITS - 1));
+      for (int idx = tid; idx < R * gl; idx += 256) {
+        const int row = idx / gl, g = idx - row * gl;
+        const int n = min(r0 + row, N - 1);
+        s_l[g * R + row] = __half2float(S[(int64_t)n * G + g0 + g]);
+        z_l[g * R + row] = a.sym ? zsym : __half2float(Z[(int64_t)n * G + g0 + g]);
+      }
     }
-    const int g = ch / cpg;
+    __syncthreads();
+
+    // ---- main loop: this wave's share of the phase's chunks ----
+    const int c_begin = (wave * nchl) >> 2, c_end = ((wave + 1) * nchl) >> 2;
+    const int cg0 = k0 >> 7;  // global index of the phase's first chunk
+    for (int ch = c_begin; ch < c_end; ++ch) {
+      uint32_t wv[T][BITS];
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (BITS == 2) {
-        f16x8 s0, s1, s2, s3;
-        decode2(wv[t][0] ^ xor_mask, s0, s1);
-        decode2(wv[t][1] ^ xor_mask, s2, s3);
-        acc = mfma_16x16x32(s0, bx[0], acc);
-        acc = mfma_16x16x32(s1, bx[1], acc);
-        acc = mfma_16x16x32(s2, bx[2], acc);
-        acc = mfma_16x16x32(s3, bx[3], acc);
+      for (int t = 0; t < T; ++t) {
+        const uint32_t* p = C + roff[t] + (cg0 + ch) * (4 * BITS);
+        if constexpr (BITS == 2) {
+          const u32x2 q = *(const u32x2*)p;
+          wv[t][0] = q.x;
+          wv[t][1] = q.y;
+        } else {
+          const u32x4 q = *(const u32x4*)p;
+          wv[t][0] = q.x;
+          wv[t][1] = q.y;
+          wv[t][2] = q.z;
+          wv[t][3] = q.w;
+        }
+      }
+      f16x8 bx[4];
+      float c1 = 0.f, c2 = 0.f;
+      if (mv) {
+        const f16x8* xp = (const f16x8*)(xs + (int64_t)li * a.xstride + ch * 128 + kb * 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bx[j] = xp[j];
+        c1 = xbias[li * ncp + ch];
+        c2 = xsum[li * ncp + ch];
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc = mfma_16x16x32(decode4(wv[t][j] ^ xor_mask), bx[j], acc);
+        for (int j = 0; j < 4; ++j) bx[j] = f16x8{};
       }
-      const f32x4 sc = *(const f32x4*)(s_l + g * R + t * 16 + 4 * kb);
-      const f32x4 zc = *(const f32x4*)(z_l + g * R + t * 16 + 4 * kb);
+      const int g = ch / cpg;  // group index within the phase
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        yacc[t][i] += sc[i] * ((acc[i] - c1) - zc[i] * c2);
+      for (int t = 0; t < T; ++t) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (BITS == 2) {
+          f16x8 s0, s1, s2, s3;
+          decode2(wv[t][0] ^ xor_mask, s0, s1);
+          decode2(wv[t][1] ^ xor_mask, s2, s3);
+          acc = mfma_16x16x32(s0, bx[0], acc);
+          acc = mfma_16x16x32(s1, bx[1], acc);
+          acc = mfma_16x16x32(s2, bx[2], acc);
+          acc = mfma_16x16x32(s3, bx[3], acc);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc = mfma_16x16x32(decode4(wv[t][j] ^ xor_mask), bx[j], acc);
+        }
+        const f32x4 sc = *(const f32x4*)(s_l + g * R + t * 16 + 4 * kb);
+        const f32x4 zc = *(const f32x4*)(z_l + g * R + t * 16 + 4 * kb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          yacc[t][i] += sc[i] * ((acc[i] - c1) - zc[i] * c2);
+      }
     }
+    __syncthreads();  // the next phase overwrites the staged x / scales
   }
 
   // ---- sum the 4 waves' K-partials ----
@@ -509,17 +519,27 @@ static int64_t workspace_bytes(int64_t items, int64_t M, int64_t K, int64_t rank
   return apart_offset(items) + align_up(items * P * M * rpad * 4, 256);
 }
 
-static size_t lds_bytes(int M, int K, int G, int T, int xstride, int apad) {
-  return (size_t)lds_layout(M, K, G, T, xstride, apad).total;
+static size_t lds_bytes(int M, int KP, int group, int T, int apad) {
+  return (size_t)lds_layout(M, KP, KP / group, T, KP + 8, apad).total;
+}
+
+// Codes per K-phase: the whole K when x fits the staging budget, else the
+// largest multiple of the group size that does.
+constexpr int kXStageBudget = 40 * 1024;
+static int64_t phase_len(int64_t M, int64_t K, int64_t group) {
+  int64_t kp = (kXStageBudget / (2 * M) - 8) / group * group;
+  if (kp < group) kp = group;
+  return kp >= K ? K : kp;
 }
 
 template <int BITS, int T>
 static int launch_t(const GemvArgs& a, int grid, size_t lds, hipStream_t s) {
-  static bool attr_set = false;
-  if (!attr_set) {
+  // Opt in to more than 64 KB of dynamic LDS only when a launch needs it.
+  static size_t attr_bytes = 64 * 1024;
+  if (lds > attr_bytes) {
     GLQ_HIP(hipFuncSetAttribute((const void*)gemv_lora_kernel<BITS, T>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds));
-    attr_set = true;
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr_bytes = lds;
   }
   gemv_lora_kernel<BITS, T><<<dim3(grid), dim3(256), lds, s>>>(a);
   GLQ_LAUNCH_CHECK("gemv_lora_kernel");
@@ -610,13 +630,14 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   a.tiles = (int)((N + 16 * T - 1) / (16 * T));
   a.kw = (int)(K * bits / 32);
   a.rpad = (int)align_up(a.rank, 32);
-  a.xstride = (int)K + 8;
+  a.kp = (int)phase_len(M, K, group);
+  a.xstride = a.kp + 8;
   a.apad = a.rpad + 8;
   a.ctr = (unsigned*)workspace;
   a.apart = (float*)((char*)workspace + apart_offset(items));
   a.spin_limit = 1 << 20;
 
-  const size_t lds = lds_bytes(a.M, a.K, a.G, T, a.xstride, a.apad);
+  const size_t lds = lds_bytes(a.M, a.kp, a.group, T, a.apad);
   GLQ_CHECK(lds <= (size_t)kMaxLds,
             "M*K too large for the GEMV path (needs %zu bytes of LDS)", lds);
   const int64_t grid = items * P + items * a.tiles;

@@ -145,26 +145,38 @@ def linear_forward_fp16(x: torch.Tensor, q: torch.Tensor, scales: torch.Tensor,
 
 
 def linear_forward_fp32(x, q, scales, zeros, groupsize, sym=False, U=None, SV=None,
-                        bias=None) -> torch.Tensor:
-    """fp32 variant: _gptq_pytorch_fallback (inference/kernels/__init__.py:
-    149-178) for the weight term, LoRA `(x @ U) @ SV.T` added in fp32 as the
-    lora_out of gptq_dequant_matmul_fused (:311-315), result cast to fp16
-    (:346)."""
+                        bias=None, precomputed_xU=None) -> torch.Tensor:
+    """The fallback of the op the fused kernel replaces: gptq_dequant_matmul_fused
+    (inference/kernels/__init__.py:284-346) when its extension raises —
+    _gptq_pytorch_fallback (:149-178: W = (q - z) * s in fp32, y = x_fp32 @ W.T)
+    plus the fp32 lora_out (:311-315), cast to fp16 once (:346).  The
+    reference's own kernel tests use the same oracle (reference_gptq_dequant_
+    matmul, inference/kernels/test_gptq_kernel.py:17-53).
+    Pinned by: tolerance against linear_forward_fp64(exact_weights=True), and
+    W = dequant_fp32 equals the exact product s*(q - z) (tests/test_oracle.py).
+    """
     xf = x.float()
     y = xf @ dequant_fp32(q, scales, zeros, groupsize, sym).T
     if SV is not None:
-        y = y + (xf @ U.float()) @ SV.float().T
+        a = precomputed_xU.float() if precomputed_xU is not None else xf @ U.float()
+        y = y + a @ SV.float().T
     if bias is not None:
         y = y + bias.float()
     return y.half()
 
 
 def linear_forward_fp64(x, q, scales, zeros, groupsize, sym=False, U=None, SV=None,
-                        precomputed_xU=None, bias=None) -> torch.Tensor:
-    """Reference-of-reference: exact fp64 sum of the fp16-dequantized weights
-    (dequant_fp16) times x, plus (x U) SV^T (or precomputed_xU SV^T) + bias."""
+                        precomputed_xU=None, bias=None, exact_weights=False) -> torch.Tensor:
+    """Reference-of-reference: fp64 sum of the dequantized weights times x, plus
+    (x U) SV^T (or precomputed_xU SV^T) + bias.  Weights are the fp16-rounded
+    ones of dequant_fp16, or with exact_weights the exact s*(q - z) (what
+    dequant_fp32 computes: an 11-bit scale times a small integer is exact in
+    fp32)."""
     xd = x.double()
-    W = dequant_fp16(q, scales, zeros, groupsize, sym).double()
+    if exact_weights:
+        W = dequant_fp32(q, scales, zeros, groupsize, sym).double()
+    else:
+        W = dequant_fp16(q, scales, zeros, groupsize, sym).double()
     y = xd @ W.T
     if SV is not None:
         a = precomputed_xU.double() if precomputed_xU is not None else xd @ U.double()

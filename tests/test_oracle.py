@@ -112,6 +112,25 @@ def test_dequant_sym():
     assert W.tolist() == [[-1.0, -0.5, 0.0, 0.5]]
 
 
+def test_dequant_fp32_is_exact_product():
+    """fp32 dequant of an 11-bit scale times a small integer is exact: compare
+    with fp64 for every 4-bit (q, z) pair."""
+    q = torch.arange(16, dtype=torch.int32).repeat_interleave(16).reshape(1, -1)
+    z = torch.arange(16, dtype=torch.int32).repeat(16).reshape(1, -1)
+    s = (torch.randn(1, 256, generator=torch.Generator().manual_seed(8)) * 0.02).abs().half()
+    W = O.dequant_fp32(q, s, z.half(), groupsize=1).double()
+    assert torch.equal(W, s.double() * (q.double() - z.double()))
+
+
+def test_fp32_forward_within_bar_of_exact_fp64():
+    for bits, K, N in [(2, 2048, 1408), (4, 2048, 2048), (4, 5632, 256)]:
+        p = fmt.make_linear(K, N, bits=bits, rank=64, M=4, seed=K + N)
+        y32 = O.linear_forward_fp32(p.x, p.q, p.scales, p.zeros, 128, U=p.U, SV=p.SV)
+        y64 = O.linear_forward_fp64(p.x, p.q, p.scales, p.zeros, 128, U=p.U, SV=p.SV,
+                                    exact_weights=True)
+        assert O.parity_ok(y32, y64), (bits, K, N)
+
+
 def test_dequant_fp32_matches_fp16_for_integer_zeros():
     p = fmt.make_linear(256, 40, bits=4, seed=11)
     w16 = O.dequant_fp16(p.q, p.scales, p.zeros, 128)
