@@ -139,7 +139,6 @@ def main():
     per_layer = fmt.algorithmic_bytes(M_, K_, N_, BITS, GROUP, RANK)
     launch_bytes = per_layer * args.pool
     gbs = launch_bytes / (ms * 1e-3) / 1e9
-    status = kernels.workspace_status(kernels.workspace(dev, 0))
 
     # single-call latency, config 0 (one layer, one launch)
     p0 = fmt.make_linear(K_, N_, bits=BITS, group=GROUP, rank=RANK, M=M_, seed=0)
@@ -189,7 +188,6 @@ def main():
         "single_call_config0_us": round(single_ms * 1e3, 2),
         "single_call_config0_GBs": round(per_layer / (single_ms * 1e-3) / 1e9, 1),
         "moe_block_decode_us_per_token": None,
-        "workspace_error_word": status,
     }
     if not args.no_cpu:
         log("cpu baseline (oracle restatement of the reference CPU fallback)")

@@ -44,8 +44,6 @@ SIGNATURES = {
         _vp, _i64,                      # y, y_stride
         _vp, _i64, _vp,                 # workspace, bytes, stream
     ]),
-    "glq_workspace_status": (_c_int, [_vp, ctypes.POINTER(ctypes.c_int32), _vp]),
-    "glq_workspace_reset": (_c_int, [_vp, _i64, _vp]),
     "glq_unpack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _c_int, _vp, _vp]),
     "glq_dequant_weight": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp, _i64, _c_int, _vp, _vp]),
     "glq_pack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp]),

@@ -89,11 +89,6 @@ __global__ void pack_kernel(const int32_t* __restrict__ q, int64_t words,
   codes[w] = v;
 }
 
-__global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
-}
-
 }  // namespace glq
 
 using namespace glq;
@@ -178,30 +173,6 @@ int glq_pack_codes(const int32_t* q, int64_t N, int64_t K, int bits,
   else
     pack_kernel<4><<<grid, bs, 0, s>>>(q, words, (uint32_t*)codes);
   GLQ_LAUNCH_CHECK("pack_kernel");
-  return GLQ_OK;
-}
-
-int glq_workspace_status(const void* workspace, int32_t* status,
-                         void* stream) {
-  clear_error();
-  GLQ_CHECK(workspace && status, "null pointer");
-  hipStream_t s = (hipStream_t)stream;
-  GLQ_HIP(hipMemcpyAsync(status, (const uint32_t*)workspace + kCtrError,
-                         sizeof(int32_t), hipMemcpyDeviceToHost, s));
-  GLQ_HIP(hipStreamSynchronize(s));
-  return GLQ_OK;
-}
-
-int glq_workspace_reset(void* workspace, int64_t workspace_bytes,
-                        void* stream) {
-  clear_error();
-  GLQ_CHECK(workspace, "null workspace");
-  GLQ_CHECK(workspace_bytes >= 4 * kCtrDone, "workspace too small");
-  const int64_t n = workspace_bytes / 4;
-  const int bs = 256;
-  fill_u32_kernel<<<dim3((unsigned)((n + bs - 1) / bs)), bs, 0,
-                    (hipStream_t)stream>>>((uint32_t*)workspace, n);
-  GLQ_LAUNCH_CHECK("fill_u32_kernel");
   return GLQ_OK;
 }
 

@@ -47,12 +47,6 @@ void clear_error();
     }                                                                       \
   } while (0)
 
-// Workspace header layout (32-bit words).  The counters are zero between
-// launches: every launch that uses them resets them before it ends.
 namespace glq {
-constexpr int kCtrTicket = 0;   // next job ticket
-constexpr int kCtrExit = 1;     // workgroups that finished
-constexpr int kCtrError = 2;    // sticky error word (nonzero = wait timed out)
-constexpr int kCtrDone = 64;    // per-item count of finished low-rank producers
 inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 }  // namespace glq

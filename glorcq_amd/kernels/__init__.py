@@ -31,8 +31,8 @@ from ..format import pack_codes
 
 logger = logging.getLogger(__name__)
 
-# workspace cache: (device index, stream handle) -> uint8 tensor (zeroed once;
-# every launch leaves its counters zeroed)
+# workspace cache: (device index, stream handle) -> uint8 tensor.  Launches on
+# one stream run in order, so one buffer per stream is enough.
 _workspaces: dict = {}
 
 GEMV_MAX_M = 16
@@ -60,12 +60,8 @@ def _require(t: torch.Tensor, name: str, dtype=None) -> None:
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zeroed workspace for the current stream of `device`, grown on demand.
-
-    Launches on one stream run in order, and each leaves the counters zero, so
-    the buffer is reused; different streams get different buffers.
-    """
-    lib = _lib.load()
+    """Scratch for the x*U partial sums, one buffer per (device, current stream),
+    grown on demand (it needs no initialisation)."""
     dev = torch.device(device)
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
     key = (idx, _lib.stream_handle(dev))
@@ -74,21 +70,9 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         size = max(nbytes, 1 << 16)
         if ws is not None:
             size = max(size, 2 * ws.numel())
-        ws = torch.zeros(size, dtype=torch.uint8, device=dev)
+        ws = torch.empty(size, dtype=torch.uint8, device=dev)
         _workspaces[key] = ws
-    del lib
     return ws
-
-
-def workspace_status(ws: torch.Tensor) -> int:
-    """Sticky error word of a workspace (0 = every low-rank wait completed)."""
-    import ctypes
-
-    lib = _lib.load()
-    out = ctypes.c_int32(0)
-    _lib.check(lib.glq_workspace_status(ws.data_ptr(), ctypes.byref(out),
-                                        _lib.stream_handle(ws.device)), "glq_workspace_status")
-    return int(out.value)
 
 
 def packed_dequant_matmul_fused(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
@@ -286,5 +270,5 @@ def _unpack_indices_2bit(packed: torch.Tensor, K: int) -> torch.Tensor:
 __all__ = [
     "is_gptq_cuda_available", "is_cuda_available", "packed_dequant_matmul_fused",
     "packed_dequant_matmul_batched", "gptq_dequant_matmul_fused", "unpack_codes",
-    "dequant_weight", "pack_codes_device", "pack_codes", "workspace", "workspace_status",
+    "dequant_weight", "pack_codes_device", "pack_codes", "workspace",
 ]

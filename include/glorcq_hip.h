@@ -43,7 +43,6 @@ extern "C" {
 #define GLQ_OK 0
 #define GLQ_ERR_INVALID 1   /* argument check failed (the TORCH_CHECK analogue) */
 #define GLQ_ERR_HIP 2       /* a HIP runtime call or kernel launch failed       */
-#define GLQ_ERR_WORKSPACE 3 /* workspace too small or in a bad state            */
 
 /* Library version (major*10000 + minor*100 + patch). */
 int glq_version(void);
@@ -53,10 +52,11 @@ const char* glq_last_error(void);
 
 /*
  * Bytes of workspace glq_gemv_lora / glq_gemv_lora_batched need for `items`
- * independent problems of shape (M, K, N, rank).  The workspace must be zeroed
- * once before first use (hipMemset); every launch leaves its counters zeroed on
- * exit, so one workspace can be reused by consecutive launches on ONE stream.
- * Launches that overlap in time (different streams) need different workspaces.
+ * independent problems of shape (M, K, N, rank) when they compute a = x U
+ * themselves (0 when rank == 0).  The workspace holds fp32 partial sums of a
+ * over K-slices of U, written by a first launch and read by the second on the
+ * same stream; it needs no initialisation.  Calls that may run concurrently
+ * (different streams) need different workspaces.
  */
 int64_t glq_gemv_workspace_bytes(int64_t items, int64_t M, int64_t K,
                                  int64_t N, int64_t rank);
@@ -71,7 +71,10 @@ int64_t glq_gemv_workspace_bytes(int64_t items, int64_t M, int64_t K,
  *             x*U, the `precomputed_xU` hook of quantized_linear.py:286); when
  *             given, U is not read.
  *   bias      optional (N) fp16
- *   workspace device buffer of glq_gemv_workspace_bytes(1, M, K, N, rank)
+ *   workspace device buffer of glq_gemv_workspace_bytes(1, M, K, N, rank),
+ *             256-byte aligned (may be NULL when xU is given or rank == 0)
+ * Launches: a K-sliced x*U partial-sum kernel (only when U is used), then the
+ * GEMV kernel, whose epilogue adds a*SV^T with MFMA and rounds once to fp16.
  */
 int glq_gemv_lora(const void* x, int64_t M, int64_t K, int64_t N,
                   const int32_t* codes, int bits, const void* scales,
@@ -100,16 +103,6 @@ int glq_gemv_lora_batched(int64_t items, const void* x, int64_t x_stride,
                           int64_t bias_stride, void* y, int64_t y_stride,
                           void* workspace, int64_t workspace_bytes,
                           void* stream);
-
-/*
- * Reads the sticky error word of a workspace into *status (host pointer) with
- * a synchronous copy on `stream` (0 = no kernel-side error seen; nonzero =
- * a consumer gave up waiting for its low-rank producers).  Debug/test use.
- */
-int glq_workspace_status(const void* workspace, int32_t* status, void* stream);
-
-/* Zeroes a workspace (counters and error word) with a fill kernel. */
-int glq_workspace_reset(void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Debug: unpack codes (N, K*bits/32) int32 -> (N, K) int32.  Codes are
