@@ -94,19 +94,19 @@ struct DenseStreamArgs {
   int tpw;  // 16-row tiles per workgroup
 };
 
-template <int BITS, int MP, int D, bool SYM>
+template <int BITS, int MP, int D, bool SYM, bool SZ2>
 __global__ __launch_bounds__(256) void gemv_stream_dense_kernel(DenseStreamArgs sa) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int item = blockIdx.x / sa.wpi, wg = blockIdx.x - item * sa.wpi;
   const int t0 = wg * sa.tpw, t1 = min(sa.ss.tiles, t0 + sa.tpw);
-  gemv_stream<BITS, MP, D, SYM>(DenseSrc{sa.a}, sa.ss, item, t0, t1, smem);
+  gemv_stream<BITS, MP, D, SYM, SZ2>(DenseSrc{sa.a}, sa.ss, item, t0, t1, smem);
 }
 
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 constexpr int kMaxLds = 160 * 1024;
-constexpr int kStreamDepth = 4;  // ring slots per wave (3 chunks in flight)
+constexpr int kStreamDepth = 3;  // ring slots per wave (2 chunks in flight; 4 workgroups per CU)
 
 static int64_t lowrank_slices(int64_t K) { return (K + kLowrankRows - 1) / kLowrankRows; }
 
@@ -204,8 +204,8 @@ int gemv_check_shape(int64_t M, int64_t K, int64_t N, int bits, int64_t group, i
 // Streaming path (glq_stream.h): group 128, N even (scales, zero-points and
 // bias move as aligned dwords), rank <= 128, and x + rings within the LDS
 // budget.
-bool stream_shape(int64_t items, int64_t M, const TileShape& sh, int bits, StreamShape& ss,
-                  size_t& lds) {
+bool stream_shape(int64_t M, const TileShape& sh, int bits, StreamShape& ss, size_t& lds,
+                  bool& sz2) {
   if (getenv("GLQ_GEMV_NO_STREAM")) return false;
   if (sh.group != 128 || sh.N % 2 != 0 || sh.rank > 128) return false;
   ss.K = sh.K;
@@ -215,22 +215,23 @@ bool stream_shape(int64_t items, int64_t M, const TileShape& sh, int bits, Strea
   ss.rpad = sh.rpad;
   ss.sym = sh.sym;
   ss.kw = sh.kw;
-  ss.nchunk = (int)((int64_t)sh.kw * 4 + 127) / 128;
+  ss.nchunk = (int)(((int64_t)sh.kw * 4 + 127) / 128);
+  ss.nsvc = sh.rank > 0 ? (sh.rank + 63) / 64 : 0;
   ss.tiles = (sh.N + 15) / 16;
   ss.xstride = stream_kpad(sh.K) + 8;
   ss.mmax = (int)M;
-  ss.apad = sh.rpad + 8;
-  ss.svb = (int)align_up(32 * (int64_t)sh.rank, 1024) + 256;
-  ss.nsv = ss.nchunk >= kStreamDepth - 1 ? 2 : kStreamDepth;
-  lds = (size_t)stream_lds<kStreamDepth>((int)M, sh.K, ss.xstride, ss.apad, ss.svb, ss.nsv).total;
-  (void)items;
-  (void)bits;
+  ss.apad = 64 * (ss.nsvc > 0 ? ss.nsvc : 1) + 8;
+  sz2 = bits == 2 && (sh.G % 2) != 0;
+  const int slot = kStreamCodeBytes + (sz2 ? 512 : 256);
+  lds = (size_t)stream_lds(kStreamDepth, slot, (int)M, sh.K, ss.xstride, ss.apad).total;
   return lds <= (size_t)kMaxLds;
 }
 
-// Workgroups per item: aim for about 4 per CU over the whole launch.
+// Workgroups per item: aim for about 4 per CU over the whole launch
+// (GLQ_STREAM_WGS overrides the target).
 void stream_split(int64_t items, int tiles, int& wpi, int& tpw) {
-  const int64_t target = 1024;
+  int64_t target = 1024;
+  if (const char* e = getenv("GLQ_STREAM_WGS")) target = atoll(e) > 0 ? atoll(e) : target;
   int64_t w = (target + items - 1) / items;
   const int64_t wmax = (tiles + 3) / 4;  // at least one tile per wave
   if (w > wmax) w = wmax;
@@ -239,33 +240,37 @@ void stream_split(int64_t items, int tiles, int& wpi, int& tpw) {
   wpi = (tiles + tpw - 1) / tpw;
 }
 
-template <int BITS, int MP, bool SYM>
-static int launch_stream_mp(const DenseStreamArgs& sa, int64_t items, size_t lds, hipStream_t s) {
+template <int BITS, int MP, bool SYM, bool SZ2>
+static int launch_stream_k(const DenseStreamArgs& sa, int64_t items, size_t lds, hipStream_t s) {
   static size_t attr_bytes = 64 * 1024;
-  int rc = set_lds_limit(gemv_stream_dense_kernel<BITS, MP, kStreamDepth, SYM>, lds, attr_bytes);
+  auto kern = gemv_stream_dense_kernel<BITS, MP, kStreamDepth, SYM, SZ2>;
+  int rc = set_lds_limit(kern, lds, attr_bytes);
   if (rc) return rc;
   const int64_t grid = items * sa.wpi;
   GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
-  gemv_stream_dense_kernel<BITS, MP, kStreamDepth, SYM>
-      <<<dim3((unsigned)grid), dim3(256), lds, s>>>(sa);
+  kern<<<dim3((unsigned)grid), dim3(256), lds, s>>>(sa);
   GLQ_LAUNCH_CHECK("gemv_stream_dense_kernel");
   return GLQ_OK;
 }
 
 template <bool SYM>
-static int launch_stream_sym(const DenseStreamArgs& sa, int64_t items, int bits, size_t lds,
-                             hipStream_t s) {
+static int launch_stream_sym(const DenseStreamArgs& sa, int64_t items, int bits, bool sz2,
+                             size_t lds, hipStream_t s) {
   if (bits == 2) {
-    if (sa.ss.mmax > 8) return launch_stream_mp<2, 2, SYM>(sa, items, lds, s);
-    return launch_stream_mp<2, 1, SYM>(sa, items, lds, s);
+    if (sa.ss.mmax > 8) {
+      if (sz2) return launch_stream_k<2, 2, SYM, true>(sa, items, lds, s);
+      return launch_stream_k<2, 2, SYM, false>(sa, items, lds, s);
+    }
+    if (sz2) return launch_stream_k<2, 1, SYM, true>(sa, items, lds, s);
+    return launch_stream_k<2, 1, SYM, false>(sa, items, lds, s);
   }
-  return launch_stream_mp<4, 1, SYM>(sa, items, lds, s);
+  return launch_stream_k<4, 1, SYM, false>(sa, items, lds, s);
 }
 
-static int launch_stream(const DenseStreamArgs& sa, int64_t items, int bits, size_t lds,
-                         hipStream_t s) {
-  if (sa.ss.sym) return launch_stream_sym<true>(sa, items, bits, lds, s);
-  return launch_stream_sym<false>(sa, items, bits, lds, s);
+static int launch_stream(const DenseStreamArgs& sa, int64_t items, int bits, bool sz2,
+                         size_t lds, hipStream_t s) {
+  if (sa.ss.sym) return launch_stream_sym<true>(sa, items, bits, sz2, lds, s);
+  return launch_stream_sym<false>(sa, items, bits, sz2, lds, s);
 }
 
 static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
@@ -335,10 +340,11 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   }
   DenseStreamArgs sa;
   size_t slds = 0;
-  if (stream_shape(items, M, sh, bits, sa.ss, slds)) {
+  bool sz2 = false;
+  if (stream_shape(M, sh, bits, sa.ss, slds, sz2)) {
     sa.a = a;
     stream_split(items, sa.ss.tiles, sa.wpi, sa.tpw);
-    return launch_stream(sa, items, bits, slds, s);
+    return launch_stream(sa, items, bits, sz2, slds, s);
   }
   const size_t lds = gemv_lds_bytes(sh, T);
   GLQ_CHECK(lds <= (size_t)kMaxLds, "M*K too large for the GEMV path (needs %zu bytes of LDS)",

@@ -4,13 +4,15 @@
 // bandwidth instead of simplicity:
 //  * Row-split: each wave owns whole 16-row tiles (full K), so it never waits
 //    on another wave after the one-time staging of x and a.
-//  * Codes, scales and zero-points reach LDS by direct global->LDS loads
-//    (global_load_lds_dwordx4 / _dword), so the data in flight occupies no
-//    VGPRs.  Each wave keeps a ring of D chunk slots; a chunk is 16 rows x
-//    128 contiguous bytes of every row (2 load instructions of 8 rows x 128 B,
-//    the pattern the MI355X memory system serves fastest) plus the chunk's
-//    scales and zero-points.  D-1 chunks are in flight while one is consumed,
-//    across tile boundaries.
+//  * Codes, scales, zero-points, SV rows and bias reach LDS by direct
+//    global->LDS loads (global_load_lds_dwordx4 / _dword), so the data in
+//    flight occupies no VGPRs.  Each wave keeps a ring of D chunk slots and
+//    streams, per tile, its code chunks (16 rows x 128 contiguous bytes of
+//    every row: 2 load instructions of 8 rows x 128 B, the pattern the MI355X
+//    memory system serves fastest, plus the chunk's scales and zero-points)
+//    and then its SV chunks (16 rows x 64 rank columns, + bias), which the
+//    tile epilogue consumes straight from the ring.  D-1 chunks are in flight
+//    while one is consumed, across tile boundaries.
 //  * The 16-byte pieces of a chunk are permuted across lanes (piece ^ (row/2))
 //    so the MFMA-layout reads from LDS are bank-conflict free.
 //  * MFMA roles: A = x (token rows), B = codes (weight rows as columns), so
@@ -22,9 +24,10 @@
 //  * The compiler does not order LDS reads after direct-to-LDS loads, so the
 //    kernel waits explicitly: before consuming chunk c it waits until at most
 //    NI*(D-1) vector-memory operations are outstanding, where NI is the number
-//    of load instructions per chunk.  Loads of one wave complete in order, and
-//    any store or ordinary load issued after chunk c's loads only makes that
-//    wait stricter, so chunk c is in LDS when the wait returns.  Before a
+//    of load instructions every chunk issues (padded with dummy loads where a
+//    chunk needs fewer).  Loads of one wave complete in order, and any store
+//    or ordinary load issued after chunk c's loads only makes that wait
+//    stricter, so chunk c is in LDS when the wait returns.  Before a
 //    slot is refilled, all LDS reads of the wave have completed (lgkmcnt(0)).
 #pragma once
 
@@ -35,8 +38,15 @@ namespace glq {
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kStreamCodeBytes = 2048;  // 16 rows x 128 B
-constexpr int kStreamSzBytes = 512;     // scales + zero-points of a chunk (dword per lane)
-constexpr int kStreamSlot = kStreamCodeBytes + kStreamSzBytes;
+
+// Scale/zero-point bytes per slot: 2-bit with odd G moves one dword per
+// (row, group) for s and for z (512 B); otherwise s and z of a chunk fit one
+// instruction (256 B).
+template <bool SZ2>
+constexpr int stream_slot() { return kStreamCodeBytes + (SZ2 ? 512 : 256); }
+// Load instructions per chunk (every chunk issues exactly this many).
+template <bool SZ2>
+constexpr int stream_ni() { return SZ2 ? 4 : 3; }
 
 // Explicit waits.  Inline asm with a memory clobber, so no compiler pass moves
 // an LDS access across them.
@@ -50,9 +60,8 @@ __device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0
 // Shape/layout of a streaming launch (every item has the same K and N).
 struct StreamShape {
   int K, N, G, rank, rpad, sym, kw;
-  int svb;         // bytes of one SV/bias buffer (32*rank rounded up to 1 KiB, + 256)
-  int nsv;         // SV/bias buffers per wave (tiles whose SV may be in flight)
-  int nchunk;      // 128-byte chunks per row (last one may be partial)
+  int nchunk;      // 128-byte code chunks per row (last one may be partial)
+  int nsvc;        // SV chunks per tile (64 rank columns each; 0 = no LoRA)
   int tiles;       // 16-row tiles per item
   int xstride;     // halves per staged token row of x
   int mmax;        // largest M of any item
@@ -63,220 +72,275 @@ struct StreamLds {
   int xs, xc, a, ring, total;  // byte offsets; xc = [chunk128][16 tokens] x 2 floats
 };
 
-// x rows are padded to a multiple of 256 codes (zeros), plus one all-zero
-// row that masked lanes read; the per-chunk sums get matching zero padding.
+// x rows are padded to a multiple of 256 codes (zeros); lanes without a token
+// read a 512-byte zero block instead (their per-step x stride is 0); the
+// per-chunk sums get matching zero padding.
 __host__ __device__ inline int stream_kpad(int K) { return (K + 255) / 256 * 256; }
 
-template <int D>
-__host__ __device__ inline StreamLds stream_lds(int mmax, int K, int xstride, int apad, int svb,
-                                                int nsv) {
+__host__ __device__ inline StreamLds stream_lds(int D, int slot, int mmax, int K, int xstride,
+                                                int apad) {
   StreamLds L;
   int o = 0;
-  L.xs = o;   o += al16((mmax + 1) * xstride * 2);
+  L.xs = o;   o += al16(mmax * xstride * 2) + 512;  // + zero block read by masked lanes
   L.xc = o;   o += al16((stream_kpad(K) / 128) * 32 * 4);
   L.a = o;    o += al16(16 * apad * 2);
-  L.ring = o; o += 4 * (D * kStreamSlot + nsv * svb);
+  L.ring = o; o += 4 * D * slot;
   L.total = o;
   return L;
 }
 
-// Issues the direct-to-LDS loads of a tile's SV rows (16 x rank fp16,
-// contiguous in memory, dwordx4 per lane) and bias (16 fp16, dword per lane).
-__device__ __forceinline__ void stream_issue_sv(const __half* SV, const __half* B,
-                                                const StreamShape& sh, int r0,
-                                                unsigned char* buf, int lane) {
-  const int rowbytes = sh.rank * 2;
-  const int nbytes = SV ? 16 * rowbytes : 0;
-  for (int I = 0; I * 1024 < nbytes; ++I) {
-    const int o = I * 1024 + 16 * lane;  // byte offset within the 16-row block
-    const int row = min(o, nbytes - 16) / rowbytes;
-    const int col = min(o, nbytes - 16) - row * rowbytes;
-    const char* src = (const char*)SV + (int64_t)min(r0 + row, sh.N - 1) * rowbytes + col;
-    __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(buf + I * 1024), 16, 0, 0);
-  }
-  if (B) {
-    // dword q (< 8) holds bias[r0 + 2q], bias[r0 + 2q + 1] (N is even); past
-    // the last row it re-reads the last dword, whose values are never stored
-    const int n = min(r0 + 2 * (lane & 7), sh.N - 2);
-    __builtin_amdgcn_global_load_lds((const void*)(B + n), (lds_void*)(buf + sh.svb - 256), 4, 0,
-                                     0);
-  }
-}
+// Per-tile load addresses of one lane (see StreamCursor::retarget).
+struct IssuePtrs {
+  const char* code[2];  // this lane's row start in the codes, per instruction
+  const char* sv[2];    // ... in SV
+  const char* s;        // scale dword base (element row*G of this lane's row), bytes
+  const char* z;        // zero-point dword base
+  const char* bias;     // bias dword of this lane
+};
 
-// Element index (row n, group g) of a scale / zero-point, clamped in bounds.
-__device__ __forceinline__ int64_t sz_index(const StreamShape& sh, int r, int g) {
-  return (int64_t)min(r, sh.N - 1) * sh.G + min(g, sh.G - 1);
-}
+// Issue-side cursor of one wave: which chunk of which tile goes out next.
+template <int BITS, bool SZ2>
+struct StreamCursor {
+  int c = 0;      // chunk within the tile (codes first, then SV chunks)
+  int r0 = 0;     // first row of the tile
+  int slot = 0;   // ring slot the next chunk lands in
+  IssuePtrs P;
 
-// Issues the direct-to-LDS loads of chunk `ch` of the tile at row r0: codes
-// (2 x dwordx4: lane q of instruction I carries row 8I + q/8, 16-byte piece
-// (q%8) ^ ((row/2)%8)), then the chunk's scales and zero-points as the
-// aligned dwords that contain them (2-bit: lane q -> row q/4, group 4ch+q%4,
-// one instruction each for s and z; 4-bit: lane q -> row (q%32)/2, group
-// 2ch+q%2, s in lanes 0-31 and z in 32-63).  The host guarantees N*G is even,
-// so every such dword lies inside the tensor.
-template <int BITS>
-__device__ __forceinline__ void stream_issue(const uint32_t* C, const __half* S, const __half* Z,
-                                             const StreamShape& sh, int r0, int ch,
-                                             unsigned char* slot, int lane) {
-  const char* cb = (const char*)C;
-  const int64_t rowbytes = (int64_t)sh.kw * 4;
-  const int64_t total = rowbytes * sh.N;
+  // Recomputes this lane's row pointers for the tile at row r0 (once per tile).
+  __device__ __forceinline__ void retarget(const uint32_t* C, const __half* S, const __half* Zs,
+                                           const __half* SV, const __half* B,
+                                           const StreamShape& sh, int lane) {
+    const int64_t rowbytes = (int64_t)sh.kw * 4;
 #pragma unroll
-  for (int I = 0; I < 2; ++I) {
-    const int row = 8 * I + (lane >> 3);
-    const int piece = (lane & 7) ^ ((row >> 1) & 7);
-    const int n = min(r0 + row, sh.N - 1);
-    int64_t off = (int64_t)n * rowbytes + 128 * ch + 16 * piece;
-    if (off + 16 > total) off = total - 16;  // tail of the last row: stay in bounds
-    __builtin_amdgcn_global_load_lds((const void*)(cb + off), (lds_void*)(slot + 1024 * I), 16,
-                                     0, 0);
+    for (int I = 0; I < 2; ++I) {
+      const int n = min(r0 + 8 * I + (lane >> 3), sh.N - 1);
+      P.code[I] = (const char*)C + n * rowbytes;
+      P.sv[I] = SV ? (const char*)SV + (int64_t)n * sh.rank * 2 : nullptr;
+    }
+    if constexpr (BITS == 2 && SZ2) {
+      const int n = min(r0 + (lane >> 2), sh.N - 1);
+      P.s = (const char*)(S + (int64_t)n * sh.G);
+      P.z = (const char*)(Zs + (int64_t)n * sh.G);
+    } else {
+      const int q = lane & 31;
+      const int n = min(r0 + (q >> 1), sh.N - 1);
+      P.s = (const char*)((lane < 32 ? S : Zs) + (int64_t)n * sh.G);
+      P.z = P.s;
+    }
+    P.bias = B ? (const char*)(B + min(r0 + 2 * (lane & 7), sh.N - 2)) : nullptr;
   }
-  const __half* Zs = sh.sym ? S : Z;
+};
+
+// Issues code chunk `ch` of the cursor's tile into `slot`: codes (16 rows x
+// 128 B: lane q of instruction I carries row 8I + q/8, 16-byte piece
+// (q%8) ^ ((row/2)%8), so MFMA-layout reads are bank-conflict free; pieces
+// past the end of a row re-read the row's last piece), then the chunk's
+// scales and zero-points as the aligned dwords that contain them:
+//   2-bit, even G: lane q -> (q<32 ? s : z), row (q%32)/2, groups 4ch+2(q%2)+{0,1}
+//   2-bit, odd G (SZ2): lane q -> row q/4, group 4ch+q%4; s then z instruction
+//   4-bit: lane q -> (q<32 ? s : z), row (q%32)/2, group 2ch+q%2
+// N is even (host check), so every dword lies inside its tensor.
+template <int BITS, bool SZ2>
+__device__ __forceinline__ void stream_issue(const IssuePtrs& P, const StreamShape& sh, int ch,
+                                             unsigned char* slot, int lane, int piece0,
+                                             int piece1) {
+  const int rowlast = sh.kw * 4 - 16;
+  __builtin_amdgcn_global_load_lds((const void*)(P.code[0] + min(128 * ch + piece0, rowlast)),
+                                   (lds_void*)slot, 16, 0, 0);
+  __builtin_amdgcn_global_load_lds((const void*)(P.code[1] + min(128 * ch + piece1, rowlast)),
+                                   (lds_void*)(slot + 1024), 16, 0, 0);
   unsigned char* szs = slot + kStreamCodeBytes;
-  if constexpr (BITS == 2) {
-    const int64_t e = sz_index(sh, r0 + (lane >> 2), 4 * ch + (lane & 3));
-    __builtin_amdgcn_global_load_lds((const void*)(S + (e & ~1ll)), (lds_void*)szs, 4, 0, 0);
-    __builtin_amdgcn_global_load_lds((const void*)(Zs + (e & ~1ll)), (lds_void*)(szs + 256), 4, 0,
-                                     0);
+  if constexpr (BITS == 2 && SZ2) {
+    const int g = min(4 * ch + (lane & 3), sh.G - 1);
+    // element row*G + g rounded down to even: the row base parity is folded
+    // in by the pointer (row*G may be odd), so round the absolute address
+    const uintptr_t sa = ((uintptr_t)(P.s + 2 * g)) & ~(uintptr_t)3;
+    const uintptr_t za = ((uintptr_t)(P.z + 2 * g)) & ~(uintptr_t)3;
+    __builtin_amdgcn_global_load_lds((const void*)sa, (lds_void*)szs, 4, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)za, (lds_void*)(szs + 256), 4, 0, 0);
+  } else if constexpr (BITS == 2) {
+    const int g = min(4 * ch + 2 * (lane & 1), sh.G - 2);  // even: G is even here
+    __builtin_amdgcn_global_load_lds((const void*)(P.s + 2 * g), (lds_void*)szs, 4, 0, 0);
   } else {
-    const int q = lane & 31;
-    const int64_t e = sz_index(sh, r0 + (q >> 1), 2 * ch + (q & 1));
-    const __half* base = lane < 32 ? S : Zs;
-    __builtin_amdgcn_global_load_lds((const void*)(base + (e & ~1ll)), (lds_void*)szs, 4, 0, 0);
+    const int g = min(2 * ch + (lane & 1), sh.G - 1);
+    const uintptr_t sa = ((uintptr_t)(P.s + 2 * g)) & ~(uintptr_t)3;
+    __builtin_amdgcn_global_load_lds((const void*)sa, (lds_void*)szs, 4, 0, 0);
   }
 }
 
-template <int BITS>
-constexpr int stream_ni() { return BITS == 2 ? 4 : 3; }
+// SV chunk `c` of the cursor's tile: rank columns [64c, 64c + 64) of 16 SV
+// rows (columns past the rank read the row's last piece; the matching a
+// values are zero), then bias dwords (lane q -> bias[r0 + 2(q%8)], +1) or a
+// dummy load, and a second dummy for NI == 4, so the chunk issues NI loads.
+template <bool SZ2>
+__device__ __forceinline__ void stream_issue_sv(const IssuePtrs& P, const StreamShape& sh, int c,
+                                                unsigned char* slot, int piece0, int piece1,
+                                                const void* dummy) {
+  unsigned char* szs = slot + kStreamCodeBytes;
+  if (P.sv[0]) {
+    const int rowlast = sh.rank * 2 - 16;
+    __builtin_amdgcn_global_load_lds((const void*)(P.sv[0] + min(128 * c + piece0, rowlast)),
+                                     (lds_void*)slot, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(P.sv[1] + min(128 * c + piece1, rowlast)),
+                                     (lds_void*)(slot + 1024), 16, 0, 0);
+  } else {  // bias only: two dummy loads keep the instruction count
+    __builtin_amdgcn_global_load_lds(dummy, (lds_void*)slot, 4, 0, 0);
+    __builtin_amdgcn_global_load_lds(dummy, (lds_void*)(slot + 1024), 4, 0, 0);
+  }
+  const void* src = P.bias ? (const void*)P.bias : dummy;
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)szs, 4, 0, 0);
+  if constexpr (SZ2) __builtin_amdgcn_global_load_lds(src, (lds_void*)(szs + 256), 4, 0, 0);
+}
 
 // Per-lane constants of the consume loop (computed once per workgroup).
 template <int MP>
 struct StreamLane {
-  int code_off[2];  // byte offset of this lane's 16 B of codes in a slot, per step
-  int xa[MP];       // half offset of this lane's x operand row (or the zero row)
-  int xcb[MP];      // float offset of this lane's c1 values in a 128-code chunk row
-  int szb;          // byte offset of this lane's scale dword in a slot
+  int code_off[2];  // byte offset of this lane's 16 B in a slot, per step
+  int xa[MP];       // half offset of this lane's x operand row (or the zero block)
+  int xstep[MP];    // halves per 256-code step along that row (0 for the zero block)
+  int xcb[MP];      // unused (kept for layout symmetry)
+  int szb;          // byte offset of the main-path scale dword (step 0)
+  int szstep;       // bytes between the scale dwords of steps 0 and 1
+  int cszb;         // byte offset of the correction scale dword (group kb)
+  int czoff;        // bytes from a scale dword to its zero-point dword
   int h;            // 2-bit: group-half of this lane's D rows and codes
 };
 
-// Consumes one chunk (2 steps) of a tile from its LDS slot into yacc.
-// Branch-free: masked lanes read the zero x row; a group past K (2-bit tail)
-// gets scale 0; rowpar = parity of the tile row's first scale element.
+// v_mfma_f32_16x16x4_f32: A 16x4, B 4x16 fp32, used for the zero-point and
+// operand-bias correction over the groups of a chunk.
+__device__ __forceinline__ f32x4 mfma_16x16x4f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// The half selected by `sh16` (0 or 16) of an fp16 pair, as float.
+__device__ __forceinline__ float half_of(uint32_t w, int sh16) {
+  return __half2float(__ushort_as_half((uint16_t)(w >> sh16)));
+}
+
+// Consumes one code chunk (2 steps) of a tile from its LDS slot.
+//   yacc += s_g * (MFMA sum of (2^e + q) x) per step (scale only), and
+//   corr -= sum_g s_g c1_g + (s_g z_g) c2_g over the chunk's groups, as two
+//   fp32 MFMAs (A = c1 / c2 of tokens x groups, B = s / s*z of groups x rows).
+// A group past K (2-bit tail) gets scale 0; `par*` select the fp16 half of
+// each staged scale dword.
 template <int BITS, int MP, bool SYM>
-__device__ __forceinline__ void stream_consume(const unsigned char* slot, int ch, int rowpar,
-                                               const StreamShape& sh, const __half* xs,
-                                               const float* xc, f32x4 (&yacc)[MP],
-                                               const StreamLane<MP>& ln,
-                                               const DecodeConsts& dk) {
+__device__ __forceinline__ void stream_consume(const unsigned char* slot, int ch, int par0,
+                                               int par1, int cpar, const StreamShape& sh,
+                                               const __half* xs, const float* xc,
+                                               f32x4 (&yacc)[MP], f32x4& corr,
+                                               const StreamLane<MP>& ln, const DecodeConsts& dk,
+                                               int li, int kb) {
   // symmetric codes are b-bit two's complement: flipping the top bit maps
   // them to q + 2^(b-1), whose zero-point is 2^(b-1)
   constexpr uint32_t xor_mask = SYM ? (BITS == 2 ? 0xAAAAAAAAu : 0x88888888u) : 0u;
-  const float zsym = (float)(1 << (BITS - 1));
+  constexpr int GPC = BITS == 2 ? 4 : 2;  // groups per chunk
   const unsigned char* sz = slot + kStreamCodeBytes;
+  // ---- correction for the chunk's groups (lane: row li, group kb) ----
+  {
+    const int g = GPC * ch + kb;
+    const bool gv = kb < GPC && g * 128 < sh.K;
+    const uint32_t sw_ = *(const uint32_t*)(sz + ln.cszb);
+    const float sc = gv ? half_of(sw_, 16 * cpar) : 0.f;
+    float zc = (float)(1 << (BITS - 1));
+    if constexpr (!SYM) zc = half_of(*(const uint32_t*)(sz + ln.cszb + ln.czoff), 16 * cpar);
+    const int gi = min(g, (stream_kpad(sh.K) >> 7) - 1);
+    const float c1 = xc[gi * 32 + li], c2 = xc[gi * 32 + 16 + li];
+    corr = mfma_16x16x4f32(c1, -sc, corr);
+    corr = mfma_16x16x4f32(c2, -sc * zc, corr);
+  }
 #pragma unroll
   for (int sp = 0; sp < 2; ++sp) {
     u32x4 w = *(const u32x4*)(slot + ln.code_off[sp]);
     if constexpr (SYM) w ^= xor_mask;
     const int st = 2 * ch + sp;
-    if constexpr (BITS == 2) {
-      // scale / zero-point of group 4ch + 2sp + h: dword (row*4 + 2sp + h)
-      const int c128 = 2 * st + ln.h;
-      const int sh16 = 16 * (rowpar ^ ln.h);
-      const uint32_t sw_ = *(const uint32_t*)(sz + ln.szb + 8 * sp);
-      float s = __half2float(__ushort_as_half((uint16_t)(sw_ >> sh16)));
-      s = c128 * 128 < sh.K ? s : 0.f;
-      float z = zsym;
-      if constexpr (!SYM) {
-        const uint32_t zw = *(const uint32_t*)(sz + 256 + ln.szb + 8 * sp);
-        z = __half2float(__ushort_as_half((uint16_t)(zw >> sh16)));
-      }
-      f32x4 acc[MP];
+    const int c128 = BITS == 2 ? 2 * st + ln.h : st;
+    const uint32_t sw_ = *(const uint32_t*)(sz + ln.szb + sp * ln.szstep);
+    float s = half_of(sw_, 16 * (sp ? par1 : par0));
+    s = c128 * 128 < sh.K ? s : 0.f;
+    f32x4 acc[MP];
 #pragma unroll
-      for (int p = 0; p < MP; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < MP; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (BITS == 2) {
         f16x8 b0, b1;
         decode2(w[i], b0, b1, dk);
 #pragma unroll
         for (int p = 0; p < MP; ++p) {
-          const __half* xr = xs + ln.xa[p] + st * 256 + 16 * i;
+          const __half* xr = xs + ln.xa[p] + st * ln.xstep[p] + 16 * i;
           acc[p] = mfma_16x16x32(*(const f16x8*)xr, b0, acc[p]);
           acc[p] = mfma_16x16x32(*(const f16x8*)(xr + 8), b1, acc[p]);
         }
+      } else {
+        const __half* xr = xs + ln.xa[0] + st * ln.xstep[0] + 8 * i;
+        acc[0] = mfma_16x16x32(*(const f16x8*)xr, decode4(w[i], dk), acc[0]);
       }
-#pragma unroll
-      for (int p = 0; p < MP; ++p) {
-        const f32x4 c1 = *(const f32x4*)(xc + c128 * 32 + ln.xcb[p]);
-        const f32x4 c2 = *(const f32x4*)(xc + c128 * 32 + 16 + ln.xcb[p]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) yacc[p][i] += s * (acc[p][i] - fmaf(z, c2[i], c1[i]));
-      }
-    } else {
-      const int sh16 = 16 * (rowpar ^ sp);
-      const uint32_t sw_ = *(const uint32_t*)(sz + ln.szb + 4 * sp);
-      float s = __half2float(__ushort_as_half((uint16_t)(sw_ >> sh16)));
-      s = st * 128 < sh.K ? s : 0.f;
-      float z = zsym;
-      if constexpr (!SYM) {
-        const uint32_t zw = *(const uint32_t*)(sz + 128 + ln.szb + 4 * sp);
-        z = __half2float(__ushort_as_half((uint16_t)(zw >> sh16)));
-      }
-      const __half* xr = xs + ln.xa[0] + st * 128;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        acc = mfma_16x16x32(*(const f16x8*)(xr + 8 * i), decode4(w[i], dk), acc);
-      const f32x4 c1 = *(const f32x4*)(xc + st * 32 + ln.xcb[0]);
-      const f32x4 c2 = *(const f32x4*)(xc + st * 32 + 16 + ln.xcb[0]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) yacc[0][i] += s * (acc[i] - fmaf(z, c2[i], c1[i]));
     }
+#pragma unroll
+    for (int p = 0; p < MP; ++p)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) yacc[p][i] = fmaf(s, acc[p][i], yacc[p][i]);
   }
 }
 
 // One workgroup: tiles [t0, t1) of one item; wave w takes t0 + w, t0 + w + 4, ...
-template <int BITS, int MP, int D, bool SYM, class Src>
+template <int BITS, int MP, int D, bool SYM, bool SZ2, class Src>
 __device__ void gemv_stream(const Src& src, const StreamShape& sh, int item, int t0, int t1,
                             unsigned char* smem) {
-  constexpr int NI = stream_ni<BITS>();
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int NI = stream_ni<SZ2>();
+  constexpr int SLOT = stream_slot<SZ2>();
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, kb = lane >> 4;
   const int M = src.m_rows(item);
-  const StreamLds L = stream_lds<D>(sh.mmax, sh.K, sh.xstride, sh.apad, sh.svb, sh.nsv);
-  __half* xs = (__half*)(smem + L.xs);  // (mmax + 1) rows; row mmax is all zero
+  const StreamLds L = stream_lds(D, SLOT, sh.mmax, sh.K, sh.xstride, sh.apad);
+  __half* xs = (__half*)(smem + L.xs);  // mmax rows, then a 512-byte zero block
   float* xc = (float*)(smem + L.xc);    // [c128][c1 x16 | c2 x16]
   __half* a_l = (__half*)(smem + L.a);
-  unsigned char* ring = smem + L.ring + wave * (D * kStreamSlot + sh.nsv * sh.svb);
-  unsigned char* svbuf = ring + D * kStreamSlot;  // nsv buffers of SV rows + bias
+  unsigned char* ring = smem + L.ring + wave * D * SLOT;
 
   const uint32_t* C = src.codes(item);
   const __half* S = src.scales(item);
-  const __half* Z = src.zeros(item);
+  const __half* Zs = SYM ? S : src.zeros(item);
   const __half* SV = src.sv(item);
   const __half* B = src.bias(item);
   const bool lora = sh.rank > 0 && SV != nullptr;
-  const bool per_tile = lora || B != nullptr;
+  const int nsvc = (lora || B != nullptr) ? (lora ? sh.nsvc : 1) : 0;
+  const int cpt = sh.nchunk + nsvc;  // chunks per tile
 
-  // This wave's work list: tiles t0 + wave + 4j, nchunk chunks each.
+  // This wave's work list: tiles t0 + wave + 4j, cpt chunks each.
   const int ntile_w = t1 - t0 > wave ? (t1 - t0 - wave + 3) / 4 : 0;
-  const int total = ntile_w * sh.nchunk;
-  auto issue = [&](int un) {
-    const int ch = un % sh.nchunk;
-    const int j = un / sh.nchunk;
-    const int r0 = (t0 + wave + 4 * j) * 16;
-    if (ch == 0 && per_tile)
-      stream_issue_sv(lora ? SV : nullptr, B, sh, r0, svbuf + (j % sh.nsv) * sh.svb, lane);
-    stream_issue<BITS>(C, S, Z, sh, r0, ch, ring + (un % D) * kStreamSlot, lane);
+  const int total = ntile_w * cpt;
+
+  // byte offsets of this lane's 16-byte pieces within a 128-byte chunk row
+  const int piece0 = 16 * ((lane & 7) ^ (((lane >> 3) >> 1) & 7));
+  const int piece1 = 16 * ((lane & 7) ^ (((8 + (lane >> 3)) >> 1) & 7));
+  StreamCursor<BITS, SZ2> cur;
+  cur.r0 = (t0 + wave) * 16;
+  cur.retarget(C, S, Zs, lora ? SV : nullptr, B, sh, lane);
+  int issued = 0;
+  auto issue_next = [&]() {
+    unsigned char* slot = ring + cur.slot * SLOT;
+    if (cur.c < sh.nchunk)
+      stream_issue<BITS, SZ2>(cur.P, sh, cur.c, slot, lane, piece0, piece1);
+    else
+      stream_issue_sv<SZ2>(cur.P, sh, cur.c - sh.nchunk, slot, piece0, piece1, (const void*)C);
+    if (++cur.slot == D) cur.slot = 0;
+    ++issued;
+    if (++cur.c == cpt) {
+      cur.c = 0;
+      cur.r0 += 64;
+      cur.retarget(C, S, Zs, lora ? SV : nullptr, B, sh, lane);
+    }
   };
 
   // ---- prologue: D-1 chunks in flight, then stage x, its sums, and a ----
-  for (int u = 0; u < D - 1 && u < total; ++u) issue(u);
+  for (int u = 0; u < D - 1 && u < total; ++u) issue_next();
 
   const int kpad = stream_kpad(sh.K);
   {
     const int nb = kpad >> 4;  // 16-code blocks per padded token row
-    const int totalb = (sh.mmax + 1) * nb;
+    const int totalb = sh.mmax * nb;
     for (int base = 0; base < totalb; base += 256) {
       const int idx = base + tid;
       const bool v = idx < totalb;
@@ -327,6 +391,8 @@ __device__ void gemv_stream(const Src& src, const StreamShape& sh, int item, int
         xc[c128 * 32 + 16 + m] = s;  // c2: sum of x
       }
     }
+    for (int idx = tid; idx < 128; idx += 256)  // the zero block
+      ((uint32_t*)(xs + sh.mmax * sh.xstride))[idx] = 0u;
     // tokens mmax..15 of every chunk read as zero
     const int nc = kpad >> 7, nz = 16 - sh.mmax;
     for (int idx = tid; idx < nc * nz; idx += 256) {
@@ -340,6 +406,11 @@ __device__ void gemv_stream(const Src& src, const StreamShape& sh, int item, int
       const int m = idx / sh.rpad, j = idx - m * sh.rpad;
       a_l[m * sh.apad + j] =
           (m < M && j < sh.rank) ? src.load_a(item, m, j) : __float2half(0.f);
+    }
+    // rank columns rpad..64*nsvc of a read as zero by the last SV chunk
+    for (int idx = tid; idx < 16 * (sh.apad - sh.rpad); idx += 256) {
+      const int m = idx / (sh.apad - sh.rpad), j = sh.rpad + idx % (sh.apad - sh.rpad);
+      a_l[m * sh.apad + j] = __float2half(0.f);
     }
   }
   __syncthreads();
@@ -357,15 +428,30 @@ __device__ void gemv_stream(const Src& src, const StreamShape& sh, int item, int
       for (int p = 0; p < MP; ++p) {
         const int m = (li & 7) + 8 * p;
         const bool act = ((li >> 3) == ln.h) && m < M;
-        ln.xa[p] = (act ? m * sh.xstride : zrow) + 64 * kb;
-        ln.xcb[p] = 8 * p + 4 * (kb & 1);
+        ln.xa[p] = act ? m * sh.xstride + 64 * kb : zrow;
+        ln.xstep[p] = act ? 256 : 0;
+        ln.xcb[p] = 0;
       }
-      ln.szb = 4 * (li * 4 + ln.h);
+      if constexpr (SZ2) {  // dword (row*4 + group%4); z 256 B after s
+        ln.szb = 4 * (li * 4 + ln.h);
+        ln.szstep = 8;
+        ln.cszb = 4 * (li * 4 + kb);
+        ln.czoff = 256;
+      } else {              // dword (row*2 + group%4/2) holds groups 2j, 2j+1; z 128 B after s
+        ln.szb = 8 * li;
+        ln.szstep = 4;
+        ln.cszb = 8 * li + 4 * (kb >> 1);
+        ln.czoff = 128;
+      }
     } else {
       ln.h = 0;
-      ln.xa[0] = (li < M ? li * sh.xstride : zrow) + 32 * kb;
-      ln.xcb[0] = 4 * kb;
+      ln.xa[0] = li < M ? li * sh.xstride + 32 * kb : zrow;
+      ln.xstep[0] = li < M ? 128 : 0;
+      ln.xcb[0] = 0;
       ln.szb = 8 * li;
+      ln.szstep = 4;
+      ln.cszb = 8 * li + 4 * (kb & 1);
+      ln.czoff = 128;
     }
   }
 
@@ -374,60 +460,84 @@ __device__ void gemv_stream(const Src& src, const StreamShape& sh, int item, int
   f32x4 yacc[MP];
 #pragma unroll
   for (int p = 0; p < MP; ++p) yacc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
-  int ch = 0, jt = 0, slot = 0;
+  f32x4 corr = {0.f, 0.f, 0.f, 0.f};
+  f32x4 y = {0.f, 0.f, 0.f, 0.f};
+  int c = 0, slot = 0;
   int r0 = (t0 + wave) * 16;
-  int rowpar = (int)(((int64_t)min(r0 + li, sh.N - 1) * sh.G) & 1);
+  // fp16 half of each staged scale dword: main path steps 0/1 and correction
+  int par0, par1, cpar;
+  auto parities = [&]() {
+    const int rowpar = (int)(((int64_t)min(r0 + li, sh.N - 1) * sh.G) & 1);
+    if constexpr (BITS == 2 && SZ2) {
+      par0 = par1 = rowpar ^ ln.h;
+      cpar = rowpar ^ (kb & 1);
+    } else if constexpr (BITS == 2) {
+      par0 = par1 = ln.h;
+      cpar = kb & 1;
+    } else {
+      par0 = rowpar;
+      par1 = rowpar ^ 1;
+      cpar = rowpar ^ (kb & 1);
+    }
+  };
+  parities();
   for (int u = 0; u < total; ++u) {
-    if (u + D - 1 < total) {
+    if (issued < total) {
       wait_lgkm0();  // slot (u-1)%D: every LDS read of it has completed
-      issue(u + D - 1);
+      issue_next();
       wait_vmcnt<NI * (D - 1)>();
     } else {
       wait_vmcnt<0>();
     }
-    stream_consume<BITS, MP, SYM>(ring + slot * kStreamSlot, ch, rowpar, sh, xs, xc, yacc, ln,
-                                  dk);
+    const unsigned char* sl = ring + slot * SLOT;
     if (++slot == D) slot = 0;
-    if (++ch == sh.nchunk) {
-      // ---- tile epilogue (this wave only); its SV rows and bias arrived
-      //      with the tile's first chunk ----
-      const unsigned char* sb = svbuf + (jt % sh.nsv) * sh.svb;
-      f32x4 y;
-      if constexpr (BITS == 2) {
-        f32x4 y0 = yacc[0], y1 = yacc[MP - 1];
+    if (c < sh.nchunk) {
+      stream_consume<BITS, MP, SYM>(sl, c, par0, par1, cpar, sh, xs, xc, yacc, corr, ln, dk, li,
+                                    kb);
+      if (c == sh.nchunk - 1) {
+        // the tile's code sums: merge the 2-bit halves into the standard
+        // MFMA layout D[token 4kb+i][row li], then add the correction
+        if constexpr (BITS == 2) {
+          f32x4 y0 = yacc[0], y1 = yacc[MP - 1];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          y0[i] += __shfl_xor(y0[i], 32);
-          if (MP == 2) y1[i] += __shfl_xor(y1[i], 32);
+          for (int i = 0; i < 4; ++i) {
+            y0[i] += __shfl_xor(y0[i], 32);
+            if (MP == 2) y1[i] += __shfl_xor(y1[i], 32);
+          }
+          y = kb < 2 ? y0 : (MP == 2 ? y1 : f32x4{0.f, 0.f, 0.f, 0.f});
+        } else {
+          y = yacc[0];
         }
-        y = kb < 2 ? y0 : (MP == 2 ? y1 : f32x4{0.f, 0.f, 0.f, 0.f});
-      } else {
-        y = yacc[0];
+        y += corr;
+        corr = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < MP; ++p) yacc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-      if (lora) {
-        const __half* svr = (const __half*)sb + li * sh.rank;
-        for (int s = 0; s < sh.rpad; s += 32) {
-          const int j = s + 8 * kb;
-          const f16x8 bv = j < sh.rank ? *(const f16x8*)(svr + j) : f16x8{};
-          const f16x8 av = *(const f16x8*)(a_l + li * sh.apad + j);
-          y = mfma_16x16x32(av, bv, y);
-        }
+    } else if (lora) {
+      // SV chunk: rank columns 64(c - nchunk) .. +64 of this tile's rows
+      const int j0 = 64 * (c - sh.nchunk);
+#pragma unroll
+      for (int sp = 0; sp < 2; ++sp) {
+        const f16x8 bv = *(const f16x8*)(sl + ln.code_off[sp]);
+        const f16x8 av = *(const f16x8*)(a_l + li * sh.apad + j0 + 32 * sp + 8 * kb);
+        y = mfma_16x16x32(av, bv, y);
       }
+    }
+    if (++c == cpt) {
+      // ---- tile epilogue: bias (in the last SV chunk's slot) and store ----
       const int n = r0 + li;
       if (n < sh.N) {
-        const float bn = B ? __half2float(((const __half*)(sb + sh.svb - 256))[li]) : 0.f;
+        const float bn =
+            B ? __half2float(((const __half*)(sl + kStreamCodeBytes))[li]) : 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int m = 4 * kb + i;
           if (m < M) src.store(item, m, n, y[i] + bn);
         }
       }
-#pragma unroll
-      for (int p = 0; p < MP; ++p) yacc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
-      ch = 0;
-      ++jt;
+      c = 0;
       r0 += 64;
-      rowpar = (int)(((int64_t)min(r0 + li, sh.N - 1) * sh.G) & 1);
+      parities();
     }
   }
 }
