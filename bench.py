@@ -5,17 +5,26 @@ Metric: 2-bit dequant-GEMV+LoRA HBM GB/s (% of peak).
 Workload (config 1's 2-bit expert projection, K=2048 -> N=1408, group 128,
 rank 64, M=1): a cold-cache pool of POOL distinct layers (own codes, scales,
 zeros, U, SV, x, y each; 512 x 1.26 MB = 645 MB, above the 256 MB Infinity
-Cache and the L2s), all computed by ONE launch of the fused kernel — the
-grouped expert GEMV of a MoE decode step.  A step is one such launch.
-value = POOL * algorithmic_bytes / step time, algorithmic bytes per layer =
-N*K*b/8 + 4*N*G + 2*r*(K+N) + 2*M*(K+N) = 1,260,288 B.
+Cache and the L2s).  One step = the fused op over the whole pool, i.e. one
+call of the batched entry point: launch 1 computes the x*U partial sums,
+launch 2 streams the packed codes, dequantizes in registers, runs the MFMA
+GEMV and adds the low-rank term a*SV^T in its epilogue.
+  value = POOL * algorithmic_bytes / step time, algorithmic bytes per layer =
+  N*K*b/8 + 4*N*G + 2*r*(K+N) + 2*M*(K+N) = 1,260,288 B.
 
-Also reported: single-call latency of config 0 (one layer, one launch), and
+roofline: the dominant kernel (the GEMV, launch 2) timed alone with HIP events
+on the launch stream, fed the same layers' a = x*U precomputed by the library;
+its algorithmic bytes per layer = N*K*b/8 + 4*N*G + 2*r*N + 2*M*(K+N) + 2*M*r
+(codes, scales+zeros, SV, x, y, a) = 998,272 B.
+
+Also reported: single-call latency of config 0 (one layer, both launches), and
 the CPU baseline = the reference's CPU fallback restated in oracle/ (fp16
 dequant loop + fp16 x@W.T + fp16 LoRA) on config 0, timed on the host cores;
 its output doubles as the parity check of the GPU result for the same input.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       python bench.py --pmc-workload   (the GEMV kernel alone + a plain copy
+                                         of known size, for rocprofv3 --pmc)
 """
 
 from __future__ import annotations
@@ -29,6 +38,7 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+METRIC = "2b dequant-GEMV+LoRA HBM GB/s (% of peak); MoE-block decode µs/token"
 HBM_PEAK_GBS = 8000.0
 POOL = 512
 K_, N_, BITS, GROUP, RANK, M_ = 2048, 1408, 2, 128, 64, 1
@@ -36,6 +46,19 @@ K_, N_, BITS, GROUP, RANK, M_ = 2048, 1408, 2, 128, 64, 1
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def layer_bytes(M=M_, K=K_, N=N_, bits=BITS, group=GROUP, rank=RANK):
+    from glorcq_amd import format as fmt
+
+    return fmt.algorithmic_bytes(M, K, N, bits, group, rank)
+
+
+def gemv_kernel_bytes(M=M_, K=K_, N=N_, bits=BITS, group=GROUP, rank=RANK):
+    """Bytes the GEMV kernel must move when a = x*U is given: codes, scales and
+    zeros, SV, x, y and a."""
+    G = K // group
+    return N * K * bits // 8 + 4 * N * G + 2 * rank * N + 2 * M * (K + N) + 2 * M * rank
 
 
 def make_pool(dev, pool, seed=1):
@@ -54,20 +77,21 @@ def make_pool(dev, pool, seed=1):
     return codes, scales, zeros, U, SV, x
 
 
-def time_launches(fn, steps, warmup):
-    """Mean ms per launch over `steps` back-to-back launches, HIP events on the
-    launch stream (torch's current stream, which the library launches on)."""
+def time_events(fn, steps, warmup):
+    """Mean ms per call of `fn` over `steps` back-to-back calls, HIP events
+    recorded on torch's current stream (the stream the library launches on)."""
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    start.record()
+    start.record(stream)
     for _ in range(steps):
         fn()
-    end.record()
+    end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
 
@@ -93,17 +117,48 @@ def cpu_baseline(gpu_y_config0, budget_s=12.0):
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
-    nbytes = fmt.algorithmic_bytes(M_, K_, N_, BITS, GROUP, RANK)
     parity = O.parity_ok(gpu_y_config0, ref)
     err = float((gpu_y_config0.float().cpu() - ref.float()).abs().max())
     return {
-        "value": round(nbytes / med / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-        "us_per_call": round(med * 1e6, 1),
+        "value": round(layer_bytes() / med / 1e9, 4), "unit": "GB/s", "cores": threads,
+        "kind": "port", "us_per_call": round(med * 1e6, 1),
         "sample": (f"{len(times)} config-0 calls (K=2048,N=1408,2-bit,g128,r64,M=1) of the "
                    f"reference CPU fallback restated in oracle/ (fp16 dequant loop + fp16 "
                    f"x@W.T + fp16 LoRA), median, torch threads={threads}, "
                    f"os.cpu_count()={os.cpu_count()}"),
     }, parity, err
+
+
+def read_traffic():
+    """HBM bytes per GEMV launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE scaled by a plain copy's reading), or None."""
+    path = os.path.join(ROOT, "profiles", "gemv_stream_pool512_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def pmc_workload():
+    """What the traffic profile runs: 5 launches of the GEMV kernel over the
+    pool (a given), then 5 plain device copies of 512 MiB."""
+    import torch
+
+    from glorcq_amd import kernels
+
+    dev = torch.device("cuda:0")
+    codes, scales, zeros, U, SV, x = make_pool(dev, POOL)
+    out = torch.empty(POOL, M_, N_, dtype=torch.float16, device=dev)
+    xu = kernels.lowrank_xu(x, U)
+    for _ in range(5):
+        kernels.packed_dequant_matmul_batched(x, codes, scales, zeros, BITS, GROUP, SV=SV, out=out,
+                                              precomputed_xU=xu)
+    src = torch.empty(512 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("pmc workload done", flush=True)
 
 
 def main():
@@ -113,11 +168,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--pool", type=int, default=POOL)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--pmc-workload", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build targets one GPU; --gpus must be 1 "
-                                   "(multi-GPU sharding is a design note, not built)"}))
+        print("bench.py: this build measures one GPU only (every box here has one); "
+              "multi-GPU sharding is described in DESIGN.md, not built. Use --gpus 1.",
+              file=sys.stderr)
         return 2
+    if args.pmc_workload:
+        pmc_workload()
+        return 0
 
     import torch
 
@@ -134,13 +194,32 @@ def main():
         kernels.packed_dequant_matmul_batched(x, codes, scales, zeros, BITS, GROUP, U=U, SV=SV,
                                               out=out)
 
-    log("timing pool launches")
-    ms = time_launches(step, args.steps, args.warmup)
-    per_layer = fmt.algorithmic_bytes(M_, K_, N_, BITS, GROUP, RANK)
-    launch_bytes = per_layer * args.pool
-    gbs = launch_bytes / (ms * 1e-3) / 1e9
+    log("timing steps (x*U partials + GEMV over the pool)")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    gbs = layer_bytes() * args.pool / (ms * 1e-3) / 1e9
 
-    # single-call latency, config 0 (one layer, one launch)
+    # dominant kernel alone, HIP events on the launch stream
+    xu = kernels.lowrank_xu(x, U)
+    out2 = torch.empty_like(out)
+
+    def gemv_only():
+        kernels.packed_dequant_matmul_batched(x, codes, scales, zeros, BITS, GROUP, SV=SV,
+                                              out=out2, precomputed_xU=xu)
+
+    log("timing the GEMV kernel alone")
+    k_ms = time_events(gemv_only, args.steps, args.warmup)
+    k_bytes = gemv_kernel_bytes() * args.pool
+    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
+    same = bool(torch.equal(out, out2))
+
+    # single-call latency, config 0 (one layer: both launches)
     p0 = fmt.make_linear(K_, N_, bits=BITS, group=GROUP, rank=RANK, M=M_, seed=0)
     d0 = [t.to(dev) for t in (p0.x, p0.codes, p0.scales, p0.zeros, p0.U, p0.SV)]
     y0 = torch.empty(M_, N_, dtype=torch.float16, device=dev)
@@ -150,17 +229,11 @@ def main():
                                             SV=d0[5], out=y0)
 
     log("timing single calls")
-    single_ms = time_launches(single, 200, 20)
+    single_ms = time_events(single, 200, 20)
     torch.cuda.synchronize()
 
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", "gemv_pool_traffic.json")
-    if os.path.exists(tf):
-        with open(tf) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
-
     result = {
-        "metric": "2b dequant-GEMV+LoRA HBM GB/s (% of peak); MoE-block decode us/token",
+        "metric": METRIC,
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -170,23 +243,25 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u2->f16 (fp32 accumulate)",
+        "dtype": "u2 codes -> f16 MFMA, f32 accumulate",
         "data": "synthetic (seeded random codes, scales, zeros, LoRA factors, activations)",
         "config": {
             "workload": (f"config 1 expert gate/up projection: {args.pool} distinct 2-bit "
-                         f"2048->1408 g128 r64 layers at M=1 in one fused launch (cold cache)"),
+                         f"2048->1408 g128 r64 layers at M=1, cold cache, one fused op "
+                         f"(x*U partials + GEMV with low-rank epilogue) per step"),
             "K": K_, "N": N_, "bits": BITS, "group": GROUP, "rank": RANK, "M": M_,
             "layers_per_step": args.pool,
         },
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "roofline": {
-            "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "glq::gemv_lora_kernel<2,4>",
-            "algorithmic_bytes_per_launch": launch_bytes,
+            "bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
+            "kernel": "glq::gemv_stream_dense_kernel<2,1,3,false,false>",
+            "kernel_avg_us": round(k_ms * 1e3, 2),
+            "algorithmic_bytes_per_launch": k_bytes,
         },
         "single_call_config0_us": round(single_ms * 1e3, 2),
-        "single_call_config0_GBs": round(per_layer / (single_ms * 1e-3) / 1e9, 1),
+        "gemv_alone_matches_step_output": same,
         "moe_block_decode_us_per_token": None,
     }
     if not args.no_cpu:

@@ -44,6 +44,13 @@ SIGNATURES = {
         _vp, _i64,                      # y, y_stride
         _vp, _i64, _vp,                 # workspace, bytes, stream
     ]),
+    "glq_lowrank_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "glq_lowrank_xu_batched": (_c_int, [
+        _i64, _vp, _i64, _i64, _i64,    # items, x, x_stride, M, K
+        _vp, _i64, _i64,                # U, u_stride, rank
+        _vp, _i64,                      # xu, xu_stride
+        _vp, _i64, _vp,                 # workspace, bytes, stream
+    ]),
     "glq_unpack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _c_int, _vp, _vp]),
     "glq_dequant_weight": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp, _i64, _c_int, _vp, _vp]),
     "glq_pack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp]),

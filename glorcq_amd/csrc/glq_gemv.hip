@@ -69,6 +69,7 @@ struct DenseSrc {
   }
 };
 
+template <int MC>
 __global__ __launch_bounds__(256) void lowrank_partial_kernel(DenseArgs a) {
   __shared__ float red[4 * 4 * 64];
   __shared__ __half xl[16 * kLowrankRows];
@@ -76,8 +77,25 @@ __global__ __launch_bounds__(256) void lowrank_partial_kernel(DenseArgs a) {
   const __half* X = a.x + (int64_t)item * a.x_es;
   const int K = a.sh.K;
   auto xrow = [&](int m) { return X + (int64_t)m * K; };
-  lowrank_partial(xrow, a.M, K, a.sh.rank, a.sh.rpad, a.u + (int64_t)item * a.u_es, p,
-                  (float*)a.apart + ((int64_t)item * a.P + p) * a.M * a.sh.rpad, red, xl);
+  lowrank_partial<MC>(xrow, a.M, K, a.sh.rank, a.sh.rpad, a.u + (int64_t)item * a.u_es, p,
+                      (float*)a.apart + ((int64_t)item * a.P + p) * a.M * a.sh.rpad, red, xl);
+}
+
+// a = fp16(sum over the P K-slices of the partials): items x M x rank.
+__global__ __launch_bounds__(256) void lowrank_finalize_kernel(const float* __restrict__ apart,
+                                                              int items, int P, int M, int rank,
+                                                              int rpad, __half* __restrict__ xu,
+                                                              int64_t xu_es) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per = (int64_t)M * rank;
+  if (idx >= items * per) return;
+  const int item = (int)(idx / per);
+  const int r = (int)(idx - item * per);
+  const int m = r / rank, j = r - m * rank;
+  const float* p = apart + ((int64_t)item * P * M + m) * rpad + j;
+  float sacc = 0.f;
+  for (int q = 0; q < P; ++q) sacc += p[(int64_t)q * M * rpad];
+  xu[(int64_t)item * xu_es + r] = __float2half(sacc);
 }
 
 template <int BITS, int T, int MP>
@@ -335,7 +353,10 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   GLQ_CHECK(items * a.tiles < (1ll << 31) && items * a.P < (1ll << 31), "too many workgroups");
   hipStream_t s = (hipStream_t)stream;
   if (need_partials) {
-    lowrank_partial_kernel<<<dim3((unsigned)(items * a.P)), dim3(256), 0, s>>>(a);
+    const dim3 grid((unsigned)(items * a.P));
+    if (M == 1) lowrank_partial_kernel<1><<<grid, dim3(256), 0, s>>>(a);
+    else if (M == 2) lowrank_partial_kernel<2><<<grid, dim3(256), 0, s>>>(a);
+    else lowrank_partial_kernel<4><<<grid, dim3(256), 0, s>>>(a);
     GLQ_LAUNCH_CHECK("lowrank_partial_kernel");
   }
   DenseStreamArgs sa;
@@ -397,6 +418,55 @@ int glq_gemv_lora_batched(int64_t items, const void* x, int64_t x_stride,
                    zeros, sz_stride, group, sym, U, u_stride, SV, sv_stride, rank,
                    xU, xu_stride, bias, bias_stride, y, y_stride, workspace,
                    workspace_bytes_given, stream);
+}
+
+int64_t glq_lowrank_workspace_bytes(int64_t items, int64_t M, int64_t K, int64_t rank) {
+  if (items < 0 || M < 0 || K < 0 || rank < 0) return -1;
+  return workspace_need(items, M, K, rank);
+}
+
+int glq_lowrank_xu_batched(int64_t items, const void* x, int64_t x_stride, int64_t M, int64_t K,
+                           const void* U, int64_t u_stride, int64_t rank, void* xu,
+                           int64_t xu_stride, void* workspace, int64_t workspace_bytes_given,
+                           void* stream) {
+  clear_error();
+  GLQ_CHECK(items >= 0 && M >= 0 && K >= 0 && rank >= 0, "negative size");
+  if (items == 0 || M == 0 || rank == 0) return GLQ_OK;
+  GLQ_CHECK(M <= 16, "takes 1 <= M <= 16 rows (got M=%lld)", (long long)M);
+  GLQ_CHECK(K > 0 && K < (1ll << 24), "bad K=%lld", (long long)K);
+  GLQ_CHECK(rank % 8 == 0 && rank <= 512, "rank=%lld must be a multiple of 8, <= 512",
+            (long long)rank);
+  GLQ_CHECK(x && U && xu, "null data pointer");
+  GLQ_CHECK(((uintptr_t)U & 15) == 0 && (items == 1 || u_stride % 8 == 0),
+            "U must be 16-byte aligned");
+  const int64_t need = workspace_need(items, M, K, rank);
+  GLQ_CHECK(workspace != nullptr && workspace_bytes_given >= need,
+            "workspace of %lld bytes needed (got %lld)", (long long)need,
+            (long long)workspace_bytes_given);
+  DenseArgs a = {};
+  a.u = (const __half*)U;
+  a.u_es = u_stride;
+  a.x = (const __half*)x;
+  a.x_es = x_stride;
+  a.apart = (const float*)workspace;
+  a.items = (int)items;
+  a.M = (int)M;
+  a.P = (int)lowrank_slices(K);
+  a.sh.K = (int)K;
+  a.sh.rank = (int)rank;
+  a.sh.rpad = (int)align_up(rank, 32);
+  GLQ_CHECK(items * a.P < (1ll << 31), "too many workgroups");
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)(items * a.P));
+  if (M == 1) lowrank_partial_kernel<1><<<grid, dim3(256), 0, s>>>(a);
+  else if (M == 2) lowrank_partial_kernel<2><<<grid, dim3(256), 0, s>>>(a);
+  else lowrank_partial_kernel<4><<<grid, dim3(256), 0, s>>>(a);
+  GLQ_LAUNCH_CHECK("lowrank_partial_kernel");
+  const int64_t n = items * M * rank;
+  lowrank_finalize_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(
+      a.apart, a.items, a.P, a.M, (int)rank, a.sh.rpad, (__half*)xu, xu_stride);
+  GLQ_LAUNCH_CHECK("lowrank_finalize_kernel");
+  return GLQ_OK;
 }
 
 }  // extern "C"

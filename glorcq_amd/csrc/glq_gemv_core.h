@@ -220,7 +220,7 @@ __device__ __forceinline__ void load_batch(u32x4 (&wv)[NB][T], const uint32_t* C
 // ---------------------------------------------------------------------------
 constexpr int kLowrankRows = 256;  // U rows per partial (K-slice)
 
-template <class XRow>
+template <int MC, class XRow>
 __device__ void lowrank_partial(const XRow& xrow, int M, int K, int rank, int rpad,
                                 const __half* __restrict__ U, int p,
                                 float* __restrict__ out /* M x rpad */,
@@ -246,24 +246,24 @@ __device__ void lowrank_partial(const XRow& xrow, int M, int K, int rank, int rp
       const int k = kr + 32 * i;
       u[i] = (jv && k < kl) ? *(const f16x8*)(U + (int64_t)(k0 + k) * rank + j) : f16x8{};
     }
-    for (int mb = 0; mb < M; mb += 4) {
-      float acc[4][8];
+    for (int mb = 0; mb < M; mb += MC) {
+      float acc[MC][8];
 #pragma unroll
-      for (int mm = 0; mm < 4; ++mm)
+      for (int mm = 0; mm < MC; ++mm)
 #pragma unroll
         for (int c = 0; c < 8; ++c) acc[mm][c] = 0.f;
 #pragma unroll
       for (int i = 0; i < RI; ++i) {
 #pragma unroll
-        for (int mm = 0; mm < 4; ++mm) {
+        for (int mm = 0; mm < MC; ++mm) {
           const int m = min(mb + mm, M - 1);
           const float xv = (float)xl[m * kLowrankRows + kr + 32 * i];
 #pragma unroll
-          for (int c = 0; c < 8; ++c) acc[mm][c] += xv * (float)u[i][c];
+          for (int c = 0; c < 8; ++c) acc[mm][c] = fmaf(xv, (float)u[i][c], acc[mm][c]);
         }
       }
 #pragma unroll
-      for (int mm = 0; mm < 4; ++mm)
+      for (int mm = 0; mm < MC; ++mm)
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
           float v = acc[mm][c];
@@ -274,14 +274,14 @@ __device__ void lowrank_partial(const XRow& xrow, int M, int K, int rank, int rp
         }
       if (lane < 8) {
 #pragma unroll
-        for (int mm = 0; mm < 4; ++mm)
+        for (int mm = 0; mm < MC; ++mm)
 #pragma unroll
           for (int c = 0; c < 8; ++c) red[(wave * 4 + mm) * 64 + 8 * lane + c] = acc[mm][c];
       }
       __syncthreads();
       {
         const int mm = tid >> 6, jj = tid & 63;
-        if (mb + mm < M && jb + jj < rpad) {
+        if (mm < MC && mb + mm < M && jb + jj < rpad) {
           const float s = red[(0 * 4 + mm) * 64 + jj] + red[(1 * 4 + mm) * 64 + jj] +
                           red[(2 * 4 + mm) * 64 + jj] + red[(3 * 4 + mm) * 64 + jj];
           out[(mb + mm) * rpad + jb + jj] = s;

@@ -153,7 +153,8 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
                                   sym: bool = False, U: torch.Tensor | None = None,
                                   SV: torch.Tensor | None = None,
                                   bias: torch.Tensor | None = None,
-                                  out: torch.Tensor | None = None) -> torch.Tensor:
+                                  out: torch.Tensor | None = None,
+                                  precomputed_xU: torch.Tensor | None = None) -> torch.Tensor:
     """E independent problems in one launch: x (E, M, K), codes (E, N, Kw),
     scales/zeros (E, N, G), U (E, K, r), SV (E, N, r), bias (E, N) -> (E, M, N).
 
@@ -175,23 +176,63 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
     rank = 0
     if SV is not None:
         _require(SV, "SV", torch.float16)
-        _require(U, "U", torch.float16)
         rank = SV.shape[2]
+        if precomputed_xU is not None:
+            _require(precomputed_xU, "precomputed_xU", torch.float16)
+            if tuple(precomputed_xU.shape) != (E, M, rank):
+                raise RuntimeError("precomputed_xU must be (E, M, r)")
+        else:
+            _require(U, "U", torch.float16)
     if bias is not None:
         _require(bias, "bias", torch.float16)
     if out is None:
         out = torch.empty(E, M, N, dtype=torch.float16, device=x.device)
     if E == 0 or M == 0 or N == 0:
         return out
-    nbytes = lib.glq_gemv_workspace_bytes(E, M, K, N, rank)
+    xu = precomputed_xU if SV is not None else None
+    nbytes = lib.glq_gemv_workspace_bytes(E, M, K, N, rank if xu is None else 0)
     ws = workspace(x.device, nbytes)
     rc = lib.glq_gemv_lora_batched(
         E, x.data_ptr(), M * K, M, K, N, codes.data_ptr(), codes.shape[1] * codes.shape[2],
         bits, scales.data_ptr(), _lib.ptr(zeros), scales.shape[1] * scales.shape[2],
-        groupsize, int(bool(sym)), _lib.ptr(U), K * rank, _lib.ptr(SV), N * rank, rank,
-        None, 0, _lib.ptr(bias), N, out.data_ptr(), M * N, ws.data_ptr(), ws.numel(),
-        _lib.stream_handle(x.device))
+        groupsize, int(bool(sym)), _lib.ptr(U if xu is None else None), K * rank, _lib.ptr(SV),
+        N * rank, rank, _lib.ptr(xu), M * rank, _lib.ptr(bias), N, out.data_ptr(), M * N,
+        ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device))
     _lib.check(rc, "glq_gemv_lora_batched")
+    return out
+
+
+def lowrank_xu(x: torch.Tensor, U: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """a = fp16(x U) on the GPU (fp32 accumulation): x (M, K) or (E, M, K) fp16,
+    U (K, r) or (E, K, r) fp16 -> (M, r) or (E, M, r).  A 2-D x with a 3-D U
+    applies the one x to every U (the cluster-shared x*U of the MoE block,
+    inference/moe_block.py:290-322)."""
+    lib = _lib.load()
+    _require(x, "x", torch.float16)
+    _require(U, "U", torch.float16)
+    batched = U.dim() == 3
+    E = U.shape[0] if batched else 1
+    K, r = U.shape[-2], U.shape[-1]
+    if x.dim() == 3:
+        if not batched or x.shape[0] != E:
+            raise RuntimeError("x (E, M, K) needs U (E, K, r)")
+        M, x_stride = x.shape[1], x.shape[1] * K
+    else:
+        M, x_stride = x.shape[0], 0
+    if x.shape[-1] != K:
+        raise RuntimeError(f"x has K={x.shape[-1]}, U has K={K}")
+    shape = (E, M, r) if batched else (M, r)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.float16, device=x.device)
+    elif tuple(out.shape) != shape:
+        raise RuntimeError(f"out must be {shape}")
+    if M == 0 or E == 0:
+        return out
+    nbytes = lib.glq_lowrank_workspace_bytes(E, M, K, r)
+    ws = workspace(x.device, nbytes)
+    _lib.check(lib.glq_lowrank_xu_batched(E, x.data_ptr(), x_stride, M, K, U.data_ptr(), K * r, r,
+                                          out.data_ptr(), M * r, ws.data_ptr(), ws.numel(),
+                                          _lib.stream_handle(x.device)), "glq_lowrank_xu_batched")
     return out
 
 
@@ -270,5 +311,5 @@ def _unpack_indices_2bit(packed: torch.Tensor, K: int) -> torch.Tensor:
 __all__ = [
     "is_gptq_cuda_available", "is_cuda_available", "packed_dequant_matmul_fused",
     "packed_dequant_matmul_batched", "gptq_dequant_matmul_fused", "unpack_codes",
-    "dequant_weight", "pack_codes_device", "pack_codes", "workspace",
+    "dequant_weight", "pack_codes_device", "pack_codes", "workspace", "lowrank_xu",
 ]

@@ -105,6 +105,23 @@ int glq_gemv_lora_batched(int64_t items, const void* x, int64_t x_stride,
                           void* stream);
 
 /*
+ * Low-rank factor a = fp16(x U) for `items` problems: x (M, K) fp16 at
+ * x + i*x_stride, U (K, rank) fp16 at U + i*u_stride, a (M, rank) fp16
+ * written at xu + i*xu_stride (fp32 accumulation, one rounding).  This is the
+ * reference's `x @ U` (inference/quantized_linear.py:344) and the
+ * cluster-shared precompute `_precompute_xU_for_experts`
+ * (inference/moe_block.py:290-322): pass x_stride = 0 to apply one x to
+ * several clusters' U.  Two launches: K-sliced fp32 partial sums into the
+ * workspace (glq_lowrank_workspace_bytes), then a summing kernel.  Feed the
+ * result to glq_gemv_lora*(xU=...).
+ */
+int64_t glq_lowrank_workspace_bytes(int64_t items, int64_t M, int64_t K, int64_t rank);
+int glq_lowrank_xu_batched(int64_t items, const void* x, int64_t x_stride, int64_t M, int64_t K,
+                           const void* U, int64_t u_stride, int64_t rank, void* xu,
+                           int64_t xu_stride, void* workspace, int64_t workspace_bytes,
+                           void* stream);
+
+/*
  * Debug: unpack codes (N, K*bits/32) int32 -> (N, K) int32.  Codes are
  * returned unsigned (0..2^b-1), or sign-extended when sym != 0.
  * Replaces _unpack_indices (inference/quantized_linear.py:115-146) and

@@ -296,3 +296,35 @@ def test_stream_bias_odd_tiles_sym(gpu, bits):
                                            None if sym else d["zeros"], bits, 128, sym=sym,
                                            U=d["U"], SV=d["SV"], bias=bias.to(gpu))
         assert_parity(y, oracle_y(p, bias=bias), f"stream bias sym={sym}")
+
+
+@pytest.mark.parametrize("E,M,K,r,shared_x", [(1, 1, 2048, 64, False), (5, 3, 1408, 64, False),
+                                              (16, 4, 2048, 64, True), (3, 16, 5632, 128, False),
+                                              (2, 2, 256, 8, True)])
+def test_lowrank_xu(gpu, E, M, K, r, shared_x):
+    """a = fp16(x U) with fp32 accumulation (reference `x @ U`,
+    inference/quantized_linear.py:344; cluster-shared form with one x,
+    inference/moe_block.py:290-322) against the fp64 product."""
+    g = torch.Generator().manual_seed(E * 100 + K)
+    U = (torch.randn(E, K, r, generator=g) * 0.01).half()
+    x = torch.randn(M, K, generator=g).half() if shared_x else torch.randn(E, M, K, generator=g).half()
+    a = K_.lowrank_xu(x.to(gpu), U.to(gpu)).cpu()
+    xd = x.double() if not shared_x else x.double().unsqueeze(0).expand(E, M, K)
+    ref = xd @ U.double()
+    # one fp16 rounding of an fp32 sum: |err| <= 2^-11 |a| + tiny
+    assert a.shape == (E, M, r)
+    err = (a.double() - ref).abs()
+    assert bool((err <= 1e-3 * ref.abs() + 1e-4).all()), float(err.max())
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_batched_precomputed_xu(gpu, bits):
+    """Batched GEMV fed a = lowrank_xu(x, U) equals the oracle with that a."""
+    E, M, K, N, r = 4, 2, 2048, 1408, 64
+    ps = [fmt.make_linear(K, N, bits=bits, rank=r, M=M, seed=300 + e) for e in range(E)]
+    st = lambda k: torch.stack([getattr(p, k) for p in ps]).to(gpu)  # noqa: E731
+    xu = K_.lowrank_xu(st("x"), st("U"))
+    y = K_.packed_dequant_matmul_batched(st("x"), st("codes"), st("scales"), st("zeros"), bits,
+                                         128, SV=st("SV"), precomputed_xU=xu)
+    for e, p in enumerate(ps):
+        assert_parity(y[e], oracle_y(p, xu=xu[e].cpu()), f"item {e}")
