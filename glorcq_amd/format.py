@@ -106,3 +106,114 @@ def algorithmic_bytes(M: int, K: int, N: int, bits: int, group: int, rank: int) 
 
 def algorithmic_flops(M: int, K: int, N: int, rank: int) -> int:
     return 2 * M * (N * K + rank * (K + N))
+
+
+# ---------------------------------------------------------------------------
+# MoE block (BASELINE config 2 shape: Qwen1.5-MoE-A2.7B decode)
+# ---------------------------------------------------------------------------
+PROJS = ("gate", "up", "down")
+
+
+@dataclass
+class QMat:
+    """Packed group-quantized weights of E (or 1) matrices (N, K)."""
+
+    codes: torch.Tensor    # (E, N, K*bits/32) int32
+    scales: torch.Tensor   # (E, N, G) fp16
+    zeros: torch.Tensor    # (E, N, G) fp16
+    bits: int
+    group: int
+
+    @property
+    def N(self) -> int:
+        return self.codes.shape[1]
+
+    @property
+    def K(self) -> int:
+        return self.codes.shape[2] * (32 // self.bits)
+
+
+@dataclass
+class MoEProblem:
+    """One Qwen2-MoE style block: router, E routed SwiGLU experts with
+    cluster-shared LoRA U (input side) and per-expert SV, a 4-bit shared expert
+    (no LoRA) with a sigmoid gate, and B tokens of hidden state."""
+
+    H: int
+    E: int
+    inter: int
+    top_k: int
+    norm_topk_prob: bool
+    rank: int
+    n_clusters: int
+    router_w: torch.Tensor         # (E, H) fp16
+    shared_gate_w: torch.Tensor    # (1, H) fp16
+    experts: dict                  # proj -> QMat (E, N, .)
+    SV: dict                       # proj -> (E, N, r) fp16
+    cluster_of: dict               # proj -> (E,) int64
+    U: dict                        # proj -> (C, K, r) fp16
+    shared: dict                   # proj -> QMat (1, N, .)
+    h: torch.Tensor                # (B, H) fp16
+
+    @property
+    def B(self) -> int:
+        return self.h.shape[0]
+
+
+def _rand_qmat(g, E, N, K, bits, group) -> QMat:
+    """Uniform codes drawn as random packed words (every code uniform over
+    0..2^b-1), |N(0,0.02)| fp16 scales, zero-points uniform over {1, 2}."""
+    G = K // group
+    words = torch.randint(-(2**31), 2**31 - 1, (E, N, K * bits // 32), generator=g,
+                          dtype=torch.int64).to(torch.int32)
+    scales = (torch.randn(E, N, G, generator=g) * 0.02).abs().half()
+    zeros = torch.randint(1, 3, (E, N, G), generator=g, dtype=torch.int32).half()
+    return QMat(codes=words, scales=scales, zeros=zeros, bits=bits, group=group)
+
+
+def make_moe(H=2048, E=60, inter=1408, top_k=4, n_clusters=16, rank=64, shared_inter=5632,
+             B=1, bits=2, shared_bits=4, group=128, norm_topk_prob=False,
+             seed=0) -> MoEProblem:
+    """Seeded MoE block in a fixed draw order (one CPU generator):
+    router W (E,H) N(0,0.02); shared-expert gate w (1,H) N(0,0.02); then for
+    proj in (gate, up, down): cluster assignment randint(0, C, (E,)), U (C,K,r)
+    N(0,0.01), expert weights (codes, scales, zeros as in make_linear), SV
+    (E,N,r) N(0,0.01); then the shared expert's gate, up, down weights
+    (shared_bits, no LoRA); then h (B,H) N(0,1).  All fp32 draws rounded to fp16.
+    Defaults are BASELINE config 2 (Qwen1.5-MoE-A2.7B)."""
+    g = torch.Generator().manual_seed(seed)
+    router_w = (torch.randn(E, H, generator=g) * 0.02).half()
+    shared_gate_w = (torch.randn(1, H, generator=g) * 0.02).half()
+    dims = {"gate": (H, inter), "up": (H, inter), "down": (inter, H)}
+    experts, SV, cluster_of, U = {}, {}, {}, {}
+    for proj in PROJS:
+        K, N = dims[proj]
+        cluster_of[proj] = torch.randint(0, n_clusters, (E,), generator=g)
+        U[proj] = (torch.randn(n_clusters, K, rank, generator=g) * 0.01).half()
+        experts[proj] = _rand_qmat(g, E, N, K, bits, group)
+        SV[proj] = (torch.randn(E, N, rank, generator=g) * 0.01).half()
+    sdims = {"gate": (H, shared_inter), "up": (H, shared_inter), "down": (shared_inter, H)}
+    shared = {proj: _rand_qmat(g, 1, sdims[proj][1], sdims[proj][0], shared_bits, group)
+              for proj in PROJS}
+    h = torch.randn(B, H, generator=g).half()
+    return MoEProblem(H=H, E=E, inter=inter, top_k=top_k, norm_topk_prob=norm_topk_prob,
+                      rank=rank, n_clusters=n_clusters, router_w=router_w,
+                      shared_gate_w=shared_gate_w, experts=experts, SV=SV,
+                      cluster_of=cluster_of, U=U, shared=shared, h=h)
+
+
+def moe_step_bytes(p: MoEProblem, active_experts: int, active_clusters: dict) -> int:
+    """Algorithmic HBM bytes of one decode step: the active experts' three
+    projections (codes, scales+zeros, SV), the active clusters' U, the shared
+    expert, the router and shared-gate weights, hidden state in and out."""
+    total = 0
+    for proj in PROJS:
+        q = p.experts[proj]
+        per = q.N * q.K * q.bits // 8 + 4 * q.N * (q.K // q.group) + 2 * q.N * p.rank
+        total += active_experts * per
+        total += active_clusters[proj] * 2 * q.K * p.rank
+        s = p.shared[proj]
+        total += s.N * s.K * s.bits // 8 + 4 * s.N * (s.K // s.group)
+    total += 2 * (p.E + 1) * p.H
+    total += 2 * 2 * p.B * p.H
+    return total

@@ -206,3 +206,115 @@ def parity_ok(y: torch.Tensor, ref: torch.Tensor, rtol: float = 1e-2, atol: floa
     y = y.double().cpu()
     ref = ref.double().cpu()
     return bool(((y - ref).abs() <= atol + rtol * ref.abs()).all())
+
+
+# ---------------------------------------------------------------------------
+# MoE block (GraphCompatibleMoeBlock.forward, inference/moe_block.py:381-436,
+# with the sparse dispatch of _forward_sparse :704-740 / the HF-style
+# GLoRCQExperts.forward, inference/quantized_linear.py:395-428)
+# ---------------------------------------------------------------------------
+def route(h: torch.Tensor, router_w: torch.Tensor, top_k: int, norm_topk_prob: bool):
+    """Router (moe_block.py:386-392): logits = gate(h) in fp16, softmax in fp32,
+    torch.topk, optional renormalisation, cast to fp16.
+    Returns (fp16 logits (B,E), fp16 weights (B,k), int64 experts (B,k))."""
+    logits = h.half() @ router_w.half().T
+    rw = torch.softmax(logits.float(), dim=1)
+    w, sel = torch.topk(rw, top_k, dim=-1)
+    if norm_topk_prob:
+        w = w / w.sum(dim=-1, keepdim=True)
+    return logits, w.half(), sel
+
+
+def _qmat_linear(x, q, e, exact, U=None, SV=None, a=None):
+    """y = x @ W_e^T (+ a @ SV_e^T, a = fp16(x @ U) unless given) for expert e of
+    a format.QMat.  exact=False: the reference's fp16 CPU fallback (fp16 dequant,
+    fp16 matmuls, quantized_linear.py:286-355); exact=True: fp64 sums of the
+    exact weights s*(q - z), with a rounded to fp16 as the reference does."""
+    codes = q.codes[e].numpy()
+    qi = torch.from_numpy(unpack_codes(codes, q.bits, q.K))
+    if exact:
+        W = dequant_fp32(qi, q.scales[e], q.zeros[e], q.group).double()
+        y = x.double() @ W.T
+        if SV is not None:
+            if a is None:
+                a = (x.double() @ U.double()).half()
+            y = y + a.double() @ SV.double().T
+        return y
+    W = dequant_fp16(qi, q.scales[e], q.zeros[e], q.group)
+    y = x.half() @ W.T
+    if SV is not None:
+        if a is None:
+            a = x.half() @ U.half()
+        y = y + a.half() @ SV.half().T
+    return y
+
+
+def moe_forward(p, exact: bool = True, h: torch.Tensor | None = None, dense: bool = False,
+                cluster_shared: bool = True):
+    """MoE block output (B, H) for format.MoEProblem p.
+
+    Rounding points kept from the reference in both modes: routing weights,
+    the cluster-shared a = fp16(h @ U_c) (_precompute_xU_for_experts,
+    moe_block.py:290-322), inter = fp16(silu(gate) * up) (act_fn on fp16,
+    :465-468), the down projection's own a = fp16(inter @ U_down), the shared
+    gate fp16(sigmoid(h @ w_sg)) (:429-433).  exact=True sums in fp64;
+    exact=False reproduces the reference's fp16 CPU arithmetic, including the
+    fp16 index_add accumulation in expert order.
+    dense=True evaluates every expert with weight 0 for the unselected ones (the
+    graph-mode identity the reference relies on, moe_block.py:11-13).
+    cluster_shared=False computes x @ U per expert instead of per cluster
+    (test_cluster_parallel.py:159 asserts the two agree)."""
+    h = p.h if h is None else h
+    B, H = h.shape
+    _, w, sel = route(h, p.router_w, p.top_k, p.norm_topk_prob)
+    acc_dtype = torch.float64 if exact else torch.float16
+    final = torch.zeros(B, H, dtype=acc_dtype)
+    xu = {}
+    for proj in ("gate", "up"):
+        for c in range(p.n_clusters):
+            xu[(proj, c)] = (h.double() @ p.U[proj][c].double()).half() if exact \
+                else h.half() @ p.U[proj][c].half()
+    experts = range(p.E) if dense else sorted(set(sel.flatten().tolist()))
+    for e in experts:
+        tok_pos = [(t, k) for t in range(B) for k in range(p.top_k) if int(sel[t, k]) == e]
+        toks = [t for t, _ in tok_pos] if tok_pos else []
+        if dense:
+            toks = list(range(B))
+        if not toks:
+            continue
+        x = h[toks]
+        outs = {}
+        for proj in ("gate", "up"):
+            c = int(p.cluster_of[proj][e])
+            a = xu[(proj, c)][toks] if cluster_shared else None
+            outs[proj] = _qmat_linear(x, p.experts[proj], e, exact, U=p.U[proj][c],
+                                      SV=p.SV[proj][e], a=a)
+        g, u = outs["gate"], outs["up"]
+        if exact:
+            inter = (torch.nn.functional.silu(g.half().float()).half().double() *
+                     u.half().double()).half()
+        else:
+            inter = torch.nn.functional.silu(g.half()) * u.half()
+        cd = int(p.cluster_of["down"][e])
+        y = _qmat_linear(inter, p.experts["down"], e, exact, U=p.U["down"][cd],
+                         SV=p.SV["down"][e])
+        wt = torch.zeros(len(toks), dtype=torch.float16)
+        for i, t in enumerate(toks):
+            for k in range(p.top_k):
+                if int(sel[t, k]) == e:
+                    wt[i] = w[t, k]
+        if exact:
+            final.index_add_(0, torch.tensor(toks), y * wt.double()[:, None])
+        else:
+            final.index_add_(0, torch.tensor(toks), (y.half() * wt[:, None]).half())
+    # shared expert (4-bit, no LoRA) with the sigmoid gate
+    sg = torch.sigmoid((h.half() @ p.shared_gate_w.half().T).float()).half()
+    sgu = {proj: _qmat_linear(h, p.shared[proj], 0, exact) for proj in ("gate", "up")}
+    if exact:
+        sinter = (torch.nn.functional.silu(sgu["gate"].half().float()).half().double() *
+                  sgu["up"].half().double()).half()
+        sd = _qmat_linear(sinter, p.shared["down"], 0, exact)
+        return final + sd.half().double() * sg.double()
+    sinter = torch.nn.functional.silu(sgu["gate"].half()) * sgu["up"].half()
+    sd = _qmat_linear(sinter, p.shared["down"], 0, exact).half()
+    return final + (sg * sd).half()
