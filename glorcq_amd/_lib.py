@@ -19,6 +19,23 @@ _c_int = ctypes.c_int
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
 
+
+
+class MoeParams(ctypes.Structure):
+    """glq_moe_params (include/glorcq_hip.h), field for field."""
+    _fields_ = [
+        ("tokens", _i64), ("hidden", _i64), ("experts", _i64), ("inter", _i64),
+        ("top_k", _i64), ("n_clusters", _i64), ("rank", _i64), ("shared_inter", _i64),
+        ("norm_topk_prob", ctypes.c_int32), ("bits", ctypes.c_int32),
+        ("shared_bits", ctypes.c_int32), ("group", ctypes.c_int32),
+        ("h", _vp), ("router_w", _vp), ("shared_gate_w", _vp),
+        ("codes", _vp * 3), ("scales", _vp * 3), ("zeros", _vp * 3),
+        ("U", _vp * 3), ("cluster_of", _vp * 3), ("SV", _vp * 3),
+        ("shared_codes", _vp * 3), ("shared_scales", _vp * 3), ("shared_zeros", _vp * 3),
+        ("out", _vp), ("router_logits", _vp),
+    ]
+
+
 # name -> (restype, argtypes); must match include/glorcq_hip.h exactly.
 SIGNATURES = {
     "glq_version": (_c_int, []),
@@ -51,6 +68,8 @@ SIGNATURES = {
         _vp, _i64,                      # xu, xu_stride
         _vp, _i64, _vp,                 # workspace, bytes, stream
     ]),
+    "glq_moe_workspace_bytes": (_i64, [ctypes.POINTER(MoeParams)]),
+    "glq_moe_decode": (_c_int, [ctypes.POINTER(MoeParams), _vp, _i64, _vp]),
     "glq_unpack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _c_int, _vp, _vp]),
     "glq_dequant_weight": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp, _i64, _c_int, _vp, _vp]),
     "glq_pack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp]),

@@ -57,6 +57,11 @@ struct DenseSrc {
   __device__ const __half* bias(int item) const {
     return a.bias ? a.bias + (int64_t)item * a.bias_es : nullptr;
   }
+  __device__ StreamMat mat(int item, int) const {
+    return StreamMat{codes(item), scales(item), a.sh.sym ? scales(item) : zeros(item), sv(item),
+                     bias(item)};
+  }
+  __device__ __half load_a(int item, int, int m, int j) const { return load_a(item, m, j); }
   __device__ __half load_a(int item, int m, int j) const {
     if (a.xu) return a.xu[(int64_t)item * a.xu_es + (int64_t)m * a.sh.rank + j];
     const float* p = a.apart + ((int64_t)item * a.P * a.M + m) * a.sh.rpad + j;
@@ -117,7 +122,7 @@ __global__ __launch_bounds__(256) void gemv_stream_dense_kernel(DenseStreamArgs 
   extern __shared__ __align__(16) unsigned char smem[];
   const int item = blockIdx.x / sa.wpi, wg = blockIdx.x - item * sa.wpi;
   const int t0 = wg * sa.tpw, t1 = min(sa.ss.tiles, t0 + sa.tpw);
-  gemv_stream<BITS, MP, D, SYM, SZ2>(DenseSrc{sa.a}, sa.ss, item, t0, t1, smem);
+  gemv_stream<BITS, MP, D, SYM, SZ2, 1>(DenseSrc{sa.a}, sa.ss, item, t0, t1, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -149,16 +154,6 @@ int64_t gemv_phase_len(int64_t M, int64_t K, int64_t group, int bits) {
 
 size_t gemv_lds_bytes(const TileShape& sh, int T) {
   return (size_t)lds_layout(sh.mmax, sh.kp, sh.kp / sh.group, T, sh.xstride, sh.apad).total;
-}
-
-template <class KernelFn>
-static int set_lds_limit(KernelFn fn, size_t lds, size_t& attr_bytes) {
-  if (lds > attr_bytes) {
-    GLQ_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds));
-    attr_bytes = lds;
-  }
-  return GLQ_OK;
 }
 
 template <int BITS, int T, int MP>
@@ -236,12 +231,15 @@ bool stream_shape(int64_t M, const TileShape& sh, int bits, StreamShape& ss, siz
   ss.nchunk = (int)(((int64_t)sh.kw * 4 + 127) / 128);
   ss.nsvc = sh.rank > 0 ? (sh.rank + 63) / 64 : 0;
   ss.tiles = (sh.N + 15) / 16;
-  ss.xstride = stream_kpad(sh.K) + 8;
+  ss.xstride = stream_kpad(sh.K, bits) + 8;
   ss.mmax = (int)M;
   ss.apad = 64 * (ss.nsvc > 0 ? ss.nsvc : 1) + 8;
+  ss.goff = 0;
+  ss.gend = sh.G;
+  ss.rowlast = sh.kw * 4 - 16;
   sz2 = bits == 2 && (sh.G % 2) != 0;
   const int slot = kStreamCodeBytes + (sz2 ? 512 : 256);
-  lds = (size_t)stream_lds(kStreamDepth, slot, (int)M, sh.K, ss.xstride, ss.apad).total;
+  lds = (size_t)stream_lds(kStreamDepth, slot, (int)M, sh.K, bits, ss.xstride, ss.apad).total;
   return lds <= (size_t)kMaxLds;
 }
 

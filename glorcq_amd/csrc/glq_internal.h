@@ -49,4 +49,16 @@ void clear_error();
 
 namespace glq {
 inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+// Raises a kernel's dynamic-LDS limit to `lds` bytes once (attr_bytes caches
+// the limit already set for that kernel).
+template <class KernelFn>
+int set_lds_limit(KernelFn fn, size_t lds, size_t& attr_bytes) {
+  if (lds > attr_bytes) {
+    GLQ_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+    attr_bytes = lds;
+  }
+  return GLQ_OK;
+}
 }  // namespace glq

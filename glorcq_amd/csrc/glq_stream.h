@@ -66,28 +66,54 @@ struct StreamShape {
   int xstride;     // halves per staged token row of x
   int mmax;        // largest M of any item
   int apad;        // halves per token row of staged a
+  // K sub-range of a work unit (the whole row for a plain GEMV): the unit's
+  // codes, scales and x start `goff` groups into the row; `gend` groups are
+  // left from there to the row end; `rowlast` = bytes from the unit's first
+  // code byte to the last 16-byte piece of the row.
+  int goff, gend, rowlast;
 };
 
 struct StreamLds {
-  int xs, xc, a, ring, total;  // byte offsets; xc = [chunk128][16 tokens] x 2 floats
+  // byte offsets; xc = [chunk128][16 tokens] x 2 floats; tl / pl: per-wave
+  // inter tile and low-rank partials of the two-matrix form (else empty)
+  int xs, xc, a, ring, tl, pl, total;
 };
 
-// x rows are padded to a multiple of 256 codes (zeros); lanes without a token
-// read a 512-byte zero block instead (their per-step x stride is 0); the
-// per-chunk sums get matching zero padding.
-__host__ __device__ inline int stream_kpad(int K) { return (K + 255) / 256 * 256; }
+// x rows are staged zero-padded over every code position the row's chunks
+// cover (a chunk is 128 bytes of a weight row: 512 codes at 2 bits, 256 at 4),
+// so the MFMA steps of a partial last chunk read zeros, never unwritten LDS
+// (0 * NaN would survive the zero scale of such a step).  Lanes without a
+// token read a 512-byte zero block instead (their per-step x stride is 0);
+// the per-128-code sums get matching zero padding.
+__host__ __device__ inline int stream_kpad(int K, int bits) {
+  const int unit = bits == 2 ? 512 : 256;
+  return (K + unit - 1) / unit * unit;
+}
 
-__host__ __device__ inline StreamLds stream_lds(int D, int slot, int mmax, int K, int xstride,
-                                                int apad) {
+__host__ __device__ inline StreamLds stream_lds(int D, int slot, int mmax, int K, int bits,
+                                                int xstride, int apad, int nmat = 1,
+                                                int postcols = 0) {
   StreamLds L;
   int o = 0;
   L.xs = o;   o += al16(mmax * xstride * 2) + 512;  // + zero block read by masked lanes
-  L.xc = o;   o += al16((stream_kpad(K) / 128) * 32 * 4);
-  L.a = o;    o += al16(16 * apad * 2);
+  L.xc = o;   o += al16((stream_kpad(K, bits) / 128) * 32 * 4);
+  L.a = o;    o += al16(nmat * 16 * apad * 2);
   L.ring = o; o += 4 * D * slot;
+  L.tl = o;   o += nmat == 2 ? 4 * 16 * 16 * 4 : 0;
+  L.pl = o;   o += 4 * mmax * postcols * 4;
   L.total = o;
   return L;
 }
+
+// Pointers of one weight matrix of a work unit, already offset to the unit's
+// K range (codes by goff*128 codes, scales/zero-points by goff groups).
+struct StreamMat {
+  const uint32_t* C;
+  const __half* S;
+  const __half* Z;   // == S for symmetric codes
+  const __half* SV;  // nullptr: no low-rank term
+  const __half* B;   // bias or nullptr
+};
 
 // Per-tile load addresses of one lane (see StreamCursor::retarget).
 struct IssuePtrs {
@@ -107,9 +133,9 @@ struct StreamCursor {
   IssuePtrs P;
 
   // Recomputes this lane's row pointers for the tile at row r0 (once per tile).
-  __device__ __forceinline__ void retarget(const uint32_t* C, const __half* S, const __half* Zs,
-                                           const __half* SV, const __half* B,
-                                           const StreamShape& sh, int lane) {
+  __device__ __forceinline__ void retarget(const StreamMat& m, const StreamShape& sh, int lane) {
+    const uint32_t* C = m.C;
+    const __half *S = m.S, *Zs = m.Z, *SV = m.SV, *B = m.B;
     const int64_t rowbytes = (int64_t)sh.kw * 4;
 #pragma unroll
     for (int I = 0; I < 2; ++I) {
@@ -139,19 +165,20 @@ struct StreamCursor {
 //   2-bit, even G: lane q -> (q<32 ? s : z), row (q%32)/2, groups 4ch+2(q%2)+{0,1}
 //   2-bit, odd G (SZ2): lane q -> row q/4, group 4ch+q%4; s then z instruction
 //   4-bit: lane q -> (q<32 ? s : z), row (q%32)/2, group 2ch+q%2
-// N is even (host check), so every dword lies inside its tensor.
+// N is even (host check), so every dword lies inside its tensor.  Groups past
+// the unit's K range read valid neighbours (scale forced to 0 on use).
 template <int BITS, bool SZ2>
 __device__ __forceinline__ void stream_issue(const IssuePtrs& P, const StreamShape& sh, int ch,
                                              unsigned char* slot, int lane, int piece0,
                                              int piece1) {
-  const int rowlast = sh.kw * 4 - 16;
+  const int rowlast = sh.rowlast;
   __builtin_amdgcn_global_load_lds((const void*)(P.code[0] + min(128 * ch + piece0, rowlast)),
                                    (lds_void*)slot, 16, 0, 0);
   __builtin_amdgcn_global_load_lds((const void*)(P.code[1] + min(128 * ch + piece1, rowlast)),
                                    (lds_void*)(slot + 1024), 16, 0, 0);
   unsigned char* szs = slot + kStreamCodeBytes;
   if constexpr (BITS == 2 && SZ2) {
-    const int g = min(4 * ch + (lane & 3), sh.G - 1);
+    const int g = min(4 * ch + (lane & 3), sh.gend - 1);
     // element row*G + g rounded down to even: the row base parity is folded
     // in by the pointer (row*G may be odd), so round the absolute address
     const uintptr_t sa = ((uintptr_t)(P.s + 2 * g)) & ~(uintptr_t)3;
@@ -159,10 +186,10 @@ __device__ __forceinline__ void stream_issue(const IssuePtrs& P, const StreamSha
     __builtin_amdgcn_global_load_lds((const void*)sa, (lds_void*)szs, 4, 0, 0);
     __builtin_amdgcn_global_load_lds((const void*)za, (lds_void*)(szs + 256), 4, 0, 0);
   } else if constexpr (BITS == 2) {
-    const int g = min(4 * ch + 2 * (lane & 1), sh.G - 2);  // even: G is even here
+    const int g = min(4 * ch + 2 * (lane & 1), sh.gend - 2);  // even: G, goff even here
     __builtin_amdgcn_global_load_lds((const void*)(P.s + 2 * g), (lds_void*)szs, 4, 0, 0);
   } else {
-    const int g = min(2 * ch + (lane & 1), sh.G - 1);
+    const int g = min(2 * ch + (lane & 1), sh.gend - 1);
     const uintptr_t sa = ((uintptr_t)(P.s + 2 * g)) & ~(uintptr_t)3;
     __builtin_amdgcn_global_load_lds((const void*)sa, (lds_void*)szs, 4, 0, 0);
   }
@@ -243,7 +270,7 @@ __device__ __forceinline__ void stream_consume(const unsigned char* slot, int ch
     const float sc = gv ? half_of(sw_, 16 * cpar) : 0.f;
     float zc = (float)(1 << (BITS - 1));
     if constexpr (!SYM) zc = half_of(*(const uint32_t*)(sz + ln.cszb + ln.czoff), 16 * cpar);
-    const int gi = min(g, (stream_kpad(sh.K) >> 7) - 1);
+    const int gi = min(g, (stream_kpad(sh.K, BITS) >> 7) - 1);
     const float c1 = xc[gi * 32 + li], c2 = xc[gi * 32 + 16 + li];
     corr = mfma_16x16x4f32(c1, -sc, corr);
     corr = mfma_16x16x4f32(c2, -sc * zc, corr);
@@ -283,30 +310,106 @@ __device__ __forceinline__ void stream_consume(const unsigned char* slot, int ch
   }
 }
 
-// One workgroup: tiles [t0, t1) of one item; wave w takes t0 + w, t0 + w + 4, ...
-template <int BITS, int MP, int D, bool SYM, bool SZ2, class Src>
+// Post chunk of the two-matrix form: lane j accumulates, for every token m of
+// the unit, sum_n inter[m][n] * Upost[n][64q + j] over the tile's 16 rows
+// into the wave's partials pl[m][64q + j].  Upost rows sit in the slot like SV
+// rows (row n at n*128 B, 16-byte piece p at position p ^ ((n/2) % 8)).
+__device__ __forceinline__ void stream_post(const unsigned char* slot, int q, int M,
+                                            const float* tl, float* pl, int pcols, int lane) {
+  float u[16];
+#pragma unroll
+  for (int n = 0; n < 16; ++n)
+    u[n] = __half2float(*(const __half*)(slot + n * 128 + ((((lane >> 3) ^ (n >> 1)) & 7) << 4) +
+                                         (lane & 7) * 2));
+  const int j = 64 * q + lane;
+  for (int m = 0; m < M; ++m) {
+    const f32x4* t4 = (const f32x4*)(tl + m * 16);
+    float acc = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const f32x4 t = t4[v];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc = fmaf(t[i], u[4 * v + i], acc);
+    }
+    pl[m * pcols + j] += acc;
+  }
+}
+
+// inter = fp16(fp16(silu(fp16(g))) * fp16(u)): the rounding points of
+// act_fn(gate(x)) * up(x) on fp16 tensors; the product of two fp16 values is
+// exact in fp32, so one rounding gives the correctly rounded fp16 product.
+__device__ __forceinline__ __half swiglu_fp16(float g, float u) {
+  const float gf = __half2float(__float2half(g));
+  const float sl = __half2float(__float2half(gf / (1.f + expf(-gf))));
+  return __float2half(sl * __half2float(__float2half(u)));
+}
+
+// One workgroup: tiles [t0, t1) of one work unit; wave w takes t0 + w,
+// t0 + w + 4, ...  Src supplies the unit: m_rows, xrow (x row m, offset to
+// the K range), mat(item, s) (StreamMat of matrix s), load_a(item, s, m, j)
+// (the low-rank input a = x U of matrix s), and
+//  * NMAT = 1: store(item, m, n, y) with y = Q(x) + a SV^T + bias.
+//  * NMAT = 2 (gate and up of a SwiGLU MLP over the same x): each tile runs
+//    matrix 0 then matrix 1; store_inter(item, m, n, inter) with
+//    inter = fp16(silu(fp16 y0) * fp16 y1).  If post(item) gives the input
+//    factor Upost (N x rank) of the projection that consumes inter, the
+//    workgroup also forms sum_n inter[m][n] Upost[n][j] over its tiles and
+//    hands it to store_post(item, m, j, partial) (one partial per workgroup).
+template <int BITS, int MP, int D, bool SYM, bool SZ2, int NMAT, class Src>
 __device__ void gemv_stream(const Src& src, const StreamShape& sh, int item, int t0, int t1,
                             unsigned char* smem) {
+  static_assert(NMAT == 1 || NMAT == 2, "one or two matrices per tile");
   constexpr int NI = stream_ni<SZ2>();
   constexpr int SLOT = stream_slot<SZ2>();
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, kb = lane >> 4;
   const int M = src.m_rows(item);
-  const StreamLds L = stream_lds(D, SLOT, sh.mmax, sh.K, sh.xstride, sh.apad);
+
+  // Segments of a tile: matrix 0 [, matrix 1, post rows].  Scalars, not
+  // arrays, so that no runtime index sends them to scratch memory.
+  StreamMat mat0 = src.mat(item, 0);
+  StreamMat mat1 = NMAT == 2 ? src.mat(item, 1) : mat0;
+  if (sh.rank <= 0) mat0.SV = mat1.SV = nullptr;  // SV rows are read only with a rank
+  if (NMAT == 2) mat0.B = mat1.B = nullptr;       // no bias in the two-matrix form
+  const bool lora0 = mat0.SV != nullptr;
+  const bool lora1 = NMAT == 2 && mat1.SV != nullptr;
+  const __half* PU = nullptr;
+  if constexpr (NMAT == 2) PU = sh.rank > 0 ? src.post(item) : nullptr;
+  const int pcols = PU ? 64 * sh.nsvc : 0;
+  // chunks of matrix s: codes, then SV chunks (or one bias chunk, NMAT == 1)
+  const int seg0 = sh.nchunk + (lora0 ? sh.nsvc : (mat0.B ? 1 : 0));
+  const int seg1 = NMAT == 2 ? sh.nchunk + (lora1 ? sh.nsvc : 0) : 0;
+  const int seg2 = PU ? sh.nsvc : 0;
+  const int cpt = seg0 + seg1 + seg2;  // chunks per tile
+  auto seg_len = [&](int sg) { return sg == 0 ? seg0 : (sg == 1 ? seg1 : seg2); };
+  auto seg_mat = [&](int sg) -> StreamMat {
+    if (sg == 0) return mat0;
+    if (sg == 1) return mat1;
+    return StreamMat{mat0.C, mat0.S, mat0.Z, PU, nullptr};
+  };
+  // next segment after sg; returns true when the tile is complete
+  auto next_seg = [&](int& sg) -> bool {
+    if constexpr (NMAT == 1) {
+      return true;
+    } else {
+      ++sg;
+      if (sg == 2 && !PU) sg = 3;
+      if (sg == 3) {
+        sg = 0;
+        return true;
+      }
+      return false;
+    }
+  };
+
+  const StreamLds L = stream_lds(D, SLOT, sh.mmax, sh.K, BITS, sh.xstride, sh.apad, NMAT, pcols);
   __half* xs = (__half*)(smem + L.xs);  // mmax rows, then a 512-byte zero block
   float* xc = (float*)(smem + L.xc);    // [c128][c1 x16 | c2 x16]
-  __half* a_l = (__half*)(smem + L.a);
+  __half* a_l = (__half*)(smem + L.a);  // [matrix][16][apad]
   unsigned char* ring = smem + L.ring + wave * D * SLOT;
-
-  const uint32_t* C = src.codes(item);
-  const __half* S = src.scales(item);
-  const __half* Zs = SYM ? S : src.zeros(item);
-  const __half* SV = src.sv(item);
-  const __half* B = src.bias(item);
-  const bool lora = sh.rank > 0 && SV != nullptr;
-  const int nsvc = (lora || B != nullptr) ? (lora ? sh.nsvc : 1) : 0;
-  const int cpt = sh.nchunk + nsvc;  // chunks per tile
+  float* tlw = (float*)(smem + L.tl) + wave * 256;              // [m][16] inter tile
+  float* plw = (float*)(smem + L.pl) + wave * sh.mmax * pcols;  // [m][pcols]
 
   // This wave's work list: tiles t0 + wave + 4j, cpt chunks each.
   const int ntile_w = t1 - t0 > wave ? (t1 - t0 - wave + 3) / 4 : 0;
@@ -315,29 +418,32 @@ __device__ void gemv_stream(const Src& src, const StreamShape& sh, int item, int
   // byte offsets of this lane's 16-byte pieces within a 128-byte chunk row
   const int piece0 = 16 * ((lane & 7) ^ (((lane >> 3) >> 1) & 7));
   const int piece1 = 16 * ((lane & 7) ^ (((8 + (lane >> 3)) >> 1) & 7));
+  const void* dummy = (const void*)mat0.C;
   StreamCursor<BITS, SZ2> cur;
+  int cur_sg = 0;
   cur.r0 = (t0 + wave) * 16;
-  cur.retarget(C, S, Zs, lora ? SV : nullptr, B, sh, lane);
+  cur.retarget(mat0, sh, lane);
   int issued = 0;
   auto issue_next = [&]() {
     unsigned char* slot = ring + cur.slot * SLOT;
-    if (cur.c < sh.nchunk)
+    if (cur_sg < NMAT && cur.c < sh.nchunk)
       stream_issue<BITS, SZ2>(cur.P, sh, cur.c, slot, lane, piece0, piece1);
     else
-      stream_issue_sv<SZ2>(cur.P, sh, cur.c - sh.nchunk, slot, piece0, piece1, (const void*)C);
+      stream_issue_sv<SZ2>(cur.P, sh, cur_sg < NMAT ? cur.c - sh.nchunk : cur.c, slot, piece0,
+                           piece1, dummy);
     if (++cur.slot == D) cur.slot = 0;
     ++issued;
-    if (++cur.c == cpt) {
+    if (++cur.c == seg_len(cur_sg)) {
       cur.c = 0;
-      cur.r0 += 64;
-      cur.retarget(C, S, Zs, lora ? SV : nullptr, B, sh, lane);
+      if (next_seg(cur_sg)) cur.r0 += 64;
+      cur.retarget(seg_mat(cur_sg), sh, lane);
     }
   };
 
   // ---- prologue: D-1 chunks in flight, then stage x, its sums, and a ----
   for (int u = 0; u < D - 1 && u < total; ++u) issue_next();
 
-  const int kpad = stream_kpad(sh.K);
+  const int kpad = stream_kpad(sh.K, BITS);
   {
     const int nb = kpad >> 4;  // 16-code blocks per padded token row
     const int totalb = sh.mmax * nb;
@@ -401,18 +507,21 @@ __device__ void gemv_stream(const Src& src, const StreamShape& sh, int item, int
       xc[c128 * 32 + 16 + m] = 0.f;
     }
   }
-  if (lora) {
+#pragma unroll
+  for (int s = 0; s < NMAT; ++s) {
+    if (!(s == 0 ? lora0 : lora1)) continue;
+    __half* as = a_l + s * 16 * sh.apad;
     for (int idx = tid; idx < 16 * sh.rpad; idx += 256) {
       const int m = idx / sh.rpad, j = idx - m * sh.rpad;
-      a_l[m * sh.apad + j] =
-          (m < M && j < sh.rank) ? src.load_a(item, m, j) : __float2half(0.f);
+      as[m * sh.apad + j] = (m < M && j < sh.rank) ? src.load_a(item, s, m, j) : __float2half(0.f);
     }
     // rank columns rpad..64*nsvc of a read as zero by the last SV chunk
     for (int idx = tid; idx < 16 * (sh.apad - sh.rpad); idx += 256) {
       const int m = idx / (sh.apad - sh.rpad), j = sh.rpad + idx % (sh.apad - sh.rpad);
-      a_l[m * sh.apad + j] = __float2half(0.f);
+      as[m * sh.apad + j] = __float2half(0.f);
     }
   }
+  for (int idx = lane; idx < sh.mmax * pcols; idx += 64) plw[idx] = 0.f;
   __syncthreads();
 
   // ---- per-lane constants ----
@@ -462,12 +571,13 @@ __device__ void gemv_stream(const Src& src, const StreamShape& sh, int item, int
   for (int p = 0; p < MP; ++p) yacc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
   f32x4 corr = {0.f, 0.f, 0.f, 0.f};
   f32x4 y = {0.f, 0.f, 0.f, 0.f};
-  int c = 0, slot = 0;
+  f32x4 y0 = {0.f, 0.f, 0.f, 0.f};  // matrix 0 result of the two-matrix form
+  int c = 0, sg = 0, slot = 0;
   int r0 = (t0 + wave) * 16;
   // fp16 half of each staged scale dword: main path steps 0/1 and correction
   int par0, par1, cpar;
   auto parities = [&]() {
-    const int rowpar = (int)(((int64_t)min(r0 + li, sh.N - 1) * sh.G) & 1);
+    const int rowpar = (int)(((int64_t)min(r0 + li, sh.N - 1) * sh.G + sh.goff) & 1);
     if constexpr (BITS == 2 && SZ2) {
       par0 = par1 = rowpar ^ ln.h;
       cpar = rowpar ^ (kb & 1);
@@ -491,20 +601,20 @@ __device__ void gemv_stream(const Src& src, const StreamShape& sh, int item, int
     }
     const unsigned char* sl = ring + slot * SLOT;
     if (++slot == D) slot = 0;
-    if (c < sh.nchunk) {
+    if (sg < NMAT && c < sh.nchunk) {
       stream_consume<BITS, MP, SYM>(sl, c, par0, par1, cpar, sh, xs, xc, yacc, corr, ln, dk, li,
                                     kb);
       if (c == sh.nchunk - 1) {
         // the tile's code sums: merge the 2-bit halves into the standard
         // MFMA layout D[token 4kb+i][row li], then add the correction
         if constexpr (BITS == 2) {
-          f32x4 y0 = yacc[0], y1 = yacc[MP - 1];
+          f32x4 ya = yacc[0], yb = yacc[MP - 1];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            y0[i] += __shfl_xor(y0[i], 32);
-            if (MP == 2) y1[i] += __shfl_xor(y1[i], 32);
+            ya[i] += __shfl_xor(ya[i], 32);
+            if (MP == 2) yb[i] += __shfl_xor(yb[i], 32);
           }
-          y = kb < 2 ? y0 : (MP == 2 ? y1 : f32x4{0.f, 0.f, 0.f, 0.f});
+          y = kb < 2 ? ya : (MP == 2 ? yb : f32x4{0.f, 0.f, 0.f, 0.f});
         } else {
           y = yacc[0];
         }
@@ -513,31 +623,66 @@ __device__ void gemv_stream(const Src& src, const StreamShape& sh, int item, int
 #pragma unroll
         for (int p = 0; p < MP; ++p) yacc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-    } else if (lora) {
-      // SV chunk: rank columns 64(c - nchunk) .. +64 of this tile's rows
-      const int j0 = 64 * (c - sh.nchunk);
+    } else if (sg < NMAT) {
+      if (sg == 0 ? lora0 : lora1) {
+        // SV chunk: rank columns 64(c - nchunk) .. +64 of this tile's rows
+        const int j0 = 64 * (c - sh.nchunk);
+        const __half* as = a_l + (NMAT == 1 ? 0 : sg) * 16 * sh.apad;
 #pragma unroll
-      for (int sp = 0; sp < 2; ++sp) {
-        const f16x8 bv = *(const f16x8*)(sl + ln.code_off[sp]);
-        const f16x8 av = *(const f16x8*)(a_l + li * sh.apad + j0 + 32 * sp + 8 * kb);
-        y = mfma_16x16x32(av, bv, y);
-      }
-    }
-    if (++c == cpt) {
-      // ---- tile epilogue: bias (in the last SV chunk's slot) and store ----
-      const int n = r0 + li;
-      if (n < sh.N) {
-        const float bn =
-            B ? __half2float(((const __half*)(sl + kStreamCodeBytes))[li]) : 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = 4 * kb + i;
-          if (m < M) src.store(item, m, n, y[i] + bn);
+        for (int sp = 0; sp < 2; ++sp) {
+          const f16x8 bv = *(const f16x8*)(sl + ln.code_off[sp]);
+          const f16x8 av = *(const f16x8*)(as + li * sh.apad + j0 + 32 * sp + 8 * kb);
+          y = mfma_16x16x32(av, bv, y);
         }
       }
+    } else {
+      stream_post(sl, c, M, tlw, plw, pcols, lane);
+    }
+    if (++c == seg_len(sg)) {
+      const int n = r0 + li;
+      if constexpr (NMAT == 1) {
+        // ---- tile epilogue: bias (in the last SV chunk's slot) and store ----
+        if (n < sh.N) {
+          const float bn =
+              mat0.B ? __half2float(((const __half*)(sl + kStreamCodeBytes))[li]) : 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int m = 4 * kb + i;
+            if (m < M) src.store(item, m, n, y[i] + bn);
+          }
+        }
+      } else {
+        if (sg == 0) {
+          y0 = y;
+        } else if (sg == 1) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int m = 4 * kb + i;
+            const __half v = swiglu_fp16(y0[i], y[i]);
+            if (m < M && n < sh.N) src.store_inter(item, m, n, v);
+            tlw[m * 16 + li] = n < sh.N ? __half2float(v) : 0.f;
+          }
+        }
+        y = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
       c = 0;
-      r0 += 64;
-      parities();
+      if (next_seg(sg)) {
+        r0 += 64;
+        parities();
+      }
+    }
+  }
+  if constexpr (NMAT == 2) {
+    if (PU) {  // workgroup sum of the waves' partials
+      __syncthreads();
+      const float* pl0 = (const float*)(smem + L.pl);
+      const int wstride = sh.mmax * pcols;
+      for (int idx = tid; idx < M * sh.rank; idx += 256) {
+        const int m = idx / sh.rank, j = idx - m * sh.rank;
+        const int o = m * pcols + j;
+        src.store_post(item, m, j, pl0[o] + pl0[wstride + o] + pl0[2 * wstride + o] +
+                                       pl0[3 * wstride + o]);
+      }
     }
   }
 }

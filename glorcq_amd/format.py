@@ -152,7 +152,7 @@ class MoEProblem:
     SV: dict                       # proj -> (E, N, r) fp16
     cluster_of: dict               # proj -> (E,) int64
     U: dict                        # proj -> (C, K, r) fp16
-    shared: dict                   # proj -> QMat (1, N, .)
+    shared: dict | None            # proj -> QMat (1, N, .); None: no shared expert
     h: torch.Tensor                # (B, H) fp16
 
     @property
@@ -179,7 +179,7 @@ def make_moe(H=2048, E=60, inter=1408, top_k=4, n_clusters=16, rank=64, shared_i
     proj in (gate, up, down): cluster assignment randint(0, C, (E,)), U (C,K,r)
     N(0,0.01), expert weights (codes, scales, zeros as in make_linear), SV
     (E,N,r) N(0,0.01); then the shared expert's gate, up, down weights
-    (shared_bits, no LoRA); then h (B,H) N(0,1).  All fp32 draws rounded to fp16.
+    (shared_bits, no LoRA; skipped when shared_inter = 0); then h (B,H) N(0,1).  All fp32 draws rounded to fp16.
     Defaults are BASELINE config 2 (Qwen1.5-MoE-A2.7B)."""
     g = torch.Generator().manual_seed(seed)
     router_w = (torch.randn(E, H, generator=g) * 0.02).half()
@@ -193,8 +193,9 @@ def make_moe(H=2048, E=60, inter=1408, top_k=4, n_clusters=16, rank=64, shared_i
         experts[proj] = _rand_qmat(g, E, N, K, bits, group)
         SV[proj] = (torch.randn(E, N, rank, generator=g) * 0.01).half()
     sdims = {"gate": (H, shared_inter), "up": (H, shared_inter), "down": (shared_inter, H)}
-    shared = {proj: _rand_qmat(g, 1, sdims[proj][1], sdims[proj][0], shared_bits, group)
-              for proj in PROJS}
+    shared = None if shared_inter == 0 else {
+        proj: _rand_qmat(g, 1, sdims[proj][1], sdims[proj][0], shared_bits, group)
+        for proj in PROJS}
     h = torch.randn(B, H, generator=g).half()
     return MoEProblem(H=H, E=E, inter=inter, top_k=top_k, norm_topk_prob=norm_topk_prob,
                       rank=rank, n_clusters=n_clusters, router_w=router_w,
@@ -212,8 +213,9 @@ def moe_step_bytes(p: MoEProblem, active_experts: int, active_clusters: dict) ->
         per = q.N * q.K * q.bits // 8 + 4 * q.N * (q.K // q.group) + 2 * q.N * p.rank
         total += active_experts * per
         total += active_clusters[proj] * 2 * q.K * p.rank
-        s = p.shared[proj]
-        total += s.N * s.K * s.bits // 8 + 4 * s.N * (s.K // s.group)
-    total += 2 * (p.E + 1) * p.H
+        if p.shared is not None:
+            s = p.shared[proj]
+            total += s.N * s.K * s.bits // 8 + 4 * s.N * (s.K // s.group)
+    total += 2 * (p.E + (1 if p.shared is not None else 0)) * p.H
     total += 2 * 2 * p.B * p.H
     return total

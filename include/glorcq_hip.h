@@ -122,6 +122,60 @@ int glq_lowrank_xu_batched(int64_t items, const void* x, int64_t x_stride, int64
                            void* stream);
 
 /*
+ * One MoE block at decode: router, top-k dispatch, routed SwiGLU experts with
+ * cluster-shared low-rank correction, sigmoid-gated shared expert, combine.
+ * Replaces GraphCompatibleMoeBlock.forward (inference/moe_block.py:381-436:
+ * router :386-392, cluster-shared x*U :290-322, per-expert
+ * down(act(gate(x)) * up(x)) with LoRA :367-379 and :438-478, shared expert
+ * :429-433) and the HF-style GLoRCQExperts.forward
+ * (inference/quantized_linear.py:395-428) for one step of `tokens` tokens.
+ * Only selected experts are read (the reference's graph mode computes all E,
+ * moe_block.py:742-890).  All routing stays on the device: no host sync, so
+ * the call can be captured in a hipGraph (graph_wrapper.py:69-131).
+ *
+ * Weights are stacked expert-major; projection index 0 = gate, 1 = up,
+ * 2 = down.  gate/up: N = inter, K = hidden; down: N = hidden, K = inter.
+ * Codes use the packed container of glq_gemv_lora (bits 2 or 4, group 128,
+ * asymmetric: zeros required).  U is the per-projection cluster pool
+ * (the reference's global U pool, model_builder.py:143-183); an expert's U is
+ * U[cluster_of[e]].  rank 0 or SV == NULL: no low-rank term.
+ */
+typedef struct glq_moe_params {
+  int64_t tokens;        /* B: rows of h (1..64) */
+  int64_t hidden;        /* H */
+  int64_t experts;       /* E (<= 256) */
+  int64_t inter;         /* routed expert intermediate size */
+  int64_t top_k;         /* <= 16, tokens * top_k <= 512 */
+  int64_t n_clusters;    /* U clusters per projection */
+  int64_t rank;          /* LoRA rank: 0, or a multiple of 8 <= 128 */
+  int64_t shared_inter;  /* shared expert intermediate size (0: no shared expert) */
+  int32_t norm_topk_prob;
+  int32_t bits;          /* routed code width: 2 or 4 */
+  int32_t shared_bits;   /* shared expert code width: 2 or 4 */
+  int32_t group;         /* quantization group: 128 */
+  const void* h;                 /* (tokens, hidden) fp16 */
+  const void* router_w;          /* (experts, hidden) fp16 */
+  const void* shared_gate_w;     /* (hidden,) fp16; NULL: shared output ungated */
+  const int32_t* codes[3];       /* (experts, N, K*bits/32) */
+  const void* scales[3];         /* (experts, N, K/group) fp16 */
+  const void* zeros[3];          /* (experts, N, K/group) fp16 */
+  const void* U[3];              /* (n_clusters, K, rank) fp16 */
+  const int32_t* cluster_of[3];  /* (experts,) int32 */
+  const void* SV[3];             /* (experts, N, rank) fp16 */
+  const int32_t* shared_codes[3];  /* (N, K*shared_bits/32) */
+  const void* shared_scales[3];    /* (N, K/group) fp16 */
+  const void* shared_zeros[3];
+  void* out;             /* (tokens, hidden) fp16 */
+  void* router_logits;   /* (tokens, experts) fp16, or NULL */
+} glq_moe_params;
+
+/* Workspace bytes glq_moe_decode needs for `p` (negative on a bad shape). */
+int64_t glq_moe_workspace_bytes(const glq_moe_params* p);
+/* Four launches on `stream`; the workspace needs no initialisation. */
+int glq_moe_decode(const glq_moe_params* p, void* workspace, int64_t workspace_bytes,
+                   void* stream);
+
+/*
  * Debug: unpack codes (N, K*bits/32) int32 -> (N, K) int32.  Codes are
  * returned unsigned (0..2^b-1), or sign-extended when sym != 0.
  * Replaces _unpack_indices (inference/quantized_linear.py:115-146) and

@@ -213,11 +213,19 @@ def parity_ok(y: torch.Tensor, ref: torch.Tensor, rtol: float = 1e-2, atol: floa
 # with the sparse dispatch of _forward_sparse :704-740 / the HF-style
 # GLoRCQExperts.forward, inference/quantized_linear.py:395-428)
 # ---------------------------------------------------------------------------
-def route(h: torch.Tensor, router_w: torch.Tensor, top_k: int, norm_topk_prob: bool):
+def route(h: torch.Tensor, router_w: torch.Tensor, top_k: int, norm_topk_prob: bool,
+          exact: bool = False):
     """Router (moe_block.py:386-392): logits = gate(h) in fp16, softmax in fp32,
     torch.topk, optional renormalisation, cast to fp16.
+    exact=True rounds the fp64 sum of each logit to fp16 once (what the
+    reference's fp16 nn.Linear does on the GPU: fp32 accumulation, one
+    rounding); exact=False uses torch's CPU fp16 matmul, whose blocked kernel
+    (from about 16 rows up) can land a few fp16 ulps away from that.
     Returns (fp16 logits (B,E), fp16 weights (B,k), int64 experts (B,k))."""
-    logits = h.half() @ router_w.half().T
+    if exact:
+        logits = (h.double() @ router_w.double().T).half()
+    else:
+        logits = h.half() @ router_w.half().T
     rw = torch.softmax(logits.float(), dim=1)
     w, sel = torch.topk(rw, top_k, dim=-1)
     if norm_topk_prob:
@@ -266,7 +274,7 @@ def moe_forward(p, exact: bool = True, h: torch.Tensor | None = None, dense: boo
     (test_cluster_parallel.py:159 asserts the two agree)."""
     h = p.h if h is None else h
     B, H = h.shape
-    _, w, sel = route(h, p.router_w, p.top_k, p.norm_topk_prob)
+    _, w, sel = route(h, p.router_w, p.top_k, p.norm_topk_prob, exact=exact)
     acc_dtype = torch.float64 if exact else torch.float16
     final = torch.zeros(B, H, dtype=acc_dtype)
     xu = {}
@@ -307,8 +315,14 @@ def moe_forward(p, exact: bool = True, h: torch.Tensor | None = None, dense: boo
             final.index_add_(0, torch.tensor(toks), y * wt.double()[:, None])
         else:
             final.index_add_(0, torch.tensor(toks), (y.half() * wt[:, None]).half())
+    if p.shared is None:  # a block without a shared expert (Mixtral-style)
+        return final
     # shared expert (4-bit, no LoRA) with the sigmoid gate
-    sg = torch.sigmoid((h.half() @ p.shared_gate_w.half().T).float()).half()
+    if exact:
+        sgl = (h.double() @ p.shared_gate_w.double().T).half()
+    else:
+        sgl = h.half() @ p.shared_gate_w.half().T
+    sg = torch.sigmoid(sgl.float()).half()
     sgu = {proj: _qmat_linear(h, p.shared[proj], 0, exact) for proj in ("gate", "up")}
     if exact:
         sinter = (torch.nn.functional.silu(sgu["gate"].half().float()).half().double() *
