@@ -17,7 +17,10 @@ on the launch stream, fed the same layers' a = x*U precomputed by the library;
 its algorithmic bytes per layer = N*K*b/8 + 4*N*G + 2*r*N + 2*M*(K+N) + 2*M*r
 (codes, scales+zeros, SV, x, y, a) = 998,272 B.
 
-Also reported: single-call latency of config 0 (one layer, both launches), and
+Also reported: the MoE block decode step of config 2 at B = 1, 4, 16, 32
+(microseconds per step and per token under hipGraph replay, achieved GB/s on
+the step's algorithmic bytes), single-call latency of config 0 (one layer,
+both launches), and
 the CPU baseline = the reference's CPU fallback restated in oracle/ (fp16
 dequant loop + fp16 x@W.T + fp16 LoRA) on config 0, timed on the host cores;
 its output doubles as the parity check of the GPU result for the same input.
@@ -161,6 +164,65 @@ def pmc_workload():
     print("pmc workload done", flush=True)
 
 
+MOE_BATCHES = (1, 4, 16, 32)
+
+
+def bench_moe(dev, seed=6, reps=20, trials=15):
+    """Config 2 (Qwen1.5-MoE-A2.7B block): one decode step of
+    the whole block per call (router, top-4 dispatch, routed 2-bit experts with
+    cluster-shared LoRA, 4-bit shared expert, combine: four launches), `reps`
+    steps captured in one hipGraph, replays timed with HIP events (median of
+    `trials`).  Bytes per step follow format.moe_step_bytes with this run's
+    active experts and clusters, read off the GPU's own router logits."""
+    import torch
+
+    from glorcq_amd import format as fmt
+    from glorcq_amd.moe_block import GraphCompatibleMoeBlock
+
+    res = {}
+    for B in MOE_BATCHES:
+        p = fmt.make_moe(B=B, seed=seed)
+        blk = GraphCompatibleMoeBlock.from_problem(p, dev)
+        h = p.h.reshape(1, B, p.H).to(dev)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                _, logits = blk(h)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                blk(h)
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        ts = []
+        for _ in range(trials):
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3 / reps)
+        ts.sort()
+        us = ts[len(ts) // 2]
+        sel = torch.topk(logits.float().cpu(), p.top_k, dim=-1).indices
+        act = sorted(set(sel.flatten().tolist()))
+        clusters = {proj: len({int(p.cluster_of[proj][e]) for e in act}) for proj in fmt.PROJS}
+        nbytes = fmt.moe_step_bytes(p, len(act), clusters)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[str(B)] = {"us_per_step": round(us, 2), "us_per_token": round(us / B, 3),
+                       "tokens_per_s": round(B / (us * 1e-6), 1),
+                       "active_experts": len(act), "active_clusters": clusters,
+                       "algorithmic_bytes": nbytes, "achieved_GBps": round(gbs, 1),
+                       "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"moe B={B}: {us:.2f} us/step, {us / B:.3f} us/token, {gbs:.0f} GB/s")
+        del graph, blk
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -169,6 +231,7 @@ def main():
     ap.add_argument("--pool", type=int, default=POOL)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--pmc-workload", action="store_true")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MoE block leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (every box here has one); "
@@ -262,8 +325,17 @@ def main():
         },
         "single_call_config0_us": round(single_ms * 1e3, 2),
         "gemv_alone_matches_step_output": same,
-        "moe_block_decode_us_per_token": None,
     }
+    if not args.no_moe:
+        log("MoE block decode step (config 2), hipGraph replays")
+        moe = bench_moe(dev)
+        result["moe_block_decode_us_per_token"] = {b: v["us_per_token"] for b, v in moe.items()}
+        result["moe_block_decode"] = {
+            "workload": ("config 2: Qwen1.5-MoE-A2.7B block (H 2048, 60 experts, inter 1408, "
+                         "top-4, 2-bit g128 routed experts with rank-64 LoRA, U shared over 16 "
+                         "clusters, 4-bit shared expert inter 5632), seed 6, one hipGraph of 20 "
+                         "steps per replay"),
+            "by_batch": moe}
     if not args.no_cpu:
         log("cpu baseline (oracle restatement of the reference CPU fallback)")
         cb, parity, err = cpu_baseline(y0)

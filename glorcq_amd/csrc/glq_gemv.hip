@@ -65,9 +65,7 @@ struct DenseSrc {
   __device__ __half load_a(int item, int m, int j) const {
     if (a.xu) return a.xu[(int64_t)item * a.xu_es + (int64_t)m * a.sh.rank + j];
     const float* p = a.apart + ((int64_t)item * a.P * a.M + m) * a.sh.rpad + j;
-    float s = 0.f;
-    for (int q = 0; q < a.P; ++q) s += p[(int64_t)q * a.M * a.sh.rpad];
-    return __float2half(s);
+    return __float2half(sum_strided(p, (int64_t)a.M * a.sh.rpad, a.P));
   }
   __device__ void store(int item, int m, int n, float v) const {
     a.y[(int64_t)item * a.y_es + (int64_t)m * a.sh.N + n] = __float2half(v);
@@ -83,7 +81,8 @@ __global__ __launch_bounds__(256) void lowrank_partial_kernel(DenseArgs a) {
   const int K = a.sh.K;
   auto xrow = [&](int m) { return X + (int64_t)m * K; };
   lowrank_partial<MC>(xrow, a.M, K, a.sh.rank, a.sh.rpad, a.u + (int64_t)item * a.u_es, p,
-                      (float*)a.apart + ((int64_t)item * a.P + p) * a.M * a.sh.rpad, red, xl);
+                      (float*)a.apart + ((int64_t)item * a.P + p) * a.M * a.sh.rpad, red, xl,
+                      (int)threadIdx.x);
 }
 
 // a = fp16(sum over the P K-slices of the partials): items x M x rank.

@@ -93,6 +93,21 @@ __host__ __device__ inline LdsLayout lds_layout(int M, int KP, int GP, int T, in
   return L;
 }
 
+// p[0] + p[stride] + ... + p[(n-1) stride] in that order, with the loads
+// issued in batches of 8 so that a batch costs one memory round trip (a plain
+// loop waits for each load before the next add).
+__device__ __forceinline__ float sum_strided(const float* __restrict__ p, int64_t stride, int n) {
+  float s = 0.f;
+  for (int q0 = 0; q0 < n; q0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = q0 + u < n ? p[(int64_t)(q0 + u) * stride] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  return s;
+}
+
 __device__ __forceinline__ f32x4 mfma_16x16x32(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -220,13 +235,18 @@ __device__ __forceinline__ void load_batch(u32x4 (&wv)[NB][T], const uint32_t* C
 // ---------------------------------------------------------------------------
 constexpr int kLowrankRows = 256;  // U rows per partial (K-slice)
 
+// `tid` is the thread's index in its group of 256 (a workgroup may run several
+// groups side by side, each with its own LDS; every group must make the same
+// calls, since the barriers are workgroup-wide).  out == nullptr: compute, but
+// write nothing (a group without a job of its own).
 template <int MC, class XRow>
 __device__ void lowrank_partial(const XRow& xrow, int M, int K, int rank, int rpad,
                                 const __half* __restrict__ U, int p,
                                 float* __restrict__ out /* M x rpad */,
                                 float* red /* LDS, 4*4*64 floats */,
-                                __half* xl /* LDS, 16 x kLowrankRows halves */) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+                                __half* xl /* LDS, 16 x kLowrankRows halves */,
+                                int tid) {
+  const int lane = tid & 63, wave = tid >> 6;
   const int j8 = tid & 7, kr = tid >> 3;  // kr in 0..31
   const int k0 = p * kLowrankRows;
   const int kl = min(kLowrankRows, K - k0);
@@ -281,7 +301,7 @@ __device__ void lowrank_partial(const XRow& xrow, int M, int K, int rank, int rp
       __syncthreads();
       {
         const int mm = tid >> 6, jj = tid & 63;
-        if (mm < MC && mb + mm < M && jb + jj < rpad) {
+        if (out && mm < MC && mb + mm < M && jb + jj < rpad) {
           const float s = red[(0 * 4 + mm) * 64 + jj] + red[(1 * 4 + mm) * 64 + jj] +
                           red[(2 * 4 + mm) * 64 + jj] + red[(3 * 4 + mm) * 64 + jj];
           out[(mb + mm) * rpad + jb + jj] = s;

@@ -29,14 +29,23 @@
 namespace glq {
 
 constexpr int kMoeTB = 8;          // tokens per routed block (one MFMA pass for 2-bit)
-constexpr int kMoeDepth = 3;       // ring slots per wave
+constexpr int kMoeDepth = 4;       // ring slots per wave (3 chunks in flight)
 constexpr int kMoeMaxE = 256;
 constexpr int kMoeMaxP = 512;      // tokens * top_k
 constexpr int kMoeMaxB = 64;
 constexpr int kMoeXBudget = 48 * 1024;  // bytes of staged x per down-projection unit
+constexpr int kMoeMaxChunks = 6;        // code chunks per down-projection K part
+// a_down = inter U_down is summed over the gate/up workgroups of a block with
+// 64-bit integer atomics on values scaled by 2^24: integer addition does not
+// depend on the order of the updates, so the sum (and the step's output) is
+// the same on every run.  |a_down| < 2^39 fits; the resolution 2^-24 is far
+// below the fp16 rounding of a_down that follows.
+constexpr float kAdqScale = 16777216.f;
 
 struct MoeArgs {
   int B, H, E, I, topk, norm, C, rank, rpad, SI;
+  int nrb;     // router workgroups (16 router rows x 16 tokens each)
+  int xurows;  // U rows per x U partial job
   int nbm;     // routed token blocks the grids are sized for
   int sus;     // K-slices of the gate/up x U partials
   int wgu;     // workgroups per routed block (gate/up)
@@ -50,6 +59,8 @@ struct MoeArgs {
   int wgsd, tpsd;  // shared down: workgroups per (token block, part), tiles per workgroup
   int bits, sbits;
   int tl_off;      // LDS byte offset of the routed block's token list (gate/up)
+  int pl_off;      // LDS byte offset of the routed block's pair list (down)
+  int lg_off;      // LDS byte offset of the router logits copy (gate/up)
   StreamShape shGU, shSGU, shD, shSD;
   const __half* h;
   const __half* rw;
@@ -70,12 +81,13 @@ struct MoeArgs {
   __half* sg;      // [B] shared-expert gate
   float* xu;       // [2][C][sus][B][rpad] gate/up x U partials
   __half* inter;   // [nbm][TB][I]
-  float* adp;      // [nbm][wgu][TB][rpad] a_down partials
+  unsigned long long* adq;  // [nbm][TB][rpad] a_down sums, fixed point (kAdqScale)
   __half* sinter;  // [B][SI]
-  float* yb;       // [sr][nbm][TB][H] routed down outputs (fp32)
+  float* yb;       // [sr][B * topk][H] routed down outputs per (token, k) pair (fp32)
   float* sdp;      // [ss][B][H] shared down partial outputs (fp32)
   __half* out;
   __half* logits;
+  __half* lgb;     // [B][E] fp16 router logits (workspace)
 };
 
 // ---------------------------------------------------------------------------
@@ -108,10 +120,11 @@ __device__ inline MoeTables moe_tables(int* w, int P, int E, int nbm) {
 }
 
 // Builds the tables (all 256 threads); returns the number of blocks.
-__device__ int moe_dispatch(const MoeArgs& a, const MoeTables& t) {
+// `sel_global`: read the top-k ids from the workspace (else t.sel holds them).
+__device__ int moe_dispatch(const MoeArgs& a, const MoeTables& t, bool sel_global = true) {
   const int P = a.B * a.topk, E = a.E, tid = threadIdx.x;
   for (int i = tid; i < P; i += 256) {
-    const int e = a.sel[i];
+    const int e = sel_global ? a.sel[i] : t.sel[i];
     t.sel[i] = (e >= 0 && e < E) ? e : -1;
   }
   __syncthreads();
@@ -172,120 +185,234 @@ __device__ int moe_dispatch(const MoeArgs& a, const MoeTables& t) {
   return *t.nblk;
 }
 
+__device__ __forceinline__ int align_up_dev(int v, int a) { return (v + a - 1) / a * a; }
+
 __device__ __forceinline__ int moe_cluster(const MoeArgs& a, int s, int e) {
   const int c = a.clus[s][e];
   return min(max(c, 0), a.C - 1);
 }
 
 // ---------------------------------------------------------------------------
-// 1. Router + gate/up cluster partials
+// 1. Router + gate/up cluster partials (1024-thread workgroups)
 // ---------------------------------------------------------------------------
-__device__ void moe_route_token(const MoeArgs& a, int t, float* lg) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const __half* hr = a.h + (int64_t)t * a.H;
-  const int nrow = a.E + (a.sgw ? 1 : 0);
-  for (int e = wave; e < nrow; e += 4) {
-    const __half* wr = e < a.E ? a.rw + (int64_t)e * a.H : a.sgw;
-    float acc = 0.f;
-    for (int k = 8 * lane; k < a.H; k += 512) {
-      const f16x8 hv = *(const f16x8*)(hr + k);
-      const f16x8 wv = *(const f16x8*)(wr + k);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) acc = fmaf((float)hv[c], (float)wv[c], acc);
+constexpr int kRouteThreads = 1024;
+
+// Softmax, top-k (and optional renormalisation) of every token at once
+// (moe_block.py:386-392): lane t of one wave routes token t (B <= 64) from an
+// fp32 LDS copy of its fp16 logits (rows of E + 1 floats: the lanes of one
+// read hit distinct banks; reads unrolled so several are in flight).  Pass j picks the best expert strictly behind pick j-1 in the order
+// (logit descending, index ascending): ties go to the lower index, and as the
+// probabilities exp(l - max) / sum are monotonic in the logit (distinct fp16
+// logits give distinct fp32 probabilities) this is the probability order.
+// Then the softmax sum in index order and the weights of the picks.  No
+// cross-lane traffic.  Ids -> sel[t * topk + j] (LDS); `publish` also writes
+// ids and fp16 weights to the workspace.
+__device__ void moe_topk_lanes(const MoeArgs& a, const float* lgf, int* sel, bool publish) {
+  const int t = threadIdx.x & 63;
+  if (t >= a.B) return;
+  const int E = a.E;
+  const float* col = lgf + t * (E + 1);  // this token's row (E + 1 floats: distinct banks)
+  float pv = INFINITY, mx = 0.f;
+  int pi = -1;
+  for (int j = 0; j < a.topk; ++j) {
+    float bv = -INFINITY;
+    int bi = -1;
+#pragma unroll 8
+    for (int e = 0; e < E; ++e) {
+      const float w = col[e];
+      const bool behind = (w < pv) | ((w == pv) & (e > pi));
+      const bool better = behind & ((w > bv) | (bi < 0));
+      bv = better ? w : bv;
+      bi = better ? e : bi;
     }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) acc += __shfl_xor(acc, d);
-    if (lane == 0) lg[e] = __half2float(__float2half(acc));  // fp16 logits
+    if (j == 0) mx = bv;
+    sel[t * a.topk + j] = bi;
+    pv = bv;
+    pi = bi;
   }
-  __syncthreads();
-  if (wave != 0) return;
-  // softmax over E in fp32 (lane holds experts lane + 64i)
-  float v[4], pr[4];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = lane + 64 * i;
-    v[i] = e < a.E ? lg[e] : -INFINITY;
-    mx = fmaxf(mx, v[i]);
-  }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+  if (!publish) return;
   float sum = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    pr[i] = lane + 64 * i < a.E ? expf(v[i] - mx) : 0.f;
-    sum += pr[i];
+#pragma unroll 8
+  for (int e = 0; e < E; ++e) sum += expf(col[e] - mx);
+  float ws = 0.f;
+  if (a.norm)
+    for (int j = 0; j < a.topk; ++j) ws += expf(col[sel[t * a.topk + j]] - mx) / sum;
+  for (int j = 0; j < a.topk; ++j) {
+    const int e = sel[t * a.topk + j];
+    float w = expf(col[e] - mx) / sum;
+    if (a.norm) w = w / ws;
+    a.sel[t * a.topk + j] = e;
+    a.wts[t * a.topk + j] = __float2half(w);
   }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) sum += __shfl_xor(sum, d);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) pr[i] = lane + 64 * i < a.E ? pr[i] / sum : -1.f;
-  // top-k: k rounds of (largest probability, lowest index)
-  float wk = 0.f, wsum = 0.f;
-  int ek = 0;
-  for (int k = 0; k < a.topk; ++k) {
-    float bv = -2.f;
-    int bi = 1 << 30;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (pr[i] > bv) {  // ascending index within the lane: strict > keeps the lowest
-        bv = pr[i];
-        bi = lane + 64 * i;
-      }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-      const float ov = __shfl_xor(bv, d);
-      const int oi = __shfl_xor(bi, d);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (lane + 64 * i == bi) pr[i] = -1.f;
-    if (lane == k) {
-      wk = bv;
-      ek = bi;
-    }
-    wsum += bv;
-  }
-  if (lane < a.topk) {
-    const float w = a.norm ? wk / wsum : wk;
-    a.sel[t * a.topk + lane] = ek;
-    a.wts[t * a.topk + lane] = __float2half(w);
-  }
-  if (a.logits)
-    for (int e = lane; e < a.E; e += 64) a.logits[(int64_t)t * a.E + e] = __float2half(lg[e]);
-  if (lane == 0)
-    a.sg[t] = a.sgw ? __float2half(1.f / (1.f + expf(-lg[a.E]))) : __float2half(1.f);
 }
 
-__global__ __launch_bounds__(256) void moe_route_kernel(MoeArgs a) {
-  __shared__ float lg[kMoeMaxE + 1];
-  __shared__ float red[4 * 4 * 64];
-  __shared__ __half xl[16 * kLowrankRows];
-  if ((int)blockIdx.x < a.B) {
-    moe_route_token(a, blockIdx.x, lg);
-    return;
+// Router logits of tokens [16 rb, 16 rb + 16) x router rows [16 tile,
+// 16 tile + 16) (the rows after the E experts: the shared-expert gate), one
+// MFMA tile (A = h rows staged in LDS, B = router rows) with K split over the
+// 16 waves: every router-row load of a wave goes out before it waits, and the
+// rows of a tile come from one workgroup per tile, so no CU pulls the whole
+// router matrix.  fp32 sums rounded to fp16 once -> workspace (and the
+// caller's router_logits); the shared-expert gate sigmoid(fp16 logit) -> sg.
+constexpr int kRouteBatch = 16;  // MFMA k-steps (32 codes each) a wave loads at once
+__device__ void moe_route_tile(const MoeArgs& a, int id, unsigned char* smem) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, kb = lane >> 4;
+  const int nrow = a.E + (a.sgw ? 1 : 0);
+  const int ntile = (nrow + 15) / 16;
+  const int tile = id % ntile, rb = id / ntile;
+  const int t0 = rb * 16, nt = min(16, a.B - t0);
+  const int hstride = a.H + 8;
+  __half* hl = (__half*)smem;                       // [16][H + 8]
+  float* red = (float*)(smem + 16 * hstride * 2);  // [16 waves][256]
+  const int kseg = max(32, a.H / 16 / 32 * 32);    // codes per wave (a multiple of 32)
+  const int nks = a.H / kseg;                       // waves with a K segment
+  const int steps = kseg / 32;
+  const int n = min(tile * 16 + li, nrow - 1);
+  const __half* wr = n < a.E ? a.rw + (int64_t)n * a.H : a.sgw;
+  const bool kv = wave < nks;
+  const int kbase = wave * kseg + 8 * kb;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  bool staged = false;
+  for (int s0 = 0; s0 < steps; s0 += kRouteBatch) {
+    f16x8 wv[kRouteBatch];
+#pragma unroll
+    for (int u = 0; u < kRouteBatch; ++u) {
+      const bool sv = kv && s0 + u < steps;
+      wv[u] = sv ? *(const f16x8*)(wr + kbase + 32 * (s0 + u)) : f16x8{};
+    }
+    if (!staged) {  // h rows into LDS while the router rows are in flight
+      for (int idx = tid; idx < 16 * (a.H / 8); idx += kRouteThreads) {
+        const int m = idx / (a.H / 8), k8 = idx - m * (a.H / 8);
+        *(f16x8*)(hl + m * hstride + 8 * k8) =
+            m < nt ? *(const f16x8*)(a.h + (int64_t)(t0 + m) * a.H + 8 * k8) : f16x8{};
+      }
+      __syncthreads();
+      staged = true;
+    }
+    if (kv) {
+#pragma unroll
+      for (int u = 0; u < kRouteBatch; ++u) {
+        if (s0 + u >= steps) break;  // only steps inside the segment read staged h
+        const f16x8 hv = *(const f16x8*)(hl + li * hstride + kbase + 32 * (s0 + u));
+        acc = mfma_16x16x32(hv, wv[u], acc);
+      }
+    }
   }
-  // x U_c partials: (projection s in {gate, up}, cluster c, K-slice q)
-  const int id = blockIdx.x - a.B;
-  const int s = id / (a.C * a.sus), rem = id - s * a.C * a.sus;
+  if (!staged) __syncthreads();  // (steps == 0 cannot happen: H >= 256)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[wave * 256 + (4 * kb + i) * 16 + li] = acc[i];
+  __syncthreads();
+  if (tid < 256) {  // token m = tid / 16, row tile*16 + tid % 16
+    const int m = tid >> 4, r = tile * 16 + (tid & 15);
+    float s = 0.f;
+    for (int w = 0; w < nks; ++w) s += red[w * 256 + tid];
+    const __half lgh = __float2half(s);
+    if (m < nt && r < a.E) {
+      a.lgb[(int64_t)(t0 + m) * a.E + r] = lgh;
+      if (a.logits) a.logits[(int64_t)(t0 + m) * a.E + r] = lgh;
+    }
+    if (m < nt && r == a.E && a.sgw)
+      a.sg[t0 + m] = __float2half(1.f / (1.f + expf(-__half2float(lgh))));
+  }
+  if (!a.sgw && tile == 0 && tid < nt) a.sg[t0 + tid] = __float2half(1.f);
+}
+
+// x U_c partials of one job (projection s in {gate, up}, cluster c, K-slice q
+// of xurows rows): part[t][r] = sum_{k in slice} x[t][k] U_c[k][r].  The U
+// slice reaches LDS by 16-byte loads; v_mfma_f32_16x16x4f32 (A = x: token x
+// 4 k, B = U: 4 k x 16 rank columns, one LDS element per lane, so U keeps its
+// row-major layout).  Wave w takes rank tile w % 4 (of <= 8) and k-range
+// w / 4 (of 4); the k-ranges add up in LDS in turn.
+__device__ void moe_xu_job(const MoeArgs& a, int job, unsigned char* smem) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, kb = lane >> 4;
+  const int s = job / (a.C * a.sus), rem = job - s * a.C * a.sus;
   const int c = rem / a.sus, q = rem - c * a.sus;
-  const __half* U = a.U[s] + (int64_t)c * a.u_es[s];
-  for (int m0 = 0; m0 < a.B; m0 += 16) {
-    const int M = min(16, a.B - m0);
-    auto xrow = [&](int m) { return a.h + (int64_t)(m0 + m) * a.H; };
-    float* out = a.xu + ((((int64_t)s * a.C + c) * a.sus + q) * a.B + m0) * a.rpad;
-    if (M == 1)
-      lowrank_partial<1>(xrow, M, a.H, a.rank, a.rpad, U, q, out, red, xl);
-    else if (M == 2)
-      lowrank_partial<2>(xrow, M, a.H, a.rank, a.rpad, U, q, out, red, xl);
-    else
-      lowrank_partial<4>(xrow, M, a.H, a.rank, a.rpad, U, q, out, red, xl);
-    __syncthreads();
+  const int xr = a.xurows;
+  const int k0 = q * xr, kl = min(xr, a.H - k0);
+  const int ntt = (a.B + 15) / 16;          // token tiles
+  const int nrt = (a.rank + 15) / 16;       // rank tiles (<= 8)
+  const int xstride = xr + 4, ustride = a.rank + 8;
+  __half* xl = (__half*)smem;                                     // [B][xr + 4]
+  __half* ul = (__half*)(smem + align_up_dev(a.B * xstride * 2, 16));  // [xr][rank + 8]
+  float* red = (float*)((unsigned char*)ul + align_up_dev(xr * ustride * 2, 16));
+  const __half* U = a.U[s] + (int64_t)c * a.u_es[s] + (int64_t)k0 * a.rank;
+  const int r8 = a.rank / 8;
+  for (int idx = tid; idx < kl * r8; idx += kRouteThreads) {  // U slice, 16 B per load
+    const int k = idx / r8, j8 = idx - k * r8;
+    const f16x8 v = *(const f16x8*)(U + (int64_t)k * a.rank + 8 * j8);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) ul[k * ustride + 8 * j8 + u] = v[u];
   }
+  for (int idx = tid; idx < a.B * (xr / 8); idx += kRouteThreads) {
+    const int m = idx / (xr / 8), k8 = idx - m * (xr / 8);
+    f16x8 v = f16x8{};
+    if (8 * k8 < kl) v = *(const f16x8*)(a.h + (int64_t)m * a.H + k0 + 8 * k8);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) xl[m * xstride + 8 * k8 + u] = v[u];
+  }
+  __syncthreads();
+  const int kr = wave >> 2;  // k-range of this wave: rows [kr * xr / 4, (kr + 1) * xr / 4)
+  const int ns = xr / 4 / 4;  // steps of 4 rows per k-range
+  // every wave runs the same number of iterations (the loop holds barriers)
+  for (int it = 0; it < (nrt + 3) / 4; ++it) {
+    const int rt = (wave & 3) + 4 * it;
+    const bool rv = rt < nrt;
+    const int col = rt * 16 + li;
+    f32x4 acc[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (rv) {
+      for (int u = 0; u < ns; ++u) {
+        const int k = kr * (xr / 4) + 4 * u + kb;
+        const float uv = (k < kl && col < a.rank) ? __half2float(ul[k * ustride + col]) : 0.f;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          if (tt < ntt) {
+            const int m = tt * 16 + li;
+            const float xv = m < a.B ? __half2float(xl[m * xstride + k]) : 0.f;
+            acc[tt] = mfma_16x16x4f32(xv, uv, acc[tt]);
+          }
+      }
+    }
+    // acc[tt][i]: token tt*16 + 4kb + i, rank column col; the four k-ranges
+    // add into one buffer in turn (k-range order: deterministic)
+    for (int r = 0; r < 4; ++r) {
+      if (r == kr && rv) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          if (tt < ntt) {
+            float* rp = red + (tt * nrt + rt) * 256;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float* d = rp + (4 * kb + i) * 16 + li;
+              *d = r == 0 ? acc[tt][i] : *d + acc[tt][i];
+            }
+          }
+      }
+      __syncthreads();
+    }
+  }
+  float* out = a.xu + (((int64_t)s * a.C + c) * a.sus + q) * a.B * a.rpad;
+  for (int idx = tid; idx < a.B * a.rpad; idx += kRouteThreads) {
+    const int m = idx / a.rpad, j = idx - m * a.rpad;
+    out[idx] = j < nrt * 16 ? red[((m >> 4) * nrt + (j >> 4)) * 256 + (m & 15) * 16 + (j & 15)]
+                            : 0.f;
+  }
+}
+
+__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(MoeArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  if (a.rank > 0) {  // this step's a_down accumulators start at zero
+    const int64_t nq = (int64_t)a.nbm * kMoeTB * a.rpad;
+    for (int64_t i = (int64_t)blockIdx.x * kRouteThreads + threadIdx.x; i < nq;
+         i += (int64_t)gridDim.x * kRouteThreads)
+      a.adq[i] = 0ull;
+  }
+  if ((int)blockIdx.x < a.nrb)
+    moe_route_tile(a, blockIdx.x, smem);
+  else
+    moe_xu_job(a, blockIdx.x - a.nrb, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -295,6 +422,7 @@ struct RoutedGateUp {
   const MoeArgs& a;
   const int* tok;  // LDS: the block's token ids
   int b, wg, e, M;
+  int cg, cu, cd;  // clusters of the expert's gate, up and down projections
   __device__ int m_rows(int) const { return M; }
   __device__ const __half* xrow(int, int m) const { return a.h + (int64_t)tok[m] * a.H; }
   __device__ StreamMat mat(int, int s) const {
@@ -303,20 +431,19 @@ struct RoutedGateUp {
                      nullptr};
   }
   __device__ __half load_a(int, int s, int m, int j) const {
-    const int c = moe_cluster(a, s, e);
+    const int c = s == 0 ? cg : cu;
     const float* p = a.xu + (((int64_t)s * a.C + c) * a.sus * a.B + tok[m]) * a.rpad + j;
-    float v = 0.f;
-    for (int q = 0; q < a.sus; ++q) v += p[(int64_t)q * a.B * a.rpad];
-    return __float2half(v);
+    return __float2half(sum_strided(p, (int64_t)a.B * a.rpad, a.sus));
   }
   __device__ const __half* post(int) const {
-    return a.U[2] ? a.U[2] + moe_cluster(a, 2, e) * a.u_es[2] : nullptr;
+    return a.U[2] ? a.U[2] + cd * a.u_es[2] : nullptr;
   }
   __device__ void store_inter(int, int m, int n, __half v) const {
     a.inter[((int64_t)b * kMoeTB + m) * a.I + n] = v;
   }
   __device__ void store_post(int, int m, int j, float v) const {
-    a.adp[(((int64_t)b * a.wgu + wg) * kMoeTB + m) * a.rpad + j] = v;
+    const long long q = llrintf(v * kAdqScale);
+    atomicAdd(a.adq + ((int64_t)b * kMoeTB + m) * a.rpad + j, (unsigned long long)q);
   }
   __device__ void store(int, int, int, float) const {}
 };
@@ -347,10 +474,36 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
   const int nr = a.nbm * a.wgu;
   if ((int)blockIdx.x < nr) {
     const int b = blockIdx.x / a.wgu, wg = blockIdx.x - b * a.wgu;
-    int* tok = (int*)(smem + a.tl_off);
+    int* tok = (int*)(smem + a.tl_off);  // [kMoeTB] tokens, expert, M, then 3E cluster ids
+    int cl[3];  // cluster ids of every expert, loaded alongside the top-k ids
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      const int i = tid + 256 * u;
+      cl[u] = (a.rank > 0 && i < 3 * a.E) ? a.clus[i / a.E][i % a.E] : 0;
+    }
     {
       const MoeTables t = moe_tables((int*)smem, a.B * a.topk, a.E, a.nbm);
-      const int nblk = moe_dispatch(a, t);
+      // routing of every token (workgroup 0 publishes it for the later launches):
+      // the logits reach LDS (fp32, rows of E + 1) in one pass, then one lane
+      // per token
+      float* lgf = (float*)(smem + a.lg_off);
+      const int nl = a.B * a.E;
+      for (int i = tid; i < nl / 8; i += 256) {  // 16-byte loads of the flat [B][E] array
+        const f16x8 v = ((const f16x8*)a.lgb)[i];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int f = 8 * i + u, tk = f / a.E;
+          lgf[f + tk] = (float)v[u];  // row tk starts at tk * (E + 1)
+        }
+      }
+      for (int f = nl / 8 * 8 + tid; f < nl; f += 256) {
+        const int tk = f / a.E;
+        lgf[f + tk] = __half2float(a.lgb[f]);
+      }
+      __syncthreads();
+      if (tid < 64) moe_topk_lanes(a, lgf, t.sel, blockIdx.x == 0);
+      __syncthreads();
+      const int nblk = moe_dispatch(a, t, false);
       if (b >= nblk) return;  // uniform over the workgroup
       if (tid < kMoeTB) {
         const int M = t.bM[b];
@@ -360,19 +513,25 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
         tok[kMoeTB] = t.bexp[b];
         tok[kMoeTB + 1] = t.bM[b];
       }
+#pragma unroll
+      for (int u = 0; u < 3; ++u)
+        if (tid + 256 * u < 3 * a.E) tok[16 + tid + 256 * u] = cl[u];
       __syncthreads();
     }
     const int e = tok[kMoeTB], M = tok[kMoeTB + 1];
+    auto clamp_c = [&](int c) { return min(max(c, 0), a.C - 1); };
+    const int cg = clamp_c(tok[16 + e]), cu = clamp_c(tok[16 + a.E + e]);
+    const int cd = clamp_c(tok[16 + 2 * a.E + e]);
     __syncthreads();  // the tables' LDS is reused by the stream from here on
     const int t0 = wg * a.tpu, t1 = min(a.shGU.tiles, t0 + a.tpu);
-    gemv_stream<BR, 1, kMoeDepth, false, BR == 2, 2>(RoutedGateUp{a, tok, b, wg, e, M}, a.shGU,
-                                                    0, t0, t1, smem);
+    gemv_stream_ks<BR, 1, kMoeDepth, false, BR == 2, 2>(
+        RoutedGateUp{a, tok, b, wg, e, M, cg, cu, cd}, a.shGU, 0, t0, t1, smem);
   } else if constexpr (BS != 0) {
     const int id = blockIdx.x - nr;
     const int sb = id / a.wgsu, wg = id - sb * a.wgsu;
     const int t0 = wg * a.tpsu, t1 = min(a.shSGU.tiles, t0 + a.tpsu);
-    gemv_stream<BS, BS == 2 ? 2 : 1, kMoeDepth, false, BS == 2, 2>(SharedGateUp{a, sb}, a.shSGU,
-                                                                  0, t0, t1, smem);
+    gemv_stream_ks<BS, BS == 2 ? 2 : 1, kMoeDepth, false, BS == 2, 2>(SharedGateUp{a, sb},
+                                                                     a.shSGU, 0, t0, t1, smem);
   }
 }
 
@@ -395,6 +554,7 @@ __device__ inline StreamShape moe_part_shape(const StreamShape& base, int Kfull,
 
 struct RoutedDown {
   const MoeArgs& a;
+  const int* pair;  // LDS: the block's pair indices (t * top_k + k)
   int b, e, M, part, k0;
   __device__ int m_rows(int) const { return M; }
   __device__ const __half* xrow(int, int m) const {
@@ -407,13 +567,11 @@ struct RoutedDown {
                      (part == 0 && a.SV[2]) ? a.SV[2] + e * a.sv_es[2] : nullptr, nullptr};
   }
   __device__ __half load_a(int, int, int m, int j) const {
-    const float* p = a.adp + ((int64_t)b * a.wgu * kMoeTB + m) * a.rpad + j;
-    float v = 0.f;
-    for (int w = 0; w < a.wgu; ++w) v += p[(int64_t)w * kMoeTB * a.rpad];
-    return __float2half(v);
+    const long long q = (long long)a.adq[((int64_t)b * kMoeTB + m) * a.rpad + j];
+    return __float2half((float)((double)q * (1.0 / kAdqScale)));
   }
   __device__ void store(int, int m, int n, float v) const {
-    a.yb[(((int64_t)part * a.nbm + b) * kMoeTB + m) * a.H + n] = v;
+    a.yb[((int64_t)part * a.B * a.topk + pair[m]) * a.H + n] = v;
   }
 };
 
@@ -444,18 +602,20 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
     const int rem = blockIdx.x - b * a.sr * a.wgd;
     const int part = rem / a.wgd, wg = rem - part * a.wgd;
     int e, M;
+    int* pair = (int*)(smem + a.pl_off);  // past the stream layout and the tables
     {
       const MoeTables t = moe_tables((int*)smem, a.B * a.topk, a.E, a.nbm);
       const int nblk = moe_dispatch(a, t);
       if (b >= nblk) return;
       e = t.bexp[b];
       M = t.bM[b];
+      if (threadIdx.x < kMoeTB) pair[threadIdx.x] = t.list[t.bfirst[b] + min((int)threadIdx.x, M - 1)];
       __syncthreads();
     }
     const StreamShape sh = moe_part_shape(a.shD, a.I, a.kr, part, BR);
     const int t0 = wg * a.tpd, t1 = min(sh.tiles, t0 + a.tpd);
-    gemv_stream<BR, 1, kMoeDepth, false, BR == 2, 1>(RoutedDown{a, b, e, M, part, part * a.kr},
-                                                    sh, 0, t0, t1, smem);
+    gemv_stream_ks<BR, 1, kMoeDepth, false, BR == 2, 1>(
+        RoutedDown{a, pair, b, e, M, part, part * a.kr}, sh, 0, t0, t1, smem);
   } else if constexpr (BS != 0) {
     const int id = blockIdx.x - nr;
     const int sb = id / (a.ss * a.wgsd);
@@ -463,7 +623,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
     const int part = rem / a.wgsd, wg = rem - part * a.wgsd;
     const StreamShape sh = moe_part_shape(a.shSD, a.SI, a.ks, part, BS);
     const int t0 = wg * a.tpsd, t1 = min(sh.tiles, t0 + a.tpsd);
-    gemv_stream<BS, BS == 2 ? 2 : 1, kMoeDepth, false, BS == 2, 1>(
+    gemv_stream_ks<BS, BS == 2 ? 2 : 1, kMoeDepth, false, BS == 2, 1>(
         SharedDown{a, sb, part, part * a.ks}, sh, 0, t0, t1, smem);
   }
 }
@@ -472,19 +632,16 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
 // 4. Combine: out[t] = fp16(sum_k w_tk y_(t,k) + gate_t * fp16(shared_t))
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int t = blockIdx.x / ((a.H + 255) / 256);
-  const int n = (blockIdx.x - t * ((a.H + 255) / 256)) * 256 + threadIdx.x;
-  const MoeTables tb = moe_tables((int*)smem, a.B * a.topk, a.E, a.nbm);
-  moe_dispatch(a, tb);
+  const int nb = (a.H + 255) / 256;
+  const int t = blockIdx.x / nb;
+  const int n = (blockIdx.x - t * nb) * 256 + threadIdx.x;
   if (n >= a.H) return;
+  const int P = a.B * a.topk;
   float acc = 0.f;
   for (int k = 0; k < a.topk; ++k) {
-    const int p = t * a.topk + k, pos = tb.pos[p];
-    if (pos < 0) continue;
+    const int p = t * a.topk + k;
     float y = 0.f;
-    for (int part = 0; part < a.sr; ++part)
-      y += a.yb[((int64_t)part * a.nbm * kMoeTB + pos) * a.H + n];
+    for (int part = 0; part < a.sr; ++part) y += a.yb[((int64_t)part * P + p) * a.H + n];
     acc = fmaf(__half2float(a.wts[p]), y, acc);
   }
   if (a.SI > 0) {
@@ -503,9 +660,9 @@ namespace {
 struct MoePlan {
   MoeArgs a;
   int64_t ws_need;
-  size_t lds_gu, lds_d, lds_c;
+  size_t lds_route, lds_gu, lds_d, lds_c;
   int64_t grid_route, grid_gu, grid_d, grid_c;
-  int64_t off_sel, off_wts, off_sg, off_xu, off_inter, off_adp, off_sinter, off_yb, off_sdp;
+  int64_t off_sel, off_lgb, off_wts, off_sg, off_xu, off_inter, off_adq, off_sinter, off_yb, off_sdp;
 };
 
 StreamShape moe_stream_shape(int K, int N, int bits, int rank, int mmax, int kpart) {
@@ -529,14 +686,26 @@ StreamShape moe_stream_shape(int K, int N, int bits, int rank, int mmax, int kpa
   return s;
 }
 
-// K parts of a down projection: the fewest parts whose x slice (mmax rows,
-// multiples of 256 codes) fits the staging budget.
-void moe_ksplit(int K, int mmax, int& parts, int& kp) {
-  int cap = kMoeXBudget / (2 * mmax) / 256 * 256;
-  if (cap < 256) cap = 256;
+// K parts of a down projection: the fewest parts whose x slice (mmax rows)
+// fits the staging budget and whose codes fit kMoeMaxChunks chunks per row
+// (a wave's serial work per tile); parts hold whole chunks.
+void moe_ksplit(int K, int mmax, int bits, int& parts, int& kp) {
+  const int unit = bits == 2 ? 512 : 256;  // codes per 128-byte chunk
+  int cap = kMoeXBudget / (2 * mmax) / unit * unit;
+  cap = std::min(cap, kMoeMaxChunks * unit);
+  if (cap < unit) cap = unit;
   parts = (K + cap - 1) / cap;
-  kp = (int)align_up((K + parts - 1) / parts, 256);
+  kp = (int)align_up((K + parts - 1) / parts, unit);
   parts = (K + kp - 1) / kp;
+}
+
+// Tiles per workgroup (all four waves work on each tile): as few as keep the
+// launch near kMoeTargetWgs workgroups, so small batches spread over the chip
+// and large ones amortise each workgroup's prologue.
+constexpr int64_t kMoeTargetWgs = 768;
+int moe_tiles_per_wg(int64_t units, int tiles) {
+  const int64_t t = (units * tiles + kMoeTargetWgs - 1) / kMoeTargetWgs;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(tiles, t));
 }
 
 int stream_slot_bytes(int bits) { return stream_slot<true>() - (bits == 2 ? 0 : 256); }
@@ -593,27 +762,29 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
   a.sbits = SI > 0 ? p->shared_bits : 0;
   const int P_ = (int)(B * k);
   a.nbm = (int)std::min<int64_t>(E, P_) + P_ / kMoeTB;
-  a.sus = (int)((H + kLowrankRows - 1) / kLowrankRows);
+  a.xurows = a.rank <= 64 ? 512 : 256;
+  a.sus = (int)((H + a.xurows - 1) / a.xurows);
   const int mr = (int)std::min<int64_t>(B, kMoeTB);  // staged rows per routed block
   // gate/up: K = H, N = I
+  a.nrb = (int)(((E + (p->shared_gate_w ? 1 : 0) + 15) / 16) * ((B + 15) / 16));
   a.shGU = moe_stream_shape((int)H, (int)I, a.bits, a.rank, mr, (int)H);
-  a.tpu = 4;
+  a.tpu = moe_tiles_per_wg(a.nbm, a.shGU.tiles);
   a.wgu = (a.shGU.tiles + a.tpu - 1) / a.tpu;
   // routed down: K = I (K parts), N = H
-  moe_ksplit((int)I, mr, a.sr, a.kr);
+  moe_ksplit((int)I, mr, a.bits, a.sr, a.kr);
   a.shD = moe_stream_shape((int)I, (int)H, a.bits, a.rank, mr, a.kr);
-  a.tpd = 4;
+  a.tpd = moe_tiles_per_wg((int64_t)a.nbm * a.sr, a.shD.tiles);
   a.wgd = (a.shD.tiles + a.tpd - 1) / a.tpd;
   if (SI > 0) {
     a.stb = a.sbits == 2 ? 16 : 16;
     a.stb = (int)std::min<int64_t>(B, a.stb);
     a.nsb = (int)((B + a.stb - 1) / a.stb);
     a.shSGU = moe_stream_shape((int)H, (int)SI, a.sbits, 0, a.stb, (int)H);
-    a.tpsu = 4;
+    a.tpsu = moe_tiles_per_wg(a.nsb, a.shSGU.tiles);
     a.wgsu = (a.shSGU.tiles + a.tpsu - 1) / a.tpsu;
-    moe_ksplit((int)SI, a.stb, a.ss, a.ks);
+    moe_ksplit((int)SI, a.stb, a.sbits, a.ss, a.ks);
     a.shSD = moe_stream_shape((int)SI, (int)H, a.sbits, 0, a.stb, a.ks);
-    a.tpsd = 4;
+    a.tpsd = moe_tiles_per_wg((int64_t)a.nsb * a.ss, a.shSD.tiles);
     a.wgsd = (a.shSD.tiles + a.tpsd - 1) / a.tpsd;
   }
   // LDS
@@ -621,26 +792,41 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
   const int pcols = a.rank > 0 ? 64 * a.shGU.nsvc : 0;
   const StreamLds Lgu = stream_lds(kMoeDepth, stream_slot_bytes(a.bits), mr, (int)H, a.bits,
                                    a.shGU.xstride, a.shGU.apad, 2, pcols);
-  // the block's token list sits past both the stream layout and the tables
-  a.tl_off = (int)align_up(std::max(Lgu.total, tbl), 16);
-  size_t lgu = (size_t)a.tl_off + 16 * 4;
+  // the block's token list sits past the stream layout (with its K-split
+  // partial tiles) and the tables
+  a.tl_off = (int)align_up(std::max(Lgu.total + stream_ks_bytes(2), tbl), 16);
+  size_t lgu = (size_t)a.tl_off + 16 * 4 + 3 * 4 * (size_t)E;
+  a.lg_off = (int)align_up(lgu, 16);  // B x (E + 1) fp32 logits for the top-k
+  lgu = a.lg_off + align_up(4 * B * (E + 1), 16);
   const StreamLds Ld = stream_lds(kMoeDepth, stream_slot_bytes(a.bits), mr, a.kr, a.bits,
                                   a.shD.xstride, a.shD.apad, 1, 0);
-  size_t ld = std::max<size_t>(Ld.total, tbl);
+  size_t ld = std::max<size_t>(Ld.total + stream_ks_bytes(1), tbl);
+  a.pl_off = (int)align_up(ld, 16);  // the routed block's pair list
+  ld = a.pl_off + 16 * 4;
   if (SI > 0) {
     const StreamLds Ls = stream_lds(kMoeDepth, stream_slot_bytes(a.sbits), a.stb, (int)H,
                                     a.sbits, a.shSGU.xstride, a.shSGU.apad, 2, 0);
-    lgu = std::max<size_t>(lgu, Ls.total);
+    lgu = std::max<size_t>(lgu, Ls.total + stream_ks_bytes(2));
     const StreamLds Lsd = stream_lds(kMoeDepth, stream_slot_bytes(a.sbits), a.stb, a.ks,
                                      a.sbits, a.shSD.xstride, a.shSD.apad, 1, 0);
-    ld = std::max<size_t>(ld, Lsd.total);
+    ld = std::max<size_t>(ld, Lsd.total + stream_ks_bytes(1));
   }
   GLQ_CHECK(lgu <= 160 * 1024 && ld <= 160 * 1024, "MoE shapes exceed the LDS budget");
   P.lds_gu = lgu;
   P.lds_d = ld;
-  P.lds_c = tbl;
+  P.lds_c = 0;
+  {
+    const size_t router = (size_t)16 * (H + 8) * 2 + (size_t)16 * 256 * 4;
+    const size_t xu = (size_t)align_up(B * (a.xurows + 4) * 2, 16) +
+                      (size_t)align_up((int64_t)a.xurows * (a.rank + 8) * 2, 16) +
+                      (size_t)((B + 15) / 16) * ((a.rank + 15) / 16) * 256 * 4;
+    P.lds_route = std::max(router, lora ? xu : (size_t)0);
+    GLQ_CHECK(P.lds_route <= 160 * 1024,
+              "hidden=%lld with %lld tokens exceeds the router's LDS budget", (long long)H,
+              (long long)B);
+  }
   // grids
-  P.grid_route = B + (lora ? 2 * a.C * a.sus : 0);
+  P.grid_route = a.nrb + (lora ? 2 * a.C * a.sus : 0);
   P.grid_gu = (int64_t)a.nbm * a.wgu + (SI > 0 ? (int64_t)a.nsb * a.wgsu : 0);
   P.grid_d = (int64_t)a.nbm * a.sr * a.wgd + (SI > 0 ? (int64_t)a.nsb * a.ss * a.wgsd : 0);
   P.grid_c = B * ((H + 255) / 256);
@@ -652,13 +838,14 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
     return at;
   };
   P.off_sel = take(4 * P_);
+  P.off_lgb = take(2 * B * E);
   P.off_wts = take(2 * P_);
   P.off_sg = take(2 * B);
   P.off_xu = take(lora ? 4 * 2 * a.C * a.sus * B * a.rpad : 0);
   P.off_inter = take(2 * (int64_t)a.nbm * kMoeTB * I);
-  P.off_adp = take(lora ? 4 * (int64_t)a.nbm * a.wgu * kMoeTB * a.rpad : 0);
+  P.off_adq = take(lora ? 8 * (int64_t)a.nbm * kMoeTB * a.rpad : 0);
   P.off_sinter = take(2 * B * SI);
-  P.off_yb = take(4 * (int64_t)a.sr * a.nbm * kMoeTB * H);
+  P.off_yb = take(4 * (int64_t)a.sr * P_ * H);
   P.off_sdp = take(SI > 0 ? 4 * (int64_t)a.ss * B * H : 0);
   P.ws_need = o;
 
@@ -690,10 +877,13 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
 template <int BR, int BS>
 int moe_launch(MoePlan& P, hipStream_t s) {
   static size_t attr_gu = 64 * 1024, attr_d = 64 * 1024, attr_c = 64 * 1024;
+  static size_t attr_r = 64 * 1024;
   const MoeArgs& a = P.a;
-  moe_route_kernel<<<dim3((unsigned)P.grid_route), dim3(256), 0, s>>>(a);
+  int rc = set_lds_limit(moe_route_kernel, P.lds_route, attr_r);
+  if (rc) return rc;
+  moe_route_kernel<<<dim3((unsigned)P.grid_route), dim3(kRouteThreads), P.lds_route, s>>>(a);
   GLQ_LAUNCH_CHECK("moe_route_kernel");
-  int rc = set_lds_limit(moe_gate_up_kernel<BR, BS>, P.lds_gu, attr_gu);
+  rc = set_lds_limit(moe_gate_up_kernel<BR, BS>, P.lds_gu, attr_gu);
   if (rc) return rc;
   moe_gate_up_kernel<BR, BS><<<dim3((unsigned)P.grid_gu), dim3(256), P.lds_gu, s>>>(a);
   GLQ_LAUNCH_CHECK("moe_gate_up_kernel");
@@ -732,11 +922,12 @@ extern "C" int glq_moe_decode(const glq_moe_params* p, void* workspace, int64_t 
   char* w = (char*)workspace;
   MoeArgs& a = P.a;
   a.sel = (int32_t*)(w + P.off_sel);
+  a.lgb = (__half*)(w + P.off_lgb);
   a.wts = (__half*)(w + P.off_wts);
   a.sg = (__half*)(w + P.off_sg);
   a.xu = (float*)(w + P.off_xu);
   a.inter = (__half*)(w + P.off_inter);
-  a.adp = (float*)(w + P.off_adp);
+  a.adq = (unsigned long long*)(w + P.off_adq);
   a.sinter = (__half*)(w + P.off_sinter);
   a.yb = (float*)(w + P.off_yb);
   a.sdp = (float*)(w + P.off_sdp);

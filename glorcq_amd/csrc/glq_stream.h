@@ -344,6 +344,176 @@ __device__ __forceinline__ __half swiglu_fp16(float g, float u) {
   return __float2half(sl * __half2float(__float2half(u)));
 }
 
+// Stages, for one work unit, the x rows (zero-padded, permuted into MFMA
+// operand order), their per-128-code sums c1 = sum(operand bias * x) and
+// c2 = sum(x), the zero block, and the low-rank inputs a of the matrices with
+// a low-rank term.  x blocks and a elements share one loop, so their global
+// loads go out together (one memory round trip for the whole prologue).
+template <int BITS, int NMAT, class Src>
+__device__ void stream_stage(const Src& src, const StreamShape& sh, int item, int M, bool lora0,
+                             bool lora1, __half* xs, float* xc, __half* a_l, int tid) {
+  const int kpad = stream_kpad(sh.K, BITS);
+  const int nb = kpad >> 4;           // 16-code blocks per padded token row
+  const int totalb = sh.mmax * nb;    // a multiple of 8: shuffle groups stay whole
+  const int na0 = lora0 ? M * sh.rank : 0;
+  const int na1 = NMAT == 2 && lora1 ? M * sh.rank : 0;
+  const int total = totalb + na0 + na1;
+  for (int base = 0; base < total; base += 256) {
+    const int idx = base + tid;
+    const bool v = idx < totalb;
+    float s = 0.f, sb = 0.f;
+    int m = 0, blk = 0;
+    if (v) {
+      m = idx / nb;
+      blk = idx - m * nb;
+      _Float16 in[16], o[16];
+      if (m < M && blk * 16 < sh.K) {
+        const f16x8* srcx = (const f16x8*)(src.xrow(item, m) + blk * 16);
+        const f16x8 in0 = srcx[0], in1 = srcx[1];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          in[c] = in0[c];
+          in[8 + c] = in1[c];
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 16; ++c) in[c] = (_Float16)0.f;
+      }
+#pragma unroll
+      for (int pos = 0; pos < 16; ++pos) {
+        o[pos] = in[perm_src<BITS>(pos)];
+        const float f = (float)o[pos];
+        s += f;
+        sb += code_bias<BITS>(pos) * f;
+      }
+      f16x8 o0, o1;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        o0[c] = o[c];
+        o1[c] = o[8 + c];
+      }
+      f16x8* dst = (f16x8*)(xs + m * sh.xstride + blk * 16);
+      dst[0] = o0;
+      dst[1] = o1;
+    } else if (idx < total) {
+      const int ai = idx - totalb;
+      const int sm = ai < na0 ? 0 : 1;
+      const int r = ai - (sm ? na0 : 0);
+      const int am = r / sh.rank, j = r - am * sh.rank;
+      a_l[(sm * 16 + am) * sh.apad + j] = src.load_a(item, sm, am, j);
+    }
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    sb += __shfl_xor(sb, 1);
+    sb += __shfl_xor(sb, 2);
+    sb += __shfl_xor(sb, 4);
+    if (v && (idx & 7) == 0 && m < sh.mmax) {
+      const int c128 = blk >> 3;
+      xc[c128 * 32 + m] = sb;      // c1: sum of operand bias * x
+      xc[c128 * 32 + 16 + m] = s;  // c2: sum of x
+    }
+  }
+  for (int idx = tid; idx < 128; idx += 256)  // the zero block
+    ((uint32_t*)(xs + sh.mmax * sh.xstride))[idx] = 0u;
+  // tokens mmax..15 of every chunk read as zero
+  const int nc = kpad >> 7, nz = 16 - sh.mmax;
+  for (int idx = tid; idx < nc * nz; idx += 256) {
+    const int c128 = idx / nz, m = sh.mmax + idx % nz;
+    xc[c128 * 32 + m] = 0.f;
+    xc[c128 * 32 + 16 + m] = 0.f;
+  }
+  // a: zero outside tokens < M and columns < rank (the SV chunks read
+  // columns up to 64 * nsvc)
+#pragma unroll
+  for (int sm = 0; sm < NMAT; ++sm) {
+    if (!(sm == 0 ? lora0 : lora1)) continue;
+    __half* as = a_l + sm * 16 * sh.apad;
+    for (int idx = tid; idx < 16 * sh.apad; idx += 256) {
+      const int m = idx / sh.apad, j = idx - m * sh.apad;
+      if (m >= M || j >= sh.rank) as[idx] = __float2half(0.f);
+    }
+  }
+}
+
+// Per-lane constants of the consume loop.
+template <int BITS, int MP, bool SZ2>
+__device__ __forceinline__ StreamLane<MP> stream_lane(const StreamShape& sh, int M, int li,
+                                                      int kb) {
+  StreamLane<MP> ln;
+  const int sw = (li >> 1) & 7;
+#pragma unroll
+  for (int sp = 0; sp < 2; ++sp) ln.code_off[sp] = li * 128 + (((4 * sp + kb) ^ sw) << 4);
+  const int zrow = sh.mmax * sh.xstride;
+  if constexpr (BITS == 2) {
+    ln.h = kb >> 1;
+#pragma unroll
+    for (int p = 0; p < MP; ++p) {
+      const int m = (li & 7) + 8 * p;
+      const bool act = ((li >> 3) == ln.h) && m < M;
+      ln.xa[p] = act ? m * sh.xstride + 64 * kb : zrow;
+      ln.xstep[p] = act ? 256 : 0;
+      ln.xcb[p] = 0;
+    }
+    if constexpr (SZ2) {  // dword (row*4 + group%4); z 256 B after s
+      ln.szb = 4 * (li * 4 + ln.h);
+      ln.szstep = 8;
+      ln.cszb = 4 * (li * 4 + kb);
+      ln.czoff = 256;
+    } else {              // dword (row*2 + group%4/2) holds groups 2j, 2j+1; z 128 B after s
+      ln.szb = 8 * li;
+      ln.szstep = 4;
+      ln.cszb = 8 * li + 4 * (kb >> 1);
+      ln.czoff = 128;
+    }
+  } else {
+    ln.h = 0;
+    ln.xa[0] = li < M ? li * sh.xstride + 32 * kb : zrow;
+    ln.xstep[0] = li < M ? 128 : 0;
+    ln.xcb[0] = 0;
+    ln.szb = 8 * li;
+    ln.szstep = 4;
+    ln.cszb = 8 * li + 4 * (kb & 1);
+    ln.czoff = 128;
+  }
+  return ln;
+}
+
+// fp16 half of each staged scale dword (main-path steps 0/1, correction) for
+// the tile at row r0.
+template <int BITS, bool SZ2>
+__device__ __forceinline__ void stream_parities(const StreamShape& sh, int r0, int li, int kb,
+                                                int h, int& par0, int& par1, int& cpar) {
+  const int rowpar = (int)(((int64_t)min(r0 + li, sh.N - 1) * sh.G + sh.goff) & 1);
+  if constexpr (BITS == 2 && SZ2) {
+    par0 = par1 = rowpar ^ h;
+    cpar = rowpar ^ (kb & 1);
+  } else if constexpr (BITS == 2) {
+    par0 = par1 = h;
+    cpar = kb & 1;
+  } else {
+    par0 = rowpar;
+    par1 = rowpar ^ 1;
+    cpar = rowpar ^ (kb & 1);
+  }
+}
+
+// The 2-bit half sums merged into the standard MFMA layout D[token 4kb+i][row li].
+template <int BITS, int MP>
+__device__ __forceinline__ f32x4 stream_merge(const f32x4 (&yacc)[MP], int kb) {
+  if constexpr (BITS == 2) {
+    f32x4 ya = yacc[0], yb = yacc[MP - 1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ya[i] += __shfl_xor(ya[i], 32);
+      if (MP == 2) yb[i] += __shfl_xor(yb[i], 32);
+    }
+    return kb < 2 ? ya : (MP == 2 ? yb : f32x4{0.f, 0.f, 0.f, 0.f});
+  } else {
+    return yacc[0];
+  }
+}
+
 // One workgroup: tiles [t0, t1) of one work unit; wave w takes t0 + w,
 // t0 + w + 4, ...  Src supplies the unit: m_rows, xrow (x row m, offset to
 // the K range), mat(item, s) (StreamMat of matrix s), load_a(item, s, m, j)
@@ -443,126 +613,10 @@ __device__ void gemv_stream(const Src& src, const StreamShape& sh, int item, int
   // ---- prologue: D-1 chunks in flight, then stage x, its sums, and a ----
   for (int u = 0; u < D - 1 && u < total; ++u) issue_next();
 
-  const int kpad = stream_kpad(sh.K, BITS);
-  {
-    const int nb = kpad >> 4;  // 16-code blocks per padded token row
-    const int totalb = sh.mmax * nb;
-    for (int base = 0; base < totalb; base += 256) {
-      const int idx = base + tid;
-      const bool v = idx < totalb;
-      float s = 0.f, sb = 0.f;
-      int m = 0, blk = 0;
-      if (v) {
-        m = idx / nb;
-        blk = idx - m * nb;
-        _Float16 in[16], o[16];
-        if (m < M && blk * 16 < sh.K) {
-          const f16x8* srcx = (const f16x8*)(src.xrow(item, m) + blk * 16);
-          const f16x8 in0 = srcx[0], in1 = srcx[1];
-#pragma unroll
-          for (int c = 0; c < 8; ++c) {
-            in[c] = in0[c];
-            in[8 + c] = in1[c];
-          }
-        } else {
-#pragma unroll
-          for (int c = 0; c < 16; ++c) in[c] = (_Float16)0.f;
-        }
-#pragma unroll
-        for (int pos = 0; pos < 16; ++pos) {
-          o[pos] = in[perm_src<BITS>(pos)];
-          const float f = (float)o[pos];
-          s += f;
-          sb += code_bias<BITS>(pos) * f;
-        }
-        f16x8 o0, o1;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          o0[c] = o[c];
-          o1[c] = o[8 + c];
-        }
-        f16x8* dst = (f16x8*)(xs + m * sh.xstride + blk * 16);
-        dst[0] = o0;
-        dst[1] = o1;
-      }
-      s += __shfl_xor(s, 1);
-      s += __shfl_xor(s, 2);
-      s += __shfl_xor(s, 4);
-      sb += __shfl_xor(sb, 1);
-      sb += __shfl_xor(sb, 2);
-      sb += __shfl_xor(sb, 4);
-      if (v && (idx & 7) == 0 && m < sh.mmax) {
-        const int c128 = blk >> 3;
-        xc[c128 * 32 + m] = sb;      // c1: sum of operand bias * x
-        xc[c128 * 32 + 16 + m] = s;  // c2: sum of x
-      }
-    }
-    for (int idx = tid; idx < 128; idx += 256)  // the zero block
-      ((uint32_t*)(xs + sh.mmax * sh.xstride))[idx] = 0u;
-    // tokens mmax..15 of every chunk read as zero
-    const int nc = kpad >> 7, nz = 16 - sh.mmax;
-    for (int idx = tid; idx < nc * nz; idx += 256) {
-      const int c128 = idx / nz, m = sh.mmax + idx % nz;
-      xc[c128 * 32 + m] = 0.f;
-      xc[c128 * 32 + 16 + m] = 0.f;
-    }
-  }
-#pragma unroll
-  for (int s = 0; s < NMAT; ++s) {
-    if (!(s == 0 ? lora0 : lora1)) continue;
-    __half* as = a_l + s * 16 * sh.apad;
-    for (int idx = tid; idx < 16 * sh.rpad; idx += 256) {
-      const int m = idx / sh.rpad, j = idx - m * sh.rpad;
-      as[m * sh.apad + j] = (m < M && j < sh.rank) ? src.load_a(item, s, m, j) : __float2half(0.f);
-    }
-    // rank columns rpad..64*nsvc of a read as zero by the last SV chunk
-    for (int idx = tid; idx < 16 * (sh.apad - sh.rpad); idx += 256) {
-      const int m = idx / (sh.apad - sh.rpad), j = sh.rpad + idx % (sh.apad - sh.rpad);
-      as[m * sh.apad + j] = __float2half(0.f);
-    }
-  }
+  stream_stage<BITS, NMAT>(src, sh, item, M, lora0, lora1, xs, xc, a_l, tid);
   for (int idx = lane; idx < sh.mmax * pcols; idx += 64) plw[idx] = 0.f;
   __syncthreads();
-
-  // ---- per-lane constants ----
-  StreamLane<MP> ln;
-  {
-    const int sw = (li >> 1) & 7;
-#pragma unroll
-    for (int sp = 0; sp < 2; ++sp) ln.code_off[sp] = li * 128 + (((4 * sp + kb) ^ sw) << 4);
-    const int zrow = sh.mmax * sh.xstride;
-    if constexpr (BITS == 2) {
-      ln.h = kb >> 1;
-#pragma unroll
-      for (int p = 0; p < MP; ++p) {
-        const int m = (li & 7) + 8 * p;
-        const bool act = ((li >> 3) == ln.h) && m < M;
-        ln.xa[p] = act ? m * sh.xstride + 64 * kb : zrow;
-        ln.xstep[p] = act ? 256 : 0;
-        ln.xcb[p] = 0;
-      }
-      if constexpr (SZ2) {  // dword (row*4 + group%4); z 256 B after s
-        ln.szb = 4 * (li * 4 + ln.h);
-        ln.szstep = 8;
-        ln.cszb = 4 * (li * 4 + kb);
-        ln.czoff = 256;
-      } else {              // dword (row*2 + group%4/2) holds groups 2j, 2j+1; z 128 B after s
-        ln.szb = 8 * li;
-        ln.szstep = 4;
-        ln.cszb = 8 * li + 4 * (kb >> 1);
-        ln.czoff = 128;
-      }
-    } else {
-      ln.h = 0;
-      ln.xa[0] = li < M ? li * sh.xstride + 32 * kb : zrow;
-      ln.xstep[0] = li < M ? 128 : 0;
-      ln.xcb[0] = 0;
-      ln.szb = 8 * li;
-      ln.szstep = 4;
-      ln.cszb = 8 * li + 4 * (kb & 1);
-      ln.czoff = 128;
-    }
-  }
+  const StreamLane<MP> ln = stream_lane<BITS, MP, SZ2>(sh, M, li, kb);
 
   // ---- stream: consume chunk u while chunks u+1 .. u+D-1 are in flight ----
   const DecodeConsts dk = DecodeConsts::make();
@@ -669,6 +723,230 @@ __device__ void gemv_stream(const Src& src, const StreamShape& sh, int item, int
       if (next_seg(sg)) {
         r0 += 64;
         parities();
+      }
+    }
+  }
+  if constexpr (NMAT == 2) {
+    if (PU) {  // workgroup sum of the waves' partials
+      __syncthreads();
+      const float* pl0 = (const float*)(smem + L.pl);
+      const int wstride = sh.mmax * pcols;
+      for (int idx = tid; idx < M * sh.rank; idx += 256) {
+        const int m = idx / sh.rank, j = idx - m * sh.rank;
+        const int o = m * pcols + j;
+        src.store_post(item, m, j, pl0[o] + pl0[wstride + o] + pl0[2 * wstride + o] +
+                                       pl0[3 * wstride + o]);
+      }
+    }
+  }
+}
+
+// LDS of the K-split form's partial tiles: two buffers x 4 waves x NMAT x 16x16 floats.
+__host__ __device__ inline int stream_ks_bytes(int nmat) { return 2 * 4 * nmat * 256 * 4; }
+
+// K-split form of gemv_stream (same Src interface and results): all four waves
+// work on every tile of [t0, t1).  A tile's chunk list (matrix 0 code chunks,
+// its SV chunks or bias chunk, [matrix 1 code chunks, SV chunks,] post chunks)
+// is dealt round-robin, chunk c to wave c % 4, so each wave's serial chain is a
+// quarter of the tile; the waves' partial tiles (codes + zero-point correction
+// + low-rank term + bias) meet in LDS after one barrier per tile
+// (double-buffered, summed in wave order: deterministic), every wave forms the
+// whole tile, wave w stores tokens 4w..4w+3, and a wave holding a post chunk
+// consumes it after the barrier from the tile's inter values.  For launches
+// with few tiles per workgroup, where one wave per tile leaves each SIMD with a
+// single latency-bound wave.
+template <int BITS, int MP, int D, bool SYM, bool SZ2, int NMAT, class Src>
+__device__ void gemv_stream_ks(const Src& src, const StreamShape& sh, int item, int t0, int t1,
+                               unsigned char* smem) {
+  static_assert(NMAT == 1 || NMAT == 2, "one or two matrices per tile");
+  constexpr int NI = stream_ni<SZ2>();
+  constexpr int SLOT = stream_slot<SZ2>();
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, kb = lane >> 4;
+  const int M = src.m_rows(item);
+
+  StreamMat mat0 = src.mat(item, 0);
+  StreamMat mat1 = NMAT == 2 ? src.mat(item, 1) : mat0;
+  if (sh.rank <= 0) mat0.SV = mat1.SV = nullptr;
+  if (NMAT == 2) mat0.B = mat1.B = nullptr;
+  const bool lora0 = mat0.SV != nullptr;
+  const bool lora1 = NMAT == 2 && mat1.SV != nullptr;
+  const __half* PU = nullptr;
+  if constexpr (NMAT == 2) PU = sh.rank > 0 ? src.post(item) : nullptr;
+  const int pcols = PU ? 64 * sh.nsvc : 0;
+  const int seg0 = sh.nchunk + (lora0 ? sh.nsvc : (mat0.B ? 1 : 0));
+  const int seg1 = NMAT == 2 ? sh.nchunk + (lora1 ? sh.nsvc : 0) : 0;
+  const int seg2 = PU ? sh.nsvc : 0;
+  const int nmain = seg0 + seg1;
+  const int cpt = nmain + seg2;
+  auto seg_of = [&](int c, int& lc) -> int {
+    if (c < seg0) {
+      lc = c;
+      return 0;
+    }
+    if (c < nmain) {
+      lc = c - seg0;
+      return 1;
+    }
+    lc = c - nmain;
+    return 2;
+  };
+  auto seg_mat = [&](int sg) -> StreamMat {
+    if (sg == 0) return mat0;
+    if (sg == 1) return mat1;
+    return StreamMat{mat0.C, mat0.S, mat0.Z, PU, nullptr};
+  };
+
+  const StreamLds L = stream_lds(D, SLOT, sh.mmax, sh.K, BITS, sh.xstride, sh.apad, NMAT, pcols);
+  __half* xs = (__half*)(smem + L.xs);
+  float* xc = (float*)(smem + L.xc);
+  __half* a_l = (__half*)(smem + L.a);
+  unsigned char* ring = smem + L.ring + wave * D * SLOT;
+  float* tlw = (float*)(smem + L.tl) + wave * 256;
+  float* plw = (float*)(smem + L.pl) + wave * sh.mmax * pcols;
+  float* red = (float*)(smem + L.total);  // [buffer][wave][matrix][256]
+
+  const int ntile = t1 > t0 ? t1 - t0 : 0;
+  const int nw = cpt > wave ? (cpt - wave + 3) / 4 : 0;  // this wave's chunks per tile
+  const int total = ntile * nw;
+
+  const int piece0 = 16 * ((lane & 7) ^ (((lane >> 3) >> 1) & 7));
+  const int piece1 = 16 * ((lane & 7) ^ (((8 + (lane >> 3)) >> 1) & 7));
+  const void* dummy = (const void*)mat0.C;
+  StreamCursor<BITS, SZ2> cur;
+  cur.r0 = -1;
+  int i_t = 0, i_c = wave, i_sg = -1, issued = 0;
+  auto issue_next = [&]() {
+    int lc;
+    const int sg = seg_of(i_c, lc);
+    const int r0 = (t0 + i_t) * 16;
+    if (sg != i_sg || r0 != cur.r0) {
+      cur.r0 = r0;
+      cur.retarget(seg_mat(sg), sh, lane);
+      i_sg = sg;
+    }
+    unsigned char* slot = ring + cur.slot * SLOT;
+    if (sg < NMAT && lc < sh.nchunk)
+      stream_issue<BITS, SZ2>(cur.P, sh, lc, slot, lane, piece0, piece1);
+    else
+      stream_issue_sv<SZ2>(cur.P, sh, sg < NMAT ? lc - sh.nchunk : lc, slot, piece0, piece1,
+                           dummy);
+    if (++cur.slot == D) cur.slot = 0;
+    ++issued;
+    i_c += 4;
+    if (i_c >= cpt) {
+      i_c = wave;
+      ++i_t;
+    }
+  };
+
+  // ---- prologue ----
+  for (int u = 0; u < D - 1 && u < total; ++u) issue_next();
+  stream_stage<BITS, NMAT>(src, sh, item, M, lora0, lora1, xs, xc, a_l, tid);
+  for (int idx = lane; idx < sh.mmax * pcols; idx += 64) plw[idx] = 0.f;
+  __syncthreads();
+  const StreamLane<MP> ln = stream_lane<BITS, MP, SZ2>(sh, M, li, kb);
+  const DecodeConsts dk = DecodeConsts::make();
+
+  int slot = 0, buf = 0;
+  auto next_slot = [&]() -> const unsigned char* {
+    if (issued < total) {
+      wait_lgkm0();
+      issue_next();
+      wait_vmcnt<NI * (D - 1)>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    const unsigned char* sl = ring + slot * SLOT;
+    if (++slot == D) slot = 0;
+    return sl;
+  };
+
+  for (int tt = 0; tt < ntile; ++tt) {
+    const int r0 = (t0 + tt) * 16;
+    int par0, par1, cpar;
+    stream_parities<BITS, SZ2>(sh, r0, li, kb, ln.h, par0, par1, cpar);
+    f32x4 yacc0[MP], yacc1[MP];
+#pragma unroll
+    for (int p = 0; p < MP; ++p) yacc0[p] = yacc1[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 corr0 = {0.f, 0.f, 0.f, 0.f}, corr1 = corr0, ysv0 = corr0, ysv1 = corr0;
+    int c = wave;
+    for (; c < nmain; c += 4) {
+      const unsigned char* sl = next_slot();
+      int lc;
+      const int sg = seg_of(c, lc);
+      if (lc < sh.nchunk) {
+        if (sg == 0)
+          stream_consume<BITS, MP, SYM>(sl, lc, par0, par1, cpar, sh, xs, xc, yacc0, corr0, ln,
+                                        dk, li, kb);
+        else
+          stream_consume<BITS, MP, SYM>(sl, lc, par0, par1, cpar, sh, xs, xc, yacc1, corr1, ln,
+                                        dk, li, kb);
+      } else {
+        if (sg == 0 ? lora0 : lora1) {
+          const int j0 = 64 * (lc - sh.nchunk);
+          const __half* as = a_l + sg * 16 * sh.apad;
+          f32x4 ysv = sg == 0 ? ysv0 : ysv1;
+#pragma unroll
+          for (int sp = 0; sp < 2; ++sp) {
+            const f16x8 bv = *(const f16x8*)(sl + ln.code_off[sp]);
+            const f16x8 av = *(const f16x8*)(as + li * sh.apad + j0 + 32 * sp + 8 * kb);
+            ysv = mfma_16x16x32(av, bv, ysv);
+          }
+          if (sg == 0)
+            ysv0 = ysv;
+          else
+            ysv1 = ysv;
+        }
+        if (NMAT == 1 && mat0.B && lc == seg0 - 1) {  // bias rides in the last chunk
+          const float bn = __half2float(((const __half*)(sl + kStreamCodeBytes))[li]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ysv0[i] += bn;
+        }
+      }
+    }
+    // ---- partial tiles meet in LDS ----
+    float* rb = red + buf * 4 * NMAT * 256;
+    {
+      const f32x4 p0 = stream_merge<BITS, MP>(yacc0, kb) + corr0 + ysv0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rb[(wave * NMAT) * 256 + (4 * kb + i) * 16 + li] = p0[i];
+      if constexpr (NMAT == 2) {
+        const f32x4 p1 = stream_merge<BITS, MP>(yacc1, kb) + corr1 + ysv1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rb[(wave * NMAT + 1) * 256 + (4 * kb + i) * 16 + li] = p1[i];
+      }
+    }
+    __syncthreads();
+    f32x4 y0 = {0.f, 0.f, 0.f, 0.f}, y1 = y0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        y0[i] += rb[(w * NMAT) * 256 + (4 * kb + i) * 16 + li];
+        if (NMAT == 2) y1[i] += rb[(w * NMAT + 1) * 256 + (4 * kb + i) * 16 + li];
+      }
+    buf ^= 1;
+    const int n = r0 + li;
+    if constexpr (NMAT == 1) {
+      if (kb == wave && n < sh.N) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (4 * kb + i < M) src.store(item, 4 * kb + i, n, y0[i]);
+      }
+    } else {
+      const bool post = c < cpt;  // this wave holds a post chunk of the tile
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = 4 * kb + i;
+        const __half v = swiglu_fp16(y0[i], y1[i]);
+        if (kb == wave && m < M && n < sh.N) src.store_inter(item, m, n, v);
+        if (post) tlw[m * 16 + li] = n < sh.N ? __half2float(v) : 0.f;
+      }
+      for (; c < cpt; c += 4) {
+        const unsigned char* sl = next_slot();
+        stream_post(sl, c - nmain, M, tlw, plw, pcols, lane);
       }
     }
   }
