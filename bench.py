@@ -165,6 +165,85 @@ def pmc_workload():
 
 
 MOE_BATCHES = (1, 4, 16, 32)
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+PREFILL = ((2048, 1408, 2, "expert gate/up 2-bit"), (2048, 2048, 4, "attention q/k/v/o 4-bit"))
+
+
+def graph_time_us(fn, reps=20, trials=15):
+    """Median time of one call of fn, from hipGraph replays of `reps` calls
+    timed with HIP events (no host launch cost in the figure)."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    ts = []
+    for _ in range(trials):
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3 / reps)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def bench_prefill(dev):
+    """Config 1's prefill batches (M = 128, 512) on the MFMA GEMM path
+    (glq_gemm_lora): the whole op (x U launches + GEMM) and the GEMM kernel
+    alone (a = x U given), as MFMA utilisation F(M) / time against the fp16
+    dense peak, F(M) = 2 M (N K + r (K + N)); beside it torch's fp16 GEMM
+    (hipBLASLt) of the same M x N x K on a dense fp16 W, the library ceiling
+    for the shape."""
+    import torch
+
+    from glorcq_amd import format as fmt
+    from glorcq_amd import kernels
+
+    res = {}
+    for K, N, bits, name in PREFILL:
+        for M in (128, 512):
+            p = fmt.make_linear(K, N, bits=bits, group=GROUP, rank=RANK, M=M, seed=M + bits)
+            d = {k: getattr(p, k).to(dev) for k in ("codes", "scales", "zeros", "U", "SV", "x")}
+            xu = kernels.lowrank_xu(d["x"], d["U"])
+            out = torch.empty(M, N, dtype=torch.float16, device=dev)
+            W = torch.randn(N, K, generator=torch.Generator().manual_seed(1)).half().to(dev)
+
+            def op():
+                kernels.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"],
+                                                    bits, GROUP, U=d["U"], SV=d["SV"], out=out)
+
+            def gemm():
+                kernels.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"],
+                                                    bits, GROUP, SV=d["SV"], precomputed_xU=xu,
+                                                    out=out)
+
+            def dense():
+                torch.matmul(d["x"], W.t())
+
+            t_op, t_gemm, t_dense = graph_time_us(op), graph_time_us(gemm), graph_time_us(dense)
+            F = fmt.algorithmic_flops(M, K, N, RANK)
+            res[f"{name} M={M}"] = {
+                "K": K, "N": N, "bits": bits, "M": M, "flops": F,
+                "op_us": round(t_op, 2), "gemm_kernel_us": round(t_gemm, 2),
+                "gemm_tflops": round(F / t_gemm / 1e6, 1),
+                "mfma_util_vs_fp16_peak": round(F / t_gemm / 1e6 / MFMA_FP16_PEAK_TFLOPS, 4),
+                "torch_fp16_dense_gemm_us": round(t_dense, 2),
+                "torch_fp16_dense_tflops": round(2 * M * N * K / t_dense / 1e6, 1)}
+            log(f"prefill {name} M={M}: op {t_op:.2f} us, GEMM {t_gemm:.2f} us "
+                f"({F / t_gemm / 1e6:.0f} TF/s), dense fp16 {t_dense:.2f} us")
+    return res
 
 
 def bench_moe(dev, seed=6, reps=20, trials=15):
@@ -326,6 +405,8 @@ def main():
         "single_call_config0_us": round(single_ms * 1e3, 2),
         "gemv_alone_matches_step_output": same,
     }
+    log("prefill GEMM (config 1, M = 128 and 512)")
+    result["prefill_gemm"] = bench_prefill(dev)
     if not args.no_moe:
         log("MoE block decode step (config 2), hipGraph replays")
         moe = bench_moe(dev)

@@ -68,6 +68,15 @@ SIGNATURES = {
         _vp, _i64,                      # xu, xu_stride
         _vp, _i64, _vp,                 # workspace, bytes, stream
     ]),
+    "glq_gemm_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "glq_gemm_lora": (_c_int, [
+        _vp, _i64, _i64, _i64,          # x, M, K, N
+        _vp, _c_int, _vp, _vp,          # codes, bits, scales, zeros
+        _i64, _c_int,                   # group, sym
+        _vp, _vp, _i64, _vp,            # U, SV, rank, xU
+        _vp, _vp,                       # bias, y
+        _vp, _i64, _vp,                 # workspace, bytes, stream
+    ]),
     "glq_moe_workspace_bytes": (_i64, [ctypes.POINTER(MoeParams)]),
     "glq_moe_decode": (_c_int, [ctypes.POINTER(MoeParams), _vp, _i64, _vp]),
     "glq_unpack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _c_int, _vp, _vp]),

@@ -82,7 +82,10 @@ def packed_dequant_matmul_fused(x: torch.Tensor, codes: torch.Tensor, scales: to
                                 precomputed_xU: torch.Tensor | None = None,
                                 bias: torch.Tensor | None = None,
                                 out: torch.Tensor | None = None) -> torch.Tensor:
-    """y = dequant(codes) x + (x U) SV^T + bias, fp16 (M, N), one HIP launch.
+    """y = dequant(codes) x + (x U) SV^T + bias, fp16 (M, N).
+
+    M <= 16: the streaming GEMV (glq_gemv_lora); M > 16 with group 128: the
+    MFMA GEMM (glq_gemm_lora); other groups: the GEMV per 16-row block.
 
     x (M, K) fp16; codes (N, K*bits/32) int32; scales/zeros (N, K/groupsize)
     fp16; U (K, r) fp16; SV (N, r) fp16; precomputed_xU (M, r) fp16 replaces
@@ -132,6 +135,17 @@ def packed_dequant_matmul_fused(x: torch.Tensor, codes: torch.Tensor, scales: to
     if M == 0 or N == 0:
         return out
     stream = _lib.stream_handle(x.device)
+    if M > GEMV_MAX_M and groupsize == 128:
+        # prefill: one MFMA GEMM over all M rows (glq_gemm_lora)
+        nbytes = lib.glq_gemm_workspace_bytes(M, K, N, rank if precomputed_xU is None else 0)
+        ws = workspace(x.device, nbytes)
+        rc = lib.glq_gemm_lora(
+            x.data_ptr(), M, K, N, codes.data_ptr(), bits, scales.data_ptr(), _lib.ptr(zeros),
+            groupsize, int(bool(sym)), _lib.ptr(U if precomputed_xU is None else None),
+            _lib.ptr(SV), rank, _lib.ptr(precomputed_xU), _lib.ptr(bias), out.data_ptr(),
+            ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, "glq_gemm_lora")
+        return out
     for m0 in range(0, M, GEMV_MAX_M):
         m1 = min(M, m0 + GEMV_MAX_M)
         mb = m1 - m0
@@ -227,6 +241,25 @@ def lowrank_xu(x: torch.Tensor, U: torch.Tensor, out: torch.Tensor | None = None
     elif tuple(out.shape) != shape:
         raise RuntimeError(f"out must be {shape}")
     if M == 0 or E == 0:
+        return out
+    if M > GEMV_MAX_M:
+        if batched:
+            raise RuntimeError(f"batched x U takes M <= {GEMV_MAX_M}")
+        # one x (M, K), one U: 16-row blocks as items sharing U (stride 0)
+        full, tail = divmod(M, GEMV_MAX_M)
+        nbytes = lib.glq_lowrank_workspace_bytes(max(full, 1), GEMV_MAX_M, K, r)
+        ws = workspace(x.device, nbytes)
+        stream = _lib.stream_handle(x.device)
+        if full:
+            _lib.check(lib.glq_lowrank_xu_batched(
+                full, x.data_ptr(), GEMV_MAX_M * K, GEMV_MAX_M, K, U.data_ptr(), 0, r,
+                out.data_ptr(), GEMV_MAX_M * r, ws.data_ptr(), ws.numel(), stream),
+                "glq_lowrank_xu_batched")
+        if tail:
+            m0 = full * GEMV_MAX_M
+            _lib.check(lib.glq_lowrank_xu_batched(
+                1, x[m0:].data_ptr(), 0, tail, K, U.data_ptr(), 0, r, out[m0:].data_ptr(), 0,
+                ws.data_ptr(), ws.numel(), stream), "glq_lowrank_xu_batched")
         return out
     nbytes = lib.glq_lowrank_workspace_bytes(E, M, K, r)
     ws = workspace(x.device, nbytes)

@@ -122,6 +122,24 @@ int glq_lowrank_xu_batched(int64_t items, const void* x, int64_t x_stride, int64
                            void* stream);
 
 /*
+ * Prefill GEMM (any M, built for M > 16): y = dequant(codes) x + (x U) SV^T
+ * + bias with the same arguments and results as glq_gemv_lora.  Replaces the
+ * reference's gptq_dequant_gemm_kernel path (inference/kernels/gptq_matmul.cu:
+ * 111-213, taken for B > 4) and the LoRA tail of GLoRCQLinear.forward
+ * (inference/quantized_linear.py:338-349).  Group 128.  Codes decode into fp16
+ * operands of v_mfma_f32_16x16x32_f16 (64-token x 64-row tiles, fp32
+ * accumulation); a = fp16(x U) comes from xU or from the low-rank launches of
+ * glq_lowrank_xu_batched into the workspace (glq_gemm_workspace_bytes).
+ */
+int64_t glq_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t rank);
+int glq_gemm_lora(const void* x, int64_t M, int64_t K, int64_t N,
+                  const int32_t* codes, int bits, const void* scales,
+                  const void* zeros, int64_t group, int sym,
+                  const void* U, const void* SV, int64_t rank, const void* xU,
+                  const void* bias, void* y, void* workspace,
+                  int64_t workspace_bytes, void* stream);
+
+/*
  * One MoE block at decode: router, top-k dispatch, routed SwiGLU experts with
  * cluster-shared low-rank correction, sigmoid-gated shared expert, combine.
  * Replaces GraphCompatibleMoeBlock.forward (inference/moe_block.py:381-436:

@@ -1,0 +1,100 @@
+"""GPU parity of the prefill MFMA GEMM (glq_gemm_lora, M > 16) against the CPU
+oracle, at the bars of test_gemv_gpu (fp32 reference fallback, exact fp64 sum,
+and for 2-bit the fp16 CPU fallback): |y - y_ref| <= 1e-3 + 1e-2 |y_ref|.
+The reference's M > 4 path is gptq_dequant_gemm_kernel
+(inference/kernels/gptq_matmul.cu:111-213); its fallback is the same
+_gptq_pytorch_fallback as the GEMV's."""
+
+import ctypes
+
+import pytest
+import torch
+
+from glorcq_amd import _lib
+from glorcq_amd import format as fmt
+from glorcq_amd import kernels as K_
+from test_gemv_gpu import assert_parity, oracle_y, to
+
+
+def test_gemm_workspace_sizes():
+    lib = _lib.load()
+    assert lib.glq_gemm_workspace_bytes(512, 2048, 1408, 0) == 0
+    n = lib.glq_gemm_workspace_bytes(512, 2048, 1408, 64)
+    assert n >= 512 * 64 * 2 and n % 256 == 0
+    # argument errors come back before any launch
+    rc = lib.glq_gemm_lora(None, 64, 2048, 64, None, 2, None, None, 64, 0, None, None, 0, None,
+                           None, None, None, 0, None)
+    assert rc == 1 and b"group" in lib.glq_last_error()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,K,N,bits,M", [
+    ("expert gate/up 2b", 2048, 1408, 2, 128),
+    ("expert gate/up 2b", 2048, 1408, 2, 512),
+    ("expert down 2b", 1408, 2048, 2, 128),
+    ("attn q/k/v/o 4b", 2048, 2048, 4, 128),
+    ("attn q/k/v/o 4b", 2048, 2048, 4, 512),
+])
+def test_config1_prefill(gpu, name, K, N, bits, M):
+    """BASELINE config 1's GEMM batch sizes."""
+    p = fmt.make_linear(K, N, bits=bits, group=128, rank=64, M=M, seed=K + N + M + bits)
+    d = to(p, gpu)
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], bits, 128,
+                                       U=d["U"], SV=d["SV"])
+    assert_parity(y, oracle_y(p), f"{name} M={M}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K,N,M,bits,rank", [
+    (384, 200, 17, 2, 16),     # odd group count, N and M tails
+    (1408, 70, 65, 4, 40),     # rank not a multiple of 32
+    (256, 64, 130, 2, 64),     # one chunk
+    (1024, 130, 300, 4, 8),
+])
+def test_edge_shapes(gpu, K, N, M, bits, rank):
+    p = fmt.make_linear(K, N, bits=bits, group=128, rank=rank, M=M, seed=K * 7 + M)
+    d = to(p, gpu)
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], bits, 128,
+                                       U=d["U"], SV=d["SV"])
+    assert_parity(y, oracle_y(p), f"K={K} N={N} M={M} b={bits} r={rank}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bits", [2, 4])
+def test_sym_bias_nolora(gpu, bits):
+    g = torch.Generator().manual_seed(3)
+    for sym in (True, False):
+        p = fmt.make_linear(1024, 192, bits=bits, rank=32, M=48, seed=30 + bits + sym, sym=sym)
+        d = to(p, gpu)
+        bias = (torch.randn(192, generator=g) * 0.1).half()
+        y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"],
+                                           None if sym else d["zeros"], bits, 128, sym=sym,
+                                           bias=bias.to(gpu))
+        assert_parity(y, oracle_y(p, lora=False, bias=bias), f"sym={sym} b={bits} no-lora+bias")
+
+
+@pytest.mark.gpu
+def test_precomputed_xu(gpu):
+    p = fmt.make_linear(2048, 256, bits=2, rank=64, M=96, seed=41)
+    d = to(p, gpu)
+    xu = (p.x.float() @ p.U.float()).half()
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], 2, 128,
+                                       SV=d["SV"], precomputed_xU=xu.to(gpu))
+    assert_parity(y, oracle_y(p, xu=xu), "precomputed xU")
+
+
+@pytest.mark.gpu
+def test_gemm_matches_gemv_blocks(gpu):
+    """The GEMM and the 16-row GEMV blocks compute the same function: both
+    within the bar of the oracle, and close to each other."""
+    p = fmt.make_linear(2048, 512, bits=2, rank=64, M=64, seed=43)
+    d = to(p, gpu)
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], 2, 128,
+                                       U=d["U"], SV=d["SV"])
+    blocks = torch.cat([K_.packed_dequant_matmul_fused(d["x"][i:i + 16], d["codes"], d["scales"],
+                                                       d["zeros"], 2, 128, U=d["U"], SV=d["SV"])
+                        for i in range(0, 64, 16)])
+    torch.cuda.synchronize()
+    diff = (y.float() - blocks.float()).abs()
+    assert float(diff.max()) <= 2e-3 + 1e-2 * float(blocks.float().abs().max())
+    assert_parity(y, oracle_y(p), "GEMM M=64")
