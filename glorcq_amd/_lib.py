@@ -77,6 +77,15 @@ SIGNATURES = {
         _vp, _vp,                       # bias, y
         _vp, _i64, _vp,                 # workspace, bytes, stream
     ]),
+    "glq_turbo_gemv_batched": (_c_int, [
+        _i64, _vp, _i64, _i64, _i64, _i64,  # items, x_rot, x_stride, M, K, N
+        _vp, _i64, _vp, _i64,               # codes, codes_stride, norms, norms_stride
+        _vp,                                # centroids
+        _vp, _i64, _vp, _i64, _i64,         # xU, xu_stride, SV, sv_stride, rank
+        _vp, _i64,                          # bias, bias_stride
+        _vp, _i64, _vp,                     # y, y_stride, stream
+    ]),
+    "glq_rht": (_c_int, [_vp, _c_int, _i64, _i64, _vp, _c_int, _vp, _c_int, _vp]),
     "glq_moe_workspace_bytes": (_i64, [ctypes.POINTER(MoeParams)]),
     "glq_moe_decode": (_c_int, [ctypes.POINTER(MoeParams), _vp, _i64, _vp]),
     "glq_unpack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _c_int, _vp, _vp]),

@@ -259,8 +259,6 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) {
 
 // x U for the GEMM path: the batched low-rank entry point over 16-token
 // blocks of x (U shared: stride 0); a lands at the end of the workspace.
-int64_t gemm_lowrank_blocks(int64_t M) { return (M + 15) / 16; }
-
 int64_t gemm_workspace_need(int64_t M, int64_t K, int64_t rank) {
   if (rank <= 0) return 0;
   const int64_t full = M / 16, tail = M % 16;

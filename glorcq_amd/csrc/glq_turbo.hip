@@ -1,0 +1,354 @@
+// TurboQuant 2-bit codebook GEMV/GEMM (the reference's own 2-bit expert format):
+//
+//   y[m][n] = fp16(norms[n] * sum_k C[q[n][k]] * x_rot[m][k])
+//
+// (inference/kernels/turbo_matmul.cu:46-137 GEMV, :150-245 GEMM, :329-415 the
+// grouped form; inference/kernels/__init__.py:121-146 the fallback).  q are
+// 2-bit codebook indices packed 4 per byte LSB-first, i.e. exactly this
+// library's 2-bit int32 container read little-endian; C is a 4-entry fp32
+// codebook; x_rot the rotated input (x Pi^T, or the randomized Hadamard
+// transform of x).
+//
+// turbo_gemv_kernel: one workgroup per (item, 16-token block, 16 rows).  The
+// four waves split K into contiguous quarters; the token rows of x_rot are
+// staged in LDS per K segment (the whole K unless 16 tokens of a long row
+// would not fit) in the decode order of glq_gemv_core.h (codes c and c+8 of a
+// word share a dword); partial sums of the waves meet in LDS at the end.
+//
+// Decode is a byte permutation: for codes a = q_c and b = q_{c+8} of a word,
+// the selector ((w >> 2c) & 0x00030003) * 0x202 + 0x01000100 picks bytes
+// (2a, 2a+1, 2b, 2b+1) of the fp16 codebook {C0, C1, C2, C3} held in two
+// dwords, so one v_perm_b32 yields a pair of MFMA operands.  The codebook is
+// split into fp16 hi + lo parts (C = hi + lo to ~22 bits), one MFMA each, so
+// the fp32-accumulated sum carries fp32-level accuracy like the reference's
+// fp32 FMA loop; y = fp16(acc * norm) as in the reference.
+#include <algorithm>
+
+#include "glq_gemv_core.h"
+
+namespace glq {
+
+constexpr int kTurboXBudget = 64 * 1024;  // LDS bytes for one x segment
+
+struct TurboArgs {
+  const __half* x;         // x_rot (items, M, K) fp16
+  int64_t x_es;            // elements between items (0: one x for all)
+  const uint32_t* codes;   // (items, N, K/16) int32 words (= (N, K/4) bytes)
+  int64_t c_es;
+  const float* norms;      // (items, N)
+  int64_t n_es;
+  const float* cent;       // (4,) fp32 codebook
+  const __half* xu;        // a = fp16(x U): (items, M, rank), or nullptr
+  int64_t xu_es;
+  const __half* sv;        // SV (items, N, rank), or nullptr: no low-rank term
+  int64_t sv_es;
+  const __half* bias;      // (items, N), or nullptr
+  int64_t bias_es;
+  __half* y;               // (items, M, N)
+  int64_t y_es;
+  int M, K, N, kw;
+  int rank, rpad, apad;    // low-rank width, padded to 32, LDS row stride of a
+  int segsteps;            // 256-code steps per staged x segment
+  int xstride;             // halves per staged token row (segment + 8)
+  int rwgs, twgs;          // row blocks (16 rows) and token blocks (16 tokens) per item
+};
+
+// fp16 codebook in v_perm_b32 form: lo dword {C0, C1}, hi dword {C2, C3}.
+struct TurboLut {
+  uint32_t lo, hi;
+};
+
+__device__ __forceinline__ TurboLut turbo_lut(const float* c, bool residual) {
+  uint32_t h[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const __half hi = __float2half(c[i]);
+    const __half v = residual ? __float2half(c[i] - __half2float(hi)) : hi;
+    h[i] = __half_as_ushort(v);
+  }
+  return TurboLut{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+}
+
+// One code word (16 codes) -> the two MFMA operand slices in decode2's order
+// (s0: codes 0,8,1,9,2,10,3,11; s1: codes 4,12,5,13,6,14,7,15), for the hi
+// and for the lo codebook.
+__device__ __forceinline__ void turbo_decode(uint32_t w, const TurboLut& H, const TurboLut& L,
+                                             f16x8& s0h, f16x8& s1h, f16x8& s0l, f16x8& s1l) {
+  u32x4 ah, bh, al, bl;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t sa = ((w >> (2 * j)) & 0x00030003u) * 0x202u + 0x01000100u;
+    const uint32_t sb = ((w >> (8 + 2 * j)) & 0x00030003u) * 0x202u + 0x01000100u;
+    ah[j] = __builtin_amdgcn_perm(H.hi, H.lo, sa);
+    bh[j] = __builtin_amdgcn_perm(H.hi, H.lo, sb);
+    al[j] = __builtin_amdgcn_perm(L.hi, L.lo, sa);
+    bl[j] = __builtin_amdgcn_perm(L.hi, L.lo, sb);
+  }
+  s0h = __builtin_bit_cast(f16x8, ah);
+  s1h = __builtin_bit_cast(f16x8, bh);
+  s0l = __builtin_bit_cast(f16x8, al);
+  s1l = __builtin_bit_cast(f16x8, bl);
+}
+
+__global__ __launch_bounds__(256) void turbo_gemv_kernel(TurboArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* red = (float*)smem;                  // [4 waves][4][64] partial sums
+  __half* a_l = (__half*)(smem + 4096);       // [16][apad] low-rank factor a
+  __half* xs = a_l + 16 * a.apad;             // [mr][xstride], one K segment
+  const int per_item = a.rwgs * a.twgs;
+  const int item = blockIdx.x / per_item;
+  const int rem = blockIdx.x - item * per_item;
+  const int tb = rem / a.rwgs, rb = rem - tb * a.rwgs;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = tid >> 6, li = lane & 15, kb = lane >> 4;
+  const int m0 = 16 * tb, mr = min(16, a.M - m0);  // token rows of this block
+  const __half* X = a.x + (int64_t)item * a.x_es + (int64_t)m0 * a.K;
+
+  const TurboLut H = turbo_lut(a.cent, false), L = turbo_lut(a.cent, true);
+  const int row = min(16 * rb + li, a.N - 1);
+  const uint32_t* crow = a.codes + (int64_t)item * a.c_es + (int64_t)row * a.kw;
+  const int wlast = a.kw - 4;  // last whole 16-byte piece (kw is a multiple of 4)
+  const __half* xr = xs + min(li, mr - 1) * a.xstride;
+  const int nsteps = (a.K + 255) >> 8;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  constexpr int PF = 4;  // 256-code steps of codes in flight per wave
+
+  for (int sb = 0; sb < nsteps; sb += a.segsteps) {
+    const int se = min(nsteps, sb + a.segsteps);
+    const int q = (se - sb + 3) >> 2;
+    const int j0 = sb + wave * q;                 // this wave's first step
+    const int jn = max(0, min(se, j0 + q) - j0);  // and its step count
+    // a step of a row is 16 words; lane kb holds words 4kb..4kb+3 (clamped:
+    // words past the row end meet zero x and add nothing)
+    u32x4 buf[PF];
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+      buf[p] = p < jn ? *(const u32x4*)(crow + min(16 * (j0 + p) + 4 * kb, wlast))
+                      : u32x4{0, 0, 0, 0};
+    if (sb > 0) __syncthreads();  // every wave is done with the previous segment
+    const int nblk = (se - sb) * 16;  // 16-code blocks of the segment
+    for (int idx = tid; idx < mr * nblk; idx += 256) {
+      const int m = idx / nblk, blk = idx - m * nblk;
+      const int k = sb * 256 + blk * 16;
+      f16x8 o0 = f16x8{}, o1 = f16x8{};
+      if (k < a.K) {
+        const f16x8 v0 = *(const f16x8*)(X + (int64_t)m * a.K + k);
+        const f16x8 v1 = *(const f16x8*)(X + (int64_t)m * a.K + k + 8);
+        o0 = __builtin_shufflevector(v0, v1, 0, 8, 1, 9, 2, 10, 3, 11);
+        o1 = __builtin_shufflevector(v0, v1, 4, 12, 5, 13, 6, 14, 7, 15);
+      }
+      f16x8* dst = (f16x8*)(xs + m * a.xstride + blk * 16);
+      dst[0] = o0;
+      dst[1] = o1;
+    }
+    __syncthreads();
+    for (int jj = 0; jj < jn; jj += PF) {
+#pragma unroll
+      for (int p = 0; p < PF; ++p) {
+        const int j = jj + p;
+        if (j >= jn) break;
+        const u32x4 w = buf[p];
+        if (j + PF < jn) buf[p] = *(const u32x4*)(crow + min(16 * (j0 + j + PF) + 4 * kb, wlast));
+        const __half* xk = xr + (j0 + j - sb) * 256 + 64 * kb;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f16x8 s0h, s1h, s0l, s1l;
+          turbo_decode(w[i], H, L, s0h, s1h, s0l, s1l);
+          const f16x8 x0 = *(const f16x8*)(xk + 16 * i);
+          const f16x8 x1 = *(const f16x8*)(xk + 16 * i + 8);
+          acc = mfma_16x16x32(x0, s0h, acc);
+          acc = mfma_16x16x32(x1, s1h, acc);
+          acc = mfma_16x16x32(x0, s0l, acc);
+          acc = mfma_16x16x32(x1, s1l, acc);
+        }
+      }
+    }
+  }
+  // acc[i] of lane (li, kb): token 4kb + i, row li of the block
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
+  const bool lora = a.sv != nullptr;
+  if (lora) {
+    for (int idx = tid; idx < mr * a.rpad; idx += 256) {
+      const int m = idx / a.rpad, j = idx - m * a.rpad;
+      a_l[m * a.apad + j] = j < a.rank
+                                ? a.xu[(int64_t)item * a.xu_es + (int64_t)(m0 + m) * a.rank + j]
+                                : __float2half(0.f);
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // y = norm * acc + a SV^T + bias, rounded once to fp16
+    const int r = 16 * rb + li, rc = min(r, a.N - 1);
+    const float nr = a.norms[(int64_t)item * a.n_es + rc];
+    f32x4 y;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      y[i] = nr * (red[i * 64 + lane] + red[(4 + i) * 64 + lane] + red[(8 + i) * 64 + lane] +
+                   red[(12 + i) * 64 + lane]);
+    if (lora) {
+      // A = a (token rows), B = SV rows: D[token 4kb + i][row li], acc's layout
+      const __half* svr = a.sv + (int64_t)item * a.sv_es + (int64_t)rc * a.rank;
+      const __half* ar = a_l + min(li, mr - 1) * a.apad;
+      for (int s0 = 0; s0 < a.rpad; s0 += 32) {
+        const int j = s0 + 8 * kb;
+        const f16x8 av = *(const f16x8*)(ar + j);
+        const f16x8 bv = j < a.rank ? *(const f16x8*)(svr + j) : f16x8{};
+        y = mfma_16x16x32(av, bv, y);
+      }
+    }
+    const float bb = a.bias ? __half2float(a.bias[(int64_t)item * a.bias_es + rc]) : 0.f;
+    if (r < a.N) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = 4 * kb + i;
+        if (m < mr) a.y[(int64_t)item * a.y_es + (int64_t)(m0 + m) * a.N + r] = __float2half(y[i] + bb);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Randomized Hadamard transform of rows of length d (a power of two):
+//   forward: y = (1/sqrt(d)) H diag(signs) x
+//   inverse: y = diag(signs) (1/sqrt(d)) H x
+// (hadamard_rotation.py:52-67 rht_forward and :70-86 rht_backward; H is the
+// Sylvester, natural-order Hadamard matrix that the external
+// fast-hadamard-transform package applies).  The hot-path call is
+// rht_forward(x.float(), signs).half() (inference/moe_block.py:351,525,649,
+// 840): fp16 in, fp32 arithmetic, fp16 out.  One workgroup per row: the row in
+// LDS as fp32, log2(d) butterfly passes with a barrier each.
+// ---------------------------------------------------------------------------
+template <class TI, class TO>
+__global__ __launch_bounds__(256) void rht_kernel(const TI* __restrict__ x,
+                                                  const float* __restrict__ signs,
+                                                  TO* __restrict__ y, int d, int logd,
+                                                  float scale, int inverse) {
+  extern __shared__ float v[];
+  const TI* xr = x + (int64_t)blockIdx.x * d;
+  for (int i = threadIdx.x; i < d; i += 256) {
+    const float xv = (float)xr[i];
+    v[i] = inverse ? xv : xv * signs[i];
+  }
+  __syncthreads();
+  for (int s = 0; s < logd; ++s) {
+    const int h = 1 << s;
+    for (int p = threadIdx.x; p < d / 2; p += 256) {
+      const int i = ((p >> s) << (s + 1)) | (p & (h - 1)), j = i + h;
+      const float u = v[i], w = v[j];
+      v[i] = u + w;
+      v[j] = u - w;
+    }
+    __syncthreads();
+  }
+  TO* yr = y + (int64_t)blockIdx.x * d;
+  for (int i = threadIdx.x; i < d; i += 256) {
+    const float o = v[i] * scale;
+    yr[i] = (TO)(inverse ? o * signs[i] : o);
+  }
+}
+
+}  // namespace glq
+
+extern "C" int glq_turbo_gemv_batched(int64_t items, const void* x_rot, int64_t x_stride,
+                                      int64_t M, int64_t K, int64_t N, const int32_t* codes,
+                                      int64_t codes_stride, const float* norms,
+                                      int64_t norms_stride, const float* centroids,
+                                      const void* xU, int64_t xu_stride, const void* SV,
+                                      int64_t sv_stride, int64_t rank, const void* bias,
+                                      int64_t bias_stride, void* y, int64_t y_stride,
+                                      void* stream) {
+  using namespace glq;
+  clear_error();
+  GLQ_CHECK(items >= 0 && M >= 0 && K >= 0 && N >= 0, "negative size");
+  if (items == 0 || M == 0 || N == 0) return GLQ_OK;
+  GLQ_CHECK(K > 0 && K % 64 == 0 && K < (1 << 24),
+            "K=%lld must be a positive multiple of 64 (whole 16-byte code pieces per row)",
+            (long long)K);
+  GLQ_CHECK(M < (1ll << 24) && N < (1ll << 26), "M or N too large");
+  GLQ_CHECK(x_rot && codes && norms && centroids && y, "null data pointer");
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  GLQ_CHECK(al16(x_rot) && al16(codes), "x_rot and codes must be 16-byte aligned");
+  GLQ_CHECK(items == 1 || (x_stride % 8 == 0 && codes_stride % 4 == 0),
+            "item strides must keep 16-byte alignment");
+  TurboArgs a;
+  a.x = (const __half*)x_rot;
+  a.x_es = x_stride;
+  a.codes = (const uint32_t*)codes;
+  a.c_es = codes_stride;
+  a.norms = norms;
+  a.n_es = norms_stride;
+  a.cent = centroids;
+  const bool lora = SV != nullptr && rank > 0;
+  GLQ_CHECK(!lora || (rank % 8 == 0 && rank <= 256),
+            "rank=%lld must be a multiple of 8 up to 256", (long long)rank);
+  GLQ_CHECK(!lora || xU, "SV given without the low-rank factor xU = x U");
+  GLQ_CHECK(!lora || (al16(SV) && (items == 1 || sv_stride % 8 == 0)),
+            "SV must be 16-byte aligned");
+  a.xu = lora ? (const __half*)xU : nullptr;
+  a.xu_es = xu_stride;
+  a.sv = lora ? (const __half*)SV : nullptr;
+  a.sv_es = sv_stride;
+  a.bias = (const __half*)bias;
+  a.bias_es = bias_stride;
+  a.rank = lora ? (int)rank : 0;
+  a.rpad = (int)align_up(a.rank, 32);
+  a.apad = a.rpad + 8;
+  a.y = (__half*)y;
+  a.y_es = y_stride;
+  a.M = (int)M;
+  a.K = (int)K;
+  a.N = (int)N;
+  a.kw = (int)(K / 16);
+  const int mr = (int)std::min<int64_t>(16, M);
+  const int nsteps = (int)((K + 255) / 256);
+  const int fit = (kTurboXBudget / (2 * mr) - 8) / 256;  // steps of a segment that fit
+  a.segsteps = std::max(1, std::min(nsteps, fit));
+  a.xstride = a.segsteps * 256 + 8;
+  a.rwgs = (int)((N + 15) / 16);
+  a.twgs = (int)((M + 15) / 16);
+  const size_t lds = 4096 + (size_t)16 * a.apad * 2 + (size_t)mr * a.xstride * 2;
+  static size_t attr = 64 * 1024;
+  int rc = set_lds_limit(turbo_gemv_kernel, lds, attr);
+  if (rc) return rc;
+  const int64_t grid = items * a.rwgs * a.twgs;
+  GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
+  turbo_gemv_kernel<<<dim3((unsigned)grid), dim3(256), lds, (hipStream_t)stream>>>(a);
+  GLQ_LAUNCH_CHECK("turbo_gemv_kernel");
+  return GLQ_OK;
+}
+
+extern "C" int glq_rht(const void* x, int x_fp32, int64_t rows, int64_t d, const float* signs,
+                       int inverse, void* y, int y_fp32, void* stream) {
+  using namespace glq;
+  clear_error();
+  GLQ_CHECK(rows >= 0 && d >= 0, "negative size");
+  if (rows == 0) return GLQ_OK;
+  GLQ_CHECK(d >= 2 && d <= 32768 && (d & (d - 1)) == 0,
+            "d=%lld must be a power of two in [2, 32768]", (long long)d);
+  GLQ_CHECK(rows < (1ll << 31), "too many rows");
+  GLQ_CHECK(x && signs && y, "null data pointer");
+  GLQ_CHECK(x != y, "y may not alias x");
+  const size_t lds = (size_t)d * 4;
+  int logd = 0;
+  while ((1ll << logd) < d) ++logd;
+  const float scale = 1.0f / sqrtf((float)d);
+  const dim3 grid((unsigned)rows), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  int rc;
+#define GLQ_RHT_LAUNCH(TI, TO)                                                        \
+  do {                                                                                \
+    static size_t attr = 64 * 1024;                                                   \
+    rc = set_lds_limit(rht_kernel<TI, TO>, lds, attr);                                \
+    if (rc) return rc;                                                                \
+    rht_kernel<TI, TO><<<grid, block, lds, s>>>((const TI*)x, signs, (TO*)y, (int)d, logd, \
+                                               scale, inverse ? 1 : 0);               \
+  } while (0)
+  if (!x_fp32 && !y_fp32) GLQ_RHT_LAUNCH(__half, __half);
+  else if (!x_fp32 && y_fp32) GLQ_RHT_LAUNCH(__half, float);
+  else if (x_fp32 && !y_fp32) GLQ_RHT_LAUNCH(float, __half);
+  else GLQ_RHT_LAUNCH(float, float);
+#undef GLQ_RHT_LAUNCH
+  GLQ_LAUNCH_CHECK("rht_kernel");
+  return GLQ_OK;
+}

@@ -219,3 +219,84 @@ def moe_step_bytes(p: MoEProblem, active_experts: int, active_clusters: dict) ->
     total += 2 * (p.E + (1 if p.shared is not None else 0)) * p.H
     total += 2 * 2 * p.B * p.H
     return total
+
+
+# ---------------------------------------------------------------------------
+# TurboQuant codec (the reference's 2-bit expert format)
+# ---------------------------------------------------------------------------
+# Lloyd-Max quantizer of N(0, 1) at 4 levels; TurboQuant's 2-bit codebook for
+# unit rows of dimension d is this scaled by 1/sqrt(d) (turbo_weight_quantizer.py
+# draws it from the external turboquant package; only its shape matters here).
+LLOYD_MAX_2BIT = (-1.5104, -0.4528, 0.4528, 1.5104)
+
+
+@dataclass
+class TurboProblem:
+    """`items` TurboQuant layers of one shape plus their inputs, on the CPU."""
+
+    packed: torch.Tensor     # (items, N, K/4) uint8: 4 indices per byte, LSB-first
+    norms: torch.Tensor      # (items, N) fp32
+    centroids: torch.Tensor  # (4,) fp32
+    x: torch.Tensor          # (items, M, K) fp16, the unrotated input
+    x_rot: torch.Tensor      # (items, M, K) fp16, the rotated input
+    U: torch.Tensor | None   # (K, r) fp16 (shared by the items)
+    SV: torch.Tensor | None  # (items, N, r) fp16
+    bias: torch.Tensor | None  # (items, N) fp16
+
+    @property
+    def items(self) -> int:
+        return self.packed.shape[0]
+
+    @property
+    def N(self) -> int:
+        return self.packed.shape[1]
+
+    @property
+    def K(self) -> int:
+        return self.packed.shape[2] * 4
+
+    @property
+    def M(self) -> int:
+        return self.x.shape[1]
+
+    def words(self) -> torch.Tensor:
+        """The packed bytes as (items, N, K/16) int32 words (no copy of bits)."""
+        return self.packed.contiguous().view(torch.int32)
+
+
+def make_turbo(K: int, N: int, M: int = 1, items: int = 1, seed: int = 0, rank: int = 0,
+               bias: bool = False, dist: str = "lloyd") -> TurboProblem:
+    """Seeded TurboQuant problem.  Draw order (one CPU generator): packed bytes
+    (items,N,K/4) uniform; norms (items,N) = |N(0,1)| + 0.1; centroids; x
+    (items,M,K) = N(0,1); x_rot = N(0,1) (an orthogonal rotation of Gaussian x
+    is Gaussian); then U, SV (N(0,0.01)) and bias (N(0,0.1)) when asked.
+    dist='lloyd': centroids = LLOYD_MAX_2BIT / sqrt(K) (realistic scale);
+    dist='randn': centroids = N(0,1), the reference's kernel test data
+    (inference/kernels/test_kernels.py:48-80)."""
+    g = torch.Generator().manual_seed(seed)
+    packed = torch.randint(0, 256, (items, N, K // 4), generator=g, dtype=torch.int32)
+    packed = packed.to(torch.uint8)
+    norms = torch.randn(items, N, generator=g).abs() + 0.1
+    if dist == "lloyd":
+        cent = torch.tensor(LLOYD_MAX_2BIT, dtype=torch.float32) / K ** 0.5
+    elif dist == "randn":
+        cent = torch.randn(4, generator=g)
+    else:
+        raise ValueError(dist)
+    x = torch.randn(items, M, K, generator=g).half()
+    x_rot = torch.randn(items, M, K, generator=g).half()
+    U = SV = b = None
+    if rank:
+        U = (torch.randn(K, rank, generator=g) * 0.01).half()
+        SV = (torch.randn(items, N, rank, generator=g) * 0.01).half()
+    if bias:
+        b = (torch.randn(items, N, generator=g) * 0.1).half()
+    return TurboProblem(packed=packed, norms=norms, centroids=cent, x=x, x_rot=x_rot, U=U,
+                        SV=SV, bias=b)
+
+
+def turbo_bytes(M: int, K: int, N: int, items: int = 1, rank: int = 0) -> int:
+    """HBM bytes one turbo call must move at minimum: 2-bit indices, fp32 norm
+    per row, fp16 x_rot in and y out (+ fp16 SV rows and x U when rank > 0)."""
+    per = N * K // 4 + 4 * N + 2 * M * (K + N) + 2 * rank * (N + M)
+    return items * per

@@ -4,7 +4,9 @@ Mirrors the reference's `inference.kernels` module (inference/kernels/
 __init__.py) so host code keeps its call sites:
 
   is_gptq_cuda_available()            __init__.py:55
-  is_cuda_available()                 __init__.py:39   (TurboQuant codec: not built)
+  is_cuda_available()                 __init__.py:39
+  turbo_dequant_matmul_fused(...)     __init__.py:184-239  (TurboQuant codec)
+  turbo_dequant_grouped_gemv_fused()  __init__.py:242-278
   gptq_dequant_matmul_fused(...)      __init__.py:284-346
   _unpack_indices_2bit(...)           __init__.py:113-118
 
@@ -13,6 +15,8 @@ plus the packed-format entry points this build adds:
   packed_dequant_matmul_fused(...)    fused dequant-GEMV/GEMM + low-rank + bias
   packed_dequant_matmul_batched(...)  many independent problems, one launch
   unpack_codes / dequant_weight / pack_codes_device   bit-exact codec checks
+  turbo_gemv(...)                     codebook GEMV/GEMM + low-rank + bias
+  rht(...)                            randomized Hadamard transform
 
 Error contract: argument problems raise RuntimeError (the reference's
 TORCH_CHECK -> RuntimeError).  Unlike the reference there is no silent
@@ -44,8 +48,15 @@ def is_gptq_cuda_available() -> bool:
 
 
 def is_cuda_available() -> bool:
-    """TurboQuant (codebook) kernels are not part of this build."""
-    return False
+    """True when the TurboQuant codebook kernels can run (the HIP library is
+    built and a GPU is visible); the reference's flag for its turbo extension
+    (inference/kernels/__init__.py:39-41)."""
+    return _lib.available() and torch.cuda.is_available()
+
+
+# The reference's feature flag for the grouped turbo GEMV (inference/kernels/
+# __init__.py:63-66); the HIP library always has it.
+_HAS_GROUPED_GEMV = True
 
 
 def _require(t: torch.Tensor, name: str, dtype=None) -> None:
@@ -334,6 +345,157 @@ def dequant_weight(codes: torch.Tensor, bits: int, K: int, scales: torch.Tensor,
     return out
 
 
+def _turbo_words(packed: torch.Tensor, K: int, lead: tuple) -> torch.Tensor:
+    """Indices as int32 words: (..., N, K/4) uint8 (the reference's
+    packed_indices) is viewed, not copied; (..., N, K/16) int32 passes."""
+    if packed.dtype == torch.uint8:
+        if packed.shape[-1] * 4 != K:
+            raise RuntimeError(f"packed_indices has {packed.shape[-1]} bytes per row, K={K}")
+        _require(packed, "packed_indices")
+        if K % 16 or packed.storage_offset() % 4:
+            raise RuntimeError("packed_indices rows must hold whole 32-bit words")
+        packed = packed.view(torch.int32)
+    _require(packed, "packed_indices", torch.int32)
+    if packed.shape[-1] * 16 != K or tuple(packed.shape[:-1]) != lead:
+        raise RuntimeError(f"packed_indices shape {tuple(packed.shape)} does not match "
+                           f"{lead} x K={K}")
+    return packed
+
+
+def turbo_gemv(x_rot: torch.Tensor, packed: torch.Tensor, norms: torch.Tensor,
+               centroids: torch.Tensor, xU: torch.Tensor | None = None,
+               SV: torch.Tensor | None = None, bias: torch.Tensor | None = None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = fp16(norms[n] * sum_k C[q(n,k)] x_rot[m,k] + (xU SV^T)[m,n] + bias[n]).
+
+    Single problem: x_rot (M, K) fp16, packed (N, K/4) uint8 or (N, K/16)
+    int32, norms (N,) fp32, centroids (4,) fp32, xU (M, r) fp16 = x U of the
+    unrotated x, SV (N, r) fp16, bias (N,) fp16 -> (M, N).
+    Batched: x_rot (E, M, K), packed (E, N, ...), norms (E, N), SV (E, N, r),
+    xU (E, M, r), bias (E, N) -> (E, M, N), one launch (glq_turbo_gemv_batched).
+    """
+    lib = _lib.load()
+    _require(x_rot, "x_rot", torch.float16)
+    _require(norms, "norms", torch.float32)
+    _require(centroids, "centroids", torch.float32)
+    if centroids.numel() != 4:
+        raise RuntimeError("the 2-bit codebook has 4 centroids")
+    batched = x_rot.dim() == 3
+    if x_rot.dim() not in (2, 3):
+        raise RuntimeError("x_rot must be (M, K) or (E, M, K)")
+    E = x_rot.shape[0] if batched else 1
+    M, K = x_rot.shape[-2], x_rot.shape[-1]
+    N = packed.shape[-2]
+    lead = (E, N) if batched else (N,)
+    words = _turbo_words(packed, K, lead)
+    if tuple(norms.shape) != lead:
+        raise RuntimeError(f"norms must be {lead}")
+    rank = 0
+    if SV is not None:
+        _require(SV, "SV", torch.float16)
+        rank = SV.shape[-1]
+        if tuple(SV.shape) != lead + (rank,):
+            raise RuntimeError(f"SV must be {lead + (rank,)}")
+        if xU is None:
+            raise RuntimeError("SV needs xU = x U")
+        _require(xU, "xU", torch.float16)
+        if tuple(xU.shape) != tuple(x_rot.shape[:-1]) + (rank,):
+            raise RuntimeError("xU must be (..., M, r)")
+    if bias is not None:
+        _require(bias, "bias", torch.float16)
+        if tuple(bias.shape) != lead:
+            raise RuntimeError(f"bias must be {lead}")
+    shape = (E, M, N) if batched else (M, N)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.float16, device=x_rot.device)
+    else:
+        _require(out, "out", torch.float16)
+        if tuple(out.shape) != shape:
+            raise RuntimeError(f"out must be {shape}")
+    if M == 0 or N == 0 or E == 0:
+        return out
+    rc = lib.glq_turbo_gemv_batched(
+        E, x_rot.data_ptr(), M * K, M, K, N, words.data_ptr(), N * K // 16, norms.data_ptr(), N,
+        centroids.data_ptr(), _lib.ptr(xU), M * rank, _lib.ptr(SV), N * rank, rank,
+        _lib.ptr(bias), N, out.data_ptr(), M * N, _lib.stream_handle(x_rot.device))
+    _lib.check(rc, "glq_turbo_gemv_batched")
+    return out
+
+
+def rht(x: torch.Tensor, signs: torch.Tensor, inverse: bool = False,
+        out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Randomized Hadamard transform of the rows of x (..., d), d a power of
+    two: (1/sqrt(d)) H diag(signs) x, or diag(signs) (1/sqrt(d)) H x when
+    inverse.  fp16 or fp32 in and out (out_dtype defaults to x's), fp32
+    arithmetic; rht(x16, signs) is the hot path's
+    rht_forward(x.float(), signs).half() in one launch."""
+    lib = _lib.load()
+    if x.dtype not in (torch.float16, torch.float32):
+        raise RuntimeError("x must be fp16 or fp32")
+    _require(x, "x")
+    _require(signs, "signs", torch.float32)
+    d = x.shape[-1]
+    if signs.numel() != d:
+        raise RuntimeError(f"signs has {signs.numel()} entries, rows have {d}")
+    od = out_dtype or x.dtype
+    if od not in (torch.float16, torch.float32):
+        raise RuntimeError("out_dtype must be fp16 or fp32")
+    out = torch.empty(x.shape, dtype=od, device=x.device)
+    rows = x.numel() // d if d else 0
+    if rows == 0:
+        return out
+    rc = lib.glq_rht(x.data_ptr(), int(x.dtype == torch.float32), rows, d, signs.data_ptr(),
+                     int(bool(inverse)), out.data_ptr(), int(od == torch.float32),
+                     _lib.stream_handle(x.device))
+    _lib.check(rc, "glq_rht")
+    return out
+
+
+def turbo_dequant_matmul_fused(x, packed_indices, norms, Pi, centroids, bits, dim,
+                               lora_USV=None, precomputed_x_rot=None):
+    """Reference signature (inference/kernels/__init__.py:184-239): x (B, K),
+    packed_indices (N, K/4) uint8, norms (N,) fp32, Pi (K, K) rotation (unused
+    when precomputed_x_rot is given), centroids (4,) fp32 -> fp16 (B, N).
+
+    x_rot = fp16(x.float() @ Pi.float().T) is a plain library GEMM (torch on
+    the GPU); precomputed_x_rot is used as given, rounded to fp16 (the
+    reference's kernel takes fp16 x_rot).  lora_USV = (U, S, V) adds
+    (x U) diag(S) V^T, fused into the turbo kernel's epilogue with one fp16
+    rounding (the reference adds it in Python afterwards).  Only 2-bit codes
+    have a kernel, as in the reference; other widths raise.
+    """
+    if bits != 2:
+        raise RuntimeError(f"the TurboQuant kernel takes 2-bit codes (got bits={bits})")
+    if precomputed_x_rot is not None:
+        x_rot = precomputed_x_rot.to(torch.float16).contiguous()
+    else:
+        x_rot = (x.float() @ Pi.float().T).half()
+    if x_rot.shape[-1] != dim:
+        raise RuntimeError(f"x_rot has K={x_rot.shape[-1]}, dim={dim}")
+    xU = SV = None
+    if lora_USV is not None:
+        U_, S_, V_ = lora_USV
+        SV = (V_.float() * S_.float().unsqueeze(0)).to(torch.float16).contiguous()
+        xU = lowrank_xu(x.to(torch.float16).contiguous(), U_.to(torch.float16).contiguous())
+    return turbo_gemv(x_rot.reshape(-1, dim), packed_indices.contiguous(),
+                      norms.float().contiguous(), centroids.float().contiguous(), xU=xU, SV=SV)
+
+
+def turbo_dequant_grouped_gemv_fused(x_grouped, packed_cat, norms_cat, centroids, N_out):
+    """Reference signature (inference/kernels/__init__.py:242-278): E experts
+    with their own input row.  x_grouped (E, K) fp16, packed_cat (E*N_out, K/4)
+    uint8, norms_cat (E*N_out,) fp32, centroids (4,) fp32 -> (E*N_out,) fp16,
+    in one launch."""
+    E, K = x_grouped.shape
+    packed = packed_cat.contiguous()
+    if packed.shape[0] != E * N_out:
+        raise RuntimeError(f"packed_cat has {packed.shape[0]} rows, E*N_out = {E * N_out}")
+    packed = packed.view(E, N_out, packed.shape[1])
+    y = turbo_gemv(x_grouped.to(torch.float16).contiguous().view(E, 1, K), packed,
+                   norms_cat.float().contiguous().view(E, N_out), centroids.float().contiguous())
+    return y.view(E * N_out)
+
+
 def _unpack_indices_2bit(packed: torch.Tensor, K: int) -> torch.Tensor:
     """Reference helper (inference/kernels/__init__.py:113-118): (N, K/4) uint8 ->
     (N, K) long, LSB-first.  Host-side format utility (not a compute path)."""
@@ -345,4 +507,5 @@ __all__ = [
     "is_gptq_cuda_available", "is_cuda_available", "packed_dequant_matmul_fused",
     "packed_dequant_matmul_batched", "gptq_dequant_matmul_fused", "unpack_codes",
     "dequant_weight", "pack_codes_device", "pack_codes", "workspace", "lowrank_xu",
+    "turbo_gemv", "rht", "turbo_dequant_matmul_fused", "turbo_dequant_grouped_gemv_fused",
 ]

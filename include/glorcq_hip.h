@@ -140,6 +140,56 @@ int glq_gemm_lora(const void* x, int64_t M, int64_t K, int64_t N,
                   int64_t workspace_bytes, void* stream);
 
 /*
+ * TurboQuant codebook matmul, for `items` independent problems:
+ *   y[i][m][n] = fp16(norms[i][n] * sum_k C[q_i(n, k)] * x_rot[i][m][k])
+ * Replaces the reference's turbo_dequant_matmul op (inference/kernels/
+ * turbo_matmul.cu:255-318 host; turbo_dequant_gemv_2bit_kernel :46-137 for
+ * B <= 4, turbo_dequant_gemm_2bit_kernel :150-245 otherwise; registered as
+ * glorcq::turbo_dequant_matmul, inference/kernels/__init__.py:68-85) with
+ * items = 1, and the grouped op turbo_dequant_grouped_gemv (turbo_matmul.cu:
+ * 417-464, kernel :329-415) with items = E, M = 1 and per-item strides.
+ *   x_rot   (items, M, K) fp16, item stride x_stride elements (0: shared)
+ *   codes   2-bit indices, (items, N, K/16) int32 words = the reference's
+ *           packed_indices (N, K/4) uint8 (4 per byte, LSB-first) read as
+ *           little-endian words; item stride codes_stride words
+ *   norms   (items, N) fp32, item stride norms_stride
+ *   centroids (4,) fp32 codebook
+ *   xU, SV  optional low-rank term + a SV^T: a = fp16(x U) (items, M, rank)
+ *           from glq_lowrank_xu_batched on the UNrotated x, SV (items, N,
+ *           rank); rank a multiple of 8 <= 256.  SV == NULL or rank 0: none.
+ *           This is GLoRCQLinear.forward's LoRA tail for turbo layers
+ *           (inference/quantized_linear.py:338-349) and lora_USV of
+ *           turbo_dequant_matmul_fused (inference/kernels/__init__.py:234-237)
+ *   bias    optional (items, N) fp16
+ *   y       (items, M, N) fp16 = fp16(norm * acc + a SV^T + bias), item
+ *           stride y_stride
+ * K must be a multiple of 64; x_rot and codes 16-byte aligned.  Any M.
+ */
+int glq_turbo_gemv_batched(int64_t items, const void* x_rot, int64_t x_stride,
+                           int64_t M, int64_t K, int64_t N, const int32_t* codes,
+                           int64_t codes_stride, const float* norms,
+                           int64_t norms_stride, const float* centroids,
+                           const void* xU, int64_t xu_stride, const void* SV,
+                           int64_t sv_stride, int64_t rank, const void* bias,
+                           int64_t bias_stride, void* y, int64_t y_stride,
+                           void* stream);
+
+/*
+ * Randomized Hadamard transform of `rows` rows of length d (a power of two
+ * <= 32768), H the Sylvester Hadamard matrix, fp32 arithmetic:
+ *   inverse == 0: y = (1/sqrt(d)) H diag(signs) x   (rht_forward,
+ *                 hadamard_rotation.py:52-67)
+ *   inverse != 0: y = diag(signs) (1/sqrt(d)) H x   (rht_backward, :70-86)
+ * x and y are fp16 (flag 0) or fp32 (flag 1); the hot-path call
+ * rht_forward(x.float(), signs).half() (inference/moe_block.py:351,525,649,
+ * 840) is x_fp32 = y_fp32 = 0.  The reference relies on the external
+ * fast-hadamard-transform package for H.  signs: (d,) fp32 of +-1.  y may not
+ * alias x.
+ */
+int glq_rht(const void* x, int x_fp32, int64_t rows, int64_t d, const float* signs,
+            int inverse, void* y, int y_fp32, void* stream);
+
+/*
  * One MoE block at decode: router, top-k dispatch, routed SwiGLU experts with
  * cluster-shared low-rank correction, sigmoid-gated shared expert, combine.
  * Replaces GraphCompatibleMoeBlock.forward (inference/moe_block.py:381-436:

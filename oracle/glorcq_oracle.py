@@ -332,3 +332,104 @@ def moe_forward(p, exact: bool = True, h: torch.Tensor | None = None, dense: boo
     sinter = torch.nn.functional.silu(sgu["gate"].half()) * sgu["up"].half()
     sd = _qmat_linear(sinter, p.shared["down"], 0, exact).half()
     return final + (sg * sd).half()
+
+
+# ---------------------------------------------------------------------------
+# TurboQuant codec (the reference's 2-bit expert format): codebook GEMV and
+# the input rotations
+# ---------------------------------------------------------------------------
+def unpack_indices_2bit(packed: np.ndarray, K: int) -> np.ndarray:
+    """(N, K/4) uint8 -> (N, K) int64 codebook indices, value j of a byte at
+    bits [2j, 2j+2) (_unpack_indices_2bit, inference/kernels/__init__.py:
+    113-118).  Pinned by: brute force over every value in every slot, and
+    equality with unpack_codes of the same bytes read as little-endian int32
+    words (tests/test_turbo_oracle.py)."""
+    p = np.asarray(packed, dtype=np.uint8)
+    out = np.empty((p.shape[0], p.shape[1] * 4), dtype=np.int64)
+    for j in range(4):
+        out[:, j::4] = (p >> (2 * j)) & 3
+    return out[:, :K]
+
+
+def turbo_matmul_fp32(x_rot: torch.Tensor, packed: np.ndarray, norms: torch.Tensor,
+                      centroids: torch.Tensor) -> torch.Tensor:
+    """The reference's pure-PyTorch path (_pytorch_fallback, inference/
+    kernels/__init__.py:121-146, and reference_turbo_matmul of
+    inference/kernels/test_kernels.py:24-41): W = C[idx] * norm[:, None] in
+    fp32, y = x_rot.float() @ W.T in fp32 (the kernels round y to fp16).
+    Pinned by: brute-force loops on tiny inputs, the closed form y = norm *
+    C[c] * sum(x) for constant codes, and equality with the GPTQ oracle when
+    C = (0, 1, 2, 3), norm = 1 (tests/test_turbo_oracle.py)."""
+    K = x_rot.shape[1]
+    idx = torch.from_numpy(unpack_indices_2bit(packed, K))
+    W = centroids.float()[idx] * norms.float()[:, None]
+    return x_rot.float() @ W.T
+
+
+def turbo_matmul_fp64(x_rot: torch.Tensor, packed: np.ndarray, norms: torch.Tensor,
+                      centroids: torch.Tensor) -> torch.Tensor:
+    """y = norm[n] * sum_k C[q(n,k)] x_rot[m,k] with fp64 sums of the exact fp32
+    codebook/norm values (the bar's reference; the CUDA kernel,
+    turbo_matmul.cu:80-137, accumulates in fp32 and multiplies by the norm
+    last).  Pinned as turbo_matmul_fp32."""
+    K = x_rot.shape[1]
+    idx = torch.from_numpy(unpack_indices_2bit(packed, K))
+    S = x_rot.double() @ centroids.double()[idx].T
+    return S * norms.double()[None, :]
+
+
+def turbo_bruteforce(x_rot: np.ndarray, packed: np.ndarray, norms: np.ndarray,
+                     centroids: np.ndarray) -> np.ndarray:
+    """Pure-Python loops over bytes and bit slots (tiny inputs only):
+    y[m, n] = norms[n] * sum_k centroids[(byte(n, k/4) >> 2(k%4)) & 3] x[m, k]."""
+    M, K = x_rot.shape
+    N = packed.shape[0]
+    y = np.zeros((M, N))
+    for m in range(M):
+        for n in range(N):
+            s = 0.0
+            for k in range(K):
+                q = (int(packed[n, k // 4]) >> (2 * (k % 4))) & 3
+                s += float(centroids[q]) * float(x_rot[m, k])
+            y[m, n] = float(norms[n]) * s
+    return y
+
+
+def hadamard_sylvester(d: int) -> np.ndarray:
+    """H_d by the Sylvester recursion H_2n = [[H, H], [H, -H]] (the ordering
+    fast-hadamard-transform applies); equals scipy.linalg.hadamard(d)."""
+    H = np.ones((1, 1))
+    while H.shape[0] < d:
+        H = np.block([[H, H], [H, -H]])
+    return H
+
+
+def rht_forward(x: torch.Tensor, signs: torch.Tensor) -> torch.Tensor:
+    """y = (1/sqrt(d)) H diag(signs) x in fp64 (hadamard_rotation.py:52-67;
+    the external package computes it in fp32).  Pinned by: scipy.linalg.
+    hadamard, norm preservation, rht_backward(rht_forward(x)) == x, and H e_0
+    = all-ones (tests/test_turbo_oracle.py)."""
+    d = x.shape[-1]
+    H = torch.from_numpy(hadamard_sylvester(d))
+    return (x.double() * signs.double()) @ H.T / np.sqrt(d)
+
+
+def rht_backward(y: torch.Tensor, signs: torch.Tensor) -> torch.Tensor:
+    """x = diag(signs) (1/sqrt(d)) H y in fp64 (hadamard_rotation.py:70-86)."""
+    d = y.shape[-1]
+    H = torch.from_numpy(hadamard_sylvester(d))
+    return (y.double() @ H.T / np.sqrt(d)) * signs.double()
+
+
+def generate_rht_signs(d: int, seed: int = 42) -> torch.Tensor:
+    """(d,) fp32 of +-1 from torch's CPU generator (hadamard_rotation.py:32-49):
+    randint(0, 2) * 2 - 1 under manual_seed(seed)."""
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    return (torch.randint(0, 2, (d,), generator=g) * 2 - 1).float()
+
+
+def rotate_qr(x: torch.Tensor, Pi: torch.Tensor) -> torch.Tensor:
+    """x_rot = fp16(x.float() @ Pi.float().T) (turbo_dequant_matmul_fused,
+    inference/kernels/__init__.py:209-212)."""
+    return (x.float() @ Pi.float().T).half()

@@ -54,8 +54,23 @@ def test_load_checks_and_lora_fusion():
     lin = GLoRCQLinear(256, 64)
     with pytest.raises(RuntimeError, match="shape"):
         lin.load_gptq(gptq_dict(p), device="cpu")
-    with pytest.raises(RuntimeError, match="TurboQuant"):
-        lin.load_turbo({}, None)
+    # turbo loader checks: code width, shape, and a rotation cache that was
+    # never given the rotation/codebook (the turboquant package is absent)
+    from glorcq_amd.quantized_linear import RotationCache
+    tp = fmt.make_turbo(256, 64, seed=5)
+    td = {"packed_indices": tp.packed[0], "norms": tp.norms[0], "bits": 3, "dim": 256}
+    with pytest.raises(RuntimeError, match="3-bit"):
+        lin.load_turbo(td, RotationCache("cpu"), device="cpu")
+    td["bits"] = 2
+    with pytest.raises(RuntimeError, match="turboquant"):
+        lin.load_turbo(td, RotationCache("cpu"), device="cpu")
+    with pytest.raises(RuntimeError, match="shape"):
+        GLoRCQLinear(256, 48).load_turbo(td, RotationCache("cpu"), device="cpu")
+    cache = RotationCache("cpu")
+    cache.put(256, 2, 42, None, tp.centroids)
+    lin.load_turbo(td, cache, device="cpu")
+    assert lin.quant_type == "turbo" and lin.turbo_words.shape == (64, 16)
+    assert torch.equal(lin.turbo_words, tp.words()[0])
     lin = GLoRCQLinear(256, 48)
     S = torch.rand(16, generator=torch.Generator().manual_seed(4)) + 0.5
     lin.load_lora(p.U, S, p.SV, device="cpu")
