@@ -9,26 +9,33 @@
 // codebook; x_rot the rotated input (x Pi^T, or the randomized Hadamard
 // transform of x).
 //
-// turbo_gemv_kernel: one workgroup per (item, 16-token block, 16 rows).  The
-// four waves split K into contiguous quarters; the token rows of x_rot are
-// staged in LDS per K segment (the whole K unless 16 tokens of a long row
-// would not fit) in the decode order of glq_gemv_core.h (codes c and c+8 of a
-// word share a dword); partial sums of the waves meet in LDS at the end.
+// turbo_gemv_kernel: a workgroup covers one (item, 16-token block) and 4/wpt
+// tiles of 16 rows; the wpt waves of a tile split K into contiguous parts
+// (wpt = 1 for large problems, 2 or 4 when there are too few tiles to fill
+// the chip) and meet in LDS at the end.  The token rows of x_rot are staged in
+// LDS per K segment (the whole K unless 16 tokens of a long row would not
+// fit), permuted into the decode order below.
 //
-// Decode is a byte permutation: for codes a = q_c and b = q_{c+8} of a word,
-// the selector ((w >> 2c) & 0x00030003) * 0x202 + 0x01000100 picks bytes
-// (2a, 2a+1, 2b, 2b+1) of the fp16 codebook {C0, C1, C2, C3} held in two
-// dwords, so one v_perm_b32 yields a pair of MFMA operands.  The codebook is
-// split into fp16 hi + lo parts (C = hi + lo to ~22 bits), one MFMA each, so
-// the fp32-accumulated sum carries fp32-level accuracy like the reference's
-// fp32 FMA loop; y = fp16(acc * norm) as in the reference.
+// Decode is a byte permutation (v_perm_b32) into an fp16 codebook held as two
+// dwords: low bytes of C0..C3 and high bytes of C0..C3.  For X = (w >> 2s) &
+// 0x03030303 (codes s, s+4, s+8, s+12 of the word, one per byte) and X4 =
+// X | 0x04040404, one permutation of (X4, X) gives the selector of a code pair
+// (a, a+4, b, b+4) and a second one looks up (C[a], C[b]).  The codebook is
+// split into fp16 hi + lo parts (C = hi + lo to ~22 bits) sharing the
+// selectors, one MFMA each, so the fp32-accumulated sum keeps fp32-level
+// accuracy like the reference's fp32 FMA loop; y = fp16(acc * norm) as in the
+// reference.
 #include <algorithm>
 
 #include "glq_gemv_core.h"
 
 namespace glq {
 
-constexpr int kTurboXBudget = 64 * 1024;  // LDS bytes for one x segment
+constexpr int kTurboXBudget = 64 * 1024;      // LDS bytes for one x segment (one-shot form)
+constexpr int kTurboStreamTiles = 2048;       // tiles from which the streaming form is used
+constexpr int kTurboStreamWgs = 1024;         // its workgroups, about 4 per CU
+constexpr int kTurboStreamLds = 80 * 1024;    // its LDS limit (the whole K of 16 tokens)
+constexpr int kTurboPF = 8;                   // steps of codes in flight per wave
 
 struct TurboArgs {
   const __half* x;         // x_rot (items, M, K) fp16
@@ -50,44 +57,179 @@ struct TurboArgs {
   int rank, rpad, apad;    // low-rank width, padded to 32, LDS row stride of a
   int segsteps;            // 256-code steps per staged x segment
   int xstride;             // halves per staged token row (segment + 8)
-  int rwgs, twgs;          // row blocks (16 rows) and token blocks (16 tokens) per item
+  int wpt;                 // waves per 16-row tile: 1, 2 or 4 (K split among them)
+  int rwgs, twgs;          // row groups (4/wpt tiles) and token blocks (16 tokens) per item
 };
 
-// fp16 codebook in v_perm_b32 form: lo dword {C0, C1}, hi dword {C2, C3}.
+// fp16 codebook in v_perm_b32 form: lb = low bytes of C0..C3, hb = high bytes.
 struct TurboLut {
-  uint32_t lo, hi;
+  uint32_t lb, hb;
 };
 
 __device__ __forceinline__ TurboLut turbo_lut(const float* c, bool residual) {
-  uint32_t h[4];
+  uint32_t lb = 0, hb = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const __half hi = __float2half(c[i]);
     const __half v = residual ? __float2half(c[i] - __half2float(hi)) : hi;
-    h[i] = __half_as_ushort(v);
+    const uint32_t u = __half_as_ushort(v);
+    lb |= (u & 0xffu) << (8 * i);
+    hb |= (u >> 8) << (8 * i);
   }
-  return TurboLut{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+  return TurboLut{lb, hb};
 }
 
-// One code word (16 codes) -> the two MFMA operand slices in decode2's order
-// (s0: codes 0,8,1,9,2,10,3,11; s1: codes 4,12,5,13,6,14,7,15), for the hi
-// and for the lo codebook.
+// One code word (16 codes) -> the two MFMA operand slices, for the hi and the
+// lo codebook: s0 = codes 0,4,1,5,2,6,3,7 and s1 = codes 8,12,9,13,10,14,11,15.
 __device__ __forceinline__ void turbo_decode(uint32_t w, const TurboLut& H, const TurboLut& L,
                                              f16x8& s0h, f16x8& s1h, f16x8& s0l, f16x8& s1l) {
   u32x4 ah, bh, al, bl;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t sa = ((w >> (2 * j)) & 0x00030003u) * 0x202u + 0x01000100u;
-    const uint32_t sb = ((w >> (8 + 2 * j)) & 0x00030003u) * 0x202u + 0x01000100u;
-    ah[j] = __builtin_amdgcn_perm(H.hi, H.lo, sa);
-    bh[j] = __builtin_amdgcn_perm(H.hi, H.lo, sb);
-    al[j] = __builtin_amdgcn_perm(L.hi, L.lo, sa);
-    bl[j] = __builtin_amdgcn_perm(L.hi, L.lo, sb);
+  for (int s = 0; s < 4; ++s) {
+    const uint32_t X = (w >> (2 * s)) & 0x03030303u;
+    const uint32_t X4 = X | 0x04040404u;
+    const uint32_t sa = __builtin_amdgcn_perm(X4, X, 0x05010400u);  // (q_s, q_s+4)
+    const uint32_t sb = __builtin_amdgcn_perm(X4, X, 0x07030602u);  // (q_s+8, q_s+12)
+    ah[s] = __builtin_amdgcn_perm(H.hb, H.lb, sa);
+    bh[s] = __builtin_amdgcn_perm(H.hb, H.lb, sb);
+    al[s] = __builtin_amdgcn_perm(L.hb, L.lb, sa);
+    bl[s] = __builtin_amdgcn_perm(L.hb, L.lb, sb);
   }
   s0h = __builtin_bit_cast(f16x8, ah);
   s1h = __builtin_bit_cast(f16x8, bh);
   s0l = __builtin_bit_cast(f16x8, al);
   s1l = __builtin_bit_cast(f16x8, bl);
+}
+
+// Writes one 16-row tile: y = norm * acc + a SV^T + bias, rounded once to fp16.
+// acc[i] of lane (li, kb) holds token 4kb + i, row r0 + li; a_l holds the
+// block's low-rank factor a (rows < mr, zero-padded to rpad columns).
+__device__ __forceinline__ void turbo_epilogue(const TurboArgs& a, f32x4 acc, int item, int m0,
+                                               int mr, int r0, const __half* a_l, int li,
+                                               int kb) {
+  const int r = r0 + li, row = min(r, a.N - 1);
+  const float nr = a.norms[(int64_t)item * a.n_es + row];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] *= nr;
+  if (a.sv) {
+    // A = a (token rows), B = SV rows: D[token 4kb + i][row li], acc's layout
+    const __half* svr = a.sv + (int64_t)item * a.sv_es + (int64_t)row * a.rank;
+    const __half* ar = a_l + min(li, mr - 1) * a.apad;
+    for (int s0 = 0; s0 < a.rpad; s0 += 32) {
+      const int j = s0 + 8 * kb;
+      const f16x8 av = *(const f16x8*)(ar + j);
+      const f16x8 bv = j < a.rank ? *(const f16x8*)(svr + j) : f16x8{};
+      acc = mfma_16x16x32(av, bv, acc);
+    }
+  }
+  const float bb = a.bias ? __half2float(a.bias[(int64_t)item * a.bias_es + row]) : 0.f;
+  if (r < a.N) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 4 * kb + i;
+      if (m < mr)
+        a.y[(int64_t)item * a.y_es + (int64_t)(m0 + m) * a.N + r] = __float2half(acc[i] + bb);
+    }
+  }
+}
+
+// Stages the block's token rows of x_rot for 256-code steps [sb, se) (permuted
+// into the decode order; zero past K) and, when there is a low-rank term, its
+// low-rank factor a.  The caller's barrier makes both visible.
+__device__ __forceinline__ void turbo_stage(const TurboArgs& a, const __half* X, int item, int m0,
+                                            int mr, int sb, int se, __half* xs, __half* a_l,
+                                            bool with_a, int tid) {
+  if (with_a && a.sv) {
+    for (int idx = tid; idx < mr * a.rpad; idx += 256) {
+      const int m = idx / a.rpad, j = idx - m * a.rpad;
+      a_l[m * a.apad + j] = j < a.rank
+                                ? a.xu[(int64_t)item * a.xu_es + (int64_t)(m0 + m) * a.rank + j]
+                                : __float2half(0.f);
+    }
+  }
+  const int nblk = (se - sb) * 16;  // 16-code blocks
+  for (int idx = tid; idx < mr * nblk; idx += 256) {
+    const int m = idx / nblk, blk = idx - m * nblk;
+    const int k = sb * 256 + blk * 16;
+    f16x8 o0 = f16x8{}, o1 = f16x8{};
+    if (k < a.K) {
+      const f16x8 v0 = *(const f16x8*)(X + (int64_t)m * a.K + k);
+      const f16x8 v1 = *(const f16x8*)(X + (int64_t)m * a.K + k + 8);
+      o0 = __builtin_shufflevector(v0, v1, 0, 4, 1, 5, 2, 6, 3, 7);
+      o1 = __builtin_shufflevector(v0, v1, 8, 12, 9, 13, 10, 14, 11, 15);
+    }
+    f16x8* dst = (f16x8*)(xs + m * a.xstride + blk * 16);
+    dst[0] = o0;
+    dst[1] = o1;
+  }
+}
+
+// Codes of one 256-code step of a row (lane kb: words 4kb..4kb+3) against the
+// staged x at step offset xk: 4 words, 16 MFMAs into acc.
+__device__ __forceinline__ void turbo_step(const u32x4& w, const __half* xk, const TurboLut& H,
+                                           const TurboLut& L, f32x4& acc) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f16x8 s0h, s1h, s0l, s1l;
+    turbo_decode(w[i], H, L, s0h, s1h, s0l, s1l);
+    const f16x8 x0 = *(const f16x8*)(xk + 16 * i);
+    const f16x8 x1 = *(const f16x8*)(xk + 16 * i + 8);
+    acc = mfma_16x16x32(x0, s0h, acc);
+    acc = mfma_16x16x32(x1, s1h, acc);
+    acc = mfma_16x16x32(x0, s0l, acc);
+    acc = mfma_16x16x32(x1, s1l, acc);
+  }
+}
+
+// turbo_stream_kernel: the streaming form for problems with many tiles and the
+// whole K of the block's tokens in LDS.  A workgroup covers one (item, token
+// block); its waves walk tiles gw, gw + 4R, ... (R workgroups per block) over
+// the full K, keeping PF steps of codes in flight across tile boundaries
+// (the slot of step s refills with step s + PF of the tile, or with step s of
+// the wave's next tile), and write each tile as soon as its sum is complete.
+template <int PF>
+__global__ __launch_bounds__(256) void turbo_stream_kernel(TurboArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __half* a_l = (__half*)smem;        // [16][apad] low-rank factor a
+  __half* xs = a_l + 16 * a.apad;     // [mr][xstride], the whole K
+  const int per_item = a.rwgs * a.twgs;
+  const int item = blockIdx.x / per_item;
+  const int rem = blockIdx.x - item * per_item;
+  const int tb = rem / a.rwgs, wl = rem - tb * a.rwgs;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), li = lane & 15, kb = lane >> 4;
+  const int m0 = 16 * tb, mr = min(16, a.M - m0);
+  const __half* X = a.x + (int64_t)item * a.x_es + (int64_t)m0 * a.K;
+  const uint32_t* C = a.codes + (int64_t)item * a.c_es;
+  const int T = (a.N + 15) >> 4, stride = 4 * a.rwgs, gw = wl * 4 + wave;
+  const int ntw = gw < T ? (T - gw + stride - 1) / stride : 0;  // tiles of this wave
+  const int nsteps = (a.K + 255) >> 8, cyc = (nsteps + PF - 1) / PF;
+  const int wlast = a.kw - 4;
+  const TurboLut H = turbo_lut(a.cent, false), L = turbo_lut(a.cent, true);
+  auto load = [&](int t, int s) {  // step s of the wave's t-th tile
+    const int row = min(16 * (gw + t * stride) + li, a.N - 1);
+    return *(const u32x4*)(C + (int64_t)row * a.kw + min(16 * s + 4 * kb, wlast));
+  };
+  u32x4 buf[PF];
+#pragma unroll
+  for (int p = 0; p < PF; ++p) buf[p] = (ntw > 0 && p < nsteps) ? load(0, p) : u32x4{0, 0, 0, 0};
+  turbo_stage(a, X, item, m0, mr, 0, nsteps, xs, a_l, true, tid);
+  __syncthreads();
+  const __half* xr = xs + min(li, mr - 1) * a.xstride + 64 * kb;
+  for (int t = 0; t < ntw; ++t) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < cyc; ++c) {
+#pragma unroll
+      for (int p = 0; p < PF; ++p) {
+        const int s = c * PF + p;
+        const u32x4 w = buf[p];
+        const int nt = c + 1 < cyc ? t : t + 1, ns = c + 1 < cyc ? s + PF : p;
+        if (nt < ntw && ns < nsteps) buf[p] = load(nt, ns);
+        if (s < nsteps) turbo_step(w, xr + s * 256, H, L, acc);
+      }
+    }
+    turbo_epilogue(a, acc, item, m0, mr, 16 * (gw + t * stride), a_l, li, kb);
+  }
 }
 
 __global__ __launch_bounds__(256) void turbo_gemv_kernel(TurboArgs a) {
@@ -98,25 +240,27 @@ __global__ __launch_bounds__(256) void turbo_gemv_kernel(TurboArgs a) {
   const int per_item = a.rwgs * a.twgs;
   const int item = blockIdx.x / per_item;
   const int rem = blockIdx.x - item * per_item;
-  const int tb = rem / a.rwgs, rb = rem - tb * a.rwgs;
+  const int tb = rem / a.rwgs, rg = rem - tb * a.rwgs;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = tid >> 6, li = lane & 15, kb = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), li = lane & 15, kb = lane >> 4;
+  const int wpt = a.wpt, tpw = 4 / wpt;            // waves per tile, tiles per workgroup
+  const int part = wave % wpt, r0 = (rg * tpw + wave / wpt) * 16;
   const int m0 = 16 * tb, mr = min(16, a.M - m0);  // token rows of this block
   const __half* X = a.x + (int64_t)item * a.x_es + (int64_t)m0 * a.K;
 
   const TurboLut H = turbo_lut(a.cent, false), L = turbo_lut(a.cent, true);
-  const int row = min(16 * rb + li, a.N - 1);
+  const int row = min(r0 + li, a.N - 1);
   const uint32_t* crow = a.codes + (int64_t)item * a.c_es + (int64_t)row * a.kw;
   const int wlast = a.kw - 4;  // last whole 16-byte piece (kw is a multiple of 4)
   const __half* xr = xs + min(li, mr - 1) * a.xstride;
   const int nsteps = (a.K + 255) >> 8;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  constexpr int PF = 4;  // 256-code steps of codes in flight per wave
+  constexpr int PF = kTurboPF;  // 256-code steps of codes in flight per wave
 
   for (int sb = 0; sb < nsteps; sb += a.segsteps) {
     const int se = min(nsteps, sb + a.segsteps);
-    const int q = (se - sb + 3) >> 2;
-    const int j0 = sb + wave * q;                 // this wave's first step
+    const int q = (se - sb + wpt - 1) / wpt;
+    const int j0 = sb + part * q;                 // this wave's first step
     const int jn = max(0, min(se, j0 + q) - j0);  // and its step count
     // a step of a row is 16 words; lane kb holds words 4kb..4kb+3 (clamped:
     // words past the row end meet zero x and add nothing)
@@ -126,86 +270,39 @@ __global__ __launch_bounds__(256) void turbo_gemv_kernel(TurboArgs a) {
       buf[p] = p < jn ? *(const u32x4*)(crow + min(16 * (j0 + p) + 4 * kb, wlast))
                       : u32x4{0, 0, 0, 0};
     if (sb > 0) __syncthreads();  // every wave is done with the previous segment
-    const int nblk = (se - sb) * 16;  // 16-code blocks of the segment
-    for (int idx = tid; idx < mr * nblk; idx += 256) {
-      const int m = idx / nblk, blk = idx - m * nblk;
-      const int k = sb * 256 + blk * 16;
-      f16x8 o0 = f16x8{}, o1 = f16x8{};
-      if (k < a.K) {
-        const f16x8 v0 = *(const f16x8*)(X + (int64_t)m * a.K + k);
-        const f16x8 v1 = *(const f16x8*)(X + (int64_t)m * a.K + k + 8);
-        o0 = __builtin_shufflevector(v0, v1, 0, 8, 1, 9, 2, 10, 3, 11);
-        o1 = __builtin_shufflevector(v0, v1, 4, 12, 5, 13, 6, 14, 7, 15);
-      }
-      f16x8* dst = (f16x8*)(xs + m * a.xstride + blk * 16);
-      dst[0] = o0;
-      dst[1] = o1;
-    }
+    turbo_stage(a, X, item, m0, mr, sb, se, xs, a_l, sb == 0, tid);
     __syncthreads();
-    for (int jj = 0; jj < jn; jj += PF) {
+    auto consume = [&](const u32x4& w, int j) {
+      turbo_step(w, xr + (j0 + j - sb) * 256 + 64 * kb, H, L, acc);
+    };
+    int jj = 0;
+    for (; jj + PF <= jn; jj += PF) {  // whole rounds: refill each slot after use
 #pragma unroll
       for (int p = 0; p < PF; ++p) {
-        const int j = jj + p;
-        if (j >= jn) break;
         const u32x4 w = buf[p];
-        if (j + PF < jn) buf[p] = *(const u32x4*)(crow + min(16 * (j0 + j + PF) + 4 * kb, wlast));
-        const __half* xk = xr + (j0 + j - sb) * 256 + 64 * kb;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          f16x8 s0h, s1h, s0l, s1l;
-          turbo_decode(w[i], H, L, s0h, s1h, s0l, s1l);
-          const f16x8 x0 = *(const f16x8*)(xk + 16 * i);
-          const f16x8 x1 = *(const f16x8*)(xk + 16 * i + 8);
-          acc = mfma_16x16x32(x0, s0h, acc);
-          acc = mfma_16x16x32(x1, s1h, acc);
-          acc = mfma_16x16x32(x0, s0l, acc);
-          acc = mfma_16x16x32(x1, s1l, acc);
-        }
+        if (jj + p + PF < jn)
+          buf[p] = *(const u32x4*)(crow + min(16 * (j0 + jj + p + PF) + 4 * kb, wlast));
+        consume(w, jj + p);
       }
     }
-  }
-  // acc[i] of lane (li, kb): token 4kb + i, row li of the block
 #pragma unroll
-  for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
-  const bool lora = a.sv != nullptr;
-  if (lora) {
-    for (int idx = tid; idx < mr * a.rpad; idx += 256) {
-      const int m = idx / a.rpad, j = idx - m * a.rpad;
-      a_l[m * a.apad + j] = j < a.rank
-                                ? a.xu[(int64_t)item * a.xu_es + (int64_t)(m0 + m) * a.rank + j]
-                                : __float2half(0.f);
+    for (int p = 0; p < PF; ++p)  // the last jn % PF steps
+      if (jj + p < jn) consume(buf[p], jj + p);
+  }
+  // acc[i] of lane (li, kb): token 4kb + i, row li of the tile
+  if (wpt > 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
+    __syncthreads();
+    if (part != 0) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = red[(wave * 4 + i) * 64 + lane];
+      for (int w2 = 1; w2 < wpt; ++w2) v += red[((wave + w2) * 4 + i) * 64 + lane];
+      acc[i] = v;
     }
   }
-  __syncthreads();
-  if (wave == 0) {
-    // y = norm * acc + a SV^T + bias, rounded once to fp16
-    const int r = 16 * rb + li, rc = min(r, a.N - 1);
-    const float nr = a.norms[(int64_t)item * a.n_es + rc];
-    f32x4 y;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      y[i] = nr * (red[i * 64 + lane] + red[(4 + i) * 64 + lane] + red[(8 + i) * 64 + lane] +
-                   red[(12 + i) * 64 + lane]);
-    if (lora) {
-      // A = a (token rows), B = SV rows: D[token 4kb + i][row li], acc's layout
-      const __half* svr = a.sv + (int64_t)item * a.sv_es + (int64_t)rc * a.rank;
-      const __half* ar = a_l + min(li, mr - 1) * a.apad;
-      for (int s0 = 0; s0 < a.rpad; s0 += 32) {
-        const int j = s0 + 8 * kb;
-        const f16x8 av = *(const f16x8*)(ar + j);
-        const f16x8 bv = j < a.rank ? *(const f16x8*)(svr + j) : f16x8{};
-        y = mfma_16x16x32(av, bv, y);
-      }
-    }
-    const float bb = a.bias ? __half2float(a.bias[(int64_t)item * a.bias_es + rc]) : 0.f;
-    if (r < a.N) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = 4 * kb + i;
-        if (m < mr) a.y[(int64_t)item * a.y_es + (int64_t)(m0 + m) * a.N + r] = __float2half(y[i] + bb);
-      }
-    }
-  }
+  turbo_epilogue(a, acc, item, m0, mr, r0, a_l, li, kb);
 }
 
 // ---------------------------------------------------------------------------
@@ -305,15 +402,40 @@ extern "C" int glq_turbo_gemv_batched(int64_t items, const void* x_rot, int64_t 
   const int fit = (kTurboXBudget / (2 * mr) - 8) / 256;  // steps of a segment that fit
   a.segsteps = std::max(1, std::min(nsteps, fit));
   a.xstride = a.segsteps * 256 + 8;
-  a.rwgs = (int)((N + 15) / 16);
   a.twgs = (int)((M + 15) / 16);
+  const int64_t T = (N + 15) / 16, tiles = items * a.twgs * T;
+  const int64_t kpad = (int64_t)nsteps * 256;
+  const size_t stream_lds = (size_t)16 * a.apad * 2 + (size_t)mr * (kpad + 8) * 2;
+  hipStream_t s = (hipStream_t)stream;
+  if (tiles >= kTurboStreamTiles && stream_lds <= (size_t)kTurboStreamLds) {
+    // streaming form: the whole K staged once per workgroup, waves walk tiles
+    a.segsteps = nsteps;
+    a.xstride = (int)kpad + 8;
+    a.wpt = 1;
+    const int64_t blocks = items * a.twgs;
+    a.rwgs = (int)std::max<int64_t>(1, std::min<int64_t>((kTurboStreamWgs + blocks - 1) / blocks,
+                                                         (T + 3) / 4));
+    static size_t attr = 64 * 1024;
+    int rc = set_lds_limit(turbo_stream_kernel<kTurboPF>, stream_lds, attr);
+    if (rc) return rc;
+    const int64_t grid = blocks * a.rwgs;
+    GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
+    turbo_stream_kernel<kTurboPF><<<dim3((unsigned)grid), dim3(256), stream_lds, s>>>(a);
+    GLQ_LAUNCH_CHECK("turbo_stream_kernel");
+    return GLQ_OK;
+  }
+  // one-shot form: one wave per tile when there are enough tiles to fill the
+  // chip; else the K dimension of a tile is split among 2 or 4 waves
+  a.wpt = tiles >= 2048 ? 1 : tiles >= 1024 ? 2 : 4;
+  const int tpw = 4 / a.wpt;
+  a.rwgs = (int)((T + tpw - 1) / tpw);
   const size_t lds = 4096 + (size_t)16 * a.apad * 2 + (size_t)mr * a.xstride * 2;
   static size_t attr = 64 * 1024;
   int rc = set_lds_limit(turbo_gemv_kernel, lds, attr);
   if (rc) return rc;
   const int64_t grid = items * a.rwgs * a.twgs;
   GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
-  turbo_gemv_kernel<<<dim3((unsigned)grid), dim3(256), lds, (hipStream_t)stream>>>(a);
+  turbo_gemv_kernel<<<dim3((unsigned)grid), dim3(256), lds, s>>>(a);
   GLQ_LAUNCH_CHECK("turbo_gemv_kernel");
   return GLQ_OK;
 }

@@ -91,6 +91,22 @@ def test_turbo_lora_bias(gpu, M):
     check(y, refs(p, lora=True, bias=True), f"lora+bias M={M}")
 
 
+@pytest.mark.parametrize("K,N,M,items,rank,bias", [
+    (2048, 40000 - 6, 1, 1, 0, False),   # many rows of one matrix, N tail
+    (1408, 2048, 1, 60, 0, False),       # grouped down over 60 experts
+    (1408, 2048, 16, 16, 32, True),      # 16 tokens, low-rank term, bias
+    (4096, 32768, 1, 1, 0, False),       # two prefetch rounds per tile
+    (1152, 40000, 3, 1, 64, True),       # partial last step, idle prefetch slots
+])
+def test_turbo_streaming_form(gpu, K, N, M, items, rank, bias):
+    """Problems of >= 2048 tiles take the streaming kernel (waves walk tiles)."""
+    print(f"turbo stream K={K} N={N} M={M} items={items} r={rank}", flush=True)
+    p = fmt.make_turbo(K, N, M=M, items=items, seed=K + N + items, rank=rank, bias=bias)
+    y = run(p, gpu, lora=rank > 0, bias=bias)
+    for i in range(items):
+        check(y[i], refs(p, i, lora=rank > 0, bias=bias), f"stream item {i}")
+
+
 def test_turbo_rank_not_multiple_of_32(gpu):
     p = fmt.make_turbo(1408, 300, M=2, seed=8, rank=40)
     check(run(p, gpu, lora=True)[0], refs(p, lora=True), "rank 40")
