@@ -302,6 +302,67 @@ def bench_moe(dev, seed=6, reps=20, trials=15):
     return res
 
 
+def bench_turbo(dev, pool_mb=1536, reps_cap=48, trials=11):
+    """The reference's own 2-bit expert format (TurboQuant codebook, SURVEY
+    F1) on the codebook kernel, M = 1, cold cache: (a) the graph-mode MoE gate
+    GEMV over every expert's rows at once (inference/moe_block.py:783-787:
+    60 x 1408 rows, K 2048), (b) the grouped down GEMV, 60 experts each with
+    its own input row (moe_block.py:858-865, turbo_matmul.cu:329-415).  A
+    hipGraph of launches cycling through distinct weight copies (>= 1.5 GB in
+    all), replays timed with HIP events; bytes = fmt.turbo_bytes."""
+    import torch
+
+    from glorcq_amd import format as fmt
+    from glorcq_amd import kernels
+
+    res = {}
+    cases = (("all-experts gate rows", 2048, 60 * 1408, 1),
+             ("grouped down, 60 experts", 1408, 2048, 60))
+    for name, K, N, items in cases:
+        per = items * N * K // 4
+        copies = max(2, min(reps_cap, (pool_mb << 20) // per))
+        g = torch.Generator(device=dev).manual_seed(7)
+        words = torch.randint(-2**31, 2**31 - 1, (copies, items, N, K // 16), dtype=torch.int32,
+                              device=dev, generator=g)
+        norms = torch.rand(items, N, device=dev, generator=g) + 0.1
+        x = torch.randn(items, 1, K, device=dev, generator=g).half()
+        cent = torch.tensor(fmt.LLOYD_MAX_2BIT, device=dev) / K ** 0.5
+        out = torch.empty(items, 1, N, dtype=torch.float16, device=dev)
+        fns = [lambda i=i: kernels.turbo_gemv(x, words[i], norms, cent, out=out)
+               for i in range(copies)]
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for f in fns[:3]:
+                f()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for f in fns:
+                f()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        ts = []
+        for _ in range(trials):
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3 / copies)
+        ts.sort()
+        us = ts[len(ts) // 2]
+        nbytes = fmt.turbo_bytes(1, K, N, items)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"K": K, "N": N, "items": items, "M": 1, "us_per_launch": round(us, 2),
+                     "algorithmic_bytes": nbytes, "achieved_GBps": round(gbs, 1),
+                     "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "weight_copies": copies}
+        log(f"turbo {name}: {us:.2f} us, {gbs:.0f} GB/s")
+        del graph, words
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -311,6 +372,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--pmc-workload", action="store_true")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE block leg")
+    ap.add_argument("--no-turbo", action="store_true", help="skip the TurboQuant codec leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (every box here has one); "
@@ -417,6 +479,9 @@ def main():
                          "clusters, 4-bit shared expert inter 5632), seed 6, one hipGraph of 20 "
                          "steps per replay"),
             "by_batch": moe}
+    if not args.no_turbo:
+        log("TurboQuant codebook GEMV (the reference's 2-bit expert format), M = 1")
+        result["turbo_codec_gemv"] = bench_turbo(dev)
     if not args.no_cpu:
         log("cpu baseline (oracle restatement of the reference CPU fallback)")
         cb, parity, err = cpu_baseline(y0)
