@@ -303,8 +303,8 @@ def bench_moe(dev, seed=6, reps=20, trials=15):
 
 
 def bench_turbo(dev, pool_mb=1536, reps_cap=48, trials=11):
-    """The reference's own 2-bit expert format (TurboQuant codebook, SURVEY
-    F1) on the codebook kernel, M = 1, cold cache: (a) the graph-mode MoE gate
+    """The reference's own 2-bit routed-expert format (TurboQuant codebook,
+    joint_optim.py:715-721) on the codebook kernel, M = 1, cold cache: (a) the graph-mode MoE gate
     GEMV over every expert's rows at once (inference/moe_block.py:783-787:
     60 x 1408 rows, K 2048), (b) the grouped down GEMV, 60 experts each with
     its own input row (moe_block.py:858-865, turbo_matmul.cu:329-415).  A
