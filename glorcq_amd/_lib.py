@@ -33,6 +33,7 @@ class MoeParams(ctypes.Structure):
         ("U", _vp * 3), ("cluster_of", _vp * 3), ("SV", _vp * 3),
         ("shared_codes", _vp * 3), ("shared_scales", _vp * 3), ("shared_zeros", _vp * 3),
         ("out", _vp), ("router_logits", _vp),
+        ("u_slot", _vp * 2), ("u_rows", _i64 * 3),
     ]
 
 
@@ -86,6 +87,7 @@ SIGNATURES = {
         _vp, _i64, _vp,                     # y, y_stride, stream
     ]),
     "glq_rht": (_c_int, [_vp, _c_int, _i64, _i64, _vp, _c_int, _vp, _c_int, _vp]),
+    "glq_dequant_factor": (_c_int, [_vp, _c_int, _i64, _i64, _vp, _c_int, _c_int, _vp, _vp]),
     "glq_moe_workspace_bytes": (_i64, [ctypes.POINTER(MoeParams)]),
     "glq_moe_decode": (_c_int, [ctypes.POINTER(MoeParams), _vp, _i64, _vp]),
     "glq_unpack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _c_int, _vp, _vp]),

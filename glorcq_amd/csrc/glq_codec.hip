@@ -93,6 +93,32 @@ __global__ void pack_kernel(const int32_t* __restrict__ q, int64_t words,
 
 using namespace glq;
 
+// LoRA factor dequantization (load time): out[r][c] = fp16((q / maxval) * scale)
+// in fp32, maxval = 2^(nbits-1) - 1, q from an int8 container or from int4
+// nibbles packing row pairs (row 2i in the low nibble of byte row i, row 2i+1
+// in the high nibble, value - 7); scale per column (cols,) or per row
+// (rows, 1).  The reference's _dequant_intN / _unpack_int4
+// (inference/model_builder.py:69-80, cross_layer_share.py:584-649) followed
+// by .half(): the same fp32 operations in the same order, so the result is
+// bit-identical.  One thread per output element.
+__global__ void dequant_factor_kernel(const int8_t* __restrict__ q8,
+                                      const uint8_t* __restrict__ q4, int64_t rows,
+                                      int64_t cols, const __half* __restrict__ scale,
+                                      int per_row, float maxval, __half* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * cols) return;
+  const int64_t r = i / cols, c = i - r * cols;
+  int qv;
+  if (q4) {
+    const uint8_t b = q4[(r >> 1) * cols + c];
+    qv = (int)((r & 1) ? (b >> 4) : (b & 0xf)) - 7;
+  } else {
+    qv = q8[i];
+  }
+  const float sc = __half2float(scale[per_row ? r : c]);
+  out[i] = __float2half_rn(((float)qv / maxval) * sc);
+}
+
 static int check_codec_shape(int64_t N, int64_t K, int bits) {
   GLQ_CHECK(bits == 2 || bits == 4, "bits must be 2 or 4 (got %d)", bits);
   GLQ_CHECK(N >= 0 && K >= 0, "negative shape N=%lld K=%lld", (long long)N,
@@ -173,6 +199,27 @@ int glq_pack_codes(const int32_t* q, int64_t N, int64_t K, int bits,
   else
     pack_kernel<4><<<grid, bs, 0, s>>>(q, words, (uint32_t*)codes);
   GLQ_LAUNCH_CHECK("pack_kernel");
+  return GLQ_OK;
+}
+
+int glq_dequant_factor(const void* q, int int4_packed, int64_t rows, int64_t cols,
+                       const void* scale, int scale_per_row, int nbits, void* out,
+                       void* stream) {
+  clear_error();
+  GLQ_CHECK(rows >= 0 && cols >= 0, "negative shape");
+  GLQ_CHECK(nbits >= 2 && nbits <= 8, "nbits must be 2..8 (got %d)", nbits);
+  GLQ_CHECK(!int4_packed || nbits == 4, "int4-packed factors have nbits = 4");
+  if (rows == 0 || cols == 0) return GLQ_OK;
+  GLQ_CHECK(q && scale && out, "null pointer");
+  GLQ_CHECK(rows * cols < (1ll << 40), "factor too large");
+  const int bs = 256;
+  const int64_t n = rows * cols;
+  const dim3 grid((unsigned)((n + bs - 1) / bs));
+  const float maxval = (float)((1 << (nbits - 1)) - 1);
+  dequant_factor_kernel<<<grid, bs, 0, (hipStream_t)stream>>>(
+      int4_packed ? nullptr : (const int8_t*)q, int4_packed ? (const uint8_t*)q : nullptr, rows,
+      cols, (const __half*)scale, scale_per_row ? 1 : 0, maxval, (__half*)out);
+  GLQ_LAUNCH_CHECK("dequant_factor_kernel");
   return GLQ_OK;
 }
 

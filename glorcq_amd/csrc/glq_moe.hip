@@ -77,6 +77,8 @@ struct MoeArgs {
   int64_t c_es[3], s_es[3], u_es[3], sv_es[3];
   const __half* U[3];
   const int32_t* clus[3];
+  const int32_t* uslot[2];  // gate/up: pool row of each cluster's U (nullptr: row = cluster)
+  int urows[3];             // rows of U[s]
   const __half* SV[3];
   const uint32_t* scodes[3];
   const __half* sscales[3];
@@ -193,10 +195,6 @@ __device__ int moe_dispatch(const MoeArgs& a, const MoeTables& t, bool sel_globa
 
 __device__ __forceinline__ int align_up_dev(int v, int a) { return (v + a - 1) / a * a; }
 
-__device__ __forceinline__ int moe_cluster(const MoeArgs& a, int s, int e) {
-  const int c = a.clus[s][e];
-  return min(max(c, 0), a.C - 1);
-}
 
 // ---------------------------------------------------------------------------
 // 1. Router + gate/up cluster partials (1024-thread workgroups)
@@ -342,7 +340,8 @@ __device__ void moe_xu_job(const MoeArgs& a, int job, unsigned char* smem) {
   __half* xl = (__half*)smem;                                     // [B][xr + 4]
   __half* ul = (__half*)(smem + align_up_dev(a.B * xstride * 2, 16));  // [xr][rank + 8]
   float* red = (float*)((unsigned char*)ul + align_up_dev(xr * ustride * 2, 16));
-  const __half* U = a.U[s] + (int64_t)c * a.u_es[s] + (int64_t)k0 * a.rank;
+  const int urow = min(max(a.uslot[s] ? a.uslot[s][c] : c, 0), a.urows[s] - 1);
+  const __half* U = a.U[s] + (int64_t)urow * a.u_es[s] + (int64_t)k0 * a.rank;
   const int r8 = a.rank / 8;
   for (int idx = tid; idx < kl * r8; idx += kRouteThreads) {  // U slice, 16 B per load
     const int k = idx / r8, j8 = idx - k * r8;
@@ -527,7 +526,7 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
     const int e = tok[kMoeTB], M = tok[kMoeTB + 1];
     auto clamp_c = [&](int c) { return min(max(c, 0), a.C - 1); };
     const int cg = clamp_c(tok[16 + e]), cu = clamp_c(tok[16 + a.E + e]);
-    const int cd = clamp_c(tok[16 + 2 * a.E + e]);
+    const int cd = min(max(tok[16 + 2 * a.E + e], 0), a.urows[2] - 1);  // row of U[2]
     __syncthreads();  // the tables' LDS is reused by the stream from here on
     const int t0 = wg * a.tpu, t1 = min(a.shGU.tiles, t0 + a.tpu);
     gemv_stream_ks<BR, 1, kMoeDepth, false, BR == 2, 2>(
@@ -739,8 +738,10 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
   if (lora) {
     GLQ_CHECK(r % 8 == 0 && r <= 128, "rank=%lld must be a multiple of 8, <= 128", (long long)r);
     GLQ_CHECK(C >= 1, "n_clusters must be >= 1 with a rank");
-    for (int s = 0; s < 3; ++s)
+    for (int s = 0; s < 3; ++s) {
       GLQ_CHECK(p->U[s] && p->cluster_of[s], "U and cluster_of are needed with a rank");
+      GLQ_CHECK(p->u_rows[s] >= 0 && p->u_rows[s] < (1ll << 24), "u_rows out of range");
+    }
   }
   GLQ_CHECK(p->h && p->router_w && p->out, "null h, router_w or out");
   auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
@@ -869,6 +870,8 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
     a.U[s] = lora ? (const __half*)p->U[s] : nullptr;
     a.u_es[s] = K * r;
     a.clus[s] = lora ? p->cluster_of[s] : nullptr;
+    if (s < 2) a.uslot[s] = lora ? p->u_slot[s] : nullptr;
+    a.urows[s] = (int)(p->u_rows[s] > 0 ? p->u_rows[s] : C);
     a.SV[s] = lora ? (const __half*)p->SV[s] : nullptr;
     a.sv_es[s] = N * r;
     a.scodes[s] = SI > 0 ? (const uint32_t*)p->shared_codes[s] : nullptr;

@@ -99,6 +99,7 @@ class GraphCompatibleMoeBlock(nn.Module):
                     cl.append(ids[key])
                 out[f"U_{proj}"] = _stack(pool)
                 out[f"cluster_{proj}"] = torch.tensor(cl, dtype=torch.int32, device=dev)
+                out[f"ckeys_{proj}"] = list(ids.keys())  # local cluster -> key
                 out[f"SV_{proj}"] = _stack([lin.SV for lin in lins])
                 n_clusters = max(n_clusters, len(pool))
         out["n_clusters"] = n_clusters
@@ -151,6 +152,42 @@ class GraphCompatibleMoeBlock(nn.Module):
             t["shared_bits"], t["shared_inter"], t["shared_gate_w"] = 0, 0, None
         return cls(stacked=t)
 
+    def set_global_pool(self, pools: dict, id_maps: dict):
+        """Points the block's U factors at cross-layer pools (the reference's
+        set_global_pool, inference/moe_block.py:85-99, fed by
+        model_builder._install_global_u_pool): pools[proj] is a (rows, K, r)
+        fp16 stack shared by every layer, id_maps[proj] maps a layer's
+        cluster_id (GLoRCQLinear.cluster_id) to its row.  gate/up keep this
+        block's x U per local cluster, read from the pool rows (u_slot); down
+        reads the pool row of each expert's cluster.  Experts without a
+        cluster_id keep their own U (a pool without their key raises)."""
+        t = self.t
+        if self.rank == 0:
+            return
+        for proj in PROJS:
+            if proj not in pools:
+                continue
+            keys = t.get(f"ckeys_{proj}")
+            if keys is None:
+                raise RuntimeError("set_global_pool needs a block built from GLoRCQLinear experts")
+            pool = pools[proj]
+            if pool.dim() != 3 or pool.shape[1:] != t[f"U_{proj}"].shape[1:]:
+                raise RuntimeError(f"{proj} pool must be (rows, K, r) = (*, "
+                                   f"{tuple(t[f'U_{proj}'].shape[1:])})")
+            rows = []
+            for key in keys:
+                if key[0] != "c" or key[1] not in id_maps[proj]:
+                    raise RuntimeError(f"{proj}: cluster {key} is not in the pool")
+                rows.append(int(id_maps[proj][key[1]]))
+            dev = pool.device
+            slot = torch.tensor(rows, dtype=torch.int32, device=dev)
+            t[f"U_{proj}"] = pool.contiguous()
+            t[f"urows_{proj}"] = int(pool.shape[0])
+            if proj == "down":  # cluster_of indexes the pool directly
+                t["cluster_down"] = slot[t["cluster_down"].long()].contiguous()
+            else:
+                t[f"uslot_{proj}"] = slot
+
     # ---- the step ----
     def _params(self, h, out, logits) -> _lib.MoeParams:
         t = self.t
@@ -171,6 +208,9 @@ class GraphCompatibleMoeBlock(nn.Module):
                 P.U[i] = t[f"U_{proj}"].data_ptr()
                 P.cluster_of[i] = t[f"cluster_{proj}"].data_ptr()
                 P.SV[i] = t[f"SV_{proj}"].data_ptr()
+                P.u_rows[i] = t.get(f"urows_{proj}", 0)
+                if i < 2:
+                    P.u_slot[i] = _lib.ptr(t.get(f"uslot_{proj}"))
             if self.shared_inter > 0:
                 P.shared_codes[i] = t[f"scodes_{proj}"].data_ptr()
                 P.shared_scales[i] = t[f"sscales_{proj}"].data_ptr()

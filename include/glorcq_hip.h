@@ -190,6 +190,21 @@ int glq_rht(const void* x, int x_fp32, int64_t rows, int64_t d, const float* sig
             int inverse, void* y, int y_fp32, void* stream);
 
 /*
+ * Load-time dequantization of an intN LoRA factor (U or SV) to fp16:
+ *   out[r][c] = fp16((q[r][c] / (2^(nbits-1) - 1)) * scale)   (fp32 math)
+ * q is int8 (rows, cols) (int4_packed == 0), or uint8 ((rows+1)/2, cols)
+ * holding row pairs in nibbles (row 2i low, row 2i+1 high, value - 7;
+ * int4_packed != 0, nbits 4).  scale is fp16 per column (cols,) or, with
+ * scale_per_row, per row (rows, 1).  Replaces _dequant_intN and _unpack_int4
+ * (inference/model_builder.py:69-80) as used by SharedUCache (:27-66) and
+ * _load_lora_for_module (:465-544); bit-identical to their fp32 arithmetic
+ * followed by .half().
+ */
+int glq_dequant_factor(const void* q, int int4_packed, int64_t rows, int64_t cols,
+                       const void* scale, int scale_per_row, int nbits, void* out,
+                       void* stream);
+
+/*
  * One MoE block at decode: router, top-k dispatch, routed SwiGLU experts with
  * cluster-shared low-rank correction, sigmoid-gated shared expert, combine.
  * Replaces GraphCompatibleMoeBlock.forward (inference/moe_block.py:381-436:
@@ -227,7 +242,7 @@ typedef struct glq_moe_params {
   const int32_t* codes[3];       /* (experts, N, K*bits/32) */
   const void* scales[3];         /* (experts, N, K/group) fp16 */
   const void* zeros[3];          /* (experts, N, K/group) fp16 */
-  const void* U[3];              /* (n_clusters, K, rank) fp16 */
+  const void* U[3];              /* (n_clusters or u_rows, K, rank) fp16 */
   const int32_t* cluster_of[3];  /* (experts,) int32 */
   const void* SV[3];             /* (experts, N, rank) fp16 */
   const int32_t* shared_codes[3];  /* (N, K*shared_bits/32) */
@@ -235,6 +250,13 @@ typedef struct glq_moe_params {
   const void* shared_zeros[3];
   void* out;             /* (tokens, hidden) fp16 */
   void* router_logits;   /* (tokens, experts) fp16, or NULL */
+  /* Cross-layer U pool (the reference's global U pool, model_builder.py:
+   * 143-183): U[s] may hold more rows than this block's clusters.
+   * u_slot[s] (s = gate, up): (n_clusters,) int32 row of U[s] holding
+   * cluster c's factor, or NULL (row = c).  For down, cluster_of[2][e] is the
+   * row of U[2] directly.  u_rows[s]: rows of U[s] (0: n_clusters). */
+  const int32_t* u_slot[2];
+  int64_t u_rows[3];
 } glq_moe_params;
 
 /* Workspace bytes glq_moe_decode needs for `p` (negative on a bad shape). */

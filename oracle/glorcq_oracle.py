@@ -433,3 +433,55 @@ def rotate_qr(x: torch.Tensor, Pi: torch.Tensor) -> torch.Tensor:
     """x_rot = fp16(x.float() @ Pi.float().T) (turbo_dequant_matmul_fused,
     inference/kernels/__init__.py:209-212)."""
     return (x.float() @ Pi.float().T).half()
+
+
+# ---------------------------------------------------------------------------
+# LoRA factor storage (load time): intN per-column / per-row absmax codes,
+# int4 row-pair nibble packing
+# ---------------------------------------------------------------------------
+def quant_intN_absmax(t: torch.Tensor, nbits: int, rowwise: bool = False):
+    """Symmetric absmax quantization to [-maxval, maxval], maxval =
+    2^(nbits-1) - 1, stored as int8, scale fp16 per column (cols,) or per row
+    (rows, 1) (cross_layer_share.py:584-595 and :604-614).  Test-data
+    generator; pinned by the round-trip bound |dequant(q) - t| <= scale /
+    (2 maxval) + fp16 rounding (tests/test_factor_oracle.py)."""
+    maxval = 2 ** (nbits - 1) - 1
+    if rowwise:
+        scale = t.float().abs().max(dim=1, keepdim=True).values.clamp(min=1e-8)
+    else:
+        scale = t.float().abs().max(dim=0).values.clamp(min=1e-8)
+    q = (t.float() / scale * maxval).round().clamp(-maxval, maxval).to(torch.int8)
+    return q, scale.half()
+
+
+def dequant_intN(q: torch.Tensor, scale: torch.Tensor, nbits: int) -> torch.Tensor:
+    """fp16(q.float() / maxval * scale.float()) in fp32 (_dequant_intN,
+    inference/model_builder.py:69-72, then the callers' .half(), :46-50,
+    :510-527).  Pinned by: q = +-maxval gives +-scale exactly, q = 0 gives 0,
+    and an explicit per-element loop for both scale layouts."""
+    maxval = 2 ** (nbits - 1) - 1
+    return (q.float() / maxval * scale.float()).half()
+
+
+def pack_int4(q: torch.Tensor) -> torch.Tensor:
+    """(rows, cols) int8 in [-7, 7] -> ((rows+1)//2, cols) uint8: row 2i in the
+    low nibble, row 2i+1 in the high nibble, each as value + 7
+    (cross_layer_share.py:619-634).  Pinned by unpack_int4 brute force."""
+    rows, cols = q.shape
+    u = (q.to(torch.int16) + 7).to(torch.uint8)
+    if rows % 2:
+        u = torch.cat([u, torch.zeros(1, cols, dtype=torch.uint8)], dim=0)
+    return (u[0::2] | (u[1::2] << 4)).to(torch.uint8)
+
+
+def unpack_int4(packed: torch.Tensor, orig_rows: int) -> torch.Tensor:
+    """Inverse of pack_int4 (_unpack_int4, inference/model_builder.py:75-80):
+    element (r, c) = ((byte(r//2, c) >> 4*(r%2)) & 15) - 7.  Pinned by every
+    nibble value in both positions and pack/unpack round trips over odd and
+    even row counts."""
+    rows = orig_rows
+    out = torch.empty(rows, packed.shape[1], dtype=torch.int8)
+    p = packed.to(torch.int16)
+    for r in range(rows):
+        out[r] = ((p[r // 2] >> (4 * (r % 2))) & 15) - 7
+    return out
