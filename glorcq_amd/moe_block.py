@@ -60,6 +60,10 @@ class GraphCompatibleMoeBlock(nn.Module):
         self.shared_inter = stacked["shared_inter"]
         self.group = 128
         self.graph_mode = True  # every step is graph-safe
+        # forward returns (final, router_logits) as the reference's block does
+        # (transformers 4.x decoder layers unpack the pair); False returns final
+        # alone, the contract of transformers 5 sparse-MoE blocks
+        self.return_router_logits = True
         self.t = stacked  # device tensors (kept alive for the kernels)
         self._ws: dict = {}
 
@@ -231,9 +235,13 @@ class GraphCompatibleMoeBlock(nn.Module):
             self._ws[B] = ws
         return ws
 
+    MAX_TOKENS = 64  # tokens per glq_moe_decode call
+
     def forward(self, hidden_states: torch.Tensor):
         """(final (b, s, H) fp16, router_logits (b*s, E) fp16), as the
-        reference's forward (moe_block.py:381-436)."""
+        reference's forward (moe_block.py:381-436); final alone when
+        return_router_logits is False.  Tokens are independent in the block,
+        so more than 64 (a prefill) run as consecutive 64-token steps."""
         lib = _lib.load()
         shape = hidden_states.shape
         h = hidden_states.reshape(-1, self.hidden)
@@ -244,12 +252,15 @@ class GraphCompatibleMoeBlock(nn.Module):
             raise RuntimeError("hidden_states must be on the GPU")
         out = torch.empty_like(h)
         logits = torch.empty(h.shape[0], self.num_experts, dtype=torch.float16, device=h.device)
-        P = self._params(h, out, logits)
-        ws = self._workspace(lib, P)
-        rc = lib.glq_moe_decode(ctypes.byref(P), ws.data_ptr(), ws.numel(),
-                                _lib.stream_handle(h.device))
-        _lib.check(rc, "glq_moe_decode")
-        return out.reshape(shape), logits
+        stream = _lib.stream_handle(h.device)
+        for t0 in range(0, h.shape[0], self.MAX_TOKENS):
+            t1 = min(h.shape[0], t0 + self.MAX_TOKENS)
+            P = self._params(h[t0:t1], out[t0:t1], logits[t0:t1])
+            ws = self._workspace(lib, P)
+            rc = lib.glq_moe_decode(ctypes.byref(P), ws.data_ptr(), ws.numel(), stream)
+            _lib.check(rc, "glq_moe_decode")
+        out = out.reshape(shape)
+        return (out, logits) if self.return_router_logits else out
 
     def extra_repr(self):
         return (f"experts={self.num_experts}, top_k={self.top_k}, hidden={self.hidden}, "
