@@ -138,7 +138,8 @@ __device__ int moe_dispatch(const MoeArgs& a, const MoeTables& t, bool sel_globa
   __syncthreads();
   for (int e = tid; e < E; e += 256) {
     int c = 0;
-    for (int p = 0; p < P; ++p) c += t.sel[p] == e;
+#pragma unroll 8
+    for (int p = 0; p < P; ++p) c += (int)(t.sel[p] == e);
     t.cnt[e] = c;
   }
   __syncthreads();
@@ -179,7 +180,8 @@ __device__ int moe_dispatch(const MoeArgs& a, const MoeTables& t, bool sel_globa
       continue;
     }
     int r = 0;
-    for (int q = 0; q < p; ++q) r += t.sel[q] == e;
+#pragma unroll 8
+    for (int q = 0; q < p; ++q) r += (int)(t.sel[q] == e);
     t.list[t.off[e] + r] = p;
     const int b = t.boff[e] + r / kMoeTB;
     t.pos[p] = b * kMoeTB + r % kMoeTB;
@@ -197,53 +199,69 @@ __device__ __forceinline__ int align_up_dev(int v, int a) { return (v + a - 1) /
 
 
 // ---------------------------------------------------------------------------
-// 1. Router + gate/up cluster partials (1024-thread workgroups)
+// 1. Router + gate/up cluster partials (256-thread workgroups)
 // ---------------------------------------------------------------------------
-constexpr int kRouteThreads = 1024;
+constexpr int kRouteThreads = 256;
+
+// Routing keys: the order (logit descending, expert index ascending) as one
+// unsigned compare.  The fp16 logit's bits map to an order-preserving 16-bit
+// value (negative: all bits flipped; positive: sign bit set; -0 taken as +0),
+// above 0xFFFF - e.  moe_key_logit inverts it.
+__device__ __forceinline__ uint32_t moe_key(uint32_t bits, int e) {  // bits: the fp16 pattern
+  uint32_t u = bits & 0xFFFFu;
+  if (u == 0x8000u) u = 0u;
+  u = (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
+  return (u << 16) | (uint32_t)(0xFFFF - e);
+}
+__device__ __forceinline__ float moe_key_logit(uint32_t k) {
+  uint32_t u = k >> 16;
+  u = (u & 0x8000u) ? (u & 0x7FFFu) : (~u & 0xFFFFu);
+  return __half2float(__ushort_as_half((unsigned short)u));
+}
+
+__host__ __device__ inline int moe_lg_stride(int E) { return ((E + 3) & ~3) + 4; }
 
 // Softmax, top-k (and optional renormalisation) of every token at once
-// (moe_block.py:386-392): lane t of one wave routes token t (B <= 64) from an
-// fp32 LDS copy of its fp16 logits (rows of E + 1 floats: the lanes of one
-// read hit distinct banks; reads unrolled so several are in flight).  Pass j picks the best expert strictly behind pick j-1 in the order
-// (logit descending, index ascending): ties go to the lower index, and as the
-// probabilities exp(l - max) / sum are monotonic in the logit (distinct fp16
-// logits give distinct fp32 probabilities) this is the probability order.
-// Then the softmax sum in index order and the weights of the picks.  No
-// cross-lane traffic.  Ids -> sel[t * topk + j] (LDS); `publish` also writes
-// ids and fp16 weights to the workspace.
-__device__ void moe_topk_lanes(const MoeArgs& a, const float* lgf, int* sel, bool publish) {
-  const int t = threadIdx.x & 63;
-  if (t >= a.B) return;
-  const int E = a.E;
-  const float* col = lgf + t * (E + 1);  // this token's row (E + 1 floats: distinct banks)
-  float pv = INFINITY, mx = 0.f;
-  int pi = -1;
-  for (int j = 0; j < a.topk; ++j) {
-    float bv = -INFINITY;
-    int bi = -1;
-#pragma unroll 8
-    for (int e = 0; e < E; ++e) {
-      const float w = col[e];
-      const bool behind = (w < pv) | ((w == pv) & (e > pi));
-      const bool better = behind & ((w > bv) | (bi < 0));
-      bv = better ? w : bv;
-      bi = better ? e : bi;
+// (moe_block.py:386-392), by all 256 threads, from the routing keys of every
+// (token, expert) in LDS (16-byte aligned rows).  Thread (t, e) counts the
+// keys above its own -- the experts ahead of e in (logit descending, index
+// ascending); ties go to the lower index, and as the probabilities
+// exp(l - max) / sum are monotonic in the logit (distinct fp16 logits give
+// distinct fp32 probabilities) this is the probability order -- and an expert
+// of rank j < topk lands in sel[t * topk + j]: one compare per pair, no
+// dependent passes.  Then (`publish`) one thread per token forms the softmax
+// sum in index order and the weights of the picks, and writes ids and fp16
+// weights to the workspace.
+__device__ void moe_topk_ranks(const MoeArgs& a, const uint32_t* lgk, int* sel, bool publish) {
+  const int E = a.E, tid = threadIdx.x, LS = moe_lg_stride(E), E4 = E & ~3;
+  for (int q = tid; q < a.B * E; q += 256) {
+    const int t = q / E, e = q - t * E;
+    const uint32_t* row = lgk + t * LS;
+    const uint32_t ke = row[e];
+    int r = 0;
+#pragma unroll 4
+    for (int j = 0; j < E4; j += 4) {  // 16-byte LDS reads, broadcast across the token's lanes
+      const uint4 v = *(const uint4*)(row + j);
+      r += (int)(v.x > ke) + (int)(v.y > ke) + (int)(v.z > ke) + (int)(v.w > ke);
     }
-    if (j == 0) mx = bv;
-    sel[t * a.topk + j] = bi;
-    pv = bv;
-    pi = bi;
+    for (int j = E4; j < E; ++j) r += (int)(row[j] > ke);
+    if (r < a.topk) sel[t * a.topk + r] = e;
   }
-  if (!publish) return;
+  __syncthreads();
+  const int t = tid;
+  if (!publish || t >= a.B) return;
+  const uint32_t* row = lgk + t * LS;
+  const float mx = moe_key_logit(row[sel[t * a.topk]]);
   float sum = 0.f;
 #pragma unroll 8
-  for (int e = 0; e < E; ++e) sum += expf(col[e] - mx);
+  for (int e = 0; e < E; ++e) sum += expf(moe_key_logit(row[e]) - mx);
   float ws = 0.f;
   if (a.norm)
-    for (int j = 0; j < a.topk; ++j) ws += expf(col[sel[t * a.topk + j]] - mx) / sum;
+    for (int j = 0; j < a.topk; ++j)
+      ws += expf(moe_key_logit(row[sel[t * a.topk + j]]) - mx) / sum;
   for (int j = 0; j < a.topk; ++j) {
     const int e = sel[t * a.topk + j];
-    float w = expf(col[e] - mx) / sum;
+    float w = expf(moe_key_logit(row[e]) - mx) / sum;
     if (a.norm) w = w / ws;
     a.sel[t * a.topk + j] = e;
     a.wts[t * a.topk + j] = __float2half(w);
@@ -253,11 +271,11 @@ __device__ void moe_topk_lanes(const MoeArgs& a, const float* lgf, int* sel, boo
 // Router logits of tokens [16 rb, 16 rb + 16) x router rows [16 tile,
 // 16 tile + 16) (the rows after the E experts: the shared-expert gate), one
 // MFMA tile (A = h rows staged in LDS, B = router rows) with K split over the
-// 16 waves: every router-row load of a wave goes out before it waits, and the
+// 4 waves: every router-row load of a wave goes out before it waits, and the
 // rows of a tile come from one workgroup per tile, so no CU pulls the whole
 // router matrix.  fp32 sums rounded to fp16 once -> workspace (and the
 // caller's router_logits); the shared-expert gate sigmoid(fp16 logit) -> sg.
-constexpr int kRouteBatch = 16;  // MFMA k-steps (32 codes each) a wave loads at once
+constexpr int kRouteBatch = 8;  // MFMA k-steps (32 codes each) a wave loads at once
 __device__ void moe_route_tile(const MoeArgs& a, int id, unsigned char* smem) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, kb = lane >> 4;
@@ -266,51 +284,38 @@ __device__ void moe_route_tile(const MoeArgs& a, int id, unsigned char* smem) {
   const int tile = id % ntile, rb = id / ntile;
   const int t0 = rb * 16, nt = min(16, a.B - t0);
   const int hstride = a.H + 8;
-  __half* hl = (__half*)smem;                       // [16][H + 8]
-  float* red = (float*)(smem + 16 * hstride * 2);  // [16 waves][256]
-  const int kseg = max(32, a.H / 16 / 32 * 32);    // codes per wave (a multiple of 32)
-  const int nks = a.H / kseg;                       // waves with a K segment
+  __half* hl = (__half*)smem;                       // [nt][H + 8]
+  float* red = (float*)(smem + 16 * hstride * 2);  // [4 waves][256]
+  const int kseg = a.H / 4;                         // codes per wave (H % 256 == 0)
   const int steps = kseg / 32;
   const int n = min(tile * 16 + li, nrow - 1);
-  const __half* wr = n < a.E ? a.rw + (int64_t)n * a.H : a.sgw;
-  const bool kv = wave < nks;
-  const int kbase = wave * kseg + 8 * kb;
+  const __half* wr = (n < a.E ? a.rw + (int64_t)n * a.H : a.sgw) + wave * kseg + 8 * kb;
+  const __half* hr = hl + min(li, nt - 1) * hstride + wave * kseg + 8 * kb;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  bool staged = false;
   for (int s0 = 0; s0 < steps; s0 += kRouteBatch) {
     f16x8 wv[kRouteBatch];
 #pragma unroll
-    for (int u = 0; u < kRouteBatch; ++u) {
-      const bool sv = kv && s0 + u < steps;
-      wv[u] = sv ? *(const f16x8*)(wr + kbase + 32 * (s0 + u)) : f16x8{};
-    }
-    if (!staged) {  // h rows into LDS while the router rows are in flight
-      for (int idx = tid; idx < 16 * (a.H / 8); idx += kRouteThreads) {
+    for (int u = 0; u < kRouteBatch; ++u)
+      wv[u] = s0 + u < steps ? *(const f16x8*)(wr + 32 * (s0 + u)) : f16x8{};
+    if (s0 == 0) {  // h rows into LDS while the router rows are in flight
+      for (int idx = tid; idx < nt * (a.H / 8); idx += kRouteThreads) {
         const int m = idx / (a.H / 8), k8 = idx - m * (a.H / 8);
-        *(f16x8*)(hl + m * hstride + 8 * k8) =
-            m < nt ? *(const f16x8*)(a.h + (int64_t)(t0 + m) * a.H + 8 * k8) : f16x8{};
+        *(f16x8*)(hl + m * hstride + 8 * k8) = *(const f16x8*)(a.h + (int64_t)(t0 + m) * a.H + 8 * k8);
       }
       __syncthreads();
-      staged = true;
     }
-    if (kv) {
 #pragma unroll
-      for (int u = 0; u < kRouteBatch; ++u) {
-        if (s0 + u >= steps) break;  // only steps inside the segment read staged h
-        const f16x8 hv = *(const f16x8*)(hl + li * hstride + kbase + 32 * (s0 + u));
-        acc = mfma_16x16x32(hv, wv[u], acc);
-      }
-    }
+    for (int u = 0; u < kRouteBatch; ++u)
+      if (s0 + u < steps) acc = mfma_16x16x32(*(const f16x8*)(hr + 32 * (s0 + u)), wv[u], acc);
   }
-  if (!staged) __syncthreads();  // (steps == 0 cannot happen: H >= 256)
+  // acc[i]: token 4kb + i, router row li of the tile
 #pragma unroll
   for (int i = 0; i < 4; ++i) red[wave * 256 + (4 * kb + i) * 16 + li] = acc[i];
   __syncthreads();
-  if (tid < 256) {  // token m = tid / 16, row tile*16 + tid % 16
+  {  // token m = tid / 16, row tile*16 + tid % 16; waves summed in order
     const int m = tid >> 4, r = tile * 16 + (tid & 15);
-    float s = 0.f;
-    for (int w = 0; w < nks; ++w) s += red[w * 256 + tid];
-    const __half lgh = __float2half(s);
+    const float sum = red[tid] + red[256 + tid] + red[512 + tid] + red[768 + tid];
+    const __half lgh = __float2half(sum);
     if (m < nt && r < a.E) {
       a.lgb[(int64_t)(t0 + m) * a.E + r] = lgh;
       if (a.logits) a.logits[(int64_t)(t0 + m) * a.E + r] = lgh;
@@ -322,87 +327,67 @@ __device__ void moe_route_tile(const MoeArgs& a, int id, unsigned char* smem) {
 }
 
 // x U_c partials of one job (projection s in {gate, up}, cluster c, K-slice q
-// of xurows rows): part[t][r] = sum_{k in slice} x[t][k] U_c[k][r].  The U
-// slice reaches LDS by 16-byte loads; v_mfma_f32_16x16x4f32 (A = x: token x
-// 4 k, B = U: 4 k x 16 rank columns, one LDS element per lane, so U keeps its
-// row-major layout).  Wave w takes rank tile w % 4 (of <= 8) and k-range
-// w / 4 (of 4); the k-ranges add up in LDS in turn.
+// of xurows rows): part[t][r] = sum_{k in slice} x[t][k] U_c[k][r], fp32.
+// The x and U slices reach LDS by 16-byte loads (both row-major); wave w takes
+// rank tiles w, w + 4 over the whole slice with v_mfma_f32_16x16x32_f16
+// (A = x rows, 16-byte LDS reads; B = 8 U values of one rank column), so the
+// sums need no cross-wave step and leave from registers.
 __device__ void moe_xu_job(const MoeArgs& a, int job, unsigned char* smem) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, kb = lane >> 4;
   const int s = job / (a.C * a.sus), rem = job - s * a.C * a.sus;
   const int c = rem / a.sus, q = rem - c * a.sus;
   const int xr = a.xurows;
-  const int k0 = q * xr, kl = min(xr, a.H - k0);
-  const int ntt = (a.B + 15) / 16;          // token tiles
-  const int nrt = (a.rank + 15) / 16;       // rank tiles (<= 8)
-  const int xstride = xr + 4, ustride = a.rank + 8;
-  __half* xl = (__half*)smem;                                     // [B][xr + 4]
+  const int k0 = q * xr, kl = min(xr, a.H - k0);  // kl is a multiple of 128
+  const int ntt = (a.B + 15) / 16;                // token tiles
+  const int nrt = (a.rank + 15) / 16;             // rank tiles (<= 8)
+  const int xstride = xr + 8, ustride = a.rank + 8;
+  __half* xl = (__half*)smem;                                           // [B][xr + 8]
   __half* ul = (__half*)(smem + align_up_dev(a.B * xstride * 2, 16));  // [xr][rank + 8]
-  float* red = (float*)((unsigned char*)ul + align_up_dev(xr * ustride * 2, 16));
   const int urow = min(max(a.uslot[s] ? a.uslot[s][c] : c, 0), a.urows[s] - 1);
   const __half* U = a.U[s] + (int64_t)urow * a.u_es[s] + (int64_t)k0 * a.rank;
   const int r8 = a.rank / 8;
   for (int idx = tid; idx < kl * r8; idx += kRouteThreads) {  // U slice, 16 B per load
     const int k = idx / r8, j8 = idx - k * r8;
-    const f16x8 v = *(const f16x8*)(U + (int64_t)k * a.rank + 8 * j8);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) ul[k * ustride + 8 * j8 + u] = v[u];
+    *(f16x8*)(ul + k * ustride + 8 * j8) = *(const f16x8*)(U + (int64_t)k * a.rank + 8 * j8);
   }
-  for (int idx = tid; idx < a.B * (xr / 8); idx += kRouteThreads) {
-    const int m = idx / (xr / 8), k8 = idx - m * (xr / 8);
-    f16x8 v = f16x8{};
-    if (8 * k8 < kl) v = *(const f16x8*)(a.h + (int64_t)m * a.H + k0 + 8 * k8);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) xl[m * xstride + 8 * k8 + u] = v[u];
+  for (int idx = tid; idx < a.B * (kl / 8); idx += kRouteThreads) {
+    const int m = idx / (kl / 8), k8 = idx - m * (kl / 8);
+    *(f16x8*)(xl + m * xstride + 8 * k8) = *(const f16x8*)(a.h + (int64_t)m * a.H + k0 + 8 * k8);
+  }
+  float* out = a.xu + (((int64_t)s * a.C + c) * a.sus + q) * a.B * a.rpad;
+  for (int idx = tid; idx < a.B * (a.rpad - nrt * 16); idx += kRouteThreads) {
+    const int w = a.rpad - nrt * 16, m = idx / w, j = nrt * 16 + idx - m * w;
+    out[(int64_t)m * a.rpad + j] = 0.f;  // rank padding
   }
   __syncthreads();
-  const int kr = wave >> 2;  // k-range of this wave: rows [kr * xr / 4, (kr + 1) * xr / 4)
-  const int ns = xr / 4 / 4;  // steps of 4 rows per k-range
-  // every wave runs the same number of iterations (the loop holds barriers)
-  for (int it = 0; it < (nrt + 3) / 4; ++it) {
-    const int rt = (wave & 3) + 4 * it;
-    const bool rv = rt < nrt;
-    const int col = rt * 16 + li;
+  const int ksteps = kl / 32;
+  for (int rt = wave; rt < nrt; rt += 4) {
     f32x4 acc[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (rv) {
-      for (int u = 0; u < ns; ++u) {
-        const int k = kr * (xr / 4) + 4 * u + kb;
-        const float uv = (k < kl && col < a.rank) ? __half2float(ul[k * ustride + col]) : 0.f;
+    const int col = min(rt * 16 + li, a.rank - 1);
+    for (int u = 0; u < ksteps; ++u) {
+      const int k = 32 * u + 8 * kb;
+      f16x8 bv;
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-          if (tt < ntt) {
-            const int m = tt * 16 + li;
-            const float xv = m < a.B ? __half2float(xl[m * xstride + k]) : 0.f;
-            acc[tt] = mfma_16x16x4f32(xv, uv, acc[tt]);
-          }
-      }
+      for (int e = 0; e < 8; ++e) bv[e] = (_Float16)ul[(k + e) * ustride + col];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+        if (tt < ntt) {  // rows past B read a staged row and are not stored
+          const int m = min(tt * 16 + li, a.B - 1);
+          acc[tt] = mfma_16x16x32(*(const f16x8*)(xl + m * xstride + k), bv, acc[tt]);
+        }
     }
-    // acc[tt][i]: token tt*16 + 4kb + i, rank column col; the four k-ranges
-    // add into one buffer in turn (k-range order: deterministic)
-    for (int r = 0; r < 4; ++r) {
-      if (r == kr && rv) {
+    // acc[tt][i]: token tt*16 + 4kb + i, rank column rt*16 + li
+    const int j = rt * 16 + li;
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-          if (tt < ntt) {
-            float* rp = red + (tt * nrt + rt) * 256;
+    for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              float* d = rp + (4 * kb + i) * 16 + li;
-              *d = r == 0 ? acc[tt][i] : *d + acc[tt][i];
-            }
-          }
+      for (int i = 0; i < 4; ++i) {
+        const int m = tt * 16 + 4 * kb + i;
+        if (tt < ntt && m < a.B) out[(int64_t)m * a.rpad + j] = j < a.rank ? acc[tt][i] : 0.f;
       }
-      __syncthreads();
-    }
-  }
-  float* out = a.xu + (((int64_t)s * a.C + c) * a.sus + q) * a.B * a.rpad;
-  for (int idx = tid; idx < a.B * a.rpad; idx += kRouteThreads) {
-    const int m = idx / a.rpad, j = idx - m * a.rpad;
-    out[idx] = j < nrt * 16 ? red[((m >> 4) * nrt + (j >> 4)) * 256 + (m & 15) * 16 + (j & 15)]
-                            : 0.f;
   }
 }
 
@@ -489,24 +474,24 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
     {
       const MoeTables t = moe_tables((int*)smem, a.B * a.topk, a.E, a.nbm);
       // routing of every token (workgroup 0 publishes it for the later launches):
-      // the logits reach LDS (fp32, rows of E + 1) in one pass, then one lane
-      // per token
-      float* lgf = (float*)(smem + a.lg_off);
-      const int nl = a.B * a.E;
+      // the logits reach LDS as routing keys (rows of moe_lg_stride(E)) in one pass
+      uint32_t* lgk = (uint32_t*)(smem + a.lg_off);
+      const int nl = a.B * a.E, LS = moe_lg_stride(a.E);
       for (int i = tid; i < nl / 8; i += 256) {  // 16-byte loads of the flat [B][E] array
-        const f16x8 v = ((const f16x8*)a.lgb)[i];
+        const uint4 v = ((const uint4*)a.lgb)[i];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          const int f = 8 * i + u, tk = f / a.E;
-          lgf[f + tk] = (float)v[u];  // row tk starts at tk * (E + 1)
+          const int f = 8 * i + u, tk = f / a.E, e = f - tk * a.E;
+          lgk[tk * LS + e] = moe_key(w[u >> 1] >> (16 * (u & 1)), e);
         }
       }
       for (int f = nl / 8 * 8 + tid; f < nl; f += 256) {
-        const int tk = f / a.E;
-        lgf[f + tk] = __half2float(a.lgb[f]);
+        const int tk = f / a.E, e = f - tk * a.E;
+        lgk[tk * LS + e] = moe_key(__half_as_ushort(a.lgb[f]), e);
       }
       __syncthreads();
-      if (tid < 64) moe_topk_lanes(a, lgf, t.sel, blockIdx.x == 0);
+      moe_topk_ranks(a, lgk, t.sel, blockIdx.x == 0);
       __syncthreads();
       const int nblk = moe_dispatch(a, t, false);
       if (b >= nblk) return;  // uniform over the workgroup
@@ -769,7 +754,7 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
   a.sbits = SI > 0 ? p->shared_bits : 0;
   const int P_ = (int)(B * k);
   a.nbm = (int)std::min<int64_t>(E, P_) + P_ / kMoeTB;
-  a.xurows = a.rank <= 64 ? 512 : 256;
+  a.xurows = (a.rank <= 64 && B <= 16) ? 512 : 256;
   a.sus = (int)((H + a.xurows - 1) / a.xurows);
   const int mr = (int)std::min<int64_t>(B, kMoeTB);  // staged rows per routed block
   // gate/up: K = H, N = I
@@ -803,8 +788,8 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
   // partial tiles) and the tables
   a.tl_off = (int)align_up(std::max(Lgu.total + stream_ks_bytes(2), tbl), 16);
   size_t lgu = (size_t)a.tl_off + 16 * 4 + 3 * 4 * (size_t)E;
-  a.lg_off = (int)align_up(lgu, 16);  // B x (E + 1) fp32 logits for the top-k
-  lgu = a.lg_off + align_up(4 * B * (E + 1), 16);
+  a.lg_off = (int)align_up(lgu, 16);  // B rows of routing keys for the top-k
+  lgu = a.lg_off + align_up(4 * B * moe_lg_stride((int)E), 16);
   const StreamLds Ld = stream_lds(kMoeDepth, stream_slot_bytes(a.bits), mr, a.kr, a.bits,
                                   a.shD.xstride, a.shD.apad, 1, 0);
   size_t ld = std::max<size_t>(Ld.total + stream_ks_bytes(1), tbl);
@@ -823,10 +808,9 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
   P.lds_d = ld;
   P.lds_c = 0;
   {
-    const size_t router = (size_t)16 * (H + 8) * 2 + (size_t)16 * 256 * 4;
-    const size_t xu = (size_t)align_up(B * (a.xurows + 4) * 2, 16) +
-                      (size_t)align_up((int64_t)a.xurows * (a.rank + 8) * 2, 16) +
-                      (size_t)((B + 15) / 16) * ((a.rank + 15) / 16) * 256 * 4;
+    const size_t router = (size_t)16 * (H + 8) * 2 + (size_t)4 * 256 * 4;
+    const size_t xu = (size_t)align_up(B * (a.xurows + 8) * 2, 16) +
+                      (size_t)a.xurows * (a.rank + 8) * 2;
     P.lds_route = std::max(router, lora ? xu : (size_t)0);
     GLQ_CHECK(P.lds_route <= 160 * 1024,
               "hidden=%lld with %lld tokens exceeds the router's LDS budget", (long long)H,

@@ -113,6 +113,29 @@ def test_config2_parity(gpu, B, seed):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("B,seed", [(1, 1), (16, 1), (32, 2), (64, 2)])
+def test_config2_routed_only(gpu, B, seed):
+    """Config 2's routed experts alone (no shared expert, whose large outputs
+    would set the bar's row term): the output is the weighted sum of the
+    selected experts, so a wrong pick or weight moves it past the bar -- an
+    oracle routed with two router rows swapped (other experts picked) fails."""
+    p = fmt.make_moe(B=B, seed=seed, shared_inter=0)
+    assert margin(p) >= 2
+    _, out, logits = run_block(p, gpu)
+    check_routing(p, logits)
+    ref = O.moe_forward(p)
+    assert bar(out, ref), float((out.double() - ref).abs().max())
+    _, _, sel = O.route(p.h, p.router_w, p.top_k, False, exact=True)
+    e0 = int(sel[0, 0])
+    other = next(e for e in range(p.E) if e not in sel[0].tolist())
+    q = fmt.make_moe(B=B, seed=seed, shared_inter=0)
+    rw = q.router_w.clone()
+    rw[[e0, other]] = rw[[other, e0]]
+    q.router_w = rw
+    assert not bar(out, O.moe_forward(q))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("B", [1, 16])
 def test_config2_lora_heavy(gpu, B):
     """U and SV scaled x30 so a wrong cluster, SV row or a_down reduction
