@@ -72,6 +72,12 @@ struct DenseSrc {
   }
 };
 
+}  // namespace glq
+
+#include "glq_lane.h"
+
+namespace glq {
+
 template <int MC>
 __global__ __launch_bounds__(256) void lowrank_partial_kernel(DenseArgs a) {
   __shared__ float red[4 * 4 * 64];
@@ -288,6 +294,71 @@ static int launch_stream(const DenseStreamArgs& sa, int64_t items, int bits, boo
   return launch_stream_sym<false>(sa, items, bits, sz2, lds, s);
 }
 
+// Lane-sliced path (glq_lane.h): one token row, group 128, a code row of at
+// most 64 16-byte pieces, rank <= 128.
+constexpr int kLanePD = 4;              // iterations of loads in flight per wave
+constexpr int64_t kLaneWaves = 4096;    // target waves per launch (4 per SIMD)
+
+static bool lane_shape(int64_t M, const TileShape& sh, int bits) {
+  if (getenv("GLQ_GEMV_NO_LANE")) return false;
+  return M == 1 && sh.group == 128 && sh.rank <= 128 && (int64_t)sh.K * bits / 128 <= 64;
+}
+
+template <int BITS, bool SYM, int LRP, int NSV, bool HASB>
+static int launch_lane_k(const LaneArgs& la, hipStream_t s) {
+  const int64_t waves = (int64_t)la.a.items * la.wpi;
+  const int64_t grid = (waves + 3) / 4;
+  GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
+  gemv_lane_kernel<BITS, SYM, LRP, kLanePD, NSV, HASB>
+      <<<dim3((unsigned)grid), dim3(256), 0, s>>>(la);
+  GLQ_LAUNCH_CHECK("gemv_lane_kernel");
+  return GLQ_OK;
+}
+
+// SV dwords per lane: rank / 2 spread over the LRP lanes of a row.
+template <int BITS, bool SYM, int LRP, bool HASB>
+static int launch_lane_sv(const LaneArgs& la, hipStream_t s) {
+  const int nsv = (la.a.sh.rank / 2 + LRP - 1) / LRP;
+  if (nsv <= 1) return launch_lane_k<BITS, SYM, LRP, 1, HASB>(la, s);
+  if constexpr (LRP <= 32) {
+    if (nsv <= 2) return launch_lane_k<BITS, SYM, LRP, 2, HASB>(la, s);
+  }
+  if constexpr (LRP == 16) return launch_lane_k<BITS, SYM, LRP, 4, HASB>(la, s);
+  GLQ_CHECK(false, "rank %d too large for the lane path", la.a.sh.rank);
+}
+
+template <int BITS, bool SYM, bool HASB>
+static int launch_lane_lrp(const LaneArgs& la, hipStream_t s) {
+  if (la.lr <= 16) return launch_lane_sv<BITS, SYM, 16, HASB>(la, s);
+  if (la.lr <= 32) return launch_lane_sv<BITS, SYM, 32, HASB>(la, s);
+  return launch_lane_sv<BITS, SYM, 64, HASB>(la, s);
+}
+
+template <int BITS>
+static int launch_lane_bits(const LaneArgs& la, hipStream_t s) {
+  const bool hb = la.a.bias != nullptr;
+  if (la.a.sh.sym) return hb ? launch_lane_lrp<BITS, true, true>(la, s)
+                             : launch_lane_lrp<BITS, true, false>(la, s);
+  return hb ? launch_lane_lrp<BITS, false, true>(la, s) : launch_lane_lrp<BITS, false, false>(la, s);
+}
+
+static int launch_lane(const DenseArgs& a, int bits, hipStream_t s) {
+  LaneArgs la;
+  la.a = a;
+  la.lr = a.sh.K * bits / 128;
+  const int lrp = la.lr <= 16 ? 16 : la.lr <= 32 ? 32 : 64;
+  la.its = (a.sh.N + 63) / 64 * lrp;
+  // about kLaneWaves waves over the launch (whole units when the launch is
+  // large, a ring's worth of iterations at least)
+  const int64_t total = (int64_t)a.items * la.its;
+  int64_t ipw = (total + kLaneWaves - 1) / kLaneWaves;
+  if (const char* e = getenv("GLQ_LANE_IPW")) ipw = atoll(e) > 0 ? atoll(e) : ipw;
+  ipw = std::min<int64_t>(std::max<int64_t>(ipw, kLanePD), la.its);
+  la.ipw = (int)((ipw + kLanePD - 1) / kLanePD * kLanePD);
+  la.wpi = (la.its + la.ipw - 1) / la.ipw;
+  return bits == 2 ? launch_lane_bits<2>(la, s) : launch_lane_bits<4>(la, s);
+}
+
 static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
                      int64_t K, int64_t N, const int32_t* codes,
                      int64_t codes_stride, int bits, const void* scales,
@@ -356,6 +427,7 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
     else lowrank_partial_kernel<4><<<grid, dim3(256), 0, s>>>(a);
     GLQ_LAUNCH_CHECK("lowrank_partial_kernel");
   }
+  if (lane_shape(M, sh, bits)) return launch_lane(a, bits, s);
   DenseStreamArgs sa;
   size_t slds = 0;
   bool sz2 = false;

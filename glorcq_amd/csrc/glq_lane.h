@@ -1,0 +1,270 @@
+// Lane-sliced fused dequant-GEMV + low-rank correction for one token row
+// (M = 1, group 128): the decode shape of every expert and attention
+// projection at batch 1.
+//
+//   y[n] = sum_g s[n,g] * sum_{k in g} (q[n,k] - z[n,g]) x[k]
+//        + sum_j a[j] SV[n,j] + bias[n],          a = fp16(x U)
+//
+// With one token row a 16x16 MFMA tile wastes 15 of its 16 token columns,
+// and the MFMA time then exceeds the decode.  Here the wave's lanes own fixed
+// K slices instead:
+//  * a row of codes is K*bits/8 bytes = LR 16-byte pieces (LR <= 64); lanes
+//    are grouped by LRP = LR rounded up to 16, 32 or 64, so one wave
+//    iteration covers RPI = 64 / LRP rows, lane l holding piece l % LRP of row
+//    l / LRP.  Every load instruction of codes is 64 lanes x 16 bytes of
+//    consecutive rows -- contiguous when LR = LRP.
+//  * lane l's x slice (the 64 or 32 codes of its piece) lives in registers
+//    for the whole run of rows, already in the decode's operand order, with
+//    its operand-bias sum c1 = sum 2^e(k) x[k] and c2 = sum x[k];
+//  * codes decode into packed fp16 (2^e + q) with one v_and_or per two codes
+//    (the same decode as the MFMA kernels) and meet x in v_dot2c_f32_f16, fp32
+//    accumulate; per row the lane adds s * (dot - c1 - z c2) and its share of
+//    a SV^T (one dword of SV per lane per 64 rank columns);
+//  * the LRP lanes of a row reduce with DPP (strides 1, 2, 4, 8) and the
+//    gfx950 permlane16/permlane32 swaps; lane l keeps the total of the row it
+//    will store, so the 64 rows of a wave's unit leave in one 128-byte store.
+//  * loads run PD iterations ahead of use in a register ring; nothing goes
+//    through LDS.
+// Semantics as gemv_tile (glq_gemv_core.h), so outputs of the two agree to
+// fp32 summation order.
+#pragma once
+
+#include "glq_gemv_core.h"
+
+namespace glq {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Codes per lane piece (16 bytes).
+template <int BITS>
+constexpr int lane_piece_codes() { return 128 / BITS; }
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c,
+                                false);
+}
+
+// Sum over the LRP lanes of each lane group; every lane of the group gets it.
+template <int LRP>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  auto dpp_add = [](float x, int ctrl) -> float {
+    int y = 0;
+    switch (ctrl) {  // the control word must be an immediate
+      case 0: y = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false); break;
+      case 1: y = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false); break;
+      case 2: y = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false); break;
+      default: y = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false); break;
+    }
+    return x + __int_as_float(y);
+  };
+  v = dpp_add(v, 0);  // quad_perm [1,0,3,2]: lane ^ 1
+  v = dpp_add(v, 1);  // quad_perm [2,3,0,1]: lane ^ 2
+  v = dpp_add(v, 2);  // row_half_mirror: lane i <-> 7 - i within each 8 (quads summed)
+  v = dpp_add(v, 3);  // row_mirror: lane i <-> 15 - i within each 16
+  if constexpr (LRP >= 32) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // rows 0+1, 2+3
+  }
+  if constexpr (LRP >= 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // halves
+  }
+  return v;
+}
+
+struct LaneArgs {
+  DenseArgs a;
+  int its;  // iterations per item: 64-row units x LRP
+  int ipw;  // iterations per wave (a multiple of the ring depth)
+  int wpi;  // waves per item
+  int lr;   // 16-byte pieces per code row
+};
+
+// Decoded operands of one code word as packed fp16 pairs (decode2 / decode4).
+__device__ __forceinline__ void decode2_words(uint32_t w, u32x4& a, u32x4& b,
+                                              const DecodeConsts& k) {
+  const uint32_t v = w >> 10;
+  a.x = (w & 0x00030003u) | k.e25;
+  a.y = (w & 0x000C000Cu) | k.e23;
+  a.z = (w & 0x00300030u) | k.e21;
+  a.w = (w & 0x00C000C0u) | k.e19;
+  b.x = (w & 0x03000300u) | k.e17;
+  b.y = (v & 0x00030003u) | k.e25;
+  b.z = (v & 0x000C000Cu) | k.e23;
+  b.w = (v & 0x00300030u) | k.e21;
+}
+__device__ __forceinline__ void decode4_words(uint32_t w, u32x4& a, const DecodeConsts& k) {
+  const uint32_t v = w >> 8;
+  a.x = (w & 0x000F000Fu) | k.e25;
+  a.y = (w & 0x00F000F0u) | k.e21;
+  a.z = (v & 0x000F000Fu) | k.e25;
+  a.w = (v & 0x00F000F0u) | k.e21;
+}
+
+// Work: the rows of an item are cut into 64-row units of NIT = LRP
+// iterations; wave w of an item runs the item's iterations [w ipw, w ipw + ipw)
+// (whole units for large launches, a few iterations each for small ones),
+// storing, at the end of each unit it touches, the rows it covered.
+// PD: iterations of loads in flight ahead of use.  Loads are issued
+// unconditionally (iterations past the wave's last one re-read its last row),
+// so the register ring needs no copies and the compiler's waits stay PD deep.
+// NSV: SV dwords per lane (rank <= 2 NSV LRP); HASB: a bias is added.
+template <int BITS, bool SYM, int LRP, int PD, int NSV, bool HASB>
+__global__ __launch_bounds__(256) void gemv_lane_kernel(LaneArgs la) {
+  constexpr int C = lane_piece_codes<BITS>();  // codes per lane
+  constexpr int RPI = 64 / LRP;                // rows per iteration
+  constexpr int NIT = LRP;                     // iterations per 64-row unit
+  static_assert(NIT % PD == 0, "ring depth must divide the unit");
+  const DenseArgs& a = la.a;
+  const DenseSrc src{a};
+  const int lane = threadIdx.x & 63;
+  const int wv = blockIdx.x * 4 + (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int item = wv / la.wpi;
+  if (item >= a.items) return;  // uniform over the wave
+  const int ib = (wv - item * la.wpi) * la.ipw;
+  const int ie = min(ib + la.ipw, la.its);
+  if (ib >= ie) return;
+  const int N = a.sh.N, G = a.sh.G, kw = a.sh.kw, rank = a.sh.rank;
+  const int ri = lane / LRP, p = lane % LRP;
+  const bool act = p < la.lr;
+  const int pc = act ? p : la.lr - 1;  // inactive lanes read a valid piece (x = 0)
+  const int g = pc * C / 128;          // the piece's quantization group
+
+  // ---- x slice in operand order, c1 = sum bias * x, c2 = sum x ----
+  uint32_t xw[C / 2];
+  float c1 = 0.f, c2 = 0.f;
+  {
+    const __half* xr = src.xrow(item, 0) + pc * C;
+#pragma unroll
+    for (int blk = 0; blk < C / 16; ++blk) {
+      const f16x8 in0 = *(const f16x8*)(xr + 16 * blk);
+      const f16x8 in1 = *(const f16x8*)(xr + 16 * blk + 8);
+      _Float16 in[16], o[16];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        in[c] = act ? in0[c] : (_Float16)0.f;
+        in[8 + c] = act ? in1[c] : (_Float16)0.f;
+      }
+#pragma unroll
+      for (int pos = 0; pos < 16; ++pos) {
+        o[pos] = in[perm_src<BITS>(pos)];
+        const float f = (float)o[pos];
+        c2 += f;
+        c1 += code_bias<BITS>(pos) * f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const f16x2 pr = {o[2 * j], o[2 * j + 1]};
+        xw[8 * blk + j] = __builtin_bit_cast(uint32_t, pr);
+      }
+    }
+  }
+  // ---- a pairs of this lane's SV dwords (zero past the rank) ----
+  const bool lora = a.sv != nullptr && rank > 0;
+  uint32_t ap[NSV];
+  int svo[NSV];  // element offset of the dword within an SV row
+#pragma unroll
+  for (int k = 0; k < NSV; ++k) {
+    const int j = p + k * LRP;  // dword j holds rank columns 2j, 2j + 1
+    const bool v = lora && 2 * j < rank;
+    svo[k] = v ? 2 * j : 0;
+    f16x2 pr = {(_Float16)0.f, (_Float16)0.f};
+    if (v) {
+      pr[0] = (_Float16)__half2float(src.load_a(item, 0, 2 * j));
+      pr[1] = (_Float16)__half2float(src.load_a(item, 0, 2 * j + 1));
+    }
+    ap[k] = __builtin_bit_cast(uint32_t, pr);
+  }
+
+  const uint32_t* Cb = src.codes(item) + pc * 4;
+  const __half* Sb = src.scales(item) + g;
+  const __half* Zb = (SYM ? src.scales(item) : src.zeros(item)) + g;
+  // without a low-rank term the SV loads read x (finite, times a = 0)
+  const __half* SVb = lora ? src.sv(item) : src.xrow(item, 0);
+  const int svr = lora ? rank : 0;
+  const __half* Bb = HASB ? src.bias(item) : nullptr;
+  const float bsel = p == 0 ? 1.f : 0.f;  // the first lane of a row group adds the bias
+  auto row_of = [&](int i) {
+    i = min(i, ie - 1);
+    return min((i / NIT) * 64 + (i % NIT) * RPI + ri, N - 1);
+  };
+
+  u32x4 cw[PD];
+  uint32_t sw[PD], zw[PD], bw[PD], vw[PD][NSV];
+  auto issue = [&](int d, int i) {
+    const int n = row_of(i);
+    if constexpr (HASB) bw[d] = *(const uint16_t*)(Bb + n);
+    cw[d] = __builtin_nontemporal_load((const u32x4*)(Cb + (int64_t)n * kw));
+    sw[d] = *(const uint16_t*)(Sb + (int64_t)n * G);
+    if constexpr (!SYM) zw[d] = *(const uint16_t*)(Zb + (int64_t)n * G);
+#pragma unroll
+    for (int k = 0; k < NSV; ++k) vw[d][k] = *(const uint32_t*)(SVb + (int64_t)n * svr + svo[k]);
+  };
+  // The prologue's loads go out in the loop's order (scheduling barriers on
+  // both sides of every issue), so the wait the compiler places at the loop
+  // head -- the tighter of the two entry states -- stays PD - 1 iterations deep.
+#pragma unroll
+  for (int d = 0; d < PD; ++d) {
+    __builtin_amdgcn_sched_barrier(0);
+    issue(d, ib + d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  const DecodeConsts dk = DecodeConsts::make();
+  constexpr uint32_t xor_mask = SYM ? (BITS == 2 ? 0xAAAAAAAAu : 0x88888888u) : 0u;
+  float yv = 0.f;
+  for (int i0 = ib; i0 < ie; i0 += PD) {
+#pragma unroll
+    for (int d = 0; d < PD; ++d) {
+      const int i = i0 + d;
+      u32x4 w = cw[d];
+      if constexpr (SYM) w ^= xor_mask;
+      float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if constexpr (BITS == 2) {
+          u32x4 da, db;
+          decode2_words(w[k], da, db, dk);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc0 = dot2(da[j], xw[8 * k + j], acc0);
+            acc1 = dot2(db[j], xw[8 * k + 4 + j], acc1);
+          }
+        } else {
+          u32x4 da;
+          decode4_words(w[k], da, dk);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (j & 1) acc1 = dot2(da[j], xw[4 * k + j], acc1);
+            else acc0 = dot2(da[j], xw[4 * k + j], acc0);
+          }
+        }
+      }
+      const float s = __half2float(__ushort_as_half((uint16_t)sw[d]));
+      float z = (float)(1 << (BITS - 1));
+      if constexpr (!SYM) z = __half2float(__ushort_as_half((uint16_t)zw[d]));
+      float part = s * (((acc0 + acc1) - c1) - z * c2);
+      if constexpr (HASB) part = fmaf(bsel, __half2float(__ushort_as_half((uint16_t)bw[d])), part);
+#pragma unroll
+      for (int k = 0; k < NSV; ++k) part = dot2(vw[d][k], ap[k], part);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(d, i + PD);
+      __builtin_amdgcn_sched_barrier(0);
+      const float tot = lane_group_sum<LRP>(part);
+      yv = p == (i & (NIT - 1)) ? tot : yv;
+    }
+    const int iend = i0 + PD;
+    if ((iend & (NIT - 1)) == 0 || iend >= ie) {  // end of a unit or of the run (uniform)
+      // lane l holds row (l % LRP) * RPI + l / LRP of the unit; it stores if
+      // this wave ran that row's iteration
+      const int u = (iend - 1) / NIT;
+      const int lo = max(ib, u * NIT) - u * NIT, hi = min(ie, u * NIT + NIT) - u * NIT;
+      const int n = u * 64 + p * RPI + ri;
+      if (p >= lo && p < hi && n < N) src.store(item, 0, n, yv);
+    }
+  }
+}
+
+}  // namespace glq

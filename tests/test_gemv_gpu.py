@@ -284,6 +284,58 @@ def test_ksplit_fallback_path(gpu, monkeypatch, K, N, M, bits):
     assert_parity(y, oracle_y(p), f"k-split K={K} N={N} M={M}")
 
 
+@pytest.mark.parametrize("bits,K,N,rank,sym,ipw", [
+    (2, 2048, 1408, 64, False, None),   # config 0 shape: 32 lanes per row, 2 rows per step
+    (2, 1408, 1462, 40, False, 12),    # 22 of 32 lanes live, ragged N, rank 40; waves of 12
+                                       # iterations start and end inside 32-iteration units
+    (4, 2048, 2048, 64, True, 96),     # 64 lanes per row, symmetric codes, 1.5 units a wave
+    (4, 1408, 200, 128, False, None),  # 44 of 64 lanes live, rank 128 (an SV dword a lane)
+    (2, 2048, 320, 128, False, 20),    # rank 128 over 32-lane groups: 2 SV dwords per lane
+    (2, 512, 130, 16, True, 48),       # 4 rows per step (16-lane groups), run past N
+    (2, 4096, 448, 0, False, 8),       # 64 lanes per row at 2 bits, no low-rank term
+    (2, 1024, 640, 128, False, None),  # 16-lane groups with 4 SV dwords per lane
+])
+def test_lane_path_m1(gpu, monkeypatch, bits, K, N, rank, sym, ipw):
+    """The one-token-row kernel (glq_lane.h) on the shapes it takes: live and
+    idle lanes, 1/2/4 rows per step, 1/2/4 SV dwords per lane, bias,
+    symmetric codes, waves covering parts of units and several units
+    (GLQ_LANE_IPW), no LoRA; against the oracle and against the streaming
+    kernel forced on the same inputs."""
+    if ipw:
+        monkeypatch.setenv("GLQ_LANE_IPW", str(ipw))
+    p = fmt.make_linear(K, N, bits=bits, rank=max(rank, 8), M=1, seed=K + N + bits, sym=sym)
+    d = to(p, gpu)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(N)) * 0.1).half()
+    kw = dict(U=d["U"], SV=d["SV"]) if rank else {}
+    zeros = None if sym else d["zeros"]
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], zeros, bits, 128,
+                                       sym=sym, bias=bias.to(gpu), **kw)
+    assert_parity(y, oracle_y(p, lora=rank > 0, bias=bias), f"lane K={K} N={N}")
+    xu = (p.x.double() @ p.U.double()).half()
+    if rank:  # the precomputed a = x U hook
+        y2 = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], zeros, bits, 128,
+                                            sym=sym, SV=d["SV"], precomputed_xU=xu.to(gpu),
+                                            bias=bias.to(gpu))
+        assert_parity(y2, oracle_y(p, xu=xu, bias=bias), "lane precomputed xU")
+    monkeypatch.setenv("GLQ_GEMV_NO_LANE", "1")
+    ys = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], zeros, bits, 128,
+                                        sym=sym, bias=bias.to(gpu), **kw)
+    assert_parity(ys, oracle_y(p, lora=rank > 0, bias=bias), "stream kernel, same inputs")
+
+
+def test_lane_path_batched_items(gpu, monkeypatch):
+    """Many items of one token row in one launch, waves of 44 iterations (a
+    unit and 3/8 of the next)."""
+    monkeypatch.setenv("GLQ_LANE_IPW", "44")
+    E, K, N, r = 9, 2048, 1408, 64
+    ps = [fmt.make_linear(K, N, bits=2, rank=r, M=1, seed=300 + e) for e in range(E)]
+    st = lambda k: torch.stack([getattr(p, k) for p in ps]).to(gpu)  # noqa: E731
+    y = K_.packed_dequant_matmul_batched(st("x"), st("codes"), st("scales"), st("zeros"), 2,
+                                         128, U=st("U"), SV=st("SV"))
+    for e, p in enumerate(ps):
+        assert_parity(y[e], oracle_y(p), f"item {e}")
+
+
 @pytest.mark.parametrize("bits", [2, 4])
 def test_stream_bias_odd_tiles_sym(gpu, bits):
     """Streaming kernel with bias, a partial last 16-row tile (N = 16k + 6),
