@@ -347,15 +347,13 @@ static int launch_lane(const DenseArgs& a, int bits, hipStream_t s) {
   la.a = a;
   la.lr = a.sh.K * bits / 128;
   const int lrp = la.lr <= 16 ? 16 : la.lr <= 32 ? 32 : 64;
-  la.its = (a.sh.N + 63) / 64 * lrp;
-  // about kLaneWaves waves over the launch (whole units when the launch is
-  // large, a ring's worth of iterations at least)
-  const int64_t total = (int64_t)a.items * la.its;
-  int64_t ipw = (total + kLaneWaves - 1) / kLaneWaves;
-  if (const char* e = getenv("GLQ_LANE_IPW")) ipw = atoll(e) > 0 ? atoll(e) : ipw;
-  ipw = std::min<int64_t>(std::max<int64_t>(ipw, kLanePD), la.its);
-  la.ipw = (int)((ipw + kLanePD - 1) / kLanePD * kLanePD);
-  la.wpi = (la.its + la.ipw - 1) / la.ipw;
+  la.rounds = (a.sh.N + 63) / 64 * lrp / kLanePD;
+  // about kLaneWaves waves over the launch
+  const int64_t total = (int64_t)a.items * la.rounds;
+  int64_t rpw = (total + kLaneWaves - 1) / kLaneWaves;
+  if (const char* e = getenv("GLQ_LANE_RPW")) rpw = atoll(e) > 0 ? atoll(e) : rpw;
+  la.rpw = (int)std::min<int64_t>(std::max<int64_t>(rpw, 1), la.rounds);
+  la.wpi = (la.rounds + la.rpw - 1) / la.rpw;
   return bits == 2 ? launch_lane_bits<2>(la, s) : launch_lane_bits<4>(la, s);
 }
 

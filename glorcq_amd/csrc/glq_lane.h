@@ -74,12 +74,17 @@ __device__ __forceinline__ float lane_group_sum(float v) {
   return v;
 }
 
+// Buffer descriptor word 3 for gfx9-family raw buffers (offset-mode range
+// check against num_records), and the load's cache-policy bits: nontemporal.
+constexpr int kBufferFlags = 0x00020000;
+constexpr int kBufferNT = 2;
+
 struct LaneArgs {
   DenseArgs a;
-  int its;  // iterations per item: 64-row units x LRP
-  int ipw;  // iterations per wave (a multiple of the ring depth)
-  int wpi;  // waves per item
-  int lr;   // 16-byte pieces per code row
+  int rounds;  // rounds of PD iterations per item (64-row units x LRP / PD)
+  int wpi;     // waves per item
+  int rpw;     // rounds per wave (consecutive rounds of one item)
+  int lr;      // 16-byte pieces per code row
 };
 
 // Decoded operands of one code word as packed fp16 pairs (decode2 / decode4).
@@ -104,9 +109,8 @@ __device__ __forceinline__ void decode4_words(uint32_t w, u32x4& a, const Decode
 }
 
 // Work: the rows of an item are cut into 64-row units of NIT = LRP
-// iterations; wave w of an item runs the item's iterations [w ipw, w ipw + ipw)
-// (whole units for large launches, a few iterations each for small ones),
-// storing, at the end of each unit it touches, the rows it covered.
+// iterations, taken in rounds of PD iterations; wave w of an item runs rounds
+// w rpw .. w rpw + rpw - 1 and stores each round's rows at the round's end.
 // PD: iterations of loads in flight ahead of use.  Loads are issued
 // unconditionally (iterations past the wave's last one re-read its last row),
 // so the register ring needs no copies and the compiler's waits stay PD deep.
@@ -123,9 +127,11 @@ __global__ __launch_bounds__(256) void gemv_lane_kernel(LaneArgs la) {
   const int wv = blockIdx.x * 4 + (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int item = wv / la.wpi;
   if (item >= a.items) return;  // uniform over the wave
-  const int ib = (wv - item * la.wpi) * la.ipw;
-  const int ie = min(ib + la.ipw, la.its);
-  if (ib >= ie) return;
+  // rounds rb .. rb + nr - 1 of PD iterations each, [PD R, PD R + PD)
+  const int rb = (wv - item * la.wpi) * la.rpw;
+  const int nr = min(la.rpw, la.rounds - rb);
+  if (nr <= 0) return;
+  const int rlast = rb + nr - 1;
   const int N = a.sh.N, G = a.sh.G, kw = a.sh.kw, rank = a.sh.rank;
   const int ri = lane / LRP, p = lane % LRP;
   const bool act = p < la.lr;
@@ -178,29 +184,43 @@ __global__ __launch_bounds__(256) void gemv_lane_kernel(LaneArgs la) {
     ap[k] = __builtin_bit_cast(uint32_t, pr);
   }
 
-  const uint32_t* Cb = src.codes(item) + pc * 4;
-  const __half* Sb = src.scales(item) + g;
-  const __half* Zb = (SYM ? src.scales(item) : src.zeros(item)) + g;
+  // Buffer loads: one descriptor per tensor of the item (sized to it, so rows
+  // past N read 0 and add 0); a lane's offset is its constant part plus the
+  // iteration's first row times the row pitch.  Row of iteration i:
+  // (i / NIT) * 64 + (i % NIT) * RPI + ri = RPI i + ri.
+  const int rowbytes = kw * 4;
+  const auto rc = __builtin_amdgcn_make_buffer_rsrc((void*)src.codes(item), 0, N * rowbytes,
+                                                    kBufferFlags);
+  const auto rsc = __builtin_amdgcn_make_buffer_rsrc((void*)src.scales(item), 0, N * G * 2,
+                                                     kBufferFlags);
+  const auto rz = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(SYM ? src.scales(item) : src.zeros(item)), 0, N * G * 2, kBufferFlags);
   // without a low-rank term the SV loads read x (finite, times a = 0)
-  const __half* SVb = lora ? src.sv(item) : src.xrow(item, 0);
+  const auto rsv = __builtin_amdgcn_make_buffer_rsrc(
+      lora ? (void*)src.sv(item) : (void*)src.xrow(item, 0), 0, lora ? N * rank * 2 : 4,
+      kBufferFlags);
+  const auto rbi = __builtin_amdgcn_make_buffer_rsrc(HASB ? (void*)src.bias(item) : nullptr, 0,
+                                                     HASB ? N * 2 : 0, kBufferFlags);
   const int svr = lora ? rank : 0;
-  const __half* Bb = HASB ? src.bias(item) : nullptr;
+  const int vc = ri * rowbytes + pc * 16, vs = (ri * G + g) * 2, vb = ri * 2;
+  int vsv[NSV];
+#pragma unroll
+  for (int k = 0; k < NSV; ++k) vsv[k] = (ri * svr + svo[k]) * 2;
   const float bsel = p == 0 ? 1.f : 0.f;  // the first lane of a row group adds the bias
-  auto row_of = [&](int i) {
-    i = min(i, ie - 1);
-    return min((i / NIT) * 64 + (i % NIT) * RPI + ri, N - 1);
-  };
 
   u32x4 cw[PD];
   uint32_t sw[PD], zw[PD], bw[PD], vw[PD][NSV];
-  auto issue = [&](int d, int i) {
-    const int n = row_of(i);
-    if constexpr (HASB) bw[d] = *(const uint16_t*)(Bb + n);
-    cw[d] = __builtin_nontemporal_load((const u32x4*)(Cb + (int64_t)n * kw));
-    sw[d] = *(const uint16_t*)(Sb + (int64_t)n * G);
-    if constexpr (!SYM) zw[d] = *(const uint16_t*)(Zb + (int64_t)n * G);
+  // loads of iteration d of the wave's round r (rounds past the last re-read it)
+  auto issue = [&](int d, int r) {
+    const int n0 = RPI * (min(rb + r, rlast) * PD + d);  // uniform
+    if constexpr (HASB) bw[d] = __builtin_amdgcn_raw_buffer_load_b16(rbi, vb + n0 * 2, 0, 0);
+    cw[d] = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, vc + n0 * rowbytes, 0, kBufferNT));
+    sw[d] = __builtin_amdgcn_raw_buffer_load_b16(rsc, vs + n0 * G * 2, 0, 0);
+    if constexpr (!SYM) zw[d] = __builtin_amdgcn_raw_buffer_load_b16(rz, vs + n0 * G * 2, 0, 0);
 #pragma unroll
-    for (int k = 0; k < NSV; ++k) vw[d][k] = *(const uint32_t*)(SVb + (int64_t)n * svr + svo[k]);
+    for (int k = 0; k < NSV; ++k)
+      vw[d][k] = __builtin_amdgcn_raw_buffer_load_b32(rsv, vsv[k] + n0 * svr * 2, 0, 0);
   };
   // The prologue's loads go out in the loop's order (scheduling barriers on
   // both sides of every issue), so the wait the compiler places at the loop
@@ -208,20 +228,21 @@ __global__ __launch_bounds__(256) void gemv_lane_kernel(LaneArgs la) {
 #pragma unroll
   for (int d = 0; d < PD; ++d) {
     __builtin_amdgcn_sched_barrier(0);
-    issue(d, ib + d);
+    issue(d, 0);
     __builtin_amdgcn_sched_barrier(0);
   }
 
   const DecodeConsts dk = DecodeConsts::make();
   constexpr uint32_t xor_mask = SYM ? (BITS == 2 ? 0xAAAAAAAAu : 0x88888888u) : 0u;
-  float yv = 0.f;
-  for (int i0 = ib; i0 < ie; i0 += PD) {
+  for (int r = 0; r < nr; ++r) {
+    const int i0 = (rb + r) * PD;  // first iteration of the round
+    float yv = 0.f;
 #pragma unroll
     for (int d = 0; d < PD; ++d) {
       const int i = i0 + d;
       u32x4 w = cw[d];
       if constexpr (SYM) w ^= xor_mask;
-      float acc0 = 0.f, acc1 = 0.f;
+      float acc0 = -c1, acc1 = 0.f;  // the operand bias leaves with c1
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         if constexpr (BITS == 2) {
@@ -245,25 +266,21 @@ __global__ __launch_bounds__(256) void gemv_lane_kernel(LaneArgs la) {
       const float s = __half2float(__ushort_as_half((uint16_t)sw[d]));
       float z = (float)(1 << (BITS - 1));
       if constexpr (!SYM) z = __half2float(__ushort_as_half((uint16_t)zw[d]));
-      float part = s * (((acc0 + acc1) - c1) - z * c2);
+      float part = s * ((acc0 + acc1) - z * c2);
       if constexpr (HASB) part = fmaf(bsel, __half2float(__ushort_as_half((uint16_t)bw[d])), part);
 #pragma unroll
       for (int k = 0; k < NSV; ++k) part = dot2(vw[d][k], ap[k], part);
       __builtin_amdgcn_sched_barrier(0);
-      issue(d, i + PD);
+      issue(d, r + 1);
       __builtin_amdgcn_sched_barrier(0);
       const float tot = lane_group_sum<LRP>(part);
       yv = p == (i & (NIT - 1)) ? tot : yv;
     }
-    const int iend = i0 + PD;
-    if ((iend & (NIT - 1)) == 0 || iend >= ie) {  // end of a unit or of the run (uniform)
-      // lane l holds row (l % LRP) * RPI + l / LRP of the unit; it stores if
-      // this wave ran that row's iteration
-      const int u = (iend - 1) / NIT;
-      const int lo = max(ib, u * NIT) - u * NIT, hi = min(ie, u * NIT + NIT) - u * NIT;
-      const int n = u * 64 + p * RPI + ri;
-      if (p >= lo && p < hi && n < N) src.store(item, 0, n, yv);
-    }
+    // lane l holds row (l % LRP) * RPI + l / LRP of the unit; the lanes of
+    // the round's PD iterations store
+    const int u = i0 / NIT, it0 = i0 & (NIT - 1);
+    const int n = u * 64 + p * RPI + ri;
+    if (p >= it0 && p < it0 + PD && n < N) src.store(item, 0, n, yv);
   }
 }
 

@@ -299,10 +299,10 @@ def test_lane_path_m1(gpu, monkeypatch, bits, K, N, rank, sym, ipw):
     """The one-token-row kernel (glq_lane.h) on the shapes it takes: live and
     idle lanes, 1/2/4 rows per step, 1/2/4 SV dwords per lane, bias,
     symmetric codes, waves covering parts of units and several units
-    (GLQ_LANE_IPW), no LoRA; against the oracle and against the streaming
+    (GLQ_LANE_RPW), no LoRA; against the oracle and against the streaming
     kernel forced on the same inputs."""
     if ipw:
-        monkeypatch.setenv("GLQ_LANE_IPW", str(ipw))
+        monkeypatch.setenv("GLQ_LANE_RPW", str(ipw // 4))
     p = fmt.make_linear(K, N, bits=bits, rank=max(rank, 8), M=1, seed=K + N + bits, sym=sym)
     d = to(p, gpu)
     bias = (torch.randn(N, generator=torch.Generator().manual_seed(N)) * 0.1).half()
@@ -326,7 +326,7 @@ def test_lane_path_m1(gpu, monkeypatch, bits, K, N, rank, sym, ipw):
 def test_lane_path_batched_items(gpu, monkeypatch):
     """Many items of one token row in one launch, waves of 44 iterations (a
     unit and 3/8 of the next)."""
-    monkeypatch.setenv("GLQ_LANE_IPW", "44")
+    monkeypatch.setenv("GLQ_LANE_RPW", "11")
     E, K, N, r = 9, 2048, 1408, 64
     ps = [fmt.make_linear(K, N, bits=2, rank=r, M=1, seed=300 + e) for e in range(E)]
     st = lambda k: torch.stack([getattr(p, k) for p in ps]).to(gpu)  # noqa: E731
