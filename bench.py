@@ -135,7 +135,7 @@ def cpu_baseline(gpu_y_config0, budget_s=12.0):
 def read_traffic():
     """HBM bytes per GEMV launch from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE scaled by a plain copy's reading), or None."""
-    path = os.path.join(ROOT, "profiles", "gemv_stream_pool512_traffic.json")
+    path = os.path.join(ROOT, "profiles", "gemv_lane_pool512_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -447,7 +447,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u2 codes -> f16 MFMA, f32 accumulate",
+        "dtype": "u2 codes -> f16 pairs (v_dot2_f32_f16), f32 accumulate",
         "data": "synthetic (seeded random codes, scales, zeros, LoRA factors, activations)",
         "config": {
             "workload": (f"config 1 expert gate/up projection: {args.pool} distinct 2-bit "
@@ -460,7 +460,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
-            "kernel": "glq::gemv_stream_dense_kernel<2,1,3,false,false>",
+            "kernel": "glq::gemv_lane_kernel<2,false,32,4,1,false>",
             "kernel_avg_us": round(k_ms * 1e3, 2),
             "algorithmic_bytes_per_launch": k_bytes,
         },

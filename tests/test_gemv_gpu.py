@@ -352,7 +352,9 @@ def test_stream_bias_odd_tiles_sym(gpu, bits):
 
 @pytest.mark.parametrize("E,M,K,r,shared_x", [(1, 1, 2048, 64, False), (5, 3, 1408, 64, False),
                                               (16, 4, 2048, 64, True), (3, 16, 5632, 128, False),
-                                              (2, 2, 256, 8, True)])
+                                              (2, 2, 256, 8, True), (7, 1, 1408, 8, False),
+                                              (3, 1, 1408, 16, True), (2, 1, 384, 128, False),
+                                              (3, 1, 2048, 40, False)])
 def test_lowrank_xu(gpu, E, M, K, r, shared_x):
     """a = fp16(x U) with fp32 accumulation (reference `x @ U`,
     inference/quantized_linear.py:344; cluster-shared form with one x,
