@@ -18,9 +18,11 @@ from test_gemv_gpu import assert_parity, oracle_y, to
 
 def test_gemm_workspace_sizes():
     lib = _lib.load()
-    assert lib.glq_gemm_workspace_bytes(512, 2048, 1408, 0) == 0
-    n = lib.glq_gemm_workspace_bytes(512, 2048, 1408, 64)
-    assert n >= 512 * 64 * 2 and n % 256 == 0
+    n0 = lib.glq_gemm_workspace_bytes(512, 2048, 1408, 0)  # split-K partial tiles only
+    n = lib.glq_gemm_workspace_bytes(512, 2048, 1408, 64)  # + the x U partials
+    assert n0 >= 512 * 1408 * 4 and n0 % 256 == 0
+    assert n >= n0 + 512 * 64 * 4 and n % 256 == 0
+    assert lib.glq_gemm_workspace_bytes(0, 2048, 1408, 64) == 0
     # argument errors come back before any launch
     rc = lib.glq_gemm_lora(None, 64, 2048, 64, None, 2, None, None, 64, 0, None, None, 0, None,
                            None, None, None, 0, None)
@@ -98,3 +100,44 @@ def test_gemm_matches_gemv_blocks(gpu):
     diff = (y.float() - blocks.float()).abs()
     assert float(diff.max()) <= 2e-3 + 1e-2 * float(blocks.float().abs().max())
     assert_parity(y, oracle_y(p), "GEMM M=64")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ks", [1, 3, 8])
+@pytest.mark.parametrize("K,N,M,bits,rank", [
+    (2048, 1408, 128, 2, 64),   # config 1 gate/up
+    (1408, 330, 70, 4, 128),    # 6 chunks, rank 128 (two rank tiles per wave in the x U jobs)
+    (1024, 200, 40, 2, 192),    # rank above the in-launch x U limit: low-rank launches
+])
+def test_split_k_variants(gpu, monkeypatch, ks, K, N, M, bits, rank):
+    """K splits forced (GLQ_GEMM_KS; capped at the chunk count): partial tiles
+    and x U partials summed by gemm_reduce_kernel, against the oracle."""
+    monkeypatch.setenv("GLQ_GEMM_KS", str(ks))
+    p = fmt.make_linear(K, N, bits=bits, group=128, rank=rank, M=M, seed=K + N + ks)
+    d = to(p, gpu)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(ks)) * 0.1).half()
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], bits, 128,
+                                       U=d["U"], SV=d["SV"], bias=bias.to(gpu))
+    assert_parity(y, oracle_y(p, bias=bias), f"ks={ks} K={K} N={N} M={M}")
+    y2 = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], bits, 128,
+                                        U=d["U"], SV=d["SV"], bias=bias.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)  # fixed summation order: the same bits every call
+
+
+@pytest.mark.gpu
+def test_no_workspace_single_split(gpu):
+    """Without a workspace (a = x U given) the launch is one split with the
+    epilogue in the tile workgroups; same result within the bar."""
+    lib = _lib.load()
+    p = fmt.make_linear(2048, 320, bits=2, rank=64, M=80, seed=51)
+    d = to(p, gpu)
+    xu = (p.x.float() @ p.U.float()).half().to(gpu)
+    y = torch.empty(80, 320, dtype=torch.float16, device=gpu)
+    rc = lib.glq_gemm_lora(d["x"].data_ptr(), 80, 2048, 320, d["codes"].data_ptr(), 2,
+                           d["scales"].data_ptr(), d["zeros"].data_ptr(), 128, 0, None,
+                           d["SV"].data_ptr(), 64, xu.data_ptr(), None, y.data_ptr(), None, 0,
+                           _lib.stream_handle(gpu))
+    _lib.check(rc, "glq_gemm_lora")
+    torch.cuda.synchronize()
+    assert_parity(y, oracle_y(p, xu=xu.cpu()), "one split, no workspace")
