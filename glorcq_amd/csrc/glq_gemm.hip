@@ -356,11 +356,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_dq2_kernel(GemmArgs g, c
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int SLOT = g2_slot<NW>();
   const int m0 = blockIdx.y * kGemmBM;
-  const int job = blockIdx.x;
-  if (job >= g.ntn * g.ks) {  // uniform over the workgroup
-    gemm_xu_job<NW>(g, m0, job - g.ntn * g.ks, smem);
+  // the x U jobs (the longer ones) take the first workgroup ids of each token
+  // tile, so they start first and overlap the weight tiles
+  const int nxu = g.apart ? g.ks : 0;
+  if ((int)blockIdx.x < nxu) {  // uniform over the workgroup
+    gemm_xu_job<NW>(g, m0, blockIdx.x, smem);
     return;
   }
+  const int job = blockIdx.x - nxu;
   const int tn = job % g.ntn, sp = job / g.ntn;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
