@@ -93,6 +93,23 @@ SIGNATURES = {
     "glq_unpack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _c_int, _vp, _vp]),
     "glq_dequant_weight": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp, _i64, _c_int, _vp, _vp]),
     "glq_pack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp]),
+    "glq_rmsnorm": (_c_int, [_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp, _vp, _vp]),
+    "glq_qk_norm_rope": (_c_int, [
+        _vp, _vp, _vp, _i64,            # q, k, v, tokens
+        _i64, _i64, _i64,               # q_heads, kv_heads, head_dim
+        _i64, _i64,                     # q_stride, kv_stride
+        _vp, _vp, ctypes.c_float,       # q_norm_w, k_norm_w, eps
+        _vp, _vp, _i64,                 # cos, sin, cs_stride
+        _vp, _vp, _vp, _i64,            # q_out, k_cache, v_cache, max_len
+        _vp, _vp, _vp,                  # pos, len_out, stream
+    ]),
+    "glq_decode_attention_lds_bytes": (_i64, [_i64]),
+    "glq_decode_attention": (_c_int, [
+        _vp, _vp, _vp, _i64,            # q, k_cache, v_cache, tokens
+        _i64, _i64, _i64, _i64,         # q_heads, kv_heads, head_dim, max_len
+        _vp, ctypes.c_float, _vp,       # len, scale, advance
+        _vp, _vp,                       # out, stream
+    ]),
 }
 
 _lib = None

@@ -1,0 +1,354 @@
+// Decoder-layer pieces of the model-level decode step that sit around the
+// GLoRCQ projections and the MoE step: RMSNorm (optionally fused with the
+// residual add before it), the per-head q/k RMSNorm + rotary embedding +
+// static-KV-cache write of one decode token, and single-query grouped-query
+// attention over the static cache.  Each replaces a chain of 5-10 small
+// framework kernels per use with one launch, with the framework's rounding
+// points kept (fp16 results where the framework rounds to fp16, fp32 inside).
+
+#include <hip/hip_fp16.h>
+
+#include "glq_internal.h"
+
+namespace glq {
+namespace {
+
+constexpr int kDecThreads = 256;
+constexpr int kHeadDim = 128;
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Sum (or max) over the 256 threads of a block; every thread gets the result.
+template <bool MAX>
+__device__ inline float block_reduce(float v, float* red) {
+  v = MAX ? wave_max(v) : wave_sum(v);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();  // red may still be read from a previous reduction
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  return MAX ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]))
+             : (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// fp16 x fp16 -> fp16 as the framework's elementwise ops compute it (fp32
+// product, one rounding).
+__device__ inline _Float16 hmul(_Float16 a, _Float16 b) { return (_Float16)((float)a * (float)b); }
+
+// ---------------------------------------------------------------------------
+// RMSNorm over rows of D fp16 values (Qwen3MoeRMSNorm.forward):
+//   y   = x (+ residual, fp16 add)            -> residual_out when fused
+//   out = fp16(w * fp16(y * rsqrt(mean(y^2) + eps)))
+// One block per row; each thread holds up to kNormIters 8-wide pieces.
+// ---------------------------------------------------------------------------
+constexpr int kNormIters = 4;  // D <= 256 * 8 * 4 = 8192
+
+__global__ __launch_bounds__(kDecThreads) void rmsnorm_kernel(
+    const __half* __restrict__ x, const __half* __restrict__ res, const __half* __restrict__ w,
+    __half* __restrict__ out, __half* __restrict__ res_out, int D, float eps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const f16x8* xr = (const f16x8*)(x + row * D);
+  const f16x8* rr = res ? (const f16x8*)(res + row * D) : nullptr;
+  f16x8 y[kNormIters];
+  float ss = 0.f;
+#pragma unroll
+  for (int it = 0; it < kNormIters; ++it) {
+    const int i = threadIdx.x + it * kDecThreads;  // 8-wide piece index
+    if (i * 8 < D) {
+      f16x8 v = xr[i];
+      if (rr) {
+        const f16x8 r = rr[i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (_Float16)((float)v[e] + (float)r[e]);
+        ((f16x8*)(res_out + row * D))[i] = v;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += (float)v[e] * (float)v[e];
+      y[it] = v;
+    }
+  }
+  const float total = block_reduce<false>(ss, red);
+  const float r = rsqrtf(total / (float)D + eps);
+  const f16x8* wr = (const f16x8*)w;
+#pragma unroll
+  for (int it = 0; it < kNormIters; ++it) {
+    const int i = threadIdx.x + it * kDecThreads;
+    if (i * 8 < D) {
+      const f16x8 wv = wr[i];
+      f16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = hmul(wv[e], (_Float16)((float)y[it][e] * r));
+      ((f16x8*)(out + row * D))[i] = o;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// One decode token per batch row: q/k head RMSNorm (weights qw / kw over the
+// 128 head dims), rotary embedding q' = q cos + rotate_half(q) sin with every
+// product and the sum rounded to fp16 (apply_rotary_pos_emb), k' and v
+// written to the static cache at position *pos; q' to q_out (B, Hq, 128).
+// One wave per head: heads [0, Hq) are q, [Hq, Hq + Hk) k, then Hk of v.
+// Lane l holds dims 2l, 2l + 1; rotate_half pairs lane l with lane l ^ 32.
+// ---------------------------------------------------------------------------
+struct QkArgs {
+  const __half *q, *k, *v;  // rows of q_stride / kv_stride values per token
+  int64_t q_stride, kv_stride;
+  const __half *qw, *kw;
+  const __half *cos, *sin;  // (B or 1, 128)
+  int64_t cs_stride;        // 0 when one row serves every token
+  __half* q_out;
+  __half *k_cache, *v_cache;  // (B, Hk, max_len, 128)
+  const int64_t* pos;         // write position (device)
+  int* len_out;               // *pos + 1, for the attention launch
+  int B, Hq, Hk, max_len;
+  float eps;
+};
+
+__global__ __launch_bounds__(kDecThreads) void qk_norm_rope_kernel(QkArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int head = blockIdx.x * (kDecThreads / 64) + (threadIdx.x >> 6);
+  const int b = blockIdx.y;
+  const int64_t p = *a.pos;
+  if (head == 0 && b == 0 && lane == 0) *a.len_out = (int)(p + 1);
+  if (head >= a.Hq + 2 * a.Hk) return;
+  const bool in_cache = p >= 0 && p < a.max_len;
+  const int kind = head < a.Hq ? 0 : (head < a.Hq + a.Hk ? 1 : 2);
+  const int h = kind == 0 ? head : (kind == 1 ? head - a.Hq : head - a.Hq - a.Hk);
+  const __half* src = kind == 0 ? a.q + b * a.q_stride
+                                : (kind == 1 ? a.k : a.v) + b * a.kv_stride;
+  const f16x2 x = ((const f16x2*)(src + h * kHeadDim))[lane];
+  const int64_t crow = (((int64_t)b * a.Hk + h) * a.max_len + (in_cache ? p : 0)) * kHeadDim;
+  if (kind == 2) {
+    if (in_cache) ((f16x2*)(a.v_cache + crow))[lane] = x;
+    return;
+  }
+  const float f0 = (float)x[0], f1 = (float)x[1];
+  const float r = rsqrtf(wave_sum(f0 * f0 + f1 * f1) / (float)kHeadDim + a.eps);
+  const f16x2 wv = ((const f16x2*)(kind == 0 ? a.qw : a.kw))[lane];
+  f16x2 n;
+  n[0] = hmul(wv[0], (_Float16)(f0 * r));
+  n[1] = hmul(wv[1], (_Float16)(f1 * r));
+  // partner dims (2l + 64 for l < 32, 2l - 64 otherwise)
+  const uint32_t nb = __builtin_bit_cast(uint32_t, n);
+  const uint32_t pb = (uint32_t)__shfl_xor((int)nb, 32);
+  f16x2 rot = __builtin_bit_cast(f16x2, pb);
+  if (lane < 32) rot = -rot;
+  const f16x2 c = ((const f16x2*)(a.cos + b * a.cs_stride))[lane];
+  const f16x2 s = ((const f16x2*)(a.sin + b * a.cs_stride))[lane];
+  f16x2 o;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) o[e] = (_Float16)((float)hmul(n[e], c[e]) + (float)hmul(rot[e], s[e]));
+  if (kind == 0)
+    ((f16x2*)(a.q_out + ((int64_t)b * a.Hq + h) * kHeadDim))[lane] = o;
+  else if (in_cache)
+    ((f16x2*)(a.k_cache + crow))[lane] = o;
+}
+
+// ---------------------------------------------------------------------------
+// Single-query attention for q head h of token b over cache positions
+// [0, L), L = *len (clamped to [1, max_len]), KV head h / (Hq / Hk):
+//   out = sum_p softmax_p(scale * q . k_p) v_p        (fp32, fp16 result)
+// Block (h, b): scores one position per thread (16-byte K loads, v_dot2 on
+// fp16 pairs) into LDS; block max / sum; then 16 lanes per position, 8 dims
+// per lane, 16 positions per block step; the 16 partial rows meet in LDS.
+// Block (0, 0) then advances *advance by one (the cache's fill counter).
+// ---------------------------------------------------------------------------
+struct AttnArgs {
+  const __half* q;  // (B, Hq, 128)
+  const __half *k_cache, *v_cache;
+  const int* len;
+  int64_t* advance;
+  __half* out;  // (B, Hq * 128)
+  int B, Hq, Hk, max_len;
+  float scale;
+};
+
+__global__ __launch_bounds__(kDecThreads) void decode_attention_kernel(AttnArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __half* qs = (__half*)smem;                // [128]
+  float* part = (float*)(smem + 2 * kHeadDim);  // [16][128] partial outputs
+  float* red = part + 16 * kHeadDim;           // [4]
+  float* sc = red + 4;                         // [max_len] scores, then weights
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int g = h / (a.Hq / a.Hk);
+  const int L = min(max(*a.len, 1), a.max_len);
+  const __half* qrow = a.q + ((int64_t)b * a.Hq + h) * kHeadDim;
+  if (tid < 16) ((f16x8*)qs)[tid] = ((const f16x8*)qrow)[tid];
+  __syncthreads();
+  f16x2 qv[64];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) qv[i] = ((const f16x2*)qs)[i];
+  const int64_t base = ((int64_t)b * a.Hk + g) * a.max_len * kHeadDim;
+  const __half* K = a.k_cache + base;
+  const __half* V = a.v_cache + base;
+  float mx = -__builtin_inff();
+  for (int p = tid; p < L; p += kDecThreads) {
+    const f16x8* kr = (const f16x8*)(K + (int64_t)p * kHeadDim);
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const f16x8 kv = kr[j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16x2 k2 = {kv[2 * e], kv[2 * e + 1]};
+        if (e & 1)
+          s1 = __builtin_amdgcn_fdot2(qv[4 * j + e], k2, s1, false);
+        else
+          s0 = __builtin_amdgcn_fdot2(qv[4 * j + e], k2, s0, false);
+      }
+    }
+    const float s = (s0 + s1) * a.scale;
+    sc[p] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = block_reduce<true>(mx, red);
+  float sum = 0.f;
+  for (int p = tid; p < L; p += kDecThreads) {
+    const float e = expf(sc[p] - mx);
+    sc[p] = e;
+    sum += e;
+  }
+  sum = block_reduce<false>(sum, red);  // its barrier also publishes sc
+  const int d8 = tid & 15, slot = tid >> 4;  // dims 8 d8.., position slot 0..15
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll 4
+  for (int p = slot; p < L; p += 16) {
+    const f16x8 vv = ((const f16x8*)(V + (int64_t)p * kHeadDim))[d8];
+    const float w = sc[p];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += w * (float)vv[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) part[slot * kHeadDim + 8 * d8 + e] = acc[e];
+  __syncthreads();
+  if (tid < kHeadDim) {
+    float o = 0.f;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) o += part[s * kHeadDim + tid];
+    a.out[(int64_t)b * a.Hq * kHeadDim + (int64_t)h * kHeadDim + tid] = __float2half(o / sum);
+  }
+  if (a.advance && h == 0 && b == 0 && tid == 0) *a.advance += 1;
+}
+
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+bool al4(const void* p) { return ((uintptr_t)p & 3) == 0; }
+
+}  // namespace
+}  // namespace glq
+
+extern "C" int glq_rmsnorm(const void* x, const void* residual, const void* weight, int64_t rows,
+                           int64_t dim, float eps, void* out, void* residual_out, void* stream) {
+  using namespace glq;
+  clear_error();
+  GLQ_CHECK(rows >= 0 && dim > 0, "rows must be >= 0 and dim > 0");
+  GLQ_CHECK(dim % 8 == 0 && dim <= kDecThreads * 8 * kNormIters,
+            "dim must be a multiple of 8 and <= %d (got %lld)", kDecThreads * 8 * kNormIters,
+            (long long)dim);
+  GLQ_CHECK(rows < (1ll << 31), "rows must be < 2^31");
+  if (rows == 0) return GLQ_OK;
+  GLQ_CHECK(x && weight && out && al16(x) && al16(weight) && al16(out),
+            "x, weight, out must be non-null and 16-byte aligned");
+  GLQ_CHECK(!residual || (residual_out && al16(residual) && al16(residual_out)),
+            "a residual needs a 16-byte aligned residual_out");
+  rmsnorm_kernel<<<dim3((unsigned)rows), dim3(kDecThreads), 0, (hipStream_t)stream>>>(
+      (const __half*)x, (const __half*)residual, (const __half*)weight, (__half*)out,
+      (__half*)residual_out, (int)dim, eps);
+  GLQ_LAUNCH_CHECK("rmsnorm_kernel");
+  return GLQ_OK;
+}
+
+extern "C" int glq_qk_norm_rope(const void* q, const void* k, const void* v, int64_t tokens,
+                                int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                int64_t q_stride, int64_t kv_stride, const void* q_norm_w,
+                                const void* k_norm_w, float eps, const void* cos, const void* sin,
+                                int64_t cs_stride, void* q_out, void* k_cache, void* v_cache,
+                                int64_t max_len, const int64_t* pos, int32_t* len_out,
+                                void* stream) {
+  using namespace glq;
+  clear_error();
+  GLQ_CHECK(head_dim == kHeadDim, "head_dim must be %d (got %lld)", kHeadDim,
+            (long long)head_dim);
+  GLQ_CHECK(tokens >= 0 && tokens <= 65535, "tokens must be in [0, 65535]");
+  GLQ_CHECK(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 && q_heads <= 1024,
+            "q_heads must be a positive multiple of kv_heads (<= 1024)");
+  GLQ_CHECK(max_len > 0 && max_len < (1ll << 31), "max_len must be in [1, 2^31)");
+  GLQ_CHECK(q_stride >= q_heads * head_dim && kv_stride >= kv_heads * head_dim &&
+                q_stride % 2 == 0 && kv_stride % 2 == 0 && cs_stride % 2 == 0 && cs_stride >= 0,
+            "row strides must cover the heads and be even");
+  if (tokens == 0) return GLQ_OK;
+  GLQ_CHECK(q && k && v && q_norm_w && k_norm_w && cos && sin && q_out && k_cache && v_cache &&
+                pos && len_out,
+            "null pointer argument");
+  GLQ_CHECK(al4(q) && al4(k) && al4(v) && al4(q_norm_w) && al4(k_norm_w) && al4(cos) &&
+                al4(sin) && al4(q_out) && al4(k_cache) && al4(v_cache) && al4(len_out) &&
+                ((uintptr_t)pos & 7) == 0,
+            "tensor arguments must be 4-byte aligned (pos 8-byte)");
+  QkArgs a;
+  a.q = (const __half*)q; a.k = (const __half*)k; a.v = (const __half*)v;
+  a.q_stride = q_stride; a.kv_stride = kv_stride;
+  a.qw = (const __half*)q_norm_w; a.kw = (const __half*)k_norm_w;
+  a.cos = (const __half*)cos; a.sin = (const __half*)sin; a.cs_stride = cs_stride;
+  a.q_out = (__half*)q_out; a.k_cache = (__half*)k_cache; a.v_cache = (__half*)v_cache;
+  a.pos = pos; a.len_out = len_out;
+  a.B = (int)tokens; a.Hq = (int)q_heads; a.Hk = (int)kv_heads; a.max_len = (int)max_len;
+  a.eps = eps;
+  const int heads = a.Hq + 2 * a.Hk, per = kDecThreads / 64;
+  qk_norm_rope_kernel<<<dim3((unsigned)((heads + per - 1) / per), (unsigned)tokens),
+                        dim3(kDecThreads), 0, (hipStream_t)stream>>>(a);
+  GLQ_LAUNCH_CHECK("qk_norm_rope_kernel");
+  return GLQ_OK;
+}
+
+extern "C" int64_t glq_decode_attention_lds_bytes(int64_t max_len) {
+  return (int64_t)4 * (16 * 128 + 4 + max_len) + 2 * 128;
+}
+
+extern "C" int glq_decode_attention(const void* q, const void* k_cache, const void* v_cache,
+                                    int64_t tokens, int64_t q_heads, int64_t kv_heads,
+                                    int64_t head_dim, int64_t max_len, const int32_t* len,
+                                    float scale, int64_t* advance, void* out, void* stream) {
+  using namespace glq;
+  clear_error();
+  static size_t attr = 64 * 1024;
+  GLQ_CHECK(head_dim == kHeadDim, "head_dim must be %d (got %lld)", kHeadDim,
+            (long long)head_dim);
+  GLQ_CHECK(tokens >= 0 && tokens <= 65535, "tokens must be in [0, 65535]");
+  GLQ_CHECK(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 && q_heads <= 65535,
+            "q_heads must be a positive multiple of kv_heads");
+  const int64_t lds = glq_decode_attention_lds_bytes(max_len);
+  GLQ_CHECK(max_len > 0 && lds <= 160 * 1024,
+            "max_len must be in [1, %lld] (the scores live in LDS)",
+            (long long)((160 * 1024 - 2 * 128) / 4 - 16 * 128 - 4));
+  if (tokens == 0) return GLQ_OK;
+  GLQ_CHECK(q && k_cache && v_cache && len && out, "null pointer argument");
+  GLQ_CHECK(al16(q) && al16(k_cache) && al16(v_cache) && al4(len) && al4(out) &&
+                (!advance || ((uintptr_t)advance & 7) == 0),
+            "q and the caches must be 16-byte aligned, len/out 4-byte, advance 8-byte");
+  AttnArgs a;
+  a.q = (const __half*)q; a.k_cache = (const __half*)k_cache; a.v_cache = (const __half*)v_cache;
+  a.len = len; a.advance = advance; a.out = (__half*)out;
+  a.B = (int)tokens; a.Hq = (int)q_heads; a.Hk = (int)kv_heads; a.max_len = (int)max_len;
+  a.scale = scale;
+  int rc = set_lds_limit(decode_attention_kernel, (size_t)lds, attr);
+  if (rc) return rc;
+  decode_attention_kernel<<<dim3((unsigned)q_heads, (unsigned)tokens), dim3(kDecThreads),
+                            (size_t)lds, (hipStream_t)stream>>>(a);
+  GLQ_LAUNCH_CHECK("decode_attention_kernel");
+  return GLQ_OK;
+}

@@ -332,11 +332,48 @@ __device__ void moe_route_tile(const MoeArgs& a, int id, unsigned char* smem) {
 // rank tiles w, w + 4 over the whole slice with v_mfma_f32_16x16x32_f16
 // (A = x rows, 16-byte LDS reads; B = 8 U values of one rank column), so the
 // sums need no cross-wave step and leave from registers.
-__device__ void moe_xu_job(const MoeArgs& a, int job, unsigned char* smem) {
+//
+// A job leaves at once when no expert's projection s uses cluster c (a
+// projection may have fewer clusters than C).  Gated (`gated`, the launch
+// after the router's), it also leaves unless some token picked an expert of
+// cluster c: the B rows of routing keys are staged in LDS (the same keys and
+// order as the top-k), and the thread of each (token, expert of c) ranks that
+// expert's key in its row by 16-byte LDS reads -- so a step reads only the
+// picked clusters' U slices.
+__device__ void moe_xu_job(const MoeArgs& a, int job, unsigned char* smem, bool gated) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, kb = lane >> 4;
   const int s = job / (a.C * a.sus), rem = job - s * a.C * a.sus;
   const int c = rem / a.sus, q = rem - c * a.sus;
+  {
+    int act = 0;
+    if (gated) {
+      uint32_t* keys = (uint32_t*)smem;  // [B][LS], reused below once all have voted
+      const int LS = moe_lg_stride(a.E), E4 = a.E & ~3;
+      const unsigned short* lg = (const unsigned short*)a.lgb;
+      for (int i = tid; i < a.B * a.E; i += kRouteThreads) {
+        const int t = i / a.E, e = i - t * a.E;
+        keys[t * LS + e] = moe_key(lg[i], e);
+      }
+      __syncthreads();
+      for (int i = tid; i < a.B * a.E; i += kRouteThreads) {
+        const int t = i / a.E, e = i - t * a.E;
+        if (a.clus[s][e] != c) continue;
+        const uint32_t* row = keys + t * LS;
+        const uint32_t ke = row[e];
+        int r = 0;
+        for (int j = 0; j < E4; j += 4) {
+          const uint4 v = *(const uint4*)(row + j);
+          r += (int)(v.x > ke) + (int)(v.y > ke) + (int)(v.z > ke) + (int)(v.w > ke);
+        }
+        for (int j = E4; j < a.E; ++j) r += (int)(row[j] > ke);
+        act |= (int)(r < a.topk);
+      }
+    } else {
+      for (int e = tid; e < a.E; e += kRouteThreads) act |= (int)(a.clus[s][e] == c);
+    }
+    if (!__syncthreads_or(act)) return;
+  }
   const int xr = a.xurows;
   const int k0 = q * xr, kl = min(xr, a.H - k0);  // kl is a multiple of 128
   const int ntt = (a.B + 15) / 16;                // token tiles
@@ -402,7 +439,14 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(MoeArgs a) {
   if ((int)blockIdx.x < a.nrb)
     moe_route_tile(a, blockIdx.x, smem);
   else
-    moe_xu_job(a, blockIdx.x - a.nrb, smem);
+    moe_xu_job(a, blockIdx.x - a.nrb, smem, false);
+}
+
+// The x U jobs in a launch of their own, after the router's, each gated on
+// its cluster being picked (steps whose clusters outnumber the picks).
+__global__ __launch_bounds__(kRouteThreads) void moe_xu_kernel(MoeArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  moe_xu_job(a, blockIdx.x, smem, true);
 }
 
 // ---------------------------------------------------------------------------
@@ -650,8 +694,9 @@ namespace {
 struct MoePlan {
   MoeArgs a;
   int64_t ws_need;
-  size_t lds_route, lds_gu, lds_d, lds_c;
-  int64_t grid_route, grid_gu, grid_d, grid_c;
+  size_t lds_route, lds_xu, lds_gu, lds_d, lds_c;
+  int64_t grid_route, grid_xu, grid_gu, grid_d, grid_c;
+  bool xu_gated;  // x U jobs in their own launch, gated on routing
   int64_t off_sel, off_lgb, off_wts, off_sg, off_xu, off_inter, off_adq, off_sinter, off_yb, off_sdp;
 };
 
@@ -812,12 +857,20 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
     const size_t xu = (size_t)align_up(B * (a.xurows + 8) * 2, 16) +
                       (size_t)a.xurows * (a.rank + 8) * 2;
     P.lds_route = std::max(router, lora ? xu : (size_t)0);
-    GLQ_CHECK(P.lds_route <= 160 * 1024,
+    // the gated jobs stage B rows of routing keys first
+    P.lds_xu = std::max(xu, (size_t)4 * B * moe_lg_stride((int)E));
+    GLQ_CHECK(std::max(P.lds_route, P.lds_xu) <= 160 * 1024,
               "hidden=%lld with %lld tokens exceeds the router's LDS budget", (long long)H,
               (long long)B);
   }
   // grids
-  P.grid_route = a.nrb + (lora ? 2 * a.C * a.sus : 0);
+  // x U jobs gated on routing (a launch of their own) when the clusters
+  // outnumber four times the (token, expert) picks, i.e. when most clusters
+  // of a step go unpicked; GLQ_MOE_XU_GATE=0/1 forces either form
+  P.xu_gated = lora && a.C > 4 * P_;
+  if (const char* g = getenv("GLQ_MOE_XU_GATE")) P.xu_gated = lora && atoi(g) != 0;
+  P.grid_route = a.nrb + (lora && !P.xu_gated ? 2 * a.C * a.sus : 0);
+  P.grid_xu = lora ? 2 * a.C * a.sus : 0;
   P.grid_gu = (int64_t)a.nbm * a.wgu + (SI > 0 ? (int64_t)a.nsb * a.wgsu : 0);
   P.grid_d = (int64_t)a.nbm * a.sr * a.wgd + (SI > 0 ? (int64_t)a.nsb * a.ss * a.wgsd : 0);
   P.grid_c = B * ((H + 255) / 256);
@@ -870,12 +923,18 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
 template <int BR, int BS>
 int moe_launch(MoePlan& P, hipStream_t s) {
   static size_t attr_gu = 64 * 1024, attr_d = 64 * 1024, attr_c = 64 * 1024;
-  static size_t attr_r = 64 * 1024;
+  static size_t attr_r = 64 * 1024, attr_x = 64 * 1024;
   const MoeArgs& a = P.a;
   int rc = set_lds_limit(moe_route_kernel, P.lds_route, attr_r);
   if (rc) return rc;
   moe_route_kernel<<<dim3((unsigned)P.grid_route), dim3(kRouteThreads), P.lds_route, s>>>(a);
   GLQ_LAUNCH_CHECK("moe_route_kernel");
+  if (P.xu_gated) {
+    rc = set_lds_limit(moe_xu_kernel, P.lds_xu, attr_x);
+    if (rc) return rc;
+    moe_xu_kernel<<<dim3((unsigned)P.grid_xu), dim3(kRouteThreads), P.lds_xu, s>>>(a);
+    GLQ_LAUNCH_CHECK("moe_xu_kernel");
+  }
   rc = set_lds_limit(moe_gate_up_kernel<BR, BS>, P.lds_gu, attr_gu);
   if (rc) return rc;
   moe_gate_up_kernel<BR, BS><<<dim3((unsigned)P.grid_gu), dim3(256), P.lds_gu, s>>>(a);

@@ -1,0 +1,133 @@
+"""Decoder layer of the model-level decode step on the MI355X kernels.
+
+The reference's model path runs everything around its quantized projections
+and MoE blocks as framework ops (its graph wrapper captures them as they are,
+inference/graph_wrapper.py:69-149).  For the Qwen3-MoE-shaped model that is
+~60 small kernels per layer per decode token (RMSNorm alone is 7), which at
+decode sizes cost more than the projections.  These modules replace them
+with one launch each, keeping the framework's fp16 rounding points:
+
+* `FusedRMSNorm` -- Qwen3MoeRMSNorm (glq_rmsnorm);
+* `GLoRCQQwen3Attention` -- Qwen3MoeAttention for one decode token against a
+  static cache: GLoRCQLinear q/k/v projections, then q/k head RMSNorm +
+  rotary embedding + cache write (glq_qk_norm_rope), single-query GQA
+  attention (glq_decode_attention), GLoRCQLinear o projection.  Prefill (more
+  than one token) and a cache that is not static or not yet allocated take
+  the wrapped module's own forward;
+* `GLoRCQQwen3DecoderLayer` -- Qwen3MoeDecoderLayer with the residual add
+  after attention fused into the post-attention RMSNorm.
+
+The cache semantics are those of transformers' StaticLayer: the token is
+written at the layer's `cumulative_length` (a device counter), attention
+covers positions [0, cumulative_length], and the counter then advances by
+one -- all on the device, so the step can be captured in a graph.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import kernels
+
+
+class FusedRMSNorm(nn.Module):
+    """Qwen3MoeRMSNorm in one launch (same weight parameter)."""
+
+    def __init__(self, norm):
+        super().__init__()
+        self.weight = norm.weight
+        self.variance_epsilon = norm.variance_epsilon
+
+    def forward(self, hidden_states):
+        return kernels.rmsnorm(hidden_states.contiguous(), self.weight, self.variance_epsilon)
+
+
+def _static_layer(past_key_values, idx, batch):
+    """The layer's StaticLayer when its buffers exist and match the batch."""
+    layers = getattr(past_key_values, "layers", None)
+    if layers is None or idx >= len(layers):
+        return None
+    lay = layers[idx]
+    cum = getattr(lay, "cumulative_length", None)
+    if not getattr(lay, "is_initialized", False) or not torch.is_tensor(cum):
+        return None
+    keys = getattr(lay, "keys", None)
+    if keys is None or keys.dim() != 4 or keys.shape[0] != batch or keys.dtype != torch.float16:
+        return None
+    return lay
+
+
+class GLoRCQQwen3Attention(nn.Module):
+    """Qwen3MoeAttention with a fused single-token decode path."""
+
+    def __init__(self, attn):
+        super().__init__()
+        self.inner = attn
+        self.layer_idx = attn.layer_idx
+        self.head_dim = attn.head_dim
+        self.scaling = attn.scaling
+        if attn.q_norm.variance_epsilon != attn.k_norm.variance_epsilon:
+            raise RuntimeError("q_norm and k_norm must share eps")
+        self._len = None  # device int32: positions the step attends to
+
+    def forward(self, hidden_states, position_embeddings, attention_mask, past_key_values=None,
+                **kwargs):
+        B, S, H = hidden_states.shape
+        lay = _static_layer(past_key_values, self.layer_idx, B) if S == 1 else None
+        if lay is None or self.head_dim != 128:
+            return self.inner(hidden_states, position_embeddings, attention_mask,
+                              past_key_values=past_key_values, **kwargs)
+        inner = self.inner
+        x = hidden_states.reshape(B, H)
+        q = inner.q_proj(x)
+        k = inner.k_proj(x)
+        v = inner.v_proj(x)
+        cos, sin = position_embeddings
+        if self._len is None or self._len.device != x.device:
+            self._len = torch.zeros(1, dtype=torch.int32, device=x.device)
+        qr = kernels.qk_norm_rope(q, k, v, inner.q_norm.weight, inner.k_norm.weight,
+                                  inner.q_norm.variance_epsilon, cos.contiguous(),
+                                  sin.contiguous(), lay.keys, lay.values, lay.cumulative_length,
+                                  self._len)
+        a = kernels.decode_attention(qr, lay.keys, lay.values, self._len, self.scaling,
+                                     advance=lay.cumulative_length)
+        return inner.o_proj(a).reshape(B, 1, -1), None
+
+
+class GLoRCQQwen3DecoderLayer(nn.Module):
+    """Qwen3MoeDecoderLayer: fused RMSNorms, the post-attention one taking the
+    residual add with it, the GLoRCQ attention above, the layer's MoE block."""
+
+    def __init__(self, layer):
+        super().__init__()
+        self.self_attn = GLoRCQQwen3Attention(layer.self_attn)
+        self.mlp = layer.mlp
+        self.input_layernorm = layer.input_layernorm
+        self.post_attention_layernorm = layer.post_attention_layernorm
+        self.hidden_size = layer.hidden_size
+
+    def forward(self, hidden_states, attention_mask=None, position_ids=None,
+                past_key_values=None, use_cache=False, position_embeddings=None, **kwargs):
+        ln1, ln2 = self.input_layernorm, self.post_attention_layernorm
+        x = hidden_states.contiguous()
+        h = kernels.rmsnorm(x, ln1.weight, ln1.variance_epsilon)
+        a, _ = self.self_attn(hidden_states=h, position_embeddings=position_embeddings,
+                              attention_mask=attention_mask, past_key_values=past_key_values,
+                              position_ids=position_ids, use_cache=use_cache, **kwargs)
+        h2, res = kernels.rmsnorm(a.contiguous(), ln2.weight, ln2.variance_epsilon, residual=x)
+        m = self.mlp(h2)
+        return res + m
+
+
+def fuse_decoder_layers(model):
+    """Swaps every decoder layer of a Qwen3-MoE causal LM for
+    GLoRCQQwen3DecoderLayer and the final norm for FusedRMSNorm (in place);
+    returns the model."""
+    inner = model.model
+    for i, layer in enumerate(inner.layers):
+        if not isinstance(layer, GLoRCQQwen3DecoderLayer):
+            inner.layers[i] = GLoRCQQwen3DecoderLayer(layer)
+    if not isinstance(inner.norm, FusedRMSNorm):
+        inner.norm = FusedRMSNorm(inner.norm)
+    return model

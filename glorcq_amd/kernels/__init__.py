@@ -509,3 +509,94 @@ __all__ = [
     "dequant_weight", "pack_codes_device", "pack_codes", "workspace", "lowrank_xu",
     "turbo_gemv", "rht", "turbo_dequant_matmul_fused", "turbo_dequant_grouped_gemv_fused",
 ]
+
+
+# ---------------------------------------------------------------------------
+# Decoder-layer pieces of the model-level decode step (no reference kernel
+# counterpart: they replace transformers' Qwen3-MoE RMSNorm, q/k norm, rotary
+# embedding, static-cache update and single-token attention, one launch each)
+# ---------------------------------------------------------------------------
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+            residual: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """Qwen3MoeRMSNorm.forward on the GPU: fp16(w * fp16(y * rsqrt(mean(y^2) +
+    eps))) over the last dim, y = x or, with `residual`, y = fp16(x + residual).
+    Returns out, or (out, y) when a residual is given."""
+    lib = _lib.load()
+    _require(x, "x", torch.float16)
+    _require(weight, "weight", torch.float16)
+    D = x.shape[-1]
+    if weight.shape != (D,):
+        raise RuntimeError(f"weight must be ({D},)")
+    rows = x.numel() // D if D else 0
+    if out is None:
+        out = torch.empty_like(x)
+    res_out = None
+    if residual is not None:
+        _require(residual, "residual", torch.float16)
+        if residual.shape != x.shape:
+            raise RuntimeError("residual must match x")
+        res_out = torch.empty_like(x)
+    _lib.check(lib.glq_rmsnorm(x.data_ptr(), _lib.ptr(residual), weight.data_ptr(), rows, D,
+                               float(eps), out.data_ptr(), _lib.ptr(res_out),
+                               _lib.stream_handle(x.device)), "glq_rmsnorm")
+    return out if residual is None else (out, res_out)
+
+
+def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_w: torch.Tensor,
+                 k_norm_w: torch.Tensor, eps: float, cos: torch.Tensor, sin: torch.Tensor,
+                 k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor,
+                 len_out: torch.Tensor, q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """One decode token per row: q (T, Hq*128), k and v (T, Hk*128) fp16 ->
+    q' (T, Hq, 128) returned; k' and v written into the static caches
+    (T, Hk, max_len, 128) at position pos (device int64 scalar); pos + 1 into
+    len_out (device int32) for decode_attention.  cos/sin: (T or 1, 128)."""
+    lib = _lib.load()
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w"),
+                 (cos, "cos"), (sin, "sin"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _require(t, n, torch.float16)
+    _require(pos, "pos", torch.int64)
+    _require(len_out, "len_out", torch.int32)
+    T, Hk, max_len, hd = k_cache.shape
+    if v_cache.shape != k_cache.shape:
+        raise RuntimeError("k_cache and v_cache differ in shape")
+    Hq = q.shape[-1] // hd
+    q2, k2, v2 = q.reshape(-1, q.shape[-1]), k.reshape(-1, k.shape[-1]), v.reshape(-1, v.shape[-1])
+    if q2.shape[0] != T or k2.shape != (T, Hk * hd) or v2.shape != (T, Hk * hd):
+        raise RuntimeError("q, k, v rows must match the cache's batch and heads")
+    c2, s2 = cos.reshape(-1, hd), sin.reshape(-1, hd)
+    if c2.shape[0] not in (1, T) or s2.shape != c2.shape:
+        raise RuntimeError("cos/sin must hold 1 or T rows of head_dim")
+    if q_out is None:
+        q_out = torch.empty(T, Hq, hd, dtype=torch.float16, device=q.device)
+    _lib.check(lib.glq_qk_norm_rope(
+        q2.data_ptr(), k2.data_ptr(), v2.data_ptr(), T, Hq, Hk, hd, q2.shape[1], k2.shape[1],
+        q_norm_w.data_ptr(), k_norm_w.data_ptr(), float(eps), c2.data_ptr(), s2.data_ptr(),
+        hd if c2.shape[0] > 1 else 0, q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        max_len, pos.data_ptr(), len_out.data_ptr(), _lib.stream_handle(q.device)),
+        "glq_qk_norm_rope")
+    return q_out
+
+
+def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     length: torch.Tensor, scale: float, advance: torch.Tensor | None = None,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Single-query GQA attention over cache positions [0, length): q (T, Hq,
+    128), caches (T, Hk, max_len, 128) -> (T, Hq*128) fp16.  `advance`
+    (device int64) is incremented by one after the launch's reads."""
+    lib = _lib.load()
+    for t, n in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _require(t, n, torch.float16)
+    _require(length, "length", torch.int32)
+    if advance is not None:
+        _require(advance, "advance", torch.int64)
+    T, Hk, max_len, hd = k_cache.shape
+    if v_cache.shape != k_cache.shape or q.shape[0] != T or q.shape[-1] != hd:
+        raise RuntimeError("q (T, Hq, 128) and caches (T, Hk, max_len, 128) must agree")
+    Hq = q.shape[1]
+    if out is None:
+        out = torch.empty(T, Hq * hd, dtype=torch.float16, device=q.device)
+    _lib.check(lib.glq_decode_attention(
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), T, Hq, Hk, hd, max_len,
+        length.data_ptr(), float(scale), _lib.ptr(advance), out.data_ptr(),
+        _lib.stream_handle(q.device)), "glq_decode_attention")
+    return out

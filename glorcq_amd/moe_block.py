@@ -102,6 +102,7 @@ class GraphCompatibleMoeBlock(nn.Module):
                         pool.append(lin.U)
                     cl.append(ids[key])
                 out[f"U_{proj}"] = _stack(pool)
+                out[f"urows_{proj}"] = len(pool)  # may be fewer than n_clusters
                 out[f"cluster_{proj}"] = torch.tensor(cl, dtype=torch.int32, device=dev)
                 out[f"ckeys_{proj}"] = list(ids.keys())  # local cluster -> key
                 out[f"SV_{proj}"] = _stack([lin.SV for lin in lins])

@@ -293,6 +293,64 @@ int glq_dequant_weight(const int32_t* codes, int64_t N, int64_t K, int bits,
 int glq_pack_codes(const int32_t* q, int64_t N, int64_t K, int bits,
                    int32_t* codes, void* stream);
 
+/*
+ * ---- Decoder-layer pieces of the model-level decode step ----
+ * The reference's model path runs these steps as framework (transformers)
+ * ops around its quantized projections (inference/graph_wrapper.py:69-149
+ * captures the whole step, model_builder.py:186-197 swaps only the MoE
+ * blocks); it has no kernels of its own for them, so these have no
+ * reference kernel counterpart.  They replace transformers' Qwen3-MoE
+ * modules (modeling_qwen3_moe: Qwen3MoeRMSNorm.forward, the decoder layer's
+ * residual adds, Qwen3MoeAttention.forward's q_norm / k_norm,
+ * apply_rotary_pos_emb, StaticLayer.update and the scaled-dot-product
+ * attention of one decode token), one launch each, with the framework's fp16
+ * rounding points kept.
+ */
+
+/*
+ * RMSNorm of `rows` rows of `dim` fp16 values (dim % 8 == 0, dim <= 8192):
+ *   y = x, or fp16(x + residual) when residual != NULL (then written to
+ *   residual_out); out = fp16(weight * fp16(y * rsqrt(mean(y^2) + eps))).
+ * x, residual, weight, out, residual_out 16-byte aligned; out may alias x.
+ */
+int glq_rmsnorm(const void* x, const void* residual, const void* weight, int64_t rows,
+                int64_t dim, float eps, void* out, void* residual_out, void* stream);
+
+/*
+ * One decode token per row (tokens rows): per-head RMSNorm of q (q_heads
+ * heads) and k (kv_heads heads) over head_dim = 128 with weights q_norm_w /
+ * k_norm_w, then the rotary embedding x' = fp16(fp16(x cos) +
+ * fp16(rotate_half(x) sin)) with cos/sin rows of 128 fp16 (cs_stride values
+ * apart; 0 = one row for all tokens).  q' goes to q_out (tokens, q_heads,
+ * 128); k' and v (unchanged) to the static caches (tokens, kv_heads, max_len,
+ * 128) at position *pos (device int64; out-of-range positions write
+ * nothing), and *pos + 1 to *len_out (device int32) for
+ * glq_decode_attention.  q, k, v rows are q_stride / kv_stride values apart.
+ */
+int glq_qk_norm_rope(const void* q, const void* k, const void* v, int64_t tokens,
+                     int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t q_stride,
+                     int64_t kv_stride, const void* q_norm_w, const void* k_norm_w, float eps,
+                     const void* cos, const void* sin, int64_t cs_stride, void* q_out,
+                     void* k_cache, void* v_cache, int64_t max_len, const int64_t* pos,
+                     int32_t* len_out, void* stream);
+
+/* Dynamic LDS bytes glq_decode_attention uses for a cache of max_len. */
+int64_t glq_decode_attention_lds_bytes(int64_t max_len);
+
+/*
+ * Single-query attention of one decode token per row over cache positions
+ * [0, L), L = *len clamped to [1, max_len] (device int32, written by
+ * glq_qk_norm_rope): for q head h, KV head h / (q_heads / kv_heads),
+ *   out[t][h*128 + d] = fp16(sum_p softmax_p(scale * q.k_p) v_p[d])
+ * with fp32 scores, softmax and sums.  q (tokens, q_heads, 128); caches as in
+ * glq_qk_norm_rope; out (tokens, q_heads * 128).  When advance != NULL,
+ * *advance (device int64, the cache's fill counter) is incremented by one.
+ */
+int glq_decode_attention(const void* q, const void* k_cache, const void* v_cache,
+                         int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                         int64_t max_len, const int32_t* len, float scale, int64_t* advance,
+                         void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -233,21 +233,29 @@ def route(h: torch.Tensor, router_w: torch.Tensor, top_k: int, norm_topk_prob: b
     return logits, w.half(), sel
 
 
-def _qmat_linear(x, q, e, exact, U=None, SV=None, a=None):
+def _qmat_linear(x, q, e, exact, U=None, SV=None, a=None, memo=None):
     """y = x @ W_e^T (+ a @ SV_e^T, a = fp16(x @ U) unless given) for expert e of
     a format.QMat.  exact=False: the reference's fp16 CPU fallback (fp16 dequant,
     fp16 matmuls, quantized_linear.py:286-355); exact=True: fp64 sums of the
-    exact weights s*(q - z), with a rounded to fp16 as the reference does."""
-    codes = q.codes[e].numpy()
-    qi = torch.from_numpy(unpack_codes(codes, q.bits, q.K))
+    exact weights s*(q - z), with a rounded to fp16 as the reference does.
+    memo (exact only): a dict that keeps each expert's exact weights across
+    calls, for callers whose weights do not change (multi-step decoding)."""
+    if exact and memo is not None and (id(q), e) in memo:
+        W = memo[(id(q), e)].double()
+    elif exact:
+        qi = torch.from_numpy(unpack_codes(q.codes[e].numpy(), q.bits, q.K))
+        W32 = dequant_fp32(qi, q.scales[e], q.zeros[e], q.group)  # exact in fp32
+        if memo is not None:
+            memo[(id(q), e)] = W32
+        W = W32.double()
     if exact:
-        W = dequant_fp32(qi, q.scales[e], q.zeros[e], q.group).double()
         y = x.double() @ W.T
         if SV is not None:
             if a is None:
                 a = (x.double() @ U.double()).half()
             y = y + a.double() @ SV.double().T
         return y
+    qi = torch.from_numpy(unpack_codes(q.codes[e].numpy(), q.bits, q.K))
     W = dequant_fp16(qi, q.scales[e], q.zeros[e], q.group)
     y = x.half() @ W.T
     if SV is not None:
@@ -258,7 +266,7 @@ def _qmat_linear(x, q, e, exact, U=None, SV=None, a=None):
 
 
 def moe_forward(p, exact: bool = True, h: torch.Tensor | None = None, dense: bool = False,
-                cluster_shared: bool = True):
+                cluster_shared: bool = True, memo: dict | None = None):
     """MoE block output (B, H) for format.MoEProblem p.
 
     Rounding points kept from the reference in both modes: routing weights,
@@ -271,7 +279,8 @@ def moe_forward(p, exact: bool = True, h: torch.Tensor | None = None, dense: boo
     dense=True evaluates every expert with weight 0 for the unselected ones (the
     graph-mode identity the reference relies on, moe_block.py:11-13).
     cluster_shared=False computes x @ U per expert instead of per cluster
-    (test_cluster_parallel.py:159 asserts the two agree)."""
+    (test_cluster_parallel.py:159 asserts the two agree).
+    memo: see _qmat_linear (routed experts, exact mode)."""
     h = p.h if h is None else h
     B, H = h.shape
     _, w, sel = route(h, p.router_w, p.top_k, p.norm_topk_prob, exact=exact)
@@ -296,7 +305,7 @@ def moe_forward(p, exact: bool = True, h: torch.Tensor | None = None, dense: boo
             c = int(p.cluster_of[proj][e])
             a = xu[(proj, c)][toks] if cluster_shared else None
             outs[proj] = _qmat_linear(x, p.experts[proj], e, exact, U=p.U[proj][c],
-                                      SV=p.SV[proj][e], a=a)
+                                      SV=p.SV[proj][e], a=a, memo=memo)
         g, u = outs["gate"], outs["up"]
         if exact:
             inter = (torch.nn.functional.silu(g.half().float()).half().double() *
@@ -305,7 +314,7 @@ def moe_forward(p, exact: bool = True, h: torch.Tensor | None = None, dense: boo
             inter = torch.nn.functional.silu(g.half()) * u.half()
         cd = int(p.cluster_of["down"][e])
         y = _qmat_linear(inter, p.experts["down"], e, exact, U=p.U["down"][cd],
-                         SV=p.SV["down"][e])
+                         SV=p.SV["down"][e], memo=memo)
         wt = torch.zeros(len(toks), dtype=torch.float16)
         for i, t in enumerate(toks):
             for k in range(p.top_k):

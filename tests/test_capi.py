@@ -87,6 +87,37 @@ def test_argument_checks_raise_before_any_launch(lib):
     assert lib.glq_unpack_codes(nul, 4, 63, 2, 0, nul, nul) == 1
 
 
+def test_decoder_entry_points_check_arguments(lib):
+    """The decoder-layer entry points reject bad shapes on the host; empty
+    work is a no-op."""
+    nul, p = None, 1 << 12
+    assert lib.glq_rmsnorm(p, nul, p, 4, 2050, 1e-6, p, nul, nul) == 1
+    assert b"multiple of 8" in lib.glq_last_error()
+    assert lib.glq_rmsnorm(p, nul, p, 4, 16384, 1e-6, p, nul, nul) == 1
+    assert lib.glq_rmsnorm(p + 2, nul, p, 4, 2048, 1e-6, p, nul, nul) == 1
+    assert b"aligned" in lib.glq_last_error()
+    assert lib.glq_rmsnorm(p, p, p, 4, 2048, 1e-6, p, nul, nul) == 1  # residual_out missing
+    assert lib.glq_rmsnorm(nul, nul, nul, 0, 2048, 1e-6, nul, nul, nul) == 0
+    args = [p, p, p, 1, 32, 4, 128, 4096, 512, p, p, 1e-6, p, p, 0, p, p, p, 640, p, p, nul]
+    bad = list(args); bad[6] = 64                       # head_dim
+    assert lib.glq_qk_norm_rope(*bad) == 1 and b"head_dim" in lib.glq_last_error()
+    bad = list(args); bad[5] = 5                        # 32 % 5
+    assert lib.glq_qk_norm_rope(*bad) == 1
+    bad = list(args); bad[7] = 2048                     # q_stride < heads * 128
+    assert lib.glq_qk_norm_rope(*bad) == 1
+    bad = list(args); bad[3] = 0
+    assert lib.glq_qk_norm_rope(*bad) == 0
+    n = lib.glq_decode_attention_lds_bytes(640)
+    assert n == 4 * (16 * 128 + 4 + 640) + 256
+    aargs = [p, p, p, 1, 32, 4, 128, 640, p, 0.088, nul, p, nul]
+    bad = list(aargs); bad[7] = 1 << 20                 # scores exceed LDS
+    assert lib.glq_decode_attention(*bad) == 1 and b"max_len" in lib.glq_last_error()
+    bad = list(aargs); bad[0] = p + 8                   # q not 16-byte aligned
+    assert lib.glq_decode_attention(*bad) == 1
+    bad = list(aargs); bad[3] = 0
+    assert lib.glq_decode_attention(*bad) == 0
+
+
 def test_python_boundary_rejects_cpu_tensors():
     import torch
 

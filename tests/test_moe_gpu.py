@@ -175,6 +175,28 @@ def test_variants(gpu, kw):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("B,seed", [(1, 3), (3, 6), (16, 7)])
+def test_config4_block_gated_xu(gpu, B, seed, monkeypatch):
+    """A Qwen3-30B-A3B-shaped block (128 experts, inter 768, top-8,
+    norm_topk_prob, no shared expert) with 100 clusters: at B = 1 and 3 the
+    clusters outnumber four times the picks, so the x U jobs run in their own
+    launch and skip unpicked clusters; at 16 they run beside the router.  LoRA
+    scaled x30 (a skipped active cluster fails the bar); the forced other form
+    gives the same bits."""
+    p = lora_heavy(fmt.make_moe(H=2048, E=128, inter=768, top_k=8, n_clusters=100, rank=64,
+                                shared_inter=0, norm_topk_prob=True, B=B, seed=seed))
+    assert margin(p) >= 2
+    blk, out, logits = run_block(p, gpu)
+    check_routing(p, logits)
+    ref = O.moe_forward(p)
+    assert bar(out, ref), float((out.double() - ref).abs().max())
+    monkeypatch.setenv("GLQ_MOE_XU_GATE", "0" if B < 4 else "1")
+    out2, _ = blk(p.h.reshape(1, p.B, p.H).to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(out2.reshape(p.B, p.H).cpu(), out)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("B", [17, 40])
 def test_skewed_routing_many_blocks(gpu, B):
     """Every token routes to expert 3 first: that expert's tokens span several
