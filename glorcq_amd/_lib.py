@@ -103,12 +103,12 @@ SIGNATURES = {
         _vp, _vp, _vp, _i64,            # q_out, k_cache, v_cache, max_len
         _vp, _vp, _vp,                  # pos, len_out, stream
     ]),
-    "glq_decode_attention_lds_bytes": (_i64, [_i64]),
+    "glq_decode_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "glq_decode_attention": (_c_int, [
         _vp, _vp, _vp, _i64,            # q, k_cache, v_cache, tokens
         _i64, _i64, _i64, _i64,         # q_heads, kv_heads, head_dim, max_len
         _vp, ctypes.c_float, _vp,       # len, scale, advance
-        _vp, _vp,                       # out, stream
+        _vp, _vp, _i64, _vp,            # out, workspace, bytes, stream
     ]),
 }
 

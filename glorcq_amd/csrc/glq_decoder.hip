@@ -159,91 +159,180 @@ __global__ __launch_bounds__(kDecThreads) void qk_norm_rope_kernel(QkArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Single-query attention for q head h of token b over cache positions
-// [0, L), L = *len (clamped to [1, max_len]), KV head h / (Hq / Hk):
+// Single-query attention of token b's q heads of KV group g over cache
+// positions [0, L), L = *len (clamped to [1, max_len]), split over blocks of
+// kAttnChunk positions (flash-decoding):
 //   out = sum_p softmax_p(scale * q . k_p) v_p        (fp32, fp16 result)
-// Block (h, b): scores one position per thread (16-byte K loads, v_dot2 on
-// fp16 pairs) into LDS; block max / sum; then 16 lanes per position, 8 dims
-// per lane, 16 positions per block step; the 16 partial rows meet in LDS.
-// Block (0, 0) then advances *advance by one (the cache's fill counter).
+// Block (split, g, b) stages its K and V rows and the group's rep <= 8 q rows
+// in LDS (every load in flight at once), scores (position, head) pairs with
+// v_dot2 on fp16 pairs, forms per-head max m, sum l and l-weighted V rows o,
+// and writes (m, l, o) to the workspace.  The last block of (b, g) to arrive
+// (an arrival counter, incremented after a device-scope fence) merges the
+// splits -- M = max m_s, out = sum o_s e^(m_s - M) / sum l_s e^(m_s - M) --
+// and zeroes the counter for the next call; the last block of (0, 0) also
+// advances *advance (the cache's fill counter) by one.
 // ---------------------------------------------------------------------------
+constexpr int kAttnChunk = 128;
+constexpr int kAttnMaxRep = 8;
+constexpr int kKStride = kHeadDim + 8;  // LDS row of K (halves), 16-byte aligned
+constexpr int kPartStride = kHeadDim + 4;  // m, l, 2 pad, o: rows 16-byte aligned
+
 struct AttnArgs {
   const __half* q;  // (B, Hq, 128)
   const __half *k_cache, *v_cache;
   const int* len;
   int64_t* advance;
-  __half* out;  // (B, Hq * 128)
-  int B, Hq, Hk, max_len;
+  __half* out;     // (B, Hq * 128)
+  float* part;     // [B][Hq][nsplit][kPartStride]: m, l, -, -, o[128]
+  unsigned* count; // [B][Hk], zero between calls
+  int B, Hq, Hk, max_len, nsplit;
   float scale;
 };
 
+constexpr size_t kAttnLds = 2 * kAttnMaxRep * kHeadDim          // q rows
+                            + 2 * kAttnChunk * kKStride          // K rows
+                            + 2 * kAttnChunk * kHeadDim          // V rows
+                            + 4 * kAttnMaxRep * kAttnChunk + 16;  // weights, flag
+
 __global__ __launch_bounds__(kDecThreads) void decode_attention_kernel(AttnArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __half* qs = (__half*)smem;                // [128]
-  float* part = (float*)(smem + 2 * kHeadDim);  // [16][128] partial outputs
-  float* red = part + 16 * kHeadDim;           // [4]
-  float* sc = red + 4;                         // [max_len] scores, then weights
-  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int g = h / (a.Hq / a.Hk);
+  __half* qs = (__half*)smem;
+  __half* ks = qs + kAttnMaxRep * kHeadDim;
+  __half* vs = ks + kAttnChunk * kKStride;
+  float* ps = (float*)(vs + kAttnChunk * kHeadDim);
+  int* flag = (int*)(ps + kAttnMaxRep * kAttnChunk);
+  const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int rep = a.Hq / a.Hk;
   const int L = min(max(*a.len, 1), a.max_len);
-  const __half* qrow = a.q + ((int64_t)b * a.Hq + h) * kHeadDim;
-  if (tid < 16) ((f16x8*)qs)[tid] = ((const f16x8*)qrow)[tid];
-  __syncthreads();
-  f16x2 qv[64];
+  const int c0 = split * kAttnChunk, n = max(0, min(kAttnChunk, L - c0));
+  const int64_t base = ((int64_t)b * a.Hk + g) * a.max_len * kHeadDim + (int64_t)c0 * kHeadDim;
+  // stage: 16-byte pieces, 16 per row; K and V rows [0, n), q rows [0, rep)
+  {
+    f16x8 kb[8], vb[8];
 #pragma unroll
-  for (int i = 0; i < 64; ++i) qv[i] = ((const f16x2*)qs)[i];
-  const int64_t base = ((int64_t)b * a.Hk + g) * a.max_len * kHeadDim;
-  const __half* K = a.k_cache + base;
-  const __half* V = a.v_cache + base;
-  float mx = -__builtin_inff();
-  for (int p = tid; p < L; p += kDecThreads) {
-    const f16x8* kr = (const f16x8*)(K + (int64_t)p * kHeadDim);
-    float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const f16x8 kv = kr[j];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const f16x2 k2 = {kv[2 * e], kv[2 * e + 1]};
-        if (e & 1)
-          s1 = __builtin_amdgcn_fdot2(qv[4 * j + e], k2, s1, false);
-        else
-          s0 = __builtin_amdgcn_fdot2(qv[4 * j + e], k2, s0, false);
+    for (int j = 0; j < 8; ++j) {
+      const int idx = j * kDecThreads + tid, r = idx >> 4;
+      if (r < n) {
+        kb[j] = ((const f16x8*)(a.k_cache + base))[idx];
+        vb[j] = ((const f16x8*)(a.v_cache + base))[idx];
       }
     }
-    const float s = (s0 + s1) * a.scale;
-    sc[p] = s;
-    mx = fmaxf(mx, s);
-  }
-  mx = block_reduce<true>(mx, red);
-  float sum = 0.f;
-  for (int p = tid; p < L; p += kDecThreads) {
-    const float e = expf(sc[p] - mx);
-    sc[p] = e;
-    sum += e;
-  }
-  sum = block_reduce<false>(sum, red);  // its barrier also publishes sc
-  const int d8 = tid & 15, slot = tid >> 4;  // dims 8 d8.., position slot 0..15
-  float acc[8];
+    if (tid < rep * 16)
+      ((f16x8*)qs)[tid] = ((const f16x8*)(a.q + ((int64_t)b * a.Hq + g * rep) * kHeadDim))[tid];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-#pragma unroll 4
-  for (int p = slot; p < L; p += 16) {
-    const f16x8 vv = ((const f16x8*)(V + (int64_t)p * kHeadDim))[d8];
-    const float w = sc[p];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += w * (float)vv[e];
+    for (int j = 0; j < 8; ++j) {
+      const int idx = j * kDecThreads + tid, r = idx >> 4, c = idx & 15;
+      if (r < n) {
+        *(f16x8*)(ks + r * kKStride + 8 * c) = kb[j];
+        ((f16x8*)vs)[idx] = vb[j];
+      }
+    }
   }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) part[slot * kHeadDim + 8 * d8 + e] = acc[e];
   __syncthreads();
-  if (tid < kHeadDim) {
-    float o = 0.f;
+  // scores: position p = tid & 127, heads h = tid >> 7, + 2, + 4, ...
+  {
+    const int p = tid & (kAttnChunk - 1);
+    for (int h = tid >> 7; h < rep; h += 2) {
+      float s = -__builtin_inff();
+      if (p < n) {
+        float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int s = 0; s < 16; ++s) o += part[s * kHeadDim + tid];
-    a.out[(int64_t)b * a.Hq * kHeadDim + (int64_t)h * kHeadDim + tid] = __float2half(o / sum);
+        for (int j = 0; j < 16; ++j) {
+          const f16x8 kv = *(const f16x8*)(ks + p * kKStride + 8 * j);
+          const f16x8 qv = *(const f16x8*)(qs + h * kHeadDim + 8 * j);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const f16x2 k2 = {kv[2 * e], kv[2 * e + 1]}, q2 = {qv[2 * e], qv[2 * e + 1]};
+            if (e & 1)
+              s1 = __builtin_amdgcn_fdot2(q2, k2, s1, false);
+            else
+              s0 = __builtin_amdgcn_fdot2(q2, k2, s0, false);
+          }
+        }
+        s = (s0 + s1) * a.scale;
+      }
+      ps[h * kAttnChunk + p] = s;
+    }
   }
-  if (a.advance && h == 0 && b == 0 && tid == 0) *a.advance += 1;
+  __syncthreads();
+  // per head (32 lanes each): chunk max and sum, weights in place
+  const int h = tid >> 5, l32 = tid & 31;
+  float m = -__builtin_inff(), l = 0.f;
+  if (h < rep) {
+    float* row = ps + h * kAttnChunk;
+#pragma unroll
+    for (int i = 0; i < kAttnChunk / 32; ++i) m = fmaxf(m, row[l32 + 32 * i]);
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (n > 0) {
+#pragma unroll
+      for (int i = 0; i < kAttnChunk / 32; ++i) {
+        const int p = l32 + 32 * i;
+        const float e = p < n ? expf(row[p] - m) : 0.f;
+        row[p] = e;
+        l += e;
+      }
+    }
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+  }
+  __syncthreads();
+  // o_h[4 l32 .. +4] = sum_p w[h][p] v[p][..]
+  float* my = a.part + (((int64_t)b * a.Hq + g * rep + h) * a.nsplit + split) * kPartStride;
+  if (h < rep) {
+    float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+    const float* row = ps + h * kAttnChunk;
+#pragma unroll 8
+    for (int p = 0; p < n; ++p) {
+      const float w = row[p];
+      const uint2 vv = *(const uint2*)(vs + p * kHeadDim + 4 * l32);
+      const f16x2 va = __builtin_bit_cast(f16x2, vv.x), vb2 = __builtin_bit_cast(f16x2, vv.y);
+      o0 += w * (float)va[0];
+      o1 += w * (float)va[1];
+      o2 += w * (float)vb2[0];
+      o3 += w * (float)vb2[1];
+    }
+    if (l32 == 0) {
+      my[0] = m;
+      my[1] = l;
+    }
+    *(float4*)(my + 4 + 4 * l32) = float4{o0, o1, o2, o3};
+  }
+  // arrival; the last block of (b, g) merges the splits
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) *flag = atomicAdd(a.count + b * a.Hk + g, 1u) == (unsigned)(a.nsplit - 1);
+  __syncthreads();
+  if (!*flag) return;
+  __threadfence();
+  if (h < rep) {
+    const volatile float* ph =
+        a.part + ((int64_t)b * a.Hq + g * rep + h) * a.nsplit * kPartStride;
+    float M = -__builtin_inff();
+    for (int s2 = 0; s2 < a.nsplit; ++s2) M = fmaxf(M, ph[s2 * kPartStride]);
+    float den = 0.f, r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
+    for (int s2 = 0; s2 < a.nsplit; ++s2) {
+      const volatile float* q = ph + s2 * kPartStride;
+      const float ms = q[0];
+      if (ms == -__builtin_inff()) continue;  // an empty split
+      const float f = expf(ms - M);
+      den += q[1] * f;
+      r0 += q[4 + 4 * l32] * f;
+      r1 += q[5 + 4 * l32] * f;
+      r2 += q[6 + 4 * l32] * f;
+      r3 += q[7 + 4 * l32] * f;
+    }
+    const float inv = 1.f / den;
+    f16x2 oa = {(_Float16)(r0 * inv), (_Float16)(r1 * inv)};
+    f16x2 ob = {(_Float16)(r2 * inv), (_Float16)(r3 * inv)};
+    __half* dst = a.out + (int64_t)b * a.Hq * kHeadDim + (int64_t)(g * rep + h) * kHeadDim;
+    *(uint2*)(dst + 4 * l32) =
+        uint2{__builtin_bit_cast(uint32_t, oa), __builtin_bit_cast(uint32_t, ob)};
+  }
+  if (tid == 0) {
+    a.count[b * a.Hk + g] = 0u;
+    if (a.advance && b == 0 && g == 0) *a.advance += 1;
+  }
 }
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -315,40 +404,54 @@ extern "C" int glq_qk_norm_rope(const void* q, const void* k, const void* v, int
   return GLQ_OK;
 }
 
-extern "C" int64_t glq_decode_attention_lds_bytes(int64_t max_len) {
-  return (int64_t)4 * (16 * 128 + 4 + max_len) + 2 * 128;
+extern "C" int64_t glq_decode_attention_workspace_bytes(int64_t tokens, int64_t q_heads,
+                                                      int64_t kv_heads, int64_t max_len) {
+  using namespace glq;
+  if (tokens < 0 || q_heads <= 0 || kv_heads <= 0 || max_len <= 0) return -1;
+  const int64_t nsplit = (max_len + kAttnChunk - 1) / kAttnChunk;
+  const int64_t part = align_up(4 * tokens * q_heads * nsplit * kPartStride, 256);
+  return part + align_up(4 * tokens * kv_heads, 256);
 }
 
 extern "C" int glq_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                                     int64_t tokens, int64_t q_heads, int64_t kv_heads,
                                     int64_t head_dim, int64_t max_len, const int32_t* len,
-                                    float scale, int64_t* advance, void* out, void* stream) {
+                                    float scale, int64_t* advance, void* out, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
   using namespace glq;
   clear_error();
   static size_t attr = 64 * 1024;
   GLQ_CHECK(head_dim == kHeadDim, "head_dim must be %d (got %lld)", kHeadDim,
             (long long)head_dim);
   GLQ_CHECK(tokens >= 0 && tokens <= 65535, "tokens must be in [0, 65535]");
-  GLQ_CHECK(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 && q_heads <= 65535,
-            "q_heads must be a positive multiple of kv_heads");
-  const int64_t lds = glq_decode_attention_lds_bytes(max_len);
-  GLQ_CHECK(max_len > 0 && lds <= 160 * 1024,
-            "max_len must be in [1, %lld] (the scores live in LDS)",
-            (long long)((160 * 1024 - 2 * 128) / 4 - 16 * 128 - 4));
+  GLQ_CHECK(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 &&
+                q_heads / kv_heads <= kAttnMaxRep && kv_heads <= 65535,
+            "q_heads must be a multiple of kv_heads with at most %d q heads per KV head",
+            kAttnMaxRep);
+  GLQ_CHECK(max_len > 0 && max_len <= (1ll << 24), "max_len must be in [1, 2^24]");
   if (tokens == 0) return GLQ_OK;
+  const int64_t need = glq_decode_attention_workspace_bytes(tokens, q_heads, kv_heads, max_len);
+  GLQ_CHECK(workspace && workspace_bytes >= need,
+            "workspace of %lld bytes needed (got %lld); its counters must start zero",
+            (long long)need, (long long)workspace_bytes);
   GLQ_CHECK(q && k_cache && v_cache && len && out, "null pointer argument");
-  GLQ_CHECK(al16(q) && al16(k_cache) && al16(v_cache) && al4(len) && al4(out) &&
-                (!advance || ((uintptr_t)advance & 7) == 0),
-            "q and the caches must be 16-byte aligned, len/out 4-byte, advance 8-byte");
+  GLQ_CHECK(al16(q) && al16(k_cache) && al16(v_cache) && al4(len) && al16(out) &&
+                ((uintptr_t)workspace & 255) == 0 && (!advance || ((uintptr_t)advance & 7) == 0),
+            "q, caches and out must be 16-byte aligned, len 4-byte, workspace 256-byte, "
+            "advance 8-byte");
   AttnArgs a;
   a.q = (const __half*)q; a.k_cache = (const __half*)k_cache; a.v_cache = (const __half*)v_cache;
   a.len = len; a.advance = advance; a.out = (__half*)out;
   a.B = (int)tokens; a.Hq = (int)q_heads; a.Hk = (int)kv_heads; a.max_len = (int)max_len;
+  a.nsplit = (int)((max_len + kAttnChunk - 1) / kAttnChunk);
   a.scale = scale;
-  int rc = set_lds_limit(decode_attention_kernel, (size_t)lds, attr);
+  a.part = (float*)workspace;
+  a.count = (unsigned*)((char*)workspace +
+                        align_up(4 * tokens * q_heads * (int64_t)a.nsplit * kPartStride, 256));
+  int rc = set_lds_limit(decode_attention_kernel, kAttnLds, attr);
   if (rc) return rc;
-  decode_attention_kernel<<<dim3((unsigned)q_heads, (unsigned)tokens), dim3(kDecThreads),
-                            (size_t)lds, (hipStream_t)stream>>>(a);
+  decode_attention_kernel<<<dim3((unsigned)a.nsplit, (unsigned)kv_heads, (unsigned)tokens),
+                            dim3(kDecThreads), kAttnLds, (hipStream_t)stream>>>(a);
   GLQ_LAUNCH_CHECK("decode_attention_kernel");
   return GLQ_OK;
 }

@@ -383,10 +383,25 @@ __device__ void moe_xu_job(const MoeArgs& a, int job, unsigned char* smem, bool 
   __half* ul = (__half*)(smem + align_up_dev(a.B * xstride * 2, 16));  // [xr][rank + 8]
   const int urow = min(max(a.uslot[s] ? a.uslot[s][c] : c, 0), a.urows[s] - 1);
   const __half* U = a.U[s] + (int64_t)urow * a.u_es[s] + (int64_t)k0 * a.rank;
-  const int r8 = a.rank / 8;
-  for (int idx = tid; idx < kl * r8; idx += kRouteThreads) {  // U slice, 16 B per load
-    const int k = idx / r8, j8 = idx - k * r8;
-    *(f16x8*)(ul + k * ustride + 8 * j8) = *(const f16x8*)(U + (int64_t)k * a.rank + 8 * j8);
+  const int r8 = a.rank / 8, nu = kl * r8;
+  for (int b0 = 0; b0 < nu; b0 += 8 * kRouteThreads) {  // U slice, 16 B per load,
+    f16x8 buf[8];                                        // 8 loads in flight per thread
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int idx = b0 + j * kRouteThreads + tid;
+      if (idx < nu) {
+        const int k = idx / r8, j8 = idx - k * r8;
+        buf[j] = *(const f16x8*)(U + (int64_t)k * a.rank + 8 * j8);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int idx = b0 + j * kRouteThreads + tid;
+      if (idx < nu) {
+        const int k = idx / r8, j8 = idx - k * r8;
+        *(f16x8*)(ul + k * ustride + 8 * j8) = buf[j];
+      }
+    }
   }
   for (int idx = tid; idx < a.B * (kl / 8); idx += kRouteThreads) {
     const int m = idx / (kl / 8), k8 = idx - m * (kl / 8);

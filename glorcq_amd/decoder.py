@@ -70,6 +70,8 @@ class GLoRCQQwen3Attention(nn.Module):
         if attn.q_norm.variance_epsilon != attn.k_norm.variance_epsilon:
             raise RuntimeError("q_norm and k_norm must share eps")
         self._len = None  # device int32: positions the step attends to
+        self._ws = None   # decode attention workspace (counters stay zero between calls)
+        self._ws_key = None
 
     def forward(self, hidden_states, position_embeddings, attention_mask, past_key_values=None,
                 **kwargs):
@@ -90,8 +92,11 @@ class GLoRCQQwen3Attention(nn.Module):
                                   inner.q_norm.variance_epsilon, cos.contiguous(),
                                   sin.contiguous(), lay.keys, lay.values, lay.cumulative_length,
                                   self._len)
+        if self._ws is None or self._ws_key != (tuple(lay.keys.shape), x.device):
+            self._ws = kernels.decode_attention_workspace(qr, lay.keys)
+            self._ws_key = (tuple(lay.keys.shape), x.device)
         a = kernels.decode_attention(qr, lay.keys, lay.values, self._len, self.scaling,
-                                     advance=lay.cumulative_length)
+                                     advance=lay.cumulative_length, workspace=self._ws)
         return inner.o_proj(a).reshape(B, 1, -1), None
 
 

@@ -577,12 +577,25 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_w: to
     return q_out
 
 
+def decode_attention_workspace(q: torch.Tensor, k_cache: torch.Tensor) -> torch.Tensor:
+    """A zeroed workspace for decode_attention at these shapes (keep it for
+    the calls that follow: every call leaves its counters zero)."""
+    lib = _lib.load()
+    T, Hk, max_len, _ = k_cache.shape
+    n = lib.glq_decode_attention_workspace_bytes(T, q.shape[1], Hk, max_len)
+    if n < 0:
+        raise RuntimeError("invalid decode attention shapes")
+    return torch.zeros(max(int(n), 256), dtype=torch.uint8, device=q.device)
+
+
 def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                      length: torch.Tensor, scale: float, advance: torch.Tensor | None = None,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
+                     out: torch.Tensor | None = None,
+                     workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Single-query GQA attention over cache positions [0, length): q (T, Hq,
     128), caches (T, Hk, max_len, 128) -> (T, Hq*128) fp16.  `advance`
-    (device int64) is incremented by one after the launch's reads."""
+    (device int64) is incremented by one after the launch's reads.
+    `workspace` from decode_attention_workspace (a fresh one when None)."""
     lib = _lib.load()
     for t, n in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache")):
         _require(t, n, torch.float16)
@@ -595,8 +608,11 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     Hq = q.shape[1]
     if out is None:
         out = torch.empty(T, Hq * hd, dtype=torch.float16, device=q.device)
+    if workspace is None:
+        workspace = decode_attention_workspace(q, k_cache)
     _lib.check(lib.glq_decode_attention(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), T, Hq, Hk, hd, max_len,
         length.data_ptr(), float(scale), _lib.ptr(advance), out.data_ptr(),
-        _lib.stream_handle(q.device)), "glq_decode_attention")
+        workspace.data_ptr(), workspace.numel(), _lib.stream_handle(q.device)),
+        "glq_decode_attention")
     return out

@@ -334,22 +334,31 @@ int glq_qk_norm_rope(const void* q, const void* k, const void* v, int64_t tokens
                      void* k_cache, void* v_cache, int64_t max_len, const int64_t* pos,
                      int32_t* len_out, void* stream);
 
-/* Dynamic LDS bytes glq_decode_attention uses for a cache of max_len. */
-int64_t glq_decode_attention_lds_bytes(int64_t max_len);
+/*
+ * Workspace bytes of glq_decode_attention (per-split partial results, then
+ * one arrival counter per (token, KV head)); -1 for invalid sizes.
+ */
+int64_t glq_decode_attention_workspace_bytes(int64_t tokens, int64_t q_heads,
+                                             int64_t kv_heads, int64_t max_len);
 
 /*
  * Single-query attention of one decode token per row over cache positions
  * [0, L), L = *len clamped to [1, max_len] (device int32, written by
- * glq_qk_norm_rope): for q head h, KV head h / (q_heads / kv_heads),
+ * glq_qk_norm_rope): for q head h, KV head h / (q_heads / kv_heads) (at most
+ * 8 q heads per KV head),
  *   out[t][h*128 + d] = fp16(sum_p softmax_p(scale * q.k_p) v_p[d])
- * with fp32 scores, softmax and sums.  q (tokens, q_heads, 128); caches as in
- * glq_qk_norm_rope; out (tokens, q_heads * 128).  When advance != NULL,
- * *advance (device int64, the cache's fill counter) is incremented by one.
+ * with fp32 scores, softmax and sums, split over 128-position blocks whose
+ * partial results the last-arriving block merges.  q (tokens, q_heads, 128);
+ * caches as in glq_qk_norm_rope; out (tokens, q_heads * 128).  workspace:
+ * glq_decode_attention_workspace_bytes, 256-byte aligned; its counters must
+ * be zero before the first call (each call leaves them zero), and calls that
+ * share a workspace must not overlap.  When advance != NULL, *advance (device
+ * int64, the cache's fill counter) is incremented by one.
  */
 int glq_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                          int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                          int64_t max_len, const int32_t* len, float scale, int64_t* advance,
-                         void* out, void* stream);
+                         void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

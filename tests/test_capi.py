@@ -107,11 +107,13 @@ def test_decoder_entry_points_check_arguments(lib):
     assert lib.glq_qk_norm_rope(*bad) == 1
     bad = list(args); bad[3] = 0
     assert lib.glq_qk_norm_rope(*bad) == 0
-    n = lib.glq_decode_attention_lds_bytes(640)
-    assert n == 4 * (16 * 128 + 4 + 640) + 256
-    aargs = [p, p, p, 1, 32, 4, 128, 640, p, 0.088, nul, p, nul]
-    bad = list(aargs); bad[7] = 1 << 20                 # scores exceed LDS
-    assert lib.glq_decode_attention(*bad) == 1 and b"max_len" in lib.glq_last_error()
+    n = lib.glq_decode_attention_workspace_bytes(2, 32, 4, 640)
+    assert n == 4 * 2 * 32 * 5 * 132 + 256  # (m, l, pad, o) per split, then the counters
+    aargs = [p, p, p, 2, 32, 4, 128, 640, p, 0.088, nul, p, 1 << 16, n, nul]
+    bad = list(aargs); bad[5] = 2                       # 16 q heads per KV head
+    assert lib.glq_decode_attention(*bad) == 1 and b"q heads" in lib.glq_last_error()
+    bad = list(aargs); bad[13] = n - 1                  # workspace too small
+    assert lib.glq_decode_attention(*bad) == 1 and b"workspace" in lib.glq_last_error()
     bad = list(aargs); bad[0] = p + 8                   # q not 16-byte aligned
     assert lib.glq_decode_attention(*bad) == 1
     bad = list(aargs); bad[3] = 0

@@ -130,7 +130,8 @@ def test_qk_norm_rope_out_of_range_position_writes_nothing(gpu):
 
 @pytest.mark.parametrize("B,Hq,Hk,L,maxlen", [(1, 32, 4, 1, 640), (1, 32, 4, 513, 640),
                                               (16, 32, 4, 600, 640), (2, 8, 8, 1000, 1024),
-                                              (3, 16, 2, 4096, 4096)])
+                                              (3, 16, 2, 4096, 4096), (1, 32, 4, 128, 130),
+                                              (2, 24, 4, 129, 129)])
 def test_decode_attention_matches_fp32(gpu, B, Hq, Hk, L, maxlen):
     hd = 128
     g = torch.Generator(device=gpu).manual_seed(L + B)
@@ -142,9 +143,12 @@ def test_decode_attention_matches_fp32(gpu, B, Hq, Hk, L, maxlen):
     ln = torch.tensor([L], dtype=torch.int32, device=gpu)
     adv = torch.tensor(L - 1, dtype=torch.int64, device=gpu)
     scale = hd ** -0.5
-    out = kernels.decode_attention(q, kc, vc, ln, scale, advance=adv)
+    ws = kernels.decode_attention_workspace(q, kc)
+    out = kernels.decode_attention(q, kc, vc, ln, scale, advance=adv, workspace=ws)
+    again = kernels.decode_attention(q, kc, vc, ln, scale, workspace=ws)  # counters reset
     torch.cuda.synchronize()
     assert int(adv) == L
+    assert torch.equal(out, again)
     rep = Hq // Hk
     K = kc[:, :, :L].float().repeat_interleave(rep, dim=1)
     V = vc[:, :, :L].float().repeat_interleave(rep, dim=1)
