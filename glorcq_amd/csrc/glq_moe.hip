@@ -66,7 +66,6 @@ struct MoeArgs {
   int bits, sbits;
   int tl_off;      // LDS byte offset of the routed block's token list (gate/up)
   int pl_off;      // LDS byte offset of the routed block's pair list (down)
-  int lg_off;      // LDS byte offset of the router logits copy (gate/up)
   StreamShape shGU, shSGU, shD, shSD;
   const __half* h;
   const __half* rw;
@@ -96,6 +95,11 @@ struct MoeArgs {
   __half* out;
   __half* logits;
   __half* lgb;     // [B][E] fp16 router logits (workspace)
+  // dispatch tables, built once per step by the router's last workgroup:
+  // [0] blocks, then bexp[nbm], bM[nbm], then kMoeTB pair ids per block
+  // (t * topk + k; slots past bM repeat the block's first pair)
+  int* tab;
+  unsigned* rcount;  // router workgroups arrived (zero between steps)
 };
 
 // ---------------------------------------------------------------------------
@@ -443,18 +447,72 @@ __device__ void moe_xu_job(const MoeArgs& a, int job, unsigned char* smem, bool 
   }
 }
 
+// Routing of every token and the dispatch tables, once per step, by the
+// router workgroup that finishes last (the logits of all tokens are then in
+// the workspace): routing keys staged in LDS, top-k ranks (ids and weights
+// published for the combine), expert-major pair lists cut into blocks, the
+// tables written to the workspace for the gate/up and down launches.
+__device__ void moe_route_finalize(const MoeArgs& a, unsigned char* smem) {
+  const int tid = threadIdx.x, nl = a.B * a.E, LS = moe_lg_stride(a.E), P = a.B * a.topk;
+  uint32_t* lgk = (uint32_t*)smem;
+  const MoeTables t =
+      moe_tables((int*)(smem + align_up_dev(4 * a.B * LS, 16)), P, a.E, a.nbm);
+  for (int i = tid; i < nl / 8; i += kRouteThreads) {  // 16-byte loads of the flat [B][E] array
+    const uint4 v = ((const uint4*)a.lgb)[i];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int f = 8 * i + u, tk = f / a.E, e = f - tk * a.E;
+      lgk[tk * LS + e] = moe_key(w[u >> 1] >> (16 * (u & 1)), e);
+    }
+  }
+  for (int f = nl / 8 * 8 + tid; f < nl; f += kRouteThreads) {
+    const int tk = f / a.E, e = f - tk * a.E;
+    lgk[tk * LS + e] = moe_key(__half_as_ushort(a.lgb[f]), e);
+  }
+  __syncthreads();
+  moe_topk_ranks(a, lgk, t.sel, true);
+  __syncthreads();
+  const int nblk = moe_dispatch(a, t, false);
+  int* g = a.tab;
+  if (tid == 0) g[0] = nblk;
+  for (int b = tid; b < a.nbm; b += kRouteThreads) {
+    const bool used = b < nblk;
+    g[1 + b] = used ? t.bexp[b] : 0;
+    g[1 + a.nbm + b] = used ? t.bM[b] : 0;
+  }
+  for (int i = tid; i < nblk * kMoeTB; i += kRouteThreads) {
+    const int b = i / kMoeTB, m = i - b * kMoeTB;
+    g[1 + 2 * a.nbm + i] = t.list[t.bfirst[b] + min(m, t.bM[b] - 1)];
+  }
+}
+
 __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(MoeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int last;
   if (a.rank > 0) {  // this step's a_down accumulators start at zero
     const int64_t nq = (int64_t)a.nbm * kMoeTB * a.rpad;
     for (int64_t i = (int64_t)blockIdx.x * kRouteThreads + threadIdx.x; i < nq;
          i += (int64_t)gridDim.x * kRouteThreads)
       a.adq[i] = 0ull;
   }
-  if ((int)blockIdx.x < a.nrb)
+  if ((int)blockIdx.x < a.nrb) {
     moe_route_tile(a, blockIdx.x, smem);
-  else
+    // arrival: the last router workgroup (after a device-scope fence on
+    // every thread's logit stores) builds the step's routing and tables and
+    // leaves the counter at zero for the next step
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) last = atomicAdd(a.rcount, 1u) == (unsigned)(a.nrb - 1);
+    __syncthreads();
+    if (last) {
+      __threadfence();
+      moe_route_finalize(a, smem);
+      if (threadIdx.x == 0) *a.rcount = 0u;
+    }
+  } else {
     moe_xu_job(a, blockIdx.x - a.nrb, smem, false);
+  }
 }
 
 // The x U jobs in a launch of their own, after the router's, each gated on
@@ -531,36 +589,16 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
       cl[u] = (a.rank > 0 && i < 3 * a.E) ? a.clus[i / a.E][i % a.E] : 0;
     }
     {
-      const MoeTables t = moe_tables((int*)smem, a.B * a.topk, a.E, a.nbm);
-      // routing of every token (workgroup 0 publishes it for the later launches):
-      // the logits reach LDS as routing keys (rows of moe_lg_stride(E)) in one pass
-      uint32_t* lgk = (uint32_t*)(smem + a.lg_off);
-      const int nl = a.B * a.E, LS = moe_lg_stride(a.E);
-      for (int i = tid; i < nl / 8; i += 256) {  // 16-byte loads of the flat [B][E] array
-        const uint4 v = ((const uint4*)a.lgb)[i];
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int f = 8 * i + u, tk = f / a.E, e = f - tk * a.E;
-          lgk[tk * LS + e] = moe_key(w[u >> 1] >> (16 * (u & 1)), e);
-        }
-      }
-      for (int f = nl / 8 * 8 + tid; f < nl; f += 256) {
-        const int tk = f / a.E, e = f - tk * a.E;
-        lgk[tk * LS + e] = moe_key(__half_as_ushort(a.lgb[f]), e);
-      }
-      __syncthreads();
-      moe_topk_ranks(a, lgk, t.sel, blockIdx.x == 0);
-      __syncthreads();
-      const int nblk = moe_dispatch(a, t, false);
+      // the block's expert and tokens from the step's dispatch tables (all
+      // four reads independent: one memory round trip)
+      const int* g = a.tab;
+      const int nblk = g[0], be = g[1 + b], bm = g[1 + a.nbm + b];
+      const int pr = g[1 + 2 * a.nbm + b * kMoeTB + (tid & (kMoeTB - 1))];
       if (b >= nblk) return;  // uniform over the workgroup
-      if (tid < kMoeTB) {
-        const int M = t.bM[b];
-        tok[tid] = tid < M ? t.list[t.bfirst[b] + tid] / a.topk : 0;
-      }
+      if (tid < kMoeTB) tok[tid] = tid < bm ? pr / a.topk : 0;
       if (tid == 0) {
-        tok[kMoeTB] = t.bexp[b];
-        tok[kMoeTB + 1] = t.bM[b];
+        tok[kMoeTB] = be;
+        tok[kMoeTB + 1] = bm;
       }
 #pragma unroll
       for (int u = 0; u < 3; ++u)
@@ -653,12 +691,13 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
     int e, M;
     int* pair = (int*)(smem + a.pl_off);  // past the stream layout and the tables
     {
-      const MoeTables t = moe_tables((int*)smem, a.B * a.topk, a.E, a.nbm);
-      const int nblk = moe_dispatch(a, t);
+      const int* g = a.tab;
+      const int nblk = g[0];
+      e = g[1 + b];
+      M = g[1 + a.nbm + b];
+      const int pr = g[1 + 2 * a.nbm + b * kMoeTB + (threadIdx.x & (kMoeTB - 1))];
       if (b >= nblk) return;
-      e = t.bexp[b];
-      M = t.bM[b];
-      if (threadIdx.x < kMoeTB) pair[threadIdx.x] = t.list[t.bfirst[b] + min((int)threadIdx.x, M - 1)];
+      if (threadIdx.x < kMoeTB) pair[threadIdx.x] = pr;
       __syncthreads();
     }
     const StreamShape sh = moe_part_shape(a.shD, a.I, a.kr, part, BR);
@@ -712,7 +751,7 @@ struct MoePlan {
   size_t lds_route, lds_xu, lds_gu, lds_d, lds_c;
   int64_t grid_route, grid_xu, grid_gu, grid_d, grid_c;
   bool xu_gated;  // x U jobs in their own launch, gated on routing
-  int64_t off_sel, off_lgb, off_wts, off_sg, off_xu, off_inter, off_adq, off_sinter, off_yb, off_sdp;
+  int64_t off_rcnt, off_tab, off_sel, off_lgb, off_wts, off_sg, off_xu, off_inter, off_adq, off_sinter, off_yb, off_sdp;
 };
 
 StreamShape moe_stream_shape(int K, int N, int bits, int rank, int mmax, int kpart) {
@@ -845,14 +884,12 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
   const StreamLds Lgu = stream_lds(kMoeDepth, stream_slot_bytes(a.bits), mr, (int)H, a.bits,
                                    a.shGU.xstride, a.shGU.apad, 2, pcols);
   // the block's token list sits past the stream layout (with its K-split
-  // partial tiles) and the tables
-  a.tl_off = (int)align_up(std::max(Lgu.total + stream_ks_bytes(2), tbl), 16);
+  // partial tiles)
+  a.tl_off = (int)align_up(Lgu.total + stream_ks_bytes(2), 16);
   size_t lgu = (size_t)a.tl_off + 16 * 4 + 3 * 4 * (size_t)E;
-  a.lg_off = (int)align_up(lgu, 16);  // B rows of routing keys for the top-k
-  lgu = a.lg_off + align_up(4 * B * moe_lg_stride((int)E), 16);
   const StreamLds Ld = stream_lds(kMoeDepth, stream_slot_bytes(a.bits), mr, a.kr, a.bits,
                                   a.shD.xstride, a.shD.apad, 1, 0);
-  size_t ld = std::max<size_t>(Ld.total + stream_ks_bytes(1), tbl);
+  size_t ld = Ld.total + stream_ks_bytes(1);
   a.pl_off = (int)align_up(ld, 16);  // the routed block's pair list
   ld = a.pl_off + 16 * 4;
   if (SI > 0) {
@@ -872,6 +909,9 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
     const size_t xu = (size_t)align_up(B * (a.xurows + 8) * 2, 16) +
                       (size_t)a.xurows * (a.rank + 8) * 2;
     P.lds_route = std::max(router, lora ? xu : (size_t)0);
+    // the router's last workgroup stages B rows of routing keys and the tables
+    P.lds_route = std::max(P.lds_route, (size_t)align_up(4 * B * moe_lg_stride((int)E), 16) +
+                                            (size_t)tbl);
     // the gated jobs stage B rows of routing keys first
     P.lds_xu = std::max(xu, (size_t)4 * B * moe_lg_stride((int)E));
     GLQ_CHECK(std::max(P.lds_route, P.lds_xu) <= 160 * 1024,
@@ -896,6 +936,8 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
     o = align_up(o + bytes, 256);
     return at;
   };
+  P.off_rcnt = take(4);  // must be zero before the first step; every step leaves it zero
+  P.off_tab = take(4 * (1 + (2 + kMoeTB) * (int64_t)a.nbm));
   P.off_sel = take(4 * P_);
   P.off_lgb = take(2 * B * E);
   P.off_wts = take(2 * P_);
@@ -988,6 +1030,8 @@ extern "C" int glq_moe_decode(const glq_moe_params* p, void* workspace, int64_t 
   GLQ_CHECK(((uintptr_t)workspace & 255) == 0, "workspace must be 256-byte aligned");
   char* w = (char*)workspace;
   MoeArgs& a = P.a;
+  a.rcount = (unsigned*)(w + P.off_rcnt);
+  a.tab = (int*)(w + P.off_tab);
   a.sel = (int32_t*)(w + P.off_sel);
   a.lgb = (__half*)(w + P.off_lgb);
   a.wts = (__half*)(w + P.off_wts);

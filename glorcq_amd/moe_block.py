@@ -231,7 +231,9 @@ class GraphCompatibleMoeBlock(nn.Module):
             n = lib.glq_moe_workspace_bytes(ctypes.byref(P))
             if n < 0:
                 _lib.check(1, "glq_moe_workspace_bytes")
-            ws = torch.empty(max(int(n), 256), dtype=torch.uint8,
+            # zero-filled once: its router arrival counter starts at zero and
+            # every step leaves it zero
+            ws = torch.zeros(max(int(n), 256), dtype=torch.uint8,
                              device=self.t["router_w"].device)
             self._ws[B] = ws
         return ws

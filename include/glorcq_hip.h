@@ -261,7 +261,12 @@ typedef struct glq_moe_params {
 
 /* Workspace bytes glq_moe_decode needs for `p` (negative on a bad shape). */
 int64_t glq_moe_workspace_bytes(const glq_moe_params* p);
-/* Four launches on `stream`; the workspace needs no initialisation. */
+/*
+ * Four launches on `stream` (five when the x*U jobs are gated on routing).
+ * The workspace (256-byte aligned) must be zero-filled before its first use:
+ * its first word counts the router workgroups of a step, and every step
+ * leaves it zero again.  Steps that share a workspace must not overlap.
+ */
 int glq_moe_decode(const glq_moe_params* p, void* workspace, int64_t workspace_bytes,
                    void* stream);
 
