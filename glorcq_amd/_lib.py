@@ -33,7 +33,7 @@ class MoeParams(ctypes.Structure):
         ("U", _vp * 3), ("cluster_of", _vp * 3), ("SV", _vp * 3),
         ("shared_codes", _vp * 3), ("shared_scales", _vp * 3), ("shared_zeros", _vp * 3),
         ("out", _vp), ("router_logits", _vp),
-        ("u_slot", _vp * 2), ("u_rows", _i64 * 3),
+        ("u_slot", _vp * 2), ("u_rows", _i64 * 3), ("residual", _vp),
     ]
 
 

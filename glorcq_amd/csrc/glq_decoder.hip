@@ -306,21 +306,33 @@ __global__ __launch_bounds__(kDecThreads) void decode_attention_kernel(AttnArgs 
   if (!*flag) return;
   __threadfence();
   if (h < rep) {
-    const volatile float* ph =
-        a.part + ((int64_t)b * a.Hq + g * rep + h) * a.nsplit * kPartStride;
-    float M = -__builtin_inff();
-    for (int s2 = 0; s2 < a.nsplit; ++s2) M = fmaxf(M, ph[s2 * kPartStride]);
-    float den = 0.f, r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
-    for (int s2 = 0; s2 < a.nsplit; ++s2) {
-      const volatile float* q = ph + s2 * kPartStride;
-      const float ms = q[0];
-      if (ms == -__builtin_inff()) continue;  // an empty split
-      const float f = expf(ms - M);
-      den += q[1] * f;
-      r0 += q[4 + 4 * l32] * f;
-      r1 += q[5 + 4 * l32] * f;
-      r2 += q[6 + 4 * l32] * f;
-      r3 += q[7 + 4 * l32] * f;
+    // the fence above made the other blocks' partials visible (it invalidates
+    // this CU's cache): plain loads, up to 8 splits' worth in flight at once,
+    // merged online (running max M, sums rescaled when M grows)
+    const float* ph = a.part + ((int64_t)b * a.Hq + g * rep + h) * a.nsplit * kPartStride;
+    float M = -__builtin_inff(), den = 0.f, r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
+    for (int s0 = 0; s0 < a.nsplit; s0 += 8) {
+      float ms[8], ls[8];
+      float4 os[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int s2 = min(s0 + j, a.nsplit - 1);
+        ms[j] = ph[s2 * kPartStride];
+        ls[j] = ph[s2 * kPartStride + 1];
+        os[j] = *(const float4*)(ph + s2 * kPartStride + 4 + 4 * l32);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (s0 + j >= a.nsplit || ms[j] == -__builtin_inff()) continue;  // none / empty split
+        const float Mn = fmaxf(M, ms[j]);
+        const float fo = expf(M - Mn), fn = expf(ms[j] - Mn);  // M = -inf: fo = 0
+        den = den * fo + ls[j] * fn;
+        r0 = r0 * fo + os[j].x * fn;
+        r1 = r1 * fo + os[j].y * fn;
+        r2 = r2 * fo + os[j].z * fn;
+        r3 = r3 * fo + os[j].w * fn;
+        M = Mn;
+      }
     }
     const float inv = 1.f / den;
     f16x2 oa = {(_Float16)(r0 * inv), (_Float16)(r1 * inv)};

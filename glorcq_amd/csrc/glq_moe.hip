@@ -93,6 +93,7 @@ struct MoeArgs {
   float* yb;       // [sr][B * topk][H] routed down outputs per (token, k) pair (fp32)
   float* sdp;      // [ss][B][H] shared down partial outputs (fp32)
   __half* out;
+  const __half* res;  // added to out (fp16 + fp16), or nullptr
   __half* logits;
   __half* lgb;     // [B][E] fp16 router logits (workspace)
   // dispatch tables, built once per step by the router's last workgroup:
@@ -233,9 +234,9 @@ __host__ __device__ inline int moe_lg_stride(int E) { return ((E + 3) & ~3) + 4;
 // exp(l - max) / sum are monotonic in the logit (distinct fp16 logits give
 // distinct fp32 probabilities) this is the probability order -- and an expert
 // of rank j < topk lands in sel[t * topk + j]: one compare per pair, no
-// dependent passes.  Then (`publish`) one thread per token forms the softmax
-// sum in index order and the weights of the picks, and writes ids and fp16
-// weights to the workspace.
+// dependent passes.  Then (`publish`) one wave per token forms the softmax
+// sum (lanes over experts, then a cross-lane sum) and the weights of the
+// picks, and writes ids and fp16 weights to the workspace.
 __device__ void moe_topk_ranks(const MoeArgs& a, const uint32_t* lgk, int* sel, bool publish) {
   const int E = a.E, tid = threadIdx.x, LS = moe_lg_stride(E), E4 = E & ~3;
   for (int q = tid; q < a.B * E; q += 256) {
@@ -252,23 +253,26 @@ __device__ void moe_topk_ranks(const MoeArgs& a, const uint32_t* lgk, int* sel, 
     if (r < a.topk) sel[t * a.topk + r] = e;
   }
   __syncthreads();
-  const int t = tid;
-  if (!publish || t >= a.B) return;
-  const uint32_t* row = lgk + t * LS;
-  const float mx = moe_key_logit(row[sel[t * a.topk]]);
-  float sum = 0.f;
-#pragma unroll 8
-  for (int e = 0; e < E; ++e) sum += expf(moe_key_logit(row[e]) - mx);
-  float ws = 0.f;
-  if (a.norm)
-    for (int j = 0; j < a.topk; ++j)
-      ws += expf(moe_key_logit(row[sel[t * a.topk + j]]) - mx) / sum;
-  for (int j = 0; j < a.topk; ++j) {
-    const int e = sel[t * a.topk + j];
-    float w = expf(moe_key_logit(row[e]) - mx) / sum;
-    if (a.norm) w = w / ws;
-    a.sel[t * a.topk + j] = e;
-    a.wts[t * a.topk + j] = __float2half(w);
+  if (!publish) return;
+  const int lane = tid & 63;
+  for (int t = tid >> 6; t < a.B; t += 4) {
+    const uint32_t* row = lgk + t * LS;
+    const float mx = moe_key_logit(row[sel[t * a.topk]]);
+    float sum = 0.f;
+    for (int e = lane; e < E; e += 64) sum += expf(moe_key_logit(row[e]) - mx);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+    // lane j < topk: the j-th pick's probability; the renormalising sum
+    // over the picks (in pick order) when norm_topk_prob
+    const int e = lane < a.topk ? sel[t * a.topk + lane] : 0;
+    const float w = lane < a.topk ? expf(moe_key_logit(row[e]) - mx) / sum : 0.f;
+    float ws = 0.f;
+    if (a.norm)
+      for (int j = 0; j < a.topk; ++j) ws += __shfl(w, j);
+    if (lane < a.topk) {
+      a.sel[t * a.topk + lane] = e;
+      a.wts[t * a.topk + lane] = __float2half(a.norm ? w / ws : w);
+    }
   }
 }
 
@@ -737,7 +741,9 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a) {
     for (int part = 0; part < a.ss; ++part) s += a.sdp[((int64_t)part * a.B + t) * a.H + n];
     acc = fmaf(__half2float(a.sg[t]), __half2float(__float2half(s)), acc);
   }
-  a.out[(int64_t)t * a.H + n] = __float2half(acc);
+  float o = __half2float(__float2half(acc));
+  if (a.res) o += __half2float(a.res[(int64_t)t * a.H + n]);  // the layer's residual add
+  a.out[(int64_t)t * a.H + n] = __float2half(o);
 }
 
 // ---------------------------------------------------------------------------
@@ -853,7 +859,9 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
   a.sbits = SI > 0 ? p->shared_bits : 0;
   const int P_ = (int)(B * k);
   a.nbm = (int)std::min<int64_t>(E, P_) + P_ / kMoeTB;
-  a.xurows = (a.rank <= 64 && B <= 16) ? 512 : 256;
+  // U rows per x U job: gated steps (few picked clusters, many idle jobs)
+  // and larger batches take short slices, small ungated batches longer ones
+  a.xurows = (a.rank <= 64 && B <= 16 && !(lora && a.C > 4 * P_)) ? 512 : 256;
   a.sus = (int)((H + a.xurows - 1) / a.xurows);
   const int mr = (int)std::min<int64_t>(B, kMoeTB);  // staged rows per routed block
   // gate/up: K = H, N = I
@@ -973,6 +981,7 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
     a.szeros[s] = SI > 0 ? (const __half*)p->shared_zeros[s] : nullptr;
   }
   a.out = (__half*)p->out;
+  a.res = (const __half*)p->residual;
   a.logits = (__half*)p->router_logits;
   return GLQ_OK;
 }

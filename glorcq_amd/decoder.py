@@ -29,6 +29,7 @@ import torch
 import torch.nn as nn
 
 from . import kernels
+from .moe_block import GraphCompatibleMoeBlock
 
 
 class FusedRMSNorm(nn.Module):
@@ -69,6 +70,16 @@ class GLoRCQQwen3Attention(nn.Module):
         self.scaling = attn.scaling
         if attn.q_norm.variance_epsilon != attn.k_norm.variance_epsilon:
             raise RuntimeError("q_norm and k_norm must share eps")
+        # q/k/v share their input: their U factors side by side, so one
+        # launch forms all three x U products
+        self._U_qkv = None
+        lins = (attn.q_proj, attn.k_proj, attn.v_proj)
+        Us = [getattr(m, "U", None) for m in lins]
+        if all(u is not None and getattr(m, "quant_type", None) == "gptq" for u, m in zip(Us, lins)) \
+                and len({tuple(u.shape) for u in Us}) == 1 and Us[0].is_cuda:
+            self._U_qkv = torch.stack(Us).contiguous()
+            for i, m in enumerate(lins):
+                m.U = self._U_qkv[i]  # the same values, now views of the stack
         self._len = None  # device int32: positions the step attends to
         self._ws = None   # decode attention workspace (counters stay zero between calls)
         self._ws_key = None
@@ -82,9 +93,15 @@ class GLoRCQQwen3Attention(nn.Module):
                               past_key_values=past_key_values, **kwargs)
         inner = self.inner
         x = hidden_states.reshape(B, H)
-        q = inner.q_proj(x)
-        k = inner.k_proj(x)
-        v = inner.v_proj(x)
+        if self._U_qkv is not None and B <= kernels.GEMV_MAX_M:
+            xu = kernels.lowrank_xu(x.contiguous(), self._U_qkv)  # (3, B, r)
+            q = inner.q_proj(x, precomputed_xU=xu[0])
+            k = inner.k_proj(x, precomputed_xU=xu[1])
+            v = inner.v_proj(x, precomputed_xU=xu[2])
+        else:
+            q = inner.q_proj(x)
+            k = inner.k_proj(x)
+            v = inner.v_proj(x)
         cos, sin = position_embeddings
         if self._len is None or self._len.device != x.device:
             self._len = torch.zeros(1, dtype=torch.int32, device=x.device)
@@ -121,8 +138,10 @@ class GLoRCQQwen3DecoderLayer(nn.Module):
                               attention_mask=attention_mask, past_key_values=past_key_values,
                               position_ids=position_ids, use_cache=use_cache, **kwargs)
         h2, res = kernels.rmsnorm(a.contiguous(), ln2.weight, ln2.variance_epsilon, residual=x)
-        m = self.mlp(h2)
-        return res + m
+        if isinstance(self.mlp, GraphCompatibleMoeBlock):
+            y = self.mlp(h2, residual=res)  # the residual add inside the MoE step
+            return y[0] if isinstance(y, tuple) else y
+        return res + self.mlp(h2)
 
 
 def fuse_decoder_layers(model):

@@ -240,11 +240,14 @@ class GraphCompatibleMoeBlock(nn.Module):
 
     MAX_TOKENS = 64  # tokens per glq_moe_decode call
 
-    def forward(self, hidden_states: torch.Tensor):
+    def forward(self, hidden_states: torch.Tensor, residual: torch.Tensor | None = None):
         """(final (b, s, H) fp16, router_logits (b*s, E) fp16), as the
         reference's forward (moe_block.py:381-436); final alone when
         return_router_logits is False.  Tokens are independent in the block,
-        so more than 64 (a prefill) run as consecutive 64-token steps."""
+        so more than 64 (a prefill) run as consecutive 64-token steps.
+        residual (the shape of hidden_states, fp16): final becomes
+        fp16(residual + fp16(block output)), the decoder layer's residual add,
+        inside the step's last launch."""
         lib = _lib.load()
         shape = hidden_states.shape
         h = hidden_states.reshape(-1, self.hidden)
@@ -253,12 +256,18 @@ class GraphCompatibleMoeBlock(nn.Module):
         h = h.contiguous()
         if not h.is_cuda:
             raise RuntimeError("hidden_states must be on the GPU")
+        res = None
+        if residual is not None:
+            if residual.shape != hidden_states.shape or residual.dtype != torch.float16:
+                raise RuntimeError("residual must match hidden_states (fp16)")
+            res = residual.reshape(-1, self.hidden).contiguous()
         out = torch.empty_like(h)
         logits = torch.empty(h.shape[0], self.num_experts, dtype=torch.float16, device=h.device)
         stream = _lib.stream_handle(h.device)
         for t0 in range(0, h.shape[0], self.MAX_TOKENS):
             t1 = min(h.shape[0], t0 + self.MAX_TOKENS)
             P = self._params(h[t0:t1], out[t0:t1], logits[t0:t1])
+            P.residual = _lib.ptr(None if res is None else res[t0:t1])
             ws = self._workspace(lib, P)
             rc = lib.glq_moe_decode(ctypes.byref(P), ws.data_ptr(), ws.numel(), stream)
             _lib.check(rc, "glq_moe_decode")

@@ -257,6 +257,9 @@ typedef struct glq_moe_params {
    * row of U[2] directly.  u_rows[s]: rows of U[s] (0: n_clusters). */
   const int32_t* u_slot[2];
   int64_t u_rows[3];
+  /* (tokens, hidden) fp16 or NULL: out = fp16(residual + fp16(block output)),
+   * the decoder layer's residual add after the MoE block. */
+  const void* residual;
 } glq_moe_params;
 
 /* Workspace bytes glq_moe_decode needs for `p` (negative on a bad shape). */
