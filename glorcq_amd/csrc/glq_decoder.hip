@@ -206,26 +206,24 @@ __global__ __launch_bounds__(kDecThreads) void decode_attention_kernel(AttnArgs 
   const int L = min(max(*a.len, 1), a.max_len);
   const int c0 = split * kAttnChunk, n = max(0, min(kAttnChunk, L - c0));
   const int64_t base = ((int64_t)b * a.Hk + g) * a.max_len * kHeadDim + (int64_t)c0 * kHeadDim;
-  // stage: 16-byte pieces, 16 per row; K and V rows [0, n), q rows [0, rep)
-  {
+  // stage: 16-byte pieces, 16 per row; K and V rows [0, n), q rows [0, rep).
+  // Every load is unconditional (rows past n re-read row n - 1, the rows past
+  // n in LDS are never read), so all 16 go out before the first wait.
+  if (n > 0) {
     f16x8 kb[8], vb[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int idx = j * kDecThreads + tid, r = idx >> 4;
-      if (r < n) {
-        kb[j] = ((const f16x8*)(a.k_cache + base))[idx];
-        vb[j] = ((const f16x8*)(a.v_cache + base))[idx];
-      }
+      const int idx = j * kDecThreads + tid, r = min(idx >> 4, n - 1), c = idx & 15;
+      kb[j] = ((const f16x8*)(a.k_cache + base))[r * 16 + c];
+      vb[j] = ((const f16x8*)(a.v_cache + base))[r * 16 + c];
     }
     if (tid < rep * 16)
       ((f16x8*)qs)[tid] = ((const f16x8*)(a.q + ((int64_t)b * a.Hq + g * rep) * kHeadDim))[tid];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int idx = j * kDecThreads + tid, r = idx >> 4, c = idx & 15;
-      if (r < n) {
-        *(f16x8*)(ks + r * kKStride + 8 * c) = kb[j];
-        ((f16x8*)vs)[idx] = vb[j];
-      }
+      *(f16x8*)(ks + r * kKStride + 8 * c) = kb[j];
+      ((f16x8*)vs)[idx] = vb[j];
     }
   }
   __syncthreads();
@@ -298,16 +296,24 @@ __global__ __launch_bounds__(kDecThreads) void decode_attention_kernel(AttnArgs 
     }
     *(float4*)(my + 4 + 4 * l32) = float4{o0, o1, o2, o3};
   }
-  // arrival; the last block of (b, g) merges the splits
-  __threadfence();
+  // arrival; the last block of (b, g) merges the splits.  Every wave waits
+  // for its own partial stores to complete (they sit in this XCD's L2), then
+  // one thread releases them at device scope (one L2 write-back per block,
+  // not one per wave) and counts the block in; the last block's thread
+  // acquires (invalidating this CU's caches) before any thread reads.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (tid == 0) *flag = atomicAdd(a.count + b * a.Hk + g, 1u) == (unsigned)(a.nsplit - 1);
+  if (tid == 0) {
+    __threadfence();
+    const bool last = atomicAdd(a.count + b * a.Hk + g, 1u) == (unsigned)(a.nsplit - 1);
+    if (last) __threadfence();
+    *flag = last;
+  }
   __syncthreads();
   if (!*flag) return;
-  __threadfence();
   if (h < rep) {
-    // the fence above made the other blocks' partials visible (it invalidates
-    // this CU's cache): plain loads, up to 8 splits' worth in flight at once,
+    // the acquire above made the other blocks' partials visible: plain
+    // loads, up to 8 splits' worth in flight at once,
     // merged online (running max M, sums rescaled when M grows)
     const float* ph = a.part + ((int64_t)b * a.Hq + g * rep + h) * a.nsplit * kPartStride;
     float M = -__builtin_inff(), den = 0.f, r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;

@@ -395,12 +395,10 @@ __device__ void moe_xu_job(const MoeArgs& a, int job, unsigned char* smem, bool 
   for (int b0 = 0; b0 < nu; b0 += 8 * kRouteThreads) {  // U slice, 16 B per load,
     f16x8 buf[8];                                        // 8 loads in flight per thread
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int idx = b0 + j * kRouteThreads + tid;
-      if (idx < nu) {
-        const int k = idx / r8, j8 = idx - k * r8;
-        buf[j] = *(const f16x8*)(U + (int64_t)k * a.rank + 8 * j8);
-      }
+    for (int j = 0; j < 8; ++j) {  // unconditional: indices past the slice re-read its last piece
+      const int idx = min(b0 + j * kRouteThreads + tid, nu - 1);
+      const int k = idx / r8, j8 = idx - k * r8;
+      buf[j] = *(const f16x8*)(U + (int64_t)k * a.rank + 8 * j8);
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -502,15 +500,20 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(MoeArgs a) {
   }
   if ((int)blockIdx.x < a.nrb) {
     moe_route_tile(a, blockIdx.x, smem);
-    // arrival: the last router workgroup (after a device-scope fence on
-    // every thread's logit stores) builds the step's routing and tables and
-    // leaves the counter at zero for the next step
-    __threadfence();
+    // arrival: every wave waits for its logit stores to complete, one
+    // thread releases them at device scope and counts the workgroup in; the
+    // last router workgroup (its thread acquiring first) builds the step's
+    // routing and tables and leaves the counter at zero for the next step
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(a.rcount, 1u) == (unsigned)(a.nrb - 1);
+    if (threadIdx.x == 0) {
+      __threadfence();
+      const bool l = atomicAdd(a.rcount, 1u) == (unsigned)(a.nrb - 1);
+      if (l) __threadfence();
+      last = l;
+    }
     __syncthreads();
     if (last) {
-      __threadfence();
       moe_route_finalize(a, smem);
       if (threadIdx.x == 0) *a.rcount = 0u;
     }
