@@ -443,6 +443,10 @@ def main():
     ap.add_argument("--no-turbo", action="store_true", help="skip the TurboQuant codec leg")
     ap.add_argument("--no-model", action="store_true",
                     help="skip the model-level decode leg (config 4)")
+    ap.add_argument("--model-only", action="store_true",
+                    help="run only the model-level decode leg and print its JSON (profiling)")
+    ap.add_argument("--model-layers", type=int, default=48)
+    ap.add_argument("--model-batches", default="1,16")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (every box here has one); "
@@ -451,6 +455,15 @@ def main():
         return 2
     if args.pmc_workload:
         pmc_workload()
+        return 0
+    if args.model_only:
+        import torch
+
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        batches = tuple(int(b) for b in args.model_batches.split(","))
+        print(json.dumps(bench_model(dev, layers=args.model_layers, batches=batches)),
+              flush=True)
         return 0
 
     import torch
@@ -555,7 +568,8 @@ def main():
     if not args.no_model:
         log("model-level greedy decode (config 4), hipGraph replays")
         try:
-            result["model_decode"] = bench_model(dev)
+            batches = tuple(int(b) for b in args.model_batches.split(","))
+            result["model_decode"] = bench_model(dev, layers=args.model_layers, batches=batches)
         except Exception as exc:  # reported in the line; the kernel legs above stand
             result["model_decode"] = {"error": f"{type(exc).__name__}: {exc}"}
     if not args.no_cpu:
