@@ -1,32 +1,37 @@
 // MoE block decode step on MI355X: GraphCompatibleMoeBlock.forward
-// (inference/moe_block.py:381-436) for B <= 64 tokens, in four launches with
-// all routing on the device (no host sync, so the step captures in a hipGraph):
+// (inference/moe_block.py:381-436) for B <= 64 tokens, in four launches (five
+// when x U is gated on routing) with all routing on the device (no host sync,
+// so the step captures in a hipGraph):
 //
-//  1. moe_route_kernel (1024-thread workgroups): router tiles (16 router rows
-//     x 16 tokens, K split over the 16 waves, fp32 sums rounded to fp16 once)
-//     write the logits and the shared-expert gate sigmoid(fp16 logit); the
-//     other workgroups form fp32 partials of x U_c for every cluster c of gate
-//     and up with MFMA (the cluster-shared precompute, moe_block.py:290-322)
-//     and clear the a_down accumulators.
-//  2. moe_gate_up_kernel: every routed workgroup stages the logits in LDS,
-//     routes every token at once (softmax, top-k, optional renormalisation,
-//     moe_block.py:386-392; workgroup 0 publishes ids and weights), rebuilds
-//     the dispatch tables (expert-major pair lists cut into blocks of <= 8
-//     tokens) and runs gate and up of one block's expert over a range of
-//     16-row tiles in one pass (two-matrix K-split stream), writing
-//     inter = fp16(silu(g) * u) and adding the workgroup's share of
-//     a_down = inter U_down[c(e)] to fixed-point accumulators; workgroups past
-//     the routed blocks run the shared expert's gate/up.
+//  1. moe_route_kernel (256-thread workgroups): router tiles (16 router rows
+//     x 16 tokens, MFMA, fp32 sums rounded to fp16 once) write the logits and
+//     the shared-expert gate sigmoid(fp16 logit); the router workgroup that
+//     arrives last routes every token (softmax, top-k, optional
+//     renormalisation, moe_block.py:386-392) and writes the ids, weights and
+//     dispatch tables (expert-major pair lists cut into blocks of <= 8
+//     tokens) once for the step; the other workgroups form fp32 partials of
+//     x U_c for every cluster c of gate and up with MFMA (the cluster-shared
+//     precompute, moe_block.py:290-322) and clear the a_down accumulators.
+//     With many more clusters than picks those jobs run as moe_xu_kernel
+//     after the router, each skipping an unpicked cluster.
+//  2. moe_gate_up_kernel: every routed workgroup runs gate and up of one
+//     block's expert over a range of 16-row tiles in one pass (two-matrix
+//     K-split stream), writing inter = fp16(silu(g) * u) and adding the
+//     workgroup's share of a_down = inter U_down[c(e)] to fixed-point
+//     accumulators; workgroups past the routed blocks run the shared
+//     expert's gate/up.
 //  3. moe_down_kernel: routed down projections per (block, K part) with the
 //     low-rank term from a_down, and the shared expert's down projection per
 //     (token block, K part); fp32 partial outputs.
-//  4. moe_combine_kernel: out = fp16(sum_k w_k y_k + sigmoid-gate * fp16(shared)).
+//  4. moe_combine_kernel: out = fp16(sum_k w_k y_k + sigmoid-gate * fp16(shared))
+//     (+ the caller's residual).
 //
 // Only the selected experts' weights are read (the reference's graph mode
 // reads all E, moe_block.py:742-890), and a cluster's U is read once per step
-// for all of its experts.  The only atomics are 64-bit integer adds of the
-// a_down shares (below), whose sum does not depend on their order: every
-// result is the same on every run.
+// for all of its experts.  The atomics are 64-bit integer adds of the a_down
+// shares (below), whose sum does not depend on their order, and the router's
+// arrival counter, which only picks the workgroup that routes: every result
+// is the same on every run.
 #include <algorithm>
 #include <cstring>
 
