@@ -59,6 +59,8 @@ struct MoeArgs {
   int xurows;  // U rows per x U partial job
   int nbm;     // routed token blocks the grids are sized for
   int sus;     // K-slices of the gate/up x U partials
+  int nxu1;    // x U jobs in the router's launch (0 when gated)
+  int shk1;    // shared expert's gate/up in the router's launch (else in gate/up's)
   int wgu;     // workgroups per routed block (gate/up)
   int tpu;     // tiles per workgroup (gate/up, routed)
   int stb;     // tokens per shared-expert block
@@ -494,39 +496,6 @@ __device__ void moe_route_finalize(const MoeArgs& a, unsigned char* smem) {
   }
 }
 
-__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(MoeArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int last;
-  if (a.rank > 0) {  // this step's a_down accumulators start at zero
-    const int64_t nq = (int64_t)a.nbm * kMoeTB * a.rpad;
-    for (int64_t i = (int64_t)blockIdx.x * kRouteThreads + threadIdx.x; i < nq;
-         i += (int64_t)gridDim.x * kRouteThreads)
-      a.adq[i] = 0ull;
-  }
-  if ((int)blockIdx.x < a.nrb) {
-    moe_route_tile(a, blockIdx.x, smem);
-    // arrival: every wave waits for its logit stores to complete, one
-    // thread releases them at device scope and counts the workgroup in; the
-    // last router workgroup (its thread acquiring first) builds the step's
-    // routing and tables and leaves the counter at zero for the next step
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      __threadfence();
-      const bool l = atomicAdd(a.rcount, 1u) == (unsigned)(a.nrb - 1);
-      if (l) __threadfence();
-      last = l;
-    }
-    __syncthreads();
-    if (last) {
-      moe_route_finalize(a, smem);
-      if (threadIdx.x == 0) *a.rcount = 0u;
-    }
-  } else {
-    moe_xu_job(a, blockIdx.x - a.nrb, smem, false);
-  }
-}
-
 // The x U jobs in a launch of their own, after the router's, each gated on
 // its cluster being picked (steps whose clusters outnumber the picks).
 __global__ __launch_bounds__(kRouteThreads) void moe_xu_kernel(MoeArgs a) {
@@ -586,6 +555,50 @@ struct SharedGateUp {
   __device__ void store(int, int, int, float) const {}
 };
 
+// Launch 1: router tiles (+ the last one's routing), the x U jobs when not
+// gated, and (shk1, small batches) the shared expert's gate/up, which does
+// not depend on routing (workgroups past the others), so it overlaps the
+// router instead of lengthening the gate/up launch.
+template <int BS>
+__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(MoeArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int last;
+  if (a.rank > 0) {  // this step's a_down accumulators start at zero
+    const int64_t nq = (int64_t)a.nbm * kMoeTB * a.rpad;
+    for (int64_t i = (int64_t)blockIdx.x * kRouteThreads + threadIdx.x; i < nq;
+         i += (int64_t)gridDim.x * kRouteThreads)
+      a.adq[i] = 0ull;
+  }
+  if ((int)blockIdx.x < a.nrb) {
+    moe_route_tile(a, blockIdx.x, smem);
+    // arrival: every wave waits for its logit stores to complete, one
+    // thread releases them at device scope and counts the workgroup in; the
+    // last router workgroup (its thread acquiring first) builds the step's
+    // routing and tables and leaves the counter at zero for the next step
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      __threadfence();
+      const bool l = atomicAdd(a.rcount, 1u) == (unsigned)(a.nrb - 1);
+      if (l) __threadfence();
+      last = l;
+    }
+    __syncthreads();
+    if (last) {
+      moe_route_finalize(a, smem);
+      if (threadIdx.x == 0) *a.rcount = 0u;
+    }
+  } else if ((int)blockIdx.x < a.nrb + a.nxu1) {
+    moe_xu_job(a, blockIdx.x - a.nrb, smem, false);
+  } else if constexpr (BS != 0) {
+    const int id = blockIdx.x - a.nrb - a.nxu1;
+    const int sb = id / a.wgsu, wg = id - sb * a.wgsu;
+    const int t0 = wg * a.tpsu, t1 = min(a.shSGU.tiles, t0 + a.tpsu);
+    gemv_stream_ks<BS, BS == 2 ? 2 : 1, kMoeDepth, false, BS == 2, 2>(SharedGateUp{a, sb},
+                                                                     a.shSGU, 0, t0, t1, smem);
+  }
+}
+
 template <int BR, int BS>
 __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -625,7 +638,7 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
     const int t0 = wg * a.tpu, t1 = min(a.shGU.tiles, t0 + a.tpu);
     gemv_stream_ks<BR, 1, kMoeDepth, false, BR == 2, 2>(
         RoutedGateUp{a, tok, b, wg, e, M, cg, cu, cd}, a.shGU, 0, t0, t1, smem);
-  } else if constexpr (BS != 0) {
+  } else if constexpr (BS != 0) {  // the shared expert's gate/up when not in launch 1
     const int id = blockIdx.x - nr;
     const int sb = id / a.wgsu, wg = id - sb * a.wgsu;
     const int t0 = wg * a.tpsu, t1 = min(a.shSGU.tiles, t0 + a.tpsu);
@@ -762,7 +775,7 @@ namespace {
 struct MoePlan {
   MoeArgs a;
   int64_t ws_need;
-  size_t lds_route, lds_xu, lds_gu, lds_d, lds_c;
+  size_t lds_route, lds_xu, lds_gu, lds_d, lds_c, lds_shgu;
   int64_t grid_route, grid_xu, grid_gu, grid_d, grid_c;
   bool xu_gated;  // x U jobs in their own launch, gated on routing
   int64_t off_rcnt, off_tab, off_sel, off_lgb, off_wts, off_sg, off_xu, off_inter, off_adq, off_sinter, off_yb, off_sdp;
@@ -908,14 +921,20 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
   size_t ld = Ld.total + stream_ks_bytes(1);
   a.pl_off = (int)align_up(ld, 16);  // the routed block's pair list
   ld = a.pl_off + 16 * 4;
+  P.lds_shgu = 0;
   if (SI > 0) {
     const StreamLds Ls = stream_lds(kMoeDepth, stream_slot_bytes(a.sbits), a.stb, (int)H,
                                     a.sbits, a.shSGU.xstride, a.shSGU.apad, 2, 0);
-    lgu = std::max<size_t>(lgu, Ls.total + stream_ks_bytes(2));
+    P.lds_shgu = Ls.total + stream_ks_bytes(2);  // in the router's launch
     const StreamLds Lsd = stream_lds(kMoeDepth, stream_slot_bytes(a.sbits), a.stb, a.ks,
                                      a.sbits, a.shSD.xstride, a.shSD.apad, 1, 0);
     ld = std::max<size_t>(ld, Lsd.total + stream_ks_bytes(1));
   }
+  // small batches run the shared gate/up in the router's launch: it then
+  // overlaps routing; larger ones keep the router launch's LDS (and its x U
+  // jobs' occupancy) small
+  a.shk1 = SI > 0 && B <= 16;
+  if (SI > 0 && !a.shk1) lgu = std::max(lgu, P.lds_shgu);
   GLQ_CHECK(lgu <= 160 * 1024 && ld <= 160 * 1024, "MoE shapes exceed the LDS budget");
   P.lds_gu = lgu;
   P.lds_d = ld;
@@ -928,6 +947,7 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
     // the router's last workgroup stages B rows of routing keys and the tables
     P.lds_route = std::max(P.lds_route, (size_t)align_up(4 * B * moe_lg_stride((int)E), 16) +
                                             (size_t)tbl);
+    if (a.shk1) P.lds_route = std::max(P.lds_route, P.lds_shgu);
     // the gated jobs stage B rows of routing keys first
     P.lds_xu = std::max(xu, (size_t)4 * B * moe_lg_stride((int)E));
     GLQ_CHECK(std::max(P.lds_route, P.lds_xu) <= 160 * 1024,
@@ -940,9 +960,10 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
   // of a step go unpicked; GLQ_MOE_XU_GATE=0/1 forces either form
   P.xu_gated = lora && a.C > 4 * P_;
   if (const char* g = getenv("GLQ_MOE_XU_GATE")) P.xu_gated = lora && atoi(g) != 0;
-  P.grid_route = a.nrb + (lora && !P.xu_gated ? 2 * a.C * a.sus : 0);
+  a.nxu1 = lora && !P.xu_gated ? 2 * a.C * a.sus : 0;
+  P.grid_route = a.nrb + a.nxu1 + (a.shk1 ? (int64_t)a.nsb * a.wgsu : 0);
   P.grid_xu = lora ? 2 * a.C * a.sus : 0;
-  P.grid_gu = (int64_t)a.nbm * a.wgu + (SI > 0 ? (int64_t)a.nsb * a.wgsu : 0);
+  P.grid_gu = (int64_t)a.nbm * a.wgu + (SI > 0 && !a.shk1 ? (int64_t)a.nsb * a.wgsu : 0);
   P.grid_d = (int64_t)a.nbm * a.sr * a.wgd + (SI > 0 ? (int64_t)a.nsb * a.ss * a.wgsd : 0);
   P.grid_c = B * ((H + 255) / 256);
   // workspace
@@ -999,9 +1020,9 @@ int moe_launch(MoePlan& P, hipStream_t s) {
   static size_t attr_gu = 64 * 1024, attr_d = 64 * 1024, attr_c = 64 * 1024;
   static size_t attr_r = 64 * 1024, attr_x = 64 * 1024;
   const MoeArgs& a = P.a;
-  int rc = set_lds_limit(moe_route_kernel, P.lds_route, attr_r);
+  int rc = set_lds_limit(moe_route_kernel<BS>, P.lds_route, attr_r);
   if (rc) return rc;
-  moe_route_kernel<<<dim3((unsigned)P.grid_route), dim3(kRouteThreads), P.lds_route, s>>>(a);
+  moe_route_kernel<BS><<<dim3((unsigned)P.grid_route), dim3(kRouteThreads), P.lds_route, s>>>(a);
   GLQ_LAUNCH_CHECK("moe_route_kernel");
   if (P.xu_gated) {
     rc = set_lds_limit(moe_xu_kernel, P.lds_xu, attr_x);
