@@ -13,16 +13,17 @@
 //     x U_c for every cluster c of gate and up with MFMA (the cluster-shared
 //     precompute, moe_block.py:290-322) and clear the a_down accumulators.
 //     With many more clusters than picks those jobs run as moe_xu_kernel
-//     after the router, each skipping an unpicked cluster.
+//     after the router, each skipping an unpicked cluster.  Workgroups past
+//     the others run the shared expert's gate/up (it does not depend on
+//     routing).
 //  2. moe_gate_up_kernel: every routed workgroup runs gate and up of one
 //     block's expert over a range of 16-row tiles in one pass (two-matrix
 //     K-split stream), writing inter = fp16(silu(g) * u) and adding the
 //     workgroup's share of a_down = inter U_down[c(e)] to fixed-point
 //     accumulators; workgroups past the routed blocks run the shared
-//     expert's gate/up.
+//     expert's down projection per (token block, K part).
 //  3. moe_down_kernel: routed down projections per (block, K part) with the
-//     low-rank term from a_down, and the shared expert's down projection per
-//     (token block, K part); fp32 partial outputs.
+//     low-rank term from a_down; fp32 partial outputs.
 //  4. moe_combine_kernel: out = fp16(sum_k w_k y_k + sigmoid-gate * fp16(shared))
 //     (+ the caller's residual).
 //
@@ -60,7 +61,6 @@ struct MoeArgs {
   int nbm;     // routed token blocks the grids are sized for
   int sus;     // K-slices of the gate/up x U partials
   int nxu1;    // x U jobs in the router's launch (0 when gated)
-  int shk1;    // shared expert's gate/up in the router's launch (else in gate/up's)
   int wgu;     // workgroups per routed block (gate/up)
   int tpu;     // tiles per workgroup (gate/up, routed)
   int stb;     // tokens per shared-expert block
@@ -556,9 +556,9 @@ struct SharedGateUp {
 };
 
 // Launch 1: router tiles (+ the last one's routing), the x U jobs when not
-// gated, and (shk1, small batches) the shared expert's gate/up, which does
-// not depend on routing (workgroups past the others), so it overlaps the
-// router instead of lengthening the gate/up launch.
+// gated, and the shared expert's gate/up, which does not depend on routing
+// (workgroups past the others), so it overlaps the router; the shared down
+// then runs in the gate/up launch, overlapping the routed experts.
 template <int BS>
 __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(MoeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -599,6 +599,9 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(MoeArgs a) {
   }
 }
 
+template <int BS>
+__device__ void moe_shared_down_job(const MoeArgs& a, int id, unsigned char* smem);
+
 template <int BR, int BS>
 __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -638,12 +641,8 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
     const int t0 = wg * a.tpu, t1 = min(a.shGU.tiles, t0 + a.tpu);
     gemv_stream_ks<BR, 1, kMoeDepth, false, BR == 2, 2>(
         RoutedGateUp{a, tok, b, wg, e, M, cg, cu, cd}, a.shGU, 0, t0, t1, smem);
-  } else if constexpr (BS != 0) {  // the shared expert's gate/up when not in launch 1
-    const int id = blockIdx.x - nr;
-    const int sb = id / a.wgsu, wg = id - sb * a.wgsu;
-    const int t0 = wg * a.tpsu, t1 = min(a.shSGU.tiles, t0 + a.tpsu);
-    gemv_stream_ks<BS, BS == 2 ? 2 : 1, kMoeDepth, false, BS == 2, 2>(SharedGateUp{a, sb},
-                                                                     a.shSGU, 0, t0, t1, smem);
+  } else if constexpr (BS != 0) {  // the shared expert's down (its gate/up ran in launch 1)
+    moe_shared_down_job<BS>(a, blockIdx.x - nr, smem);
   }
 }
 
@@ -705,6 +704,19 @@ struct SharedDown {
   }
 };
 
+// The shared expert's down projection for (token block, K part, tile range)
+// `id`, in the gate/up launch (its inter is ready after launch 1).
+template <int BS>
+__device__ void moe_shared_down_job(const MoeArgs& a, int id, unsigned char* smem) {
+  const int sb = id / (a.ss * a.wgsd);
+  const int rem = id - sb * a.ss * a.wgsd;
+  const int part = rem / a.wgsd, wg = rem - part * a.wgsd;
+  const StreamShape sh = moe_part_shape(a.shSD, a.SI, a.ks, part, BS);
+  const int t0 = wg * a.tpsd, t1 = min(sh.tiles, t0 + a.tpsd);
+  gemv_stream_ks<BS, BS == 2 ? 2 : 1, kMoeDepth, false, BS == 2, 1>(
+      SharedDown{a, sb, part, part * a.ks}, sh, 0, t0, t1, smem);
+}
+
 template <int BR, int BS>
 __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -729,15 +741,6 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
     const int t0 = wg * a.tpd, t1 = min(sh.tiles, t0 + a.tpd);
     gemv_stream_ks<BR, 1, kMoeDepth, false, BR == 2, 1>(
         RoutedDown{a, pair, b, e, M, part, part * a.kr}, sh, 0, t0, t1, smem);
-  } else if constexpr (BS != 0) {
-    const int id = blockIdx.x - nr;
-    const int sb = id / (a.ss * a.wgsd);
-    const int rem = id - sb * a.ss * a.wgsd;
-    const int part = rem / a.wgsd, wg = rem - part * a.wgsd;
-    const StreamShape sh = moe_part_shape(a.shSD, a.SI, a.ks, part, BS);
-    const int t0 = wg * a.tpsd, t1 = min(sh.tiles, t0 + a.tpsd);
-    gemv_stream_ks<BS, BS == 2 ? 2 : 1, kMoeDepth, false, BS == 2, 1>(
-        SharedDown{a, sb, part, part * a.ks}, sh, 0, t0, t1, smem);
   }
 }
 
@@ -775,7 +778,7 @@ namespace {
 struct MoePlan {
   MoeArgs a;
   int64_t ws_need;
-  size_t lds_route, lds_xu, lds_gu, lds_d, lds_c, lds_shgu;
+  size_t lds_route, lds_xu, lds_gu, lds_d, lds_c, lds_shgu, lds_shd;
   int64_t grid_route, grid_xu, grid_gu, grid_d, grid_c;
   bool xu_gated;  // x U jobs in their own launch, gated on routing
   int64_t off_rcnt, off_tab, off_sel, off_lgb, off_wts, off_sg, off_xu, off_inter, off_adq, off_sinter, off_yb, off_sdp;
@@ -922,19 +925,16 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
   a.pl_off = (int)align_up(ld, 16);  // the routed block's pair list
   ld = a.pl_off + 16 * 4;
   P.lds_shgu = 0;
+  P.lds_shd = 0;
   if (SI > 0) {
     const StreamLds Ls = stream_lds(kMoeDepth, stream_slot_bytes(a.sbits), a.stb, (int)H,
                                     a.sbits, a.shSGU.xstride, a.shSGU.apad, 2, 0);
     P.lds_shgu = Ls.total + stream_ks_bytes(2);  // in the router's launch
     const StreamLds Lsd = stream_lds(kMoeDepth, stream_slot_bytes(a.sbits), a.stb, a.ks,
                                      a.sbits, a.shSD.xstride, a.shSD.apad, 1, 0);
-    ld = std::max<size_t>(ld, Lsd.total + stream_ks_bytes(1));
+    P.lds_shd = Lsd.total + stream_ks_bytes(1);
   }
-  // small batches run the shared gate/up in the router's launch: it then
-  // overlaps routing; larger ones keep the router launch's LDS (and its x U
-  // jobs' occupancy) small
-  a.shk1 = SI > 0 && B <= 16;
-  if (SI > 0 && !a.shk1) lgu = std::max(lgu, P.lds_shgu);
+  lgu = std::max(lgu, P.lds_shd);  // the shared down runs in the gate/up launch
   GLQ_CHECK(lgu <= 160 * 1024 && ld <= 160 * 1024, "MoE shapes exceed the LDS budget");
   P.lds_gu = lgu;
   P.lds_d = ld;
@@ -947,7 +947,7 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
     // the router's last workgroup stages B rows of routing keys and the tables
     P.lds_route = std::max(P.lds_route, (size_t)align_up(4 * B * moe_lg_stride((int)E), 16) +
                                             (size_t)tbl);
-    if (a.shk1) P.lds_route = std::max(P.lds_route, P.lds_shgu);
+    P.lds_route = std::max(P.lds_route, P.lds_shgu);  // the shared gate/up runs here
     // the gated jobs stage B rows of routing keys first
     P.lds_xu = std::max(xu, (size_t)4 * B * moe_lg_stride((int)E));
     GLQ_CHECK(std::max(P.lds_route, P.lds_xu) <= 160 * 1024,
@@ -961,10 +961,10 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
   P.xu_gated = lora && a.C > 4 * P_;
   if (const char* g = getenv("GLQ_MOE_XU_GATE")) P.xu_gated = lora && atoi(g) != 0;
   a.nxu1 = lora && !P.xu_gated ? 2 * a.C * a.sus : 0;
-  P.grid_route = a.nrb + a.nxu1 + (a.shk1 ? (int64_t)a.nsb * a.wgsu : 0);
+  P.grid_route = a.nrb + a.nxu1 + (SI > 0 ? (int64_t)a.nsb * a.wgsu : 0);
   P.grid_xu = lora ? 2 * a.C * a.sus : 0;
-  P.grid_gu = (int64_t)a.nbm * a.wgu + (SI > 0 && !a.shk1 ? (int64_t)a.nsb * a.wgsu : 0);
-  P.grid_d = (int64_t)a.nbm * a.sr * a.wgd + (SI > 0 ? (int64_t)a.nsb * a.ss * a.wgsd : 0);
+  P.grid_gu = (int64_t)a.nbm * a.wgu + (SI > 0 ? (int64_t)a.nsb * a.ss * a.wgsd : 0);
+  P.grid_d = (int64_t)a.nbm * a.sr * a.wgd;
   P.grid_c = B * ((H + 255) / 256);
   // workspace
   int64_t o = 0;
