@@ -61,6 +61,7 @@ struct MoeArgs {
   int nbm;     // routed token blocks the grids are sized for
   int sus;     // K-slices of the gate/up x U partials
   int nxu1;    // x U jobs in the router's launch (0 when gated)
+  int nxc;     // gated: picked-cluster slots per projection, min(C, B * topk)
   int wgu;     // workgroups per routed block (gate/up)
   int tpu;     // tiles per workgroup (gate/up, routed)
   int stb;     // tokens per shared-expert block
@@ -105,7 +106,8 @@ struct MoeArgs {
   __half* lgb;     // [B][E] fp16 router logits (workspace)
   // dispatch tables, built once per step by the router's last workgroup:
   // [0] blocks, then bexp[nbm], bM[nbm], then kMoeTB pair ids per block
-  // (t * topk + k; slots past bM repeat the block's first pair)
+  // (t * topk + k; slots past bM repeat the block's first pair), then (gated
+  // x U) the number of picked gate and up clusters and their lists [2][nxc]
   int* tab;
   unsigned* rcount;  // router workgroups arrived (zero between steps)
 };
@@ -350,43 +352,28 @@ __device__ void moe_route_tile(const MoeArgs& a, int id, unsigned char* smem) {
 //
 // A job leaves at once when no expert's projection s uses cluster c (a
 // projection may have fewer clusters than C).  Gated (`gated`, the launch
-// after the router's), it also leaves unless some token picked an expert of
-// cluster c: the B rows of routing keys are staged in LDS (the same keys and
-// order as the top-k), and the thread of each (token, expert of c) ranks that
-// expert's key in its row by 16-byte LDS reads -- so a step reads only the
-// picked clusters' U slices.
+// after the router's), jobs run over the router's list of picked clusters
+// instead -- min(C, B * topk) slots per projection, unused slots leave at
+// once -- so a step reads only the picked clusters' U slices.
 __device__ void moe_xu_job(const MoeArgs& a, int job, unsigned char* smem, bool gated) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, kb = lane >> 4;
-  const int s = job / (a.C * a.sus), rem = job - s * a.C * a.sus;
-  const int c = rem / a.sus, q = rem - c * a.sus;
-  {
+  int s, c, q;
+  if (gated) {  // job -> (projection, picked-cluster slot, slice) from the router's lists
+    const int per = a.nxc * a.sus;
+    s = job / per;
+    const int rem = job - s * per, i = rem / a.sus;
+    q = rem - i * a.sus;
+    const int* pc = a.tab + 1 + (2 + kMoeTB) * a.nbm;
+    if (i >= pc[s]) return;  // uniform over the workgroup
+    c = pc[2 + s * a.nxc + i];
+  } else {
+    s = job / (a.C * a.sus);
+    const int rem = job - s * a.C * a.sus;
+    c = rem / a.sus;
+    q = rem - c * a.sus;
     int act = 0;
-    if (gated) {
-      uint32_t* keys = (uint32_t*)smem;  // [B][LS], reused below once all have voted
-      const int LS = moe_lg_stride(a.E), E4 = a.E & ~3;
-      const unsigned short* lg = (const unsigned short*)a.lgb;
-      for (int i = tid; i < a.B * a.E; i += kRouteThreads) {
-        const int t = i / a.E, e = i - t * a.E;
-        keys[t * LS + e] = moe_key(lg[i], e);
-      }
-      __syncthreads();
-      for (int i = tid; i < a.B * a.E; i += kRouteThreads) {
-        const int t = i / a.E, e = i - t * a.E;
-        if (a.clus[s][e] != c) continue;
-        const uint32_t* row = keys + t * LS;
-        const uint32_t ke = row[e];
-        int r = 0;
-        for (int j = 0; j < E4; j += 4) {
-          const uint4 v = *(const uint4*)(row + j);
-          r += (int)(v.x > ke) + (int)(v.y > ke) + (int)(v.z > ke) + (int)(v.w > ke);
-        }
-        for (int j = E4; j < a.E; ++j) r += (int)(row[j] > ke);
-        act |= (int)(r < a.topk);
-      }
-    } else {
-      for (int e = tid; e < a.E; e += kRouteThreads) act |= (int)(a.clus[s][e] == c);
-    }
+    for (int e = tid; e < a.E; e += kRouteThreads) act |= (int)(a.clus[s][e] == c);
     if (!__syncthreads_or(act)) return;
   }
   const int xr = a.xurows;
@@ -493,6 +480,26 @@ __device__ void moe_route_finalize(const MoeArgs& a, unsigned char* smem) {
   for (int i = tid; i < nblk * kMoeTB; i += kRouteThreads) {
     const int b = i / kMoeTB, m = i - b * kMoeTB;
     g[1 + 2 * a.nbm + i] = t.list[t.bfirst[b] + min(m, t.bM[b] - 1)];
+  }
+  if (a.nxc > 0) {  // gated x U: the picked gate and up clusters, compacted
+    int* flag = t.nblk + 1;      // [2][C]
+    int* cnt = flag + 2 * a.C;   // [2]
+    for (int i = tid; i < 2 * a.C; i += kRouteThreads) flag[i] = 0;
+    if (tid < 2) cnt[tid] = 0;
+    __syncthreads();
+    for (int i = tid; i < 2 * P; i += kRouteThreads) {
+      const int sp = i / P, e = t.sel[i - sp * P];
+      if (e >= 0) flag[sp * a.C + min(max(a.clus[sp][e], 0), a.C - 1)] = 1;
+    }
+    __syncthreads();
+    int* pc = g + 1 + (2 + kMoeTB) * a.nbm;
+    for (int i = tid; i < 2 * a.C; i += kRouteThreads)
+      if (flag[i]) {  // list order does not matter: each job writes its own cluster's slot
+        const int sp = i / a.C, slot = atomicAdd(cnt + sp, 1);
+        if (slot < a.nxc) pc[2 + sp * a.nxc + slot] = i - sp * a.C;
+      }
+    __syncthreads();
+    if (tid < 2) pc[tid] = min(cnt[tid], a.nxc);
   }
 }
 
@@ -946,7 +953,7 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
     P.lds_route = std::max(router, lora ? xu : (size_t)0);
     // the router's last workgroup stages B rows of routing keys and the tables
     P.lds_route = std::max(P.lds_route, (size_t)align_up(4 * B * moe_lg_stride((int)E), 16) +
-                                            (size_t)tbl);
+                                            (size_t)tbl + 4 * (2 * (size_t)a.C + 2));
     P.lds_route = std::max(P.lds_route, P.lds_shgu);  // the shared gate/up runs here
     // the gated jobs stage B rows of routing keys first
     P.lds_xu = std::max(xu, (size_t)4 * B * moe_lg_stride((int)E));
@@ -961,8 +968,9 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
   P.xu_gated = lora && a.C > 4 * P_;
   if (const char* g = getenv("GLQ_MOE_XU_GATE")) P.xu_gated = lora && atoi(g) != 0;
   a.nxu1 = lora && !P.xu_gated ? 2 * a.C * a.sus : 0;
+  a.nxc = P.xu_gated ? std::min(a.C, P_) : 0;
   P.grid_route = a.nrb + a.nxu1 + (SI > 0 ? (int64_t)a.nsb * a.wgsu : 0);
-  P.grid_xu = lora ? 2 * a.C * a.sus : 0;
+  P.grid_xu = lora ? 2 * (int64_t)a.nxc * a.sus : 0;
   P.grid_gu = (int64_t)a.nbm * a.wgu + (SI > 0 ? (int64_t)a.nsb * a.ss * a.wgsd : 0);
   P.grid_d = (int64_t)a.nbm * a.sr * a.wgd;
   P.grid_c = B * ((H + 255) / 256);
@@ -974,7 +982,9 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
     return at;
   };
   P.off_rcnt = take(4);  // must be zero before the first step; every step leaves it zero
-  P.off_tab = take(4 * (1 + (2 + kMoeTB) * (int64_t)a.nbm));
+  // (the picked-cluster lists are sized whether or not this step is gated,
+  // so the workspace size does not depend on the form)
+  P.off_tab = take(4 * (1 + (2 + kMoeTB) * (int64_t)a.nbm + 2 + 2 * std::min<int64_t>(a.C, P_)));
   P.off_sel = take(4 * P_);
   P.off_lgb = take(2 * B * E);
   P.off_wts = take(2 * P_);
