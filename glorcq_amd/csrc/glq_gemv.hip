@@ -120,6 +120,7 @@ struct DenseStreamArgs {
   StreamShape ss;
   int wpi;  // workgroups per item
   int tpw;  // 16-row tiles per workgroup
+  int ks;   // K-split form: all four waves on each tile
 };
 
 template <int BITS, int MP, int D, bool SYM, bool SZ2>
@@ -127,7 +128,10 @@ __global__ __launch_bounds__(256) void gemv_stream_dense_kernel(DenseStreamArgs 
   extern __shared__ __align__(16) unsigned char smem[];
   const int item = blockIdx.x / sa.wpi, wg = blockIdx.x - item * sa.wpi;
   const int t0 = wg * sa.tpw, t1 = min(sa.ss.tiles, t0 + sa.tpw);
-  gemv_stream<BITS, MP, D, SYM, SZ2, 1>(DenseSrc{sa.a}, sa.ss, item, t0, t1, smem);
+  if (sa.ks)
+    gemv_stream_ks<BITS, MP, D, SYM, SZ2, 1>(DenseSrc{sa.a}, sa.ss, item, t0, t1, smem);
+  else
+    gemv_stream<BITS, MP, D, SYM, SZ2, 1>(DenseSrc{sa.a}, sa.ss, item, t0, t1, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -250,11 +254,20 @@ bool stream_shape(int64_t M, const TileShape& sh, int bits, StreamShape& ss, siz
 
 // Workgroups per item: aim for about 4 per CU over the whole launch
 // (GLQ_STREAM_WGS overrides the target).
-void stream_split(int64_t items, int tiles, int& wpi, int& tpw) {
+// A launch whose tiles would leave most CUs idle (fewer than 256 workgroups
+// at one tile per wave) with long tiles (>= 4 chunks) takes the K-split
+// form instead: one tile per workgroup, its chunks dealt over the four waves,
+// so each wave's serial chain is a quarter of the tile (GLQ_STREAM_KS=0/1
+// forces either form).
+void stream_split(int64_t items, int tiles, int nchunk, bool allow_ks, int& wpi, int& tpw,
+                  int& ks) {
   int64_t target = 1024;
   if (const char* e = getenv("GLQ_STREAM_WGS")) target = atoll(e) > 0 ? atoll(e) : target;
+  ks = items * ((tiles + 3) / 4) < 256 && nchunk >= 4;
+  if (const char* e = getenv("GLQ_STREAM_KS")) ks = atoi(e) != 0;
+  ks = ks && allow_ks;
   int64_t w = (target + items - 1) / items;
-  const int64_t wmax = (tiles + 3) / 4;  // at least one tile per wave
+  const int64_t wmax = ks ? tiles : (tiles + 3) / 4;  // at least one tile per wave / workgroup
   if (w > wmax) w = wmax;
   if (w < 1) w = 1;
   tpw = (int)((tiles + w - 1) / w);
@@ -431,7 +444,10 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   bool sz2 = false;
   if (stream_shape(M, sh, bits, sa.ss, slds, sz2)) {
     sa.a = a;
-    stream_split(items, sa.ss.tiles, sa.wpi, sa.tpw);
+    // the K-split form also holds the waves' partial tiles in LDS
+    const bool ks_fits = slds + stream_ks_bytes(1) <= (size_t)kMaxLds;
+    stream_split(items, sa.ss.tiles, sa.ss.nchunk, ks_fits, sa.wpi, sa.tpw, sa.ks);
+    if (sa.ks) slds += stream_ks_bytes(1);
     return launch_stream(sa, items, bits, sz2, slds, s);
   }
   const size_t lds = gemv_lds_bytes(sh, T);

@@ -382,3 +382,34 @@ def test_batched_precomputed_xu(gpu, bits):
                                          128, SV=st("SV"), precomputed_xU=xu)
     for e, p in enumerate(ps):
         assert_parity(y[e], oracle_y(p, xu=xu[e].cpu()), f"item {e}")
+
+
+@pytest.mark.parametrize("ks", ["0", "1"])
+@pytest.mark.parametrize("K,N,bits,M,items,bias", [
+    (4096, 2048, 4, 1, 1, False),    # the Qwen3 o projection at one token
+    (4096, 2048, 4, 16, 1, True),
+    (2048, 1408, 2, 8, 1, False),
+    (2048, 1462, 2, 12, 3, True),    # ragged N, several items
+    (5632, 2048, 4, 4, 1, False),
+])
+def test_stream_forms(gpu, monkeypatch, ks, K, N, bits, M, items, bias):
+    """The streaming GEMV in both forms (GLQ_STREAM_KS: one wave per tile, or
+    the K-split form with a tile's chunks dealt over the four waves and the
+    partial tiles summed in a fixed order) against the oracle; the lane path
+    is switched off so M = 1 streams too."""
+    monkeypatch.setenv("GLQ_STREAM_KS", ks)
+    monkeypatch.setenv("GLQ_GEMV_NO_LANE", "1")
+    ps = [fmt.make_linear(K, N, bits=bits, rank=64, M=M, seed=7 * K + N + M + e)
+          for e in range(items)]
+    g = torch.Generator().manual_seed(N)
+    bs = [(torch.randn(N, generator=g) * 0.1).half() if bias else None for _ in range(items)]
+    st = lambda k: torch.stack([getattr(p, k) for p in ps]).to(gpu)  # noqa: E731
+    B = torch.stack(bs).to(gpu) if bias else None
+    y = K_.packed_dequant_matmul_batched(st("x"), st("codes"), st("scales"), st("zeros"), bits,
+                                         128, U=st("U"), SV=st("SV"), bias=B)
+    again = K_.packed_dequant_matmul_batched(st("x"), st("codes"), st("scales"), st("zeros"),
+                                             bits, 128, U=st("U"), SV=st("SV"), bias=B)
+    torch.cuda.synchronize()
+    assert torch.equal(y, again)
+    for e, p in enumerate(ps):
+        assert_parity(y[e], oracle_y(p, bias=bs[e]), f"ks={ks} item {e}")
