@@ -250,6 +250,42 @@ __device__ void lowrank_partial(const XRow& xrow, int M, int K, int rank, int rp
   const int j8 = tid & 7, kr = tid >> 3;  // kr in 0..31
   const int k0 = p * kLowrankRows;
   const int kl = min(kLowrankRows, K - k0);
+  if constexpr (MC == 4) {
+    // 3..16 token rows: one v_mfma_f32_16x16x32_f16 tile per 16 rank columns
+    // (A = the x slice, 16 rows staged in LDS with zeros past M; B = U
+    // straight from memory, lane = column, so the 16 lanes of a k row read
+    // 32 contiguous bytes), waves over the column tiles.
+    for (int idx = tid; idx < 16 * kLowrankRows; idx += 256) {
+      const int m = idx / kLowrankRows, k = idx - m * kLowrankRows;
+      xl[idx] = (m < M && k < kl) ? xrow(m)[k0 + k] : __float2half(0.f);
+    }
+    __syncthreads();
+    const int li = lane & 15, kb = lane >> 4;
+    for (int ct = wave; ct * 16 < rpad; ct += 4) {
+      const int col = ct * 16 + li;
+      const bool cv = col < rank;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kLowrankRows / 32; ++ks) {
+        const int kk = 32 * ks + 8 * kb;
+        f16x8 bv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          bv[e] = (cv && kk + e < kl) ? (_Float16)__half2float(U[(int64_t)(k0 + kk + e) * rank + col])
+                                      : (_Float16)0.f;
+        acc = mfma_16x16x32(*(const f16x8*)(xl + li * kLowrankRows + kk), bv, acc);
+      }
+      // acc[i] = sum over the slice for token 4 kb + i, column col
+      if (out && col < rpad) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 4 * kb + i;
+          if (m < M) out[m * rpad + col] = cv ? acc[i] : 0.f;
+        }
+      }
+    }
+    return;
+  }
   // stage the x slice (M x kl) in LDS
   for (int idx = tid; idx < M * kLowrankRows; idx += 256) {
     const int m = idx / kLowrankRows, k = idx - m * kLowrankRows;
