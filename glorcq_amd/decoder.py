@@ -80,6 +80,28 @@ class GLoRCQQwen3Attention(nn.Module):
             self._U_qkv = torch.stack(Us).contiguous()
             for i, m in enumerate(lins):
                 m.U = self._U_qkv[i]  # the same values, now views of the stack
+        # One decode token: q, k and v as ONE batched GEMV launch (plus its
+        # x U partials) over items of kv_out rows -- q's rows as q_out/kv_out
+        # items, then k, then v -- with the three layers' codes, scales,
+        # zero-points and SV laid end to end (the layers keep views of them)
+        # and each item's U (q's repeated per q item).
+        self._qkv = None
+        q, k, v = lins
+        nkv = k.out_features
+        if (self._U_qkv is not None and v.out_features == nkv and q.out_features % nkv == 0
+                and all(m.bias_param is None and not m.gptq_sym and m.zeros is not None
+                        and m.pack_bits == q.pack_bits and m.gptq_groupsize == q.gptq_groupsize
+                        for m in lins)):
+            nq = q.out_features // nkv
+            cat = {}
+            for name in ("codes", "scales", "zeros", "SV"):
+                full = torch.cat([getattr(m, name) for m in lins]).contiguous()
+                cat[name] = full.view(nq + 2, nkv, *full.shape[1:])
+                setattr(q, name, full[:q.out_features])
+                setattr(k, name, full[q.out_features:q.out_features + nkv])
+                setattr(v, name, full[q.out_features + nkv:])
+            cat["U"] = torch.stack([q.U] * nq + [k.U, v.U]).contiguous()
+            self._qkv = cat
         self._len = None  # device int32: positions the step attends to
         self._ws = None   # decode attention workspace (counters stay zero between calls)
         self._ws_key = None
@@ -93,7 +115,15 @@ class GLoRCQQwen3Attention(nn.Module):
                               past_key_values=past_key_values, **kwargs)
         inner = self.inner
         x = hidden_states.reshape(B, H)
-        if self._U_qkv is not None and B <= kernels.GEMV_MAX_M:
+        if self._qkv is not None and B == 1:
+            c = self._qkv
+            y = kernels.packed_dequant_matmul_batched(
+                x.contiguous(), c["codes"], c["scales"], c["zeros"], inner.q_proj.pack_bits,
+                inner.q_proj.gptq_groupsize, U=c["U"], SV=c["SV"]).reshape(1, -1)
+            nq = inner.q_proj.out_features
+            nkv = inner.k_proj.out_features
+            q, k, v = y[:, :nq], y[:, nq:nq + nkv], y[:, nq + nkv:]
+        elif self._U_qkv is not None and B <= kernels.GEMV_MAX_M:
             xu = kernels.lowrank_xu(x.contiguous(), self._U_qkv)  # (3, B, r)
             q = inner.q_proj(x, precomputed_xU=xu[0])
             k = inner.k_proj(x, precomputed_xU=xu[1])

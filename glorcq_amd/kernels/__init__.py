@@ -182,6 +182,7 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
                                   precomputed_xU: torch.Tensor | None = None) -> torch.Tensor:
     """E independent problems in one launch: x (E, M, K), codes (E, N, Kw),
     scales/zeros (E, N, G), U (E, K, r), SV (E, N, r), bias (E, N) -> (E, M, N).
+    A 2-D x (M, K) is the one input of every problem (x stride 0).
 
     The packed-format counterpart of turbo_dequant_grouped_gemv_fused
     (inference/kernels/__init__.py:242-278), with the low-rank term fused.
@@ -192,7 +193,11 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
     _require(scales, "scales", torch.float16)
     if not sym:
         _require(zeros, "zeros", torch.float16)
-    E, M, K = x.shape
+    if x.dim() == 2:  # one x for every problem
+        E, (M, K), x_stride = codes.shape[0], x.shape, 0
+    else:
+        E, M, K = x.shape
+        x_stride = M * K
     N = codes.shape[1]
     if codes.shape[0] != E or codes.shape[2] * (32 // bits) != K:
         raise RuntimeError("codes must be (E, N, K*bits/32)")
@@ -218,7 +223,7 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
     nbytes = lib.glq_gemv_workspace_bytes(E, M, K, N, rank if xu is None else 0)
     ws = workspace(x.device, nbytes)
     rc = lib.glq_gemv_lora_batched(
-        E, x.data_ptr(), M * K, M, K, N, codes.data_ptr(), codes.shape[1] * codes.shape[2],
+        E, x.data_ptr(), x_stride, M, K, N, codes.data_ptr(), codes.shape[1] * codes.shape[2],
         bits, scales.data_ptr(), _lib.ptr(zeros), scales.shape[1] * scales.shape[2],
         groupsize, int(bool(sym)), _lib.ptr(U if xu is None else None), K * rank, _lib.ptr(SV),
         N * rank, rank, _lib.ptr(xu), M * rank, _lib.ptr(bias), N, out.data_ptr(), M * N,
