@@ -10,7 +10,8 @@ gate/up (:290-322), per-expert down(act(gate) * up) with its own low-rank term,
 and the sigmoid-gated shared expert (:429-433).
 
 Differences:
-* One C-ABI call (`glq_moe_decode`, four launches) for the whole step, with
+* One C-ABI call (`glq_moe_decode`, four launches, five when the x U jobs are
+  gated on routing) for the whole step, with
   routing kept on the device: no `.tolist()` host syncs (reference :410,454),
   no per-step weight concatenation (:509-510), and only the selected experts'
   weights are read (the reference's graph mode runs all E, :742-890).  Every
