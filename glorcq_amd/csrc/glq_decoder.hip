@@ -210,9 +210,10 @@ __global__ __launch_bounds__(kDecThreads) void decode_attention_kernel(AttnArgs 
   // Every load is unconditional (rows past n re-read row n - 1, the rows past
   // n in LDS are never read), so all 16 go out before the first wait.
   if (n > 0) {
-    f16x8 kb[8], vb[8];
+    constexpr int NJ = kAttnChunk * 16 / kDecThreads;  // 16-byte pieces per thread
+    f16x8 kb[NJ], vb[NJ];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int idx = j * kDecThreads + tid, r = min(idx >> 4, n - 1), c = idx & 15;
       kb[j] = ((const f16x8*)(a.k_cache + base))[r * 16 + c];
       vb[j] = ((const f16x8*)(a.v_cache + base))[r * 16 + c];
@@ -220,17 +221,17 @@ __global__ __launch_bounds__(kDecThreads) void decode_attention_kernel(AttnArgs 
     if (tid < rep * 16)
       ((f16x8*)qs)[tid] = ((const f16x8*)(a.q + ((int64_t)b * a.Hq + g * rep) * kHeadDim))[tid];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int idx = j * kDecThreads + tid, r = idx >> 4, c = idx & 15;
       *(f16x8*)(ks + r * kKStride + 8 * c) = kb[j];
       ((f16x8*)vs)[idx] = vb[j];
     }
   }
   __syncthreads();
-  // scores: position p = tid & 127, heads h = tid >> 7, + 2, + 4, ...
+  // scores: position p = tid % chunk, heads h = tid / chunk, + 256 / chunk, ...
   {
     const int p = tid & (kAttnChunk - 1);
-    for (int h = tid >> 7; h < rep; h += 2) {
+    for (int h = tid / kAttnChunk; h < rep; h += kDecThreads / kAttnChunk) {
       float s = -__builtin_inff();
       if (p < n) {
         float s0 = 0.f, s1 = 0.f;
