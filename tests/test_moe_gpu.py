@@ -175,12 +175,13 @@ def test_variants(gpu, kw):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,seed", [(1, 3), (3, 6), (16, 7)])
+@pytest.mark.parametrize("B,seed", [(1, 3), (3, 6), (16, 7), (64, 14)])
 def test_config4_block_gated_xu(gpu, B, seed, monkeypatch):
     """A Qwen3-30B-A3B-shaped block (128 experts, inter 768, top-8,
     norm_topk_prob, no shared expert) with 100 clusters: at B = 1 and 3 the
     clusters outnumber four times the picks, so the x U jobs run in their own
-    launch and skip unpicked clusters; at 16 they run beside the router.  LoRA
+    launch and skip unpicked clusters; at 16 and 64 (the 512 picks of a
+    prefill chunk, the step's maximum) they run beside the router.  LoRA
     scaled x30 (a skipped active cluster fails the bar); the forced other form
     gives the same bits."""
     p = lora_heavy(fmt.make_moe(H=2048, E=128, inter=768, top_k=8, n_clusters=100, rank=64,
