@@ -97,7 +97,7 @@ SIGNATURES = {
     "glq_qk_norm_rope": (_c_int, [
         _vp, _vp, _vp, _i64,            # q, k, v, tokens
         _i64, _i64, _i64,               # q_heads, kv_heads, head_dim
-        _i64, _i64,                     # q_stride, kv_stride
+        _i64, _i64, _i64,               # q_stride, q_item_rows, kv_stride
         _vp, _vp, ctypes.c_float,       # q_norm_w, k_norm_w, eps
         _vp, _vp, _i64,                 # cos, sin, cs_stride
         _vp, _vp, _vp, _i64,            # q_out, k_cache, v_cache, max_len

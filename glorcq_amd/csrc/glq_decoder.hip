@@ -107,6 +107,7 @@ __global__ __launch_bounds__(kDecThreads) void rmsnorm_kernel(
 struct QkArgs {
   const __half *q, *k, *v;  // rows of q_stride / kv_stride values per token
   int64_t q_stride, kv_stride;
+  int q_item;  // > 0: q item-major, [Hq*128 / q_item][B][q_item] (a batched GEMV's output)
   const __half *qw, *kw;
   const __half *cos, *sin;  // (B or 1, 128)
   int64_t cs_stride;        // 0 when one row serves every token
@@ -128,9 +129,12 @@ __global__ __launch_bounds__(kDecThreads) void qk_norm_rope_kernel(QkArgs a) {
   const bool in_cache = p >= 0 && p < a.max_len;
   const int kind = head < a.Hq ? 0 : (head < a.Hq + a.Hk ? 1 : 2);
   const int h = kind == 0 ? head : (kind == 1 ? head - a.Hq : head - a.Hq - a.Hk);
-  const __half* src = kind == 0 ? a.q + b * a.q_stride
-                                : (kind == 1 ? a.k : a.v) + b * a.kv_stride;
-  const f16x2 x = ((const f16x2*)(src + h * kHeadDim))[lane];
+  const int hc = h * kHeadDim;  // the head's first column
+  const __half* src =
+      kind != 0 ? (kind == 1 ? a.k : a.v) + b * a.kv_stride + hc
+      : a.q_item > 0 ? a.q + ((int64_t)(hc / a.q_item) * a.B + b) * a.q_item + hc % a.q_item
+                     : a.q + b * a.q_stride + hc;
+  const f16x2 x = ((const f16x2*)src)[lane];
   const int64_t crow = (((int64_t)b * a.Hk + h) * a.max_len + (in_cache ? p : 0)) * kHeadDim;
   if (kind == 2) {
     if (in_cache) ((f16x2*)(a.v_cache + crow))[lane] = x;
@@ -383,7 +387,8 @@ extern "C" int glq_rmsnorm(const void* x, const void* residual, const void* weig
 
 extern "C" int glq_qk_norm_rope(const void* q, const void* k, const void* v, int64_t tokens,
                                 int64_t q_heads, int64_t kv_heads, int64_t head_dim,
-                                int64_t q_stride, int64_t kv_stride, const void* q_norm_w,
+                                int64_t q_stride, int64_t q_item_rows, int64_t kv_stride,
+                                const void* q_norm_w,
                                 const void* k_norm_w, float eps, const void* cos, const void* sin,
                                 int64_t cs_stride, void* q_out, void* k_cache, void* v_cache,
                                 int64_t max_len, const int64_t* pos, int32_t* len_out,
@@ -399,6 +404,9 @@ extern "C" int glq_qk_norm_rope(const void* q, const void* k, const void* v, int
   GLQ_CHECK(q_stride >= q_heads * head_dim && kv_stride >= kv_heads * head_dim &&
                 q_stride % 2 == 0 && kv_stride % 2 == 0 && cs_stride % 2 == 0 && cs_stride >= 0,
             "row strides must cover the heads and be even");
+  GLQ_CHECK(q_item_rows >= 0 && q_item_rows % head_dim == 0 &&
+                (q_item_rows == 0 || (q_heads * head_dim) % q_item_rows == 0),
+            "q_item_rows must be 0 or a multiple of head_dim dividing q_heads * head_dim");
   if (tokens == 0) return GLQ_OK;
   GLQ_CHECK(q && k && v && q_norm_w && k_norm_w && cos && sin && q_out && k_cache && v_cache &&
                 pos && len_out,
@@ -409,7 +417,7 @@ extern "C" int glq_qk_norm_rope(const void* q, const void* k, const void* v, int
             "tensor arguments must be 4-byte aligned (pos 8-byte)");
   QkArgs a;
   a.q = (const __half*)q; a.k = (const __half*)k; a.v = (const __half*)v;
-  a.q_stride = q_stride; a.kv_stride = kv_stride;
+  a.q_stride = q_stride; a.kv_stride = kv_stride; a.q_item = (int)q_item_rows;
   a.qw = (const __half*)q_norm_w; a.kw = (const __half*)k_norm_w;
   a.cos = (const __half*)cos; a.sin = (const __half*)sin; a.cs_stride = cs_stride;
   a.q_out = (__half*)q_out; a.k_cache = (__half*)k_cache; a.v_cache = (__half*)v_cache;

@@ -80,11 +80,12 @@ class GLoRCQQwen3Attention(nn.Module):
             self._U_qkv = torch.stack(Us).contiguous()
             for i, m in enumerate(lins):
                 m.U = self._U_qkv[i]  # the same values, now views of the stack
-        # One decode token: q, k and v as ONE batched GEMV launch (plus its
-        # x U partials) over items of kv_out rows -- q's rows as q_out/kv_out
-        # items, then k, then v -- with the three layers' codes, scales,
-        # zero-points and SV laid end to end (the layers keep views of them)
-        # and each item's U (q's repeated per q item).
+        # Decode tokens (up to 16): q, k and v as ONE batched GEMV launch
+        # (plus its x U partials) over items of kv_out rows -- q's rows as
+        # q_out/kv_out items, then k, then v -- with the three layers' codes,
+        # scales, zero-points and SV laid end to end (the layers keep views of
+        # them) and each item's U (q's repeated per q item); q comes out
+        # item-major, which the norm/rotary kernel reads as it is.
         self._qkv = None
         q, k, v = lins
         nkv = k.out_features
@@ -115,14 +116,13 @@ class GLoRCQQwen3Attention(nn.Module):
                               past_key_values=past_key_values, **kwargs)
         inner = self.inner
         x = hidden_states.reshape(B, H)
-        if self._qkv is not None and B == 1:
+        if self._qkv is not None and B <= kernels.GEMV_MAX_M:
             c = self._qkv
             y = kernels.packed_dequant_matmul_batched(
                 x.contiguous(), c["codes"], c["scales"], c["zeros"], inner.q_proj.pack_bits,
-                inner.q_proj.gptq_groupsize, U=c["U"], SV=c["SV"]).reshape(1, -1)
-            nq = inner.q_proj.out_features
-            nkv = inner.k_proj.out_features
-            q, k, v = y[:, :nq], y[:, nq:nq + nkv], y[:, nq + nkv:]
+                inner.q_proj.gptq_groupsize, U=c["U"], SV=c["SV"])  # (items, B, kv rows)
+            n = y.shape[0] - 2
+            q, k, v = y[:n], y[n], y[n + 1]  # q item-major: the norm/rotary kernel reads it so
         elif self._U_qkv is not None and B <= kernels.GEMV_MAX_M:
             xu = kernels.lowrank_xu(x.contiguous(), self._U_qkv)  # (3, B, r)
             q = inner.q_proj(x, precomputed_xU=xu[0])

@@ -551,10 +551,12 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_w: to
                  k_norm_w: torch.Tensor, eps: float, cos: torch.Tensor, sin: torch.Tensor,
                  k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor,
                  len_out: torch.Tensor, q_out: torch.Tensor | None = None) -> torch.Tensor:
-    """One decode token per row: q (T, Hq*128), k and v (T, Hk*128) fp16 ->
-    q' (T, Hq, 128) returned; k' and v written into the static caches
-    (T, Hk, max_len, 128) at position pos (device int64 scalar); pos + 1 into
-    len_out (device int32) for decode_attention.  cos/sin: (T or 1, 128)."""
+    """One decode token per row: q (T, Hq*128) -- or item-major (n, T, R), a
+    batched GEMV's output over R-row slices of the q projection -- k and v
+    (T, Hk*128) fp16 -> q' (T, Hq, 128) returned; k' and v written into the
+    static caches (T, Hk, max_len, 128) at position pos (device int64
+    scalar); pos + 1 into len_out (device int32) for decode_attention.
+    cos/sin: (T or 1, 128)."""
     lib = _lib.load()
     for t, n in ((q, "q"), (k, "k"), (v, "v"), (q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w"),
                  (cos, "cos"), (sin, "sin"), (k_cache, "k_cache"), (v_cache, "v_cache")):
@@ -564,9 +566,17 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_w: to
     T, Hk, max_len, hd = k_cache.shape
     if v_cache.shape != k_cache.shape:
         raise RuntimeError("k_cache and v_cache differ in shape")
-    Hq = q.shape[-1] // hd
-    q2, k2, v2 = q.reshape(-1, q.shape[-1]), k.reshape(-1, k.shape[-1]), v.reshape(-1, v.shape[-1])
-    if q2.shape[0] != T or k2.shape != (T, Hk * hd) or v2.shape != (T, Hk * hd):
+    item_rows = 0
+    if q.dim() == 3 and q.shape[1] == T and q.shape[0] > 1:  # item-major
+        item_rows = q.shape[2]
+        Hq = q.shape[0] * item_rows // hd
+        q2 = q
+    else:
+        Hq = q.shape[-1] // hd
+        q2 = q.reshape(-1, q.shape[-1])
+    k2, v2 = k.reshape(-1, k.shape[-1]), v.reshape(-1, v.shape[-1])
+    if (not item_rows and q2.shape[0] != T) or k2.shape != (T, Hk * hd) or \
+            v2.shape != (T, Hk * hd):
         raise RuntimeError("q, k, v rows must match the cache's batch and heads")
     c2, s2 = cos.reshape(-1, hd), sin.reshape(-1, hd)
     if c2.shape[0] not in (1, T) or s2.shape != c2.shape:
@@ -574,7 +584,8 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_w: to
     if q_out is None:
         q_out = torch.empty(T, Hq, hd, dtype=torch.float16, device=q.device)
     _lib.check(lib.glq_qk_norm_rope(
-        q2.data_ptr(), k2.data_ptr(), v2.data_ptr(), T, Hq, Hk, hd, q2.shape[1], k2.shape[1],
+        q2.data_ptr(), k2.data_ptr(), v2.data_ptr(), T, Hq, Hk, hd,
+        Hq * hd if item_rows else q2.shape[1], item_rows, k2.shape[1],
         q_norm_w.data_ptr(), k_norm_w.data_ptr(), float(eps), c2.data_ptr(), s2.data_ptr(),
         hd if c2.shape[0] > 1 else 0, q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
         max_len, pos.data_ptr(), len_out.data_ptr(), _lib.stream_handle(q.device)),

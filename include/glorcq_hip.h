@@ -333,11 +333,15 @@ int glq_rmsnorm(const void* x, const void* residual, const void* weight, int64_t
  * 128); k' and v (unchanged) to the static caches (tokens, kv_heads, max_len,
  * 128) at position *pos (device int64; out-of-range positions write
  * nothing), and *pos + 1 to *len_out (device int32) for
- * glq_decode_attention.  q, k, v rows are q_stride / kv_stride values apart.
+ * glq_decode_attention.  q, k, v rows are q_stride / kv_stride values apart;
+ * with q_item_rows > 0, q is instead item-major (q_heads * 128 / q_item_rows,
+ * tokens, q_item_rows) -- the output of a batched GEMV whose items are
+ * q_item_rows-row slices of the q projection.
  */
 int glq_qk_norm_rope(const void* q, const void* k, const void* v, int64_t tokens,
                      int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t q_stride,
-                     int64_t kv_stride, const void* q_norm_w, const void* k_norm_w, float eps,
+                     int64_t q_item_rows, int64_t kv_stride, const void* q_norm_w,
+                     const void* k_norm_w, float eps,
                      const void* cos, const void* sin, int64_t cs_stride, void* q_out,
                      void* k_cache, void* v_cache, int64_t max_len, const int64_t* pos,
                      int32_t* len_out, void* stream);

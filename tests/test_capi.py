@@ -98,13 +98,15 @@ def test_decoder_entry_points_check_arguments(lib):
     assert b"aligned" in lib.glq_last_error()
     assert lib.glq_rmsnorm(p, p, p, 4, 2048, 1e-6, p, nul, nul) == 1  # residual_out missing
     assert lib.glq_rmsnorm(nul, nul, nul, 0, 2048, 1e-6, nul, nul, nul) == 0
-    args = [p, p, p, 1, 32, 4, 128, 4096, 512, p, p, 1e-6, p, p, 0, p, p, p, 640, p, p, nul]
+    args = [p, p, p, 1, 32, 4, 128, 4096, 0, 512, p, p, 1e-6, p, p, 0, p, p, p, 640, p, p, nul]
     bad = list(args); bad[6] = 64                       # head_dim
     assert lib.glq_qk_norm_rope(*bad) == 1 and b"head_dim" in lib.glq_last_error()
     bad = list(args); bad[5] = 5                        # 32 % 5
     assert lib.glq_qk_norm_rope(*bad) == 1
     bad = list(args); bad[7] = 2048                     # q_stride < heads * 128
     assert lib.glq_qk_norm_rope(*bad) == 1
+    bad = list(args); bad[8] = 384                      # item rows not dividing 4096
+    assert lib.glq_qk_norm_rope(*bad) == 1 and b"q_item_rows" in lib.glq_last_error()
     bad = list(args); bad[3] = 0
     assert lib.glq_qk_norm_rope(*bad) == 0
     n = lib.glq_decode_attention_workspace_bytes(2, 32, 4, 640)

@@ -94,7 +94,13 @@ def test_qk_norm_rope_matches_framework(gpu, B, pos, shared_rows):
         rq = qn(q.view(B, 1, Hq, hd)).transpose(1, 2)
         rk = kn(k.view(B, 1, Hk, hd)).transpose(1, 2)
         rq, rk = apply_rotary_pos_emb(rq, rk, cos, sin)
+        # q item-major (a batched GEMV's output over 512-row slices): same bits
+        kc2, vc2 = torch.zeros_like(kc), torch.zeros_like(vc)
+        q_im = q.view(B, Hq * hd // 512, 512).transpose(0, 1).contiguous()
+        qo2 = kernels.qk_norm_rope(q_im, k, v, qn.weight, kn.weight, 1e-6, cos, sin, kc2, vc2, p,
+                                   ln)
     torch.cuda.synchronize()
+    assert torch.equal(qo2, qo) and torch.equal(kc2, kc) and torch.equal(vc2, vc)
     assert int(ln) == pos + 1
     eps = torch.finfo(torch.float16).eps
     for got, ref, nrm in ((qo, rq[:, :, 0], qn(q.view(B, Hq, hd))),
