@@ -173,13 +173,15 @@ def _rand_qmat(g, E, N, K, bits, group) -> QMat:
 
 def make_moe(H=2048, E=60, inter=1408, top_k=4, n_clusters=16, rank=64, shared_inter=5632,
              B=1, bits=2, shared_bits=4, group=128, norm_topk_prob=False,
-             seed=0) -> MoEProblem:
+             seed=0, balanced_clusters=False) -> MoEProblem:
     """Seeded MoE block in a fixed draw order (one CPU generator):
     router W (E,H) N(0,0.02); shared-expert gate w (1,H) N(0,0.02); then for
     proj in (gate, up, down): cluster assignment randint(0, C, (E,)), U (C,K,r)
     N(0,0.01), expert weights (codes, scales, zeros as in make_linear), SV
     (E,N,r) N(0,0.01); then the shared expert's gate, up, down weights
     (shared_bits, no LoRA; skipped when shared_inter = 0); then h (B,H) N(0,1).  All fp32 draws rounded to fp16.
+    balanced_clusters: the cluster assignment is randperm(E) % C instead (clusters
+    of E/C experts each).
     Defaults are BASELINE config 2 (Qwen1.5-MoE-A2.7B)."""
     g = torch.Generator().manual_seed(seed)
     router_w = (torch.randn(E, H, generator=g) * 0.02).half()
@@ -188,7 +190,10 @@ def make_moe(H=2048, E=60, inter=1408, top_k=4, n_clusters=16, rank=64, shared_i
     experts, SV, cluster_of, U = {}, {}, {}, {}
     for proj in PROJS:
         K, N = dims[proj]
-        cluster_of[proj] = torch.randint(0, n_clusters, (E,), generator=g)
+        if balanced_clusters:
+            cluster_of[proj] = torch.randperm(E, generator=g) % n_clusters
+        else:
+            cluster_of[proj] = torch.randint(0, n_clusters, (E,), generator=g)
         U[proj] = (torch.randn(n_clusters, K, rank, generator=g) * 0.01).half()
         experts[proj] = _rand_qmat(g, E, N, K, bits, group)
         SV[proj] = (torch.randn(E, N, rank, generator=g) * 0.01).half()
@@ -201,6 +206,17 @@ def make_moe(H=2048, E=60, inter=1408, top_k=4, n_clusters=16, rank=64, shared_i
                       rank=rank, n_clusters=n_clusters, router_w=router_w,
                       shared_gate_w=shared_gate_w, experts=experts, SV=SV,
                       cluster_of=cluster_of, U=U, shared=shared, h=h)
+
+
+def make_mixtral_layer(B=1, seed=0, **kw) -> MoEProblem:
+    """a Mixtral-8x7B-shaped MoE layer -- hidden 4096, ffn
+    14336, 8 experts, top-2 with the weights renormalised (Mixtral's router),
+    SwiGLU experts with 2-bit g128 codes, rank-64 LoRA whose U is shared by 2
+    random clusters of 4 experts per projection, no shared expert."""
+    args = dict(H=4096, E=8, inter=14336, top_k=2, n_clusters=2, rank=64, shared_inter=0,
+                norm_topk_prob=True, balanced_clusters=True)
+    args.update(kw)
+    return make_moe(B=B, seed=seed, **args)
 
 
 def moe_step_bytes(p: MoEProblem, active_experts: int, active_clusters: dict) -> int:

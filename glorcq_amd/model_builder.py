@@ -7,7 +7,6 @@ sit on the hot path's data (same names and meaning):
   _dequant_intN, _unpack_int4        :69-80   LoRA factor storage
   _build_global_u_pool               :143-173 one U pool per projection type
   _install_global_u_pool             :176-183 pool shared by every MoE layer
-  _find_linear_modules               :435-444
   _load_lora_for_module              :465-544 U + SV (int4 / fp16 / intN / old V+S)
   is_regular_expert, is_shared_expert, extract_expert_info
                                      (utils/moe_utils.py:9-36)
@@ -31,7 +30,6 @@ from __future__ import annotations
 import os
 
 import torch
-import torch.nn as nn
 
 from . import _lib
 from .hadamard_rotation import generate_rht_signs
@@ -39,7 +37,7 @@ from .quantized_linear import GLoRCQLinear, RotationCache
 
 __all__ = [
     "SharedUCache", "RotationCache", "_dequant_intN", "_unpack_int4", "_build_global_u_pool",
-    "build_u_pool_stacks", "_install_global_u_pool", "_find_linear_modules",
+    "build_u_pool_stacks", "_install_global_u_pool",
     "_load_lora_for_module", "build_assignment_lookup", "load_glorcq_checkpoint",
     "build_glorcq_layers", "is_regular_expert", "is_shared_expert", "extract_expert_info",
 ]
@@ -229,18 +227,6 @@ def _install_global_u_pool(model, u_cache):
             m.set_global_pool(stacks, id_maps)
             n += 1
     return n
-
-
-def _find_linear_modules(module, prefix=""):
-    """{name: (parent, attr, module)} of every nn.Linear below `module`."""
-    result = {}
-    for name, child in module.named_children():
-        full = f"{prefix}.{name}" if prefix else name
-        if isinstance(child, nn.Linear):
-            result[full] = (module, name, child)
-        else:
-            result.update(_find_linear_modules(child, full))
-    return result
 
 
 def build_assignment_lookup(assignments):
