@@ -50,6 +50,14 @@ SIGNATURES = {
         _vp, _vp,                       # bias, y
         _vp, _i64, _vp,                 # workspace, bytes, stream
     ]),
+    "glq_gemv_noalloc_max_scratch_bytes": (_i64, []),
+    "glq_gemv_lora_noalloc": (_c_int, [
+        _vp, _i64, _i64, _i64,          # x, M, K, N
+        _vp, _c_int, _vp, _vp,          # codes, bits, scales, zeros
+        _i64, _c_int,                   # group, sym
+        _vp, _vp, _i64, _vp,            # U, SV, rank, xU
+        _vp, _vp, _vp,                  # bias, y, stream
+    ]),
     "glq_gemv_lora_batched": (_c_int, [
         _i64, _vp, _i64,                # items, x, x_stride
         _i64, _i64, _i64,               # M, K, N

@@ -14,6 +14,8 @@
 
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "glq_stream.h"
 
 namespace glq {
@@ -463,11 +465,70 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   return launch_dense<4, 4>(a, lds, s);
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free form: the x*U partials live in a file-scope device array
+// (one copy per GPU, held until the process ends) instead of a caller's
+// workspace.  Host code never passes the array's name to a kernel: its
+// device address is looked up once per device with hipGetSymbolAddress and
+// kept here.
+// ---------------------------------------------------------------------------
+constexpr int64_t kScratchBytes = 4ll << 20;  // 4 MiB per GPU
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::once_flag g_scratch_once[kMaxDevices];
+static hipError_t g_scratch_rc[kMaxDevices];
+
+// Device address of `scratch` on the current device (looked up on the first
+// call for that device).
+static int scratch_ptr(void** out) {
+  int dev = -1;
+  GLQ_HIP(hipGetDevice(&dev));
+  GLQ_CHECK(dev >= 0 && dev < kMaxDevices, "device %d out of range", dev);
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_rc[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_rc[dev] == hipSuccess ? p : nullptr;
+  });
+  if (g_scratch_rc[dev] != hipSuccess || g_scratch_ptr[dev] == nullptr) {
+    set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+              hipGetErrorString(g_scratch_rc[dev]));
+    return GLQ_ERR_HIP;
+  }
+  *out = g_scratch_ptr[dev];
+  return GLQ_OK;
+}
+
 }  // namespace glq
 
 using namespace glq;
 
 extern "C" {
+
+int64_t glq_gemv_noalloc_max_scratch_bytes(void) { return kScratchBytes; }
+
+int glq_gemv_lora_noalloc(const void* x, int64_t M, int64_t K, int64_t N,
+                          const int32_t* codes, int bits, const void* scales,
+                          const void* zeros, int64_t group, int sym, const void* U,
+                          const void* SV, int64_t rank, const void* xU, const void* bias,
+                          void* y, void* stream) {
+  clear_error();
+  GLQ_CHECK(M >= 0 && K >= 0 && N >= 0 && rank >= 0, "negative size");
+  const bool partials = SV != nullptr && rank > 0 && xU == nullptr && M > 0 && N > 0;
+  const int64_t need = partials ? workspace_need(1, M, K, rank) : 0;
+  GLQ_CHECK(need <= kScratchBytes,
+            "x*U partials need %lld bytes, above the %lld-byte static scratch of the "
+            "allocation-free entry point (use glq_gemv_lora with a workspace)",
+            (long long)need, (long long)kScratchBytes);
+  void* ws = nullptr;
+  if (partials) {
+    int rc = scratch_ptr(&ws);
+    if (rc) return rc;
+  }
+  return gemv_impl(1, x, 0, M, K, N, codes, 0, bits, scales, zeros, 0, group, sym,
+                   U, 0, SV, 0, rank, xU, 0, bias, 0, y, 0, ws, need, stream);
+}
 
 int64_t glq_gemv_workspace_bytes(int64_t items, int64_t M, int64_t K, int64_t N,
                                  int64_t rank) {

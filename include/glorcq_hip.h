@@ -84,6 +84,26 @@ int glq_gemv_lora(const void* x, int64_t M, int64_t K, int64_t N,
                   int64_t workspace_bytes, void* stream);
 
 /*
+ * Allocation-free form of glq_gemv_lora.  It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory or pass a
+ * workspace (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments and results as glq_gemv_lora,
+ * without the workspace: the x*U partials go to a static per-GPU scratch
+ * array of glq_gemv_noalloc_max_scratch_bytes() bytes (4 MiB) inside the
+ * library, so calls needing more (glq_gemv_workspace_bytes(1, M, K, N, rank)
+ * when U is used) fail with GLQ_ERR_INVALID.  Every call on one GPU shares
+ * that GPU's scratch: calls that may overlap on one GPU (different streams,
+ * or different host threads) race and must be ordered by the caller.  The
+ * partials are fully rewritten by each call, so nothing needs clearing.
+ */
+int64_t glq_gemv_noalloc_max_scratch_bytes(void);
+int glq_gemv_lora_noalloc(const void* x, int64_t M, int64_t K, int64_t N,
+                          const int32_t* codes, int bits, const void* scales,
+                          const void* zeros, int64_t group, int sym, const void* U,
+                          const void* SV, int64_t rank, const void* xU,
+                          const void* bias, void* y, void* stream);
+
+/*
  * Batched form: `items` independent problems of one shape in ONE launch, item
  * i reading codes + i*codes_stride (int32 elements), scales/zeros + i*sz_stride,
  * U + i*u_stride, SV + i*sv_stride, bias + i*bias_stride, x + i*x_stride,
