@@ -95,6 +95,26 @@ def packed_dequant_matmul_fused(x: torch.Tensor, codes: torch.Tensor, scales: to
                                 out: torch.Tensor | None = None) -> torch.Tensor:
     """y = dequant(codes) x + (x U) SV^T + bias, fp16 (M, N).
 
+    Without `out` this is the operator glorcq_hip::packed_dequant_matmul
+    (torch.library, with a fake kernel, so torch.compile traces it without a
+    graph break); with `out` (a caller's buffer, e.g. under graph capture) the
+    library is called directly.  Arguments as _packed_dequant_matmul_eager."""
+    if out is None:
+        return torch.ops.glorcq_hip.packed_dequant_matmul(
+            x, codes, scales, zeros, bits, groupsize, bool(sym), U, SV, precomputed_xU, bias)
+    return _packed_dequant_matmul_eager(x, codes, scales, zeros, bits, groupsize, sym, U, SV,
+                                        precomputed_xU, bias, out)
+
+
+def _packed_dequant_matmul_eager(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
+                                 zeros: torch.Tensor | None, bits: int, groupsize: int,
+                                 sym: bool = False, U: torch.Tensor | None = None,
+                                 SV: torch.Tensor | None = None,
+                                 precomputed_xU: torch.Tensor | None = None,
+                                 bias: torch.Tensor | None = None,
+                                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = dequant(codes) x + (x U) SV^T + bias, fp16 (M, N).
+
     M <= 16: the streaming GEMV (glq_gemv_lora); M > 16 with group 128: the
     MFMA GEMM (glq_gemm_lora); other groups: the GEMV per 16-row block.
 
@@ -117,14 +137,18 @@ def packed_dequant_matmul_fused(x: torch.Tensor, codes: torch.Tensor, scales: to
     N = codes.shape[0]
     if codes.shape[1] * (32 // bits) != K:
         raise RuntimeError(f"codes shape {tuple(codes.shape)} does not match K={K} at {bits} bits")
+    if groupsize <= 0 or K % groupsize:
+        raise RuntimeError(f"groupsize {groupsize} must divide K={K}")
     if scales.shape != (N, K // groupsize):
         raise RuntimeError(f"scales shape {tuple(scales.shape)} != ({N}, {K // groupsize})")
+    if not sym and zeros.shape != scales.shape:
+        raise RuntimeError(f"zeros shape {tuple(zeros.shape)} != ({N}, {K // groupsize})")
     rank = 0
     if SV is not None:
         _require(SV, "SV", torch.float16)
-        rank = SV.shape[1]
-        if SV.shape[0] != N:
+        if SV.dim() != 2 or SV.shape[0] != N:
             raise RuntimeError("SV must be (N, r)")
+        rank = SV.shape[1]
         if precomputed_xU is not None:
             _require(precomputed_xU, "precomputed_xU", torch.float16)
             if precomputed_xU.shape != (M, rank):
@@ -137,6 +161,8 @@ def packed_dequant_matmul_fused(x: torch.Tensor, codes: torch.Tensor, scales: to
                 raise RuntimeError("U must be (K, r)")
     if bias is not None:
         _require(bias, "bias", torch.float16)
+        if tuple(bias.shape) != (N,):
+            raise RuntimeError(f"bias must be ({N},)")
     if out is None:
         out = torch.empty(M, N, dtype=torch.float16, device=x.device)
     else:
@@ -198,25 +224,46 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
     else:
         E, M, K = x.shape
         x_stride = M * K
+    if codes.dim() != 3:
+        raise RuntimeError("codes must be (E, N, K*bits/32)")
     N = codes.shape[1]
     if codes.shape[0] != E or codes.shape[2] * (32 // bits) != K:
         raise RuntimeError("codes must be (E, N, K*bits/32)")
     if M > GEMV_MAX_M:
         raise RuntimeError(f"batched GEMV takes M <= {GEMV_MAX_M}")
+    if groupsize <= 0 or K % groupsize:
+        raise RuntimeError(f"groupsize {groupsize} must divide K={K}")
+    G = K // groupsize
+    if tuple(scales.shape) != (E, N, G):
+        raise RuntimeError(f"scales must be ({E}, {N}, {G})")
+    if not sym and tuple(zeros.shape) != (E, N, G):
+        raise RuntimeError(f"zeros must be ({E}, {N}, {G})")
     rank = 0
     if SV is not None:
         _require(SV, "SV", torch.float16)
+        if SV.dim() != 3 or tuple(SV.shape[:2]) != (E, N):
+            raise RuntimeError(f"SV must be ({E}, {N}, r)")
         rank = SV.shape[2]
         if precomputed_xU is not None:
             _require(precomputed_xU, "precomputed_xU", torch.float16)
             if tuple(precomputed_xU.shape) != (E, M, rank):
                 raise RuntimeError("precomputed_xU must be (E, M, r)")
         else:
+            if U is None:
+                raise RuntimeError("LoRA needs U or precomputed_xU")
             _require(U, "U", torch.float16)
+            if tuple(U.shape) != (E, K, rank):
+                raise RuntimeError(f"U must be ({E}, {K}, {rank})")
     if bias is not None:
         _require(bias, "bias", torch.float16)
+        if tuple(bias.shape) != (E, N):
+            raise RuntimeError(f"bias must be ({E}, {N})")
     if out is None:
         out = torch.empty(E, M, N, dtype=torch.float16, device=x.device)
+    else:
+        _require(out, "out", torch.float16)
+        if tuple(out.shape) != (E, M, N):
+            raise RuntimeError(f"out must be ({E}, {M}, {N})")
     if E == 0 or M == 0 or N == 0:
         return out
     xu = precomputed_xU if SV is not None else None
@@ -233,6 +280,15 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
 
 
 def lowrank_xu(x: torch.Tensor, U: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """a = fp16(x U): the operator glorcq_hip::lowrank_xu without `out`, else
+    the library directly (see _lowrank_xu_eager)."""
+    if out is None:
+        return torch.ops.glorcq_hip.lowrank_xu(x, U)
+    return _lowrank_xu_eager(x, U, out)
+
+
+def _lowrank_xu_eager(x: torch.Tensor, U: torch.Tensor,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
     """a = fp16(x U) on the GPU (fp32 accumulation): x (M, K) or (E, M, K) fp16,
     U (K, r) or (E, K, r) fp16 -> (M, r) or (E, M, r).  A 2-D x with a 3-D U
     applies the one x to every U (the cluster-shared x*U of the MoE block,
@@ -371,6 +427,18 @@ def turbo_gemv(x_rot: torch.Tensor, packed: torch.Tensor, norms: torch.Tensor,
                centroids: torch.Tensor, xU: torch.Tensor | None = None,
                SV: torch.Tensor | None = None, bias: torch.Tensor | None = None,
                out: torch.Tensor | None = None) -> torch.Tensor:
+    """The codebook matmul: the operator glorcq_hip::turbo_dequant_matmul
+    without `out`, else the library directly (see _turbo_gemv_eager)."""
+    if out is None:
+        return torch.ops.glorcq_hip.turbo_dequant_matmul(x_rot, packed, norms, centroids, xU,
+                                                         SV, bias)
+    return _turbo_gemv_eager(x_rot, packed, norms, centroids, xU, SV, bias, out)
+
+
+def _turbo_gemv_eager(x_rot: torch.Tensor, packed: torch.Tensor, norms: torch.Tensor,
+                      centroids: torch.Tensor, xU: torch.Tensor | None = None,
+                      SV: torch.Tensor | None = None, bias: torch.Tensor | None = None,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
     """y = fp16(norms[n] * sum_k C[q(n,k)] x_rot[m,k] + (xU SV^T)[m,n] + bias[n]).
 
     Single problem: x_rot (M, K) fp16, packed (N, K/4) uint8 or (N, K/16)
@@ -429,6 +497,14 @@ def turbo_gemv(x_rot: torch.Tensor, packed: torch.Tensor, norms: torch.Tensor,
 
 def rht(x: torch.Tensor, signs: torch.Tensor, inverse: bool = False,
         out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Randomized Hadamard transform: the operator glorcq_hip::rht (see
+    _rht_eager)."""
+    od = out_dtype or x.dtype
+    return torch.ops.glorcq_hip.rht(x, signs, bool(inverse), od == torch.float32)
+
+
+def _rht_eager(x: torch.Tensor, signs: torch.Tensor, inverse: bool = False,
+               out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """Randomized Hadamard transform of the rows of x (..., d), d a power of
     two: (1/sqrt(d)) H diag(signs) x, or diag(signs) (1/sqrt(d)) H x when
     inverse.  fp16 or fp32 in and out (out_dtype defaults to x's), fp32

@@ -66,7 +66,6 @@ class GraphCompatibleMoeBlock(nn.Module):
         # alone, the contract of transformers 5 sparse-MoE blocks
         self.return_router_logits = True
         self.t = stacked  # device tensors (kept alive for the kernels)
-        self._ws: dict = {}
 
     # ---- construction ----
     @staticmethod
@@ -195,61 +194,35 @@ class GraphCompatibleMoeBlock(nn.Module):
                 t[f"uslot_{proj}"] = slot
 
     # ---- the step ----
-    def _params(self, h, out, logits) -> _lib.MoeParams:
+    def _op_args(self):
+        """The block's tensors as the list arguments of the glorcq_hip MoE ops."""
         t = self.t
-        P = _lib.MoeParams()
-        P.tokens, P.hidden, P.experts, P.inter = h.shape[0], self.hidden, self.num_experts, \
-            self.inter
-        P.top_k, P.n_clusters, P.rank = self.top_k, self.n_clusters, self.rank
-        P.shared_inter = self.shared_inter
-        P.norm_topk_prob = int(self.norm_topk_prob)
-        P.bits, P.shared_bits, P.group = self.bits, self.shared_bits or 4, self.group
-        P.h, P.router_w = h.data_ptr(), t["router_w"].data_ptr()
-        P.shared_gate_w = _lib.ptr(t["shared_gate_w"])
-        for i, proj in enumerate(PROJS):
-            P.codes[i] = t[f"codes_{proj}"].data_ptr()
-            P.scales[i] = t[f"scales_{proj}"].data_ptr()
-            P.zeros[i] = t[f"zeros_{proj}"].data_ptr()
-            if self.rank > 0:
-                P.U[i] = t[f"U_{proj}"].data_ptr()
-                P.cluster_of[i] = t[f"cluster_{proj}"].data_ptr()
-                P.SV[i] = t[f"SV_{proj}"].data_ptr()
-                P.u_rows[i] = t.get(f"urows_{proj}", 0)
-                if i < 2:
-                    P.u_slot[i] = _lib.ptr(t.get(f"uslot_{proj}"))
-            if self.shared_inter > 0:
-                P.shared_codes[i] = t[f"scodes_{proj}"].data_ptr()
-                P.shared_scales[i] = t[f"sscales_{proj}"].data_ptr()
-                P.shared_zeros[i] = t[f"szeros_{proj}"].data_ptr()
-        P.out = out.data_ptr()
-        P.router_logits = _lib.ptr(logits)
-        return P
+        lora = self.rank > 0
+        codes = [t[f"codes_{p}"] for p in PROJS]
+        scales = [t[f"scales_{p}"] for p in PROJS]
+        zeros = [t[f"zeros_{p}"] for p in PROJS]
+        U = [t[f"U_{p}"] for p in PROJS] if lora else []
+        cl = [t[f"cluster_{p}"] for p in PROJS] if lora else []
+        SV = [t[f"SV_{p}"] for p in PROJS] if lora else []
+        u_slot = [t.get(f"uslot_{p}") for p in ("gate", "up")] if lora else []
+        u_rows = [int(t.get(f"urows_{p}", 0)) for p in PROJS] if lora else []
+        shared = self.shared_inter > 0
+        sc = [t[f"scodes_{p}"] for p in PROJS] if shared else []
+        ss = [t[f"sscales_{p}"] for p in PROJS] if shared else []
+        sz = [t[f"szeros_{p}"] for p in PROJS] if shared else []
+        return codes, scales, zeros, U, cl, SV, u_slot, u_rows, sc, ss, sz
 
-    def _workspace(self, lib, P) -> torch.Tensor:
-        B = P.tokens
-        ws = self._ws.get(B)
-        if ws is None:
-            n = lib.glq_moe_workspace_bytes(ctypes.byref(P))
-            if n < 0:
-                _lib.check(1, "glq_moe_workspace_bytes")
-            # zero-filled once: its router arrival counter starts at zero and
-            # every step leaves it zero
-            ws = torch.zeros(max(int(n), 256), dtype=torch.uint8,
-                             device=self.t["router_w"].device)
-            self._ws[B] = ws
-        return ws
-
-    MAX_TOKENS = 64  # tokens per glq_moe_decode call
+    MAX_TOKENS = 64  # tokens per decode step (glq_moe_decode)
 
     def forward(self, hidden_states: torch.Tensor, residual: torch.Tensor | None = None):
         """(final (b, s, H) fp16, router_logits (b*s, E) fp16), as the
         reference's forward (moe_block.py:381-436); final alone when
-        return_router_logits is False.  Tokens are independent in the block,
-        so more than 64 (a prefill) run as consecutive 64-token steps.
+        return_router_logits is False.  Up to 64 tokens run as one decode step
+        (glorcq_hip::moe_decode); more (a prefill) run through
+        glorcq_hip::moe_prefill.
         residual (the shape of hidden_states, fp16): final becomes
         fp16(residual + fp16(block output)), the decoder layer's residual add,
         inside the step's last launch."""
-        lib = _lib.load()
         shape = hidden_states.shape
         h = hidden_states.reshape(-1, self.hidden)
         if h.dtype != torch.float16:
@@ -262,16 +235,18 @@ class GraphCompatibleMoeBlock(nn.Module):
             if residual.shape != hidden_states.shape or residual.dtype != torch.float16:
                 raise RuntimeError("residual must match hidden_states (fp16)")
             res = residual.reshape(-1, self.hidden).contiguous()
-        out = torch.empty_like(h)
-        logits = torch.empty(h.shape[0], self.num_experts, dtype=torch.float16, device=h.device)
-        stream = _lib.stream_handle(h.device)
-        for t0 in range(0, h.shape[0], self.MAX_TOKENS):
-            t1 = min(h.shape[0], t0 + self.MAX_TOKENS)
-            P = self._params(h[t0:t1], out[t0:t1], logits[t0:t1])
-            P.residual = _lib.ptr(None if res is None else res[t0:t1])
-            ws = self._workspace(lib, P)
-            rc = lib.glq_moe_decode(ctypes.byref(P), ws.data_ptr(), ws.numel(), stream)
-            _lib.check(rc, "glq_moe_decode")
+        t = self.t
+        codes, scales, zeros, U, cl, SV, u_slot, u_rows, sc, ss, sz = self._op_args()
+        if h.shape[0] <= self.MAX_TOKENS:
+            out, logits = torch.ops.glorcq_hip.moe_decode(
+                h, t["router_w"], t["shared_gate_w"], codes, scales, zeros, U, cl, SV, u_slot,
+                u_rows, sc, ss, sz, res, self.inter, self.top_k, self.norm_topk_prob, self.rank,
+                self.n_clusters, self.bits, self.shared_bits, self.shared_inter)
+        else:
+            out, logits = torch.ops.glorcq_hip.moe_prefill(
+                h, t["router_w"], t["shared_gate_w"], codes, scales, zeros, U, cl, SV, u_slot,
+                u_rows, sc, ss, sz, res, self.inter, self.top_k, self.norm_topk_prob, self.rank,
+                self.n_clusters, self.bits, self.shared_bits, self.shared_inter)
         out = out.reshape(shape)
         return (out, logits) if self.return_router_logits else out
 
@@ -279,3 +254,97 @@ class GraphCompatibleMoeBlock(nn.Module):
         return (f"experts={self.num_experts}, top_k={self.top_k}, hidden={self.hidden}, "
                 f"inter={self.inter}, bits={self.bits}, rank={self.rank}, "
                 f"clusters={self.n_clusters}, shared_inter={self.shared_inter}")
+
+
+# ---------------------------------------------------------------------------
+# Real kernels of the glorcq_hip MoE operators (glorcq_amd/ops.py)
+# ---------------------------------------------------------------------------
+# decode workspaces: (device index, stream handle, tokens) -> zero-filled
+# uint8 tensor.  Each step leaves the router's arrival counter zero again and
+# steps on one stream run in order, so every block of a model shares them.
+_moe_ws: dict = {}
+
+
+def _moe_params(h, router_w, shared_gate_w, codes, scales, zeros, U, cluster_of, SV, u_slot,
+                u_rows, shared_codes, shared_scales, shared_zeros, residual, out, logits,
+                inter, top_k, norm_topk_prob, rank, n_clusters, bits, shared_bits,
+                shared_inter) -> _lib.MoeParams:
+    P = _lib.MoeParams()
+    P.tokens, P.hidden, P.experts, P.inter = h.shape[0], h.shape[1], router_w.shape[0], inter
+    P.top_k, P.n_clusters, P.rank = top_k, n_clusters, rank
+    P.shared_inter = shared_inter
+    P.norm_topk_prob = int(bool(norm_topk_prob))
+    P.bits, P.shared_bits, P.group = bits, shared_bits or 4, 128
+    P.h, P.router_w = h.data_ptr(), router_w.data_ptr()
+    P.shared_gate_w = _lib.ptr(shared_gate_w)
+    if len(codes) != 3 or len(scales) != 3 or len(zeros) != 3:
+        raise RuntimeError("codes, scales and zeros hold (gate, up, down)")
+    for i in range(3):
+        P.codes[i] = codes[i].data_ptr()
+        P.scales[i] = scales[i].data_ptr()
+        P.zeros[i] = zeros[i].data_ptr()
+        if rank > 0:
+            P.U[i] = U[i].data_ptr()
+            P.cluster_of[i] = cluster_of[i].data_ptr()
+            P.SV[i] = SV[i].data_ptr()
+            P.u_rows[i] = u_rows[i] if u_rows else 0
+            if i < 2 and u_slot:
+                P.u_slot[i] = _lib.ptr(u_slot[i])
+        if shared_inter > 0:
+            P.shared_codes[i] = shared_codes[i].data_ptr()
+            P.shared_scales[i] = shared_scales[i].data_ptr()
+            P.shared_zeros[i] = shared_zeros[i].data_ptr()
+    P.out = out.data_ptr()
+    P.router_logits = _lib.ptr(logits)
+    P.residual = _lib.ptr(residual)
+    return P
+
+
+def moe_decode_launch(h, router_w, shared_gate_w, codes, scales, zeros, U, cluster_of, SV,
+                      u_slot, u_rows, shared_codes, shared_scales, shared_zeros, residual, inter,
+                      top_k, norm_topk_prob, rank, n_clusters, bits, shared_bits, shared_inter,
+                      out=None, logits=None):
+    """One glq_moe_decode step (<= 64 tokens) on torch's current stream."""
+    lib = _lib.load()
+    if h.dim() != 2 or h.dtype != torch.float16 or not h.is_contiguous():
+        raise RuntimeError("h must be contiguous fp16 (tokens, hidden)")
+    if out is None:
+        out = torch.empty_like(h)
+    if logits is None:
+        logits = torch.empty(h.shape[0], router_w.shape[0], dtype=torch.float16,
+                             device=h.device)
+    P = _moe_params(h, router_w, shared_gate_w, codes, scales, zeros, U, cluster_of, SV, u_slot,
+                    u_rows, shared_codes, shared_scales, shared_zeros, residual, out, logits,
+                    inter, top_k, norm_topk_prob, rank, n_clusters, bits, shared_bits,
+                    shared_inter)
+    n = lib.glq_moe_workspace_bytes(ctypes.byref(P))
+    if n < 0:
+        _lib.check(1, "glq_moe_workspace_bytes")
+    stream = _lib.stream_handle(h.device)
+    key = (h.device.index, stream, h.shape[0])
+    ws = _moe_ws.get(key)
+    if ws is None or ws.numel() < n:
+        # zero-filled once: the router's arrival counter starts at zero and
+        # every step leaves it zero
+        ws = torch.zeros(max(int(n), 256), dtype=torch.uint8, device=h.device)
+        _moe_ws[key] = ws
+    _lib.check(lib.glq_moe_decode(ctypes.byref(P), ws.data_ptr(), ws.numel(), stream),
+               "glq_moe_decode")
+    return out, logits
+
+
+def moe_prefill_launch(h, router_w, shared_gate_w, codes, scales, zeros, U, cluster_of, SV,
+                       u_slot, u_rows, shared_codes, shared_scales, shared_zeros, residual, inter,
+                       top_k, norm_topk_prob, rank, n_clusters, bits, shared_bits, shared_inter):
+    """A block over many tokens: consecutive 64-token decode steps."""
+    out = torch.empty_like(h)
+    logits = torch.empty(h.shape[0], router_w.shape[0], dtype=torch.float16, device=h.device)
+    step = GraphCompatibleMoeBlock.MAX_TOKENS
+    for t0 in range(0, h.shape[0], step):
+        t1 = min(h.shape[0], t0 + step)
+        moe_decode_launch(h[t0:t1], router_w, shared_gate_w, codes, scales, zeros, U, cluster_of,
+                          SV, u_slot, u_rows, shared_codes, shared_scales, shared_zeros,
+                          None if residual is None else residual[t0:t1], inter, top_k,
+                          norm_topk_prob, rank, n_clusters, bits, shared_bits, shared_inter,
+                          out=out[t0:t1], logits=logits[t0:t1])
+    return out, logits
