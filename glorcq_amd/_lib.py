@@ -98,6 +98,8 @@ SIGNATURES = {
     "glq_dequant_factor": (_c_int, [_vp, _c_int, _i64, _i64, _vp, _c_int, _c_int, _vp, _vp]),
     "glq_moe_workspace_bytes": (_i64, [ctypes.POINTER(MoeParams)]),
     "glq_moe_decode": (_c_int, [ctypes.POINTER(MoeParams), _vp, _i64, _vp]),
+    "glq_moe_prefill_workspace_bytes": (_i64, [ctypes.POINTER(MoeParams)]),
+    "glq_moe_prefill": (_c_int, [ctypes.POINTER(MoeParams), _vp, _i64, _vp]),
     "glq_unpack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _c_int, _vp, _vp]),
     "glq_dequant_weight": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp, _i64, _c_int, _vp, _vp]),
     "glq_pack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp]),

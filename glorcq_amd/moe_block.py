@@ -66,6 +66,11 @@ class GraphCompatibleMoeBlock(nn.Module):
         # alone, the contract of transformers 5 sparse-MoE blocks
         self.return_router_logits = True
         self.t = stacked  # device tensors (kept alive for the kernels)
+        # the prefill kernels take integer zero-points (GPTQ's are); checked
+        # once here, otherwise a prefill runs as consecutive decode steps
+        self.zeros_integral = all(
+            bool(torch.equal(stacked[f"zeros_{p}"], stacked[f"zeros_{p}"].round()))
+            for p in PROJS)
 
     # ---- construction ----
     @staticmethod
@@ -246,7 +251,8 @@ class GraphCompatibleMoeBlock(nn.Module):
             out, logits = torch.ops.glorcq_hip.moe_prefill(
                 h, t["router_w"], t["shared_gate_w"], codes, scales, zeros, U, cl, SV, u_slot,
                 u_rows, sc, ss, sz, res, self.inter, self.top_k, self.norm_topk_prob, self.rank,
-                self.n_clusters, self.bits, self.shared_bits, self.shared_inter)
+                self.n_clusters, self.bits, self.shared_bits, self.shared_inter,
+                self.zeros_integral)
         out = out.reshape(shape)
         return (out, logits) if self.return_router_logits else out
 
@@ -335,16 +341,35 @@ def moe_decode_launch(h, router_w, shared_gate_w, codes, scales, zeros, U, clust
 
 def moe_prefill_launch(h, router_w, shared_gate_w, codes, scales, zeros, U, cluster_of, SV,
                        u_slot, u_rows, shared_codes, shared_scales, shared_zeros, residual, inter,
-                       top_k, norm_topk_prob, rank, n_clusters, bits, shared_bits, shared_inter):
-    """A block over many tokens: consecutive 64-token decode steps."""
+                       top_k, norm_topk_prob, rank, n_clusters, bits, shared_bits, shared_inter,
+                       zeros_integral=True):
+    """A block over many tokens: glq_moe_prefill (grouped GEMMs over each
+    expert's gathered tokens); blocks whose routed zero-points are not all
+    integers run consecutive 64-token decode steps instead."""
     out = torch.empty_like(h)
     logits = torch.empty(h.shape[0], router_w.shape[0], dtype=torch.float16, device=h.device)
-    step = GraphCompatibleMoeBlock.MAX_TOKENS
-    for t0 in range(0, h.shape[0], step):
-        t1 = min(h.shape[0], t0 + step)
-        moe_decode_launch(h[t0:t1], router_w, shared_gate_w, codes, scales, zeros, U, cluster_of,
-                          SV, u_slot, u_rows, shared_codes, shared_scales, shared_zeros,
-                          None if residual is None else residual[t0:t1], inter, top_k,
-                          norm_topk_prob, rank, n_clusters, bits, shared_bits, shared_inter,
-                          out=out[t0:t1], logits=logits[t0:t1])
+    if not zeros_integral:
+        step = GraphCompatibleMoeBlock.MAX_TOKENS
+        for t0 in range(0, h.shape[0], step):
+            t1 = min(h.shape[0], t0 + step)
+            moe_decode_launch(h[t0:t1], router_w, shared_gate_w, codes, scales, zeros, U,
+                              cluster_of, SV, u_slot, u_rows, shared_codes, shared_scales,
+                              shared_zeros, None if residual is None else residual[t0:t1], inter,
+                              top_k, norm_topk_prob, rank, n_clusters, bits, shared_bits,
+                              shared_inter, out=out[t0:t1], logits=logits[t0:t1])
+        return out, logits
+    lib = _lib.load()
+    if h.dim() != 2 or h.dtype != torch.float16 or not h.is_contiguous():
+        raise RuntimeError("h must be contiguous fp16 (tokens, hidden)")
+    P = _moe_params(h, router_w, shared_gate_w, codes, scales, zeros, U, cluster_of, SV, u_slot,
+                    u_rows, shared_codes, shared_scales, shared_zeros, residual, out, logits,
+                    inter, top_k, norm_topk_prob, rank, n_clusters, bits, shared_bits,
+                    shared_inter)
+    n = lib.glq_moe_prefill_workspace_bytes(ctypes.byref(P))
+    if n < 0:
+        _lib.check(1, "glq_moe_prefill_workspace_bytes")
+    from .kernels import workspace
+    ws = workspace(h.device, max(int(n), 256))
+    _lib.check(lib.glq_moe_prefill(ctypes.byref(P), ws.data_ptr(), ws.numel(),
+                                   _lib.stream_handle(h.device)), "glq_moe_prefill")
     return out, logits

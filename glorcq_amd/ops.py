@@ -155,18 +155,18 @@ def moe_prefill(h: Tensor, router_w: Tensor, shared_gate_w: Optional[Tensor],
                 shared_scales: List[Tensor], shared_zeros: List[Tensor],
                 residual: Optional[Tensor], inter: int, top_k: int, norm_topk_prob: bool,
                 rank: int, n_clusters: int, bits: int, shared_bits: int,
-                shared_inter: int) -> List[Tensor]:
+                shared_inter: int, zeros_integral: bool) -> List[Tensor]:
     from .moe_block import moe_prefill_launch
     return list(moe_prefill_launch(h, router_w, shared_gate_w, codes, scales, zeros, U,
                                    cluster_of, SV, u_slot, u_rows, shared_codes, shared_scales,
                                    shared_zeros, residual, inter, top_k, norm_topk_prob, rank,
-                                   n_clusters, bits, shared_bits, shared_inter))
+                                   n_clusters, bits, shared_bits, shared_inter, zeros_integral))
 
 
 @moe_prefill.register_fake
 def _(h, router_w, shared_gate_w, codes, scales, zeros, U, cluster_of, SV, u_slot, u_rows,
       shared_codes, shared_scales, shared_zeros, residual, inter, top_k, norm_topk_prob, rank,
-      n_clusters, bits, shared_bits, shared_inter):
+      n_clusters, bits, shared_bits, shared_inter, zeros_integral):
     if h.dim() != 2 or h.shape[1] != router_w.shape[1]:
         _fail("h must be (tokens, hidden) with hidden = router_w's columns")
     return [torch.empty_like(h), h.new_empty((h.shape[0], router_w.shape[0]))]

@@ -146,10 +146,12 @@ int glq_lowrank_xu_batched(int64_t items, const void* x, int64_t x_stride, int64
  * + bias with the same arguments and results as glq_gemv_lora.  Replaces the
  * reference's gptq_dequant_gemm_kernel path (inference/kernels/gptq_matmul.cu:
  * 111-213, taken for B > 4) and the LoRA tail of GLoRCQLinear.forward
- * (inference/quantized_linear.py:338-349).  Group 128.  Codes decode into fp16
- * operands of v_mfma_f32_16x16x32_f16 (64-token x 64-row tiles, fp32
- * accumulation); a = fp16(x U) comes from xU or from the low-rank launches of
- * glq_lowrank_xu_batched into the workspace (glq_gemm_workspace_bytes).
+ * (inference/quantized_linear.py:338-349).  Group 128.  Codes decode into
+ * exact fp16 operands (q - zero-point's integer part) of
+ * v_mfma_f32_16x16x32_f16, each group's fp32 sum scaled once (any zero-point,
+ * symmetric or not); a = fp16(x U) comes from xU or from a low-rank launch.
+ * The workspace (glq_gemm_workspace_bytes, 256-byte aligned) is required; it
+ * needs no initialisation.
  */
 int64_t glq_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t rank);
 int glq_gemm_lora(const void* x, int64_t M, int64_t K, int64_t N,
@@ -292,6 +294,23 @@ int64_t glq_moe_workspace_bytes(const glq_moe_params* p);
  */
 int glq_moe_decode(const glq_moe_params* p, void* workspace, int64_t workspace_bytes,
                    void* stream);
+
+/*
+ * One MoE block over many tokens (a prompt): the reference's _forward_sparse
+ * (inference/moe_block.py:704-740) -- every active expert's SwiGLU
+ * projections on its gathered tokens -- with the same params as
+ * glq_moe_decode and the decode step's routing and combine arithmetic.
+ * tokens up to 2^20; routed codes must use integer zero-points (GPTQ
+ * zero-points are integers; run glq_moe_decode steps otherwise).  Launches:
+ * router (+ x in the GEMMs' decode order), dispatch (pairs sorted by expert,
+ * token tiles), the low-rank a = x U per pair, the grouped gate/up GEMM with
+ * SwiGLU, the low-rank a of the down input, the grouped down GEMM, the
+ * shared expert's two GEMMs, the combine.  The workspace (256-byte aligned,
+ * glq_moe_prefill_workspace_bytes) needs no initialisation.
+ */
+int64_t glq_moe_prefill_workspace_bytes(const glq_moe_params* p);
+int glq_moe_prefill(const glq_moe_params* p, void* workspace, int64_t workspace_bytes,
+                    void* stream);
 
 /*
  * Debug: unpack codes (N, K*bits/32) int32 -> (N, K) int32.  Codes are

@@ -18,10 +18,10 @@ from test_gemv_gpu import assert_parity, oracle_y, to
 
 def test_gemm_workspace_sizes():
     lib = _lib.load()
-    n0 = lib.glq_gemm_workspace_bytes(512, 2048, 1408, 0)  # split-K partial tiles only
-    n = lib.glq_gemm_workspace_bytes(512, 2048, 1408, 64)  # + the x U partials
-    assert n0 >= 512 * 1408 * 4 and n0 % 256 == 0
-    assert n >= n0 + 512 * 64 * 4 and n % 256 == 0
+    n0 = lib.glq_gemm_workspace_bytes(512, 2048, 1408, 0)  # x in decode order + split-K tiles
+    n = lib.glq_gemm_workspace_bytes(512, 2048, 1408, 64)  # + a = x U
+    assert n0 >= 512 * 2048 * 2 and n0 % 256 == 0
+    assert n >= n0 + 512 * 64 * 2 and n % 256 == 0
     assert lib.glq_gemm_workspace_bytes(0, 2048, 1408, 64) == 0
     # argument errors come back before any launch
     rc = lib.glq_gemm_lora(None, 64, 2048, 64, None, 2, None, None, 64, 0, None, None, 0, None,
@@ -110,9 +110,10 @@ def test_gemm_matches_gemv_blocks(gpu):
     (1024, 200, 40, 2, 192),    # rank above the in-launch x U limit: low-rank launches
 ])
 def test_split_k_variants(gpu, monkeypatch, ks, K, N, M, bits, rank):
-    """K splits forced (GLQ_GEMM_KS; capped at the chunk count): partial tiles
-    and x U partials summed by gemm_reduce_kernel, against the oracle."""
-    monkeypatch.setenv("GLQ_GEMM_KS", str(ks))
+    """K splits forced (GLQ_PF_KS; capped at the group count): each tile's
+    last-arriving split sums the partial tiles in split order and runs the
+    epilogue; rank 192 takes the low-rank entry point first."""
+    monkeypatch.setenv("GLQ_PF_KS", str(ks))
     p = fmt.make_linear(K, N, bits=bits, group=128, rank=rank, M=M, seed=K + N + ks)
     d = to(p, gpu)
     bias = (torch.randn(N, generator=torch.Generator().manual_seed(ks)) * 0.1).half()
@@ -125,19 +126,35 @@ def test_split_k_variants(gpu, monkeypatch, ks, K, N, M, bits, rank):
     assert torch.equal(y, y2)  # fixed summation order: the same bits every call
 
 
-@pytest.mark.gpu
-def test_no_workspace_single_split(gpu):
-    """Without a workspace (a = x U given) the launch is one split with the
-    epilogue in the tile workgroups; same result within the bar."""
+def test_gemm_requires_workspace():
+    """The prefill path keeps x in decode order in the workspace: a missing or
+    short workspace is an argument error, raised before any launch."""
     lib = _lib.load()
-    p = fmt.make_linear(2048, 320, bits=2, rank=64, M=80, seed=51)
+    fake = 1 << 20  # never dereferenced: the checks run first
+    args = [fake, 80, 2048, 320, fake, 2, fake, fake, 128, 0, None, fake, 64, fake, None, fake]
+    assert lib.glq_gemm_lora(*args, None, 0, None) == 1
+    assert b"workspace" in lib.glq_last_error()
+    need = lib.glq_gemm_workspace_bytes(80, 2048, 320, 0)
+    assert lib.glq_gemm_lora(*args, fake, need - 256, None) == 1
+    assert b"workspace" in lib.glq_last_error()
+
+
+@pytest.mark.gpu
+def test_config1_down_m512(gpu):
+    """The config-1 down projection (1408 -> 2048) at the prefill size M=512."""
+    p = fmt.make_linear(1408, 2048, bits=2, group=128, rank=64, M=512, seed=1408 + 512)
     d = to(p, gpu)
-    xu = (p.x.float() @ p.U.float()).half().to(gpu)
-    y = torch.empty(80, 320, dtype=torch.float16, device=gpu)
-    rc = lib.glq_gemm_lora(d["x"].data_ptr(), 80, 2048, 320, d["codes"].data_ptr(), 2,
-                           d["scales"].data_ptr(), d["zeros"].data_ptr(), 128, 0, None,
-                           d["SV"].data_ptr(), 64, xu.data_ptr(), None, y.data_ptr(), None, 0,
-                           _lib.stream_handle(gpu))
-    _lib.check(rc, "glq_gemm_lora")
-    torch.cuda.synchronize()
-    assert_parity(y, oracle_y(p, xu=xu.cpu()), "one split, no workspace")
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], 2, 128,
+                                       U=d["U"], SV=d["SV"])
+    assert_parity(y, oracle_y(p), "expert down 2b M=512")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bits", [2, 4])
+def test_large_prefill_tiles(gpu, bits):
+    """M = 1024 over K = 4096 (128-token tiles for 2-bit, one K split)."""
+    p = fmt.make_linear(4096, 1024, bits=bits, group=128, rank=64, M=1024, seed=77 + bits)
+    d = to(p, gpu)
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], bits, 128,
+                                       U=d["U"], SV=d["SV"])
+    assert_parity(y, oracle_y(p), f"M=1024 K=4096 b={bits}")
