@@ -4,18 +4,21 @@ Metric: 2-bit dequant-GEMV+LoRA HBM GB/s (% of peak).
 
 Workload (config 1's 2-bit expert projection, K=2048 -> N=1408, group 128,
 rank 64, M=1): a cold-cache pool of POOL distinct layers (own codes, scales,
-zeros, U, SV, x, y each; 512 x 1.26 MB = 645 MB, above the 256 MB Infinity
-Cache and the L2s).  One step = the fused op over the whole pool, i.e. one
-call of the batched entry point: launch 1 computes the x*U partial sums,
-launch 2 streams the packed codes, dequantizes in registers, runs the MFMA
-GEMV and adds the low-rank term a*SV^T in its epilogue.
+zeros, U, SV, x, y each; 2048 x 1.26 MB = 2.58 GB, ten times the 256 MB
+Infinity Cache, so no layer's data survives until the next step reads it, as
+in a model's decode step).  One step = the fused op over the whole pool, i.e. one
+call of the batched entry point, which is ONE launch (gemv_lane_kernel with
+the x*U form): each workgroup forms a = fp16(x*U) for its layer, then streams
+the packed codes, dequantizes in registers (v_dot2 against x) and adds the
+low-rank term a*SV^T per row.
   value = POOL * algorithmic_bytes / step time, algorithmic bytes per layer =
   N*K*b/8 + 4*N*G + 2*r*(K+N) + 2*M*(K+N) = 1,260,288 B.
 
-roofline: the dominant kernel (the GEMV, launch 2) timed alone with HIP events
-on the launch stream, fed the same layers' a = x*U precomputed by the library;
-its algorithmic bytes per layer = N*K*b/8 + 4*N*G + 2*r*N + 2*M*(K+N) + 2*M*r
-(codes, scales+zeros, SV, x, y, a) = 998,272 B.
+roofline: that one kernel, timed with HIP events on the launch stream, over
+the same algorithmic bytes.  Beside it, the same GEMV fed a = x*U precomputed
+by the library (the separate-launch form; bytes per layer N*K*b/8 + 4*N*G +
+2*r*N + 2*M*(K+N) + 2*M*r = 998,272 B), whose output must agree with the
+step's to the fp32 summation order of a.
 
 Also reported: the MoE block decode step of config 2 at B = 1, 4, 16, 32
 (microseconds per step and per token under hipGraph replay, achieved GB/s on
@@ -43,7 +46,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "2b dequant-GEMV+LoRA HBM GB/s (% of peak); MoE-block decode µs/token"
 HBM_PEAK_GBS = 8000.0
-POOL = 512
+POOL = 2048
 K_, N_, BITS, GROUP, RANK, M_ = 2048, 1408, 2, 128, 64, 1
 
 
@@ -143,8 +146,8 @@ def read_traffic():
 
 
 def pmc_workload():
-    """What the traffic profile runs: 5 launches of the GEMV kernel over the
-    pool (a given), then 5 plain device copies of 512 MiB."""
+    """What the traffic profile runs: 5 launches of the fused kernel over the
+    pool (the bench step), then 5 plain device copies of 512 MiB."""
     import torch
 
     from glorcq_amd import kernels
@@ -152,10 +155,9 @@ def pmc_workload():
     dev = torch.device("cuda:0")
     codes, scales, zeros, U, SV, x = make_pool(dev, POOL)
     out = torch.empty(POOL, M_, N_, dtype=torch.float16, device=dev)
-    xu = kernels.lowrank_xu(x, U)
     for _ in range(5):
-        kernels.packed_dequant_matmul_batched(x, codes, scales, zeros, BITS, GROUP, SV=SV, out=out,
-                                              precomputed_xU=xu)
+        kernels.packed_dequant_matmul_batched(x, codes, scales, zeros, BITS, GROUP, U=U, SV=SV,
+                                              out=out)
     src = torch.empty(512 << 20, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     for _ in range(5):
@@ -435,7 +437,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--pool", type=int, default=POOL)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--pmc-workload", action="store_true")
@@ -481,7 +483,7 @@ def main():
         kernels.packed_dequant_matmul_batched(x, codes, scales, zeros, BITS, GROUP, U=U, SV=SV,
                                               out=out)
 
-    log("timing steps (x*U partials + GEMV over the pool)")
+    log("timing steps (one fused launch over the pool)")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -492,7 +494,13 @@ def main():
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     gbs = layer_bytes() * args.pool / (ms * 1e-3) / 1e9
 
-    # dominant kernel alone, HIP events on the launch stream
+    # the step's one kernel, HIP events on the launch stream
+    log("timing the fused kernel with HIP events")
+    k_ms = time_events(step, args.steps, args.warmup)
+    k_bytes = layer_bytes() * args.pool
+    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
+
+    # the GEMV fed a precomputed a = x*U (the separate-launch form)
     xu = kernels.lowrank_xu(x, U)
     out2 = torch.empty_like(out)
 
@@ -500,11 +508,11 @@ def main():
         kernels.packed_dequant_matmul_batched(x, codes, scales, zeros, BITS, GROUP, SV=SV,
                                               out=out2, precomputed_xU=xu)
 
-    log("timing the GEMV kernel alone")
-    k_ms = time_events(gemv_only, args.steps, args.warmup)
-    k_bytes = gemv_kernel_bytes() * args.pool
-    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
-    same = bool(torch.equal(out, out2))
+    log("timing the GEMV with a precomputed a = x*U")
+    g_ms = time_events(gemv_only, args.steps, args.warmup)
+    g_bytes = gemv_kernel_bytes() * args.pool
+    diff = (out.float() - out2.float()).abs()
+    agree = bool((diff <= 1e-4 + 2e-3 * out2.float().abs()).all())
 
     # single-call latency, config 0 (one layer: both launches)
     p0 = fmt.make_linear(K_, N_, bits=BITS, group=GROUP, rank=RANK, M=M_, seed=0)
@@ -534,8 +542,8 @@ def main():
         "data": "synthetic (seeded random codes, scales, zeros, LoRA factors, activations)",
         "config": {
             "workload": (f"config 1 expert gate/up projection: {args.pool} distinct 2-bit "
-                         f"2048->1408 g128 r64 layers at M=1, cold cache, one fused op "
-                         f"(x*U partials + GEMV with low-rank epilogue) per step"),
+                         f"2048->1408 g128 r64 layers at M=1, cold cache, one fused launch "
+                         f"(a = x*U, dequant-GEMV, + a*SV^T) per step"),
             "K": K_, "N": N_, "bits": BITS, "group": GROUP, "rank": RANK, "M": M_,
             "layers_per_step": args.pool,
         },
@@ -543,12 +551,19 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
-            "kernel": "glq::gemv_lane_kernel<2,false,32,4,1,false>",
+            "kernel": "glq::gemv_lane_kernel<2,false,32,4,1,false,true>",
             "kernel_avg_us": round(k_ms * 1e3, 2),
             "algorithmic_bytes_per_launch": k_bytes,
         },
+        "gemv_with_precomputed_a": {
+            "kernel": "glq::gemv_lane_kernel<2,false,32,4,1,false,false>",
+            "kernel_avg_us": round(g_ms * 1e3, 2),
+            "achieved_gbs": round(g_bytes / (g_ms * 1e-3) / 1e9, 1),
+            "algorithmic_bytes_per_launch": g_bytes,
+            "matches_step_output": agree,
+            "max_abs_diff": float(diff.max()),
+        },
         "single_call_config0_us": round(single_ms * 1e3, 2),
-        "gemv_alone_matches_step_output": same,
     }
     log("prefill GEMM (config 1, M = 128 and 512)")
     result["prefill_gemm"] = bench_prefill(dev)

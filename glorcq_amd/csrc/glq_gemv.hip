@@ -319,45 +319,63 @@ static bool lane_shape(int64_t M, const TileShape& sh, int bits) {
   return M == 1 && sh.group == 128 && sh.rank <= 128 && (int64_t)sh.K * bits / 128 <= 64;
 }
 
+// Bytes of LDS the fused-x U form needs (partials of a, then a in fp16).
+static size_t lane_xu_lds(const LaneArgs& la) {
+  return (size_t)LaneXu(la.a.sh.rank).lds_bytes(la.a.sh.rank);
+}
+
 template <int BITS, bool SYM, int LRP, int NSV, bool HASB>
-static int launch_lane_k(const LaneArgs& la, hipStream_t s) {
+static int launch_lane_k(const LaneArgs& la, bool xu, hipStream_t s) {
   const int64_t waves = (int64_t)la.a.items * la.wpi;
-  const int64_t grid = (waves + 3) / 4;
-  GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
-  gemv_lane_kernel<BITS, SYM, LRP, kLanePD, NSV, HASB>
-      <<<dim3((unsigned)grid), dim3(256), 0, s>>>(la);
+  if (xu) {
+    const int64_t grid = waves / 8;  // wpi is a multiple of 8
+    GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
+    const size_t lds = lane_xu_lds(la);
+    static size_t attr = 64 * 1024;
+    int rc = set_lds_limit(gemv_lane_kernel<BITS, SYM, LRP, kLanePD, NSV, HASB, true>, lds, attr);
+    if (rc) return rc;
+    gemv_lane_kernel<BITS, SYM, LRP, kLanePD, NSV, HASB, true>
+        <<<dim3((unsigned)grid), dim3(512), lds, s>>>(la);
+  } else {
+    const int64_t grid = (waves + 3) / 4;
+    GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
+    gemv_lane_kernel<BITS, SYM, LRP, kLanePD, NSV, HASB, false>
+        <<<dim3((unsigned)grid), dim3(256), 0, s>>>(la);
+  }
   GLQ_LAUNCH_CHECK("gemv_lane_kernel");
   return GLQ_OK;
 }
 
 // SV dwords per lane: rank / 2 spread over the LRP lanes of a row.
 template <int BITS, bool SYM, int LRP, bool HASB>
-static int launch_lane_sv(const LaneArgs& la, hipStream_t s) {
+static int launch_lane_sv(const LaneArgs& la, bool xu, hipStream_t s) {
   const int nsv = (la.a.sh.rank / 2 + LRP - 1) / LRP;
-  if (nsv <= 1) return launch_lane_k<BITS, SYM, LRP, 1, HASB>(la, s);
+  if (nsv <= 1) return launch_lane_k<BITS, SYM, LRP, 1, HASB>(la, xu, s);
   if constexpr (LRP <= 32) {
-    if (nsv <= 2) return launch_lane_k<BITS, SYM, LRP, 2, HASB>(la, s);
+    if (nsv <= 2) return launch_lane_k<BITS, SYM, LRP, 2, HASB>(la, xu, s);
   }
-  if constexpr (LRP == 16) return launch_lane_k<BITS, SYM, LRP, 4, HASB>(la, s);
+  if constexpr (LRP == 16) return launch_lane_k<BITS, SYM, LRP, 4, HASB>(la, xu, s);
   GLQ_CHECK(false, "rank %d too large for the lane path", la.a.sh.rank);
 }
 
 template <int BITS, bool SYM, bool HASB>
-static int launch_lane_lrp(const LaneArgs& la, hipStream_t s) {
-  if (la.lr <= 16) return launch_lane_sv<BITS, SYM, 16, HASB>(la, s);
-  if (la.lr <= 32) return launch_lane_sv<BITS, SYM, 32, HASB>(la, s);
-  return launch_lane_sv<BITS, SYM, 64, HASB>(la, s);
+static int launch_lane_lrp(const LaneArgs& la, bool xu, hipStream_t s) {
+  if (la.lr <= 16) return launch_lane_sv<BITS, SYM, 16, HASB>(la, xu, s);
+  if (la.lr <= 32) return launch_lane_sv<BITS, SYM, 32, HASB>(la, xu, s);
+  return launch_lane_sv<BITS, SYM, 64, HASB>(la, xu, s);
 }
 
 template <int BITS>
-static int launch_lane_bits(const LaneArgs& la, hipStream_t s) {
+static int launch_lane_bits(const LaneArgs& la, bool xu, hipStream_t s) {
   const bool hb = la.a.bias != nullptr;
-  if (la.a.sh.sym) return hb ? launch_lane_lrp<BITS, true, true>(la, s)
-                             : launch_lane_lrp<BITS, true, false>(la, s);
-  return hb ? launch_lane_lrp<BITS, false, true>(la, s) : launch_lane_lrp<BITS, false, false>(la, s);
+  if (la.a.sh.sym) return hb ? launch_lane_lrp<BITS, true, true>(la, xu, s)
+                             : launch_lane_lrp<BITS, true, false>(la, xu, s);
+  return hb ? launch_lane_lrp<BITS, false, true>(la, xu, s)
+            : launch_lane_lrp<BITS, false, false>(la, xu, s);
 }
 
-static int launch_lane(const DenseArgs& a, int bits, hipStream_t s) {
+// xu: a = x U formed in the launch (8-wave workgroups, wpi a multiple of 8).
+static int launch_lane(const DenseArgs& a, int bits, bool xu, hipStream_t s) {
   LaneArgs la;
   la.a = a;
   la.lr = a.sh.K * bits / 128;
@@ -369,7 +387,11 @@ static int launch_lane(const DenseArgs& a, int bits, hipStream_t s) {
   if (const char* e = getenv("GLQ_LANE_RPW")) rpw = atoll(e) > 0 ? atoll(e) : rpw;
   la.rpw = (int)std::min<int64_t>(std::max<int64_t>(rpw, 1), la.rounds);
   la.wpi = (la.rounds + la.rpw - 1) / la.rpw;
-  return bits == 2 ? launch_lane_bits<2>(la, s) : launch_lane_bits<4>(la, s);
+  if (xu) {  // whole 8-wave workgroups per item, the rounds spread over all of them
+    la.wpi = (la.wpi + 7) / 8 * 8;
+    la.rpw = (la.rounds + la.wpi - 1) / la.wpi;
+  }
+  return bits == 2 ? launch_lane_bits<2>(la, xu, s) : launch_lane_bits<4>(la, xu, s);
 }
 
 static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
@@ -397,7 +419,10 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
                            (!lora || sv_stride % 8 == 0) && (!lora || !U || u_stride % 8 == 0)),
             "item strides must keep 16-byte alignment");
   const bool need_partials = lora && xU == nullptr;
-  const int64_t need = need_partials ? workspace_need(items, M, K, rank) : 0;
+  // one token row with U given: the lane kernel forms a = x U itself (one
+  // launch, no workspace); GLQ_LANE_NO_XU=1 keeps the separate partial-sum launch
+  const bool lane_xu = need_partials && lane_shape(M, sh, bits) && !getenv("GLQ_LANE_NO_XU");
+  const int64_t need = need_partials && !lane_xu ? workspace_need(items, M, K, rank) : 0;
   if (need > 0) {
     GLQ_CHECK(workspace != nullptr && workspace_bytes_given >= need,
               "workspace of %lld bytes needed (got %lld)", (long long)need,
@@ -424,15 +449,16 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   a.y_es = y_stride;
   a.xu = lora ? (const __half*)xU : nullptr;
   a.xu_es = xu_stride;
-  a.apart = need_partials ? (const float*)workspace : nullptr;
+  a.apart = need_partials && !lane_xu ? (const float*)workspace : nullptr;
   a.items = (int)items;
   a.M = (int)M;
-  a.P = need_partials ? (int)lowrank_slices(K) : 0;
+  a.P = need_partials && !lane_xu ? (int)lowrank_slices(K) : 0;
   a.tiles = (int)((N + 16 * T - 1) / (16 * T));
   a.sh = sh;
 
   GLQ_CHECK(items * a.tiles < (1ll << 31) && items * a.P < (1ll << 31), "too many workgroups");
   hipStream_t s = (hipStream_t)stream;
+  if (lane_xu) return launch_lane(a, bits, true, s);
   if (need_partials) {
     const dim3 grid((unsigned)(items * a.P));
     if (M == 1) lowrank_partial_kernel<1><<<grid, dim3(256), 0, s>>>(a);
@@ -440,7 +466,7 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
     else lowrank_partial_kernel<4><<<grid, dim3(256), 0, s>>>(a);
     GLQ_LAUNCH_CHECK("lowrank_partial_kernel");
   }
-  if (lane_shape(M, sh, bits)) return launch_lane(a, bits, s);
+  if (lane_shape(M, sh, bits)) return launch_lane(a, bits, false, s);
   DenseStreamArgs sa;
   size_t slds = 0;
   bool sz2 = false;

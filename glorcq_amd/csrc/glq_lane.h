@@ -108,6 +108,22 @@ __device__ __forceinline__ void decode4_words(uint32_t w, u32x4& a, const Decode
   a.w = (v & 0x00F000F0u) | k.e21;
 }
 
+// The x U phase of the lane kernel (XU): 512 threads, thread t owns column
+// block b = t % NB (8 rank columns, one 16-byte load per U row) and K slot
+// t / NB of KS = 512 / NB slots; slot s sums 8-row chunks s, s + KS, ...
+// Its fp32 partials go to LDS (KS x rank), are summed first over slots
+// s = seg (mod NSEG) by 512 threads (NSEG = 512 / rank segments per column),
+// then over the segments, both in a fixed order.
+struct LaneXu {
+  int nb, ks, nseg;
+  __host__ __device__ explicit LaneXu(int rank)
+      : nb(rank / 8), ks(512 / (rank / 8)), nseg(512 / rank) {}
+  // LDS bytes: slot partials, segment sums, a in fp16
+  __host__ __device__ int lds_bytes(int rank) const {
+    return ks * rank * 4 + nseg * rank * 4 + rank * 2;
+  }
+};
+
 // Work: the rows of an item are cut into 64-row units of NIT = LRP
 // iterations, taken in rounds of PD iterations; wave w of an item runs rounds
 // w rpw .. w rpw + rpw - 1 and stores each round's rows at the round's end.
@@ -115,23 +131,33 @@ __device__ __forceinline__ void decode4_words(uint32_t w, u32x4& a, const Decode
 // unconditionally (iterations past the wave's last one re-read its last row),
 // so the register ring needs no copies and the compiler's waits stay PD deep.
 // NSV: SV dwords per lane (rank <= 2 NSV LRP); HASB: a bias is added.
-template <int BITS, bool SYM, int LRP, int PD, int NSV, bool HASB>
-__global__ __launch_bounds__(256) void gemv_lane_kernel(LaneArgs la) {
+//
+// XU: the low-rank factor a = fp16(x U) is formed in the same launch, first:
+// each workgroup (8 waves, all of one item) reads the item's U with every
+// wave-wide load covering whole 128-byte U rows (layout in LaneXu), two
+// chunks of loads in flight per thread, v_dot2 over row pairs into fp32; the
+// partials are summed in LDS in a fixed order and rounded to fp16 once.
+// Then the waves take their x slices and stream their rows.  An item whose
+// rows are spread over several workgroups has each of them form a.
+template <int BITS, bool SYM, int LRP, int PD, int NSV, bool HASB, bool XU>
+__global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) {
   constexpr int C = lane_piece_codes<BITS>();  // codes per lane
   constexpr int RPI = 64 / LRP;                // rows per iteration
   constexpr int NIT = LRP;                     // iterations per 64-row unit
+  constexpr int WPB = XU ? 8 : 4;              // waves per workgroup
   static_assert(NIT % PD == 0, "ring depth must divide the unit");
   const DenseArgs& a = la.a;
   const DenseSrc src{a};
   const int lane = threadIdx.x & 63;
-  const int wv = blockIdx.x * 4 + (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wvb = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wv = blockIdx.x * WPB + wvb;
   const int item = wv / la.wpi;
-  if (item >= a.items) return;  // uniform over the wave
+  if (item >= a.items) return;  // uniform over the workgroup (XU: wpi is a multiple of 8)
   // rounds rb .. rb + nr - 1 of PD iterations each, [PD R, PD R + PD)
   const int rb = (wv - item * la.wpi) * la.rpw;
   const int nr = min(la.rpw, la.rounds - rb);
-  if (nr <= 0) return;
-  const int rlast = rb + nr - 1;
+  if (!XU && nr <= 0) return;  // (XU: every wave takes part in forming a)
+  const int rlast = min(rb + max(nr, 1), la.rounds) - 1;  // idle waves re-read a valid round
   const int N = a.sh.N, G = a.sh.G, kw = a.sh.kw, rank = a.sh.rank;
   const int ri = lane / LRP, p = lane % LRP;
   const bool act = p < la.lr;
@@ -141,7 +167,7 @@ __global__ __launch_bounds__(256) void gemv_lane_kernel(LaneArgs la) {
   // ---- x slice in operand order, c1 = sum bias * x, c2 = sum x ----
   uint32_t xw[C / 2];
   float c1 = 0.f, c2 = 0.f;
-  {
+  auto load_x = [&]() {
     const __half* xr = src.xrow(item, 0) + pc * C;
 #pragma unroll
     for (int blk = 0; blk < C / 16; ++blk) {
@@ -166,22 +192,14 @@ __global__ __launch_bounds__(256) void gemv_lane_kernel(LaneArgs la) {
         xw[8 * blk + j] = __builtin_bit_cast(uint32_t, pr);
       }
     }
-  }
-  // ---- a pairs of this lane's SV dwords (zero past the rank) ----
+  };
+  if constexpr (!XU) load_x();
   const bool lora = a.sv != nullptr && rank > 0;
-  uint32_t ap[NSV];
   int svo[NSV];  // element offset of the dword within an SV row
 #pragma unroll
   for (int k = 0; k < NSV; ++k) {
     const int j = p + k * LRP;  // dword j holds rank columns 2j, 2j + 1
-    const bool v = lora && 2 * j < rank;
-    svo[k] = v ? 2 * j : 0;
-    f16x2 pr = {(_Float16)0.f, (_Float16)0.f};
-    if (v) {
-      pr[0] = (_Float16)__half2float(src.load_a(item, 0, 2 * j));
-      pr[1] = (_Float16)__half2float(src.load_a(item, 0, 2 * j + 1));
-    }
-    ap[k] = __builtin_bit_cast(uint32_t, pr);
+    svo[k] = lora && 2 * j < rank ? 2 * j : 0;
   }
 
   // Buffer loads: one descriptor per tensor of the item (sized to it, so rows
@@ -225,11 +243,104 @@ __global__ __launch_bounds__(256) void gemv_lane_kernel(LaneArgs la) {
   // The prologue's loads go out in the loop's order (scheduling barriers on
   // both sides of every issue), so the wait the compiler places at the loop
   // head -- the tighter of the two entry states -- stays PD - 1 iterations deep.
+  auto prologue = [&]() {
 #pragma unroll
-  for (int d = 0; d < PD; ++d) {
-    __builtin_amdgcn_sched_barrier(0);
-    issue(d, 0);
-    __builtin_amdgcn_sched_barrier(0);
+    for (int d = 0; d < PD; ++d) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue(d, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  if constexpr (!XU) prologue();
+
+  // ---- a pairs of this lane's SV dwords (zero past the rank) ----
+  uint32_t ap[NSV];
+  if constexpr (XU) {
+    // a = fp16(x U) in this workgroup (layout in LaneXu)
+    extern __shared__ float xu_lds[];
+    const LaneXu L(rank);
+    const int t = threadIdx.x;
+    float* part = xu_lds;                      // (ks, rank)
+    float* segs = xu_lds + L.ks * rank;        // (nseg, rank)
+    __half* ah = (__half*)(segs + L.nseg * rank);
+    if (lora) {
+      const int b = t % L.nb, slot = t / L.nb;
+      if (slot < L.ks) {
+        const int nch = a.sh.K / 8;  // 8-row chunks
+        const __half* ub = a.u + (int64_t)item * a.u_es + 8 * b;
+        const __half* xr = src.xrow(item, 0);
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        u32x4 u0[8], u1[8], x0, x1;
+        auto load = [&](int c, u32x4 (&u)[8], u32x4& xv) {
+          c = min(c, nch - 1);  // past the end: re-read the last chunk (not used)
+          xv = *(const u32x4*)(xr + 8 * c);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) u[q] = *(const u32x4*)(ub + (int64_t)(8 * c + q) * rank);
+        };
+        auto fma_chunk = [&](const u32x4 (&u)[8], const u32x4& xv) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {  // rows 2i, 2i + 1 against (x_2i, x_2i+1)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint32_t lo = __builtin_amdgcn_perm(u[2 * i + 1][j], u[2 * i][j], 0x05040100u);
+              const uint32_t hi = __builtin_amdgcn_perm(u[2 * i + 1][j], u[2 * i][j], 0x07060302u);
+              acc[2 * j] = dot2(lo, xv[i], acc[2 * j]);
+              acc[2 * j + 1] = dot2(hi, xv[i], acc[2 * j + 1]);
+            }
+          }
+        };
+        // two chunks in flight: slot, slot + ks, ...; a slot at or past the
+        // last chunk adds nothing
+        load(slot, u0, x0);
+        for (int c = slot; c < nch; c += 2 * L.ks) {
+          load(c + L.ks, u1, x1);
+          fma_chunk(u0, x0);
+          if (c + L.ks >= nch) break;
+          load(c + 2 * L.ks, u0, x0);
+          fma_chunk(u1, x1);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) part[slot * rank + 8 * b + c] = acc[c];
+      }
+      __syncthreads();
+      const int col = t % rank, seg = t / rank;
+      if (seg < L.nseg) {  // level 1: slots seg, seg + nseg, ... in order
+        float sum = 0.f;
+        for (int q = seg; q < L.ks; q += L.nseg) sum += part[q * rank + col];
+        segs[seg * rank + col] = sum;
+      }
+      __syncthreads();
+      if (t < rank) {  // level 2: the segments in order
+        float sum = 0.f;
+        for (int q = 0; q < L.nseg; ++q) sum += segs[q * rank + t];
+        ah[t] = __float2half(sum);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < NSV; ++k) {
+      const int j = p + k * LRP;
+      f16x2 pr = {(_Float16)0.f, (_Float16)0.f};
+      if (lora && 2 * j < rank) {
+        pr[0] = (_Float16)__half2float(ah[2 * j]);
+        pr[1] = (_Float16)__half2float(ah[2 * j + 1]);
+      }
+      ap[k] = __builtin_bit_cast(uint32_t, pr);
+    }
+    if (nr <= 0) return;  // a wave with no rows of its own
+    load_x();
+    prologue();
+  } else {
+#pragma unroll
+    for (int k = 0; k < NSV; ++k) {
+      const int j = p + k * LRP;
+      f16x2 pr = {(_Float16)0.f, (_Float16)0.f};
+      if (lora && 2 * j < rank) {
+        pr[0] = (_Float16)__half2float(src.load_a(item, 0, 2 * j));
+        pr[1] = (_Float16)__half2float(src.load_a(item, 0, 2 * j + 1));
+      }
+      ap[k] = __builtin_bit_cast(uint32_t, pr);
+    }
   }
 
   const DecodeConsts dk = DecodeConsts::make();

@@ -819,7 +819,8 @@ int pf_dense_gemm(const void* x, int64_t M, int64_t K, int64_t N, const int32_t*
                   const void* SV, int64_t rank, const void* xU, const void* bias, void* y,
                   void* workspace, int64_t workspace_bytes, hipStream_t s) {
   const bool lora = SV != nullptr && rank > 0;
-  const PfDensePlan P = pf_dense_plan(M, K, N, lora ? rank : 0, bits);
+  // a = x U needs room only when it is formed here
+  const PfDensePlan P = pf_dense_plan(M, K, N, lora && xU == nullptr ? rank : 0, bits);
   GLQ_CHECK(workspace != nullptr && workspace_bytes >= P.total,
             "workspace of %lld bytes needed (got %lld)", (long long)P.total,
             (long long)workspace_bytes);

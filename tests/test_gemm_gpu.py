@@ -86,6 +86,28 @@ def test_precomputed_xu(gpu):
 
 
 @pytest.mark.gpu
+def test_precomputed_xu_exact_workspace(gpu):
+    """With a = x U given the workspace is the rank-0 size, exactly: the call
+    takes a buffer of glq_gemm_workspace_bytes(M, K, N, 0) bytes and no more."""
+    lib = _lib.load()
+    M, K, N = 512, 2048, 1408
+    p = fmt.make_linear(K, N, bits=2, rank=64, M=M, seed=44)
+    d = to(p, gpu)
+    xu = (p.x.float() @ p.U.float()).half()
+    xg = xu.to(gpu)
+    need = lib.glq_gemm_workspace_bytes(M, K, N, 0)
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    y = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    rc = lib.glq_gemm_lora(d["x"].data_ptr(), M, K, N, d["codes"].data_ptr(), 2,
+                           d["scales"].data_ptr(), d["zeros"].data_ptr(), 128, 0, None,
+                           d["SV"].data_ptr(), 64, xg.data_ptr(), None, y.data_ptr(),
+                           ws.data_ptr(), need, _lib.stream_handle(gpu))
+    _lib.check(rc, "glq_gemm_lora")
+    torch.cuda.synchronize()
+    assert_parity(y, oracle_y(p, xu=xu), "precomputed xU, exact workspace")
+
+
+@pytest.mark.gpu
 def test_gemm_matches_gemv_blocks(gpu):
     """The GEMM and the 16-row GEMV blocks compute the same function: both
     within the bar of the oracle, and close to each other."""

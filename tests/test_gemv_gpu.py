@@ -294,6 +294,8 @@ def test_ksplit_fallback_path(gpu, monkeypatch, K, N, M, bits):
     (2, 512, 130, 16, True, 48),       # 4 rows per step (16-lane groups), run past N
     (2, 4096, 448, 0, False, 8),       # 64 lanes per row at 2 bits, no low-rank term
     (2, 1024, 640, 128, False, None),  # 16-lane groups with 4 SV dwords per lane
+    (2, 2048, 512, 8, False, None),    # rank 8: one U column block, x U split over codes
+    (4, 1024, 300, 48, False, 8),      # rank 48 (6 column blocks), waves past the last round
 ])
 def test_lane_path_m1(gpu, monkeypatch, bits, K, N, rank, sym, ipw):
     """The one-token-row kernel (glq_lane.h) on the shapes it takes: live and
@@ -311,6 +313,14 @@ def test_lane_path_m1(gpu, monkeypatch, bits, K, N, rank, sym, ipw):
     y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], zeros, bits, 128,
                                        sym=sym, bias=bias.to(gpu), **kw)
     assert_parity(y, oracle_y(p, lora=rank > 0, bias=bias), f"lane K={K} N={N}")
+    if rank:  # a = x U formed in the launch vs by the separate partial-sum launch
+        monkeypatch.setenv("GLQ_LANE_NO_XU", "1")
+        y1 = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], zeros, bits, 128,
+                                            sym=sym, bias=bias.to(gpu), **kw)
+        monkeypatch.delenv("GLQ_LANE_NO_XU")
+        assert_parity(y1, oracle_y(p, bias=bias), "lane, separate x U launch")
+        # the two differ only in the fp32 summation order of a = x U
+        assert bool(((y.float() - y1.float()).abs() <= 1e-4 + 2e-3 * y1.float().abs()).all())
     xu = (p.x.double() @ p.U.double()).half()
     if rank:  # the precomputed a = x U hook
         y2 = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], zeros, bits, 128,
