@@ -1,12 +1,11 @@
 // Prefill entry point glq_gemm_lora: argument checks, then the grouped
 // dequant-to-fp16 MFMA GEMM of glq_prefill.hip in its dense form (one
 // "expert", token rows in order):
-//   launch 1  pf_lowrank_kernel   x in the code decode order, and a = fp16(x U)
-//                                 when U is given (rank <= 128; larger ranks
-//                                 take glq_lowrank_xu_batched first)
-//   launch 2  pf_gemm_kernel      y = fp16(x W_fp16^T + a SV^T + bias), K split
-//                                 over workgroups with the last split of each
-//                                 tile reducing in split order
+//   launch 1  pf_lowrank_kernel   a = fp16(x U), only when U is given (rank
+//   (+ finalize)                  <= 128; larger ranks take
+//                                 glq_lowrank_xu_batched first)
+//   launch 2  pf_gemm_kernel      y = fp16(x W^T + a SV^T + bias) over tiles
+//                                 sized to the problem, x read as given
 // Reference: gptq_dequant_gemm_kernel (inference/kernels/gptq_matmul.cu:
 // 111-213, used for B > 4) and the LoRA tail of GLoRCQLinear.forward
 // (inference/quantized_linear.py:338-349).

@@ -7,43 +7,44 @@
 // inference/moe_block.py:704-740: each active expert's projections on its
 // gathered tokens).
 //
-// pf_gemm_kernel<BITS, TM, RT, MODE, SYM>: a workgroup of 4 waves owns TM
-// token rows x (4 * 16 RT) weight rows (MODE gate/up: 4 * 8 RT row indices of
-// the gate AND the up matrix) and a range of K.
-//  * A (activations) reaches LDS by direct global->LDS loads, one 128-code
-//    group of TM rows per slot, two slots: the next group is in flight while
-//    the current one is consumed.  The rows are pre-permuted in global memory
-//    into the code decode order (glq_gemv_core.h perm_src) and gathered per
-//    row through an index list (the expert's tokens).  16-byte piece c of
-//    slot row r sits at c ^ (r % 16), so 16 lanes reading one piece of 16
-//    rows hit 16 distinct bank groups.
-//  * B (weights) never touch LDS: each wave loads its own rows' codes, scale
-//    and zero-point per group straight into VGPRs (one group ahead) and
-//    decodes them into exact fp16 MFMA operands q - zi (zi the zero-point's
-//    nearest integer): one v_and_or per code pair lands q under an exponent
-//    chosen per bit position (exactly 2^e + q), one packed fp16 add removes
-//    2^e + zi.  Each group's fp32 MFMA sum is scaled once,
+// pf_gemm_kernel<BITS, TM, RT, MODE, SYM, ZF, DEEP>: a workgroup of 4 waves
+// owns TM token rows x (4 * 16 RT) weight rows (MODE gate/up: 4 * 8 RT row
+// indices of the gate AND the up matrix) and a range of K.
+//  * Per 128-code group one LDS slot receives, by direct global->LDS loads,
+//    the TM rows of A (16-byte piece c of slot row r at c ^ (r % 16), so 16
+//    lanes reading one piece of 16 rows hit 16 distinct bank groups), each
+//    wave's codes, and its rows' scales and zero-points.  A ring of D slots
+//    keeps D - 1 groups in flight; each thread waits for its own loads of a
+//    group (vmcnt), one barrier makes them everyone's and frees the oldest
+//    slot for the next issue.  DEEP rings give half the CU's LDS to one
+//    workgroup (for small launches); others take 2 or 3 slots.
+//  * A: the dense form reads the caller's x in natural order and builds each
+//    MFMA operand in the decode's order with v_perm (pf_nat_a); the MoE forms
+//    read rows that their producers already wrote in decode order
+//    (glq_gemv_core.h perm_src), gathered through an index list.
+//  * B: codes decode into exact fp16 MFMA operands q - zi (zi the
+//    zero-point's nearest integer): one v_and_or per code pair lands q under
+//    an exponent chosen per bit position (exactly 2^e + q), one packed fp16
+//    add removes 2^e + zi.  Each group's fp32 MFMA sum is scaled once,
 //    y += s (acc - zf c2), zf = z - zi and c2 the group's sum of x (only for
-//    non-integer zero-points), so W = s (q - z) enters exactly, as in the
-//    reference's fp32 kernel.  Lane group kb of a wave holds code words 2kb,
-//    2kb+1 (2-bit) or 4kb..4kb+3 (4-bit) of a group, and k-step t of the group
-//    uses slice t of them; A piece 4kb + t of a row is the matching slice of x.
+//    non-integer zero-points: an MFMA of A against ones in the dense form),
+//    so W = s (q - z) enters exactly, as in the reference's fp32 kernel.
+//    Lane group kb of a wave holds code words 2kb, 2kb+1 (2-bit) or
+//    4kb..4kb+3 (4-bit) of a group; k-step t uses slice t of them.
 //  * v_mfma_f32_16x16x32_f16 with A = 16 token rows, B = 16 weight rows: each
-//    A piece read from LDS feeds RT MFMAs and each decoded B operand TM/16.
-//    Two workgroups per CU (2 waves per SIMD) let one wave's decode VALU run
-//    under the other's MFMAs.
-//  * Split K (ks > 1): each (tile, split) workgroup writes an fp32 partial
-//    tile; the last of a tile's splits to arrive (a per-tile counter, left
-//    zero again) sums the partials in split order and runs the epilogue, so
-//    the result does not depend on arrival order.
+//    A operand feeds RT MFMAs and each decoded B operand TM/16.
+//  * Split K (ks > 1, the MoE launches): each (tile, split) workgroup writes
+//    an fp32 partial tile; the last of a tile's splits to arrive (a per-tile
+//    counter, left zero again) sums the partials in split order and runs the
+//    epilogue, so the result does not depend on arrival order.
 //  * Epilogues: DENSE y = fp16(acc + a SV^T + bias); GATE/UP inter =
 //    fp16(fp16(silu(fp16 g)) * fp16 u) with each projection's own a SV^T,
 //    stored in the down projection's decode order; DOWN fp32 y + a SV^T.
 //
 // pf_lowrank_kernel: a = x U for the low-rank term (fp32 accumulation, one
-// fp16 rounding), 16 rows per workgroup with U staged in LDS; for the dense
-// path it also writes x in decode order and its per-group sums for the GEMM.
+// fp16 rounding), 16 rows per workgroup with U staged in LDS.
 #include <algorithm>
+#include <cstdio>
 
 #include "glq_stream.h"
 
@@ -158,6 +159,35 @@ __device__ __forceinline__ f16x8 pf_decode(const uint32_t* w, const PfK<BITS>& k
   return __builtin_bit_cast(f16x8, o);
 }
 
+// A operand of k-step t (0..3) from an LDS row holding x in NATURAL order
+// (16-byte piece P at position P ^ li): the decode's order is made with
+// v_perm.  2-bit step t pairs codes (j, j + 8) of word 2kb + t / 2, i.e.
+// halves j of natural pieces 4kb + 2 (t / 2) and + 1 (j = 0..3 for even t,
+// 4..7 for odd); 4-bit step t pairs codes (j, j + 4) of word 4kb + t, halves
+// j and j + 4 of natural piece 4kb + t.
+template <int BITS>
+__device__ __forceinline__ f16x8 pf_nat_a(const unsigned char* row, int kb, int t, int li) {
+  u32x4 o;
+  if constexpr (BITS == 2) {
+    const int p0 = 4 * kb + 2 * (t >> 1);
+    const u32x4 lo = *(const u32x4*)(row + ((p0 ^ li) << 4));
+    const u32x4 hi = *(const u32x4*)(row + (((p0 + 1) ^ li) << 4));
+    const uint32_t a0 = (t & 1) ? lo.z : lo.x, a1 = (t & 1) ? lo.w : lo.y;
+    const uint32_t b0 = (t & 1) ? hi.z : hi.x, b1 = (t & 1) ? hi.w : hi.y;
+    o.x = __builtin_amdgcn_perm(b0, a0, 0x05040100u);
+    o.y = __builtin_amdgcn_perm(b0, a0, 0x07060302u);
+    o.z = __builtin_amdgcn_perm(b1, a1, 0x05040100u);
+    o.w = __builtin_amdgcn_perm(b1, a1, 0x07060302u);
+  } else {
+    const u32x4 v = *(const u32x4*)(row + (((4 * kb + t) ^ li) << 4));
+    o.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
+    o.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
+    o.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+    o.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
+  }
+  return __builtin_bit_cast(f16x8, o);
+}
+
 // Weight row of row tile rt of a wave (see the file comment); may be >= N
 // (clamp for loads).
 template <int RT, int MODE>
@@ -169,30 +199,39 @@ template <int RT, int MODE>
 constexpr int pf_wg_rows() { return MODE == kPfGateUp ? 4 * 8 * RT : 4 * 16 * RT; }
 
 // LDS slot of one group: A (TM token rows x 256 B, swizzled pieces), then per
-// wave its RT row tiles' codes (16 rows x CB bytes each), scales and zero-points
-// (one fp16 per (row tile, row) at a 4-byte stride, as the 2-byte direct-to-LDS
-// load places them).
-template <int BITS, int TM, int RT>
+// wave its RT row tiles' codes (16 rows x CB bytes each, padded to whole
+// 1 KB load instructions), scales and zero-points (one fp16 per (row tile,
+// row) at a 4-byte stride, as the 2-byte direct-to-LDS load places them).
+// Ring depth D: DEEP rings take half the CU's 160 KB (two workgroups per
+// CU, as many groups in flight as fit); otherwise 3 slots when two
+// workgroups fit a CU, else 2.
+template <int BITS, int TM, int RT, bool DEEP = false>
 struct PfSlot {
   static constexpr int CB = BITS == 2 ? 32 : 64;        // code bytes per row per group
+  static constexpr int CW = RT * 16 * CB;                // code bytes per wave
+  static constexpr int CR = CW < 1024 ? 1024 : CW;       // LDS bytes per wave (whole loads)
   static constexpr int A = 0;
   static constexpr int C = TM * 256;
-  static constexpr int S = C + 4 * RT * 16 * CB;
+  static constexpr int S = C + 4 * CR;
   static constexpr int Z = S + 4 * 256;
   static constexpr int BYTES = Z + 4 * 256;
-  static constexpr int NC = RT * 16 * CB / 1024;          // code load instructions per wave
-  // ring depth: 3 slots when two workgroups still fit a CU, else 2
-  static constexpr int D = 2 * 3 * BYTES <= 160 * 1024 ? 3 : 2;
+  static constexpr int NC = CR / 1024;                   // code load instructions per wave
+  static constexpr int NI = TM / 16 + NC + 2;            // loads per lane per group (max)
+  static constexpr int DMAX = 2 + 63 / NI;               // the vmcnt field is 6 bits
+  static constexpr int DFIT = (80 * 1024 - 64) / BYTES;  // two workgroups per CU
+  static constexpr int D = DEEP ? (DFIT < DMAX ? (DFIT < 16 ? DFIT : 16) : (DMAX < 16 ? DMAX : 16))
+                                : (2 * 3 * BYTES <= 160 * 1024 ? 3 : 2);
 };
 
-template <int BITS, int TM, int RT, int MODE, bool SYM, bool ZF>
+template <int BITS, int TM, int RT, int MODE, bool SYM, bool ZF, bool DEEP>
 __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
   extern __shared__ __align__(16) unsigned char smem[];
-  using SL = PfSlot<BITS, TM, RT>;
+  using SL = PfSlot<BITS, TM, RT, DEEP>;
   constexpr int TT = TM / 16;
   constexpr int XI = TM / 16;  // A load instructions per wave per group (4 rows each)
   constexpr int WGR = pf_wg_rows<RT, MODE>();
   constexpr int NMAT = MODE == kPfGateUp ? 2 : 1;
+  constexpr bool NAT = MODE == kPfDense;  // A rows in natural order (the caller's x)
   constexpr int D = SL::D;
   constexpr int NI = XI + SL::NC + 1 + (SYM ? 0 : 1);  // loads per lane per group
   const int tid = threadIdx.x, lane = tid & 63;
@@ -233,10 +272,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
     zb[m] = SYM ? sb[m] : g.zeros[m] + e * g.sz_es;
   }
   // codes: instruction q covers bytes q*1024 + 16*lane of the wave's region
+  // (lanes past the wave's code bytes re-load its first ones into the padding)
   int coff[SL::NC], cmat[SL::NC];
 #pragma unroll
   for (int q = 0; q < SL::NC; ++q) {
-    const int o = q * 1024 + 16 * lane;
+    const int o = (q * 1024 + 16 * lane) % SL::CW;
     const int rt = o / (16 * SL::CB), row = (o % (16 * SL::CB)) / SL::CB;
     const int piece = (o % SL::CB) / 16;
     const int n = min(pf_row<RT, MODE>(n0, wave, rt, row), g.N - 1);
@@ -260,7 +300,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
     for (int q = 0; q < SL::NC; ++q) {
       const uint32_t* base = NMAT == 2 && cmat[q] ? cb[NMAT - 1] : cb[0];
       __builtin_amdgcn_global_load_lds((const void*)(base + coff[q] + grp * (SL::CB / 4)),
-                                       (lds_void*)(slot + SL::C + wave * (RT * 16 * SL::CB) + q * 1024),
+                                       (lds_void*)(slot + SL::C + wave * SL::CR + q * 1024),
                                        16, 0, 0);
     }
     const __half* sbase = NMAT == 2 && smat ? sb[NMAT - 1] : sb[0];
@@ -295,7 +335,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
     PfK<BITS> kc[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const unsigned char* cr = sl + SL::C + wave * (RT * 16 * SL::CB) + (rt * 16 + li) * SL::CB;
+      const unsigned char* cr = sl + SL::C + wave * SL::CR + (rt * 16 + li) * SL::CB;
       if constexpr (BITS == 2) {
         const u32x2 v = *(const u32x2*)(cr + 8 * kb);
         w[rt][0] = v.x;
@@ -312,23 +352,45 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
       kc[rt] = pf_consts<BITS, SYM>(sh, zh);
     }
     // the group's sum of x (q - zi), fp32
+    auto a_op = [&](int i, int t) -> f16x8 {
+      const unsigned char* row = sl + SL::A + (16 * i + li) * 256;
+      if constexpr (NAT) return pf_nat_a<BITS>(row, kb, t, li);
+      else return *(const f16x8*)(row + (((4 * kb + t) ^ li) << 4));
+    };
     f32x4 acc[TT][RT];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       f16x8 bf[RT];
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) bf[rt] = pf_decode<BITS, SYM>(w[rt], kc[rt], t, dk);
-      const int pc = ((4 * kb + t) ^ li) * 16;
 #pragma unroll
       for (int i = 0; i < TT; ++i) {
-        const f16x8 av = *(const f16x8*)(sl + SL::A + (16 * i + li) * 256 + pc);
+        const f16x8 av = a_op(i, t);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
           acc[i][rt] = mfma_16x16x32(av, bf[rt], t == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][rt]);
       }
     }
-    // y += s (acc - zf c2): c2 = the group's sum of x per token, loaded only
-    // for non-integer zero-points (zf != 0)
+    // y += s (acc - zf c2): c2 = the group's sum of x per token, needed only
+    // for non-integer zero-points (zf != 0); natural-order A forms it here
+    // (an MFMA against ones, when any row of the wave has zf != 0), the
+    // decode-order A of the MoE forms reads it from g.c2
+    f32x4 c2v[TT];
+    if constexpr (ZF && NAT) {
+      bool any = false;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) any |= kc[rt].zf != 0.f;
+      if (__builtin_amdgcn_ballot_w64(any) != 0) {  // uniform over the wave
+        const f16x8 ones = __builtin_bit_cast(f16x8, u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u,
+                                                           0x3C003C00u});
+#pragma unroll
+        for (int i = 0; i < TT; ++i) {
+          c2v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) c2v[i] = mfma_16x16x32(a_op(i, t), ones, c2v[i]);
+        }
+      }
+    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const float s = kc[rt].s;
@@ -336,9 +398,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
         const float zf = kc[rt].zf;
 #pragma unroll
         for (int i = 0; i < TT; ++i) {
-          // rows past the tile's last are read (the layout has whole tiles)
-          // and never stored
-          const float4 c2 = *(const float4*)(g.c2 + (int64_t)grp * g.c2_ld + p0 + 16 * i + 4 * kb);
+          float4 c2;
+          if constexpr (NAT) {
+            c2 = float4{c2v[i][0], c2v[i][1], c2v[i][2], c2v[i][3]};
+          } else {
+            // rows past the tile's last are read (the layout has whole
+            // tiles) and never stored
+            c2 = *(const float4*)(g.c2 + (int64_t)grp * g.c2_ld + p0 + 16 * i + 4 * kb);
+          }
           y[i][rt][0] = fmaf(s, acc[i][rt][0] - zf * c2.x, y[i][rt][0]);
           y[i][rt][1] = fmaf(s, acc[i][rt][1] - zf * c2.y, y[i][rt][1]);
           y[i][rt][2] = fmaf(s, acc[i][rt][2] - zf * c2.z, y[i][rt][2]);
@@ -484,11 +551,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
 struct PfLowrank {
   const __half* x;         // A rows, K halves each
   const int32_t* arow;     // A row of sorted row p (null: p)
-  __half* xperm_out;       // dense prep: x in decode order, or null
-  int xperm_bits;
-  float* c2_out;           // dense prep: per (group, row) sum of x, (K/128, c2_ld), or null
-  int64_t c2_ld;
-  int n_prep;              // workgroups of the dense prep (0: none)
   int aperm;               // 0: A natural; 2 or 4: A in that decode order
   const __half* U[2];      // (C, K, rank) per matrix
   int64_t u_cs;            // elements between clusters
@@ -506,45 +568,6 @@ struct PfLowrank {
 
 constexpr int kLrRows = 16;  // rows per lowrank workgroup (one 16-row MFMA tile)
 
-// Dense only: x in the decode order of xperm_bits and (c2_out) its per-group
-// sums, one thread per (row, 128-code group).
-__device__ void pf_prep_rows(const PfLowrank& L, int64_t idx) {
-  const int G = L.K / 128;
-  if (idx >= (int64_t)L.rows_total * G) return;
-  const int row = (int)(idx / G), grp = (int)(idx - (int64_t)row * G);
-  const __half* src = L.x + (int64_t)row * L.K + 128 * grp;
-  __half* dst = L.xperm_out + (int64_t)row * L.K + 128 * grp;
-  f16x8 v[16];
-#pragma unroll
-  for (int b = 0; b < 16; ++b) v[b] = *(const f16x8*)(src + 8 * b);
-  float sum = 0.f;
-#pragma unroll
-  for (int blk = 0; blk < 8; ++blk) {  // 16-code blocks
-    _Float16 in[16], o[16];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      in[c] = v[2 * blk][c];
-      in[8 + c] = v[2 * blk + 1][c];
-      sum += (float)in[c] + (float)in[8 + c];
-    }
-    if (L.xperm_bits == 2) {
-#pragma unroll
-      for (int pos = 0; pos < 16; ++pos) o[pos] = in[perm_src<2>(pos)];
-    } else {
-#pragma unroll
-      for (int pos = 0; pos < 16; ++pos) o[pos] = in[perm_src<4>(pos)];
-    }
-    f16x8 o0, o1;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      o0[c] = o[c];
-      o1[c] = o[8 + c];
-    }
-    *(f16x8*)(dst + 16 * blk) = o0;
-    *(f16x8*)(dst + 16 * blk + 8) = o1;
-  }
-  if (L.c2_out) L.c2_out[(int64_t)grp * L.c2_ld + row] = sum;
-}
 
 // One (16 rows, K split) job of a = x U: fp32 partial sums into
 // part[sp][row][m * rank + j].  A rows (16 x 128 codes) and U (128 x rank of
@@ -658,18 +681,13 @@ __device__ void pf_lowrank_job(const PfLowrank& L, int job, int sp, unsigned cha
   }
 }
 
-// Grid: n_prep workgroups of pf_prep_rows (256 (row, group) items each), then
-// n_jobs * ks lowrank jobs.
+// Grid: n_jobs * ks lowrank jobs.
 __global__ __launch_bounds__(kPfThreads) void pf_lowrank_kernel(PfLowrank L) {
   extern __shared__ __align__(16) unsigned char smem[];
   if (L.zero_cnt && blockIdx.x == 0)
     for (int i = threadIdx.x; i < L.n_cnt; i += kPfThreads) L.zero_cnt[i] = 0u;
-  const int b = blockIdx.x;
-  if (b < L.n_prep) {
-    pf_prep_rows(L, (int64_t)b * kPfThreads + threadIdx.x);
-    return;
-  }
-  const int j = b - L.n_prep;
+  if (L.nmat == 0) return;  // the counters were all there was to do
+  const int j = blockIdx.x;
   pf_lowrank_job(L, j / L.ks, j % L.ks, smem);
 }
 
@@ -677,15 +695,15 @@ __global__ __launch_bounds__(kPfThreads) void pf_lowrank_kernel(PfLowrank L) {
 // Host side shared by the dense GEMM and the MoE prefill
 // ---------------------------------------------------------------------------
 
-template <int BITS, int TM, int RT, int MODE, bool SYM, bool ZF>
+template <int BITS, int TM, int RT, int MODE, bool SYM, bool ZF, bool DEEP = false>
 static int pf_launch_k(const PfArgs& g, hipStream_t s) {
   static size_t attr = 64 * 1024;
-  using SL = PfSlot<BITS, TM, RT>;
+  using SL = PfSlot<BITS, TM, RT, DEEP>;
   const size_t lds = (size_t)SL::D * SL::BYTES;
-  int rc = set_lds_limit(pf_gemm_kernel<BITS, TM, RT, MODE, SYM, ZF>, lds, attr);
+  int rc = set_lds_limit(pf_gemm_kernel<BITS, TM, RT, MODE, SYM, ZF, DEEP>, lds, attr);
   if (rc) return rc;
   const dim3 grid((unsigned)(g.ntn * g.ks), (unsigned)g.max_tiles);
-  pf_gemm_kernel<BITS, TM, RT, MODE, SYM, ZF><<<grid, dim3(kPfThreads), lds, s>>>(g);
+  pf_gemm_kernel<BITS, TM, RT, MODE, SYM, ZF, DEEP><<<grid, dim3(kPfThreads), lds, s>>>(g);
   GLQ_LAUNCH_CHECK("pf_gemm_kernel");
   return GLQ_OK;
 }
@@ -713,9 +731,37 @@ static int pf_launch_shape(const PfArgs& g, int bits, int tm, hipStream_t s) {
   return pf_launch_k<4, 32, 4, MODE, SYM, ZF>(g, s);
 }
 
-static int pf_launch_dense(const PfArgs& g, int bits, int tm, bool sym, hipStream_t s) {
-  if (sym) return pf_launch_shape<kPfDense, true, false>(g, bits, tm, s);
-  return pf_launch_shape<kPfDense, false, true>(g, bits, tm, s);
+// Tile of a dense launch: TM token rows x 64 RT weight rows, ring depth.
+struct PfTile {
+  int tm, rt;
+  bool deep;
+};
+
+template <int BITS, bool SYM, bool ZF>
+static int pf_launch_dense_bits(const PfArgs& g, PfTile t, hipStream_t s) {
+  if (t.deep) {
+    if (t.tm == 16) {
+      if (t.rt == 1) return pf_launch_k<BITS, 16, 1, kPfDense, SYM, ZF, true>(g, s);
+      return pf_launch_k<BITS, 16, 2, kPfDense, SYM, ZF, true>(g, s);
+    }
+    if (t.tm == 32) {
+      if (t.rt == 1) return pf_launch_k<BITS, 32, 1, kPfDense, SYM, ZF, true>(g, s);
+      return pf_launch_k<BITS, 32, 2, kPfDense, SYM, ZF, true>(g, s);
+    }
+    return pf_launch_k<BITS, 64, 2, kPfDense, SYM, ZF, true>(g, s);
+  }
+  if (t.tm == 128) return pf_launch_k<BITS, 128, 2, kPfDense, SYM, ZF>(g, s);
+  if (t.tm == 64) return pf_launch_k<BITS, 64, 2, kPfDense, SYM, ZF>(g, s);
+  return pf_launch_k<BITS, 32, 4, kPfDense, SYM, ZF>(g, s);
+}
+
+static int pf_launch_dense(const PfArgs& g, int bits, PfTile t, bool sym, hipStream_t s) {
+  if (bits == 2) {
+    return sym ? pf_launch_dense_bits<2, true, false>(g, t, s)
+               : pf_launch_dense_bits<2, false, true>(g, t, s);
+  }
+  return sym ? pf_launch_dense_bits<4, true, false>(g, t, s)
+             : pf_launch_dense_bits<4, false, true>(g, t, s);
 }
 
 // Weight rows per workgroup for a token tile.
@@ -738,14 +784,15 @@ __global__ __launch_bounds__(256) void pf_lowrank_finalize_kernel(const float* p
   a[i] = __float2half(s);
 }
 
-// n_jobs: 16-row lowrank jobs (times L.ks splits) after L.n_prep prep
-// workgroups.
+// n_jobs: 16-row lowrank jobs (times L.ks splits); with none, one workgroup
+// still clears L.zero_cnt.
 static int pf_lowrank_launch(const PfLowrank& L, int n_jobs, hipStream_t s) {
   static size_t attr = 64 * 1024;
   const size_t lds = L.nmat > 0 ? pf_lowrank_lds(L.nmat, L.rank) : 0;
   int rc = set_lds_limit(pf_lowrank_kernel, lds, attr);
   if (rc) return rc;
-  const int64_t grid = (int64_t)L.n_prep + (L.nmat > 0 ? (int64_t)n_jobs * L.ks : 0);
+  int64_t grid = L.nmat > 0 ? (int64_t)n_jobs * L.ks : 0;
+  if (grid == 0 && L.zero_cnt) grid = 1;  // the job index is past the list: no job
   if (grid == 0) return GLQ_OK;
   GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
   pf_lowrank_kernel<<<dim3((unsigned)grid), dim3(kPfThreads), lds, s>>>(L);
@@ -772,35 +819,59 @@ static void pf_lowrank_split(int64_t K, int& ks, int& kps) {
 // Dense plan: token tile, K splits and workspace of one projection.
 // ---------------------------------------------------------------------------
 struct PfDensePlan {
-  int tm, ntn, ntm, ks, gps, lr_ks, lr_kps;
-  int64_t xp_bytes, c2_bytes, a_bytes, lp_bytes, part_bytes, cnt_bytes, total;
+  int tm, rt, ntn, ntm, ks, gps, lr_ks, lr_kps;
+  bool deep;
+  int64_t a_bytes, lp_bytes, part_bytes, cnt_bytes, total;
 };
 
 static PfDensePlan pf_dense_plan(int64_t M, int64_t K, int64_t N, int64_t rank, int bits) {
   PfDensePlan P;
-  // 128-token tiles once there are enough tiles to fill the chip, else 64
-  P.tm = M > 32 ? 64 : 32;
-  if (M >= 128 && (M / 128) * ((N + 127) / 128) >= 256) P.tm = 128;
-  if (const char* e = getenv("GLQ_PF_TM")) P.tm = atoi(e) >= 128 ? 128 : (atoi(e) >= 64 ? 64 : 32);
-  const int wgr = pf_wg_rows_rt(kPfDense, P.tm);
+  // Big launches (a 64 x 128 tile per CU or more): 64- or 128-token tiles,
+  // shallow rings, two workgroups per CU.  Smaller ones: 32-token tiles of
+  // 128 rows from 256 tokens, else 16-token tiles of 64 rows, with deep rings
+  // (the whole K range of a small tile nearly in flight).  No K split: the
+  // tiles are sized to give the chip enough workgroups without one.
+  const int64_t t64 = ((M + 63) / 64) * ((N + 127) / 128);
+  if (t64 >= 256) {
+    P.tm = (M >= 128 && (M / 128) * ((N + 127) / 128) >= 256) ? 128 : 64;
+    P.rt = 2;
+    P.deep = false;
+  } else if (M >= 256) {
+    P.tm = 32;
+    P.rt = 2;
+    P.deep = true;
+  } else {
+    P.tm = 16;
+    P.rt = 1;
+    P.deep = true;
+  }
+  if (const char* e = getenv("GLQ_PF_CFG")) {  // "tm,rt,deep": a supported tile
+    int tm = 0, rt = 0, deep = 0;
+    if (sscanf(e, "%d,%d,%d", &tm, &rt, &deep) == 3) {
+      const bool ok = deep ? ((tm == 16 || tm == 32) && (rt == 1 || rt == 2)) || (tm == 64 && rt == 2)
+                           : (tm == 32 && rt == 4) || ((tm == 64 || tm == 128) && rt == 2);
+      if (ok) {
+        P.tm = tm;
+        P.rt = rt;
+        P.deep = deep != 0;
+      }
+    }
+  }
+  const int wgr = 64 * P.rt;
   P.ntn = (int)((N + wgr - 1) / wgr);
   P.ntm = (int)((M + P.tm - 1) / P.tm);
   const int G = (int)(K / 128);
-  // about one workgroup per CU over the launch, each split at least 2 groups
-  const int64_t tiles = (int64_t)P.ntn * P.ntm;
-  int ks = (int)std::max<int64_t>(1, std::min<int64_t>(G / 2, (256 + tiles - 1) / tiles));
+  int ks = 1;
   if (const char* e = getenv("GLQ_PF_KS")) ks = std::max(1, std::min(G, atoi(e)));
   P.gps = (G + ks - 1) / ks;
   P.ks = (G + P.gps - 1) / P.gps;
-  P.xp_bytes = align_up(M * K * 2, 256);
-  P.c2_bytes = align_up((int64_t)G * P.ntm * P.tm * 4, 256);  // (G, ntm * tm)
   pf_lowrank_split(K, P.lr_ks, P.lr_kps);
   P.a_bytes = rank > 0 ? align_up(M * rank * 2, 256) : 0;
   P.lp_bytes = rank > 0 && P.lr_ks > 1 ? align_up((int64_t)P.lr_ks * M * rank * 4, 256) : 0;
-  P.part_bytes = P.ks > 1 ? align_up((int64_t)P.ks * P.ntm * P.tm * P.ntn * 64 *
-                                     pf_rt(kPfDense, P.tm) * 4, 256) : 0;
+  P.part_bytes = P.ks > 1 ? align_up((int64_t)P.ks * P.ntm * P.tm * P.ntn * 64 * P.rt * 4, 256)
+                          : 0;
   P.cnt_bytes = P.ks > 1 ? align_up((int64_t)P.ntm * P.ntn * 4, 256) : 0;
-  P.total = P.xp_bytes + P.c2_bytes + P.a_bytes + P.lp_bytes + P.part_bytes + P.cnt_bytes;
+  P.total = P.a_bytes + P.lp_bytes + P.part_bytes + P.cnt_bytes;
   return P;
 }
 
@@ -821,47 +892,41 @@ int pf_dense_gemm(const void* x, int64_t M, int64_t K, int64_t N, const int32_t*
   const bool lora = SV != nullptr && rank > 0;
   // a = x U needs room only when it is formed here
   const PfDensePlan P = pf_dense_plan(M, K, N, lora && xU == nullptr ? rank : 0, bits);
-  GLQ_CHECK(workspace != nullptr && workspace_bytes >= P.total,
+  GLQ_CHECK(P.total == 0 || (workspace != nullptr && workspace_bytes >= P.total),
             "workspace of %lld bytes needed (got %lld)", (long long)P.total,
             (long long)workspace_bytes);
   GLQ_CHECK(M * K < (1ll << 31), "M*K too large for the prefill path");
   char* w = (char*)workspace;
-  __half* xp = (__half*)w;
-  float* c2 = (float*)(w + P.xp_bytes);
-  char* w2 = w + P.xp_bytes + P.c2_bytes;
-  __half* abuf = lora ? (__half*)w2 : nullptr;
-  float* lpart = P.lp_bytes ? (float*)(w2 + P.a_bytes) : nullptr;
-  char* w3 = w2 + P.a_bytes + P.lp_bytes;
+  __half* abuf = P.a_bytes ? (__half*)w : nullptr;
+  float* lpart = P.lp_bytes ? (float*)(w + P.a_bytes) : nullptr;
+  char* w3 = w + P.a_bytes + P.lp_bytes;
   float* part = P.ks > 1 ? (float*)w3 : nullptr;
   unsigned* cnt = P.ks > 1 ? (unsigned*)(w3 + P.part_bytes) : nullptr;
-  // launch 1: x in decode order and its group sums (+ the split partials of
-  // a = x U when U is given)
-  PfLowrank L = {};
-  L.x = (const __half*)x;
-  L.xperm_out = xp;
-  L.xperm_bits = bits;
-  L.c2_out = sym ? nullptr : c2;  // per-group sums of x (non-integer zero-points)
-  L.c2_ld = (int64_t)P.ntm * P.tm;
-  L.n_prep = (int)((M * (K / 128) + kPfThreads - 1) / kPfThreads);
-  L.aperm = 0;
-  L.nmat = (lora && xU == nullptr) ? 1 : 0;
-  L.U[0] = (const __half*)U;
-  L.u_cs = 0;
-  L.tile_rows = kLrRows;
-  L.rows_total = (int)M;
-  L.K = (int)K;
-  L.rank = L.nmat ? (int)rank : 8;
-  L.ks = P.lr_ks;
-  L.kps = P.lr_kps;
-  L.part = lpart;
-  L.a_out = abuf;
-  L.zero_cnt = cnt;  // the GEMM's split-K counters start at zero
-  L.n_cnt = P.ntm * P.ntn;
-  int rc = pf_lowrank_launch(L, (int)((M + kLrRows - 1) / kLrRows), s);
-  if (rc) return rc;
-  // launch 2: the GEMM
+  // launch 1 (when U is given, or split-K counters need clearing): the split
+  // partials of a = x U, summed by a finalize launch
+  if (P.a_bytes || cnt) {
+    PfLowrank L = {};
+    L.x = (const __half*)x;
+    L.aperm = 0;
+    L.nmat = P.a_bytes ? 1 : 0;
+    L.U[0] = (const __half*)U;
+    L.u_cs = 0;
+    L.tile_rows = kLrRows;
+    L.rows_total = (int)M;
+    L.K = (int)K;
+    L.rank = L.nmat ? (int)rank : 8;
+    L.ks = P.lr_ks;
+    L.kps = P.lr_kps;
+    L.part = lpart;
+    L.a_out = abuf;
+    L.zero_cnt = cnt;  // the GEMM's split-K counters start at zero
+    L.n_cnt = P.ntm * P.ntn;
+    int rc = pf_lowrank_launch(L, (int)((M + kLrRows - 1) / kLrRows), s);
+    if (rc) return rc;
+  }
+  // launch 2: the GEMM, A = x in natural order
   PfArgs g = {};
-  g.xp = xp;
+  g.xp = (const __half*)x;
   g.codes[0] = (const uint32_t*)codes;
   g.scales[0] = (const __half*)scales;
   g.zeros[0] = (const __half*)zeros;
@@ -883,9 +948,7 @@ int pf_dense_gemm(const void* x, int64_t M, int64_t K, int64_t N, const int32_t*
   g.ks = P.ks;
   g.gps = P.gps;
   g.max_tiles = P.ntm;
-  g.c2 = c2;
-  g.c2_ld = (int64_t)P.ntm * P.tm;
-  return pf_launch_dense(g, bits, P.tm, sym != 0, s);
+  return pf_launch_dense(g, bits, PfTile{P.tm, P.rt, P.deep}, sym != 0, s);
 }
 }  // namespace glq
 

@@ -72,8 +72,9 @@ def test_argument_checks_raise_before_any_launch(lib):
     rc = lib.glq_gemv_lora(1 << 12, 1, 2048, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 64, 0,
                            nul, nul, 0, nul, nul, 1 << 12, 1 << 12, 1 << 20, nul)
     assert rc == 1 and b"group" in lib.glq_last_error()
-    # workspace too small
-    rc = lib.glq_gemv_lora(1 << 12, 1, 2048, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 128, 0,
+    # workspace too small (two token rows: the x U partials need one; one row
+    # forms x U inside its launch)
+    rc = lib.glq_gemv_lora(1 << 12, 2, 2048, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 128, 0,
                            1 << 12, 1 << 12, 64, nul, nul, 1 << 12, 1 << 12, 16, nul)
     assert rc == 1 and b"workspace" in lib.glq_last_error()
     # misaligned x
