@@ -321,12 +321,12 @@ static bool lane_shape(int64_t M, const TileShape& sh, int bits) {
 
 // Bytes of LDS the fused-x U form needs (partials of a, then a in fp16).
 static size_t lane_xu_lds(const LaneArgs& la) {
-  return (size_t)LaneXu(la.a.sh.rank).lds_bytes(la.a.sh.rank);
+  return (size_t)LaneXu(la.g.rank).lds_bytes(la.g.rank);
 }
 
 template <int BITS, bool SYM, int LRP, int NSV, bool HASB>
 static int launch_lane_k(const LaneArgs& la, bool xu, hipStream_t s) {
-  const int64_t waves = (int64_t)la.a.items * la.wpi;
+  const int64_t waves = (int64_t)la.g.items * la.g.wpi;
   if (xu) {
     const int64_t grid = waves / 8;  // wpi is a multiple of 8
     GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
@@ -349,7 +349,7 @@ static int launch_lane_k(const LaneArgs& la, bool xu, hipStream_t s) {
 // SV dwords per lane: rank / 2 spread over the LRP lanes of a row.
 template <int BITS, bool SYM, int LRP, bool HASB>
 static int launch_lane_sv(const LaneArgs& la, bool xu, hipStream_t s) {
-  const int nsv = (la.a.sh.rank / 2 + LRP - 1) / LRP;
+  const int nsv = (la.g.rank / 2 + LRP - 1) / LRP;
   if (nsv <= 1) return launch_lane_k<BITS, SYM, LRP, 1, HASB>(la, xu, s);
   if constexpr (LRP <= 32) {
     if (nsv <= 2) return launch_lane_k<BITS, SYM, LRP, 2, HASB>(la, xu, s);
@@ -360,8 +360,8 @@ static int launch_lane_sv(const LaneArgs& la, bool xu, hipStream_t s) {
 
 template <int BITS, bool SYM, bool HASB>
 static int launch_lane_lrp(const LaneArgs& la, bool xu, hipStream_t s) {
-  if (la.lr <= 16) return launch_lane_sv<BITS, SYM, 16, HASB>(la, xu, s);
-  if (la.lr <= 32) return launch_lane_sv<BITS, SYM, 32, HASB>(la, xu, s);
+  if (la.g.lr <= 16) return launch_lane_sv<BITS, SYM, 16, HASB>(la, xu, s);
+  if (la.g.lr <= 32) return launch_lane_sv<BITS, SYM, 32, HASB>(la, xu, s);
   return launch_lane_sv<BITS, SYM, 64, HASB>(la, xu, s);
 }
 
@@ -378,18 +378,25 @@ static int launch_lane_bits(const LaneArgs& la, bool xu, hipStream_t s) {
 static int launch_lane(const DenseArgs& a, int bits, bool xu, hipStream_t s) {
   LaneArgs la;
   la.a = a;
-  la.lr = a.sh.K * bits / 128;
-  const int lrp = la.lr <= 16 ? 16 : la.lr <= 32 ? 32 : 64;
-  la.rounds = (a.sh.N + 63) / 64 * lrp / kLanePD;
+  LaneGeom& g = la.g;
+  g.N = a.sh.N;
+  g.K = a.sh.K;
+  g.G = a.sh.G;
+  g.kw = a.sh.kw;
+  g.rank = a.sh.rank;
+  g.items = a.items;
+  g.lr = a.sh.K * bits / 128;
+  const int lrp = g.lr <= 16 ? 16 : g.lr <= 32 ? 32 : 64;
+  g.rounds = (a.sh.N + 63) / 64 * lrp / kLanePD;
   // about kLaneWaves waves over the launch
-  const int64_t total = (int64_t)a.items * la.rounds;
+  const int64_t total = (int64_t)a.items * g.rounds;
   int64_t rpw = (total + kLaneWaves - 1) / kLaneWaves;
   if (const char* e = getenv("GLQ_LANE_RPW")) rpw = atoll(e) > 0 ? atoll(e) : rpw;
-  la.rpw = (int)std::min<int64_t>(std::max<int64_t>(rpw, 1), la.rounds);
-  la.wpi = (la.rounds + la.rpw - 1) / la.rpw;
+  g.rpw = (int)std::min<int64_t>(std::max<int64_t>(rpw, 1), g.rounds);
+  g.wpi = (g.rounds + g.rpw - 1) / g.rpw;
   if (xu) {  // whole 8-wave workgroups per item, the rounds spread over all of them
-    la.wpi = (la.wpi + 7) / 8 * 8;
-    la.rpw = (la.rounds + la.wpi - 1) / la.wpi;
+    g.wpi = (g.wpi + 7) / 8 * 8;
+    g.rpw = (g.rounds + g.wpi - 1) / g.wpi;
   }
   return bits == 2 ? launch_lane_bits<2>(la, xu, s) : launch_lane_bits<4>(la, xu, s);
 }

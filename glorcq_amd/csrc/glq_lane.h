@@ -79,14 +79,6 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 constexpr int kBufferFlags = 0x00020000;
 constexpr int kBufferNT = 2;
 
-struct LaneArgs {
-  DenseArgs a;
-  int rounds;  // rounds of PD iterations per item (64-row units x LRP / PD)
-  int wpi;     // waves per item
-  int rpw;     // rounds per wave (consecutive rounds of one item)
-  int lr;      // 16-byte pieces per code row
-};
-
 // Decoded operands of one code word as packed fp16 pairs (decode2 / decode4).
 __device__ __forceinline__ void decode2_words(uint32_t w, u32x4& a, u32x4& b,
                                               const DecodeConsts& k) {
@@ -124,13 +116,32 @@ struct LaneXu {
   }
 };
 
-// Work: the rows of an item are cut into 64-row units of NIT = LRP
-// iterations, taken in rounds of PD iterations; wave w of an item runs rounds
+// Geometry of one lane launch (or one role of a launch): every item has N
+// rows of K codes; rows are cut into 64-row units of NIT = LRP iterations,
+// taken in rounds of PD iterations; wave w of an item runs rounds
 // w rpw .. w rpw + rpw - 1 and stores each round's rows at the round's end.
-// PD: iterations of loads in flight ahead of use.  Loads are issued
-// unconditionally (iterations past the wave's last one re-read its last row),
-// so the register ring needs no copies and the compiler's waits stay PD deep.
-// NSV: SV dwords per lane (rank <= 2 NSV LRP); HASB: a bias is added.
+struct LaneGeom {
+  int N, K, G, kw, rank;
+  int lr;      // 16-byte pieces per code row
+  int rounds;  // rounds of PD iterations per item (64-row units x LRP / PD)
+  int wpi;     // waves per item
+  int rpw;     // rounds per wave (consecutive rounds of one item)
+  int items;
+};
+
+// Item data of a lane launch.  A source type provides, per item:
+//   lora(item)            the low-rank term is present
+//   codes/scales/zeros/sv/bias/u(item)   the item's tensors (bias may be null)
+//   x8(item, k)           8 halves of the item's activation row at k (k % 8 == 0)
+//   load_a(item, j)       a[j] when a is given (not XU)
+//   store(item, n, v)     the item's output row n
+//
+// Work per wave: PD iterations of loads in flight ahead of use.  Loads are
+// issued unconditionally (iterations past the wave's last one re-read its
+// last row), so the register ring needs no copies and the compiler's waits
+// stay PD deep.  NP: 16-byte pieces per lane (a row of up to 64 NP pieces;
+// lane l holds pieces l % LRP + j LRP).  NSV: SV dwords per lane (rank <= 2
+// NSV LRP); HASB: a bias is added.
 //
 // XU: the low-rank factor a = fp16(x U) is formed in the same launch, first:
 // each workgroup (8 waves, all of one item) reads the item's U with every
@@ -139,62 +150,69 @@ struct LaneXu {
 // partials are summed in LDS in a fixed order and rounded to fp16 once.
 // Then the waves take their x slices and stream their rows.  An item whose
 // rows are spread over several workgroups has each of them form a.
-template <int BITS, bool SYM, int LRP, int PD, int NSV, bool HASB, bool XU>
-__global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) {
-  constexpr int C = lane_piece_codes<BITS>();  // codes per lane
+template <class Src, int BITS, bool SYM, int LRP, int NP, int PD, int NSV, bool HASB, bool XU>
+__device__ __forceinline__ void lane_run(const Src& src, const LaneGeom& lg, int wv, int wvb,
+                                         float* xu_lds) {
+  constexpr int C = lane_piece_codes<BITS>();  // codes per piece
   constexpr int RPI = 64 / LRP;                // rows per iteration
   constexpr int NIT = LRP;                     // iterations per 64-row unit
-  constexpr int WPB = XU ? 8 : 4;              // waves per workgroup
   static_assert(NIT % PD == 0, "ring depth must divide the unit");
-  const DenseArgs& a = la.a;
-  const DenseSrc src{a};
+  static_assert(NP == 1 || LRP == 64, "several pieces per lane take whole waves per row");
   const int lane = threadIdx.x & 63;
-  const int wvb = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wv = blockIdx.x * WPB + wvb;
-  const int item = wv / la.wpi;
-  if (item >= a.items) return;  // uniform over the workgroup (XU: wpi is a multiple of 8)
+  const int item = wv / lg.wpi;
+  if (item >= lg.items) return;  // uniform over the workgroup (XU: wpi is a multiple of 8)
   // rounds rb .. rb + nr - 1 of PD iterations each, [PD R, PD R + PD)
-  const int rb = (wv - item * la.wpi) * la.rpw;
-  const int nr = min(la.rpw, la.rounds - rb);
+  const int rb = (wv - item * lg.wpi) * lg.rpw;
+  const int nr = min(lg.rpw, lg.rounds - rb);
   if (!XU && nr <= 0) return;  // (XU: every wave takes part in forming a)
-  const int rlast = min(rb + max(nr, 1), la.rounds) - 1;  // idle waves re-read a valid round
-  const int N = a.sh.N, G = a.sh.G, kw = a.sh.kw, rank = a.sh.rank;
+  const int rlast = min(rb + max(nr, 1), lg.rounds) - 1;  // idle waves re-read a valid round
+  const int N = lg.N, G = lg.G, kw = lg.kw, rank = lg.rank;
   const int ri = lane / LRP, p = lane % LRP;
-  const bool act = p < la.lr;
-  const int pc = act ? p : la.lr - 1;  // inactive lanes read a valid piece (x = 0)
-  const int g = pc * C / 128;          // the piece's quantization group
+  bool act[NP];
+  int pc[NP], gq[NP];
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const int pj = p + j * LRP;
+    act[j] = pj < lg.lr;
+    pc[j] = act[j] ? pj : lg.lr - 1;  // inactive pieces read a valid one (x = 0)
+    gq[j] = pc[j] * C / 128;          // the piece's quantization group
+  }
 
-  // ---- x slice in operand order, c1 = sum bias * x, c2 = sum x ----
-  uint32_t xw[C / 2];
-  float c1 = 0.f, c2 = 0.f;
+  // ---- x slices in operand order, c1 = sum bias * x, c2 = sum x ----
+  uint32_t xw[NP][C / 2];
+  float c1[NP], c2[NP];
   auto load_x = [&]() {
-    const __half* xr = src.xrow(item, 0) + pc * C;
 #pragma unroll
-    for (int blk = 0; blk < C / 16; ++blk) {
-      const f16x8 in0 = *(const f16x8*)(xr + 16 * blk);
-      const f16x8 in1 = *(const f16x8*)(xr + 16 * blk + 8);
-      _Float16 in[16], o[16];
+    for (int j = 0; j < NP; ++j) {
+      c1[j] = 0.f;
+      c2[j] = 0.f;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        in[c] = act ? in0[c] : (_Float16)0.f;
-        in[8 + c] = act ? in1[c] : (_Float16)0.f;
-      }
+      for (int blk = 0; blk < C / 16; ++blk) {
+        const f16x8 in0 = __builtin_bit_cast(f16x8, src.x8(item, pc[j] * C + 16 * blk));
+        const f16x8 in1 = __builtin_bit_cast(f16x8, src.x8(item, pc[j] * C + 16 * blk + 8));
+        _Float16 in[16], o[16];
 #pragma unroll
-      for (int pos = 0; pos < 16; ++pos) {
-        o[pos] = in[perm_src<BITS>(pos)];
-        const float f = (float)o[pos];
-        c2 += f;
-        c1 += code_bias<BITS>(pos) * f;
-      }
+        for (int c = 0; c < 8; ++c) {
+          in[c] = act[j] ? in0[c] : (_Float16)0.f;
+          in[8 + c] = act[j] ? in1[c] : (_Float16)0.f;
+        }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const f16x2 pr = {o[2 * j], o[2 * j + 1]};
-        xw[8 * blk + j] = __builtin_bit_cast(uint32_t, pr);
+        for (int pos = 0; pos < 16; ++pos) {
+          o[pos] = in[perm_src<BITS>(pos)];
+          const float f = (float)o[pos];
+          c2[j] += f;
+          c1[j] += code_bias<BITS>(pos) * f;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const f16x2 pr = {o[2 * q], o[2 * q + 1]};
+          xw[j][8 * blk + q] = __builtin_bit_cast(uint32_t, pr);
+        }
       }
     }
   };
   if constexpr (!XU) load_x();
-  const bool lora = a.sv != nullptr && rank > 0;
+  const bool lora = src.lora(item);
   int svo[NSV];  // element offset of the dword within an SV row
 #pragma unroll
   for (int k = 0; k < NSV; ++k) {
@@ -213,29 +231,39 @@ __global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) 
                                                      kBufferFlags);
   const auto rz = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(SYM ? src.scales(item) : src.zeros(item)), 0, N * G * 2, kBufferFlags);
-  // without a low-rank term the SV loads read x (finite, times a = 0)
+  // without a low-rank term the SV loads read the codes (finite, times a = 0)
   const auto rsv = __builtin_amdgcn_make_buffer_rsrc(
-      lora ? (void*)src.sv(item) : (void*)src.xrow(item, 0), 0, lora ? N * rank * 2 : 4,
+      lora ? (void*)src.sv(item) : (void*)src.codes(item), 0, lora ? N * rank * 2 : 4,
       kBufferFlags);
   const auto rbi = __builtin_amdgcn_make_buffer_rsrc(HASB ? (void*)src.bias(item) : nullptr, 0,
                                                      HASB ? N * 2 : 0, kBufferFlags);
   const int svr = lora ? rank : 0;
-  const int vc = ri * rowbytes + pc * 16, vs = (ri * G + g) * 2, vb = ri * 2;
+  int vc[NP], vs[NP];
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    vc[j] = ri * rowbytes + pc[j] * 16;
+    vs[j] = (ri * G + gq[j]) * 2;
+  }
+  const int vb = ri * 2;
   int vsv[NSV];
 #pragma unroll
   for (int k = 0; k < NSV; ++k) vsv[k] = (ri * svr + svo[k]) * 2;
   const float bsel = p == 0 ? 1.f : 0.f;  // the first lane of a row group adds the bias
 
-  u32x4 cw[PD];
-  uint32_t sw[PD], zw[PD], bw[PD], vw[PD][NSV];
+  u32x4 cw[PD][NP];
+  uint32_t sw[PD][NP], zw[PD][NP], bw[PD], vw[PD][NSV];
   // loads of iteration d of the wave's round r (rounds past the last re-read it)
   auto issue = [&](int d, int r) {
     const int n0 = RPI * (min(rb + r, rlast) * PD + d);  // uniform
     if constexpr (HASB) bw[d] = __builtin_amdgcn_raw_buffer_load_b16(rbi, vb + n0 * 2, 0, 0);
-    cw[d] = __builtin_bit_cast(
-        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, vc + n0 * rowbytes, 0, kBufferNT));
-    sw[d] = __builtin_amdgcn_raw_buffer_load_b16(rsc, vs + n0 * G * 2, 0, 0);
-    if constexpr (!SYM) zw[d] = __builtin_amdgcn_raw_buffer_load_b16(rz, vs + n0 * G * 2, 0, 0);
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      cw[d][j] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, vc[j] + n0 * rowbytes, 0, kBufferNT));
+      sw[d][j] = __builtin_amdgcn_raw_buffer_load_b16(rsc, vs[j] + n0 * G * 2, 0, 0);
+      if constexpr (!SYM)
+        zw[d][j] = __builtin_amdgcn_raw_buffer_load_b16(rz, vs[j] + n0 * G * 2, 0, 0);
+    }
 #pragma unroll
     for (int k = 0; k < NSV; ++k)
       vw[d][k] = __builtin_amdgcn_raw_buffer_load_b32(rsv, vsv[k] + n0 * svr * 2, 0, 0);
@@ -257,7 +285,6 @@ __global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) 
   uint32_t ap[NSV];
   if constexpr (XU) {
     // a = fp16(x U) in this workgroup (layout in LaneXu)
-    extern __shared__ float xu_lds[];
     const LaneXu L(rank);
     const int t = threadIdx.x;
     float* part = xu_lds;                      // (ks, rank)
@@ -266,14 +293,13 @@ __global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) 
     if (lora) {
       const int b = t % L.nb, slot = t / L.nb;
       if (slot < L.ks) {
-        const int nch = a.sh.K / 8;  // 8-row chunks
-        const __half* ub = a.u + (int64_t)item * a.u_es + 8 * b;
-        const __half* xr = src.xrow(item, 0);
+        const int nch = lg.K / 8;  // 8-row chunks
+        const __half* ub = src.u(item) + 8 * b;
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         u32x4 u0[8], u1[8], x0, x1;
         auto load = [&](int c, u32x4 (&u)[8], u32x4& xv) {
           c = min(c, nch - 1);  // past the end: re-read the last chunk (not used)
-          xv = *(const u32x4*)(xr + 8 * c);
+          xv = src.x8(item, 8 * c);
 #pragma unroll
           for (int q = 0; q < 8; ++q) u[q] = *(const u32x4*)(ub + (int64_t)(8 * c + q) * rank);
         };
@@ -336,8 +362,8 @@ __global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) 
       const int j = p + k * LRP;
       f16x2 pr = {(_Float16)0.f, (_Float16)0.f};
       if (lora && 2 * j < rank) {
-        pr[0] = (_Float16)__half2float(src.load_a(item, 0, 2 * j));
-        pr[1] = (_Float16)__half2float(src.load_a(item, 0, 2 * j + 1));
+        pr[0] = (_Float16)__half2float(src.load_a(item, 2 * j));
+        pr[1] = (_Float16)__half2float(src.load_a(item, 2 * j + 1));
       }
       ap[k] = __builtin_bit_cast(uint32_t, pr);
     }
@@ -351,33 +377,37 @@ __global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) 
 #pragma unroll
     for (int d = 0; d < PD; ++d) {
       const int i = i0 + d;
-      u32x4 w = cw[d];
-      if constexpr (SYM) w ^= xor_mask;
-      float acc0 = -c1, acc1 = 0.f;  // the operand bias leaves with c1
+      float part = 0.f;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        if constexpr (BITS == 2) {
-          u32x4 da, db;
-          decode2_words(w[k], da, db, dk);
+      for (int j = 0; j < NP; ++j) {
+        u32x4 w = cw[d][j];
+        if constexpr (SYM) w ^= xor_mask;
+        float acc0 = -c1[j], acc1 = 0.f;  // the operand bias leaves with c1
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            acc0 = dot2(da[j], xw[8 * k + j], acc0);
-            acc1 = dot2(db[j], xw[8 * k + 4 + j], acc1);
-          }
-        } else {
-          u32x4 da;
-          decode4_words(w[k], da, dk);
+        for (int k = 0; k < 4; ++k) {
+          if constexpr (BITS == 2) {
+            u32x4 da, db;
+            decode2_words(w[k], da, db, dk);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            if (j & 1) acc1 = dot2(da[j], xw[4 * k + j], acc1);
-            else acc0 = dot2(da[j], xw[4 * k + j], acc0);
+            for (int q = 0; q < 4; ++q) {
+              acc0 = dot2(da[q], xw[j][8 * k + q], acc0);
+              acc1 = dot2(db[q], xw[j][8 * k + 4 + q], acc1);
+            }
+          } else {
+            u32x4 da;
+            decode4_words(w[k], da, dk);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              if (q & 1) acc1 = dot2(da[q], xw[j][4 * k + q], acc1);
+              else acc0 = dot2(da[q], xw[j][4 * k + q], acc0);
+            }
           }
         }
+        const float s = __half2float(__ushort_as_half((uint16_t)sw[d][j]));
+        float z = (float)(1 << (BITS - 1));
+        if constexpr (!SYM) z = __half2float(__ushort_as_half((uint16_t)zw[d][j]));
+        part = fmaf(s, (acc0 + acc1) - z * c2[j], part);
       }
-      const float s = __half2float(__ushort_as_half((uint16_t)sw[d]));
-      float z = (float)(1 << (BITS - 1));
-      if constexpr (!SYM) z = __half2float(__ushort_as_half((uint16_t)zw[d]));
-      float part = s * ((acc0 + acc1) - z * c2);
       if constexpr (HASB) part = fmaf(bsel, __half2float(__ushort_as_half((uint16_t)bw[d])), part);
 #pragma unroll
       for (int k = 0; k < NSV; ++k) part = dot2(vw[d][k], ap[k], part);
@@ -391,8 +421,46 @@ __global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) 
     // the round's PD iterations store
     const int u = i0 / NIT, it0 = i0 & (NIT - 1);
     const int n = u * 64 + p * RPI + ri;
-    if (p >= it0 && p < it0 + PD && n < N) src.store(item, 0, n, yv);
+    if (p >= it0 && p < it0 + PD && n < N) src.store(item, n, yv);
   }
+}
+
+// Dense items (glq_gemv.hip): item i at base + i * stride, one token row.
+struct DenseLaneSrc {
+  const DenseArgs& a;
+  __device__ bool lora(int) const { return a.sv != nullptr && a.sh.rank > 0; }
+  __device__ const uint32_t* codes(int item) const { return a.codes + (int64_t)item * a.codes_es; }
+  __device__ const __half* scales(int item) const { return a.scales + (int64_t)item * a.sz_es; }
+  __device__ const __half* zeros(int item) const { return a.zeros + (int64_t)item * a.sz_es; }
+  __device__ const __half* sv(int item) const { return a.sv + (int64_t)item * a.sv_es; }
+  __device__ const __half* bias(int item) const { return a.bias + (int64_t)item * a.bias_es; }
+  __device__ const __half* u(int item) const { return a.u + (int64_t)item * a.u_es; }
+  __device__ u32x4 x8(int item, int k) const {
+    return *(const u32x4*)(a.x + (int64_t)item * a.x_es + k);
+  }
+  __device__ __half load_a(int item, int j) const {
+    if (a.xu) return a.xu[(int64_t)item * a.xu_es + j];
+    const float* pp = a.apart + (int64_t)item * a.P * a.M * a.sh.rpad + j;
+    return __float2half(sum_strided(pp, (int64_t)a.M * a.sh.rpad, a.P));
+  }
+  __device__ void store(int item, int n, float v) const {
+    a.y[(int64_t)item * a.y_es + n] = __float2half(v);
+  }
+};
+
+struct LaneArgs {
+  DenseArgs a;
+  LaneGeom g;
+};
+
+template <int BITS, bool SYM, int LRP, int PD, int NSV, bool HASB, bool XU>
+__global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) {
+  extern __shared__ float xu_lds[];
+  constexpr int WPB = XU ? 8 : 4;  // waves per workgroup
+  const DenseLaneSrc src{la.a};
+  const int wvb = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  lane_run<DenseLaneSrc, BITS, SYM, LRP, 1, PD, NSV, HASB, XU>(src, la.g, blockIdx.x * WPB + wvb,
+                                                               wvb, xu_lds);
 }
 
 }  // namespace glq
