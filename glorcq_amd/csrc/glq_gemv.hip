@@ -80,6 +80,48 @@ struct DenseSrc {
 
 namespace glq {
 
+// Dense items of the lane kernel: item i at base + i * stride, one token row.
+struct DenseLaneItem {
+  const DenseArgs& a;
+  int item;
+  __device__ bool lora() const { return a.sv != nullptr && a.sh.rank > 0; }
+  __device__ const uint32_t* codes() const { return a.codes + (int64_t)item * a.codes_es; }
+  __device__ const __half* scales() const { return a.scales + (int64_t)item * a.sz_es; }
+  __device__ const __half* zeros() const { return a.zeros + (int64_t)item * a.sz_es; }
+  __device__ const __half* sv() const { return a.sv + (int64_t)item * a.sv_es; }
+  __device__ const __half* bias() const { return a.bias + (int64_t)item * a.bias_es; }
+  __device__ const __half* u() const { return a.u + (int64_t)item * a.u_es; }
+  __device__ u32x4 x8(int k) const { return *(const u32x4*)(a.x + (int64_t)item * a.x_es + k); }
+  __device__ __half load_a(int j) const {
+    if (a.xu) return a.xu[(int64_t)item * a.xu_es + j];
+    const float* pp = a.apart + (int64_t)item * a.P * a.M * a.sh.rpad + j;
+    return __float2half(sum_strided(pp, (int64_t)a.M * a.sh.rpad, a.P));
+  }
+  __device__ void store(int n, float v) const {
+    a.y[(int64_t)item * a.y_es + n] = __float2half(v);
+  }
+};
+struct DenseLaneSrc {
+  const DenseArgs& a;
+  __device__ DenseLaneItem bind(int item) const { return DenseLaneItem{a, item}; }
+};
+
+struct LaneArgs {
+  DenseArgs a;
+  LaneGeom g;
+};
+
+template <int BITS, bool SYM, int LRP, int PD, int NSV, bool HASB, bool XU>
+__global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) {
+  extern __shared__ float xu_lds[];
+  constexpr int WPB = XU ? 8 : 4;  // waves per workgroup
+  const DenseLaneSrc src{la.a};
+  const int wvb = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  lane_run<DenseLaneSrc, BITS, SYM, LRP, 1, PD, NSV, HASB, XU>(src, la.g, blockIdx.x * WPB + wvb,
+                                                               wvb, xu_lds);
+}
+
+
 template <int MC>
 __global__ __launch_bounds__(256) void lowrank_partial_kernel(DenseArgs a) {
   __shared__ float red[4 * 4 * 64];

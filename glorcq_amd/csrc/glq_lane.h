@@ -116,6 +116,73 @@ struct LaneXu {
   }
 };
 
+// a = fp16(x U) of one item by all 512 threads of the workgroup (layout in
+// LaneXu): U rows read by whole-row wave loads, two 8-row chunks in flight
+// per thread, v_dot2 over row pairs into fp32, the partials summed in LDS in
+// a fixed order and rounded to fp16 once.  Returns a's LDS copy (rank halves);
+// every thread of the workgroup must call it (it holds barriers).
+template <class View>
+__device__ __half* lane_xu_phase(const View& src, int K, int rank, bool lora, float* xu_lds) {
+  const LaneXu L(rank);
+  const int t = threadIdx.x;
+  float* part = xu_lds;                      // (ks, rank)
+  float* segs = xu_lds + L.ks * rank;        // (nseg, rank)
+  __half* ah = (__half*)(segs + L.nseg * rank);
+  if (!lora) return ah;
+  const int b = t % L.nb, slot = t / L.nb;
+  if (slot < L.ks) {
+    const int nch = K / 8;  // 8-row chunks
+    const __half* ub = src.u() + 8 * b;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    u32x4 u0[8], u1[8], x0, x1;
+    auto load = [&](int c, u32x4 (&u)[8], u32x4& xv) {
+      c = min(c, nch - 1);  // past the end: re-read the last chunk (not used)
+      xv = src.x8(8 * c);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) u[q] = *(const u32x4*)(ub + (int64_t)(8 * c + q) * rank);
+    };
+    auto fma_chunk = [&](const u32x4 (&u)[8], const u32x4& xv) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {  // rows 2i, 2i + 1 against (x_2i, x_2i+1)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t lo = __builtin_amdgcn_perm(u[2 * i + 1][j], u[2 * i][j], 0x05040100u);
+          const uint32_t hi = __builtin_amdgcn_perm(u[2 * i + 1][j], u[2 * i][j], 0x07060302u);
+          acc[2 * j] = dot2(lo, xv[i], acc[2 * j]);
+          acc[2 * j + 1] = dot2(hi, xv[i], acc[2 * j + 1]);
+        }
+      }
+    };
+    // two chunks in flight: slot, slot + ks, ...; a slot at or past the last
+    // chunk adds nothing
+    load(slot, u0, x0);
+    for (int c = slot; c < nch; c += 2 * L.ks) {
+      load(c + L.ks, u1, x1);
+      fma_chunk(u0, x0);
+      if (c + L.ks >= nch) break;
+      load(c + 2 * L.ks, u0, x0);
+      fma_chunk(u1, x1);
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) part[slot * rank + 8 * b + c] = acc[c];
+  }
+  __syncthreads();
+  const int col = t % rank, seg = t / rank;
+  if (seg < L.nseg) {  // level 1: slots seg, seg + nseg, ... in order
+    float sum = 0.f;
+    for (int q = seg; q < L.ks; q += L.nseg) sum += part[q * rank + col];
+    segs[seg * rank + col] = sum;
+  }
+  __syncthreads();
+  if (t < rank) {  // level 2: the segments in order
+    float sum = 0.f;
+    for (int q = 0; q < L.nseg; ++q) sum += segs[q * rank + t];
+    ah[t] = __float2half(sum);
+  }
+  __syncthreads();
+  return ah;
+}
+
 // Geometry of one lane launch (or one role of a launch): every item has N
 // rows of K codes; rows are cut into 64-row units of NIT = LRP iterations,
 // taken in rounds of PD iterations; wave w of an item runs rounds
@@ -129,12 +196,13 @@ struct LaneGeom {
   int items;
 };
 
-// Item data of a lane launch.  A source type provides, per item:
-//   lora(item)            the low-rank term is present
-//   codes/scales/zeros/sv/bias/u(item)   the item's tensors (bias may be null)
-//   x8(item, k)           8 halves of the item's activation row at k (k % 8 == 0)
-//   load_a(item, j)       a[j] when a is given (not XU)
-//   store(item, n, v)     the item's output row n
+// Item data of a lane launch.  A source type's bind(item) gives a view of one
+// item with:
+//   lora()                the low-rank term is present
+//   codes/scales/zeros/sv/bias/u()   the item's tensors (bias may be null)
+//   x8(k)                 8 halves of the item's activation row at k (k % 8 == 0)
+//   load_a(j)             a[j] when a is given (not XU)
+//   store(n, v)           the item's output row n
 //
 // Work per wave: PD iterations of loads in flight ahead of use.  Loads are
 // issued unconditionally (iterations past the wave's last one re-read its
@@ -150,13 +218,16 @@ struct LaneGeom {
 // partials are summed in LDS in a fixed order and rounded to fp16 once.
 // Then the waves take their x slices and stream their rows.  An item whose
 // rows are spread over several workgroups has each of them form a.
-template <class Src, int BITS, bool SYM, int LRP, int NP, int PD, int NSV, bool HASB, bool XU>
-__device__ __forceinline__ void lane_run(const Src& src, const LaneGeom& lg, int wv, int wvb,
+template <class Src, int BITS, bool SYM, int LRP, int NP, int PD, int NSV, bool HASB, bool XU,
+          bool PAIR = false>
+__device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, int wv, int wvb,
                                          float* xu_lds) {
   constexpr int C = lane_piece_codes<BITS>();  // codes per piece
   constexpr int RPI = 64 / LRP;                // rows per iteration
-  constexpr int NIT = LRP;                     // iterations per 64-row unit
+  constexpr int NIT = LRP;                     // row groups per 64-row unit
+  constexpr int M2 = PAIR ? 2 : 1;             // matrices
   static_assert(NIT % PD == 0, "ring depth must divide the unit");
+  static_assert(!PAIR || (PD % 2 == 0 && !XU && !HASB), "pairs: even depth, a given");
   static_assert(NP == 1 || LRP == 64, "several pieces per lane take whole waves per row");
   const int lane = threadIdx.x & 63;
   const int item = wv / lg.wpi;
@@ -165,6 +236,7 @@ __device__ __forceinline__ void lane_run(const Src& src, const LaneGeom& lg, int
   const int rb = (wv - item * lg.wpi) * lg.rpw;
   const int nr = min(lg.rpw, lg.rounds - rb);
   if (!XU && nr <= 0) return;  // (XU: every wave takes part in forming a)
+  const auto src = srcs.bind(item);
   const int rlast = min(rb + max(nr, 1), lg.rounds) - 1;  // idle waves re-read a valid round
   const int N = lg.N, G = lg.G, kw = lg.kw, rank = lg.rank;
   const int ri = lane / LRP, p = lane % LRP;
@@ -188,8 +260,8 @@ __device__ __forceinline__ void lane_run(const Src& src, const LaneGeom& lg, int
       c2[j] = 0.f;
 #pragma unroll
       for (int blk = 0; blk < C / 16; ++blk) {
-        const f16x8 in0 = __builtin_bit_cast(f16x8, src.x8(item, pc[j] * C + 16 * blk));
-        const f16x8 in1 = __builtin_bit_cast(f16x8, src.x8(item, pc[j] * C + 16 * blk + 8));
+        const f16x8 in0 = __builtin_bit_cast(f16x8, src.x8(pc[j] * C + 16 * blk));
+        const f16x8 in1 = __builtin_bit_cast(f16x8, src.x8(pc[j] * C + 16 * blk + 8));
         _Float16 in[16], o[16];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -212,7 +284,12 @@ __device__ __forceinline__ void lane_run(const Src& src, const LaneGeom& lg, int
     }
   };
   if constexpr (!XU) load_x();
-  const bool lora = src.lora(item);
+  const bool lora = src.lora();
+  // the item's tensors of matrix m (PAIR: 0 and 1, iterations alternating)
+  auto t_codes = [&](int m) { if constexpr (PAIR) return src.codes(m); else return src.codes(); };
+  auto t_scales = [&](int m) { if constexpr (PAIR) return src.scales(m); else return src.scales(); };
+  auto t_zeros = [&](int m) { if constexpr (PAIR) return src.zeros(m); else return src.zeros(); };
+  auto t_sv = [&](int m) { if constexpr (PAIR) return src.sv(m); else return src.sv(); };
   int svo[NSV];  // element offset of the dword within an SV row
 #pragma unroll
   for (int k = 0; k < NSV; ++k) {
@@ -223,20 +300,26 @@ __device__ __forceinline__ void lane_run(const Src& src, const LaneGeom& lg, int
   // Buffer loads: one descriptor per tensor of the item (sized to it, so rows
   // past N read 0 and add 0); a lane's offset is its constant part plus the
   // iteration's first row times the row pitch.  Row of iteration i:
-  // (i / NIT) * 64 + (i % NIT) * RPI + ri = RPI i + ri.
+  // (i / NIT) * 64 + (i % NIT) * RPI + ri = RPI i + ri (PAIR: matrix i % 2,
+  // row RPI (i / 2) + ri).
   const int rowbytes = kw * 4;
-  const auto rc = __builtin_amdgcn_make_buffer_rsrc((void*)src.codes(item), 0, N * rowbytes,
-                                                    kBufferFlags);
-  const auto rsc = __builtin_amdgcn_make_buffer_rsrc((void*)src.scales(item), 0, N * G * 2,
+  decltype(__builtin_amdgcn_make_buffer_rsrc(nullptr, 0, 0, 0)) rc[M2], rsc[M2], rz[M2], rsv[M2];
+#pragma unroll
+  for (int m = 0; m < M2; ++m) {
+    rc[m] = __builtin_amdgcn_make_buffer_rsrc((void*)t_codes(m), 0, N * rowbytes, kBufferFlags);
+    rsc[m] = __builtin_amdgcn_make_buffer_rsrc((void*)t_scales(m), 0, N * G * 2, kBufferFlags);
+    rz[m] = __builtin_amdgcn_make_buffer_rsrc((void*)(SYM ? t_scales(m) : t_zeros(m)), 0,
+                                              N * G * 2, kBufferFlags);
+    // without a low-rank term the SV descriptor has no records: its loads read 0
+    rsv[m] = __builtin_amdgcn_make_buffer_rsrc(lora ? (void*)t_sv(m) : (void*)t_codes(m), 0,
+                                               lora ? N * rank * 2 : 0, kBufferFlags);
+  }
+  auto bias_ptr = [&]() -> void* {
+    if constexpr (HASB) return (void*)src.bias();
+    else return nullptr;
+  };
+  const auto rbi = __builtin_amdgcn_make_buffer_rsrc(bias_ptr(), 0, HASB ? N * 2 : 0,
                                                      kBufferFlags);
-  const auto rz = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(SYM ? src.scales(item) : src.zeros(item)), 0, N * G * 2, kBufferFlags);
-  // without a low-rank term the SV loads read the codes (finite, times a = 0)
-  const auto rsv = __builtin_amdgcn_make_buffer_rsrc(
-      lora ? (void*)src.sv(item) : (void*)src.codes(item), 0, lora ? N * rank * 2 : 4,
-      kBufferFlags);
-  const auto rbi = __builtin_amdgcn_make_buffer_rsrc(HASB ? (void*)src.bias(item) : nullptr, 0,
-                                                     HASB ? N * 2 : 0, kBufferFlags);
   const int svr = lora ? rank : 0;
   int vc[NP], vs[NP];
 #pragma unroll
@@ -254,19 +337,21 @@ __device__ __forceinline__ void lane_run(const Src& src, const LaneGeom& lg, int
   uint32_t sw[PD][NP], zw[PD][NP], bw[PD], vw[PD][NSV];
   // loads of iteration d of the wave's round r (rounds past the last re-read it)
   auto issue = [&](int d, int r) {
-    const int n0 = RPI * (min(rb + r, rlast) * PD + d);  // uniform
+    const int m = PAIR ? (d & 1) : 0;  // compile-time once unrolled
+    const int it = min(rb + r, rlast) * PD + d;
+    const int n0 = RPI * (PAIR ? it >> 1 : it);  // uniform
     if constexpr (HASB) bw[d] = __builtin_amdgcn_raw_buffer_load_b16(rbi, vb + n0 * 2, 0, 0);
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
-      cw[d][j] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, vc[j] + n0 * rowbytes, 0, kBufferNT));
-      sw[d][j] = __builtin_amdgcn_raw_buffer_load_b16(rsc, vs[j] + n0 * G * 2, 0, 0);
+      cw[d][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rc[m], vc[j] + n0 * rowbytes, 0, kBufferNT));
+      sw[d][j] = __builtin_amdgcn_raw_buffer_load_b16(rsc[m], vs[j] + n0 * G * 2, 0, 0);
       if constexpr (!SYM)
-        zw[d][j] = __builtin_amdgcn_raw_buffer_load_b16(rz, vs[j] + n0 * G * 2, 0, 0);
+        zw[d][j] = __builtin_amdgcn_raw_buffer_load_b16(rz[m], vs[j] + n0 * G * 2, 0, 0);
     }
 #pragma unroll
     for (int k = 0; k < NSV; ++k)
-      vw[d][k] = __builtin_amdgcn_raw_buffer_load_b32(rsv, vsv[k] + n0 * svr * 2, 0, 0);
+      vw[d][k] = __builtin_amdgcn_raw_buffer_load_b32(rsv[m], vsv[k] + n0 * svr * 2, 0, 0);
   };
   // The prologue's loads go out in the loop's order (scheduling barriers on
   // both sides of every issue), so the wait the compiler places at the loop
@@ -282,67 +367,9 @@ __device__ __forceinline__ void lane_run(const Src& src, const LaneGeom& lg, int
   if constexpr (!XU) prologue();
 
   // ---- a pairs of this lane's SV dwords (zero past the rank) ----
-  uint32_t ap[NSV];
+  uint32_t ap[M2][NSV];
   if constexpr (XU) {
-    // a = fp16(x U) in this workgroup (layout in LaneXu)
-    const LaneXu L(rank);
-    const int t = threadIdx.x;
-    float* part = xu_lds;                      // (ks, rank)
-    float* segs = xu_lds + L.ks * rank;        // (nseg, rank)
-    __half* ah = (__half*)(segs + L.nseg * rank);
-    if (lora) {
-      const int b = t % L.nb, slot = t / L.nb;
-      if (slot < L.ks) {
-        const int nch = lg.K / 8;  // 8-row chunks
-        const __half* ub = src.u(item) + 8 * b;
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        u32x4 u0[8], u1[8], x0, x1;
-        auto load = [&](int c, u32x4 (&u)[8], u32x4& xv) {
-          c = min(c, nch - 1);  // past the end: re-read the last chunk (not used)
-          xv = src.x8(item, 8 * c);
-#pragma unroll
-          for (int q = 0; q < 8; ++q) u[q] = *(const u32x4*)(ub + (int64_t)(8 * c + q) * rank);
-        };
-        auto fma_chunk = [&](const u32x4 (&u)[8], const u32x4& xv) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {  // rows 2i, 2i + 1 against (x_2i, x_2i+1)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const uint32_t lo = __builtin_amdgcn_perm(u[2 * i + 1][j], u[2 * i][j], 0x05040100u);
-              const uint32_t hi = __builtin_amdgcn_perm(u[2 * i + 1][j], u[2 * i][j], 0x07060302u);
-              acc[2 * j] = dot2(lo, xv[i], acc[2 * j]);
-              acc[2 * j + 1] = dot2(hi, xv[i], acc[2 * j + 1]);
-            }
-          }
-        };
-        // two chunks in flight: slot, slot + ks, ...; a slot at or past the
-        // last chunk adds nothing
-        load(slot, u0, x0);
-        for (int c = slot; c < nch; c += 2 * L.ks) {
-          load(c + L.ks, u1, x1);
-          fma_chunk(u0, x0);
-          if (c + L.ks >= nch) break;
-          load(c + 2 * L.ks, u0, x0);
-          fma_chunk(u1, x1);
-        }
-#pragma unroll
-        for (int c = 0; c < 8; ++c) part[slot * rank + 8 * b + c] = acc[c];
-      }
-      __syncthreads();
-      const int col = t % rank, seg = t / rank;
-      if (seg < L.nseg) {  // level 1: slots seg, seg + nseg, ... in order
-        float sum = 0.f;
-        for (int q = seg; q < L.ks; q += L.nseg) sum += part[q * rank + col];
-        segs[seg * rank + col] = sum;
-      }
-      __syncthreads();
-      if (t < rank) {  // level 2: the segments in order
-        float sum = 0.f;
-        for (int q = 0; q < L.nseg; ++q) sum += segs[q * rank + t];
-        ah[t] = __float2half(sum);
-      }
-      __syncthreads();
-    }
+    __half* ah = lane_xu_phase(src, lg.K, rank, lora, xu_lds);
 #pragma unroll
     for (int k = 0; k < NSV; ++k) {
       const int j = p + k * LRP;
@@ -351,32 +378,40 @@ __device__ __forceinline__ void lane_run(const Src& src, const LaneGeom& lg, int
         pr[0] = (_Float16)__half2float(ah[2 * j]);
         pr[1] = (_Float16)__half2float(ah[2 * j + 1]);
       }
-      ap[k] = __builtin_bit_cast(uint32_t, pr);
+      ap[0][k] = __builtin_bit_cast(uint32_t, pr);
     }
     if (nr <= 0) return;  // a wave with no rows of its own
     load_x();
     prologue();
   } else {
 #pragma unroll
-    for (int k = 0; k < NSV; ++k) {
-      const int j = p + k * LRP;
-      f16x2 pr = {(_Float16)0.f, (_Float16)0.f};
-      if (lora && 2 * j < rank) {
-        pr[0] = (_Float16)__half2float(src.load_a(item, 2 * j));
-        pr[1] = (_Float16)__half2float(src.load_a(item, 2 * j + 1));
+    for (int m = 0; m < M2; ++m)
+#pragma unroll
+      for (int k = 0; k < NSV; ++k) {
+        const int j = p + k * LRP;
+        f16x2 pr = {(_Float16)0.f, (_Float16)0.f};
+        if (lora && 2 * j < rank) {
+          if constexpr (PAIR) {
+            pr[0] = (_Float16)__half2float(src.load_a(m, 2 * j));
+            pr[1] = (_Float16)__half2float(src.load_a(m, 2 * j + 1));
+          } else {
+            pr[0] = (_Float16)__half2float(src.load_a(2 * j));
+            pr[1] = (_Float16)__half2float(src.load_a(2 * j + 1));
+          }
+        }
+        ap[m][k] = __builtin_bit_cast(uint32_t, pr);
       }
-      ap[k] = __builtin_bit_cast(uint32_t, pr);
-    }
   }
 
   const DecodeConsts dk = DecodeConsts::make();
   constexpr uint32_t xor_mask = SYM ? (BITS == 2 ? 0xAAAAAAAAu : 0x88888888u) : 0u;
   for (int r = 0; r < nr; ++r) {
     const int i0 = (rb + r) * PD;  // first iteration of the round
-    float yv = 0.f;
+    float yv = 0.f, yu = 0.f;      // (PAIR: matrix 0 and matrix 1 of a row)
 #pragma unroll
     for (int d = 0; d < PD; ++d) {
       const int i = i0 + d;
+      const int m = PAIR ? (d & 1) : 0;
       float part = 0.f;
 #pragma unroll
       for (int j = 0; j < NP; ++j) {
@@ -410,57 +445,30 @@ __device__ __forceinline__ void lane_run(const Src& src, const LaneGeom& lg, int
       }
       if constexpr (HASB) part = fmaf(bsel, __half2float(__ushort_as_half((uint16_t)bw[d])), part);
 #pragma unroll
-      for (int k = 0; k < NSV; ++k) part = dot2(vw[d][k], ap[k], part);
+      for (int k = 0; k < NSV; ++k) part = dot2(vw[d][k], ap[m][k], part);
       __builtin_amdgcn_sched_barrier(0);
       issue(d, r + 1);
       __builtin_amdgcn_sched_barrier(0);
       const float tot = lane_group_sum<LRP>(part);
-      yv = p == (i & (NIT - 1)) ? tot : yv;
+      if constexpr (PAIR) {
+        const bool mine = p == ((i >> 1) & (NIT - 1));
+        if (m == 0) yv = mine ? tot : yv;
+        else yu = mine ? tot : yu;
+      } else {
+        yv = p == (i & (NIT - 1)) ? tot : yv;
+      }
     }
     // lane l holds row (l % LRP) * RPI + l / LRP of the unit; the lanes of
-    // the round's PD iterations store
-    const int u = i0 / NIT, it0 = i0 & (NIT - 1);
+    // the round's row groups store
+    constexpr int RG = PAIR ? PD / 2 : PD;  // row groups per round
+    const int g0 = PAIR ? i0 >> 1 : i0;
+    const int u = g0 / NIT, it0 = g0 & (NIT - 1);
     const int n = u * 64 + p * RPI + ri;
-    if (p >= it0 && p < it0 + PD && n < N) src.store(item, n, yv);
+    if (p >= it0 && p < it0 + RG && n < N) {
+      if constexpr (PAIR) src.store(n, yv, yu);
+      else src.store(n, yv);
+    }
   }
-}
-
-// Dense items (glq_gemv.hip): item i at base + i * stride, one token row.
-struct DenseLaneSrc {
-  const DenseArgs& a;
-  __device__ bool lora(int) const { return a.sv != nullptr && a.sh.rank > 0; }
-  __device__ const uint32_t* codes(int item) const { return a.codes + (int64_t)item * a.codes_es; }
-  __device__ const __half* scales(int item) const { return a.scales + (int64_t)item * a.sz_es; }
-  __device__ const __half* zeros(int item) const { return a.zeros + (int64_t)item * a.sz_es; }
-  __device__ const __half* sv(int item) const { return a.sv + (int64_t)item * a.sv_es; }
-  __device__ const __half* bias(int item) const { return a.bias + (int64_t)item * a.bias_es; }
-  __device__ const __half* u(int item) const { return a.u + (int64_t)item * a.u_es; }
-  __device__ u32x4 x8(int item, int k) const {
-    return *(const u32x4*)(a.x + (int64_t)item * a.x_es + k);
-  }
-  __device__ __half load_a(int item, int j) const {
-    if (a.xu) return a.xu[(int64_t)item * a.xu_es + j];
-    const float* pp = a.apart + (int64_t)item * a.P * a.M * a.sh.rpad + j;
-    return __float2half(sum_strided(pp, (int64_t)a.M * a.sh.rpad, a.P));
-  }
-  __device__ void store(int item, int n, float v) const {
-    a.y[(int64_t)item * a.y_es + n] = __float2half(v);
-  }
-};
-
-struct LaneArgs {
-  DenseArgs a;
-  LaneGeom g;
-};
-
-template <int BITS, bool SYM, int LRP, int PD, int NSV, bool HASB, bool XU>
-__global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) {
-  extern __shared__ float xu_lds[];
-  constexpr int WPB = XU ? 8 : 4;  // waves per workgroup
-  const DenseLaneSrc src{la.a};
-  const int wvb = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  lane_run<DenseLaneSrc, BITS, SYM, LRP, 1, PD, NSV, HASB, XU>(src, la.g, blockIdx.x * WPB + wvb,
-                                                               wvb, xu_lds);
 }
 
 }  // namespace glq

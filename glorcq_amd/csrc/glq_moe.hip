@@ -36,6 +36,7 @@
 #include <algorithm>
 #include <cstring>
 
+#include "glq_moe_route.h"
 #include "glq_stream.h"
 
 namespace glq {
@@ -216,22 +217,6 @@ __device__ __forceinline__ int align_up_dev(int v, int a) { return (v + a - 1) /
 // 1. Router + gate/up cluster partials (256-thread workgroups)
 // ---------------------------------------------------------------------------
 constexpr int kRouteThreads = 256;
-
-// Routing keys: the order (logit descending, expert index ascending) as one
-// unsigned compare.  The fp16 logit's bits map to an order-preserving 16-bit
-// value (negative: all bits flipped; positive: sign bit set; -0 taken as +0),
-// above 0xFFFF - e.  moe_key_logit inverts it.
-__device__ __forceinline__ uint32_t moe_key(uint32_t bits, int e) {  // bits: the fp16 pattern
-  uint32_t u = bits & 0xFFFFu;
-  if (u == 0x8000u) u = 0u;
-  u = (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
-  return (u << 16) | (uint32_t)(0xFFFF - e);
-}
-__device__ __forceinline__ float moe_key_logit(uint32_t k) {
-  uint32_t u = k >> 16;
-  u = (u & 0x8000u) ? (u & 0x7FFFu) : (~u & 0xFFFFu);
-  return __half2float(__ushort_as_half((unsigned short)u));
-}
 
 __host__ __device__ inline int moe_lg_stride(int E) { return ((E + 3) & ~3) + 4; }
 
@@ -1062,7 +1047,8 @@ extern "C" int64_t glq_moe_workspace_bytes(const glq_moe_params* p) {
   glq::clear_error();
   glq::MoePlan P;
   if (glq::moe_plan(p, P) != GLQ_OK) return -1;
-  return P.ws_need;
+  const int64_t lane = glq::moe_lane_workspace_bytes(p);  // the path glq_moe_decode takes
+  return lane >= 0 ? lane : P.ws_need;
 }
 
 extern "C" int glq_moe_decode(const glq_moe_params* p, void* workspace, int64_t workspace_bytes,
@@ -1072,6 +1058,8 @@ extern "C" int glq_moe_decode(const glq_moe_params* p, void* workspace, int64_t 
   MoePlan P;
   int rc = moe_plan(p, P);
   if (rc) return rc;
+  if (moe_lane_workspace_bytes(p) >= 0)  // a few tokens: the lane path
+    return moe_lane_decode(p, workspace, workspace_bytes, (hipStream_t)stream);
   GLQ_CHECK(workspace != nullptr && workspace_bytes >= P.ws_need,
             "workspace of %lld bytes needed (got %lld)", (long long)P.ws_need,
             (long long)workspace_bytes);

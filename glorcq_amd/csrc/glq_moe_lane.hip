@@ -1,0 +1,679 @@
+// MoE block decode step for a few tokens (glq_moe_decode with tokens <=
+// kMoeLaneMaxB): GraphCompatibleMoeBlock.forward (inference/moe_block.py:
+// 381-436) on the lane-sliced GEMV of glq_lane.h, one token row per work item,
+// no cross-workgroup handshake inside any launch:
+//
+//  1. moe_lane_route_kernel  one workgroup per token: router logits (fp32 dot
+//                            products rounded to fp16 once), softmax, top-k
+//                            (ties to the lower index), optional
+//                            renormalisation (moe_block.py:386-392), the
+//                            shared-expert gate sigmoid(fp16 logit); the other
+//                            workgroups run the shared expert's gate and up
+//                            rows in pairs and write its inter = fp16(fp16(
+//                            silu(g)) * u) (moe_block.py:465-468)
+//  2. moe_lane_xu_kernel     (with LoRA) one workgroup per (pick, gate/up):
+//                            a = fp16(x U_c) of the pick's cluster (the
+//                            cluster-shared precompute, moe_block.py:290-322)
+//  3. moe_lane_gu_kernel     routed gate and up rows of every pick in pairs
+//                            (both matrices' row n in one lane group), with
+//                            their a SV^T terms, writing the pick's inter
+//  4. moe_lane_down_kernel   routed down rows of every pick without the
+//                            low-rank term (fp32); with LoRA, workgroups past
+//                            them form each pick's a_down = fp16(inter U_down)
+//  5. moe_lane_sdown_kernel  the shared expert's down rows, each row's store
+//                            combining out = fp16(sum_k w_k (y_k + a_down,k
+//                            SV_k^T) + gate * fp16(shared)) (+ the caller's
+//                            residual); without a shared expert
+//                            moe_lane_combine_kernel does the sum alone
+//
+// Only the picked experts' weights are read, a pick's U once.  Every sum has
+// a fixed order, so the step gives the same bits on every run; routing and the
+// combine's order of terms follow the many-token launches (glq_moe.hip).
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
+#include "glq_internal.h"
+#include "glq_lane.h"
+#include "glq_moe_route.h"
+#include "glq_stream.h"
+
+namespace glq {
+
+constexpr int kMoeLaneThreads = 512;  // 8 waves (the lane x U form)
+constexpr int kMoeLaneWaves = 4096;   // target waves per lane role
+constexpr int64_t kMoeLaneXuAllBytes = 12ll << 20;  // all clusters' x U in the router launch
+
+struct MoeLaneArgs {
+  int B, H, E, I, SI, topk, norm, C, rank;
+  int urows[3];
+  const __half* h;
+  const __half* rw;
+  const __half* sgw;
+  const uint32_t* codes[3];
+  const __half* scales[3];
+  const __half* zeros[3];
+  int64_t c_es[3], s_es[3], sv_es[3];
+  const __half* U[3];
+  const int32_t* clus[3];
+  const int32_t* uslot[2];
+  const __half* SV[3];
+  const uint32_t* scodes[3];
+  const __half* sscales[3];
+  const __half* szeros[3];
+  // workspace
+  int32_t* sel;     // [P] expert of pick p = t * topk + k
+  __half* wts;      // [P] routing weights
+  __half* sg;       // [B] shared-expert gate
+  __half* agu;      // [2][P][rank] a of each pick's gate and up, or (xuall)
+                    // [2][C][B][rank] a of every cluster's gate and up
+  int xuall;        // 1: a for every cluster in the router's launch
+  __half* inter;    // [P][I] each pick's inter
+  float* yb;        // [P][H] routed down outputs without the low-rank term
+  __half* ad;       // [P][rank] a_down of each pick
+  __half* sinter;   // [B][SI] the shared expert's inter
+  // outputs
+  __half* out;
+  const __half* res;
+  __half* logits;
+  LaneGeom gSGU, gRGU, gRD, gSD;
+  int nrd;          // workgroups of the routed down rows
+};
+
+__device__ __forceinline__ int moe_lane_clamp(int v, int n) { return min(max(v, 0), n - 1); }
+
+// U row of matrix m (gate 0, up 1, down 2) for expert e.
+__device__ __forceinline__ const __half* moe_lane_u(const MoeLaneArgs& a, int m, int e) {
+  const int K = m == 2 ? a.I : a.H;
+  int row;
+  if (m == 2) {
+    row = moe_lane_clamp(a.clus[2][e], a.urows[2]);  // the pool row itself
+  } else {
+    const int c = moe_lane_clamp(a.clus[m][e], a.C);
+    row = moe_lane_clamp(a.uslot[m] ? a.uslot[m][c] : c, a.urows[m]);
+  }
+  return a.U[m] + (int64_t)row * K * a.rank;
+}
+
+// ---- item views (glq_lane.h source types) ----
+// Routed gate and up of pick p, in pairs; stores the pick's inter.
+struct RguItem {
+  const MoeLaneArgs& a;
+  int p, e;
+  const __half* x;
+  __device__ bool lora() const { return a.rank > 0 && a.SV[0] != nullptr; }
+  __device__ const uint32_t* codes(int m) const { return a.codes[m] + (int64_t)e * a.c_es[m]; }
+  __device__ const __half* scales(int m) const { return a.scales[m] + (int64_t)e * a.s_es[m]; }
+  __device__ const __half* zeros(int m) const { return a.zeros[m] + (int64_t)e * a.s_es[m]; }
+  __device__ const __half* sv(int m) const { return a.SV[m] + (int64_t)e * a.sv_es[m]; }
+  __device__ u32x4 x8(int k) const { return *(const u32x4*)(x + k); }
+  __device__ __half load_a(int m, int j) const {
+    if (a.xuall) {
+      const int c = moe_lane_clamp(a.clus[m][e], a.C);
+      return a.agu[(((int64_t)m * a.C + c) * a.B + p / a.topk) * a.rank + j];
+    }
+    return a.agu[((int64_t)m * a.B * a.topk + p) * a.rank + j];
+  }
+  __device__ void store(int n, float g, float u) const {
+    a.inter[(int64_t)p * a.I + n] = swiglu_fp16(g, u);
+  }
+};
+struct RguSrc {
+  const MoeLaneArgs& a;
+  __device__ RguItem bind(int p) const {
+    return RguItem{a, p, a.sel[p], a.h + (int64_t)(p / a.topk) * a.H};
+  }
+};
+
+// Routed down rows of pick p without the low-rank term (added at the combine).
+struct RdItem {
+  const MoeLaneArgs& a;
+  int p, e;
+  __device__ bool lora() const { return false; }
+  __device__ const uint32_t* codes() const { return a.codes[2] + (int64_t)e * a.c_es[2]; }
+  __device__ const __half* scales() const { return a.scales[2] + (int64_t)e * a.s_es[2]; }
+  __device__ const __half* zeros() const { return a.zeros[2] + (int64_t)e * a.s_es[2]; }
+  __device__ const __half* sv() const { return nullptr; }
+  __device__ const __half* bias() const { return nullptr; }
+  __device__ const __half* u() const { return nullptr; }
+  __device__ u32x4 x8(int k) const { return *(const u32x4*)(a.inter + (int64_t)p * a.I + k); }
+  __device__ __half load_a(int) const { return __float2half(0.f); }
+  __device__ void store(int n, float v) const { a.yb[(int64_t)p * a.H + n] = v; }
+};
+struct RdSrc {
+  const MoeLaneArgs& a;
+  __device__ RdItem bind(int p) const { return RdItem{a, p, a.sel[p]}; }
+};
+
+// x U jobs: the input row and U of one (pick, matrix).
+struct XuJob {
+  const __half* x;
+  const __half* uu;
+  __device__ const __half* u() const { return uu; }
+  __device__ u32x4 x8(int k) const { return *(const u32x4*)(x + k); }
+};
+
+// Shared gate and up of token t, in pairs; stores the shared inter.
+struct SguItem {
+  const MoeLaneArgs& a;
+  int t;
+  __device__ bool lora() const { return false; }
+  __device__ const uint32_t* codes(int m) const { return a.scodes[m]; }
+  __device__ const __half* scales(int m) const { return a.sscales[m]; }
+  __device__ const __half* zeros(int m) const { return a.szeros[m]; }
+  __device__ const __half* sv(int) const { return nullptr; }
+  __device__ u32x4 x8(int k) const { return *(const u32x4*)(a.h + (int64_t)t * a.H + k); }
+  __device__ __half load_a(int, int) const { return __float2half(0.f); }
+  __device__ void store(int n, float g, float u) const {
+    a.sinter[(int64_t)t * a.SI + n] = swiglu_fp16(g, u);
+  }
+};
+struct SguSrc {
+  const MoeLaneArgs& a;
+  __device__ SguItem bind(int t) const { return SguItem{a, t}; }
+};
+
+// Routed part of output row n of token t: sum_k w_k (y_k[n] + a_down,k
+// SV_down,k[n]^T), in pick order (the many-token combine's order).
+__device__ __forceinline__ float moe_lane_routed(const MoeLaneArgs& a, int t, int n) {
+  float acc = 0.f;
+  for (int k = 0; k < a.topk; ++k) {
+    const int p = t * a.topk + k;
+    float y = a.yb[(int64_t)p * a.H + n];
+    if (a.rank > 0 && a.SV[2]) {
+      const int e = a.sel[p];
+      const __half* sv = a.SV[2] + (int64_t)e * a.sv_es[2] + (int64_t)n * a.rank;
+      const __half* ad = a.ad + (int64_t)p * a.rank;
+      float l = 0.f;
+      for (int j = 0; j < a.rank; j += 8) {
+        const u32x4 s8 = *(const u32x4*)(sv + j), a8 = *(const u32x4*)(ad + j);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) l = dot2(s8[q], a8[q], l);
+      }
+      y += l;
+    }
+    acc = fmaf(__half2float(a.wts[p]), y, acc);
+  }
+  return acc;
+}
+
+// Shared down rows of token t, the combine in each row's store.
+struct SdItem {
+  const MoeLaneArgs& a;
+  int t;
+  __device__ bool lora() const { return false; }
+  __device__ const uint32_t* codes() const { return a.scodes[2]; }
+  __device__ const __half* scales() const { return a.sscales[2]; }
+  __device__ const __half* zeros() const { return a.szeros[2]; }
+  __device__ const __half* sv() const { return nullptr; }
+  __device__ const __half* bias() const { return nullptr; }
+  __device__ const __half* u() const { return nullptr; }
+  __device__ u32x4 x8(int k) const {
+    return *(const u32x4*)(a.sinter + (int64_t)t * a.SI + k);
+  }
+  __device__ __half load_a(int) const { return __float2half(0.f); }
+  // out = fp16(routed + gate * fp16(shared)) (+ residual)
+  __device__ void store(int n, float v) const {
+    float acc = moe_lane_routed(a, t, n);
+    acc = fmaf(__half2float(a.sg[t]), __half2float(__float2half(v)), acc);
+    float o = __half2float(__float2half(acc));
+    if (a.res) o += __half2float(a.res[(int64_t)t * a.H + n]);
+    a.out[(int64_t)t * a.H + n] = __float2half(o);
+  }
+};
+struct SdSrc {
+  const MoeLaneArgs& a;
+  __device__ SdItem bind(int t) const { return SdItem{a, t}; }
+};
+
+// ---- router: one workgroup per token ----
+// Logits of the E router rows (+ the shared-expert gate row) as fp32 dot
+// products over the lanes (16-byte loads, v_dot2), each rounded to fp16 once;
+// a wave loads RB rows at once (RC 8-half chunks a lane each).  Then the
+// routing of moe_topk_ranks (glq_moe.hip) for this one token: thread e ranks
+// expert e by counting the keys above its own, wave 0 forms the softmax sum
+// (a cross-lane sum in the same order) and the weights.
+template <int RC>
+__device__ void moe_lane_router(const MoeLaneArgs& a, int t, unsigned char* smem) {
+  constexpr int RB = RC >= 8 ? 2 : 16 / RC;  // rows per wave per pass
+  uint16_t* lgh = (uint16_t*)smem;                                    // [E + 1] fp16 logits
+  uint32_t* keys = (uint32_t*)(smem + ((2 * (a.E + 1) + 15) & ~15));  // [E]
+  int* sl = (int*)(keys + a.E);                                       // [topk]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nrow = a.E + (a.sgw ? 1 : 0);
+  const __half* hx = a.h + (int64_t)t * a.H;
+  u32x4 hv[RC];
+#pragma unroll
+  for (int j = 0; j < RC; ++j) {
+    const int k = 8 * lane + 512 * j;
+    hv[j] = k < a.H ? *(const u32x4*)(hx + k) : u32x4{0u, 0u, 0u, 0u};
+  }
+  for (int r0 = RB * wave; r0 < nrow; r0 += 8 * RB) {
+    u32x4 v[RB][RC];
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      const int r = min(r0 + q, nrow - 1);
+      const __half* w = r < a.E ? a.rw + (int64_t)r * a.H : a.sgw;
+#pragma unroll
+      for (int j = 0; j < RC; ++j) {
+        const int k = 8 * lane + 512 * j;
+        v[q][j] = k < a.H ? *(const u32x4*)(w + k) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      float sacc = 0.f;
+#pragma unroll
+      for (int j = 0; j < RC; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sacc = dot2(v[q][j][c], hv[j][c], sacc);
+      sacc = lane_group_sum<64>(sacc);
+      if (lane == 0 && r0 + q < nrow) lgh[r0 + q] = __half_as_ushort(__float2half(sacc));
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < a.E; e += kMoeLaneThreads) {
+    keys[e] = moe_key(lgh[e], e);
+    if (a.logits) a.logits[(int64_t)t * a.E + e] = __ushort_as_half(lgh[e]);
+  }
+  if (tid == 0)
+    a.sg[t] = a.sgw ? __float2half(1.f / (1.f + expf(-__half2float(__ushort_as_half(lgh[a.E])))))
+                    : __float2half(1.f);
+  __syncthreads();
+  for (int e = tid; e < a.E; e += kMoeLaneThreads) {
+    const uint32_t ke = keys[e];
+    int r = 0;
+    for (int j = 0; j < a.E; ++j) r += (int)(keys[j] > ke);
+    if (r < a.topk) sl[r] = e;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const float mx = moe_key_logit(keys[sl[0]]);
+    float sum = 0.f;
+    for (int e = lane; e < a.E; e += 64) sum += expf(moe_key_logit(keys[e]) - mx);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+    const int e = lane < a.topk ? sl[lane] : 0;
+    const float w = lane < a.topk ? expf(moe_key_logit(keys[e]) - mx) / sum : 0.f;
+    float ws = 0.f;
+    if (a.norm)
+      for (int j = 0; j < a.topk; ++j) ws += __shfl(w, j);
+    if (lane < a.topk) {
+      a.sel[t * a.topk + lane] = e;
+      a.wts[t * a.topk + lane] = __float2half(a.norm ? w / ws : w);
+    }
+  }
+}
+
+// ---- kernels ----
+__device__ __forceinline__ int moe_lane_wave() {
+  return (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
+// Workgroups [0, B): the router of each token; then (xuall) one per (matrix,
+// cluster, token) forming a = fp16(h_t U_c); then the shared expert's
+// gate/up rows.
+template <int SBITS, int SLRP, int RC>
+__global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_route_kernel(MoeLaneArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  int b = blockIdx.x;
+  if (b < a.B) {
+    moe_lane_router<RC>(a, b, smem);
+    return;
+  }
+  b -= a.B;
+  const int nxu = a.xuall ? 2 * a.C * a.B : 0;
+  if (b < nxu) {  // job b = (m C + c) B + t
+    const int t = b % a.B, mc = b / a.B, m = mc / a.C, c = mc - m * a.C;
+    const int row = moe_lane_clamp(a.uslot[m] ? a.uslot[m][c] : c, a.urows[m]);
+    const __half* u = a.U[m] + (int64_t)row * a.H * a.rank;
+    const __half* ah = lane_xu_phase(XuJob{a.h + (int64_t)t * a.H, u}, a.H, a.rank, true,
+                                     (float*)smem);
+    if ((int)threadIdx.x < a.rank) a.agu[(int64_t)b * a.rank + threadIdx.x] = ah[threadIdx.x];
+    return;
+  }
+  b -= nxu;
+  if constexpr (SBITS != 0) {
+    const int wvb = moe_lane_wave();
+    lane_run<SguSrc, SBITS, false, SLRP, 1, 4, 1, false, false, true>(SguSrc{a}, a.gSGU,
+                                                                     b * 8 + wvb, wvb, nullptr);
+  }
+}
+
+// a of (pick, gate/up) job j = m P + p.
+__global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_xu_kernel(MoeLaneArgs a) {
+  extern __shared__ float lds[];
+  const int P = a.B * a.topk, j = blockIdx.x, m = j >= P ? 1 : 0, p = j - m * P;
+  const XuJob job{a.h + (int64_t)(p / a.topk) * a.H, moe_lane_u(a, m, a.sel[p])};
+  const __half* ah = lane_xu_phase(job, a.H, a.rank, true, lds);
+  if ((int)threadIdx.x < a.rank) a.agu[(int64_t)j * a.rank + threadIdx.x] = ah[threadIdx.x];
+}
+
+template <int BITS, int LRP, int NSV>
+__global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_gu_kernel(MoeLaneArgs a) {
+  const int wvb = moe_lane_wave();
+  lane_run<RguSrc, BITS, false, LRP, 1, 4, NSV, false, false, true>(
+      RguSrc{a}, a.gRGU, blockIdx.x * 8 + wvb, wvb, nullptr);
+}
+
+constexpr int moe_lane_pd(int np) { return np >= 3 ? 2 : 4; }
+
+template <int BITS, int LRP, int NP>
+__global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_down_kernel(MoeLaneArgs a) {
+  extern __shared__ float lds[];
+  if ((int)blockIdx.x >= a.nrd) {  // a_down of pick p
+    const int p = blockIdx.x - a.nrd;
+    const XuJob job{a.inter + (int64_t)p * a.I, moe_lane_u(a, 2, a.sel[p])};
+    const __half* ah = lane_xu_phase(job, a.I, a.rank, true, lds);
+    if ((int)threadIdx.x < a.rank) a.ad[(int64_t)p * a.rank + threadIdx.x] = ah[threadIdx.x];
+    return;
+  }
+  const int wvb = moe_lane_wave();
+  lane_run<RdSrc, BITS, false, LRP, NP, moe_lane_pd(NP), 1, false, false>(
+      RdSrc{a}, a.gRD, blockIdx.x * 8 + wvb, wvb, nullptr);
+}
+
+template <int SBITS, int SLRP, int SNP>
+__global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_sdown_kernel(MoeLaneArgs a) {
+  const int wvb = moe_lane_wave();
+  lane_run<SdSrc, SBITS, false, SLRP, SNP, moe_lane_pd(SNP), 1, false, false>(
+      SdSrc{a}, a.gSD, blockIdx.x * 8 + wvb, wvb, nullptr);
+}
+
+// Without a shared expert: out = fp16(routed) (+ residual).
+__global__ __launch_bounds__(256) void moe_lane_combine_kernel(MoeLaneArgs a) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.B * a.H) return;
+  const int t = i / a.H, n = i - t * a.H;
+  float o = __half2float(__float2half(moe_lane_routed(a, t, n)));
+  if (a.res) o += __half2float(a.res[i]);
+  a.out[i] = __float2half(o);
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+namespace {
+
+int lane_lrp(int lr) { return lr <= 16 ? 16 : lr <= 32 ? 32 : 64; }
+
+// Geometry of a lane role: N rows of K codes per item (pairs: N rows of each
+// of two matrices), about kMoeLaneWaves waves over the role.
+LaneGeom role_geom(int N, int K, int bits, int rank, int items, bool pair) {
+  LaneGeom g;
+  g.N = N;
+  g.K = K;
+  g.G = K / 128;
+  g.kw = K * bits / 32;
+  g.rank = rank;
+  g.items = items;
+  g.lr = K * bits / 128;
+  const int lrp = lane_lrp(g.lr), np = (g.lr + 63) / 64;
+  const int pd = pair ? 4 : moe_lane_pd(np);
+  g.rounds = (N + 63) / 64 * lrp * (pair ? 2 : 1) / pd;
+  const int64_t total = (int64_t)items * g.rounds;
+  const int64_t rpw = std::max<int64_t>(1, (total + kMoeLaneWaves - 1) / kMoeLaneWaves);
+  g.wpi = (int)((g.rounds + rpw - 1) / rpw);
+  g.rpw = (g.rounds + g.wpi - 1) / g.wpi;
+  return g;
+}
+
+int64_t role_blocks(const LaneGeom& g) { return ((int64_t)g.items * g.wpi + 7) / 8; }
+
+struct MoeLanePlan {
+  MoeLaneArgs a;
+  int bits, sbits, rc;
+  bool lora;
+  int64_t off_sel, off_wts, off_sg, off_agu, off_inter, off_yb, off_ad, off_sinter, ws_need;
+  size_t lds_route, lds_xu;
+};
+
+}  // namespace
+
+// The lane path takes the step when the batch is small and every projection
+// fits its form (gate/up rows of at most 64 pieces, down rows of at most 256,
+// H <= 4096).  p has passed the many-token path's checks (moe_plan).
+static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
+  int maxb = kMoeLaneMaxB;
+  if (const char* e = getenv("GLQ_MOE_LANE_MAXB")) maxb = atoi(e);
+  if (getenv("GLQ_MOE_NO_LANE")) return false;
+  const int64_t B = p->tokens, H = p->hidden, I = p->inter, SI = p->shared_inter;
+  if (B > maxb) return false;
+  const bool lora = p->rank > 0 && p->SV[0] && p->SV[1] && p->SV[2];
+  const int r = lora ? (int)p->rank : 0;
+  const int bits = p->bits, sbits = SI > 0 ? p->shared_bits : 0;
+  if (H * bits / 128 > 64 || I * bits / 128 > 256 || H > 4096) return false;
+  if (SI > 0 && (H * sbits / 128 > 64 || SI * sbits / 128 > 256)) return false;
+  MoeLaneArgs& a = P.a;
+  memset(&a, 0, sizeof(a));
+  a.B = (int)B; a.H = (int)H; a.E = (int)p->experts; a.I = (int)I; a.SI = (int)SI;
+  a.topk = (int)p->top_k;
+  a.norm = p->norm_topk_prob ? 1 : 0;
+  a.C = lora ? (int)p->n_clusters : 1;
+  a.rank = r;
+  a.h = (const __half*)p->h;
+  a.rw = (const __half*)p->router_w;
+  a.sgw = SI > 0 ? (const __half*)p->shared_gate_w : nullptr;
+  const int64_t Ks[3] = {H, H, I}, Ns[3] = {I, I, H};
+  for (int s = 0; s < 3; ++s) {
+    a.codes[s] = (const uint32_t*)p->codes[s];
+    a.scales[s] = (const __half*)p->scales[s];
+    a.zeros[s] = (const __half*)p->zeros[s];
+    a.c_es[s] = Ns[s] * (Ks[s] * bits / 32);
+    a.s_es[s] = Ns[s] * (Ks[s] / 128);
+    a.sv_es[s] = Ns[s] * r;
+    if (lora) {
+      a.U[s] = (const __half*)p->U[s];
+      a.clus[s] = p->cluster_of[s];
+      a.SV[s] = (const __half*)p->SV[s];
+      a.urows[s] = p->u_rows[s] > 0 ? (int)p->u_rows[s] : a.C;
+    } else {
+      a.urows[s] = 1;
+    }
+    if (SI > 0) {
+      a.scodes[s] = (const uint32_t*)p->shared_codes[s];
+      a.sscales[s] = (const __half*)p->shared_scales[s];
+      a.szeros[s] = (const __half*)p->shared_zeros[s];
+    }
+  }
+  if (lora) {
+    a.uslot[0] = p->u_slot[0];
+    a.uslot[1] = p->u_slot[1];
+  }
+  a.out = (__half*)p->out;
+  a.res = (const __half*)p->residual;
+  a.logits = (__half*)p->router_logits;
+  const int P_ = (int)(B * p->top_k);
+  P.bits = bits;
+  P.sbits = sbits;
+  P.lora = lora;
+  P.rc = H <= 512 ? 1 : H <= 1024 ? 2 : H <= 2048 ? 4 : 8;
+  a.gRGU = role_geom((int)I, (int)H, bits, r, P_, true);
+  a.gRD = role_geom((int)H, (int)I, bits, 0, P_, false);
+  a.nrd = (int)role_blocks(a.gRD);
+  if (SI > 0) {
+    a.gSGU = role_geom((int)SI, (int)H, sbits, 0, (int)B, true);
+    a.gSD = role_geom((int)H, (int)SI, sbits, 0, (int)B, false);
+  }
+  // The first 256 bytes hold the many-token path's router arrival counter,
+  // which must stay zero between steps (glq_moe.hip): a workspace may serve
+  // both paths (steps of different sizes), so this path never writes there.
+  int64_t o = 256;
+  auto take = [&](int64_t bytes) {
+    const int64_t at = o;
+    o += align_up(std::max<int64_t>(bytes, 1), 256);
+    return at;
+  };
+  P.off_sel = take(4 * P_);
+  P.off_wts = take(2 * P_);
+  P.off_sg = take(2 * B);
+  // a of every cluster in the router's launch when all clusters' U take a few
+  // MB (the block's clusters few), else of the picks after routing
+  const int64_t ubytes = 2 * (int64_t)a.C * H * r * 2;
+  a.xuall = lora && ubytes <= kMoeLaneXuAllBytes && !getenv("GLQ_MOE_LANE_XU_GATE") ? 1 : 0;
+  P.off_agu = take(2 * 2 * (int64_t)r * (a.xuall ? (int64_t)a.C * B : P_));
+  P.off_inter = take(2 * (int64_t)P_ * I);
+  P.off_yb = take(4 * (int64_t)P_ * H);
+  P.off_ad = take(2 * (int64_t)P_ * r);
+  P.off_sinter = take(SI > 0 ? 2 * B * SI : 0);
+  P.ws_need = o;
+  P.lds_route = (size_t)(((2 * (a.E + 1) + 15) & ~15) + 4 * a.E + 4 * 16);
+  P.lds_xu = lora ? (size_t)LaneXu(r).lds_bytes(r) : 0;
+  return true;
+}
+
+// ---- launches ----
+template <int SBITS, int SLRP, int RC>
+static int launch_route(const MoeLanePlan& P, hipStream_t s) {
+  const MoeLaneArgs& a = P.a;
+  const int64_t grid = a.B + (a.xuall ? 2 * a.C * a.B : 0) + (SBITS ? role_blocks(a.gSGU) : 0);
+  const size_t lds = a.xuall ? std::max(P.lds_route, P.lds_xu) : P.lds_route;
+  static size_t attr = 64 * 1024;
+  int rc = set_lds_limit(moe_lane_route_kernel<SBITS, SLRP, RC>, lds, attr);
+  if (rc) return rc;
+  moe_lane_route_kernel<SBITS, SLRP, RC><<<dim3((unsigned)grid), dim3(kMoeLaneThreads), lds,
+                                           s>>>(a);
+  GLQ_LAUNCH_CHECK("moe_lane_route_kernel");
+  return GLQ_OK;
+}
+
+template <int SBITS, int SLRP>
+static int launch_route_rc(const MoeLanePlan& P, hipStream_t s) {
+  if (P.rc == 1) return launch_route<SBITS, SLRP, 1>(P, s);
+  if (P.rc == 2) return launch_route<SBITS, SLRP, 2>(P, s);
+  if (P.rc == 4) return launch_route<SBITS, SLRP, 4>(P, s);
+  return launch_route<SBITS, SLRP, 8>(P, s);
+}
+
+template <int BITS, int LRP, int NSV>
+static int launch_gu(const MoeLanePlan& P, hipStream_t s) {
+  const int64_t grid = role_blocks(P.a.gRGU);
+  moe_lane_gu_kernel<BITS, LRP, NSV><<<dim3((unsigned)grid), dim3(kMoeLaneThreads), 0, s>>>(P.a);
+  GLQ_LAUNCH_CHECK("moe_lane_gu_kernel");
+  return GLQ_OK;
+}
+
+template <int BITS, int LRP, int NP>
+static int launch_down(const MoeLanePlan& P, hipStream_t s) {
+  const int64_t grid = P.a.nrd + (P.lora ? (int64_t)P.a.B * P.a.topk : 0);
+  static size_t attr = 64 * 1024;
+  int rc = set_lds_limit(moe_lane_down_kernel<BITS, LRP, NP>, P.lds_xu, attr);
+  if (rc) return rc;
+  moe_lane_down_kernel<BITS, LRP, NP><<<dim3((unsigned)grid), dim3(kMoeLaneThreads), P.lds_xu,
+                                        s>>>(P.a);
+  GLQ_LAUNCH_CHECK("moe_lane_down_kernel");
+  return GLQ_OK;
+}
+
+template <int SBITS, int SLRP, int SNP>
+static int launch_sdown(const MoeLanePlan& P, hipStream_t s) {
+  const int64_t grid = role_blocks(P.a.gSD);
+  moe_lane_sdown_kernel<SBITS, SLRP, SNP><<<dim3((unsigned)grid), dim3(kMoeLaneThreads), 0,
+                                            s>>>(P.a);
+  GLQ_LAUNCH_CHECK("moe_lane_sdown_kernel");
+  return GLQ_OK;
+}
+
+// Template arguments from the plan: LRP from a row's pieces, NP pieces per
+// lane (LRP 64 only), NSV SV dwords per lane (rank <= 2 NSV LRP).
+template <int BITS>
+static int dispatch_gu(const MoeLanePlan& P, hipStream_t s) {
+  const int lrp = lane_lrp(P.a.gRGU.lr), r = P.a.rank;
+  if (lrp == 64) return launch_gu<BITS, 64, 1>(P, s);
+  if (lrp == 32) return r <= 64 ? launch_gu<BITS, 32, 1>(P, s) : launch_gu<BITS, 32, 2>(P, s);
+  if (r <= 32) return launch_gu<BITS, 16, 1>(P, s);
+  return r <= 64 ? launch_gu<BITS, 16, 2>(P, s) : launch_gu<BITS, 16, 4>(P, s);
+}
+
+template <int BITS>
+static int dispatch_down(const MoeLanePlan& P, hipStream_t s) {
+  const int lr = P.a.gRD.lr, lrp = lane_lrp(lr), np = (lr + 63) / 64;
+  if (lrp == 64) {
+    if (np == 1) return launch_down<BITS, 64, 1>(P, s);
+    if (np == 2) return launch_down<BITS, 64, 2>(P, s);
+    if (np == 3) return launch_down<BITS, 64, 3>(P, s);
+    return launch_down<BITS, 64, 4>(P, s);
+  }
+  if (lrp == 32) return launch_down<BITS, 32, 1>(P, s);
+  return launch_down<BITS, 16, 1>(P, s);
+}
+
+template <int SBITS>
+static int dispatch_shared(const MoeLanePlan& P, hipStream_t s, bool route) {
+  if (route) {
+    const int lrp = lane_lrp(P.a.gSGU.lr);
+    if (lrp == 64) return launch_route_rc<SBITS, 64>(P, s);
+    if (lrp == 32) return launch_route_rc<SBITS, 32>(P, s);
+    return launch_route_rc<SBITS, 16>(P, s);
+  }
+  const int lr = P.a.gSD.lr, lrp = lane_lrp(lr), np = (lr + 63) / 64;
+  if (lrp == 64) {
+    if (np == 1) return launch_sdown<SBITS, 64, 1>(P, s);
+    if (np == 2) return launch_sdown<SBITS, 64, 2>(P, s);
+    if (np == 3) return launch_sdown<SBITS, 64, 3>(P, s);
+    return launch_sdown<SBITS, 64, 4>(P, s);
+  }
+  if (lrp == 32) return launch_sdown<SBITS, 32, 1>(P, s);
+  return launch_sdown<SBITS, 16, 1>(P, s);
+}
+
+static int moe_lane_launch(const MoeLanePlan& P, hipStream_t s) {
+  const MoeLaneArgs& a = P.a;
+  int rc;
+  // 1. router (+ shared gate/up)
+  if (P.sbits == 2) rc = dispatch_shared<2>(P, s, true);
+  else if (P.sbits == 4) rc = dispatch_shared<4>(P, s, true);
+  else rc = launch_route_rc<0, 16>(P, s);
+  if (rc) return rc;
+  // 2. a of each pick's gate and up (unless formed for every cluster in 1)
+  if (P.lora && !a.xuall) {
+    static size_t attr = 64 * 1024;
+    rc = set_lds_limit(moe_lane_xu_kernel, P.lds_xu, attr);
+    if (rc) return rc;
+    moe_lane_xu_kernel<<<dim3((unsigned)(2 * a.B * a.topk)), dim3(kMoeLaneThreads), P.lds_xu,
+                         s>>>(a);
+    GLQ_LAUNCH_CHECK("moe_lane_xu_kernel");
+  }
+  // 3. routed gate/up
+  rc = P.bits == 2 ? dispatch_gu<2>(P, s) : dispatch_gu<4>(P, s);
+  if (rc) return rc;
+  // 4. routed down (+ a_down)
+  rc = P.bits == 2 ? dispatch_down<2>(P, s) : dispatch_down<4>(P, s);
+  if (rc) return rc;
+  // 5. shared down + combine, or the combine alone
+  if (P.sbits == 2) return dispatch_shared<2>(P, s, false);
+  if (P.sbits == 4) return dispatch_shared<4>(P, s, false);
+  const int64_t n = (int64_t)a.B * a.H;
+  moe_lane_combine_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(a);
+  GLQ_LAUNCH_CHECK("moe_lane_combine_kernel");
+  return GLQ_OK;
+}
+
+int64_t moe_lane_workspace_bytes(const glq_moe_params* p) {
+  MoeLanePlan P;
+  if (!moe_lane_plan(p, P)) return -1;
+  return P.ws_need;
+}
+
+int moe_lane_decode(const glq_moe_params* p, void* workspace, int64_t workspace_bytes,
+                    hipStream_t s) {
+  MoeLanePlan P;
+  GLQ_CHECK(moe_lane_plan(p, P), "the lane path does not take this step");
+  GLQ_CHECK(workspace != nullptr && workspace_bytes >= P.ws_need,
+            "workspace of %lld bytes needed (got %lld)", (long long)P.ws_need,
+            (long long)workspace_bytes);
+  GLQ_CHECK(((uintptr_t)workspace & 255) == 0, "workspace must be 256-byte aligned");
+  char* w = (char*)workspace;
+  MoeLaneArgs& a = P.a;
+  a.sel = (int32_t*)(w + P.off_sel);
+  a.wts = (__half*)(w + P.off_wts);
+  a.sg = (__half*)(w + P.off_sg);
+  a.agu = (__half*)(w + P.off_agu);
+  a.inter = (__half*)(w + P.off_inter);
+  a.yb = (float*)(w + P.off_yb);
+  a.ad = (__half*)(w + P.off_ad);
+  a.sinter = (__half*)(w + P.off_sinter);
+  return moe_lane_launch(P, s);
+}
+
+}  // namespace glq

@@ -1,0 +1,136 @@
+"""MoE decode steps of a few tokens (glq_moe_decode's lane path,
+glorcq_amd/csrc/glq_moe_lane.hip: per-token router workgroups, lane-sliced
+expert rows with x U formed in the workgroup, the combine in the shared
+expert's down rows) against the MoE oracle and against the many-token path
+forced on the same inputs (GLQ_MOE_NO_LANE=1).
+
+Bars as tests/test_moe_gpu.py: routing ids identical (seeds with no near-tie,
+asserted), router logits within one fp16 ulp, block output within the MoE
+bar; the two paths within the same bar of each other (their fp32 sums run in
+different orders)."""
+
+import pytest
+import torch
+
+from glorcq_amd import format as fmt
+from glorcq_amd.moe_block import GraphCompatibleMoeBlock
+from oracle import glorcq_oracle as O
+from test_moe_gpu import check_routing, margin, small
+from test_moe_oracle import bar, lora_heavy
+
+pytestmark = pytest.mark.gpu
+
+
+def step(p, gpu, monkeypatch, lane):
+    if lane:
+        monkeypatch.delenv("GLQ_MOE_NO_LANE", raising=False)
+    else:
+        monkeypatch.setenv("GLQ_MOE_NO_LANE", "1")
+    blk = GraphCompatibleMoeBlock.from_problem(p, gpu)
+    out, logits = blk(p.h.reshape(1, p.B, p.H).to(gpu))
+    torch.cuda.synchronize()
+    return out.reshape(p.B, p.H).cpu(), logits.cpu()
+
+
+def check_both(p, gpu, monkeypatch, what):
+    print(what, flush=True)
+    out, logits = step(p, gpu, monkeypatch, True)
+    check_routing(p, logits)
+    ref = O.moe_forward(p)
+    assert bar(out, ref), (what, float((out.double() - ref).abs().max()))
+    old, old_logits = step(p, gpu, monkeypatch, False)
+    assert bar(out, old.double()), (what, "vs many-token path",
+                                    float((out.double() - old.double()).abs().max()))
+    return out
+
+
+@pytest.mark.parametrize("B,seed", [(1, 0), (2, 3), (4, 1)])
+def test_config2(gpu, monkeypatch, B, seed):
+    """BASELINE config 2 (Qwen1.5-MoE-A2.7B block: 60 experts, top-4, 16
+    clusters, 4-bit shared expert of 5632 whose down rows take three 16-byte
+    pieces per lane)."""
+    p = fmt.make_moe(B=B, seed=seed)
+    assert margin(p) >= 2
+    check_both(p, gpu, monkeypatch, f"config 2 B={B}")
+
+
+@pytest.mark.parametrize("B", [1, 4])
+def test_config2_lora_heavy(gpu, monkeypatch, B):
+    """LoRA factors x30: a wrong cluster, U row or a = x U sum fails."""
+    p = lora_heavy(fmt.make_moe(B=B, seed=1))
+    assert margin(p) >= 2
+    check_both(p, gpu, monkeypatch, f"config 2 lora x30 B={B}")
+
+
+def test_config3_mixtral_decode(gpu, monkeypatch):
+    """BASELINE config 3 at M=1: H 4096 (64 pieces a gate/up row), ffn 14336
+    (the routed down rows take four pieces per lane), no shared expert."""
+    p = lora_heavy(fmt.make_mixtral_layer(B=1, seed=3), f=3.0)
+    assert margin(p) >= 2
+    check_both(p, gpu, monkeypatch, "config 3 B=1")
+
+
+def test_config4_block(gpu, monkeypatch):
+    """A Qwen3-30B-A3B block (128 experts, inter 768: 16-lane row groups with
+    several SV dwords a lane, top-8, norm_topk_prob) with 100 clusters."""
+    p = lora_heavy(fmt.make_moe(H=2048, E=128, inter=768, top_k=8, n_clusters=100, rank=64,
+                                shared_inter=0, norm_topk_prob=True, B=1, seed=3))
+    assert margin(p) >= 2
+    check_both(p, gpu, monkeypatch, "config 4 B=1")
+
+
+@pytest.mark.parametrize("kw", [
+    dict(norm_topk_prob=True),
+    dict(shared_inter=0),
+    dict(rank=0),
+    dict(bits=4),
+    dict(shared_bits=2),
+    dict(top_k=8, E=8),
+    dict(inter=4096, rank=64, bits=4),   # routed down rows of two pieces a lane
+    dict(H=512, shared_inter=8192),      # shared down rows of four pieces a lane
+    dict(n_clusters=1, rank=128),        # rank 128: two SV dwords a lane
+], ids=lambda kw: ",".join(f"{k}={v}" for k, v in kw.items()))
+@pytest.mark.parametrize("B", [1, 3])
+def test_variants(gpu, monkeypatch, kw, B):
+    p = small(B=B, seed=21, **kw)
+    if p.rank:
+        p = lora_heavy(p)
+    seed = 21
+    while margin(p) < 2 and seed < 60:  # a seed with no near-tie at the top-k boundary
+        seed += 1
+        p = small(B=B, seed=seed, **kw)
+        if p.rank:
+            p = lora_heavy(p)
+    assert margin(p) >= 2
+    check_both(p, gpu, monkeypatch, f"{kw} B={B}")
+
+
+def test_residual_and_repeat(gpu, monkeypatch):
+    """The residual add in the combine; repeated steps give the same bits."""
+    monkeypatch.delenv("GLQ_MOE_NO_LANE", raising=False)
+    p = fmt.make_moe(B=2, seed=3)
+    blk = GraphCompatibleMoeBlock.from_problem(p, gpu)
+    res = (torch.randn(1, 2, p.H, generator=torch.Generator().manual_seed(4)) * 0.5).half()
+    h = p.h.reshape(1, 2, p.H).to(gpu)
+    o1, _ = blk(h, residual=res.to(gpu))
+    o2, _ = blk(h, residual=res.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    ref = O.moe_forward(p).half().double() + res.reshape(2, p.H).double()
+    assert bar(o1.reshape(2, p.H).cpu(), ref)
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_xu_forms_agree(gpu, monkeypatch, B):
+    """a = x U of gate/up formed for every cluster in the router's launch (few
+    clusters) or for the picks in a launch of its own (GLQ_MOE_LANE_XU_GATE):
+    the same sums in the same order, so the same bits."""
+    monkeypatch.delenv("GLQ_MOE_NO_LANE", raising=False)
+    p = lora_heavy(fmt.make_moe(B=B, seed=1))
+    blk = GraphCompatibleMoeBlock.from_problem(p, gpu)
+    h = p.h.reshape(1, B, p.H).to(gpu)
+    o1, _ = blk(h)
+    monkeypatch.setenv("GLQ_MOE_LANE_XU_GATE", "1")
+    o2, _ = blk(h)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
