@@ -116,28 +116,27 @@ struct LaneXu {
   }
 };
 
-// a = fp16(x U) of one item by all 512 threads of the workgroup (layout in
-// LaneXu): U rows read by whole-row wave loads, two 8-row chunks in flight
-// per thread, v_dot2 over row pairs into fp32, the partials summed in LDS in
-// a fixed order and rounded to fp16 once.  Returns a's LDS copy (rank halves);
-// every thread of the workgroup must call it (it holds barriers).
+// sum_{k0 <= k < k0 + kn} x[k] U[k][:] (fp32, kn a multiple of 8) of one item
+// by all 512 threads of the workgroup (layout in LaneXu): U rows read by
+// whole-row wave loads, two 8-row chunks in flight per thread, v_dot2 over
+// row pairs into fp32, the partials summed in LDS in a fixed order.  Returns
+// the sums' LDS copy (rank floats); every thread of the workgroup must call
+// it (it holds barriers).
 template <class View>
-__device__ __half* lane_xu_phase(const View& src, int K, int rank, bool lora, float* xu_lds) {
+__device__ float* lane_xu_sum(const View& src, int k0, int kn, int rank, float* xu_lds) {
   const LaneXu L(rank);
   const int t = threadIdx.x;
   float* part = xu_lds;                      // (ks, rank)
   float* segs = xu_lds + L.ks * rank;        // (nseg, rank)
-  __half* ah = (__half*)(segs + L.nseg * rank);
-  if (!lora) return ah;
   const int b = t % L.nb, slot = t / L.nb;
   if (slot < L.ks) {
-    const int nch = K / 8;  // 8-row chunks
-    const __half* ub = src.u() + 8 * b;
+    const int nch = kn / 8;  // 8-row chunks
+    const __half* ub = src.u() + (int64_t)k0 * rank + 8 * b;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     u32x4 u0[8], u1[8], x0, x1;
     auto load = [&](int c, u32x4 (&u)[8], u32x4& xv) {
       c = min(c, nch - 1);  // past the end: re-read the last chunk (not used)
-      xv = src.x8(8 * c);
+      xv = src.x8(k0 + 8 * c);
 #pragma unroll
       for (int q = 0; q < 8; ++q) u[q] = *(const u32x4*)(ub + (int64_t)(8 * c + q) * rank);
     };
@@ -174,11 +173,23 @@ __device__ __half* lane_xu_phase(const View& src, int K, int rank, bool lora, fl
     segs[seg * rank + col] = sum;
   }
   __syncthreads();
-  if (t < rank) {  // level 2: the segments in order
+  if (t < rank) {  // level 2: the segments in order, into part's first row
     float sum = 0.f;
     for (int q = 0; q < L.nseg; ++q) sum += segs[q * rank + t];
-    ah[t] = __float2half(sum);
+    part[t] = sum;
   }
+  __syncthreads();
+  return part;
+}
+
+// a = fp16(x U) over the whole row (K codes), in LDS (rank halves).
+template <class View>
+__device__ __half* lane_xu_phase(const View& src, int K, int rank, bool lora, float* xu_lds) {
+  const LaneXu L(rank);
+  __half* ah = (__half*)(xu_lds + L.ks * rank + L.nseg * rank);
+  if (!lora) return ah;
+  const float* sums = lane_xu_sum(src, 0, K, rank, xu_lds);
+  if ((int)threadIdx.x < rank) ah[threadIdx.x] = __float2half(sums[threadIdx.x]);
   __syncthreads();
   return ah;
 }
@@ -283,7 +294,6 @@ __device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, in
       }
     }
   };
-  if constexpr (!XU) load_x();
   const bool lora = src.lora();
   // the item's tensors of matrix m (PAIR: 0 and 1, iterations alternating)
   auto t_codes = [&](int m) { if constexpr (PAIR) return src.codes(m); else return src.codes(); };
@@ -364,7 +374,11 @@ __device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, in
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  if constexpr (!XU) prologue();
+  // the rows' loads go out first; x and a (below) arrive under them
+  if constexpr (!XU) {
+    prologue();
+    load_x();
+  }
 
   // ---- a pairs of this lane's SV dwords (zero past the rank) ----
   uint32_t ap[M2][NSV];

@@ -65,12 +65,15 @@ struct MoeLaneArgs {
   int32_t* sel;     // [P] expert of pick p = t * topk + k
   __half* wts;      // [P] routing weights
   __half* sg;       // [B] shared-expert gate
-  __half* agu;      // [2][P][rank] a of each pick's gate and up, or (xuall)
-                    // [2][C][B][rank] a of every cluster's gate and up
+  float* agu;       // fp32 partial sums of a over K slices of kXuSlice codes:
+                    // [2][P][S][rank] for each pick's gate and up, or (xuall)
+                    // [2][C][B][S][rank] for every cluster's gate and up
   int xuall;        // 1: a for every cluster in the router's launch
+  int su;           // K slices of gate/up (H), and of down (I)
+  int sd;
   __half* inter;    // [P][I] each pick's inter
   float* yb;        // [P][H] routed down outputs without the low-rank term
-  __half* ad;       // [P][rank] a_down of each pick
+  float* ad;        // [P][sd][rank] fp32 partial sums of each pick's a_down
   __half* sinter;   // [B][SI] the shared expert's inter
   // outputs
   __half* out;
@@ -78,7 +81,10 @@ struct MoeLaneArgs {
   __half* logits;
   LaneGeom gSGU, gRGU, gRD, gSD;
   int nrd;          // workgroups of the routed down rows
+  int rows_wg;      // output rows per shared-down workgroup (its combine)
 };
+
+constexpr int kXuSlice = 512;  // codes per x U job
 
 __device__ __forceinline__ int moe_lane_clamp(int v, int n) { return min(max(v, 0), n - 1); }
 
@@ -107,12 +113,12 @@ struct RguItem {
   __device__ const __half* zeros(int m) const { return a.zeros[m] + (int64_t)e * a.s_es[m]; }
   __device__ const __half* sv(int m) const { return a.SV[m] + (int64_t)e * a.sv_es[m]; }
   __device__ u32x4 x8(int k) const { return *(const u32x4*)(x + k); }
+  // a = fp16(sum of the slices' partials, in slice order)
   __device__ __half load_a(int m, int j) const {
-    if (a.xuall) {
-      const int c = moe_lane_clamp(a.clus[m][e], a.C);
-      return a.agu[(((int64_t)m * a.C + c) * a.B + p / a.topk) * a.rank + j];
-    }
-    return a.agu[((int64_t)m * a.B * a.topk + p) * a.rank + j];
+    const int64_t job = a.xuall ? ((int64_t)m * a.C + moe_lane_clamp(a.clus[m][e], a.C)) * a.B +
+                                      p / a.topk
+                                : (int64_t)m * a.B * a.topk + p;
+    return __float2half(sum_strided(a.agu + job * a.su * a.rank + j, a.rank, a.su));
   }
   __device__ void store(int n, float g, float u) const {
     a.inter[(int64_t)p * a.I + n] = swiglu_fp16(g, u);
@@ -173,34 +179,52 @@ struct SguSrc {
   __device__ SguItem bind(int t) const { return SguItem{a, t}; }
 };
 
-// Routed part of output row n of token t: sum_k w_k (y_k[n] + a_down,k
-// SV_down,k[n]^T), in pick order (the many-token combine's order).
-__device__ __forceinline__ float moe_lane_routed(const MoeLaneArgs& a, int t, int n) {
-  float acc = 0.f;
-  for (int k = 0; k < a.topk; ++k) {
-    const int p = t * a.topk + k;
-    float y = a.yb[(int64_t)p * a.H + n];
-    if (a.rank > 0 && a.SV[2]) {
-      const int e = a.sel[p];
-      const __half* sv = a.SV[2] + (int64_t)e * a.sv_es[2] + (int64_t)n * a.rank;
-      const __half* ad = a.ad + (int64_t)p * a.rank;
+// Routed part of output rows [n0, n0 + nrows) of token t into LDS routed[]:
+// sum_k w_k (y_k[n] + a_down,k SV_down,k[n]^T), fmaf over the picks in pick
+// order (the many-token combine's order), a_down = fp16(sum of its slices'
+// partials).  All `nth` threads of the workgroup call it (barriers inside).
+// LDS: adl (topk x rank halves), contrib (nrows x topk floats), routed.
+__device__ void moe_lane_routed_rows(const MoeLaneArgs& a, int t, int n0, int nrows, int nth,
+                                     __half* adl, float* contrib, float* routed) {
+  const int tid = threadIdx.x, K = a.topk, r = a.rank;
+  const bool lora = r > 0 && a.SV[2] != nullptr;
+  if (lora)
+    for (int i = tid; i < K * r; i += nth) {
+      const int k = i / r, j = i - k * r;
+      adl[i] = __float2half(sum_strided(a.ad + (int64_t)(t * K + k) * a.sd * r + j, r, a.sd));
+    }
+  __syncthreads();
+  for (int i = tid; i < nrows * K; i += nth) {
+    const int rr = i / K, k = i - rr * K, n = min(n0 + rr, a.H - 1), pk = t * K + k;
+    float y = a.yb[(int64_t)pk * a.H + n];
+    if (lora) {
+      const __half* sv = a.SV[2] + (int64_t)a.sel[pk] * a.sv_es[2] + (int64_t)n * r;
+      const __half* ak = adl + k * r;
       float l = 0.f;
-      for (int j = 0; j < a.rank; j += 8) {
-        const u32x4 s8 = *(const u32x4*)(sv + j), a8 = *(const u32x4*)(ad + j);
+      for (int j = 0; j < r; j += 8) {
+        const u32x4 s8 = *(const u32x4*)(sv + j), a8 = *(const u32x4*)(ak + j);
 #pragma unroll
         for (int q = 0; q < 4; ++q) l = dot2(s8[q], a8[q], l);
       }
       y += l;
     }
-    acc = fmaf(__half2float(a.wts[p]), y, acc);
+    contrib[i] = y;
   }
-  return acc;
+  __syncthreads();
+  for (int rr = tid; rr < nrows; rr += nth) {
+    float acc = 0.f;
+    for (int k = 0; k < K; ++k) acc = fmaf(__half2float(a.wts[t * K + k]), contrib[rr * K + k], acc);
+    routed[rr] = acc;
+  }
+  __syncthreads();
 }
 
-// Shared down rows of token t, the combine in each row's store.
+// Shared down rows of token t, the combine in each row's store (the rows'
+// routed parts precomputed in LDS from row n0).
 struct SdItem {
   const MoeLaneArgs& a;
-  int t;
+  int t, n0;
+  const float* routed;
   __device__ bool lora() const { return false; }
   __device__ const uint32_t* codes() const { return a.scodes[2]; }
   __device__ const __half* scales() const { return a.sscales[2]; }
@@ -214,7 +238,7 @@ struct SdItem {
   __device__ __half load_a(int) const { return __float2half(0.f); }
   // out = fp16(routed + gate * fp16(shared)) (+ residual)
   __device__ void store(int n, float v) const {
-    float acc = moe_lane_routed(a, t, n);
+    float acc = routed[n - n0];
     acc = fmaf(__half2float(a.sg[t]), __half2float(__float2half(v)), acc);
     float o = __half2float(__float2half(acc));
     if (a.res) o += __half2float(a.res[(int64_t)t * a.H + n]);
@@ -223,7 +247,9 @@ struct SdItem {
 };
 struct SdSrc {
   const MoeLaneArgs& a;
-  __device__ SdItem bind(int t) const { return SdItem{a, t}; }
+  int n0;
+  const float* routed;
+  __device__ SdItem bind(int t) const { return SdItem{a, t, n0, routed}; }
 };
 
 // ---- router: one workgroup per token ----
@@ -322,14 +348,16 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_route_kernel(MoeLane
     return;
   }
   b -= a.B;
-  const int nxu = a.xuall ? 2 * a.C * a.B : 0;
-  if (b < nxu) {  // job b = (m C + c) B + t
-    const int t = b % a.B, mc = b / a.B, m = mc / a.C, c = mc - m * a.C;
+  const int nxu = a.xuall ? 2 * a.C * a.B * a.su : 0;
+  if (b < nxu) {  // job b = ((m C + c) B + t) su + s
+    const int s = b % a.su, mct = b / a.su, t = mct % a.B, mc = mct / a.B;
+    const int m = mc / a.C, c = mc - m * a.C;
     const int row = moe_lane_clamp(a.uslot[m] ? a.uslot[m][c] : c, a.urows[m]);
     const __half* u = a.U[m] + (int64_t)row * a.H * a.rank;
-    const __half* ah = lane_xu_phase(XuJob{a.h + (int64_t)t * a.H, u}, a.H, a.rank, true,
-                                     (float*)smem);
-    if ((int)threadIdx.x < a.rank) a.agu[(int64_t)b * a.rank + threadIdx.x] = ah[threadIdx.x];
+    const int k0 = s * kXuSlice;
+    const float* sums = lane_xu_sum(XuJob{a.h + (int64_t)t * a.H, u}, k0,
+                                    min(kXuSlice, a.H - k0), a.rank, (float*)smem);
+    if ((int)threadIdx.x < a.rank) a.agu[(int64_t)b * a.rank + threadIdx.x] = sums[threadIdx.x];
     return;
   }
   b -= nxu;
@@ -340,13 +368,15 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_route_kernel(MoeLane
   }
 }
 
-// a of (pick, gate/up) job j = m P + p.
+// Partial a of (pick, gate/up, K slice) job b = (m P + p) su + s.
 __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_xu_kernel(MoeLaneArgs a) {
   extern __shared__ float lds[];
-  const int P = a.B * a.topk, j = blockIdx.x, m = j >= P ? 1 : 0, p = j - m * P;
+  const int P = a.B * a.topk, b = blockIdx.x, s = b % a.su, j = b / a.su;
+  const int m = j >= P ? 1 : 0, p = j - m * P;
   const XuJob job{a.h + (int64_t)(p / a.topk) * a.H, moe_lane_u(a, m, a.sel[p])};
-  const __half* ah = lane_xu_phase(job, a.H, a.rank, true, lds);
-  if ((int)threadIdx.x < a.rank) a.agu[(int64_t)j * a.rank + threadIdx.x] = ah[threadIdx.x];
+  const int k0 = s * kXuSlice;
+  const float* sums = lane_xu_sum(job, k0, min(kXuSlice, a.H - k0), a.rank, lds);
+  if ((int)threadIdx.x < a.rank) a.agu[(int64_t)b * a.rank + threadIdx.x] = sums[threadIdx.x];
 }
 
 template <int BITS, int LRP, int NSV>
@@ -361,11 +391,12 @@ constexpr int moe_lane_pd(int np) { return np >= 3 ? 2 : 4; }
 template <int BITS, int LRP, int NP>
 __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_down_kernel(MoeLaneArgs a) {
   extern __shared__ float lds[];
-  if ((int)blockIdx.x >= a.nrd) {  // a_down of pick p
-    const int p = blockIdx.x - a.nrd;
+  if ((int)blockIdx.x >= a.nrd) {  // partial a_down of (pick, K slice) job b = p sd + s
+    const int b = blockIdx.x - a.nrd, s = b % a.sd, p = b / a.sd;
     const XuJob job{a.inter + (int64_t)p * a.I, moe_lane_u(a, 2, a.sel[p])};
-    const __half* ah = lane_xu_phase(job, a.I, a.rank, true, lds);
-    if ((int)threadIdx.x < a.rank) a.ad[(int64_t)p * a.rank + threadIdx.x] = ah[threadIdx.x];
+    const int k0 = s * kXuSlice;
+    const float* sums = lane_xu_sum(job, k0, min(kXuSlice, a.I - k0), a.rank, lds);
+    if ((int)threadIdx.x < a.rank) a.ad[(int64_t)b * a.rank + threadIdx.x] = sums[threadIdx.x];
     return;
   }
   const int wvb = moe_lane_wave();
@@ -373,21 +404,45 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_down_kernel(MoeLaneA
       RdSrc{a}, a.gRD, blockIdx.x * 8 + wvb, wvb, nullptr);
 }
 
+// Each workgroup holds one token's rows (wpi a multiple of 8): first the
+// routed parts of its output rows, then its shared-down rows, whose stores
+// combine.
 template <int SBITS, int SLRP, int SNP>
 __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_sdown_kernel(MoeLaneArgs a) {
+  extern __shared__ float lds[];
+  constexpr int RPI = 64 / SLRP, PD = moe_lane_pd(SNP);
+  const LaneGeom& g = a.gSD;
+  const int wv0 = blockIdx.x * 8, t = wv0 / g.wpi;
+  if (t >= g.items) return;  // uniform over the workgroup
+  const int n0 = RPI * PD * (wv0 - t * g.wpi) * g.rpw;
+  const int nrows = min(a.rows_wg, a.H - n0);
+  if (nrows <= 0) return;
+  __half* adl = (__half*)lds;                          // topk x rank
+  float* contrib = lds + (a.topk * a.rank + 1) / 2;    // rows_wg x topk
+  float* routed = contrib + a.rows_wg * a.topk;        // rows_wg
+  moe_lane_routed_rows(a, t, n0, nrows, kMoeLaneThreads, adl, contrib, routed);
   const int wvb = moe_lane_wave();
-  lane_run<SdSrc, SBITS, false, SLRP, SNP, moe_lane_pd(SNP), 1, false, false>(
-      SdSrc{a}, a.gSD, blockIdx.x * 8 + wvb, wvb, nullptr);
+  lane_run<SdSrc, SBITS, false, SLRP, SNP, PD, 1, false, false>(SdSrc{a, n0, routed}, g,
+                                                                wv0 + wvb, wvb, nullptr);
 }
 
-// Without a shared expert: out = fp16(routed) (+ residual).
+// Without a shared expert: out = fp16(routed) (+ residual), 256 threads a
+// workgroup, rows_wg rows of one token each.
 __global__ __launch_bounds__(256) void moe_lane_combine_kernel(MoeLaneArgs a) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= a.B * a.H) return;
-  const int t = i / a.H, n = i - t * a.H;
-  float o = __half2float(__float2half(moe_lane_routed(a, t, n)));
-  if (a.res) o += __half2float(a.res[i]);
-  a.out[i] = __float2half(o);
+  extern __shared__ float lds[];
+  const int nb = (a.H + a.rows_wg - 1) / a.rows_wg;
+  const int t = blockIdx.x / nb, n0 = (blockIdx.x - t * nb) * a.rows_wg;
+  const int nrows = min(a.rows_wg, a.H - n0);
+  __half* adl = (__half*)lds;
+  float* contrib = lds + (a.topk * a.rank + 1) / 2;
+  float* routed = contrib + a.rows_wg * a.topk;
+  moe_lane_routed_rows(a, t, n0, nrows, 256, adl, contrib, routed);
+  for (int r = threadIdx.x; r < nrows; r += 256) {
+    const int n = n0 + r;
+    float o = __half2float(__float2half(routed[r]));
+    if (a.res) o += __half2float(a.res[(int64_t)t * a.H + n]);
+    a.out[(int64_t)t * a.H + n] = __float2half(o);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -399,7 +454,8 @@ int lane_lrp(int lr) { return lr <= 16 ? 16 : lr <= 32 ? 32 : 64; }
 
 // Geometry of a lane role: N rows of K codes per item (pairs: N rows of each
 // of two matrices), about kMoeLaneWaves waves over the role.
-LaneGeom role_geom(int N, int K, int bits, int rank, int items, bool pair) {
+LaneGeom role_geom(int N, int K, int bits, int rank, int items, bool pair,
+                   bool whole_wgs = false) {
   LaneGeom g;
   g.N = N;
   g.K = K;
@@ -414,6 +470,7 @@ LaneGeom role_geom(int N, int K, int bits, int rank, int items, bool pair) {
   const int64_t total = (int64_t)items * g.rounds;
   const int64_t rpw = std::max<int64_t>(1, (total + kMoeLaneWaves - 1) / kMoeLaneWaves);
   g.wpi = (int)((g.rounds + rpw - 1) / rpw);
+  if (whole_wgs) g.wpi = (g.wpi + 7) / 8 * 8;  // each workgroup within one item
   g.rpw = (g.rounds + g.wpi - 1) / g.wpi;
   return g;
 }
@@ -425,7 +482,7 @@ struct MoeLanePlan {
   int bits, sbits, rc;
   bool lora;
   int64_t off_sel, off_wts, off_sg, off_agu, off_inter, off_yb, off_ad, off_sinter, ws_need;
-  size_t lds_route, lds_xu;
+  size_t lds_route, lds_xu, lds_comb;
 };
 
 }  // namespace
@@ -491,9 +548,15 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   a.gRGU = role_geom((int)I, (int)H, bits, r, P_, true);
   a.gRD = role_geom((int)H, (int)I, bits, 0, P_, false);
   a.nrd = (int)role_blocks(a.gRD);
+  a.su = (int)((H + kXuSlice - 1) / kXuSlice);
+  a.sd = (int)((I + kXuSlice - 1) / kXuSlice);
   if (SI > 0) {
     a.gSGU = role_geom((int)SI, (int)H, sbits, 0, (int)B, true);
-    a.gSD = role_geom((int)H, (int)SI, sbits, 0, (int)B, false);
+    a.gSD = role_geom((int)H, (int)SI, sbits, 0, (int)B, false, true);
+    const int lr = a.gSD.lr, rpi = 64 / lane_lrp(lr), pd = moe_lane_pd((lr + 63) / 64);
+    a.rows_wg = rpi * pd * 8 * a.gSD.rpw;
+  } else {
+    a.rows_wg = std::max(1, 256 / a.topk);
   }
   // The first 256 bytes hold the many-token path's router arrival counter,
   // which must stay zero between steps (glq_moe.hip): a workspace may serve
@@ -511,14 +574,15 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   // MB (the block's clusters few), else of the picks after routing
   const int64_t ubytes = 2 * (int64_t)a.C * H * r * 2;
   a.xuall = lora && ubytes <= kMoeLaneXuAllBytes && !getenv("GLQ_MOE_LANE_XU_GATE") ? 1 : 0;
-  P.off_agu = take(2 * 2 * (int64_t)r * (a.xuall ? (int64_t)a.C * B : P_));
+  P.off_agu = take(4 * 2 * (int64_t)r * a.su * (a.xuall ? (int64_t)a.C * B : P_));
   P.off_inter = take(2 * (int64_t)P_ * I);
   P.off_yb = take(4 * (int64_t)P_ * H);
-  P.off_ad = take(2 * (int64_t)P_ * r);
+  P.off_ad = take(4 * (int64_t)P_ * a.sd * r);
   P.off_sinter = take(SI > 0 ? 2 * B * SI : 0);
   P.ws_need = o;
   P.lds_route = (size_t)(((2 * (a.E + 1) + 15) & ~15) + 4 * a.E + 4 * 16);
   P.lds_xu = lora ? (size_t)LaneXu(r).lds_bytes(r) : 0;
+  P.lds_comb = (size_t)(4 * ((a.topk * r + 1) / 2) + 4 * a.rows_wg * (a.topk + 1));
   return true;
 }
 
@@ -526,7 +590,8 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
 template <int SBITS, int SLRP, int RC>
 static int launch_route(const MoeLanePlan& P, hipStream_t s) {
   const MoeLaneArgs& a = P.a;
-  const int64_t grid = a.B + (a.xuall ? 2 * a.C * a.B : 0) + (SBITS ? role_blocks(a.gSGU) : 0);
+  const int64_t grid =
+      a.B + (a.xuall ? 2 * a.C * a.B * a.su : 0) + (SBITS ? role_blocks(a.gSGU) : 0);
   const size_t lds = a.xuall ? std::max(P.lds_route, P.lds_xu) : P.lds_route;
   static size_t attr = 64 * 1024;
   int rc = set_lds_limit(moe_lane_route_kernel<SBITS, SLRP, RC>, lds, attr);
@@ -555,7 +620,7 @@ static int launch_gu(const MoeLanePlan& P, hipStream_t s) {
 
 template <int BITS, int LRP, int NP>
 static int launch_down(const MoeLanePlan& P, hipStream_t s) {
-  const int64_t grid = P.a.nrd + (P.lora ? (int64_t)P.a.B * P.a.topk : 0);
+  const int64_t grid = P.a.nrd + (P.lora ? (int64_t)P.a.B * P.a.topk * P.a.sd : 0);
   static size_t attr = 64 * 1024;
   int rc = set_lds_limit(moe_lane_down_kernel<BITS, LRP, NP>, P.lds_xu, attr);
   if (rc) return rc;
@@ -568,8 +633,11 @@ static int launch_down(const MoeLanePlan& P, hipStream_t s) {
 template <int SBITS, int SLRP, int SNP>
 static int launch_sdown(const MoeLanePlan& P, hipStream_t s) {
   const int64_t grid = role_blocks(P.a.gSD);
-  moe_lane_sdown_kernel<SBITS, SLRP, SNP><<<dim3((unsigned)grid), dim3(kMoeLaneThreads), 0,
-                                            s>>>(P.a);
+  static size_t attr = 64 * 1024;
+  int rc = set_lds_limit(moe_lane_sdown_kernel<SBITS, SLRP, SNP>, P.lds_comb, attr);
+  if (rc) return rc;
+  moe_lane_sdown_kernel<SBITS, SLRP, SNP><<<dim3((unsigned)grid), dim3(kMoeLaneThreads),
+                                            P.lds_comb, s>>>(P.a);
   GLQ_LAUNCH_CHECK("moe_lane_sdown_kernel");
   return GLQ_OK;
 }
@@ -630,8 +698,8 @@ static int moe_lane_launch(const MoeLanePlan& P, hipStream_t s) {
     static size_t attr = 64 * 1024;
     rc = set_lds_limit(moe_lane_xu_kernel, P.lds_xu, attr);
     if (rc) return rc;
-    moe_lane_xu_kernel<<<dim3((unsigned)(2 * a.B * a.topk)), dim3(kMoeLaneThreads), P.lds_xu,
-                         s>>>(a);
+    moe_lane_xu_kernel<<<dim3((unsigned)(2 * a.B * a.topk * a.su)), dim3(kMoeLaneThreads),
+                         P.lds_xu, s>>>(a);
     GLQ_LAUNCH_CHECK("moe_lane_xu_kernel");
   }
   // 3. routed gate/up
@@ -643,8 +711,13 @@ static int moe_lane_launch(const MoeLanePlan& P, hipStream_t s) {
   // 5. shared down + combine, or the combine alone
   if (P.sbits == 2) return dispatch_shared<2>(P, s, false);
   if (P.sbits == 4) return dispatch_shared<4>(P, s, false);
-  const int64_t n = (int64_t)a.B * a.H;
-  moe_lane_combine_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(a);
+  {
+    static size_t attr = 64 * 1024;
+    rc = set_lds_limit(moe_lane_combine_kernel, P.lds_comb, attr);
+    if (rc) return rc;
+  }
+  const int64_t nb = (int64_t)a.B * ((a.H + a.rows_wg - 1) / a.rows_wg);
+  moe_lane_combine_kernel<<<dim3((unsigned)nb), dim3(256), P.lds_comb, s>>>(a);
   GLQ_LAUNCH_CHECK("moe_lane_combine_kernel");
   return GLQ_OK;
 }
@@ -668,10 +741,10 @@ int moe_lane_decode(const glq_moe_params* p, void* workspace, int64_t workspace_
   a.sel = (int32_t*)(w + P.off_sel);
   a.wts = (__half*)(w + P.off_wts);
   a.sg = (__half*)(w + P.off_sg);
-  a.agu = (__half*)(w + P.off_agu);
+  a.agu = (float*)(w + P.off_agu);
   a.inter = (__half*)(w + P.off_inter);
   a.yb = (float*)(w + P.off_yb);
-  a.ad = (__half*)(w + P.off_ad);
+  a.ad = (float*)(w + P.off_ad);
   a.sinter = (__half*)(w + P.off_sinter);
   return moe_lane_launch(P, s);
 }
