@@ -102,43 +102,88 @@ def time_events(fn, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
-def cpu_baseline(gpu_y_config0, budget_s=12.0):
-    """Times the oracle's restatement of the reference CPU fallback on config 0
-    (bounded sample) and checks the GPU's config-0 output against it."""
+def cpu_model_name():
+    """The host CPU's model name (what lscpu prints as "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_call(fn, budget_s, max_calls=2000):
+    """3 warm-ups, then timed calls until the budget (at least 20), median s."""
+    for _ in range(3):
+        fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while (time.perf_counter() < t_end or len(times) < 20) and len(times) < max_calls:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baseline(gpu_y_config0, budget_s=4.0):
+    """Times the oracle's restatements of the reference's CPU fallbacks on
+    config 0 (bounded samples, median of >= 20 calls after 3 warm-ups) and
+    checks the GPU's config-0 output against the fp16 one.  `value` is the
+    fp16 GLoRCQLinear fallback (quantized_linear.py:271-284,313-314,338-349)
+    at all torch threads; `rows` adds it at 1 thread, the fp32
+    _gptq_pytorch_fallback + lora_out (inference/kernels/__init__.py:149-178,
+    311-315) at both thread counts, and the fp16 path at M = 16."""
     import torch
 
     from glorcq_amd import format as fmt
     from oracle import glorcq_oracle as O
 
     p = fmt.make_linear(K_, N_, bits=BITS, group=GROUP, rank=RANK, M=M_, seed=0)
+    p16 = fmt.make_linear(K_, N_, bits=BITS, group=GROUP, rank=RANK, M=16, seed=0)
     threads = torch.get_num_threads()
     ref = O.linear_forward_fp16(p.x, p.q, p.scales, p.zeros, GROUP, U=p.U, SV=p.SV)
-    for _ in range(2):
-        O.linear_forward_fp16(p.x, p.q, p.scales, p.zeros, GROUP, U=p.U, SV=p.SV)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end and len(times) < 2000:
-        t0 = time.perf_counter()
-        O.linear_forward_fp16(p.x, p.q, p.scales, p.zeros, GROUP, U=p.U, SV=p.SV)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
+
+    def fp16(pp):
+        return lambda: O.linear_forward_fp16(pp.x, pp.q, pp.scales, pp.zeros, GROUP, U=pp.U,
+                                             SV=pp.SV)
+
+    def fp32(pp):
+        return lambda: O.linear_forward_fp32(pp.x, pp.q, pp.scales, pp.zeros, GROUP, U=pp.U,
+                                             SV=pp.SV)
+
+    rows = []
+    for path, M, fn in (("fp16", 1, fp16(p)), ("fp32", 1, fp32(p)), ("fp16", 16, fp16(p16))):
+        for t in ((threads, 1) if M == 1 else (threads,)):
+            torch.set_num_threads(t)
+            try:
+                med, n = _median_call(fn, budget_s)
+            finally:
+                torch.set_num_threads(threads)
+            rows.append({"path": path, "M": M, "threads": t, "calls": n,
+                         "us_per_call": round(med * 1e6, 1),
+                         "GB/s": round(layer_bytes(M=M) / med / 1e9, 4)})
+    main_row = rows[0]
     parity = O.parity_ok(gpu_y_config0, ref)
     err = float((gpu_y_config0.float().cpu() - ref.float()).abs().max())
     return {
-        "value": round(layer_bytes() / med / 1e9, 4), "unit": "GB/s", "cores": threads,
-        "kind": "port", "us_per_call": round(med * 1e6, 1),
-        "sample": (f"{len(times)} config-0 calls (K=2048,N=1408,2-bit,g128,r64,M=1) of the "
-                   f"reference CPU fallback restated in oracle/ (fp16 dequant loop + fp16 "
-                   f"x@W.T + fp16 LoRA), median, torch threads={threads}, "
+        "value": main_row["GB/s"], "unit": "GB/s", "cores": threads,
+        "kind": "port", "us_per_call": main_row["us_per_call"],
+        "sample": (f"{main_row['calls']} config-0 calls (K=2048,N=1408,2-bit,g128,r64,M=1) of "
+                   f"the reference CPU fallback restated in oracle/ (fp16 dequant loop + fp16 "
+                   f"x@W.T + fp16 LoRA), median after 3 warm-ups, torch threads={threads}, "
                    f"os.cpu_count()={os.cpu_count()}"),
+        "cpu_model": cpu_model_name(),
+        "rows": rows,
     }, parity, err
 
 
 def read_traffic():
-    """HBM bytes per GEMV launch from the committed rocprofv3 --pmc summary
+    """HBM bytes per fused launch from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE scaled by a plain copy's reading), or None."""
-    path = os.path.join(ROOT, "profiles", "gemv_lane_pool512_traffic.json")
+    path = os.path.join(ROOT, "profiles", "gemv_lane_fused_pool2048_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:

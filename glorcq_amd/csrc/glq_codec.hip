@@ -36,13 +36,15 @@ __global__ void unpack_kernel(const uint32_t* __restrict__ codes, int64_t words,
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
     int32_t q = (int32_t)((v >> (BITS * c)) & MASK);
-    if (sym && q >= (1 << (BITS - 1))) q -= (1 << BITS);
+    if (sym == 1 && q >= (1 << (BITS - 1))) q -= (1 << BITS);  // two's complement
+    if (sym == 2) q -= (1 << (BITS - 1));                       // stored offset by 2^(b-1)
     out[w * CPW + c] = q;
   }
 }
 
 // One thread per packed word: emits cpw fp16 weights, each rounded exactly as
-// the reference's fp16 dequant loop does: fp16(fp16(q - z) * s) (sym: q * s).
+// the reference's fp16 dequant loop does: fp16(fp16(q - z) * s) (sym: q * s;
+// sym == 2: q is the stored code minus 2^(b-1)).
 template <int BITS>
 __global__ void dequant_kernel(const uint32_t* __restrict__ codes, int64_t N,
                                int64_t K, const __half* __restrict__ scales,
@@ -64,10 +66,11 @@ __global__ void dequant_kernel(const uint32_t* __restrict__ codes, int64_t N,
     int32_t q = (int32_t)((v >> (BITS * c)) & MASK);
     __half s = scales[n * G + g];
     __half wq;
-    if (sym) {
+    if (sym == 1) {
       if (q >= (1 << (BITS - 1))) q -= (1 << BITS);
       wq = __hmul(__int2half_rn(q), s);
     } else {
+      if (sym == 2) q -= (1 << (BITS - 1));
       wq = __hmul(__hsub(__int2half_rn(q), zeros[n * G + g]), s);
     }
     W[n * K + k] = wq;
@@ -140,6 +143,7 @@ int glq_unpack_codes(const int32_t* codes, int64_t N, int64_t K, int bits,
   clear_error();
   int rc = check_codec_shape(N, K, bits);
   if (rc) return rc;
+  GLQ_CHECK(sym >= 0 && sym <= 2, "sym must be 0, 1 or 2 (got %d)", sym);
   const int64_t words = N * K / (32 / bits);
   if (words == 0) return GLQ_OK;
   GLQ_CHECK(codes && out, "null pointer");
@@ -163,9 +167,10 @@ int glq_dequant_weight(const int32_t* codes, int64_t N, int64_t K, int bits,
   GLQ_CHECK(group > 0 && K % group == 0,
             "K=%lld must be a multiple of group=%lld", (long long)K,
             (long long)group);
+  GLQ_CHECK(sym >= 0 && sym <= 2, "sym must be 0, 1 or 2 (got %d)", sym);
   const int64_t words = N * K / (32 / bits);
   if (words == 0) return GLQ_OK;
-  GLQ_CHECK(codes && scales && W && (sym || zeros), "null pointer");
+  GLQ_CHECK(codes && scales && W && (sym == 1 || zeros), "null pointer");
   const int bs = 256;
   const dim3 grid((unsigned)((words + bs - 1) / bs));
   hipStream_t s = (hipStream_t)stream;

@@ -56,11 +56,12 @@ extern "C" int glq_gemm_lora(const void* x, int64_t M, int64_t K, int64_t N,
   GLQ_CHECK(M >= 0 && K >= 0 && N >= 0, "negative size");
   if (M == 0 || N == 0) return GLQ_OK;
   GLQ_CHECK(bits == 2 || bits == 4, "bits must be 2 or 4 (got %d)", bits);
+  GLQ_CHECK(sym >= 0 && sym <= 2, "sym must be 0, 1 or 2 (got %d)", sym);
   GLQ_CHECK(group == 128, "the GEMM path takes group 128 (got %lld)", (long long)group);
   GLQ_CHECK(K > 0 && K % 128 == 0 && K < (1 << 24), "K=%lld must be a positive multiple of 128",
             (long long)K);
   GLQ_CHECK(N < (1ll << 30) && M < (1ll << 31) / 2 && M * K < (1ll << 31), "shape too large");
-  GLQ_CHECK(x && codes && scales && y && (sym || zeros), "null data pointer");
+  GLQ_CHECK(x && codes && scales && y && (sym == 1 || zeros), "null data pointer");
   const bool lora = SV != nullptr && rank > 0;
   if (lora) {
     GLQ_CHECK(rank % 8 == 0 && rank <= 512, "rank=%lld must be a multiple of 8, <= 512",

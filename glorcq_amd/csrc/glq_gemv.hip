@@ -243,10 +243,13 @@ int gemv_pick_tiles(int64_t items, int64_t N) {
 int gemv_check_shape(int64_t M, int64_t K, int64_t N, int bits, int64_t group, int sym,
                      int64_t rank, TileShape& sh) {
   GLQ_CHECK(bits == 2 || bits == 4, "bits must be 2 or 4 (got %d)", bits);
+  GLQ_CHECK(sym >= 0 && sym <= 2, "sym must be 0, 1 or 2 (got %d)", sym);
   GLQ_CHECK(M <= 16, "GEMV path takes 1 <= M <= 16 rows (got M=%lld)", (long long)M);
-  GLQ_CHECK(K > 0 && K % 128 == 0, "K=%lld must be a positive multiple of 128", (long long)K);
-  GLQ_CHECK(group > 0 && group % 128 == 0 && K % group == 0,
-            "group=%lld must be a multiple of 128 dividing K=%lld", (long long)group,
+  const int pc = 128 / bits;  // codes per 16-byte piece
+  GLQ_CHECK(K > 0 && K % pc == 0, "K=%lld must be a positive multiple of %d at %d bits",
+            (long long)K, pc, bits);
+  GLQ_CHECK(group > 0 && group % pc == 0 && K % group == 0,
+            "group=%lld must be a multiple of %d dividing K=%lld", (long long)group, pc,
             (long long)K);
   GLQ_CHECK(N < (1ll << 30) && K < (1ll << 24), "shape too large");
   if (rank > 0)
@@ -257,7 +260,8 @@ int gemv_check_shape(int64_t M, int64_t K, int64_t N, int bits, int64_t group, i
   sh.G = (int)(K / group);
   sh.group = (int)group;
   sh.rank = rank > 0 ? (int)rank : 0;
-  sh.sym = sym ? 1 : 0;
+  sh.sym = sym == 1 ? 1 : 0;
+  sh.zoff = sym == 2 ? (float)(1 << (bits - 1)) : 0.f;
   sh.kw = (int)(K * bits / 32);
   sh.rpad = (int)align_up(sh.rank, 32);
   sh.kp = (int)gemv_phase_len(M, K, group, bits);
@@ -280,6 +284,7 @@ bool stream_shape(int64_t M, const TileShape& sh, int bits, StreamShape& ss, siz
   ss.rank = sh.rank;
   ss.rpad = sh.rpad;
   ss.sym = sh.sym;
+  ss.zoff = sh.zoff;
   ss.kw = sh.kw;
   ss.nchunk = (int)(((int64_t)sh.kw * 4 + 127) / 128);
   ss.nsvc = sh.rank > 0 ? (sh.rank + 63) / 64 : 0;
@@ -351,15 +356,23 @@ static int launch_stream(const DenseStreamArgs& sa, int64_t items, int bits, boo
   return launch_stream_sym<false>(sa, items, bits, sz2, lds, s);
 }
 
-// Lane-sliced path (glq_lane.h): one token row, group 128, a code row of at
-// most 64 16-byte pieces, rank <= 128.
+// Lane-sliced path (glq_lane.h): one token row, groups of whole 16-byte
+// pieces, a code row of at most 64 pieces, rank <= 128.
 constexpr int kLanePD = 4;              // iterations of loads in flight per wave
 constexpr int64_t kLaneWaves = 4096;    // target waves per launch (4 per SIMD)
 
-static bool lane_shape(int64_t M, const TileShape& sh, int bits) {
+static bool lane_row_shape(const TileShape& sh, int bits) {
   if (getenv("GLQ_GEMV_NO_LANE")) return false;
-  return M == 1 && sh.group == 128 && sh.rank <= 128 && (int64_t)sh.K * bits / 128 <= 64;
+  return sh.group % (128 / bits) == 0 && sh.rank <= 128 && (int64_t)sh.K * bits / 128 <= 64;
 }
+
+static bool lane_shape(int64_t M, const TileShape& sh, int bits) {
+  return M == 1 && lane_row_shape(sh, bits);
+}
+
+// The tile and streaming kernels step over 128-code chunks, one group each
+// (or several whole groups).
+static bool tile_shape(const TileShape& sh) { return sh.K % 128 == 0 && sh.group % 128 == 0; }
 
 // Bytes of LDS the fused-x U form needs (partials of a, then a in fp16).
 static size_t lane_xu_lds(const LaneArgs& la) {
@@ -424,6 +437,8 @@ static int launch_lane(const DenseArgs& a, int bits, bool xu, hipStream_t s) {
   g.N = a.sh.N;
   g.K = a.sh.K;
   g.G = a.sh.G;
+  g.group = a.sh.group;
+  g.zoff = a.sh.zoff;
   g.kw = a.sh.kw;
   g.rank = a.sh.rank;
   g.items = a.items;
@@ -459,8 +474,24 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   TileShape sh;
   int rc = gemv_check_shape(M, K, N, bits, group, sym, lora ? rank : 0, sh);
   if (rc) return rc;
-  GLQ_CHECK(x && codes && scales && y && (sym || zeros), "null data pointer");
+  GLQ_CHECK(x && codes && scales && y && (sym == 1 || zeros), "null data pointer");
   if (lora) GLQ_CHECK(U != nullptr || xU != nullptr, "LoRA needs U or a precomputed xU");
+  GLQ_CHECK(tile_shape(sh) || lane_row_shape(sh, bits),
+            "K=%lld, group=%lld at %d bits: rows or groups that are not whole 128-code "
+            "chunks take the lane kernel only (at most %d codes a row, rank <= 128)",
+            (long long)K, (long long)group, bits, 64 * 128 / bits);
+  if (!tile_shape(sh) && M > 1) {
+    // one lane launch per token row (x, a and y rows of the items advance together)
+    for (int64_t m = 0; m < M; ++m) {
+      rc = gemv_impl(items, (const __half*)x + m * K, x_stride, 1, K, N, codes, codes_stride,
+                     bits, scales, zeros, sz_stride, group, sym, U, u_stride, SV, sv_stride,
+                     rank, xU ? (const __half*)xU + m * rank : nullptr, xu_stride, bias,
+                     bias_stride, (__half*)y + m * N, y_stride, workspace,
+                     workspace_bytes_given, stream);
+      if (rc) return rc;
+    }
+    return GLQ_OK;
+  }
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   GLQ_CHECK(al16(x) && al16(codes) && (!lora || al16(SV)) && (!lora || !U || al16(U)),
             "x, codes, U and SV must be 16-byte aligned");

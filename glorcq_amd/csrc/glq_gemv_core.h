@@ -62,6 +62,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // Problem shape shared by every item of one launch.
 struct TileShape {
   int K, N, G, group, rank, sym;
+  float zoff;   // added to every zero-point (signed codes stored offset by 2^(b-1))
   int kw;       // int32 words per weight row
   int rpad;     // rank rounded up to 32
   int kp;       // codes per K-phase staged in LDS (multiple of group)
@@ -546,7 +547,7 @@ __device__ void gemv_tile(const Src& src, const TileShape& sh, int item, int til
         const int row = idx / gl, g = idx - row * gl;
         const int n = min(r0 + row, N - 1);
         s_l[g * R + row] = __half2float(S[(int64_t)n * G + g0 + g]);
-        z_l[g * R + row] = sh.sym ? zsym : __half2float(Z[(int64_t)n * G + g0 + g]);
+        z_l[g * R + row] = sh.sym ? zsym : __half2float(Z[(int64_t)n * G + g0 + g]) + sh.zoff;
       }
     }
     __syncthreads();

@@ -200,6 +200,8 @@ __device__ __half* lane_xu_phase(const View& src, int K, int rank, bool lora, fl
 // w rpw .. w rpw + rpw - 1 and stores each round's rows at the round's end.
 struct LaneGeom {
   int N, K, G, kw, rank;
+  int group;   // codes per quantization group (a multiple of the piece's codes)
+  float zoff;  // added to every zero-point (signed codes stored offset by 2^(b-1))
   int lr;      // 16-byte pieces per code row
   int rounds;  // rounds of PD iterations per item (64-row units x LRP / PD)
   int wpi;     // waves per item
@@ -258,7 +260,7 @@ __device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, in
     const int pj = p + j * LRP;
     act[j] = pj < lg.lr;
     pc[j] = act[j] ? pj : lg.lr - 1;  // inactive pieces read a valid one (x = 0)
-    gq[j] = pc[j] * C / 128;          // the piece's quantization group
+    gq[j] = pc[j] * C / lg.group;     // the piece's quantization group
   }
 
   // ---- x slices in operand order, c1 = sum bias * x, c2 = sum x ----
@@ -292,6 +294,8 @@ __device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, in
           xw[j][8 * blk + q] = __builtin_bit_cast(uint32_t, pr);
         }
       }
+      // the zero-point offset leaves with the operand bias: z + zoff per piece
+      if constexpr (!SYM) c1[j] = fmaf(lg.zoff, c2[j], c1[j]);
     }
   };
   const bool lora = src.lora();

@@ -784,6 +784,7 @@ StreamShape moe_stream_shape(int K, int N, int bits, int rank, int mmax, int kpa
   s.rank = rank;
   s.rpad = (int)align_up(rank, 32);
   s.sym = 0;
+  s.zoff = 0.f;
   s.kw = K * bits / 32;
   s.nchunk = (kpart * bits / 8 + 127) / 128;
   s.nsvc = rank > 0 ? (rank + 63) / 64 : 0;

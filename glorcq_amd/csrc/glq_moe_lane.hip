@@ -460,6 +460,8 @@ LaneGeom role_geom(int N, int K, int bits, int rank, int items, bool pair,
   g.N = N;
   g.K = K;
   g.G = K / 128;
+  g.group = 128;
+  g.zoff = 0.f;
   g.kw = K * bits / 32;
   g.rank = rank;
   g.items = items;

@@ -83,6 +83,7 @@ struct PfArgs {
   int ks, gps;               // K splits, groups per split
   int out_bits;              // GATE/UP: decode order of inter's consumer (2 or 4)
   int max_tiles;             // token tiles in the grid (y dimension)
+  float zoff;                // added to every zero-point (signed codes stored offset by 2^(b-1))
 };
 
 // Position of natural column c inside its 16-code block in decode order
@@ -109,9 +110,9 @@ struct PfK {
 };
 
 template <int BITS, bool SYM>
-__device__ __forceinline__ PfK<BITS> pf_consts(__half sh, __half zh) {
+__device__ __forceinline__ PfK<BITS> pf_consts(__half sh, __half zh, float zoff) {
   PfK<BITS> k;
-  const float z = SYM ? (float)(1 << (BITS - 1)) : __half2float(zh);
+  const float z = SYM ? (float)(1 << (BITS - 1)) : __half2float(zh) + zoff;
   const float zi = rintf(z);
   k.zf = z - zi;
   k.s = __half2float(sh);
@@ -349,7 +350,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
       }
       const __half sh = *(const __half*)(sl + SL::S + wave * 256 + (rt * 16 + li) * 4);
       const __half zh = SYM ? sh : *(const __half*)(sl + SL::Z + wave * 256 + (rt * 16 + li) * 4);
-      kc[rt] = pf_consts<BITS, SYM>(sh, zh);
+      kc[rt] = pf_consts<BITS, SYM>(sh, zh, g.zoff);
     }
     // the group's sum of x (q - zi), fp32
     auto a_op = [&](int i, int t) -> f16x8 {
@@ -948,7 +949,8 @@ int pf_dense_gemm(const void* x, int64_t M, int64_t K, int64_t N, const int32_t*
   g.ks = P.ks;
   g.gps = P.gps;
   g.max_tiles = P.ntm;
-  return pf_launch_dense(g, bits, PfTile{P.tm, P.rt, P.deep}, sym != 0, s);
+  g.zoff = sym == 2 ? (float)(1 << (bits - 1)) : 0.f;
+  return pf_launch_dense(g, bits, PfTile{P.tm, P.rt, P.deep}, sym == 1, s);
 }
 }  // namespace glq
 

@@ -60,6 +60,7 @@ __device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0
 // Shape/layout of a streaming launch (every item has the same K and N).
 struct StreamShape {
   int K, N, G, rank, rpad, sym, kw;
+  float zoff;      // added to every zero-point (signed codes stored offset by 2^(b-1))
   int nchunk;      // 128-byte code chunks per row (last one may be partial)
   int nsvc;        // SV chunks per tile (64 rank columns each; 0 = no LoRA)
   int tiles;       // 16-row tiles per item
@@ -245,11 +246,14 @@ __device__ __forceinline__ float half_of(uint32_t w, int sh16) {
 }
 
 // Consumes one code chunk (2 steps) of a tile from its LDS slot.
-//   yacc += s_g * (MFMA sum of (2^e + q) x) per step (scale only), and
-//   corr -= sum_g s_g c1_g + (s_g z_g) c2_g over the chunk's groups, as two
-//   fp32 MFMAs (A = c1 / c2 of tokens x groups, B = s / s*z of groups x rows).
-// A group past K (2-bit tail) gets scale 0; `par*` select the fp16 half of
-// each staged scale dword.
+//   yacc += s_g * (MFMA sum of (2^e + q) x - c1_g) per step, the operand bias
+//   c1 = sum 2^e x of each D row's (token, group) leaving before the scale
+//   (so no sum of large terms runs across groups), and
+//   corr -= sum_g (s_g z_g) c2_g over the chunk's groups, as one fp32 MFMA
+//   (A = c2 of tokens x groups, B = s*z of groups x rows).
+// D rows: 4-bit, token 4kb+i of the step's group; 2-bit, token 8p + 4(kb&1)+i
+// of half kb>>1.  A group past K (2-bit tail) gets scale 0; `par*` select the
+// fp16 half of each staged scale dword.
 template <int BITS, int MP, bool SYM>
 __device__ __forceinline__ void stream_consume(const unsigned char* slot, int ch, int par0,
                                                int par1, int cpar, const StreamShape& sh,
@@ -269,10 +273,10 @@ __device__ __forceinline__ void stream_consume(const unsigned char* slot, int ch
     const uint32_t sw_ = *(const uint32_t*)(sz + ln.cszb);
     const float sc = gv ? half_of(sw_, 16 * cpar) : 0.f;
     float zc = (float)(1 << (BITS - 1));
-    if constexpr (!SYM) zc = half_of(*(const uint32_t*)(sz + ln.cszb + ln.czoff), 16 * cpar);
+    if constexpr (!SYM)
+      zc = half_of(*(const uint32_t*)(sz + ln.cszb + ln.czoff), 16 * cpar) + sh.zoff;
     const int gi = min(g, (stream_kpad(sh.K, BITS) >> 7) - 1);
-    const float c1 = xc[gi * 32 + li], c2 = xc[gi * 32 + 16 + li];
-    corr = mfma_16x16x4f32(c1, -sc, corr);
+    const float c2 = xc[gi * 32 + 16 + li];
     corr = mfma_16x16x4f32(c2, -sc * zc, corr);
   }
 #pragma unroll
@@ -284,6 +288,10 @@ __device__ __forceinline__ void stream_consume(const unsigned char* slot, int ch
     const uint32_t sw_ = *(const uint32_t*)(sz + ln.szb + sp * ln.szstep);
     float s = half_of(sw_, 16 * (sp ? par1 : par0));
     s = c128 * 128 < sh.K ? s : 0.f;
+    f32x4 cb[MP];  // c1 of the lane's D rows
+#pragma unroll
+    for (int p = 0; p < MP; ++p)
+      cb[p] = *(const f32x4*)(xc + c128 * 32 + (BITS == 2 ? 8 * p + 4 * (kb & 1) : 4 * kb));
     f32x4 acc[MP];
 #pragma unroll
     for (int p = 0; p < MP; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -306,7 +314,7 @@ __device__ __forceinline__ void stream_consume(const unsigned char* slot, int ch
 #pragma unroll
     for (int p = 0; p < MP; ++p)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) yacc[p][i] = fmaf(s, acc[p][i], yacc[p][i]);
+      for (int i = 0; i < 4; ++i) yacc[p][i] = fmaf(s, acc[p][i] - cb[p][i], yacc[p][i]);
   }
 }
 

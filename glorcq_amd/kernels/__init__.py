@@ -70,6 +70,19 @@ def _require(t: torch.Tensor, name: str, dtype=None) -> None:
         raise RuntimeError(f"{name} must be {dtype} (got {t.dtype})")
 
 
+SYM_UNSIGNED, SYM_SIGNED, SYM_SIGNED_ZEROS = 0, 1, 2
+
+
+def _sym_mode(sym) -> int:
+    """Code format of the C ABI's `sym` argument: False/0 unsigned codes with
+    zero-points, True/1 symmetric two's-complement codes, 2 signed codes with
+    zero-points stored offset by 2^(b-1)."""
+    m = int(sym)
+    if m not in (SYM_UNSIGNED, SYM_SIGNED, SYM_SIGNED_ZEROS):
+        raise RuntimeError(f"sym must be False/True or 0, 1, 2 (got {sym!r})")
+    return m
+
+
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Scratch for the x*U partial sums, one buffer per (device, current stream),
     grown on demand (it needs no initialisation)."""
@@ -101,7 +114,7 @@ def packed_dequant_matmul_fused(x: torch.Tensor, codes: torch.Tensor, scales: to
     library is called directly.  Arguments as _packed_dequant_matmul_eager."""
     if out is None:
         return torch.ops.glorcq_hip.packed_dequant_matmul(
-            x, codes, scales, zeros, bits, groupsize, bool(sym), U, SV, precomputed_xU, bias)
+            x, codes, scales, zeros, bits, groupsize, _sym_mode(sym), U, SV, precomputed_xU, bias)
     return _packed_dequant_matmul_eager(x, codes, scales, zeros, bits, groupsize, sym, U, SV,
                                         precomputed_xU, bias, out)
 
@@ -127,7 +140,8 @@ def _packed_dequant_matmul_eager(x: torch.Tensor, codes: torch.Tensor, scales: t
     _require(x, "x", torch.float16)
     _require(codes, "codes", torch.int32)
     _require(scales, "scales", torch.float16)
-    if not sym:
+    asym = _sym_mode(sym) != SYM_SIGNED
+    if asym:
         if zeros is None:
             raise RuntimeError("zeros required for asymmetric codes")
         _require(zeros, "zeros", torch.float16)
@@ -141,7 +155,7 @@ def _packed_dequant_matmul_eager(x: torch.Tensor, codes: torch.Tensor, scales: t
         raise RuntimeError(f"groupsize {groupsize} must divide K={K}")
     if scales.shape != (N, K // groupsize):
         raise RuntimeError(f"scales shape {tuple(scales.shape)} != ({N}, {K // groupsize})")
-    if not sym and zeros.shape != scales.shape:
+    if asym and zeros.shape != scales.shape:
         raise RuntimeError(f"zeros shape {tuple(zeros.shape)} != ({N}, {K // groupsize})")
     rank = 0
     if SV is not None:
@@ -178,7 +192,7 @@ def _packed_dequant_matmul_eager(x: torch.Tensor, codes: torch.Tensor, scales: t
         ws = workspace(x.device, nbytes)
         rc = lib.glq_gemm_lora(
             x.data_ptr(), M, K, N, codes.data_ptr(), bits, scales.data_ptr(), _lib.ptr(zeros),
-            groupsize, int(bool(sym)), _lib.ptr(U if precomputed_xU is None else None),
+            groupsize, _sym_mode(sym), _lib.ptr(U if precomputed_xU is None else None),
             _lib.ptr(SV), rank, _lib.ptr(precomputed_xU), _lib.ptr(bias), out.data_ptr(),
             ws.data_ptr(), ws.numel(), stream)
         _lib.check(rc, "glq_gemm_lora")
@@ -191,7 +205,7 @@ def _packed_dequant_matmul_eager(x: torch.Tensor, codes: torch.Tensor, scales: t
         xu = None if precomputed_xU is None else precomputed_xU[m0:m1]
         rc = lib.glq_gemv_lora(
             x[m0:m1].data_ptr(), mb, K, N, codes.data_ptr(), bits, scales.data_ptr(),
-            _lib.ptr(zeros), groupsize, int(bool(sym)),
+            _lib.ptr(zeros), groupsize, _sym_mode(sym),
             _lib.ptr(U if precomputed_xU is None else None), _lib.ptr(SV), rank,
             _lib.ptr(xu), _lib.ptr(bias), out[m0:m1].data_ptr(),
             ws.data_ptr(), ws.numel(), stream)
@@ -217,7 +231,7 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
     _require(x, "x", torch.float16)
     _require(codes, "codes", torch.int32)
     _require(scales, "scales", torch.float16)
-    if not sym:
+    if _sym_mode(sym) != SYM_SIGNED:
         _require(zeros, "zeros", torch.float16)
     if x.dim() == 2:  # one x for every problem
         E, (M, K), x_stride = codes.shape[0], x.shape, 0
@@ -272,7 +286,7 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
     rc = lib.glq_gemv_lora_batched(
         E, x.data_ptr(), x_stride, M, K, N, codes.data_ptr(), codes.shape[1] * codes.shape[2],
         bits, scales.data_ptr(), _lib.ptr(zeros), scales.shape[1] * scales.shape[2],
-        groupsize, int(bool(sym)), _lib.ptr(U if xu is None else None), K * rank, _lib.ptr(SV),
+        groupsize, _sym_mode(sym), _lib.ptr(U if xu is None else None), K * rank, _lib.ptr(SV),
         N * rank, rank, _lib.ptr(xu), M * rank, _lib.ptr(bias), N, out.data_ptr(), M * N,
         ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device))
     _lib.check(rc, "glq_gemv_lora_batched")
@@ -345,19 +359,48 @@ def gptq_dequant_matmul_fused(x, qweight_int, scales, zeros, groupsize, sym=Fals
                               lora_USV=None, bits: int | None = None):
     """Reference signature (inference/kernels/__init__.py:284): unpacked (N, K)
     integer codes, fp16 scales/zeros, optional (U, S, V) low-rank tuple ->
-    fp16 (B, N).
+    fp16 (B, N).  W = q s (sym) or (q - z) s, q the codes as given (the
+    reference's int8 cast, gptq_matmul.cu:15-16, 81-82).
 
     The reference casts the (N, K) int32 codes to int8 on every call; here they
-    are packed on the device instead (4-bit container unless `bits` is given,
-    which holds any code width <= 4).  Keep weights packed (GLoRCQLinear) to
-    avoid the per-call pack.
+    are range-checked (one aminmax, a host sync) and packed on the device into
+    the narrowest container that holds them (2 or 4 bits, or the `bits`
+    given): unsigned asymmetric codes as they are, signed ones (symmetric, or
+    asymmetric like the reference's tests' codes in [-2, 2] with non-integer
+    zero-points) offset by 2^(b-1) with the zero-points applied exactly.
+    Codes that fit no 4-bit form raise.  Keep weights packed (GLoRCQLinear)
+    to avoid the per-call check and pack.
     """
-    b = 4 if bits is None else bits
-    if b not in (2, 4):
-        b = 4 if b < 4 else b
-    if b > 4:
+    if bits is not None and bits not in (2, 4):
         raise RuntimeError(f"{bits}-bit codes are not supported (2 or 4)")
-    codes = pack_codes_device(qweight_int.to(torch.int32).contiguous(), b)
+    q = qweight_int
+    if q.dim() != 2:
+        raise RuntimeError("qweight_int must be (N, K)")
+    lo, hi = (0, 0) if q.numel() == 0 else (int(v) for v in torch.aminmax(q))
+    mode = None
+    K = q.shape[1]
+    # containers whose 16-byte pieces tile the rows and the groups
+    fits = [c for c in (2, 4) if K % (128 // c) == 0 and groupsize % (128 // c) == 0] or [4]
+    for b in ((bits,) if bits is not None else fits):
+        h = 1 << (b - 1)
+        if sym:
+            if -h <= lo and hi < h:
+                mode = SYM_SIGNED
+        elif 0 <= lo and hi < 2 * h:
+            mode = SYM_UNSIGNED
+        elif -h <= lo and hi < h:
+            mode = SYM_SIGNED_ZEROS
+        if mode is not None:
+            break
+    if mode is None:
+        raise RuntimeError(
+            f"{'symmetric' if sym else 'asymmetric'} codes span [{lo}, {hi}], which no "
+            f"{bits or 4}-bit container holds (unsigned 0..{(1 << (bits or 4)) - 1} or signed "
+            f"{-(1 << ((bits or 4) - 1))}..{(1 << ((bits or 4) - 1)) - 1})")
+    qi = q.to(torch.int32)
+    if mode == SYM_SIGNED_ZEROS:
+        qi = qi + (1 << (b - 1))  # stored offset by 2^(b-1); z is applied as given
+    codes = pack_codes_device(qi.contiguous(), b)
     xh = x.to(torch.float16).contiguous()
     U = SV = None
     if lora_USV is not None:
@@ -365,8 +408,8 @@ def gptq_dequant_matmul_fused(x, qweight_int, scales, zeros, groupsize, sym=Fals
         U = U_.to(torch.float16).contiguous()
         SV = (V_.float() * S_.float().unsqueeze(0)).to(torch.float16).contiguous()
     return packed_dequant_matmul_fused(xh, codes, scales.contiguous(),
-                                       None if zeros is None else zeros.contiguous(),
-                                       b, groupsize, sym, U=U, SV=SV)
+                                       None if mode == SYM_SIGNED else zeros.contiguous(),
+                                       b, groupsize, mode, U=U, SV=SV)
 
 
 def pack_codes_device(q: torch.Tensor, bits: int) -> torch.Tensor:
@@ -386,7 +429,7 @@ def unpack_codes(codes: torch.Tensor, bits: int, K: int, sym: bool = False) -> t
     _require(codes, "codes", torch.int32)
     N = codes.shape[0]
     out = torch.empty(N, K, dtype=torch.int32, device=codes.device)
-    _lib.check(lib.glq_unpack_codes(codes.data_ptr(), N, K, bits, int(bool(sym)), out.data_ptr(),
+    _lib.check(lib.glq_unpack_codes(codes.data_ptr(), N, K, bits, _sym_mode(sym), out.data_ptr(),
                                     _lib.stream_handle(codes.device)), "glq_unpack_codes")
     return out
 
@@ -401,7 +444,7 @@ def dequant_weight(codes: torch.Tensor, bits: int, K: int, scales: torch.Tensor,
     N = codes.shape[0]
     out = torch.empty(N, K, dtype=torch.float16, device=codes.device)
     _lib.check(lib.glq_dequant_weight(codes.data_ptr(), N, K, bits, scales.data_ptr(),
-                                      _lib.ptr(zeros), groupsize, int(bool(sym)), out.data_ptr(),
+                                      _lib.ptr(zeros), groupsize, _sym_mode(sym), out.data_ptr(),
                                       _lib.stream_handle(codes.device)), "glq_dequant_weight")
     return out
 

@@ -43,7 +43,7 @@ def _fail(msg: str):
 # ---------------------------------------------------------------------------
 @torch.library.custom_op(f"{_NS}::packed_dequant_matmul", mutates_args=())
 def packed_dequant_matmul(x: Tensor, codes: Tensor, scales: Tensor, zeros: Optional[Tensor],
-                          bits: int, groupsize: int, sym: bool, U: Optional[Tensor],
+                          bits: int, groupsize: int, sym: int, U: Optional[Tensor],
                           SV: Optional[Tensor], precomputed_xU: Optional[Tensor],
                           bias: Optional[Tensor]) -> Tensor:
     return _k._packed_dequant_matmul_eager(x, codes, scales, zeros, bits, groupsize, sym, U, SV,

@@ -5,15 +5,20 @@
  * correction" that a GLoRCQ quantized linear layer runs for every projection:
  *
  *     y[m, n] = sum_k W[n, k] * x[m, k]  +  sum_j a[m, j] * SV[n, j]  + bias[n]
- *     W[n, k] = s[n, k/g] * (q[n, k] - z[n, k/g])       (asymmetric)
- *     W[n, k] = s[n, k/g] * q_signed[n, k]              (symmetric)
+ *     W[n, k] = s[n, k/g] * (q[n, k] - z[n, k/g])       (asymmetric, sym = 0)
+ *     W[n, k] = s[n, k/g] * q_signed[n, k]              (symmetric, sym = 1)
+ *     W[n, k] = s[n, k/g] * (q_signed[n, k] - z[n, k/g])   (signed asymmetric, sym = 2)
  *     a[m, j] = sum_k x[m, k] * U[k, j]                 (or a caller-supplied a)
  *
  * Data format (device memory, all row-major, little-endian):
  *   codes   int32 (N, K*bits/32): b-bit codes packed LSB-first along K; code k
  *           of row n sits in word k/(32/b) at bit offset b*(k % (32/b)).
- *           Symmetric codes are stored as b-bit two's complement.
- *   scales  fp16 (N, K/g)     zeros fp16 (N, K/g) (ignored when sym != 0)
+ *           sym = 0: unsigned codes 0..2^b-1.  sym = 1: b-bit two's
+ *           complement.  sym = 2: signed codes -2^(b-1)..2^(b-1)-1 stored
+ *           as q + 2^(b-1) (two's complement with the sign bit flipped), so
+ *           that z stays exact in fp16 (the reference's int8 codes with
+ *           non-integer zero-points, gptq_matmul.cu:15-16).
+ *   scales  fp16 (N, K/g)     zeros fp16 (N, K/g) (ignored when sym == 1)
  *   U       fp16 (K, r)       input-side low-rank factor (shared per cluster)
  *   SV      fp16 (N, r)       output-side low-rank factor with S fused in
  *   x       fp16 (M, K)       y fp16 (M, N)      bias fp16 (N) or NULL
@@ -65,7 +70,12 @@ int64_t glq_gemv_workspace_bytes(int64_t items, int64_t M, int64_t K,
  * Fused dequant-GEMV + low-rank correction, 1 <= M <= 16 (decode).
  * Replaces gptq_dequant_matmul_fused (inference/kernels/__init__.py:284) and
  * the LoRA tail of GLoRCQLinear.forward (inference/quantized_linear.py:338-349).
- *   bits      2 or 4;  group % 128 == 0;  K % group == 0
+ *   bits      2 or 4;  K % group == 0;  group % 128 == 0, or any group of
+ *             whole 16-byte pieces (a multiple of 128/bits codes) when a
+ *             code row has at most 64 pieces and rank <= 128 (one lane-
+ *             kernel launch per token row: the reference's 64 x 64, group
+ *             64 case, test_gptq_kernel.py:193)
+ *   sym       0, 1 or 2 (code formats above)
  *   U, SV     may be NULL (no correction) ; rank % 8 == 0, rank <= 512
  *   xU        optional precomputed a = x*U (M, rank) fp16 (cluster-shared
  *             x*U, the `precomputed_xU` hook of quantized_linear.py:286); when

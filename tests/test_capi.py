@@ -68,10 +68,30 @@ def test_argument_checks_raise_before_any_launch(lib):
     rc = lib.glq_gemv_lora(1 << 12, 17, 2048, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 128, 0,
                            nul, nul, 0, nul, nul, 1 << 12, 1 << 12, 1 << 20, nul)
     assert rc == 1 and b"M" in lib.glq_last_error()
-    # group not multiple of 128
-    rc = lib.glq_gemv_lora(1 << 12, 1, 2048, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 64, 0,
+    # group 64 on a row too long for the lane kernel (the one kernel that takes
+    # groups below 128 codes)
+    rc = lib.glq_gemv_lora(1 << 12, 1, 16384, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 64, 0,
                            nul, nul, 0, nul, nul, 1 << 12, 1 << 12, 1 << 20, nul)
     assert rc == 1 and b"group" in lib.glq_last_error()
+    # group not a whole number of 16-byte pieces (64 codes at 2 bits)
+    rc = lib.glq_gemv_lora(1 << 12, 1, 2048, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 32, 0,
+                           nul, nul, 0, nul, nul, 1 << 12, 1 << 12, 1 << 20, nul)
+    assert rc == 1 and b"group" in lib.glq_last_error()
+    # K not a whole number of pieces (4-bit: 32 codes)
+    rc = lib.glq_gemv_lora(1 << 12, 1, 80, 64, 1 << 12, 4, 1 << 12, 1 << 12, 16, 0,
+                           nul, nul, 0, nul, nul, 1 << 12, 1 << 12, 1 << 20, nul)
+    assert rc == 1 and b"K=80" in lib.glq_last_error()
+    # code format
+    rc = lib.glq_gemv_lora(1 << 12, 1, 2048, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 128, 3,
+                           nul, nul, 0, nul, nul, 1 << 12, 1 << 12, 1 << 20, nul)
+    assert rc == 1 and b"sym" in lib.glq_last_error()
+    rc = lib.glq_gemm_lora(1 << 12, 64, 2048, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 128, 3,
+                           nul, nul, 0, nul, nul, 1 << 12, 1 << 12, 1 << 20, nul)
+    assert rc == 1 and b"sym" in lib.glq_last_error()
+    # signed codes with zero-points need the zero-points
+    rc = lib.glq_gemv_lora(1 << 12, 1, 2048, 1408, 1 << 12, 2, 1 << 12, nul, 128, 2,
+                           nul, nul, 0, nul, nul, 1 << 12, 1 << 12, 1 << 20, nul)
+    assert rc == 1 and b"null" in lib.glq_last_error()
     # workspace too small (two token rows: the x U partials need one; one row
     # forms x U inside its launch)
     rc = lib.glq_gemv_lora(1 << 12, 2, 2048, 1408, 1 << 12, 2, 1 << 12, 1 << 12, 128, 0,
@@ -134,3 +154,36 @@ def test_python_boundary_rejects_cpu_tensors():
     with pytest.raises(RuntimeError, match="GPU"):
         kernels.packed_dequant_matmul_fused(x, codes, s, s, 2, 128)
     assert kernels.is_cuda_available() is False
+
+
+def test_gptq_signature_range_checks_codes():
+    """gptq_dequant_matmul_fused takes the reference's (N, K) integer codes;
+    codes no 4-bit container holds raise before any device work (the
+    reference would wrap them in its int8 cast)."""
+    import torch
+
+    from glorcq_amd import kernels
+
+    x = torch.zeros(1, 128, dtype=torch.float32)
+    s = torch.ones(16, 1, dtype=torch.float16)
+    q = torch.zeros(16, 128, dtype=torch.int32)
+    q[3, 5] = 16                                   # asymmetric: above 0..15
+    with pytest.raises(RuntimeError, match=r"span \[0, 16\]"):
+        kernels.gptq_dequant_matmul_fused(x, q, s, s, 128, False)
+    q[3, 5] = -9                                   # signed: below -8
+    with pytest.raises(RuntimeError, match="span"):
+        kernels.gptq_dequant_matmul_fused(x, q, s, s, 128, False)
+    q[3, 5] = 8                                    # symmetric: above 7
+    with pytest.raises(RuntimeError, match="symmetric codes span"):
+        kernels.gptq_dequant_matmul_fused(x, q, s, None, 128, True)
+    q[3, 5] = 2                                    # a 2-bit container asked for [-2, 2]
+    q[4, 5] = -2
+    with pytest.raises(RuntimeError, match="2-bit"):
+        kernels.gptq_dequant_matmul_fused(x, q, s, s, 128, False, bits=2)
+    with pytest.raises(RuntimeError, match="2 or 4"):
+        kernels.gptq_dequant_matmul_fused(x, q, s, s, 128, False, bits=3)
+    # in range: the pack is the first device step
+    with pytest.raises(RuntimeError, match="GPU"):
+        kernels.gptq_dequant_matmul_fused(x, q, s, s, 128, False)
+    with pytest.raises(RuntimeError, match="sym must be"):
+        kernels._sym_mode(3)
