@@ -211,7 +211,7 @@ def pmc_workload():
     print("pmc workload done", flush=True)
 
 
-MOE_BATCHES = (1, 4, 16, 32)
+MOE_BATCHES = (1, 2, 4, 16, 32)
 MFMA_FP16_PEAK_TFLOPS = 2500.0
 PREFILL = ((2048, 1408, 2, "expert gate/up 2-bit"), (2048, 2048, 4, "attention q/k/v/o 4-bit"))
 
@@ -293,59 +293,111 @@ def bench_prefill(dev):
     return res
 
 
-def bench_moe(dev, seed=6, reps=20, trials=15):
-    """Config 2 (Qwen1.5-MoE-A2.7B block, BASELINE.json): one decode step of
-    the whole block per call (router, top-4 dispatch, routed 2-bit experts with
-    cluster-shared LoRA, 4-bit shared expert, combine: four launches), `reps`
-    steps captured in one hipGraph, replays timed with HIP events (median of
-    `trials`).  Bytes per step follow format.moe_step_bytes with this run's
-    active experts and clusters, read off the GPU's own router logits."""
+def _graph_step_us(fn, reps, trials):
+    """Median over `trials` replays of one hipGraph holding `reps` calls of fn
+    (captured after 3 warm-up calls on a side stream), us per call."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    ts = []
+    for _ in range(trials):
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3 / reps)
+    ts.sort()
+    del graph
+    return ts[len(ts) // 2]
+
+
+def _moe_decode_leg(dev, p, reps, trials):
+    """One decode step of the block built from MoE problem p: us, bytes, GB/s."""
     import torch
 
     from glorcq_amd import format as fmt
     from glorcq_amd.moe_block import GraphCompatibleMoeBlock
 
+    B = p.B
+    blk = GraphCompatibleMoeBlock.from_problem(p, dev)
+    h = p.h.reshape(1, B, p.H).to(dev)
+    _, logits = blk(h)
+    us = _graph_step_us(lambda: blk(h), reps, trials)
+    sel = torch.topk(logits.float().cpu(), p.top_k, dim=-1).indices
+    act = sorted(set(sel.flatten().tolist()))
+    clusters = {proj: len({int(p.cluster_of[proj][e]) for e in act}) for proj in fmt.PROJS}
+    nbytes = fmt.moe_step_bytes(p, len(act), clusters)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del blk
+    return {"us_per_step": round(us, 2), "us_per_token": round(us / B, 3),
+            "tokens_per_s": round(B / (us * 1e-6), 1),
+            "active_experts": len(act), "active_clusters": clusters,
+            "algorithmic_bytes": nbytes, "achieved_GBps": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def bench_moe(dev, seed=6, reps=20, trials=15):
+    """Config 2 (Qwen1.5-MoE-A2.7B block, BASELINE.json): one decode step of
+    the whole block per call (router, top-4 dispatch, routed 2-bit experts with
+    cluster-shared LoRA, 4-bit shared expert, combine), `reps` steps captured
+    in one hipGraph, replays timed with HIP events (median of `trials`).
+    Bytes per step follow format.moe_step_bytes with this run's active
+    experts and clusters, read off the GPU's own router logits."""
+    from glorcq_amd import format as fmt
+
     res = {}
     for B in MOE_BATCHES:
-        p = fmt.make_moe(B=B, seed=seed)
-        blk = GraphCompatibleMoeBlock.from_problem(p, dev)
-        h = p.h.reshape(1, B, p.H).to(dev)
-        side = torch.cuda.Stream(device=dev)
-        side.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(side):
-            for _ in range(3):
-                _, logits = blk(h)
-        torch.cuda.current_stream(dev).wait_stream(side)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for _ in range(reps):
-                blk(h)
-        for _ in range(3):
-            graph.replay()
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        ts = []
-        for _ in range(trials):
-            e0.record()
-            graph.replay()
-            e1.record()
-            torch.cuda.synchronize()
-            ts.append(e0.elapsed_time(e1) * 1e3 / reps)
-        ts.sort()
-        us = ts[len(ts) // 2]
-        sel = torch.topk(logits.float().cpu(), p.top_k, dim=-1).indices
-        act = sorted(set(sel.flatten().tolist()))
-        clusters = {proj: len({int(p.cluster_of[proj][e]) for e in act}) for proj in fmt.PROJS}
-        nbytes = fmt.moe_step_bytes(p, len(act), clusters)
-        gbs = nbytes / (us * 1e-6) / 1e9
-        res[str(B)] = {"us_per_step": round(us, 2), "us_per_token": round(us / B, 3),
-                       "tokens_per_s": round(B / (us * 1e-6), 1),
-                       "active_experts": len(act), "active_clusters": clusters,
-                       "algorithmic_bytes": nbytes, "achieved_GBps": round(gbs, 1),
-                       "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
-        log(f"moe B={B}: {us:.2f} us/step, {us / B:.3f} us/token, {gbs:.0f} GB/s")
-        del graph, blk
+        r = _moe_decode_leg(dev, fmt.make_moe(B=B, seed=seed), reps, trials)
+        res[str(B)] = r
+        log(f"moe B={B}: {r['us_per_step']:.2f} us/step, {r['us_per_token']:.3f} us/token, "
+            f"{r['achieved_GBps']:.0f} GB/s")
+    return res
+
+
+def bench_mixtral(dev, seed=3, reps=20, trials=11, prefill_tokens=512):
+    """Config 3 (a Mixtral-8x7B-shaped MoE layer: H 4096, ffn 14336, 8 experts,
+    top-2 renormalised, 2-bit g128 experts, rank-64 LoRA over 2 clusters, no
+    shared expert): decode steps at B = 1, 4, 16 (hipGraph replays, bytes as
+    bench_moe), and a prefill of `prefill_tokens` tokens through the grouped
+    GEMM path (glq_moe_prefill), timed the same way."""
+    import torch
+
+    from glorcq_amd import format as fmt
+    from glorcq_amd.moe_block import GraphCompatibleMoeBlock
+
+    res = {"decode": {}}
+    for B in (1, 4, 16):
+        r = _moe_decode_leg(dev, fmt.make_mixtral_layer(B=B, seed=seed), reps, trials)
+        res["decode"][str(B)] = r
+        log(f"mixtral decode B={B}: {r['us_per_step']:.2f} us/step, "
+            f"{r['achieved_GBps']:.0f} GB/s")
+    T = prefill_tokens
+    p = fmt.make_mixtral_layer(B=T, seed=seed)
+    blk = GraphCompatibleMoeBlock.from_problem(p, dev)
+    h = p.h.reshape(1, T, p.H).to(dev)
+    us = _graph_step_us(lambda: blk(h), 3, trials)
+    q = p.experts["gate"]
+    flops = 2 * T * p.top_k * 3 * p.H * p.inter + 2 * T * p.top_k * 3 * p.rank * (p.H + p.inter)
+    res["prefill"] = {"tokens": T, "us": round(us, 1), "tokens_per_s": round(T / (us * 1e-6), 1),
+                      "flops": flops, "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+                      "expert_bits": q.bits}
+    log(f"mixtral prefill T={T}: {us:.1f} us, {flops / (us * 1e-6) / 1e12:.1f} TF/s")
+    del blk
+    torch.cuda.synchronize()
     return res
 
 
@@ -622,6 +674,8 @@ def main():
                          "clusters, 4-bit shared expert inter 5632), seed 6, one hipGraph of 20 "
                          "steps per replay"),
             "by_batch": moe}
+        log("Mixtral-shaped MoE layer (config 3): decode steps and a prefill")
+        result["mixtral_layer"] = bench_mixtral(dev)
     if not args.no_turbo:
         log("TurboQuant codebook GEMV (the reference's 2-bit expert format), M = 1")
         result["turbo_codec_gemv"] = bench_turbo(dev)

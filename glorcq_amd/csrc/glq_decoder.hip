@@ -100,7 +100,8 @@ __global__ __launch_bounds__(kDecThreads) void rmsnorm_kernel(
 // One decode token per batch row: q/k head RMSNorm (weights qw / kw over the
 // 128 head dims), rotary embedding q' = q cos + rotate_half(q) sin with every
 // product and the sum rounded to fp16 (apply_rotary_pos_emb), k' and v
-// written to the static cache at position *pos; q' to q_out (B, Hq, 128).
+// written to the static cache at position *pos; q' to q_out (B, Hq, 128)
+// (NaN when *pos is outside the cache).
 // One wave per head: heads [0, Hq) are q, [Hq, Hq + Hk) k, then Hk of v.
 // Lane l holds dims 2l, 2l + 1; rotate_half pairs lane l with lane l ^ 32.
 // ---------------------------------------------------------------------------
@@ -156,9 +157,13 @@ __global__ __launch_bounds__(kDecThreads) void qk_norm_rope_kernel(QkArgs a) {
   f16x2 o;
 #pragma unroll
   for (int e = 0; e < 2; ++e) o[e] = (_Float16)((float)hmul(n[e], c[e]) + (float)hmul(rot[e], s[e]));
-  if (kind == 0)
+  if (kind == 0) {
+    // a position past the static cache attends without this token: q' goes
+    // out as NaN so the step's output shows it (transformers' StaticLayer
+    // raises on the out-of-range cache write instead)
+    if (!in_cache) o = f16x2{(_Float16)__builtin_nanf(""), (_Float16)__builtin_nanf("")};
     ((f16x2*)(a.q_out + ((int64_t)b * a.Hq + h) * kHeadDim))[lane] = o;
-  else if (in_cache)
+  } else if (in_cache)
     ((f16x2*)(a.k_cache + crow))[lane] = o;
 }
 

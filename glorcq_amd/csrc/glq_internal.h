@@ -53,7 +53,7 @@ inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 // MoE decode steps of at most this many tokens take the lane path
 // (glq_moe_lane.hip) when their shapes fit it; both entry points return -1 /
 // an error when it does not.
-constexpr int kMoeLaneMaxB = 4;
+constexpr int kMoeLaneMaxB = 16;
 int64_t moe_lane_workspace_bytes(const glq_moe_params* p);
 int moe_lane_decode(const glq_moe_params* p, void* workspace, int64_t workspace_bytes,
                     hipStream_t s);

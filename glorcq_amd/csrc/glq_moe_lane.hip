@@ -18,8 +18,11 @@
 //                            (both matrices' row n in one lane group), with
 //                            their a SV^T terms, writing the pick's inter
 //  4. moe_lane_down_kernel   routed down rows of every pick without the
-//                            low-rank term (fp32); with LoRA, workgroups past
-//                            them form each pick's a_down = fp16(inter U_down)
+//                            low-rank term (fp32); rows of more than 64
+//                            pieces in K parts of at most 64 (one a lane),
+//                            summed in part order at the combine; with LoRA,
+//                            workgroups past them form each pick's a_down =
+//                            fp16(inter U_down)
 //  5. moe_lane_sdown_kernel  the shared expert's down rows, each row's store
 //                            combining out = fp16(sum_k w_k (y_k + a_down,k
 //                            SV_k^T) + gate * fp16(shared)) (+ the caller's
@@ -41,7 +44,7 @@
 namespace glq {
 
 constexpr int kMoeLaneThreads = 512;  // 8 waves (the lane x U form)
-constexpr int kMoeLaneWaves = 4096;   // target waves per lane role
+constexpr int kMoeLaneWaves = 2048;   // target waves per lane role
 constexpr int64_t kMoeLaneXuAllBytes = 12ll << 20;  // all clusters' x U in the router launch
 
 struct MoeLaneArgs {
@@ -71,8 +74,9 @@ struct MoeLaneArgs {
   int xuall;        // 1: a for every cluster in the router's launch
   int su;           // K slices of gate/up (H), and of down (I)
   int sd;
+  int kd, kdp;      // routed down: K parts of a row (one lane piece each), codes per part
   __half* inter;    // [P][I] each pick's inter
-  float* yb;        // [P][H] routed down outputs without the low-rank term
+  float* yb;        // [kd][P][H] routed down outputs per K part, without the low-rank term
   float* ad;        // [P][sd][rank] fp32 partial sums of each pick's a_down
   __half* sinter;   // [B][SI] the shared expert's inter
   // outputs
@@ -85,6 +89,17 @@ struct MoeLaneArgs {
 };
 
 constexpr int kXuSlice = 512;  // codes per x U job
+
+// Iterations of row loads in flight per wave: gate/up pairs; single rows of
+// np pieces a lane (fewer for several pieces, whose x slices hold registers).
+#ifndef GLQ_MOE_PAIR_PD
+#define GLQ_MOE_PAIR_PD 4
+#endif
+#ifndef GLQ_MOE_ROW_PD
+#define GLQ_MOE_ROW_PD 4
+#endif
+constexpr int kMoePairPD = GLQ_MOE_PAIR_PD;
+constexpr int moe_lane_pd(int np) { return np >= 3 ? 2 : np == 2 ? 4 : GLQ_MOE_ROW_PD; }
 
 __device__ __forceinline__ int moe_lane_clamp(int v, int n) { return min(max(v, 0), n - 1); }
 
@@ -131,24 +146,41 @@ struct RguSrc {
   }
 };
 
-// Routed down rows of pick p without the low-rank term (added at the combine).
+// Routed down rows of pick p over K part q (codes q kdp .. + kdp of each
+// row) without the low-rank term (added at the combine, with the parts).
+template <int BITS>
 struct RdItem {
   const MoeLaneArgs& a;
-  int p, e;
+  int p, e, q;
   __device__ bool lora() const { return false; }
-  __device__ const uint32_t* codes() const { return a.codes[2] + (int64_t)e * a.c_es[2]; }
-  __device__ const __half* scales() const { return a.scales[2] + (int64_t)e * a.s_es[2]; }
-  __device__ const __half* zeros() const { return a.zeros[2] + (int64_t)e * a.s_es[2]; }
+  __device__ const uint32_t* codes() const {
+    return a.codes[2] + (int64_t)e * a.c_es[2] + q * (a.kdp * BITS / 32);
+  }
+  __device__ const __half* scales() const {
+    return a.scales[2] + (int64_t)e * a.s_es[2] + q * (a.kdp / 128);
+  }
+  __device__ const __half* zeros() const {
+    return a.zeros[2] + (int64_t)e * a.s_es[2] + q * (a.kdp / 128);
+  }
   __device__ const __half* sv() const { return nullptr; }
   __device__ const __half* bias() const { return nullptr; }
   __device__ const __half* u() const { return nullptr; }
-  __device__ u32x4 x8(int k) const { return *(const u32x4*)(a.inter + (int64_t)p * a.I + k); }
+  __device__ u32x4 x8(int k) const {
+    return *(const u32x4*)(a.inter + (int64_t)p * a.I + q * a.kdp + k);
+  }
   __device__ __half load_a(int) const { return __float2half(0.f); }
-  __device__ void store(int n, float v) const { a.yb[(int64_t)p * a.H + n] = v; }
+  __device__ void store(int n, float v) const {
+    a.yb[((int64_t)q * a.B * a.topk + p) * a.H + n] = v;
+  }
 };
+template <int BITS>
 struct RdSrc {
   const MoeLaneArgs& a;
-  __device__ RdItem bind(int p) const { return RdItem{a, p, a.sel[p]}; }
+  // item = p kd + q
+  __device__ RdItem<BITS> bind(int item) const {
+    const int p = item / a.kd;
+    return RdItem<BITS>{a, p, a.sel[p], item - p * a.kd};
+  }
 };
 
 // x U jobs: the input row and U of one (pick, matrix).
@@ -196,7 +228,8 @@ __device__ void moe_lane_routed_rows(const MoeLaneArgs& a, int t, int n0, int nr
   __syncthreads();
   for (int i = tid; i < nrows * K; i += nth) {
     const int rr = i / K, k = i - rr * K, n = min(n0 + rr, a.H - 1), pk = t * K + k;
-    float y = a.yb[(int64_t)pk * a.H + n];
+    float y = 0.f;
+    for (int q = 0; q < a.kd; ++q) y += a.yb[((int64_t)q * a.B * K + pk) * a.H + n];
     if (lora) {
       const __half* sv = a.SV[2] + (int64_t)a.sel[pk] * a.sv_es[2] + (int64_t)n * r;
       const __half* ak = adl + k * r;
@@ -363,7 +396,7 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_route_kernel(MoeLane
   b -= nxu;
   if constexpr (SBITS != 0) {
     const int wvb = moe_lane_wave();
-    lane_run<SguSrc, SBITS, false, SLRP, 1, 4, 1, false, false, true>(SguSrc{a}, a.gSGU,
+    lane_run<SguSrc, SBITS, false, SLRP, 1, kMoePairPD, 1, false, false, true>(SguSrc{a}, a.gSGU,
                                                                      b * 8 + wvb, wvb, nullptr);
   }
 }
@@ -382,11 +415,10 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_xu_kernel(MoeLaneArg
 template <int BITS, int LRP, int NSV>
 __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_gu_kernel(MoeLaneArgs a) {
   const int wvb = moe_lane_wave();
-  lane_run<RguSrc, BITS, false, LRP, 1, 4, NSV, false, false, true>(
+  lane_run<RguSrc, BITS, false, LRP, 1, kMoePairPD, NSV, false, false, true>(
       RguSrc{a}, a.gRGU, blockIdx.x * 8 + wvb, wvb, nullptr);
 }
 
-constexpr int moe_lane_pd(int np) { return np >= 3 ? 2 : 4; }
 
 template <int BITS, int LRP, int NP>
 __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_down_kernel(MoeLaneArgs a) {
@@ -400,8 +432,8 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_down_kernel(MoeLaneA
     return;
   }
   const int wvb = moe_lane_wave();
-  lane_run<RdSrc, BITS, false, LRP, NP, moe_lane_pd(NP), 1, false, false>(
-      RdSrc{a}, a.gRD, blockIdx.x * 8 + wvb, wvb, nullptr);
+  lane_run<RdSrc<BITS>, BITS, false, LRP, NP, moe_lane_pd(NP), 1, false, false>(
+      RdSrc<BITS>{a}, a.gRD, blockIdx.x * 8 + wvb, wvb, nullptr);
 }
 
 // Each workgroup holds one token's rows (wpi a multiple of 8): first the
@@ -467,10 +499,12 @@ LaneGeom role_geom(int N, int K, int bits, int rank, int items, bool pair,
   g.items = items;
   g.lr = K * bits / 128;
   const int lrp = lane_lrp(g.lr), np = (g.lr + 63) / 64;
-  const int pd = pair ? 4 : moe_lane_pd(np);
+  const int pd = pair ? kMoePairPD : moe_lane_pd(np);
   g.rounds = (N + 63) / 64 * lrp * (pair ? 2 : 1) / pd;
   const int64_t total = (int64_t)items * g.rounds;
-  const int64_t rpw = std::max<int64_t>(1, (total + kMoeLaneWaves - 1) / kMoeLaneWaves);
+  int64_t waves = kMoeLaneWaves;
+  if (const char* e = getenv("GLQ_MOE_LANE_WAVES")) waves = std::max(1, atoi(e));
+  const int64_t rpw = std::max<int64_t>(1, (total + waves - 1) / waves);
   g.wpi = (int)((g.rounds + rpw - 1) / rpw);
   if (whole_wgs) g.wpi = (g.wpi + 7) / 8 * 8;  // each workgroup within one item
   g.rpw = (g.rounds + g.wpi - 1) / g.wpi;
@@ -548,7 +582,20 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   P.lora = lora;
   P.rc = H <= 512 ? 1 : H <= 1024 ? 2 : H <= 2048 ? 4 : 8;
   a.gRGU = role_geom((int)I, (int)H, bits, r, P_, true);
-  a.gRD = role_geom((int)H, (int)I, bits, 0, P_, false);
+  // routed down rows longer than 64 pieces: K parts of whole groups, each at
+  // most 64 pieces (one a lane), the smallest such count that divides the row
+  a.kd = 1;
+  if (I * bits / 128 > 64)
+    for (int kd = 2; kd <= (int)(I / 128); ++kd)
+      if ((I / 128) % kd == 0 && (I / 128 / kd) * bits <= 64) {
+        a.kd = kd;
+        break;
+      }
+  if (const char* e = getenv("GLQ_MOE_LANE_KD")) a.kd = atoi(e) == 1 ? 1 : a.kd;
+  a.kdp = (int)(I / a.kd);
+  a.gRD = role_geom((int)H, a.kdp, bits, 0, P_ * a.kd, false);
+  a.gRD.G = (int)(I / 128);       // scale rows and code rows keep their full pitch
+  a.gRD.kw = (int)(I * bits / 32);
   a.nrd = (int)role_blocks(a.gRD);
   a.su = (int)((H + kXuSlice - 1) / kXuSlice);
   a.sd = (int)((I + kXuSlice - 1) / kXuSlice);
@@ -578,7 +625,7 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   a.xuall = lora && ubytes <= kMoeLaneXuAllBytes && !getenv("GLQ_MOE_LANE_XU_GATE") ? 1 : 0;
   P.off_agu = take(4 * 2 * (int64_t)r * a.su * (a.xuall ? (int64_t)a.C * B : P_));
   P.off_inter = take(2 * (int64_t)P_ * I);
-  P.off_yb = take(4 * (int64_t)P_ * H);
+  P.off_yb = take(4 * (int64_t)a.kd * P_ * H);
   P.off_ad = take(4 * (int64_t)P_ * a.sd * r);
   P.off_sinter = take(SI > 0 ? 2 * B * SI : 0);
   P.ws_need = o;

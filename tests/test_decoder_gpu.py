@@ -120,6 +120,8 @@ def test_qk_norm_rope_matches_framework(gpu, B, pos, shared_rows):
 
 
 def test_qk_norm_rope_out_of_range_position_writes_nothing(gpu):
+    """A position past the static cache writes no cache row and turns q' into
+    NaN, so the step's attention output shows the overflow."""
     B, Hq, Hk, hd, L = 1, 32, 4, 128, 64
     q = torch.randn(B, Hq * hd, device=gpu).half()
     k, v = torch.randn(B, Hk * hd, device=gpu).half(), torch.randn(B, Hk * hd, device=gpu).half()
@@ -128,10 +130,11 @@ def test_qk_norm_rope_out_of_range_position_writes_nothing(gpu):
     kc = torch.zeros(B, Hk, L, hd, dtype=torch.float16, device=gpu)
     vc = torch.zeros_like(kc)
     ln = torch.zeros(1, dtype=torch.int32, device=gpu)
-    kernels.qk_norm_rope(q, k, v, w, w, 1e-6, cos, sin, kc, vc,
-                         torch.tensor(L, dtype=torch.int64, device=gpu), ln)
+    qo = kernels.qk_norm_rope(q, k, v, w, w, 1e-6, cos, sin, kc, vc,
+                              torch.tensor(L, dtype=torch.int64, device=gpu), ln)
     torch.cuda.synchronize()
     assert not kc.any() and not vc.any() and int(ln) == L + 1
+    assert torch.isnan(qo.float()).all()
 
 
 @pytest.mark.parametrize("B,Hq,Hk,L,maxlen", [(1, 32, 4, 1, 640), (1, 32, 4, 513, 640),

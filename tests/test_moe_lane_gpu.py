@@ -44,7 +44,7 @@ def check_both(p, gpu, monkeypatch, what):
     return out
 
 
-@pytest.mark.parametrize("B,seed", [(1, 0), (2, 3), (4, 1)])
+@pytest.mark.parametrize("B,seed", [(1, 0), (2, 3), (4, 1), (8, 6), (16, 6)])
 def test_config2(gpu, monkeypatch, B, seed):
     """BASELINE config 2 (Qwen1.5-MoE-A2.7B block: 60 experts, top-4, 16
     clusters, 4-bit shared expert of 5632 whose down rows take three 16-byte
@@ -62,12 +62,14 @@ def test_config2_lora_heavy(gpu, monkeypatch, B):
     check_both(p, gpu, monkeypatch, f"config 2 lora x30 B={B}")
 
 
-def test_config3_mixtral_decode(gpu, monkeypatch):
-    """BASELINE config 3 at M=1: H 4096 (64 pieces a gate/up row), ffn 14336
-    (the routed down rows take four pieces per lane), no shared expert."""
-    p = lora_heavy(fmt.make_mixtral_layer(B=1, seed=3), f=3.0)
+@pytest.mark.parametrize("B", [1, 8])
+def test_config3_mixtral_decode(gpu, monkeypatch, B):
+    """H 4096 (64 pieces a gate/up row), ffn 14336 (the
+    routed down rows in four K parts of 56 pieces, summed at the combine), no
+    shared expert."""
+    p = lora_heavy(fmt.make_mixtral_layer(B=B, seed=3), f=3.0)
     assert margin(p) >= 2
-    check_both(p, gpu, monkeypatch, "config 3 B=1")
+    check_both(p, gpu, monkeypatch, f"config 3 B={B}")
 
 
 def test_config4_block(gpu, monkeypatch):
