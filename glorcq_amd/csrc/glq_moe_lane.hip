@@ -46,6 +46,7 @@ namespace glq {
 constexpr int kMoeLaneThreads = 512;  // 8 waves (the lane x U form)
 constexpr int kMoeLaneWaves = 2048;   // target waves per lane role
 constexpr int64_t kMoeLaneXuAllBytes = 12ll << 20;  // all clusters' x U in the router launch
+constexpr int64_t kMoeLaneXuAllPairs = 32;          // ... for at most this many (cluster, token)
 
 struct MoeLaneArgs {
   int B, H, E, I, SI, topk, norm, C, rank;
@@ -619,10 +620,15 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   P.off_sel = take(4 * P_);
   P.off_wts = take(2 * P_);
   P.off_sg = take(2 * B);
-  // a of every cluster in the router's launch when all clusters' U take a few
-  // MB (the block's clusters few), else of the picks after routing
+  // a of every (cluster, token) in the router's launch when all clusters' U
+  // take a few MB and the pairs are few (then it saves a launch), else of the
+  // picks after routing (measured on config 2: every pair wins at B <= 2,
+  // the picks from B = 4)
   const int64_t ubytes = 2 * (int64_t)a.C * H * r * 2;
-  a.xuall = lora && ubytes <= kMoeLaneXuAllBytes && !getenv("GLQ_MOE_LANE_XU_GATE") ? 1 : 0;
+  a.xuall = lora && ubytes <= kMoeLaneXuAllBytes && (int64_t)a.C * B <= kMoeLaneXuAllPairs &&
+                    !getenv("GLQ_MOE_LANE_XU_GATE")
+                ? 1
+                : 0;
   P.off_agu = take(4 * 2 * (int64_t)r * a.su * (a.xuall ? (int64_t)a.C * B : P_));
   P.off_inter = take(2 * (int64_t)P_ * I);
   P.off_yb = take(4 * (int64_t)a.kd * P_ * H);

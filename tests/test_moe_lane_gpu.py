@@ -122,11 +122,12 @@ def test_residual_and_repeat(gpu, monkeypatch):
     assert bar(o1.reshape(2, p.H).cpu(), ref)
 
 
-@pytest.mark.parametrize("B", [1, 3])
+@pytest.mark.parametrize("B", [1, 2])
 def test_xu_forms_agree(gpu, monkeypatch, B):
-    """a = x U of gate/up formed for every cluster in the router's launch (few
-    clusters) or for the picks in a launch of its own (GLQ_MOE_LANE_XU_GATE):
-    the same sums in the same order, so the same bits."""
+    """a = x U of gate/up formed for every (cluster, token) in the router's
+    launch (16 clusters x B <= 2 tokens) or for the picks in a launch of its
+    own (GLQ_MOE_LANE_XU_GATE): the same sums in the same order, so the same
+    bits."""
     monkeypatch.delenv("GLQ_MOE_NO_LANE", raising=False)
     p = lora_heavy(fmt.make_moe(B=B, seed=1))
     blk = GraphCompatibleMoeBlock.from_problem(p, gpu)
