@@ -31,6 +31,8 @@ its output doubles as the parity check of the GPU result for the same input.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --pmc-workload   (the GEMV kernel alone + a plain copy
                                          of known size, for rocprofv3 --pmc)
+       python bench.py --pmc-workload-kernels   (MoE decode steps and prefill
+                                                 GEMMs, for rocprofv3 --pmc)
 """
 
 from __future__ import annotations
@@ -209,6 +211,42 @@ def pmc_workload():
         dst.copy_(src)
     torch.cuda.synchronize()
     print("pmc workload done", flush=True)
+
+
+def pmc_workload_kernels():
+    """What the MoE and prefill counter profiles run: 4 eager decode steps of
+    the config-2 block (B = 1, 16) and of the config-3 layer (B = 1, 16), then
+    4 prefill GEMMs with a precomputed a per config-1 shape at M = 512."""
+    import torch
+
+    from glorcq_amd import format as fmt
+    from glorcq_amd import kernels
+    from glorcq_amd.moe_block import GraphCompatibleMoeBlock
+
+    dev = torch.device("cuda:0")
+    for tag, p in (("config 2 B=1", fmt.make_moe(B=1, seed=6)),
+                   ("config 2 B=16", fmt.make_moe(B=16, seed=6)),
+                   ("config 3 B=1", fmt.make_mixtral_layer(B=1, seed=3)),
+                   ("config 3 B=16", fmt.make_mixtral_layer(B=16, seed=3))):
+        blk = GraphCompatibleMoeBlock.from_problem(p, dev)
+        h = p.h.reshape(1, p.B, p.H).to(dev)
+        for _ in range(4):
+            blk(h)
+        torch.cuda.synchronize()
+        print(tag, flush=True)
+        del blk
+    for K, N, bits, name in PREFILL:
+        M = 512
+        p = fmt.make_linear(K, N, bits=bits, group=GROUP, rank=RANK, M=M, seed=3)
+        d = {k: getattr(p, k).to(dev) for k in ("codes", "scales", "zeros", "U", "SV", "x")}
+        xu = kernels.lowrank_xu(d["x"], d["U"])
+        out = torch.empty(M, N, dtype=torch.float16, device=dev)
+        for _ in range(4):
+            kernels.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"],
+                                                bits, GROUP, SV=d["SV"], precomputed_xU=xu,
+                                                out=out)
+        torch.cuda.synchronize()
+        print(name, flush=True)
 
 
 MOE_BATCHES = (1, 2, 4, 16, 32)
@@ -538,6 +576,8 @@ def main():
     ap.add_argument("--pool", type=int, default=POOL)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--pmc-workload", action="store_true")
+    ap.add_argument("--pmc-workload-kernels", action="store_true",
+                    help="the MoE and prefill counter profiles' workload")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE block leg")
     ap.add_argument("--no-turbo", action="store_true", help="skip the TurboQuant codec leg")
     ap.add_argument("--no-model", action="store_true",
@@ -552,6 +592,9 @@ def main():
               "multi-GPU sharding is described in DESIGN.md, not built. Use --gpus 1.",
               file=sys.stderr)
         return 2
+    if args.pmc_workload_kernels:
+        pmc_workload_kernels()
+        return 0
     if args.pmc_workload:
         pmc_workload()
         return 0

@@ -80,6 +80,9 @@ struct MoeLaneArgs {
   float* yb;        // [kd][P][H] routed down outputs per K part, without the low-rank term
   float* ad;        // [P][sd][rank] fp32 partial sums of each pick's a_down
   __half* sinter;   // [B][SI] the shared expert's inter
+  int nrw;          // router workgroups per token (each a slice of the router rows)
+  __half* lgw;      // [B][E + 1] logits of the sliced router
+  unsigned* rcnt;   // [B] router arrival counters (zero between steps)
   // outputs
   __half* out;
   const __half* res;
@@ -286,15 +289,18 @@ struct SdSrc {
   __device__ SdItem bind(int t) const { return SdItem{a, t, n0, routed}; }
 };
 
-// ---- router: one workgroup per token ----
+// ---- router: a.nrw workgroups per token ----
 // Logits of the E router rows (+ the shared-expert gate row) as fp32 dot
 // products over the lanes (16-byte loads, v_dot2), each rounded to fp16 once;
-// a wave loads RB rows at once (RC 8-half chunks a lane each).  Then the
-// routing of moe_topk_ranks (glq_moe.hip) for this one token: thread e ranks
-// expert e by counting the keys above its own, wave 0 forms the softmax sum
-// (a cross-lane sum in the same order) and the weights.
+// a wave loads RB rows at once (RC 8-half chunks a lane each), workgroup q
+// of the token the rows of pass q (8 RB rows).  With several workgroups each
+// publishes its logits and counts itself in; the last (acquiring them) routes
+// the token and leaves the counter at zero for the next step.  The routing is
+// moe_topk_ranks' (glq_moe.hip) for this one token: thread e ranks expert e
+// by counting the keys above its own, wave 0 forms the softmax sum (a
+// cross-lane sum in the same order) and the weights.
 template <int RC>
-__device__ void moe_lane_router(const MoeLaneArgs& a, int t, unsigned char* smem) {
+__device__ void moe_lane_router(const MoeLaneArgs& a, int t, int q, unsigned char* smem) {
   constexpr int RB = RC >= 8 ? 2 : 16 / RC;  // rows per wave per pass
   uint16_t* lgh = (uint16_t*)smem;                                    // [E + 1] fp16 logits
   uint32_t* keys = (uint32_t*)(smem + ((2 * (a.E + 1) + 15) & ~15));  // [E]
@@ -308,28 +314,51 @@ __device__ void moe_lane_router(const MoeLaneArgs& a, int t, unsigned char* smem
     const int k = 8 * lane + 512 * j;
     hv[j] = k < a.H ? *(const u32x4*)(hx + k) : u32x4{0u, 0u, 0u, 0u};
   }
-  for (int r0 = RB * wave; r0 < nrow; r0 += 8 * RB) {
+  const int rend = a.nrw > 1 ? min(nrow, 8 * RB * (q + 1)) : nrow;
+  for (int r0 = 8 * RB * q + RB * wave; r0 < rend; r0 += 8 * RB) {
     u32x4 v[RB][RC];
 #pragma unroll
-    for (int q = 0; q < RB; ++q) {
-      const int r = min(r0 + q, nrow - 1);
+    for (int i = 0; i < RB; ++i) {
+      const int r = min(r0 + i, nrow - 1);
       const __half* w = r < a.E ? a.rw + (int64_t)r * a.H : a.sgw;
 #pragma unroll
       for (int j = 0; j < RC; ++j) {
         const int k = 8 * lane + 512 * j;
-        v[q][j] = k < a.H ? *(const u32x4*)(w + k) : u32x4{0u, 0u, 0u, 0u};
+        v[i][j] = k < a.H ? *(const u32x4*)(w + k) : u32x4{0u, 0u, 0u, 0u};
       }
     }
 #pragma unroll
-    for (int q = 0; q < RB; ++q) {
+    for (int i = 0; i < RB; ++i) {
       float sacc = 0.f;
 #pragma unroll
       for (int j = 0; j < RC; ++j)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) sacc = dot2(v[q][j][c], hv[j][c], sacc);
+        for (int c = 0; c < 4; ++c) sacc = dot2(v[i][j][c], hv[j][c], sacc);
       sacc = lane_group_sum<64>(sacc);
-      if (lane == 0 && r0 + q < nrow) lgh[r0 + q] = __half_as_ushort(__float2half(sacc));
+      if (lane == 0 && r0 + i < rend) {
+        const __half lg = __float2half(sacc);
+        lgh[r0 + i] = __half_as_ushort(lg);
+        if (a.nrw > 1) a.lgw[(int64_t)t * (a.E + 1) + r0 + i] = lg;
+      }
     }
+  }
+  if (a.nrw > 1) {
+    // arrival (as the many-token router's): stores complete, released at
+    // device scope, counted; the last workgroup acquires every slice
+    __shared__ int last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      __threadfence();
+      const bool l = atomicAdd(a.rcnt + t, 1u) == (unsigned)(a.nrw - 1);
+      if (l) __threadfence();
+      last = l;
+    }
+    __syncthreads();
+    if (!last) return;
+    for (int r = tid; r < nrow; r += kMoeLaneThreads)
+      lgh[r] = __half_as_ushort(a.lgw[(int64_t)t * (a.E + 1) + r]);
+    if (tid == 0) a.rcnt[t] = 0u;
   }
   __syncthreads();
   for (int e = tid; e < a.E; e += kMoeLaneThreads) {
@@ -377,11 +406,11 @@ template <int SBITS, int SLRP, int RC>
 __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_route_kernel(MoeLaneArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   int b = blockIdx.x;
-  if (b < a.B) {
-    moe_lane_router<RC>(a, b, smem);
+  if (b < a.B * a.nrw) {
+    moe_lane_router<RC>(a, b / a.nrw, b % a.nrw, smem);
     return;
   }
-  b -= a.B;
+  b -= a.B * a.nrw;
   const int nxu = a.xuall ? 2 * a.C * a.B * a.su : 0;
   if (b < nxu) {  // job b = ((m C + c) B + t) su + s
     const int s = b % a.su, mct = b / a.su, t = mct % a.B, mc = mct / a.B;
@@ -518,7 +547,8 @@ struct MoeLanePlan {
   MoeLaneArgs a;
   int bits, sbits, rc;
   bool lora;
-  int64_t off_sel, off_wts, off_sg, off_agu, off_inter, off_yb, off_ad, off_sinter, ws_need;
+  int64_t off_sel, off_wts, off_sg, off_lgw, off_agu, off_inter, off_yb, off_ad, off_sinter,
+      ws_need;
   size_t lds_route, lds_xu, lds_comb;
 };
 
@@ -582,6 +612,13 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   P.sbits = sbits;
   P.lora = lora;
   P.rc = H <= 512 ? 1 : H <= 1024 ? 2 : H <= 2048 ? 4 : 8;
+  {
+    // router rows per workgroup: one pass of 8 waves x RB rows
+    const int rb = P.rc >= 8 ? 2 : 16 / P.rc, nrow = (int)p->experts + (SI > 0 ? 1 : 0);
+    a.nrw = (nrow + 8 * rb - 1) / (8 * rb);
+    // (the counters of 48 tokens fill bytes 64 .. 255 of the workspace)
+    if (getenv("GLQ_MOE_LANE_ROUTER1") || B > 48) a.nrw = 1;
+  }
   a.gRGU = role_geom((int)I, (int)H, bits, r, P_, true);
   // routed down rows longer than 64 pieces: K parts of whole groups, each at
   // most 64 pieces (one a lane), the smallest such count that divides the row
@@ -608,9 +645,10 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   } else {
     a.rows_wg = std::max(1, 256 / a.topk);
   }
-  // The first 256 bytes hold the many-token path's router arrival counter,
-  // which must stay zero between steps (glq_moe.hip): a workspace may serve
-  // both paths (steps of different sizes), so this path never writes there.
+  // The first 256 bytes hold the many-token path's router arrival counter
+  // (word 0) and this path's per-token router counters (bytes 64 ..), all of
+  // which must be zero between steps: a workspace may serve both paths
+  // (steps of different sizes).
   int64_t o = 256;
   auto take = [&](int64_t bytes) {
     const int64_t at = o;
@@ -620,6 +658,7 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   P.off_sel = take(4 * P_);
   P.off_wts = take(2 * P_);
   P.off_sg = take(2 * B);
+  P.off_lgw = take(2 * B * (p->experts + 1));
   // a of every (cluster, token) in the router's launch when all clusters' U
   // take a few MB and the pairs are few (then it saves a launch), else of the
   // picks after routing (measured on config 2: every pair wins at B <= 2,
@@ -646,7 +685,7 @@ template <int SBITS, int SLRP, int RC>
 static int launch_route(const MoeLanePlan& P, hipStream_t s) {
   const MoeLaneArgs& a = P.a;
   const int64_t grid =
-      a.B + (a.xuall ? 2 * a.C * a.B * a.su : 0) + (SBITS ? role_blocks(a.gSGU) : 0);
+      a.B * a.nrw + (a.xuall ? 2 * a.C * a.B * a.su : 0) + (SBITS ? role_blocks(a.gSGU) : 0);
   const size_t lds = a.xuall ? std::max(P.lds_route, P.lds_xu) : P.lds_route;
   static size_t attr = 64 * 1024;
   int rc = set_lds_limit(moe_lane_route_kernel<SBITS, SLRP, RC>, lds, attr);
@@ -796,6 +835,11 @@ int moe_lane_decode(const glq_moe_params* p, void* workspace, int64_t workspace_
   a.sel = (int32_t*)(w + P.off_sel);
   a.wts = (__half*)(w + P.off_wts);
   a.sg = (__half*)(w + P.off_sg);
+  a.lgw = (__half*)(w + P.off_lgw);
+  // the per-token router counters sit in bytes 64 .. 127, which the
+  // many-token path leaves unused (its counter is word 0; its tables start at
+  // 256): both zero before the first step and after every step
+  a.rcnt = (unsigned*)(w + 64);
   a.agu = (float*)(w + P.off_agu);
   a.inter = (__half*)(w + P.off_inter);
   a.yb = (float*)(w + P.off_yb);
