@@ -54,6 +54,13 @@ inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 // (glq_moe_lane.hip) when their shapes fit it; both entry points return -1 /
 // an error when it does not.
 constexpr int kMoeLaneMaxB = 16;
+// Both MoE decode paths start their workspace tables at kMoeWsHeader bytes.
+// The header holds arrival counters, zero between steps: word 0 (the
+// many-token router), bytes 64 .. 255 (the lane path's per-token router
+// counters), bytes 1024 .. 2559 and 2560 .. 4095 (the lane path's token-tile
+// row-block counters of the shared gate/up and the shared down).
+constexpr int64_t kMoeWsHeader = 4096;
+constexpr int kMoeT16MaxRB = 384;  // row blocks a token-tile role may count
 int64_t moe_lane_workspace_bytes(const glq_moe_params* p);
 int moe_lane_decode(const glq_moe_params* p, void* workspace, int64_t workspace_bytes,
                     hipStream_t s);

@@ -968,6 +968,7 @@ int moe_plan(const glq_moe_params* p, MoePlan& P) {
     return at;
   };
   P.off_rcnt = take(4);  // must be zero before the first step; every step leaves it zero
+  o = kMoeWsHeader;      // the rest of the header: the lane path's counters
   // (the picked-cluster lists are sized whether or not this step is gated,
   // so the workspace size does not depend on the form)
   P.off_tab = take(4 * (1 + (2 + kMoeTB) * (int64_t)a.nbm + 2 + 2 * std::min<int64_t>(a.C, P_)));

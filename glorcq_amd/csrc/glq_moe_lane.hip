@@ -10,7 +10,8 @@
 //                            shared-expert gate sigmoid(fp16 logit); the other
 //                            workgroups run the shared expert's gate and up
 //                            rows in pairs and write its inter = fp16(fp16(
-//                            silu(g)) * u) (moe_block.py:465-468)
+//                            silu(g)) * u) (moe_block.py:465-468); from 8
+//                            tokens in the token-tile form (glq_tile16.h)
 //  2. moe_lane_xu_kernel     (with LoRA) one workgroup per (pick, gate/up):
 //                            a = fp16(x U_c) of the pick's cluster (the
 //                            cluster-shared precompute, moe_block.py:290-322)
@@ -40,6 +41,7 @@
 #include "glq_lane.h"
 #include "glq_moe_route.h"
 #include "glq_stream.h"
+#include "glq_tile16.h"
 
 namespace glq {
 
@@ -88,6 +90,9 @@ struct MoeLaneArgs {
   const __half* res;
   __half* logits;
   LaneGeom gSGU, gRGU, gRD, gSD;
+  T16Geom gS16, gSD16;  // the shared gate/up and down in the tile form (t16s, t16d)
+  int t16s, t16d;
+  float* rtd;           // [B][H] routed part of the outputs (t16d)
   int nrd;          // workgroups of the routed down rows
   int rows_wg;      // output rows per shared-down workgroup (its combine)
 };
@@ -215,6 +220,25 @@ struct SguSrc {
   __device__ SguItem bind(int t) const { return SguItem{a, t}; }
 };
 
+// Shared gate and up of every token at once (glq_tile16.h: one decode of each
+// code for all token rows), storing the shared inter.
+struct SguTileView {
+  const MoeLaneArgs& a;
+  __device__ const uint32_t* codes(int m) const { return a.scodes[m]; }
+  __device__ const __half* scales(int m) const { return a.sscales[m]; }
+  __device__ const __half* zeros(int m) const { return a.szeros[m]; }
+  __device__ const __half* xrow(int t) const { return a.h + (int64_t)t * a.H; }
+  __device__ void prep(int, int, int) const {}
+  __device__ void store(int n, int t, float g, float u) const {
+    a.sinter[(int64_t)t * a.SI + n] = swiglu_fp16(g, u);
+  }
+};
+struct SguTileSrc {
+  const MoeLaneArgs& a;
+  __device__ SguTileView bind() const { return SguTileView{a}; }
+};
+constexpr int kMoeT16MinB = 8;  // tokens from which the shared expert takes the tile form
+
 // Routed part of output rows [n0, n0 + nrows) of token t into LDS routed[]:
 // sum_k w_k (y_k[n] + a_down,k SV_down,k[n]^T), fmaf over the picks in pick
 // order (the many-token combine's order), a_down = fp16(sum of its slices'
@@ -287,6 +311,71 @@ struct SdSrc {
   int n0;
   const float* routed;
   __device__ SdItem bind(int t) const { return SdItem{a, t, n0, routed}; }
+};
+
+// Shared down rows of every token in the token-tile form.  Before it
+// publishes its block, K slice s of row block rb forms the routed part of the
+// block's rows for tokens s, s + ks, ... (the sums of moe_lane_routed_rows, in
+// its order: a_down = fp16(sum of its slices' partials) into LDS, each pick's
+// y (K parts in order) + a_down SV^T, then the picks in pick order) into
+// rtd[t][n]; the finishing workgroup's store combines as SdItem's.
+struct SdTileView {
+  const MoeLaneArgs& a;
+  __half* adl;     // LDS [P][rank]
+  float* contrib;  // LDS [tokens of the slice][64][topk]
+  __device__ const uint32_t* codes(int) const { return a.scodes[2]; }
+  __device__ const __half* scales(int) const { return a.sscales[2]; }
+  __device__ const __half* zeros(int) const { return a.szeros[2]; }
+  __device__ const __half* xrow(int t) const { return a.sinter + (int64_t)t * a.SI; }
+  __device__ void prep(int rb, int s, int ks) const {
+    const int tid = threadIdx.x, K = a.topk, r = a.rank, n0 = kT16Rows * rb;
+    const bool lora = r > 0 && a.SV[2] != nullptr;
+    const int nt = (a.B - s + ks - 1) / ks;  // tokens s, s + ks, ...
+    if (lora)
+      for (int i = tid; i < nt * K * r; i += kMoeLaneThreads) {
+        const int tk = i / r, j = i - tk * r, pk = (s + ks * (tk / K)) * K + tk % K;
+        adl[pk * r + j] = __float2half(sum_strided(a.ad + (int64_t)pk * a.sd * r + j, r, a.sd));
+      }
+    __syncthreads();
+    for (int i = tid; i < nt * kT16Rows * K; i += kMoeLaneThreads) {
+      const int k = i % K, tr = i / K, t = s + ks * (tr / kT16Rows);
+      const int n = min(n0 + tr % kT16Rows, a.H - 1), pk = t * K + k;
+      float y = 0.f;
+      for (int q = 0; q < a.kd; ++q) y += a.yb[((int64_t)q * a.B * K + pk) * a.H + n];
+      if (lora) {
+        const __half* sv = a.SV[2] + (int64_t)a.sel[pk] * a.sv_es[2] + (int64_t)n * r;
+        const __half* ak = adl + pk * r;
+        float l = 0.f;
+        for (int j = 0; j < r; j += 8) {
+          const u32x4 s8 = *(const u32x4*)(sv + j), a8 = *(const u32x4*)(ak + j);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) l = dot2(s8[q], a8[q], l);
+        }
+        y += l;
+      }
+      contrib[i] = y;
+    }
+    __syncthreads();
+    for (int tr = tid; tr < nt * kT16Rows; tr += kMoeLaneThreads) {
+      const int t = s + ks * (tr / kT16Rows), n = n0 + tr % kT16Rows;
+      float acc = 0.f;
+      for (int k = 0; k < K; ++k)
+        acc = fmaf(__half2float(a.wts[t * K + k]), contrib[tr * K + k], acc);
+      if (n < a.H) t16_put(a.rtd + (int64_t)t * a.H + n, acc);
+    }
+  }
+  // out = fp16(routed + gate * fp16(shared)) (+ residual)
+  __device__ void store(int n, int t, float v) const {
+    float acc = t16_get(a.rtd + (int64_t)t * a.H + n);
+    acc = fmaf(__half2float(a.sg[t]), __half2float(__float2half(v)), acc);
+    float o = __half2float(__float2half(acc));
+    if (a.res) o += __half2float(a.res[(int64_t)t * a.H + n]);
+    a.out[(int64_t)t * a.H + n] = __float2half(o);
+  }
+};
+struct SdTileSrc {
+  SdTileView v;
+  __device__ SdTileView bind() const { return v; }
 };
 
 // ---- router: a.nrw workgroups per token ----
@@ -402,7 +491,7 @@ __device__ __forceinline__ int moe_lane_wave() {
 // Workgroups [0, B): the router of each token; then (xuall) one per (matrix,
 // cluster, token) forming a = fp16(h_t U_c); then the shared expert's
 // gate/up rows.
-template <int SBITS, int SLRP, int RC>
+template <int SBITS, int SLRP, int RC, bool T16>
 __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_route_kernel(MoeLaneArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   int b = blockIdx.x;
@@ -424,7 +513,9 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_route_kernel(MoeLane
     return;
   }
   b -= nxu;
-  if constexpr (SBITS != 0) {
+  if constexpr (T16) {
+    t16_run<SguTileSrc, true>(SguTileSrc{a}, a.gS16, b, (float*)smem);
+  } else if constexpr (SBITS != 0) {
     const int wvb = moe_lane_wave();
     lane_run<SguSrc, SBITS, false, SLRP, 1, kMoePairPD, 1, false, false, true>(SguSrc{a}, a.gSGU,
                                                                      b * 8 + wvb, wvb, nullptr);
@@ -488,6 +579,15 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_sdown_kernel(MoeLane
                                                                 wv0 + wvb, wvb, nullptr);
 }
 
+// The shared down and combine in the token-tile form (4-bit shared codes).
+// LDS: the tile form's partial blocks, then adl and contrib.
+__global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_sdown_t16_kernel(MoeLaneArgs a) {
+  extern __shared__ __align__(16) float lds[];
+  __half* adl = (__half*)(lds + t16_lds_bytes(false) / 4);
+  float* contrib = lds + t16_lds_bytes(false) / 4 + (a.B * a.topk * a.rank + 7) / 8 * 4;
+  t16_run<SdTileSrc, false>(SdTileSrc{SdTileView{a, adl, contrib}}, a.gSD16, blockIdx.x, lds);
+}
+
 // Without a shared expert: out = fp16(routed) (+ residual), 256 threads a
 // workgroup, rows_wg rows of one token each.
 __global__ __launch_bounds__(256) void moe_lane_combine_kernel(MoeLaneArgs a) {
@@ -543,13 +643,28 @@ LaneGeom role_geom(int N, int K, int bits, int rank, int items, bool pair,
 
 int64_t role_blocks(const LaneGeom& g) { return ((int64_t)g.items * g.wpi + 7) / 8; }
 
+// Token-tile role of N rows of K 4-bit codes for M tokens (glq_tile16.h);
+// part and cnt are set with the workspace.
+T16Geom t16_geom(int N, int K, int M) {
+  T16Geom t{};
+  t.N = N;
+  t.K = K;
+  t.G = K / 128;
+  t.kw = K / 8;
+  t.M = M;
+  t.RB = (N + kT16Rows - 1) / kT16Rows;
+  t.ks = (t.G + kT16Waves - 1) / kT16Waves;
+  return t;
+}
+int64_t t16_wgs(const T16Geom& t) { return (int64_t)t.RB * t.ks; }
+
 struct MoeLanePlan {
   MoeLaneArgs a;
   int bits, sbits, rc;
   bool lora;
   int64_t off_sel, off_wts, off_sg, off_lgw, off_agu, off_inter, off_yb, off_ad, off_sinter,
-      ws_need;
-  size_t lds_route, lds_xu, lds_comb;
+      off_t16p, off_rtd, ws_need;
+  size_t lds_route, lds_xu, lds_comb, lds_sd16;
 };
 
 }  // namespace
@@ -639,17 +754,27 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   a.sd = (int)((I + kXuSlice - 1) / kXuSlice);
   if (SI > 0) {
     a.gSGU = role_geom((int)SI, (int)H, sbits, 0, (int)B, true);
+    // from kMoeT16MinB tokens the shared gate/up runs in the tile form: each
+    // code decoded once for every token (4-bit codes, 8 <= H/128 <= 32)
+    a.t16s = sbits == 4 && B >= kMoeT16MinB && H >= 1024 && (SI + 63) / 64 <= kMoeT16MaxRB &&
+             !getenv("GLQ_MOE_NO_T16");
+    if (a.t16s) a.gS16 = t16_geom((int)SI, (int)H, (int)B);
     a.gSD = role_geom((int)H, (int)SI, sbits, 0, (int)B, false, true);
+    // (the shared down's routed part is formed by the K slices: at least 2)
+    a.t16d = sbits == 4 && B >= kMoeT16MinB && SI > 1024 && (H + 63) / 64 <= kMoeT16MaxRB &&
+             !getenv("GLQ_MOE_NO_T16");
+    if (a.t16d) a.gSD16 = t16_geom((int)H, (int)SI, (int)B);
     const int lr = a.gSD.lr, rpi = 64 / lane_lrp(lr), pd = moe_lane_pd((lr + 63) / 64);
     a.rows_wg = rpi * pd * 8 * a.gSD.rpw;
   } else {
     a.rows_wg = std::max(1, 256 / a.topk);
   }
-  // The first 256 bytes hold the many-token path's router arrival counter
-  // (word 0) and this path's per-token router counters (bytes 64 ..), all of
+  // The header (kMoeWsHeader bytes) holds the many-token path's router
+  // arrival counter (word 0), this path's per-token router counters (bytes
+  // 64 ..) and its token-tile row-block counters (bytes 1024 ..), all of
   // which must be zero between steps: a workspace may serve both paths
   // (steps of different sizes).
-  int64_t o = 256;
+  int64_t o = kMoeWsHeader;
   auto take = [&](int64_t bytes) {
     const int64_t at = o;
     o += align_up(std::max<int64_t>(bytes, 1), 256);
@@ -673,27 +798,44 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   P.off_yb = take(4 * (int64_t)a.kd * P_ * H);
   P.off_ad = take(4 * (int64_t)P_ * a.sd * r);
   P.off_sinter = take(SI > 0 ? 2 * B * SI : 0);
+  // the token-tile roles' partial blocks (the shared gate/up's and the shared
+  // down's run in different launches and share them) and the routed part
+  const int64_t t16p = std::max(a.t16s ? t16_wgs(a.gS16) * 2 : 0, a.t16d ? t16_wgs(a.gSD16) : 0);
+  P.off_t16p = take(4 * t16p * kT16Elems);
+  P.off_rtd = take(a.t16d ? 4 * B * H : 0);
   P.ws_need = o;
   P.lds_route = (size_t)(((2 * (a.E + 1) + 15) & ~15) + 4 * a.E + 4 * 16);
   P.lds_xu = lora ? (size_t)LaneXu(r).lds_bytes(r) : 0;
   P.lds_comb = (size_t)(4 * ((a.topk * r + 1) / 2) + 4 * a.rows_wg * (a.topk + 1));
+  P.lds_sd16 = 0;
+  if (a.t16d) {
+    const int64_t nt = (B + a.gSD16.ks - 1) / a.gSD16.ks;  // tokens of a K slice's routed part
+    P.lds_sd16 = (size_t)(t16_lds_bytes(false) + 16 * ((P_ * r + 7) / 8) + 4 * nt * kT16Rows * a.topk);
+  }
   return true;
 }
 
 // ---- launches ----
-template <int SBITS, int SLRP, int RC>
-static int launch_route(const MoeLanePlan& P, hipStream_t s) {
+template <int SBITS, int SLRP, int RC, bool T16>
+static int launch_route_t(const MoeLanePlan& P, hipStream_t s) {
   const MoeLaneArgs& a = P.a;
-  const int64_t grid =
-      a.B * a.nrw + (a.xuall ? 2 * a.C * a.B * a.su : 0) + (SBITS ? role_blocks(a.gSGU) : 0);
-  const size_t lds = a.xuall ? std::max(P.lds_route, P.lds_xu) : P.lds_route;
+  const int64_t shared = T16 ? t16_wgs(a.gS16) : SBITS ? role_blocks(a.gSGU) : 0;
+  const int64_t grid = a.B * a.nrw + (a.xuall ? 2 * a.C * a.B * a.su : 0) + shared;
+  size_t lds = a.xuall ? std::max(P.lds_route, P.lds_xu) : P.lds_route;
+  if (T16) lds = std::max(lds, (size_t)t16_lds_bytes(true));
   static size_t attr = 64 * 1024;
-  int rc = set_lds_limit(moe_lane_route_kernel<SBITS, SLRP, RC>, lds, attr);
+  int rc = set_lds_limit(moe_lane_route_kernel<SBITS, SLRP, RC, T16>, lds, attr);
   if (rc) return rc;
-  moe_lane_route_kernel<SBITS, SLRP, RC><<<dim3((unsigned)grid), dim3(kMoeLaneThreads), lds,
-                                           s>>>(a);
+  moe_lane_route_kernel<SBITS, SLRP, RC, T16><<<dim3((unsigned)grid), dim3(kMoeLaneThreads), lds,
+                                                s>>>(a);
   GLQ_LAUNCH_CHECK("moe_lane_route_kernel");
   return GLQ_OK;
+}
+template <int SBITS, int SLRP, int RC>
+static int launch_route(const MoeLanePlan& P, hipStream_t s) {
+  if constexpr (SBITS == 4)
+    if (P.a.t16s) return launch_route_t<SBITS, SLRP, RC, true>(P, s);
+  return launch_route_t<SBITS, SLRP, RC, false>(P, s);
 }
 
 template <int SBITS, int SLRP>
@@ -721,6 +863,16 @@ static int launch_down(const MoeLanePlan& P, hipStream_t s) {
   moe_lane_down_kernel<BITS, LRP, NP><<<dim3((unsigned)grid), dim3(kMoeLaneThreads), P.lds_xu,
                                         s>>>(P.a);
   GLQ_LAUNCH_CHECK("moe_lane_down_kernel");
+  return GLQ_OK;
+}
+
+static int launch_sdown_t16(const MoeLanePlan& P, hipStream_t s) {
+  static size_t attr = 64 * 1024;
+  int rc = set_lds_limit(moe_lane_sdown_t16_kernel, P.lds_sd16, attr);
+  if (rc) return rc;
+  moe_lane_sdown_t16_kernel<<<dim3((unsigned)t16_wgs(P.a.gSD16)), dim3(kMoeLaneThreads), P.lds_sd16,
+                              s>>>(P.a);
+  GLQ_LAUNCH_CHECK("moe_lane_sdown_t16_kernel");
   return GLQ_OK;
 }
 
@@ -768,6 +920,7 @@ static int dispatch_shared(const MoeLanePlan& P, hipStream_t s, bool route) {
     if (lrp == 32) return launch_route_rc<SBITS, 32>(P, s);
     return launch_route_rc<SBITS, 16>(P, s);
   }
+  if (SBITS == 4 && P.a.t16d) return launch_sdown_t16(P, s);
   const int lr = P.a.gSD.lr, lrp = lane_lrp(lr), np = (lr + 63) / 64;
   if (lrp == 64) {
     if (np == 1) return launch_sdown<SBITS, 64, 1>(P, s);
@@ -845,6 +998,10 @@ int moe_lane_decode(const glq_moe_params* p, void* workspace, int64_t workspace_
   a.yb = (float*)(w + P.off_yb);
   a.ad = (float*)(w + P.off_ad);
   a.sinter = (__half*)(w + P.off_sinter);
+  a.gS16.part = a.gSD16.part = (float*)(w + P.off_t16p);
+  a.gS16.cnt = (unsigned*)(w + 1024);
+  a.gSD16.cnt = (unsigned*)(w + 1024 + 4 * kMoeT16MaxRB);
+  a.rtd = (float*)(w + P.off_rtd);
   return moe_lane_launch(P, s);
 }
 

@@ -1,0 +1,226 @@
+// Token-tile GEMV for a few token rows against the same weight rows (the
+// shared expert of a MoE step at 8..16 tokens): 4-bit group-128 codes,
+//
+//   y[t][n] = sum_g s[n,g] * sum_{k in g} fp16(q[n,k] - z[n,g]) x[t][k]
+//
+// One v_mfma_f32_16x16x32_f16 per 32 codes of a 16-row tile takes all 16
+// token rows at once (A = x, tokens as rows; B = the decoded codes, weight rows
+// as columns), so each code is decoded once for every token; the lane form
+// (glq_lane.h) decodes it once per token.
+//
+//  * Workgroup (rb, s) takes rows [64 rb, 64 rb + 64) (four tiles) over K
+//    slice s: groups [8 s, 8 s + 8), one group a wave.  A wave holds the x of
+//    every token over its group (16 VGPRs) and the codes of its group in all
+//    four tiles; per workgroup that is M x 1024 x 2 bytes of x against
+//    64 x 512 bytes of codes, so x (read from L2 by every row block) costs no
+//    more than the codes.
+//  * Lane (li, kb) = (row li of a tile, 32-code quarter kb of the group)
+//    loads 16 bytes of codes per tile; the four 8-code dwords are the four
+//    MFMA steps (both operands take the same k order, so the sums are the
+//    group's).  Decode: one v_and_or per two codes gives the exact fp16
+//    q - round(z) (the prefill GEMM's decode), and a packed fp16 subtract of
+//    the fractional part gives fp16(q - z), the reference's fp16 dequant
+//    rounding point; the group's fp32 sum is scaled once.
+//  * The waves' partial blocks meet in LDS and are summed in wave order.  With
+//    several K slices each workgroup writes its block to the workspace and
+//    counts itself in on the row block's counter; the last one sums the slices
+//    in slice order and stores.  Both orders are fixed: the same bits on every
+//    run.  The blocks go out as agent-scope atomic stores and come back as
+//    agent-scope atomic loads (L2-coherent across the XCDs), and the counter
+//    is bumped once they are complete (s_waitcnt vmcnt(0)), so the arrival
+//    needs no device-scope fence: on gfx950 __threadfence() writes back and
+//    invalidates the whole L2, which cost more than the GEMV itself here.
+//  * PAIR adds a second matrix of the same shape taken in the same pass (gate
+//    and up), stored together.
+#pragma once
+
+#include "glq_gemv_core.h"
+
+namespace glq {
+
+constexpr int kT16Waves = 8;              // waves (K groups) a workgroup
+constexpr int kT16Tiles = 4;              // 16-row tiles a row block
+constexpr int kT16Rows = 16 * kT16Tiles;  // rows a row block
+constexpr int kT16Elems = kT16Rows * 16;  // outputs (rows x token rows) a block and matrix
+
+// LDS bytes: every wave's partial block of each matrix.
+__host__ __device__ constexpr int t16_lds_bytes(bool pair) {
+  return (pair ? 2 : 1) * kT16Waves * kT16Elems * 4;
+}
+
+// The 4 B operands (8 fp16 each, decode order) of one group's 16 bytes of
+// 4-bit codes: fp16(q - z).  zi = round(z), zf = z - zi (exact in fp16).
+__device__ __forceinline__ void t16_decode4(const u32x4& w, float z, const DecodeConsts& dk,
+                                            f16x8 (&b)[4]) {
+  const float zi = rintf(z);
+  const _Float16 zf = (_Float16)(z - zi);
+  const _Float16 c0 = (_Float16)(-(1024.f + zi)), c1 = (_Float16)(-(64.f + zi));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 k0 = {c0, c0}, k1 = {c1, c1}, kf = {zf, zf};
+  auto sub = [&](uint32_t v, h2 c) -> uint32_t {
+    return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, v) + c) - kf);
+  };
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const uint32_t wd = w[s], v = wd >> 8;
+    u32x4 o;
+    o.x = sub((wd & 0x000F000Fu) | dk.e25, k0);  // codes 0, 4
+    o.y = sub((wd & 0x00F000F0u) | dk.e21, k1);  // codes 1, 5
+    o.z = sub((v & 0x000F000Fu) | dk.e25, k0);   // codes 2, 6
+    o.w = sub((v & 0x00F000F0u) | dk.e21, k1);   // codes 3, 7
+    b[s] = __builtin_bit_cast(f16x8, o);
+  }
+}
+
+// Geometry of one token-tile role: N rows of K codes (G groups of 128), M <=
+// 16 token rows; RB row blocks of 64 rows, ks K slices of 8 groups; workgroup
+// wg = rb ks + s.  With ks > 1, part holds [RB][ks][matrices][kT16Elems]
+// partial blocks and cnt[RB] the arrival counters (zero between launches; the
+// last workgroup of a row block leaves its counter at zero).
+struct T16Geom {
+  int N, K, G, kw;  // kw: int32 words per code row
+  int M;
+  int RB, ks;
+  float* part;
+  unsigned* cnt;
+};
+
+// Stores and loads of data handed between the workgroups of a launch.
+__device__ __forceinline__ void t16_put(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float t16_get(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Output element e of a block: tile j = e / 256, D index i, lane l -> token
+// row 4 (l / 16) + i, weight row 64 rb + 16 j + l % 16.
+__device__ __forceinline__ void t16_elem(int e, int rb, int& n, int& t) {
+  const int l = e & 63;
+  t = 4 * (l >> 4) + ((e >> 6) & 3);
+  n = kT16Rows * rb + 16 * (e >> 8) + (l & 15);
+}
+
+// Src::bind() gives a view with codes(m), scales(m), zeros(m) (m = 0, or 0
+// and 1 with PAIR), xrow(t) (token t's activation row, t < M), prep(rb, s,
+// ks) (called by every thread of every slice workgroup before its block is
+// published; may hold barriers; what it writes for the finishing workgroup
+// must go out through t16_put) and store(n, t, y) / PAIR store(n, t, y0, y1),
+// called for every output of the row block by the workgroup that finishes it
+// (reading prep's data through t16_get).  All 512 threads of the workgroup
+// call t16_run (barriers inside).
+template <class Src, bool PAIR>
+__device__ void t16_run(const Src& srcs, const T16Geom& tg, int wg, float* lds) {
+  constexpr int M2 = PAIR ? 2 : 1;
+  const int rb = wg / tg.ks, sl = wg - rb * tg.ks;
+  if (rb >= tg.RB) return;  // uniform over the workgroup
+  const auto src = srcs.bind();
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, kb = lane >> 4;
+  const int gw = sl * kT16Waves + wave;  // this wave's group
+  const bool gon = gw < tg.G;            // past G: x = 0, codes of group G - 1 (adds 0)
+  const int g = gon ? gw : tg.G - 1;
+
+  // ---- loads: the codes of the four tiles, then x; all in flight at once ----
+  u32x4 cw[M2][kT16Tiles];
+  __half sv[M2][kT16Tiles], zv[M2][kT16Tiles];
+#pragma unroll
+  for (int m = 0; m < M2; ++m)
+#pragma unroll
+    for (int j = 0; j < kT16Tiles; ++j) {
+      const int row = min(kT16Rows * rb + 16 * j + li, tg.N - 1);
+      cw[m][j] = *(const u32x4*)((const uint32_t*)src.codes(m) + (int64_t)row * tg.kw + 16 * g +
+                                 4 * kb);
+      sv[m][j] = src.scales(m)[(int64_t)row * tg.G + g];
+      zv[m][j] = src.zeros(m)[(int64_t)row * tg.G + g];
+    }
+  const bool xon = gon && li < tg.M;
+  const __half* xr = src.xrow(li < tg.M ? li : 0) + (int64_t)128 * g + 32 * kb;
+  f16x8 xv[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) xv[s] = *(const f16x8*)(xr + 8 * s);
+  __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the decode
+
+  f16x8 xa[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    // codes of a dword come decoded as 0,4,1,5,2,6,3,7
+    const f16x8 sh = __builtin_shufflevector(xv[s], xv[s], 0, 4, 1, 5, 2, 6, 3, 7);
+    xa[s] = xon ? sh : f16x8{};
+  }
+  const DecodeConsts dk = DecodeConsts::make();
+#pragma unroll
+  for (int m = 0; m < M2; ++m)
+#pragma unroll
+    for (int j = 0; j < kT16Tiles; ++j) {
+      f16x8 b[4];
+      t16_decode4(cw[m][j], __half2float(zv[m][j]), dk, b);
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) acc = mfma_16x16x32(xa[s], b[s], acc);
+      const float sc = __half2float(sv[m][j]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        lds[((m * kT16Waves + wave) * kT16Tiles + j) * 256 + i * 64 + lane] = sc * acc[i];
+    }
+  __syncthreads();
+
+  // ---- the block: waves summed in order; thread tid takes elements tid + 512 q ----
+  constexpr int EPT = kT16Elems / (kT16Waves * 64);
+  float v[M2][EPT];
+#pragma unroll
+  for (int m = 0; m < M2; ++m)
+#pragma unroll
+    for (int q = 0; q < EPT; ++q) {
+      const int e = tid + q * kT16Waves * 64;
+      float a = 0.f;
+#pragma unroll
+      for (int w = 0; w < kT16Waves; ++w) a += lds[(m * kT16Waves + w) * kT16Elems + e];
+      v[m][q] = a;
+    }
+
+  if (tg.ks > 1) {
+    float* pb = tg.part + (int64_t)(rb * tg.ks + sl) * M2 * kT16Elems;
+#pragma unroll
+    for (int m = 0; m < M2; ++m)
+#pragma unroll
+      for (int q = 0; q < EPT; ++q) t16_put(pb + m * kT16Elems + tid + q * kT16Waves * 64, v[m][q]);
+    src.prep(rb, sl, tg.ks);
+    // arrival: every coherent store complete, then counted
+    __shared__ int last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0)
+      last = __hip_atomic_fetch_add(tg.cnt + rb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (unsigned)(tg.ks - 1);
+    __syncthreads();
+    if (!last) return;
+    const float* p0 = tg.part + (int64_t)rb * tg.ks * M2 * kT16Elems;
+#pragma unroll
+    for (int m = 0; m < M2; ++m)
+#pragma unroll
+      for (int q = 0; q < EPT; ++q) {
+        const int e = m * kT16Elems + tid + q * kT16Waves * 64;
+        float a = 0.f;
+        for (int s = 0; s < tg.ks; ++s) a += t16_get(p0 + (int64_t)s * M2 * kT16Elems + e);
+        v[m][q] = a;
+      }
+    if (tid == 0) __hip_atomic_store(tg.cnt + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    src.prep(rb, 0, 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+#pragma unroll
+  for (int q = 0; q < EPT; ++q) {
+    int n, t;
+    t16_elem(tid + q * kT16Waves * 64, rb, n, t);
+    if (n < tg.N && t < tg.M) {
+      if constexpr (PAIR) src.store(n, t, v[0][q], v[1][q]);
+      else src.store(n, t, v[0][q]);
+    }
+  }
+}
+
+}  // namespace glq

@@ -299,8 +299,9 @@ int64_t glq_moe_workspace_bytes(const glq_moe_params* p);
 /*
  * Four launches on `stream` (five when the x*U jobs are gated on routing).
  * The workspace (256-byte aligned) must be zero-filled before its first use:
- * its first word counts the router workgroups of a step, and every step
- * leaves it zero again.  Steps that share a workspace must not overlap.
+ * its first 4096 bytes hold arrival counters (router workgroups, token-tile
+ * row blocks), and every step leaves them zero again.  Steps that share a
+ * workspace must not overlap.
  */
 int glq_moe_decode(const glq_moe_params* p, void* workspace, int64_t workspace_bytes,
                    void* stream);
