@@ -8,6 +8,7 @@
 
 #include <hip/hip_fp16.h>
 
+#include "glq_handoff.h"
 #include "glq_internal.h"
 
 namespace glq {
@@ -301,29 +302,19 @@ __global__ __launch_bounds__(kDecThreads) void decode_attention_kernel(AttnArgs 
       o3 += w * (float)vb2[1];
     }
     if (l32 == 0) {
-      my[0] = m;
-      my[1] = l;
+      handoff_put(my, m);
+      handoff_put(my + 1, l);
     }
-    *(float4*)(my + 4 + 4 * l32) = float4{o0, o1, o2, o3};
+    handoff_put(my + 4 + 4 * l32, o0);
+    handoff_put(my + 5 + 4 * l32, o1);
+    handoff_put(my + 6 + 4 * l32, o2);
+    handoff_put(my + 7 + 4 * l32, o3);
   }
-  // arrival; the last block of (b, g) merges the splits.  Every wave waits
-  // for its own partial stores to complete (they sit in this XCD's L2), then
-  // one thread releases them at device scope (one L2 write-back per block,
-  // not one per wave) and counts the block in; the last block's thread
-  // acquires (invalidating this CU's caches) before any thread reads.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    const bool last = atomicAdd(a.count + b * a.Hk + g, 1u) == (unsigned)(a.nsplit - 1);
-    if (last) __threadfence();
-    *flag = last;
-  }
-  __syncthreads();
-  if (!*flag) return;
+  // arrival (glq_handoff.h); the last block of (b, g) merges the splits
+  if (!handoff_arrive(a.count + b * a.Hk + g, (unsigned)a.nsplit, flag)) return;
   if (h < rep) {
-    // the acquire above made the other blocks' partials visible: plain
-    // loads, up to 8 splits' worth in flight at once,
+    // the other blocks' partials through coherent loads, up to 8 splits'
+    // worth in flight at once,
     // merged online (running max M, sums rescaled when M grows)
     const float* ph = a.part + ((int64_t)b * a.Hq + g * rep + h) * a.nsplit * kPartStride;
     float M = -__builtin_inff(), den = 0.f, r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
@@ -333,9 +324,11 @@ __global__ __launch_bounds__(kDecThreads) void decode_attention_kernel(AttnArgs 
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int s2 = min(s0 + j, a.nsplit - 1);
-        ms[j] = ph[s2 * kPartStride];
-        ls[j] = ph[s2 * kPartStride + 1];
-        os[j] = *(const float4*)(ph + s2 * kPartStride + 4 + 4 * l32);
+        const float* pp = ph + s2 * kPartStride;
+        ms[j] = handoff_get(pp);
+        ls[j] = handoff_get(pp + 1);
+        os[j] = float4{handoff_get(pp + 4 + 4 * l32), handoff_get(pp + 5 + 4 * l32),
+                       handoff_get(pp + 6 + 4 * l32), handoff_get(pp + 7 + 4 * l32)};
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -358,7 +351,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_attention_kernel(AttnArgs 
         uint2{__builtin_bit_cast(uint32_t, oa), __builtin_bit_cast(uint32_t, ob)};
   }
   if (tid == 0) {
-    a.count[b * a.Hk + g] = 0u;
+    handoff_reset(a.count + b * a.Hk + g);
     if (a.advance && b == 0 && g == 0) *a.advance += 1;
   }
 }

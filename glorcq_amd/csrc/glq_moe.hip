@@ -36,6 +36,7 @@
 #include <algorithm>
 #include <cstring>
 
+#include "glq_handoff.h"
 #include "glq_moe_route.h"
 #include "glq_stream.h"
 
@@ -319,7 +320,7 @@ __device__ void moe_route_tile(const MoeArgs& a, int id, unsigned char* smem) {
     const float sum = red[tid] + red[256 + tid] + red[512 + tid] + red[768 + tid];
     const __half lgh = __float2half(sum);
     if (m < nt && r < a.E) {
-      a.lgb[(int64_t)(t0 + m) * a.E + r] = lgh;
+      handoff_put((uint16_t*)a.lgb + (int64_t)(t0 + m) * a.E + r, __half_as_ushort(lgh));
       if (a.logits) a.logits[(int64_t)(t0 + m) * a.E + r] = lgh;
     }
     if (m < nt && r == a.E && a.sgw)
@@ -438,9 +439,10 @@ __device__ void moe_route_finalize(const MoeArgs& a, unsigned char* smem) {
   uint32_t* lgk = (uint32_t*)smem;
   const MoeTables t =
       moe_tables((int*)(smem + align_up_dev(4 * a.B * LS, 16)), P, a.E, a.nbm);
-  for (int i = tid; i < nl / 8; i += kRouteThreads) {  // 16-byte loads of the flat [B][E] array
-    const uint4 v = ((const uint4*)a.lgb)[i];
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  for (int i = tid; i < nl / 8; i += kRouteThreads) {  // 16 bytes of the flat [B][E] array
+    const uint32_t* lw = (const uint32_t*)a.lgb + 4 * i;
+    const uint32_t w[4] = {handoff_get(lw), handoff_get(lw + 1), handoff_get(lw + 2),
+                           handoff_get(lw + 3)};
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int f = 8 * i + u, tk = f / a.E, e = f - tk * a.E;
@@ -449,7 +451,7 @@ __device__ void moe_route_finalize(const MoeArgs& a, unsigned char* smem) {
   }
   for (int f = nl / 8 * 8 + tid; f < nl; f += kRouteThreads) {
     const int tk = f / a.E, e = f - tk * a.E;
-    lgk[tk * LS + e] = moe_key(__half_as_ushort(a.lgb[f]), e);
+    lgk[tk * LS + e] = moe_key(handoff_get((const uint16_t*)a.lgb + f), e);
   }
   __syncthreads();
   moe_topk_ranks(a, lgk, t.sel, true);
@@ -563,22 +565,11 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(MoeArgs a) {
   }
   if ((int)blockIdx.x < a.nrb) {
     moe_route_tile(a, blockIdx.x, smem);
-    // arrival: every wave waits for its logit stores to complete, one
-    // thread releases them at device scope and counts the workgroup in; the
-    // last router workgroup (its thread acquiring first) builds the step's
+    // arrival (glq_handoff.h): the last router workgroup builds the step's
     // routing and tables and leaves the counter at zero for the next step
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      __threadfence();
-      const bool l = atomicAdd(a.rcount, 1u) == (unsigned)(a.nrb - 1);
-      if (l) __threadfence();
-      last = l;
-    }
-    __syncthreads();
-    if (last) {
+    if (handoff_arrive(a.rcount, (unsigned)a.nrb, &last)) {
       moe_route_finalize(a, smem);
-      if (threadIdx.x == 0) *a.rcount = 0u;
+      if (threadIdx.x == 0) handoff_reset(a.rcount);
     }
   } else if ((int)blockIdx.x < a.nrb + a.nxu1) {
     moe_xu_job(a, blockIdx.x - a.nrb, smem, false);

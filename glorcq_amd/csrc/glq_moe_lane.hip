@@ -37,6 +37,7 @@
 #include <cstdlib>
 #include <cstring>
 
+#include "glq_handoff.h"
 #include "glq_internal.h"
 #include "glq_lane.h"
 #include "glq_moe_route.h"
@@ -361,12 +362,12 @@ struct SdTileView {
       float acc = 0.f;
       for (int k = 0; k < K; ++k)
         acc = fmaf(__half2float(a.wts[t * K + k]), contrib[tr * K + k], acc);
-      if (n < a.H) t16_put(a.rtd + (int64_t)t * a.H + n, acc);
+      if (n < a.H) handoff_put(a.rtd + (int64_t)t * a.H + n, acc);
     }
   }
   // out = fp16(routed + gate * fp16(shared)) (+ residual)
   __device__ void store(int n, int t, float v) const {
-    float acc = t16_get(a.rtd + (int64_t)t * a.H + n);
+    float acc = handoff_get(a.rtd + (int64_t)t * a.H + n);
     acc = fmaf(__half2float(a.sg[t]), __half2float(__float2half(v)), acc);
     float o = __half2float(__float2half(acc));
     if (a.res) o += __half2float(a.res[(int64_t)t * a.H + n]);
@@ -427,27 +428,17 @@ __device__ void moe_lane_router(const MoeLaneArgs& a, int t, int q, unsigned cha
       if (lane == 0 && r0 + i < rend) {
         const __half lg = __float2half(sacc);
         lgh[r0 + i] = __half_as_ushort(lg);
-        if (a.nrw > 1) a.lgw[(int64_t)t * (a.E + 1) + r0 + i] = lg;
+        if (a.nrw > 1) handoff_put((uint16_t*)a.lgw + (int64_t)t * (a.E + 1) + r0 + i, __half_as_ushort(lg));
       }
     }
   }
   if (a.nrw > 1) {
-    // arrival (as the many-token router's): stores complete, released at
-    // device scope, counted; the last workgroup acquires every slice
+    // arrival (glq_handoff.h); the last workgroup reads every slice's logits
     __shared__ int last;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-      __threadfence();
-      const bool l = atomicAdd(a.rcnt + t, 1u) == (unsigned)(a.nrw - 1);
-      if (l) __threadfence();
-      last = l;
-    }
-    __syncthreads();
-    if (!last) return;
+    if (!handoff_arrive(a.rcnt + t, (unsigned)a.nrw, &last)) return;
     for (int r = tid; r < nrow; r += kMoeLaneThreads)
-      lgh[r] = __half_as_ushort(a.lgw[(int64_t)t * (a.E + 1) + r]);
-    if (tid == 0) a.rcnt[t] = 0u;
+      lgh[r] = handoff_get((const uint16_t*)a.lgw + (int64_t)t * (a.E + 1) + r);
+    if (tid == 0) handoff_reset(a.rcnt + t);
   }
   __syncthreads();
   for (int e = tid; e < a.E; e += kMoeLaneThreads) {

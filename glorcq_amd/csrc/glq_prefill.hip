@@ -46,6 +46,7 @@
 #include <algorithm>
 #include <cstdio>
 
+#include "glq_handoff.h"
 #include "glq_stream.h"
 
 namespace glq {
@@ -435,25 +436,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
       for (int rt = 0; rt < RT; ++rt) {
         const int c = cbase + rt * 16;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) mine[(int64_t)(16 * i + 4 * kb + j) * ncol + c] = y[i][rt][j];
+        for (int j = 0; j < 4; ++j)
+          handoff_put(mine + (int64_t)(16 * i + 4 * kb + j) * ncol + c, y[i][rt][j]);
       }
-    // every wave waits for its own stores; one thread releases them at device
-    // scope and counts the workgroup in; the last one acquires
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    // arrival (glq_handoff.h); the last split reduces and leaves the counter
+    // at zero for the next launch
     __shared__ int last;
-    if (tid == 0) {
-      __threadfence();
-      unsigned* c = g.cnt + (int64_t)ty * g.ntn + tn;
-      const bool l = atomicAdd(c, 1u) == (unsigned)(g.ks - 1);
-      if (l) {
-        __threadfence();
-        *c = 0;  // ready for the next launch
-      }
-      last = l;
-    }
-    __syncthreads();
-    if (!last) return;
+    unsigned* cnt = g.cnt + (int64_t)ty * g.ntn + tn;
+    if (!handoff_arrive(cnt, (unsigned)g.ks, &last)) return;
+    if (tid == 0) handoff_reset(cnt);
 #pragma unroll
     for (int i = 0; i < TT; ++i)
 #pragma unroll
@@ -466,7 +457,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
         for (int rt = 0; rt < RT; ++rt) {
           const int c = cbase + rt * 16;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) y[i][rt][j] += ps[(int64_t)(16 * i + 4 * kb + j) * ncol + c];
+          for (int j = 0; j < 4; ++j)
+            y[i][rt][j] += handoff_get(ps + (int64_t)(16 * i + 4 * kb + j) * ncol + c);
         }
     }
   }

@@ -25,16 +25,14 @@
 //    several K slices each workgroup writes its block to the workspace and
 //    counts itself in on the row block's counter; the last one sums the slices
 //    in slice order and stores.  Both orders are fixed: the same bits on every
-//    run.  The blocks go out as agent-scope atomic stores and come back as
-//    agent-scope atomic loads (L2-coherent across the XCDs), and the counter
-//    is bumped once they are complete (s_waitcnt vmcnt(0)), so the arrival
-//    needs no device-scope fence: on gfx950 __threadfence() writes back and
-//    invalidates the whole L2, which cost more than the GEMV itself here.
+//    run.  The blocks and the arrival go through glq_handoff.h (coherent
+//    atomic stores and loads, no device-scope fence).
 //  * PAIR adds a second matrix of the same shape taken in the same pass (gate
 //    and up), stored together.
 #pragma once
 
 #include "glq_gemv_core.h"
+#include "glq_handoff.h"
 
 namespace glq {
 
@@ -85,14 +83,6 @@ struct T16Geom {
   unsigned* cnt;
 };
 
-// Stores and loads of data handed between the workgroups of a launch.
-__device__ __forceinline__ void t16_put(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float t16_get(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Output element e of a block: tile j = e / 256, D index i, lane l -> token
 // row 4 (l / 16) + i, weight row 64 rb + 16 j + l % 16.
 __device__ __forceinline__ void t16_elem(int e, int rb, int& n, int& t) {
@@ -105,9 +95,9 @@ __device__ __forceinline__ void t16_elem(int e, int rb, int& n, int& t) {
 // and 1 with PAIR), xrow(t) (token t's activation row, t < M), prep(rb, s,
 // ks) (called by every thread of every slice workgroup before its block is
 // published; may hold barriers; what it writes for the finishing workgroup
-// must go out through t16_put) and store(n, t, y) / PAIR store(n, t, y0, y1),
-// called for every output of the row block by the workgroup that finishes it
-// (reading prep's data through t16_get).  All 512 threads of the workgroup
+// must go out through handoff_put) and store(n, t, y) / PAIR store(n, t, y0,
+// y1), called for every output of the row block by the workgroup that
+// finishes it (reading prep's data through handoff_get).  All 512 threads of the workgroup
 // call t16_run (barriers inside).
 template <class Src, bool PAIR>
 __device__ void t16_run(const Src& srcs, const T16Geom& tg, int wg, float* lds) {
@@ -185,17 +175,11 @@ __device__ void t16_run(const Src& srcs, const T16Geom& tg, int wg, float* lds) 
 #pragma unroll
     for (int m = 0; m < M2; ++m)
 #pragma unroll
-      for (int q = 0; q < EPT; ++q) t16_put(pb + m * kT16Elems + tid + q * kT16Waves * 64, v[m][q]);
+      for (int q = 0; q < EPT; ++q)
+        handoff_put(pb + m * kT16Elems + tid + q * kT16Waves * 64, v[m][q]);
     src.prep(rb, sl, tg.ks);
-    // arrival: every coherent store complete, then counted
     __shared__ int last;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0)
-      last = __hip_atomic_fetch_add(tg.cnt + rb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-             (unsigned)(tg.ks - 1);
-    __syncthreads();
-    if (!last) return;
+    if (!handoff_arrive(tg.cnt + rb, (unsigned)tg.ks, &last)) return;
     const float* p0 = tg.part + (int64_t)rb * tg.ks * M2 * kT16Elems;
 #pragma unroll
     for (int m = 0; m < M2; ++m)
@@ -203,10 +187,10 @@ __device__ void t16_run(const Src& srcs, const T16Geom& tg, int wg, float* lds) 
       for (int q = 0; q < EPT; ++q) {
         const int e = m * kT16Elems + tid + q * kT16Waves * 64;
         float a = 0.f;
-        for (int s = 0; s < tg.ks; ++s) a += t16_get(p0 + (int64_t)s * M2 * kT16Elems + e);
+        for (int s = 0; s < tg.ks; ++s) a += handoff_get(p0 + (int64_t)s * M2 * kT16Elems + e);
         v[m][q] = a;
       }
-    if (tid == 0) __hip_atomic_store(tg.cnt + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) handoff_reset(tg.cnt + rb);
   } else {
     src.prep(rb, 0, 1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
