@@ -77,6 +77,11 @@ SIGNATURES = {
         _vp, _i64,                      # xu, xu_stride
         _vp, _i64, _vp,                 # workspace, bytes, stream
     ]),
+    "glq_lowrank_xu_routed": (_c_int, [
+        _i64, _vp, _i64, _vp, _i64, _i64,  # picks, x, K, U, u_rows, rank
+        _vp, _i64, _vp, _vp,               # sel, experts, cluster_of, xu
+        _vp, _i64, _vp,                    # workspace, bytes, stream
+    ]),
     "glq_gemm_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "glq_gemm_lora": (_c_int, [
         _vp, _i64, _i64, _i64,          # x, M, K, N
@@ -100,6 +105,22 @@ SIGNATURES = {
     "glq_moe_decode": (_c_int, [ctypes.POINTER(MoeParams), _vp, _i64, _vp]),
     "glq_moe_prefill_workspace_bytes": (_i64, [ctypes.POINTER(MoeParams)]),
     "glq_moe_prefill": (_c_int, [ctypes.POINTER(MoeParams), _vp, _i64, _vp]),
+    "glq_moe_route_workspace_bytes": (_i64, [_i64, _i64]),
+    "glq_moe_route": (_c_int, [
+        _vp, _vp, _vp,                  # h, router_w, shared_gate_w
+        _i64, _i64, _i64, _i64, _c_int,  # tokens, hidden, experts, top_k, norm
+        _vp, _vp, _vp, _vp,             # sel, weights, shared_gate, logits
+        _vp, _i64, _vp,                 # workspace, bytes, stream
+    ]),
+    "glq_turbo_moe_gemv": (_c_int, [
+        _i64, _i64, _vp, _i64, _i64, _i64,  # picks, x_div, x_rot, K, N, experts
+        _vp, _vp, _vp, _vp,                 # sel, codes, norms, centroids
+        _vp, _vp, _i64, _i64,               # xU, xu_cluster, xu_tokens, xu_rows
+        _vp, _i64, _vp, _vp,                # SV, rank, bias, gate
+        _vp, _vp,                           # y, stream
+    ]),
+    "glq_moe_combine": (_c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "glq_swiglu": (_c_int, [_vp, _vp, _i64, _vp, _vp]),
     "glq_unpack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _c_int, _vp, _vp]),
     "glq_dequant_weight": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp, _i64, _c_int, _vp, _vp]),
     "glq_pack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp]),

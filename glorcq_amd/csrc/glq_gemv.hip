@@ -41,6 +41,10 @@ struct DenseArgs {
   const float* apart;  // launch-1 partials (items x P x M x rpad), or null
   int items, M, P, tiles;
   TileShape sh;
+  // routed picks (glq_lowrank_xu_routed): item i takes U row ucl[usel[i]]
+  const int32_t* usel;
+  const int32_t* ucl;
+  int nsel, nu;
 };
 
 // Item data of a dense launch: item i is at base + i * stride.
@@ -130,7 +134,12 @@ __global__ __launch_bounds__(256) void lowrank_partial_kernel(DenseArgs a) {
   const __half* X = a.x + (int64_t)item * a.x_es;
   const int K = a.sh.K;
   auto xrow = [&](int m) { return X + (int64_t)m * K; };
-  lowrank_partial<MC>(xrow, a.M, K, a.sh.rank, a.sh.rpad, a.u + (int64_t)item * a.u_es, p,
+  int64_t ui = item;
+  if (a.usel) {
+    const int e = min(max(a.usel[item], 0), a.nsel - 1);
+    ui = min(max(a.ucl[e], 0), a.nu - 1);
+  }
+  lowrank_partial<MC>(xrow, a.M, K, a.sh.rank, a.sh.rpad, a.u + ui * a.u_es, p,
                       (float*)a.apart + ((int64_t)item * a.P + p) * a.M * a.sh.rpad, red, xl,
                       (int)threadIdx.x);
 }
@@ -715,6 +724,49 @@ int glq_lowrank_xu_batched(int64_t items, const void* x, int64_t x_stride, int64
   const int64_t n = items * M * rank;
   lowrank_finalize_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(
       a.apart, a.items, a.P, a.M, (int)rank, a.sh.rpad, (__half*)xu, xu_stride);
+  GLQ_LAUNCH_CHECK("lowrank_finalize_kernel");
+  return GLQ_OK;
+}
+
+int glq_lowrank_xu_routed(int64_t picks, const void* x, int64_t K, const void* U, int64_t u_rows,
+                          int64_t rank, const int32_t* sel, int64_t experts,
+                          const int32_t* cluster_of, void* xu, void* workspace,
+                          int64_t workspace_bytes_given, void* stream) {
+  clear_error();
+  GLQ_CHECK(picks >= 0 && K >= 0 && rank >= 0 && u_rows >= 1 && experts >= 1, "bad size");
+  if (picks == 0 || rank == 0) return GLQ_OK;
+  GLQ_CHECK(K > 0 && K < (1ll << 24), "bad K=%lld", (long long)K);
+  GLQ_CHECK(rank % 8 == 0 && rank <= 512, "rank=%lld must be a multiple of 8, <= 512",
+            (long long)rank);
+  GLQ_CHECK(x && U && xu && sel && cluster_of, "null pointer");
+  GLQ_CHECK(((uintptr_t)U & 15) == 0, "U must be 16-byte aligned");
+  const int64_t need = workspace_need(picks, 1, K, rank);
+  GLQ_CHECK(workspace != nullptr && workspace_bytes_given >= need,
+            "workspace of %lld bytes needed (got %lld)", (long long)need,
+            (long long)workspace_bytes_given);
+  DenseArgs a = {};
+  a.u = (const __half*)U;
+  a.u_es = K * rank;
+  a.x = (const __half*)x;
+  a.x_es = K;
+  a.apart = (const float*)workspace;
+  a.items = (int)picks;
+  a.M = 1;
+  a.P = (int)lowrank_slices(K);
+  a.sh.K = (int)K;
+  a.sh.rank = (int)rank;
+  a.sh.rpad = (int)align_up(rank, 32);
+  a.usel = sel;
+  a.ucl = cluster_of;
+  a.nsel = (int)std::min<int64_t>(experts, 1 << 30);
+  a.nu = (int)std::min<int64_t>(u_rows, 1 << 30);
+  GLQ_CHECK(picks * a.P < (1ll << 31), "too many workgroups");
+  hipStream_t s = (hipStream_t)stream;
+  lowrank_partial_kernel<1><<<dim3((unsigned)(picks * a.P)), dim3(256), 0, s>>>(a);
+  GLQ_LAUNCH_CHECK("lowrank_partial_kernel");
+  const int64_t n = picks * rank;
+  lowrank_finalize_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(
+      a.apart, a.items, a.P, 1, (int)rank, a.sh.rpad, (__half*)xu, rank);
   GLQ_LAUNCH_CHECK("lowrank_finalize_kernel");
   return GLQ_OK;
 }

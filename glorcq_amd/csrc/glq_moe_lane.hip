@@ -980,9 +980,9 @@ int moe_lane_decode(const glq_moe_params* p, void* workspace, int64_t workspace_
   a.wts = (__half*)(w + P.off_wts);
   a.sg = (__half*)(w + P.off_sg);
   a.lgw = (__half*)(w + P.off_lgw);
-  // the per-token router counters sit in bytes 64 .. 127, which the
-  // many-token path leaves unused (its counter is word 0; its tables start at
-  // 256): both zero before the first step and after every step
+  // the per-token router counters sit in bytes 64 .. 127 of the header, which
+  // the many-token path leaves unused (its counter is word 0): both zero
+  // before the first step and after every step
   a.rcnt = (unsigned*)(w + 64);
   a.agu = (float*)(w + P.off_agu);
   a.inter = (__half*)(w + P.off_inter);
@@ -996,4 +996,136 @@ int moe_lane_decode(const glq_moe_params* p, void* workspace, int64_t workspace_
   return moe_lane_launch(P, s);
 }
 
+// ---------------------------------------------------------------------------
+// The pieces of a step whose routed experts are not GPTQ (TurboQuant experts,
+// glorcq_amd/moe_block.py): routing alone, the weighted combine, SwiGLU.
+// ---------------------------------------------------------------------------
+
+// Routing of B tokens: the lane router, nrw workgroups per token.
+template <int RC>
+__global__ __launch_bounds__(kMoeLaneThreads) void moe_route_only_kernel(MoeLaneArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  moe_lane_router<RC>(a, blockIdx.x / a.nrw, blockIdx.x % a.nrw, smem);
+}
+
+// out[t][n] = fp16(sum_k w[t][k] y[t k + k][n] + sg[t] shared[t][n])
+// (+ residual): the lane path's combine (fmaf over the picks in pick order,
+// then the gated shared term), one thread per output.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const __half* y, const __half* wts,
+                                                          const __half* shared, const __half* sg,
+                                                          const __half* res, __half* out, int B,
+                                                          int H, int topk) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)B * H) return;
+  const int t = (int)(i / H), n = (int)(i - (int64_t)t * H);
+  float acc = 0.f;
+  for (int k = 0; k < topk; ++k)
+    acc = fmaf(__half2float(wts[t * topk + k]),
+               __half2float(y[((int64_t)t * topk + k) * H + n]), acc);
+  if (shared) acc = fmaf(__half2float(sg[t]), __half2float(shared[i]), acc);
+  float o = __half2float(__float2half(acc));
+  if (res) o += __half2float(res[i]);
+  out[i] = __float2half(o);
+}
+
+// out = fp16(fp16(silu(g)) * u) elementwise (act_fn(gate) * up on fp16).
+__global__ __launch_bounds__(256) void swiglu_kernel(const __half* g, const __half* u, __half* out,
+                                                     int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = swiglu_fp16(__half2float(g[i]), __half2float(u[i]));
+}
+
+namespace {
+int moe_route_shape(int64_t B, int64_t H, int64_t E, int64_t k) {
+  GLQ_CHECK(B >= 1 && B <= 4096, "tokens=%lld must be in 1..4096", (long long)B);
+  GLQ_CHECK(E >= 1 && E <= 256, "experts=%lld must be in 1..256", (long long)E);
+  GLQ_CHECK(k >= 1 && k <= 16 && k <= E, "top_k=%lld out of range", (long long)k);
+  GLQ_CHECK(H >= 8 && H % 8 == 0 && H <= 4096, "hidden=%lld must be a multiple of 8, <= 4096",
+            (long long)H);
+  return GLQ_OK;
+}
+}  // namespace
+
 }  // namespace glq
+
+extern "C" int64_t glq_moe_route_workspace_bytes(int64_t tokens, int64_t experts) {
+  glq::clear_error();
+  if (tokens < 1 || experts < 1) return -1;
+  // per-token arrival counters (zero between calls), then the logits
+  return 4 * glq::align_up(tokens, 64) + 2 * tokens * (experts + 1);
+}
+
+extern "C" int glq_moe_route(const void* h, const void* router_w, const void* shared_gate_w,
+                             int64_t tokens, int64_t hidden, int64_t experts, int64_t top_k,
+                             int norm_topk_prob, int32_t* sel, void* weights, void* shared_gate,
+                             void* logits, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  using namespace glq;
+  clear_error();
+  if (int rc = moe_route_shape(tokens, hidden, experts, top_k)) return rc;
+  GLQ_CHECK(h && router_w && sel && weights && shared_gate, "null h, router_w or outputs");
+  GLQ_CHECK(((uintptr_t)h & 15) == 0 && ((uintptr_t)router_w & 15) == 0 &&
+                (!shared_gate_w || ((uintptr_t)shared_gate_w & 15) == 0),
+            "h, router_w and shared_gate_w must be 16-byte aligned");
+  const int64_t need = glq_moe_route_workspace_bytes(tokens, experts);
+  GLQ_CHECK(workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15) == 0,
+            "workspace of %lld bytes needed, 16-byte aligned", (long long)need);
+  MoeLaneArgs a;
+  memset(&a, 0, sizeof(a));
+  a.B = (int)tokens;
+  a.H = (int)hidden;
+  a.E = (int)experts;
+  a.topk = (int)top_k;
+  a.norm = norm_topk_prob ? 1 : 0;
+  a.h = (const __half*)h;
+  a.rw = (const __half*)router_w;
+  a.sgw = (const __half*)shared_gate_w;
+  a.sel = sel;
+  a.wts = (__half*)weights;
+  a.sg = (__half*)shared_gate;
+  a.logits = (__half*)logits;
+  a.rcnt = (unsigned*)workspace;
+  a.lgw = (__half*)((char*)workspace + 4 * align_up(tokens, 64));
+  const int rc = hidden <= 512 ? 1 : hidden <= 1024 ? 2 : hidden <= 2048 ? 4 : 8;
+  const int rb = rc >= 8 ? 2 : 16 / rc, nrow = (int)experts + (shared_gate_w ? 1 : 0);
+  a.nrw = (nrow + 8 * rb - 1) / (8 * rb);
+  const size_t lds = (size_t)(((2 * (experts + 1) + 15) & ~15) + 4 * experts + 4 * 16);
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)(tokens * a.nrw)), block(kMoeLaneThreads);
+  if (rc == 1) moe_route_only_kernel<1><<<grid, block, lds, s>>>(a);
+  else if (rc == 2) moe_route_only_kernel<2><<<grid, block, lds, s>>>(a);
+  else if (rc == 4) moe_route_only_kernel<4><<<grid, block, lds, s>>>(a);
+  else moe_route_only_kernel<8><<<grid, block, lds, s>>>(a);
+  GLQ_LAUNCH_CHECK("moe_route_only_kernel");
+  return GLQ_OK;
+}
+
+extern "C" int glq_moe_combine(const void* y, const void* weights, const void* shared,
+                               const void* shared_gate, const void* residual, int64_t tokens,
+                               int64_t hidden, int64_t top_k, void* out, void* stream) {
+  using namespace glq;
+  clear_error();
+  GLQ_CHECK(tokens >= 0 && hidden >= 1 && top_k >= 1 && top_k <= 16, "bad sizes");
+  GLQ_CHECK(tokens * hidden < (1ll << 31), "tokens * hidden must be < 2^31");
+  if (tokens == 0) return GLQ_OK;
+  GLQ_CHECK(y && weights && out && (!shared || shared_gate), "null y, weights, out or gate");
+  const int64_t n = tokens * hidden;
+  moe_combine_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream>>>(
+      (const __half*)y, (const __half*)weights, (const __half*)shared,
+      (const __half*)shared_gate, (const __half*)residual, (__half*)out, (int)tokens,
+      (int)hidden, (int)top_k);
+  GLQ_LAUNCH_CHECK("moe_combine_kernel");
+  return GLQ_OK;
+}
+
+extern "C" int glq_swiglu(const void* gate, const void* up, int64_t n, void* out, void* stream) {
+  using namespace glq;
+  clear_error();
+  GLQ_CHECK(n >= 0 && n < (1ll << 40), "bad size");
+  if (n == 0) return GLQ_OK;
+  GLQ_CHECK(gate && up && out, "null pointer");
+  swiglu_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream>>>(
+      (const __half*)gate, (const __half*)up, (__half*)out, n);
+  GLQ_LAUNCH_CHECK("swiglu_kernel");
+  return GLQ_OK;
+}

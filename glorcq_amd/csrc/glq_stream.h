@@ -343,15 +343,6 @@ __device__ __forceinline__ void stream_post(const unsigned char* slot, int q, in
   }
 }
 
-// inter = fp16(fp16(silu(fp16(g))) * fp16(u)): the rounding points of
-// act_fn(gate(x)) * up(x) on fp16 tensors; the product of two fp16 values is
-// exact in fp32, so one rounding gives the correctly rounded fp16 product.
-__device__ __forceinline__ __half swiglu_fp16(float g, float u) {
-  const float gf = __half2float(__float2half(g));
-  const float sl = __half2float(__float2half(gf / (1.f + expf(-gf))));
-  return __float2half(sl * __half2float(__float2half(u)));
-}
-
 // Stages, for one work unit, the x rows (zero-padded, permuted into MFMA
 // operand order), their per-128-code sums c1 = sum(operand bias * x) and
 // c2 = sum(x), the zero block, and the low-rank inputs a of the matrices with

@@ -59,7 +59,28 @@ struct TurboArgs {
   int xstride;             // halves per staged token row (segment + 8)
   int wpt;                 // waves per 16-row tile: 1, 2 or 4 (K split among them)
   int rwgs, twgs;          // row groups (4/wpt tiles) and token blocks (16 tokens) per item
+  // routed picks of a MoE step (glq_turbo_moe_gemv); the plain batched call
+  // leaves wsel, xclus and gate null and x_div 1
+  const int32_t* wsel;     // weight set (codes, norms, SV, bias) of item i: wsel[i] (< nw)
+  int nw;
+  int x_div;               // x row of item i: i / x_div
+  const int32_t* xclus;    // a row of item i: xclus[wsel[i]] * xu_tok + i / x_div (< xu_rows)
+  int xu_tok, xu_rows;
+  const __half* gate;      // (items, M, N): y = fp16(fp16(silu(gate)) * y)
 };
+
+// Weight set, x row and low-rank row of an item.
+__device__ __forceinline__ int turbo_w(const TurboArgs& a, int item) {
+  return a.wsel ? min(max(a.wsel[item], 0), a.nw - 1) : item;
+}
+__device__ __forceinline__ int64_t turbo_xrow(const TurboArgs& a, int item) {
+  return item / a.x_div;
+}
+__device__ __forceinline__ int64_t turbo_arow(const TurboArgs& a, int item) {
+  if (!a.xclus) return item;
+  const int64_t r = (int64_t)a.xclus[turbo_w(a, item)] * a.xu_tok + item / a.x_div;
+  return min(max(r, (int64_t)0), (int64_t)a.xu_rows - 1);
+}
 
 // fp16 codebook in v_perm_b32 form: lb = low bytes of C0..C3, hb = high bytes.
 struct TurboLut {
@@ -107,13 +128,13 @@ __device__ __forceinline__ void turbo_decode(uint32_t w, const TurboLut& H, cons
 __device__ __forceinline__ void turbo_epilogue(const TurboArgs& a, f32x4 acc, int item, int m0,
                                                int mr, int r0, const __half* a_l, int li,
                                                int kb) {
-  const int r = r0 + li, row = min(r, a.N - 1);
-  const float nr = a.norms[(int64_t)item * a.n_es + row];
+  const int r = r0 + li, row = min(r, a.N - 1), w = turbo_w(a, item);
+  const float nr = a.norms[(int64_t)w * a.n_es + row];
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i] *= nr;
   if (a.sv) {
     // A = a (token rows), B = SV rows: D[token 4kb + i][row li], acc's layout
-    const __half* svr = a.sv + (int64_t)item * a.sv_es + (int64_t)row * a.rank;
+    const __half* svr = a.sv + (int64_t)w * a.sv_es + (int64_t)row * a.rank;
     const __half* ar = a_l + min(li, mr - 1) * a.apad;
     for (int s0 = 0; s0 < a.rpad; s0 += 32) {
       const int j = s0 + 8 * kb;
@@ -122,13 +143,16 @@ __device__ __forceinline__ void turbo_epilogue(const TurboArgs& a, f32x4 acc, in
       acc = mfma_16x16x32(av, bv, acc);
     }
   }
-  const float bb = a.bias ? __half2float(a.bias[(int64_t)item * a.bias_es + row]) : 0.f;
+  const float bb = a.bias ? __half2float(a.bias[(int64_t)w * a.bias_es + row]) : 0.f;
   if (r < a.N) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = 4 * kb + i;
-      if (m < mr)
-        a.y[(int64_t)item * a.y_es + (int64_t)(m0 + m) * a.N + r] = __float2half(acc[i] + bb);
+      if (m < mr) {
+        const int64_t o = (int64_t)item * a.y_es + (int64_t)(m0 + m) * a.N + r;
+        a.y[o] = a.gate ? swiglu_fp16(__half2float(a.gate[o]), acc[i] + bb)
+                        : __float2half(acc[i] + bb);
+      }
     }
   }
 }
@@ -142,9 +166,9 @@ __device__ __forceinline__ void turbo_stage(const TurboArgs& a, const __half* X,
   if (with_a && a.sv) {
     for (int idx = tid; idx < mr * a.rpad; idx += 256) {
       const int m = idx / a.rpad, j = idx - m * a.rpad;
-      a_l[m * a.apad + j] = j < a.rank
-                                ? a.xu[(int64_t)item * a.xu_es + (int64_t)(m0 + m) * a.rank + j]
-                                : __float2half(0.f);
+      a_l[m * a.apad + j] = j < a.rank ? a.xu[turbo_arow(a, item) * a.xu_es +
+                                              (int64_t)(m0 + m) * a.rank + j]
+                                       : __float2half(0.f);
     }
   }
   const int nblk = (se - sb) * 16;  // 16-code blocks
@@ -199,8 +223,8 @@ __global__ __launch_bounds__(256) void turbo_stream_kernel(TurboArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), li = lane & 15, kb = lane >> 4;
   const int m0 = 16 * tb, mr = min(16, a.M - m0);
-  const __half* X = a.x + (int64_t)item * a.x_es + (int64_t)m0 * a.K;
-  const uint32_t* C = a.codes + (int64_t)item * a.c_es;
+  const __half* X = a.x + turbo_xrow(a, item) * a.x_es + (int64_t)m0 * a.K;
+  const uint32_t* C = a.codes + (int64_t)turbo_w(a, item) * a.c_es;
   const int T = (a.N + 15) >> 4, stride = 4 * a.rwgs, gw = wl * 4 + wave;
   const int ntw = gw < T ? (T - gw + stride - 1) / stride : 0;  // tiles of this wave
   const int nsteps = (a.K + 255) >> 8, cyc = (nsteps + PF - 1) / PF;
@@ -246,11 +270,12 @@ __global__ __launch_bounds__(256) void turbo_gemv_kernel(TurboArgs a) {
   const int wpt = a.wpt, tpw = 4 / wpt;            // waves per tile, tiles per workgroup
   const int part = wave % wpt, r0 = (rg * tpw + wave / wpt) * 16;
   const int m0 = 16 * tb, mr = min(16, a.M - m0);  // token rows of this block
-  const __half* X = a.x + (int64_t)item * a.x_es + (int64_t)m0 * a.K;
+  const __half* X = a.x + turbo_xrow(a, item) * a.x_es + (int64_t)m0 * a.K;
 
   const TurboLut H = turbo_lut(a.cent, false), L = turbo_lut(a.cent, true);
   const int row = min(r0 + li, a.N - 1);
-  const uint32_t* crow = a.codes + (int64_t)item * a.c_es + (int64_t)row * a.kw;
+  const uint32_t* crow =
+      a.codes + (int64_t)turbo_w(a, item) * a.c_es + (int64_t)row * a.kw;
   const int wlast = a.kw - 4;  // last whole 16-byte piece (kw is a multiple of 4)
   const __half* xr = xs + min(li, mr - 1) * a.xstride;
   const int nsteps = (a.K + 255) >> 8;
@@ -347,6 +372,54 @@ __global__ __launch_bounds__(256) void rht_kernel(const TI* __restrict__ x,
 
 }  // namespace glq
 
+namespace glq {
+namespace {
+// Picks the form and launches; a holds every pointer, size and item field.
+int turbo_run(TurboArgs& a, int64_t items, int64_t M, int64_t K, int64_t N, hipStream_t s) {
+  const int mr = (int)std::min<int64_t>(16, M);
+  const int nsteps = (int)((K + 255) / 256);
+  const int fit = (kTurboXBudget / (2 * mr) - 8) / 256;  // steps of a segment that fit
+  a.segsteps = std::max(1, std::min(nsteps, fit));
+  a.xstride = a.segsteps * 256 + 8;
+  a.twgs = (int)((M + 15) / 16);
+  const int64_t T = (N + 15) / 16, tiles = items * a.twgs * T;
+  const int64_t kpad = (int64_t)nsteps * 256;
+  const size_t stream_lds = (size_t)16 * a.apad * 2 + (size_t)mr * (kpad + 8) * 2;
+  if (tiles >= kTurboStreamTiles && stream_lds <= (size_t)kTurboStreamLds) {
+    // streaming form: the whole K staged once per workgroup, waves walk tiles
+    a.segsteps = nsteps;
+    a.xstride = (int)kpad + 8;
+    a.wpt = 1;
+    const int64_t blocks = items * a.twgs;
+    a.rwgs = (int)std::max<int64_t>(1, std::min<int64_t>((kTurboStreamWgs + blocks - 1) / blocks,
+                                                         (T + 3) / 4));
+    static size_t attr = 64 * 1024;
+    int rc = set_lds_limit(turbo_stream_kernel<kTurboPF>, stream_lds, attr);
+    if (rc) return rc;
+    const int64_t grid = blocks * a.rwgs;
+    GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
+    turbo_stream_kernel<kTurboPF><<<dim3((unsigned)grid), dim3(256), stream_lds, s>>>(a);
+    GLQ_LAUNCH_CHECK("turbo_stream_kernel");
+    return GLQ_OK;
+  }
+  // one-shot form: one wave per tile when there are enough tiles to fill the
+  // chip; else the K dimension of a tile is split among 2 or 4 waves
+  a.wpt = tiles >= 2048 ? 1 : tiles >= 1024 ? 2 : 4;
+  const int tpw = 4 / a.wpt;
+  a.rwgs = (int)((T + tpw - 1) / tpw);
+  const size_t lds = 4096 + (size_t)16 * a.apad * 2 + (size_t)mr * a.xstride * 2;
+  static size_t attr = 64 * 1024;
+  int rc = set_lds_limit(turbo_gemv_kernel, lds, attr);
+  if (rc) return rc;
+  const int64_t grid = items * a.rwgs * a.twgs;
+  GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
+  turbo_gemv_kernel<<<dim3((unsigned)grid), dim3(256), lds, s>>>(a);
+  GLQ_LAUNCH_CHECK("turbo_gemv_kernel");
+  return GLQ_OK;
+}
+}  // namespace
+}  // namespace glq
+
 extern "C" int glq_turbo_gemv_batched(int64_t items, const void* x_rot, int64_t x_stride,
                                       int64_t M, int64_t K, int64_t N, const int32_t* codes,
                                       int64_t codes_stride, const float* norms,
@@ -397,47 +470,70 @@ extern "C" int glq_turbo_gemv_batched(int64_t items, const void* x_rot, int64_t 
   a.K = (int)K;
   a.N = (int)N;
   a.kw = (int)(K / 16);
-  const int mr = (int)std::min<int64_t>(16, M);
-  const int nsteps = (int)((K + 255) / 256);
-  const int fit = (kTurboXBudget / (2 * mr) - 8) / 256;  // steps of a segment that fit
-  a.segsteps = std::max(1, std::min(nsteps, fit));
-  a.xstride = a.segsteps * 256 + 8;
-  a.twgs = (int)((M + 15) / 16);
-  const int64_t T = (N + 15) / 16, tiles = items * a.twgs * T;
-  const int64_t kpad = (int64_t)nsteps * 256;
-  const size_t stream_lds = (size_t)16 * a.apad * 2 + (size_t)mr * (kpad + 8) * 2;
-  hipStream_t s = (hipStream_t)stream;
-  if (tiles >= kTurboStreamTiles && stream_lds <= (size_t)kTurboStreamLds) {
-    // streaming form: the whole K staged once per workgroup, waves walk tiles
-    a.segsteps = nsteps;
-    a.xstride = (int)kpad + 8;
-    a.wpt = 1;
-    const int64_t blocks = items * a.twgs;
-    a.rwgs = (int)std::max<int64_t>(1, std::min<int64_t>((kTurboStreamWgs + blocks - 1) / blocks,
-                                                         (T + 3) / 4));
-    static size_t attr = 64 * 1024;
-    int rc = set_lds_limit(turbo_stream_kernel<kTurboPF>, stream_lds, attr);
-    if (rc) return rc;
-    const int64_t grid = blocks * a.rwgs;
-    GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
-    turbo_stream_kernel<kTurboPF><<<dim3((unsigned)grid), dim3(256), stream_lds, s>>>(a);
-    GLQ_LAUNCH_CHECK("turbo_stream_kernel");
-    return GLQ_OK;
-  }
-  // one-shot form: one wave per tile when there are enough tiles to fill the
-  // chip; else the K dimension of a tile is split among 2 or 4 waves
-  a.wpt = tiles >= 2048 ? 1 : tiles >= 1024 ? 2 : 4;
-  const int tpw = 4 / a.wpt;
-  a.rwgs = (int)((T + tpw - 1) / tpw);
-  const size_t lds = 4096 + (size_t)16 * a.apad * 2 + (size_t)mr * a.xstride * 2;
-  static size_t attr = 64 * 1024;
-  int rc = set_lds_limit(turbo_gemv_kernel, lds, attr);
-  if (rc) return rc;
-  const int64_t grid = items * a.rwgs * a.twgs;
-  GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
-  turbo_gemv_kernel<<<dim3((unsigned)grid), dim3(256), lds, s>>>(a);
-  GLQ_LAUNCH_CHECK("turbo_gemv_kernel");
-  return GLQ_OK;
+  a.wsel = nullptr;
+  a.nw = (int)std::min<int64_t>(items, 1 << 30);
+  a.x_div = 1;
+  a.xclus = nullptr;
+  a.xu_tok = a.xu_rows = 0;
+  a.gate = nullptr;
+  return turbo_run(a, items, M, K, N, (hipStream_t)stream);
+}
+
+extern "C" int glq_turbo_moe_gemv(int64_t picks, int64_t x_div, const void* x_rot, int64_t K,
+                                  int64_t N, int64_t experts, const int32_t* sel,
+                                  const int32_t* codes, const float* norms,
+                                  const float* centroids, const void* xU,
+                                  const int32_t* xu_cluster, int64_t xu_tokens,
+                                  int64_t xu_rows, const void* SV, int64_t rank,
+                                  const void* bias, const void* gate, void* y, void* stream) {
+  using namespace glq;
+  clear_error();
+  GLQ_CHECK(picks >= 0 && K >= 0 && N >= 0 && experts >= 1 && x_div >= 1, "bad size");
+  if (picks == 0 || N == 0) return GLQ_OK;
+  GLQ_CHECK(K > 0 && K % 64 == 0 && K < (1 << 24),
+            "K=%lld must be a positive multiple of 64 (whole 16-byte code pieces per row)",
+            (long long)K);
+  GLQ_CHECK(picks < (1 << 20) && N < (1ll << 26) && experts < (1 << 20), "sizes too large");
+  GLQ_CHECK(x_rot && sel && codes && norms && centroids && y, "null data pointer");
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  GLQ_CHECK(al16(x_rot) && al16(codes), "x_rot and codes must be 16-byte aligned");
+  const bool lora = SV != nullptr && rank > 0;
+  GLQ_CHECK(!lora || (rank % 8 == 0 && rank <= 256),
+            "rank=%lld must be a multiple of 8 up to 256", (long long)rank);
+  GLQ_CHECK(!lora || (xU && al16(SV)), "SV needs xU, and 16-byte alignment");
+  GLQ_CHECK(!lora || !xu_cluster || (xu_tokens >= 1 && xu_rows >= 1),
+            "xu_cluster needs xu_tokens and xu_rows");
+  TurboArgs a;
+  a.x = (const __half*)x_rot;
+  a.x_es = K;
+  a.codes = (const uint32_t*)codes;
+  a.c_es = N * (K / 16);
+  a.norms = norms;
+  a.n_es = N;
+  a.cent = centroids;
+  a.xu = lora ? (const __half*)xU : nullptr;
+  a.xu_es = lora ? rank : 0;
+  a.sv = lora ? (const __half*)SV : nullptr;
+  a.sv_es = N * rank;
+  a.bias = (const __half*)bias;
+  a.bias_es = N;
+  a.rank = lora ? (int)rank : 0;
+  a.rpad = (int)align_up(a.rank, 32);
+  a.apad = a.rpad + 8;
+  a.y = (__half*)y;
+  a.y_es = N;
+  a.M = 1;
+  a.K = (int)K;
+  a.N = (int)N;
+  a.kw = (int)(K / 16);
+  a.wsel = sel;
+  a.nw = (int)experts;
+  a.x_div = (int)x_div;
+  a.xclus = lora ? xu_cluster : nullptr;
+  a.xu_tok = (int)xu_tokens;
+  a.xu_rows = (int)std::min<int64_t>(xu_rows, 1 << 30);
+  a.gate = (const __half*)gate;
+  return turbo_run(a, picks, 1, K, N, (hipStream_t)stream);
 }
 
 extern "C" int glq_rht(const void* x, int x_fp32, int64_t rows, int64_t d, const float* signs,

@@ -316,3 +316,87 @@ def turbo_bytes(M: int, K: int, N: int, items: int = 1, rank: int = 0) -> int:
     per row, fp16 x_rot in and y out (+ fp16 SV rows and x U when rank > 0)."""
     per = N * K // 4 + 4 * N + 2 * M * (K + N) + 2 * rank * (N + M)
     return items * per
+
+
+@dataclass
+class TurboMat:
+    """TurboQuant weights of E matrices (N, K) sharing one rotation and
+    codebook (one (dim, bits, seed) configuration, the reference's
+    RotationCache key): y = norm[n] * sum_k C[q[n,k]] x_rot[k], x_rot the
+    randomized Hadamard transform of x (signs) or x Pi^T (Pi)."""
+
+    packed: torch.Tensor     # (E, N, K/4) uint8: 4 indices per byte, LSB-first
+    norms: torch.Tensor      # (E, N) fp32
+    centroids: torch.Tensor  # (4,) fp32
+    signs: torch.Tensor | None  # (K,) fp32 +-1: RHT rotation, or None
+    Pi: torch.Tensor | None     # (K, K) fp16 QR rotation when signs is None
+    bits: int = 2
+
+    @property
+    def N(self) -> int:
+        return self.packed.shape[1]
+
+    @property
+    def K(self) -> int:
+        return self.packed.shape[2] * 4
+
+    def words(self) -> torch.Tensor:
+        """(E, N, K/16) int32 view of the packed bytes."""
+        return self.packed.contiguous().view(torch.int32)
+
+
+def random_orthogonal(K: int, g: torch.Generator) -> torch.Tensor:
+    """Pi = Q of the QR factorisation of a Gaussian (K, K) matrix, signs fixed
+    by diag(R) > 0 (how TurboQuant draws its rotation), rounded to fp16."""
+    A = torch.randn(K, K, generator=g, dtype=torch.float64)
+    Q, R = torch.linalg.qr(A)
+    Q = Q * torch.sign(torch.diagonal(R))[None, :]
+    return Q.half()
+
+
+def _rand_turbo(g, E, N, K, rotation: str) -> TurboMat:
+    packed = torch.randint(0, 256, (E, N, K // 4), generator=g, dtype=torch.int32).to(torch.uint8)
+    norms = torch.randn(E, N, generator=g).abs() * 0.5 + 0.5
+    cent = torch.tensor(LLOYD_MAX_2BIT, dtype=torch.float32) / K ** 0.5
+    if rotation == "rht":
+        signs = (torch.randint(0, 2, (K,), generator=g) * 2 - 1).float()
+        return TurboMat(packed=packed, norms=norms, centroids=cent, signs=signs, Pi=None)
+    if rotation == "qr":
+        return TurboMat(packed=packed, norms=norms, centroids=cent, signs=None,
+                        Pi=random_orthogonal(K, g))
+    raise ValueError(rotation)
+
+
+def make_turbo_moe(H=2048, E=60, inter=1408, top_k=4, n_clusters=16, rank=64,
+                   shared_inter=5632, B=1, shared_bits=4, group=128, norm_topk_prob=False,
+                   seed=0, rot_gate_up="rht", rot_down="qr") -> MoEProblem:
+    """make_moe's block with TurboQuant routed experts (the reference's 2-bit
+    expert format): same draw order, with each projection's GPTQ weights
+    replaced by a TurboMat (indices uniform, norms |N(0,0.5)| + 0.5, the
+    Lloyd-Max codebook / sqrt(K); gate and up by default rotated by an RHT --
+    H is a power of two -- and down by a QR Pi, since config 2's inter 1408 is
+    not).  The shared expert stays GPTQ (shared_bits)."""
+    g = torch.Generator().manual_seed(seed)
+    router_w = (torch.randn(E, H, generator=g) * 0.02).half()
+    shared_gate_w = (torch.randn(1, H, generator=g) * 0.02).half()
+    dims = {"gate": (H, inter), "up": (H, inter), "down": (inter, H)}
+    rots = {"gate": rot_gate_up, "up": rot_gate_up, "down": rot_down}
+    experts, SV, cluster_of, U = {}, {}, {}, {}
+    for proj in PROJS:
+        K, N = dims[proj]
+        cluster_of[proj] = torch.randint(0, n_clusters, (E,), generator=g)
+        U[proj] = (torch.randn(n_clusters, K, rank, generator=g) * 0.01).half()
+        experts[proj] = _rand_turbo(g, E, N, K, rots[proj])
+        SV[proj] = (torch.randn(E, N, rank, generator=g) * 0.01).half()
+    if rot_gate_up == "rht":  # gate and up share one configuration, as in a real model
+        experts["up"].signs = experts["gate"].signs
+        experts["up"].centroids = experts["gate"].centroids
+    sdims = {"gate": (H, shared_inter), "up": (H, shared_inter), "down": (shared_inter, H)}
+    shared = None if shared_inter == 0 else {
+        proj: _rand_qmat(g, 1, sdims[proj][1], sdims[proj][0], shared_bits, group)
+        for proj in PROJS}
+    h = torch.randn(B, H, generator=g).half()
+    return MoEProblem(H=H, E=E, inter=inter, top_k=top_k, norm_topk_prob=norm_topk_prob,
+                      rank=rank, n_clusters=n_clusters, router_w=router_w,
+                      shared_gate_w=shared_gate_w, experts=experts, SV=SV,
+                      cluster_of=cluster_of, U=U, shared=shared, h=h)

@@ -19,7 +19,19 @@ Differences:
 * The experts' packed weights are stacked expert-major once, at construction,
   and the cluster U factors form one pool per projection (the reference's
   global U pool, model_builder.py:143-183).
-* GPTQ layers only (asymmetric, group 128, 2- or 4-bit containers).
+* Routed experts are GPTQ layers (asymmetric, group 128, 2- or 4-bit
+  containers) or TurboQuant layers (the reference's 2-bit expert format).
+  A TurboQuant block runs as a sequence of launches on the current stream,
+  still graph-safe with routing on the device: glq_moe_route; the input
+  rotation of gate/up (glq_rht, or x Pi^T as a library GEMM, as the
+  reference); x U of every cluster (glq_lowrank_xu_batched); the gate, then
+  the up GEMV of every pick with the SwiGLU inter formed in the up launch's
+  store (glq_turbo_moe_gemv); the rotation of inter; each pick's own
+  a_down = fp16(inter U_c) (glq_lowrank_xu_routed); the down GEMV of every
+  pick; the shared expert (its own GLoRCQLinear projections); and the
+  weighted combine with the gated shared term (glq_moe_combine).  Each step
+  reads only the picked experts' weights (the reference's graph mode runs
+  all E, :742-890).
 """
 
 from __future__ import annotations
@@ -49,6 +61,7 @@ class GraphCompatibleMoeBlock(nn.Module):
             if original_block is None:
                 raise RuntimeError("GraphCompatibleMoeBlock needs a block or stacked weights")
             stacked = self._stack_block(original_block)
+        self.kind = stacked.get("kind", "gptq")
         self.num_experts = stacked["E"]
         self.top_k = stacked["top_k"]
         self.norm_topk_prob = bool(stacked["norm_topk_prob"])
@@ -56,7 +69,7 @@ class GraphCompatibleMoeBlock(nn.Module):
         self.inter = stacked["inter"]
         self.rank = stacked["rank"]
         self.n_clusters = stacked["n_clusters"]
-        self.bits = stacked["bits"]
+        self.bits = stacked.get("bits", 2)
         self.shared_bits = stacked["shared_bits"]
         self.shared_inter = stacked["shared_inter"]
         self.group = 128
@@ -68,7 +81,7 @@ class GraphCompatibleMoeBlock(nn.Module):
         self.t = stacked  # device tensors (kept alive for the kernels)
         # the prefill kernels take integer zero-points (GPTQ's are); checked
         # once here, otherwise a prefill runs as consecutive decode steps
-        self.zeros_integral = all(
+        self.zeros_integral = self.kind == "gptq" and all(
             bool(torch.equal(stacked[f"zeros_{p}"], stacked[f"zeros_{p}"].round()))
             for p in PROJS)
 
@@ -82,6 +95,8 @@ class GraphCompatibleMoeBlock(nn.Module):
         experts = list(blk.experts)
         E = len(experts)
         lin0 = experts[0].gate_proj
+        if lin0.quant_type == "turbo":
+            return _stack_turbo_block(blk)
         dev = lin0.codes.device
         out = {"E": E, "top_k": int(blk.top_k), "norm_topk_prob": bool(blk.norm_topk_prob),
                "H": lin0.in_features, "inter": lin0.out_features,
@@ -136,6 +151,8 @@ class GraphCompatibleMoeBlock(nn.Module):
     def from_problem(cls, p: MoEProblem, device) -> "GraphCompatibleMoeBlock":
         """Block from a format.MoEProblem (synthetic configs, tests, bench)."""
         d = torch.device(device)
+        if hasattr(p.experts["gate"], "centroids"):  # TurboQuant experts
+            return cls(stacked=_turbo_from_problem(p, d))
         t = {"E": p.E, "top_k": p.top_k, "norm_topk_prob": p.norm_topk_prob, "H": p.H,
              "inter": p.inter, "bits": p.experts["gate"].bits, "rank": p.rank,
              "n_clusters": p.n_clusters,
@@ -173,6 +190,19 @@ class GraphCompatibleMoeBlock(nn.Module):
         cluster_id keep their own U (a pool without their key raises)."""
         t = self.t
         if self.rank == 0:
+            return
+        if self.kind == "turbo":
+            # the turbo step reads U by local cluster: gather the pool rows once
+            for proj in PROJS:
+                if proj not in pools:
+                    continue
+                rows = []
+                for key in t[f"ckeys_{proj}"]:
+                    if key[0] != "c" or key[1] not in id_maps[proj]:
+                        raise RuntimeError(f"{proj}: cluster {key} is not in the pool")
+                    rows.append(int(id_maps[proj][key[1]]))
+                idx = torch.tensor(rows, dtype=torch.long, device=pools[proj].device)
+                t[f"U_{proj}"] = pools[proj].index_select(0, idx).contiguous()
             return
         for proj in PROJS:
             if proj not in pools:
@@ -241,6 +271,18 @@ class GraphCompatibleMoeBlock(nn.Module):
                 raise RuntimeError("residual must match hidden_states (fp16)")
             res = residual.reshape(-1, self.hidden).contiguous()
         t = self.t
+        if self.kind == "turbo":
+            outs, logits = [], []
+            for t0 in range(0, h.shape[0], TURBO_MAX_TOKENS):
+                t1 = min(h.shape[0], t0 + TURBO_MAX_TOKENS)
+                o, lg = turbo_step(self, h[t0:t1].contiguous(),
+                                   None if res is None else res[t0:t1].contiguous())
+                outs.append(o)
+                logits.append(lg)
+            out = outs[0] if len(outs) == 1 else torch.cat(outs)
+            lg = logits[0] if len(logits) == 1 else torch.cat(logits)
+            out = out.reshape(shape)
+            return (out, lg) if self.return_router_logits else out
         codes, scales, zeros, U, cl, SV, u_slot, u_rows, sc, ss, sz = self._op_args()
         if h.shape[0] <= self.MAX_TOKENS:
             out, logits = torch.ops.glorcq_hip.moe_decode(
@@ -257,9 +299,231 @@ class GraphCompatibleMoeBlock(nn.Module):
         return (out, logits) if self.return_router_logits else out
 
     def extra_repr(self):
+        kind = "turbo" if self.kind == "turbo" else f"bits={self.bits}"
         return (f"experts={self.num_experts}, top_k={self.top_k}, hidden={self.hidden}, "
-                f"inter={self.inter}, bits={self.bits}, rank={self.rank}, "
+                f"inter={self.inter}, {kind}, rank={self.rank}, "
                 f"clusters={self.n_clusters}, shared_inter={self.shared_inter}")
+
+
+# ---------------------------------------------------------------------------
+# TurboQuant routed experts
+# ---------------------------------------------------------------------------
+TURBO_MAX_TOKENS = 16  # tokens per turbo step (the cluster-shared x U takes <= 16 rows)
+
+
+def _turbo_rotation(lins, proj):
+    """(signs, Pi, centroids) of one projection's experts, which must share one
+    (dim, bits, seed) configuration (the reference's rotation-cache key,
+    moe_block.py:331-357)."""
+    l0 = lins[0]
+    key = (l0.turbo_dim, l0.turbo_bits, l0.turbo_seed)
+    for lin in lins:
+        if (lin.turbo_dim, lin.turbo_bits, lin.turbo_seed) != key:
+            raise RuntimeError(f"{proj}: experts need one TurboQuant (dim, bits, seed)")
+        if (lin._rht_signs is None) != (l0._rht_signs is None):
+            raise RuntimeError(f"{proj}: experts need one rotation kind (RHT or Pi)")
+    cent = l0._rotation_cache.get_centroids(*key).float().contiguous()
+    if l0._rht_signs is not None:
+        return l0._rht_signs.float().contiguous(), None, cent
+    return None, l0._rotation_cache.get_pi(*key).contiguous(), cent
+
+
+def _stack_turbo_block(blk) -> dict:
+    """Stacks a block whose routed experts are TurboQuant GLoRCQLinear layers;
+    the shared expert keeps its own projections (any GLoRCQLinear kind)."""
+    experts = list(blk.experts)
+    E = len(experts)
+    lin0 = experts[0].gate_proj
+    dev = lin0.turbo_words.device
+    out = {"kind": "turbo", "E": E, "top_k": int(blk.top_k),
+           "norm_topk_prob": bool(getattr(blk, "norm_topk_prob", False)),
+           "H": lin0.in_features, "inter": lin0.out_features, "rank": lin0.rank}
+    out["router_w"] = blk.gate.weight.detach().to(dev, torch.float16).contiguous()
+    n_clusters = 0
+    for proj in PROJS:
+        lins = [getattr(ex, _PROJ_ATTR[proj]) for ex in experts]
+        for lin in lins:
+            if lin.quant_type != "turbo":
+                raise RuntimeError("routed experts must all be TurboQuant or all GPTQ")
+            if lin.rank != out["rank"]:
+                raise RuntimeError("all experts need one LoRA rank")
+            if getattr(lin, "bias_param", None) is not None:
+                raise RuntimeError("TurboQuant MoE experts take no bias")
+        out[f"words_{proj}"] = _stack([lin.turbo_words for lin in lins])
+        out[f"norms_{proj}"] = _stack([lin.norms for lin in lins])
+        signs, Pi, cent = _turbo_rotation(lins, proj)
+        out[f"signs_{proj}"], out[f"Pi_{proj}"], out[f"cent_{proj}"] = signs, Pi, cent
+        if out["rank"] > 0:
+            ids, pool, cl = {}, [], []
+            for e, lin in enumerate(lins):
+                key = ("c", lin.cluster_id) if lin.cluster_id is not None else ("e", e)
+                if key not in ids:
+                    ids[key] = len(pool)
+                    pool.append(lin.U)
+                cl.append(ids[key])
+            out[f"U_{proj}"] = _stack(pool)
+            out[f"cluster_{proj}"] = torch.tensor(cl, dtype=torch.int32, device=dev)
+            out[f"ckeys_{proj}"] = list(ids.keys())
+            out[f"SV_{proj}"] = _stack([lin.SV for lin in lins])
+            n_clusters = max(n_clusters, len(pool))
+    out["n_clusters"] = n_clusters
+    sh = getattr(blk, "shared_expert", None)
+    if sh is not None:
+        out["shared_mods"] = tuple(getattr(sh, _PROJ_ATTR[p]) for p in PROJS)
+        out["shared_inter"] = out["shared_mods"][0].out_features
+        g = getattr(blk, "shared_expert_gate", None)
+        out["shared_gate_w"] = (None if g is None else
+                                g.weight.detach().reshape(-1).to(dev, torch.float16).contiguous())
+    else:
+        out["shared_inter"], out["shared_gate_w"] = 0, None
+    out["shared_bits"] = 0
+    out["same_rot_gu"] = _same_rotation(out)
+    return out
+
+
+def _turbo_from_problem(p: MoEProblem, d) -> dict:
+    """Turbo block tensors from a format.MoEProblem whose experts are
+    format.TurboMat (the shared expert, if any, a GPTQ format.QMat)."""
+    t = {"kind": "turbo", "E": p.E, "top_k": p.top_k, "norm_topk_prob": p.norm_topk_prob,
+         "H": p.H, "inter": p.inter, "rank": p.rank, "n_clusters": p.n_clusters,
+         "router_w": p.router_w.to(d).contiguous(), "shared_bits": 0}
+    for proj in PROJS:
+        q = p.experts[proj]
+        t[f"words_{proj}"] = q.words().to(d).contiguous()
+        t[f"norms_{proj}"] = q.norms.to(d, torch.float32).contiguous()
+        t[f"cent_{proj}"] = q.centroids.to(d, torch.float32).contiguous()
+        t[f"signs_{proj}"] = None if q.signs is None else q.signs.to(d, torch.float32).contiguous()
+        t[f"Pi_{proj}"] = None if q.Pi is None else q.Pi.to(d, torch.float16).contiguous()
+        if p.rank > 0:
+            t[f"U_{proj}"] = p.U[proj].to(d).contiguous()
+            t[f"cluster_{proj}"] = p.cluster_of[proj].to(d, torch.int32).contiguous()
+            t[f"SV_{proj}"] = p.SV[proj].to(d).contiguous()
+            t[f"ckeys_{proj}"] = [("c", c) for c in range(p.n_clusters)]
+    if p.shared is not None:
+        t["shared_q"] = {proj: (p.shared[proj].codes[0].to(d).contiguous(),
+                                p.shared[proj].scales[0].to(d).contiguous(),
+                                p.shared[proj].zeros[0].to(d).contiguous(),
+                                p.shared[proj].bits) for proj in PROJS}
+        t["shared_inter"] = p.shared["gate"].N
+        t["shared_gate_w"] = p.shared_gate_w.reshape(-1).to(d).contiguous()
+    else:
+        t["shared_inter"], t["shared_gate_w"] = 0, None
+    t["same_rot_gu"] = _same_rotation(t)
+    return t
+
+
+def _same_rotation(t: dict) -> bool:
+    """gate and up rotate x alike (one x_rot serves both); checked once, at
+    construction, so a step makes no host sync."""
+    sg, su, pg, pu = t["signs_gate"], t["signs_up"], t["Pi_gate"], t["Pi_up"]
+    if sg is not None and su is not None:
+        return sg is su or bool(torch.equal(sg, su))
+    if pg is not None and pu is not None:
+        return pg is pu or bool(torch.equal(pg, pu))
+    return False
+
+
+# routing workspaces: (device index, stream handle) -> zero-filled uint8 tensor
+_route_ws: dict = {}
+
+
+def _rotate(x: torch.Tensor, signs, Pi) -> torch.Tensor:
+    """x_rot = fp16(RHT(x)) (one glq_rht launch) or fp16(x.float() @ Pi.float().T)
+    (a library GEMM, as the reference computes it, moe_block.py:352-356)."""
+    from .kernels import _rht_eager
+    if signs is not None:
+        return _rht_eager(x, signs)
+    return (x.float() @ Pi.float().T).half()
+
+
+def turbo_step(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.Tensor | None):
+    """One decode step of a TurboQuant block (<= TURBO_MAX_TOKENS tokens):
+    (out (B, H) fp16, router logits (B, E) fp16)."""
+    from .kernels import _lowrank_xu_eager, _packed_dequant_matmul_eager, workspace
+    lib = _lib.load()
+    t = blk.t
+    dev = h.device
+    B, H = h.shape
+    E, k, I, r = blk.num_experts, blk.top_k, blk.inter, blk.rank
+    P = B * k
+    stream = _lib.stream_handle(dev)
+    # 1. routing on the device
+    sel = torch.empty(P, dtype=torch.int32, device=dev)
+    wts = torch.empty(P, dtype=torch.float16, device=dev)
+    sg = torch.empty(B, dtype=torch.float16, device=dev)
+    logits = torch.empty(B, E, dtype=torch.float16, device=dev)
+    n = lib.glq_moe_route_workspace_bytes(B, E)
+    key = (dev.index, stream)
+    ws = _route_ws.get(key)
+    if ws is None or ws.numel() < n:
+        ws = torch.zeros(max(int(n), 256), dtype=torch.uint8, device=dev)  # counters start at zero
+        _route_ws[key] = ws
+    _lib.check(lib.glq_moe_route(h.data_ptr(), t["router_w"].data_ptr(),
+                                 _lib.ptr(t["shared_gate_w"]), B, H, E, k,
+                                 int(blk.norm_topk_prob), sel.data_ptr(), wts.data_ptr(),
+                                 sg.data_ptr(), logits.data_ptr(), ws.data_ptr(), ws.numel(),
+                                 stream), "glq_moe_route")
+
+    def gemv(x_rot, x_div, K, N, proj, xU, xclus, xtok, xrows, gate, y):
+        _lib.check(lib.glq_turbo_moe_gemv(
+            P, x_div, x_rot.data_ptr(), K, N, E, sel.data_ptr(), t[f"words_{proj}"].data_ptr(),
+            t[f"norms_{proj}"].data_ptr(), t[f"cent_{proj}"].data_ptr(), _lib.ptr(xU),
+            _lib.ptr(xclus), xtok, xrows, _lib.ptr(t.get(f"SV_{proj}")) if r else None, r, None,
+            _lib.ptr(gate), y.data_ptr(), stream), "glq_turbo_moe_gemv")
+
+    # 2. gate and up: x rotated once per configuration, x U once per cluster
+    xg = _rotate(h, t["signs_gate"], t["Pi_gate"])
+    xu_ = xg if t["same_rot_gu"] else _rotate(h, t["signs_up"], t["Pi_up"])
+    ag = au = None
+    if r:
+        ag = _lowrank_xu_eager(h, t["U_gate"])  # (C, B, r)
+        au = _lowrank_xu_eager(h, t["U_up"])
+    g = torch.empty(P, I, dtype=torch.float16, device=dev)
+    gemv(xg, k, H, I, "gate", ag, t.get("cluster_gate"), B, 0 if ag is None else ag.shape[0] * B,
+         None, g)
+    inter = torch.empty(P, I, dtype=torch.float16, device=dev)
+    gemv(xu_, k, H, I, "up", au, t.get("cluster_up"), B, 0 if au is None else au.shape[0] * B,
+         g, inter)
+    # 3. down: inter rotated, each pick's own a_down = fp16(inter U_c)
+    xd = _rotate(inter, t["signs_down"], t["Pi_down"])
+    ad = None
+    if r:
+        ad = torch.empty(P, r, dtype=torch.float16, device=dev)
+        nb = lib.glq_lowrank_workspace_bytes(P, 1, I, r)
+        wl = workspace(dev, max(int(nb), 256))
+        U = t["U_down"]
+        _lib.check(lib.glq_lowrank_xu_routed(P, inter.data_ptr(), I, U.data_ptr(), U.shape[0], r,
+                                             sel.data_ptr(), E, t["cluster_down"].data_ptr(),
+                                             ad.data_ptr(), wl.data_ptr(), wl.numel(), stream),
+                   "glq_lowrank_xu_routed")
+    yd = torch.empty(P, H, dtype=torch.float16, device=dev)
+    gemv(xd, 1, I, H, "down", ad, None, 0, 0, None, yd)
+    # 4. the shared expert and the combine
+    shared = None
+    if blk.shared_inter > 0:
+        if "shared_mods" in t:
+            mg, mu, md = t["shared_mods"]
+            sgo, suo = mg(h), mu(h)
+        else:
+            q = t["shared_q"]
+            sgo = _packed_dequant_matmul_eager(h, q["gate"][0], q["gate"][1], q["gate"][2],
+                                               q["gate"][3], 128)
+            suo = _packed_dequant_matmul_eager(h, q["up"][0], q["up"][1], q["up"][2],
+                                               q["up"][3], 128)
+        si = torch.empty_like(sgo)
+        _lib.check(lib.glq_swiglu(sgo.data_ptr(), suo.data_ptr(), si.numel(), si.data_ptr(),
+                                  stream), "glq_swiglu")
+        if "shared_mods" in t:
+            shared = md(si).contiguous()
+        else:
+            q = t["shared_q"]
+            shared = _packed_dequant_matmul_eager(si, q["down"][0], q["down"][1], q["down"][2],
+                                                  q["down"][3], 128)
+    out = torch.empty(B, H, dtype=torch.float16, device=dev)
+    _lib.check(lib.glq_moe_combine(yd.data_ptr(), wts.data_ptr(), _lib.ptr(shared), sg.data_ptr(),
+                                   _lib.ptr(res), B, H, k, out.data_ptr(), stream),
+               "glq_moe_combine")
+    return out, logits
 
 
 # ---------------------------------------------------------------------------

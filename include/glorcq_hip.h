@@ -150,6 +150,18 @@ int glq_lowrank_xu_batched(int64_t items, const void* x, int64_t x_stride, int64
                            const void* U, int64_t u_stride, int64_t rank, void* xu,
                            int64_t xu_stride, void* workspace, int64_t workspace_bytes,
                            void* stream);
+/*
+ * The same for the picks of a MoE step: a[p] = fp16(x[p] U_c) (x (picks, K)
+ * fp16, a (picks, rank) fp16) with U_c row c = cluster_of[sel[p]] of U
+ * (u_rows, K, rank) -- each routed expert's down projection's own
+ * a = fp16(inter @ U_down) (inference/moe_block.py:661-676).  sel values are
+ * clamped into [0, experts), cluster_of values into [0, u_rows).  Workspace:
+ * glq_lowrank_workspace_bytes(picks, 1, K, rank).
+ */
+int glq_lowrank_xu_routed(int64_t picks, const void* x, int64_t K, const void* U,
+                          int64_t u_rows, int64_t rank, const int32_t* sel, int64_t experts,
+                          const int32_t* cluster_of, void* xu, void* workspace,
+                          int64_t workspace_bytes, void* stream);
 
 /*
  * Prefill GEMM (any M, built for M > 16): y = dequant(codes) x + (x U) SV^T
@@ -322,6 +334,61 @@ int glq_moe_decode(const glq_moe_params* p, void* workspace, int64_t workspace_b
 int64_t glq_moe_prefill_workspace_bytes(const glq_moe_params* p);
 int glq_moe_prefill(const glq_moe_params* p, void* workspace, int64_t workspace_bytes,
                     void* stream);
+
+/*
+ * The pieces of a decode step whose routed experts are TurboQuant layers
+ * (the reference's 2-bit expert format; inference/moe_block.py:381-436 with
+ * the turbo expert projections of :480-702), composed by
+ * glorcq_amd/moe_block.py.  Picks are p = t * top_k + k.
+ *
+ * glq_moe_route: the router of glq_moe_decode alone (moe_block.py:386-392):
+ * fp16 logits, fp32 softmax, top-k (ties to the lower index), optional
+ * renormalisation, weights rounded to fp16; sel (tokens * top_k) int32,
+ * weights (tokens * top_k) fp16, shared_gate (tokens) fp16 =
+ * sigmoid(h . shared_gate_w) (1 when shared_gate_w is NULL), logits (tokens,
+ * experts) fp16 or NULL.  hidden a multiple of 8, <= 4096.  The workspace
+ * (glq_moe_route_workspace_bytes, 16-byte aligned) must be zero-filled before
+ * its first use; every call leaves its counters zero.
+ */
+int64_t glq_moe_route_workspace_bytes(int64_t tokens, int64_t experts);
+int glq_moe_route(const void* h, const void* router_w, const void* shared_gate_w,
+                  int64_t tokens, int64_t hidden, int64_t experts, int64_t top_k,
+                  int norm_topk_prob, int32_t* sel, void* weights, void* shared_gate,
+                  void* logits, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Turbo GEMV of every pick (turbo_dequant_matmul_fused per expert,
+ * inference/kernels/__init__.py:184-239, as _batched_proj_forward and
+ * _batched_down_forward call it, moe_block.py:480-702): pick p multiplies x
+ * row p / x_div of x_rot (K) by expert sel[p]'s codes (experts, N, K/16)
+ * int32, norms (experts, N) fp32 and the shared centroids, plus
+ * a SV_sel[p]^T with a = xU row xu_cluster[sel[p]] * xu_tokens + p / x_div
+ * (xU rows clamped below xu_rows; xu_cluster NULL: row p), SV (experts, N,
+ * rank), and bias (experts, N) if given.  y (picks, N) fp16; with gate
+ * (picks, N) fp16 the store is fp16(fp16(silu(gate)) * fp16(y)) (the up
+ * projection's launch forms the SwiGLU inter).  sel values are clamped into
+ * [0, experts).
+ */
+int glq_turbo_moe_gemv(int64_t picks, int64_t x_div, const void* x_rot, int64_t K, int64_t N,
+                       int64_t experts, const int32_t* sel, const int32_t* codes,
+                       const float* norms, const float* centroids, const void* xU,
+                       const int32_t* xu_cluster, int64_t xu_tokens, int64_t xu_rows,
+                       const void* SV, int64_t rank, const void* bias, const void* gate,
+                       void* y, void* stream);
+
+/*
+ * out[t] = fp16(sum_k weights[t][k] y[t top_k + k] + shared_gate[t] shared[t])
+ * (+ residual[t]): the block's weighted sum (moe_block.py:470-476) and the
+ * gated shared expert (:429-435) in fp32, rounded once (shared NULL: no
+ * shared term; residual NULL: none).  y (tokens * top_k, hidden) fp16.
+ */
+int glq_moe_combine(const void* y, const void* weights, const void* shared,
+                    const void* shared_gate, const void* residual, int64_t tokens,
+                    int64_t hidden, int64_t top_k, void* out, void* stream);
+
+/* out = fp16(fp16(silu(gate)) * up), n fp16 elements (act_fn(gate) * up,
+ * moe_block.py:465-468 on a shared expert). */
+int glq_swiglu(const void* gate, const void* up, int64_t n, void* out, void* stream);
 
 /*
  * Debug: unpack codes (N, K*bits/32) int32 -> (N, K) int32.  Codes are

@@ -233,13 +233,52 @@ def route(h: torch.Tensor, router_w: torch.Tensor, top_k: int, norm_topk_prob: b
     return logits, w.half(), sel
 
 
+def turbo_rotate(x: torch.Tensor, q, exact: bool) -> torch.Tensor:
+    """x_rot of a format.TurboMat's configuration, rounded to fp16 as the
+    reference's rotation cache does: fp16(rht_forward(x.float(), signs))
+    (inference/moe_block.py:349-351) or fp16(x.float() @ Pi.float().T) (:352-356).
+    exact=True takes both in fp64 before the rounding (the package and torch
+    compute them in fp32)."""
+    if q.signs is not None:
+        return rht_forward(x.float(), q.signs).half()
+    if exact:
+        return (x.double() @ q.Pi.double().T).half()
+    return rotate_qr(x, q.Pi)
+
+
+def _turbo_linear(x, q, e, exact, U=None, SV=None, a=None):
+    """TurboQuant expert e of a format.TurboMat as the MoE block calls it
+    (GLoRCQLinear's turbo forward with a precomputed x_rot, inference/
+    quantized_linear.py:315-349; moe_block.py:480-702): x_rot = turbo_rotate(x);
+    y = norm * C[q] x_rot (+ a @ SV_e^T, a = fp16(x @ U) of the unrotated x
+    unless given).  exact=True: fp64 sums; else the reference's fp32 fallback
+    rounded to fp16 and fp16 low-rank matmuls."""
+    xr = turbo_rotate(x, q, exact)
+    packed = q.packed[e].numpy()
+    if exact:
+        y = turbo_matmul_fp64(xr, packed, q.norms[e], q.centroids)
+        if SV is not None:
+            if a is None:
+                a = (x.double() @ U.double()).half()
+            y = y + a.double() @ SV.double().T
+        return y
+    y = turbo_matmul_fp32(xr, packed, q.norms[e], q.centroids).half()
+    if SV is not None:
+        if a is None:
+            a = x.half() @ U.half()
+        y = y + a.half() @ SV.half().T
+    return y
+
+
 def _qmat_linear(x, q, e, exact, U=None, SV=None, a=None, memo=None):
     """y = x @ W_e^T (+ a @ SV_e^T, a = fp16(x @ U) unless given) for expert e of
-    a format.QMat.  exact=False: the reference's fp16 CPU fallback (fp16 dequant,
+    a format.QMat (a format.TurboMat goes to _turbo_linear).  exact=False: the reference's fp16 CPU fallback (fp16 dequant,
     fp16 matmuls, quantized_linear.py:286-355); exact=True: fp64 sums of the
     exact weights s*(q - z), with a rounded to fp16 as the reference does.
     memo (exact only): a dict that keeps each expert's exact weights across
     calls, for callers whose weights do not change (multi-step decoding)."""
+    if hasattr(q, "centroids"):
+        return _turbo_linear(x, q, e, exact, U=U, SV=SV, a=a)
     if exact and memo is not None and (id(q), e) in memo:
         W = memo[(id(q), e)].double()
     elif exact:
