@@ -373,9 +373,9 @@ def make_turbo_moe(H=2048, E=60, inter=1408, top_k=4, n_clusters=16, rank=64,
     """make_moe's block with TurboQuant routed experts (the reference's 2-bit
     expert format): same draw order, with each projection's GPTQ weights
     replaced by a TurboMat (indices uniform, norms |N(0,0.5)| + 0.5, the
-    Lloyd-Max codebook / sqrt(K); gate and up by default rotated by an RHT --
-    H is a power of two -- and down by a QR Pi, since config 2's inter 1408 is
-    not).  The shared expert stays GPTQ (shared_bits)."""
+    Lloyd-Max codebook / sqrt(K); gate and up share one rotation, by default an
+    RHT -- H is a power of two -- and down a QR Pi, since config 2's inter 1408
+    is not).  The shared expert stays GPTQ (shared_bits)."""
     g = torch.Generator().manual_seed(seed)
     router_w = (torch.randn(E, H, generator=g) * 0.02).half()
     shared_gate_w = (torch.randn(1, H, generator=g) * 0.02).half()
@@ -388,9 +388,10 @@ def make_turbo_moe(H=2048, E=60, inter=1408, top_k=4, n_clusters=16, rank=64,
         U[proj] = (torch.randn(n_clusters, K, rank, generator=g) * 0.01).half()
         experts[proj] = _rand_turbo(g, E, N, K, rots[proj])
         SV[proj] = (torch.randn(E, N, rank, generator=g) * 0.01).half()
-    if rot_gate_up == "rht":  # gate and up share one configuration, as in a real model
-        experts["up"].signs = experts["gate"].signs
-        experts["up"].centroids = experts["gate"].centroids
+    # gate and up share one (dim, bits, seed) configuration, as in a real model
+    experts["up"].signs = experts["gate"].signs
+    experts["up"].Pi = experts["gate"].Pi
+    experts["up"].centroids = experts["gate"].centroids
     sdims = {"gate": (H, shared_inter), "up": (H, shared_inter), "down": (shared_inter, H)}
     shared = None if shared_inter == 0 else {
         proj: _rand_qmat(g, 1, sdims[proj][1], sdims[proj][0], shared_bits, group)

@@ -151,3 +151,71 @@ def test_turbo_step_in_a_hip_graph(gpu):
         assert torch.equal(static_out, ref)
         _ = blk(hs[0])  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_turbo_block_from_checkpoint(gpu, tmp_path):
+    """A checkpoint in the reference's format (glorcq_model.pt with
+    packed_indices / norms / bits / dim / seed per expert module, the shared
+    expert as GPTQ; cross_layer_info.pt with cluster U and per-expert SV)
+    loaded by load_glorcq_checkpoint + build_glorcq_layers, placed into a block
+    and run as GraphCompatibleMoeBlock, against the oracle.  Rotation 'qr':
+    the RotationCache holds Pi and the codebook per (dim, bits, seed)."""
+    from glorcq_amd import model_builder as MB
+    from glorcq_amd.quantized_linear import RotationCache
+
+    p = problem(3, 4, shared_inter=512, E=8, top_k=2, rot_gate_up="qr")
+    assert margin(p) >= 2
+    seed = 42
+    layers = {0: {}}
+    for e in range(p.E):
+        for proj in fmt.PROJS:
+            q = p.experts[proj]
+            layers[0][f"mlp.experts.{e}.{proj}_proj"] = {
+                "packed_indices": q.packed[e].clone(), "norms": q.norms[e].clone(),
+                "bits": 2, "dim": q.K, "seed": seed}
+    for proj in fmt.PROJS:
+        s = p.shared[proj]
+        qi = torch.from_numpy(O.unpack_codes(s.codes[0].numpy(), s.bits, s.K))
+        layers[0][f"mlp.shared_expert.{proj}_proj"] = {
+            "qweight_int": qi, "scales": s.scales[0].clone(), "zeros": s.zeros[0].clone(),
+            "bits": s.bits, "groupsize": s.group, "sym": False}
+    model_data = {"model_config": {"uv_bits": 16, "rotation_type": "qr", "qbit": 2},
+                  "layers": layers}
+    shared, per_expert_V, assignments = {}, {}, {}
+    for proj in fmt.PROJS:
+        w = f"{proj}_proj"
+        shared[w] = {c: {"U_fp16": p.U[proj][c].clone()} for c in range(p.n_clusters)}
+        assignments[w] = [{"layer": 0, "expert": e, "group_id": int(p.cluster_of[proj][e])}
+                          for e in range(p.E)]
+        per_expert_V[w] = [{"SV_fp16": p.SV[proj][e].clone()} for e in range(p.E)]
+    cross = {"config": {"uv_bits": 16}, "assignments": assignments,
+             "shared_matrices": shared, "per_expert_V": per_expert_V}
+    torch.save(model_data, tmp_path / "glorcq_model.pt")
+    torch.save(cross, tmp_path / "cross_layer_info.pt")
+    cache = RotationCache(device=gpu)
+    for proj in ("gate", "down"):
+        q = p.experts[proj]
+        cache.put(q.K, 2, seed, q.Pi, q.centroids)
+    md, cl = MB.load_glorcq_checkpoint(str(tmp_path))
+    built, _ = MB.build_glorcq_layers(md, cl, device=gpu, rotation_cache=cache)
+    mods = built[0]
+
+    class Proj(nn.Module):
+        def __init__(self, prefix):
+            super().__init__()
+            for proj in fmt.PROJS:
+                setattr(self, f"{proj}_proj", mods[f"{prefix}.{proj}_proj"])
+
+    blk = nn.Module()
+    blk.num_experts, blk.top_k, blk.norm_topk_prob = p.E, p.top_k, False
+    blk.gate = nn.Linear(p.H, p.E, bias=False)
+    blk.gate.weight.data = p.router_w.clone()
+    blk.experts = nn.ModuleList([Proj(f"mlp.experts.{e}") for e in range(p.E)])
+    blk.shared_expert = Proj("mlp.shared_expert")
+    blk.shared_expert_gate = nn.Linear(p.H, 1, bias=False)
+    blk.shared_expert_gate.weight.data = p.shared_gate_w.clone()
+    mine = GraphCompatibleMoeBlock(blk)
+    assert mine.kind == "turbo"
+    out, logits = run(mine, p, gpu)
+    check_routing(p, logits)
+    assert bar(out, O.moe_forward(p))
