@@ -406,6 +406,27 @@ def bench_moe(dev, seed=6, reps=20, trials=15):
     return res
 
 
+def bench_moe_turbo(dev, seed=6, reps=10, trials=9):
+    """Config 2's block with TurboQuant routed experts (the reference's 2-bit
+    expert format; format.make_turbo_moe: gate/up rotated by an RHT, down by a
+    QR Pi, the 4-bit GPTQ shared expert): one decode step per call through
+    GraphCompatibleMoeBlock's turbo step, hipGraph replays as bench_moe."""
+    from glorcq_amd import format as fmt
+    from glorcq_amd.moe_block import GraphCompatibleMoeBlock
+
+    res = {}
+    for B in (1, 4, 16):
+        p = fmt.make_turbo_moe(B=B, seed=seed)
+        blk = GraphCompatibleMoeBlock.from_problem(p, dev)
+        h = p.h.reshape(1, B, p.H).to(dev)
+        blk(h)
+        us = _graph_step_us(lambda: blk(h), reps, trials)
+        res[str(B)] = {"us_per_step": round(us, 2), "us_per_token": round(us / B, 3)}
+        log(f"moe turbo experts B={B}: {us:.2f} us/step")
+        del blk
+    return res
+
+
 def bench_mixtral(dev, seed=3, reps=20, trials=11, prefill_tokens=512):
     """Config 3 (a Mixtral-8x7B-shaped MoE layer: H 4096, ffn 14336, 8 experts,
     top-2 renormalised, 2-bit g128 experts, rank-64 LoRA over 2 clusters, no
@@ -719,6 +740,8 @@ def main():
             "by_batch": moe}
         log("Mixtral-shaped MoE layer (config 3): decode steps and a prefill")
         result["mixtral_layer"] = bench_mixtral(dev)
+        log("config 2 block with TurboQuant routed experts")
+        result["moe_turbo_experts_decode"] = bench_moe_turbo(dev)
     if not args.no_turbo:
         log("TurboQuant codebook GEMV (the reference's 2-bit expert format), M = 1")
         result["turbo_codec_gemv"] = bench_turbo(dev)
