@@ -41,10 +41,11 @@ struct DenseArgs {
   const float* apart;  // launch-1 partials (items x P x M x rpad), or null
   int items, M, P, tiles;
   TileShape sh;
-  // routed picks (glq_lowrank_xu_routed): item i takes U row ucl[usel[i]]
-  const int32_t* usel;
-  const int32_t* ucl;
-  int nsel, nu;
+  // routed picks (glq_lowrank_xu_routed): item i takes U row ucl[usel[i]];
+  // null usel (every other launch): U of item i
+  const int32_t* usel = nullptr;
+  const int32_t* ucl = nullptr;
+  int nsel = 0, nu = 0;
 };
 
 // Item data of a dense launch: item i is at base + i * stride.
@@ -520,7 +521,7 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   }
 
   const int T = gemv_pick_tiles(items, N);
-  DenseArgs a;
+  DenseArgs a = {};
   a.codes = (const uint32_t*)codes;
   a.codes_es = codes_stride;
   a.scales = (const __half*)scales;

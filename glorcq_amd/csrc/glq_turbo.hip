@@ -61,12 +61,12 @@ struct TurboArgs {
   int rwgs, twgs;          // row groups (4/wpt tiles) and token blocks (16 tokens) per item
   // routed picks of a MoE step (glq_turbo_moe_gemv); the plain batched call
   // leaves wsel, xclus and gate null and x_div 1
-  const int32_t* wsel;     // weight set (codes, norms, SV, bias) of item i: wsel[i] (< nw)
-  int nw;
-  int x_div;               // x row of item i: i / x_div
-  const int32_t* xclus;    // a row of item i: xclus[wsel[i]] * xu_tok + i / x_div (< xu_rows)
-  int xu_tok, xu_rows;
-  const __half* gate;      // (items, M, N): y = fp16(fp16(silu(gate)) * y)
+  const int32_t* wsel = nullptr;  // weight set (codes, norms, SV, bias) of item i: wsel[i] (< nw)
+  int nw = 0;
+  int x_div = 1;                  // x row of item i: i / x_div
+  const int32_t* xclus = nullptr;  // a row of item i: xclus[wsel[i]] * xu_tok + i / x_div (< xu_rows)
+  int xu_tok = 0, xu_rows = 0;
+  const __half* gate = nullptr;   // (items, M, N): y = fp16(fp16(silu(gate)) * y)
 };
 
 // Weight set, x row and low-rank row of an item.
