@@ -143,6 +143,53 @@ def test_decoder_entry_points_check_arguments(lib):
     assert lib.glq_decode_attention(*bad) == 0
 
 
+def test_turbo_moe_entry_points_check_arguments(lib):
+    """The pieces of a TurboQuant-expert MoE step reject bad shapes on the
+    host, before any launch; empty work is a no-op."""
+    nul, p = None, 1 << 12
+    n = lib.glq_moe_route_workspace_bytes(4, 60)
+    assert n == 4 * 64 + 2 * 4 * 61
+    assert lib.glq_moe_route_workspace_bytes(0, 60) == -1
+    rargs = [p, p, nul, 4, 2048, 60, 4, 0, p, p, p, nul, p, n, nul]
+    bad = list(rargs); bad[6] = 0                        # top_k
+    assert lib.glq_moe_route(*bad) == 1 and b"top_k" in lib.glq_last_error()
+    bad = list(rargs); bad[4] = 8192                     # hidden past the router's 4096
+    assert lib.glq_moe_route(*bad) == 1 and b"hidden" in lib.glq_last_error()
+    bad = list(rargs); bad[5] = 300                      # experts
+    assert lib.glq_moe_route(*bad) == 1
+    bad = list(rargs); bad[13] = n - 1                   # workspace too small
+    assert lib.glq_moe_route(*bad) == 1 and b"workspace" in lib.glq_last_error()
+    bad = list(rargs); bad[0] = p + 2                    # h not 16-byte aligned
+    assert lib.glq_moe_route(*bad) == 1
+    targs = [16, 4, p, 2048, 1408, 60, p, p, p, p, p, p, 4, 16, p, 64, nul, nul, p, nul]
+    bad = list(targs); bad[3] = 2000                     # K not a multiple of 64
+    assert lib.glq_turbo_moe_gemv(*bad) == 1 and b"multiple of 64" in lib.glq_last_error()
+    bad = list(targs); bad[15] = 60                      # rank not a multiple of 8
+    assert lib.glq_turbo_moe_gemv(*bad) == 1 and b"rank" in lib.glq_last_error()
+    bad = list(targs); bad[10] = nul                     # SV without xU
+    assert lib.glq_turbo_moe_gemv(*bad) == 1
+    bad = list(targs); bad[12] = 0                       # a cluster table without its rows
+    assert lib.glq_turbo_moe_gemv(*bad) == 1
+    bad = list(targs); bad[1] = 0                        # x_div
+    assert lib.glq_turbo_moe_gemv(*bad) == 1
+    bad = list(targs); bad[0] = 0
+    assert lib.glq_turbo_moe_gemv(*bad) == 0
+    largs = [16, p, 1408, p, 4, 64, p, 60, p, p, p, 1 << 20, nul]
+    bad = list(largs); bad[5] = 60                       # rank
+    assert lib.glq_lowrank_xu_routed(*bad) == 1 and b"rank" in lib.glq_last_error()
+    bad = list(largs); bad[11] = 16                      # workspace too small
+    assert lib.glq_lowrank_xu_routed(*bad) == 1 and b"workspace" in lib.glq_last_error()
+    bad = list(largs); bad[8] = nul                      # no cluster table
+    assert lib.glq_lowrank_xu_routed(*bad) == 1
+    bad = list(largs); bad[0] = 0
+    assert lib.glq_lowrank_xu_routed(*bad) == 0
+    assert lib.glq_moe_combine(p, p, nul, nul, nul, 4, 2048, 17, p, nul) == 1  # top_k
+    assert lib.glq_moe_combine(p, p, p, nul, nul, 4, 2048, 4, p, nul) == 1  # shared, no gate
+    assert lib.glq_moe_combine(nul, nul, nul, nul, nul, 0, 2048, 4, nul, nul) == 0
+    assert lib.glq_swiglu(nul, p, 16, p, nul) == 1
+    assert lib.glq_swiglu(nul, nul, 0, nul, nul) == 0
+
+
 def test_python_boundary_rejects_cpu_tensors():
     import torch
 
