@@ -203,6 +203,7 @@ class GraphCompatibleMoeBlock(nn.Module):
                     rows.append(int(id_maps[proj][key[1]]))
                 idx = torch.tensor(rows, dtype=torch.long, device=pools[proj].device)
                 t[f"U_{proj}"] = pools[proj].index_select(0, idx).contiguous()
+            _turbo_derived(t)
             return
         for proj in PROJS:
             if proj not in pools:
@@ -378,6 +379,7 @@ def _stack_turbo_block(blk) -> dict:
         out["shared_inter"], out["shared_gate_w"] = 0, None
     out["shared_bits"] = 0
     out["same_rot_gu"] = _same_rotation(out)
+    _turbo_derived(out)
     return out
 
 
@@ -409,7 +411,19 @@ def _turbo_from_problem(p: MoEProblem, d) -> dict:
     else:
         t["shared_inter"], t["shared_gate_w"] = 0, None
     t["same_rot_gu"] = _same_rotation(t)
+    _turbo_derived(t)
     return t
+
+
+def _turbo_derived(t: dict) -> None:
+    """Tensors the turbo step reads that follow from the block's own: Pi^T per
+    QR-rotated projection (x Pi^T as one fp16 GEMM with fp32 accumulation), and
+    the gate and up U stacked (one x U launch for both)."""
+    for proj in PROJS:
+        Pi = t[f"Pi_{proj}"]
+        t[f"PiT_{proj}"] = None if Pi is None else Pi.t().contiguous()
+    if t["rank"] > 0:
+        t["U_gu"] = torch.cat([t["U_gate"], t["U_up"]]).contiguous()
 
 
 def _same_rotation(t: dict) -> bool:
@@ -427,13 +441,15 @@ def _same_rotation(t: dict) -> bool:
 _route_ws: dict = {}
 
 
-def _rotate(x: torch.Tensor, signs, Pi) -> torch.Tensor:
-    """x_rot = fp16(RHT(x)) (one glq_rht launch) or fp16(x.float() @ Pi.float().T)
-    (a library GEMM, as the reference computes it, moe_block.py:352-356)."""
+def _rotate(x: torch.Tensor, signs, PiT) -> torch.Tensor:
+    """x_rot = fp16(RHT(x)) (one glq_rht launch) or x Pi^T as one library GEMM
+    of the fp16 operands with fp32 accumulation, rounded once to fp16 (the
+    reference's fp16(x.float() @ Pi.float().T), moe_block.py:352-356: the
+    products of fp16 values are exact in fp32 either way)."""
     from .kernels import _rht_eager
     if signs is not None:
         return _rht_eager(x, signs)
-    return (x.float() @ Pi.float().T).half()
+    return torch.matmul(x, PiT)
 
 
 def turbo_step(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.Tensor | None):
@@ -472,12 +488,13 @@ def turbo_step(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.Tensor 
             _lib.ptr(gate), y.data_ptr(), stream), "glq_turbo_moe_gemv")
 
     # 2. gate and up: x rotated once per configuration, x U once per cluster
-    xg = _rotate(h, t["signs_gate"], t["Pi_gate"])
-    xu_ = xg if t["same_rot_gu"] else _rotate(h, t["signs_up"], t["Pi_up"])
+    xg = _rotate(h, t["signs_gate"], t["PiT_gate"])
+    xu_ = xg if t["same_rot_gu"] else _rotate(h, t["signs_up"], t["PiT_up"])
     ag = au = None
     if r:
-        ag = _lowrank_xu_eager(h, t["U_gate"])  # (C, B, r)
-        au = _lowrank_xu_eager(h, t["U_up"])
+        agu = _lowrank_xu_eager(h, t["U_gu"])  # (Cg + Cu, B, r): gate's clusters, then up's
+        cg = t["U_gate"].shape[0]
+        ag, au = agu[:cg], agu[cg:]
     g = torch.empty(P, I, dtype=torch.float16, device=dev)
     gemv(xg, k, H, I, "gate", ag, t.get("cluster_gate"), B, 0 if ag is None else ag.shape[0] * B,
          None, g)
@@ -485,7 +502,7 @@ def turbo_step(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.Tensor 
     gemv(xu_, k, H, I, "up", au, t.get("cluster_up"), B, 0 if au is None else au.shape[0] * B,
          g, inter)
     # 3. down: inter rotated, each pick's own a_down = fp16(inter U_c)
-    xd = _rotate(inter, t["signs_down"], t["Pi_down"])
+    xd = _rotate(inter, t["signs_down"], t["PiT_down"])
     ad = None
     if r:
         ad = torch.empty(P, r, dtype=torch.float16, device=dev)
