@@ -452,10 +452,46 @@ def _rotate(x: torch.Tensor, signs, PiT) -> torch.Tensor:
     return torch.matmul(x, PiT)
 
 
+_side_streams: dict = {}
+
+
+def _side_stream(dev) -> torch.cuda.Stream:
+    """One side stream per device (default priority), for the shared expert."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    st = _side_streams.get(idx)
+    if st is None:
+        st = torch.cuda.Stream(device=dev)
+        _side_streams[idx] = st
+    return st
+
+
+def _turbo_shared_expert(t: dict, h: torch.Tensor, lib) -> torch.Tensor:
+    """down(fp16(silu(gate(h))) * up(h)) of the shared expert on the current
+    stream: its own GLoRCQLinear projections, or the problem's GPTQ weights."""
+    from .kernels import _packed_dequant_matmul_eager
+    if "shared_mods" in t:
+        mg, mu, md = t["shared_mods"]
+        sgo, suo = mg(h), mu(h)
+    else:
+        q = t["shared_q"]
+        sgo = _packed_dequant_matmul_eager(h, q["gate"][0], q["gate"][1], q["gate"][2],
+                                           q["gate"][3], 128)
+        suo = _packed_dequant_matmul_eager(h, q["up"][0], q["up"][1], q["up"][2],
+                                           q["up"][3], 128)
+    si = torch.empty_like(sgo)
+    _lib.check(lib.glq_swiglu(sgo.data_ptr(), suo.data_ptr(), si.numel(), si.data_ptr(),
+                              _lib.stream_handle(h.device)), "glq_swiglu")
+    if "shared_mods" in t:
+        return t["shared_mods"][2](si).contiguous()
+    q = t["shared_q"]
+    return _packed_dequant_matmul_eager(si, q["down"][0], q["down"][1], q["down"][2],
+                                        q["down"][3], 128)
+
+
 def turbo_step(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.Tensor | None):
     """One decode step of a TurboQuant block (<= TURBO_MAX_TOKENS tokens):
     (out (B, H) fp16, router logits (B, E) fp16)."""
-    from .kernels import _lowrank_xu_eager, _packed_dequant_matmul_eager, workspace
+    from .kernels import _lowrank_xu_eager, workspace
     lib = _lib.load()
     t = blk.t
     dev = h.device
@@ -463,6 +499,16 @@ def turbo_step(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.Tensor 
     E, k, I, r = blk.num_experts, blk.top_k, blk.inter, blk.rank
     P = B * k
     stream = _lib.stream_handle(dev)
+    # 0. the shared expert (routing-independent) on a side stream, overlapping
+    # the routed chain (the reference's side-stream overlap, moe_block.py:
+    # 661-700); the combine joins it
+    shared = side = None
+    if blk.shared_inter > 0:
+        cur = torch.cuda.current_stream(dev)
+        side = _side_stream(dev)
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            shared = _turbo_shared_expert(t, h, lib)
     # 1. routing on the device
     sel = torch.empty(P, dtype=torch.int32, device=dev)
     wts = torch.empty(P, dtype=torch.float16, device=dev)
@@ -515,27 +561,10 @@ def turbo_step(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.Tensor 
                    "glq_lowrank_xu_routed")
     yd = torch.empty(P, H, dtype=torch.float16, device=dev)
     gemv(xd, 1, I, H, "down", ad, None, 0, 0, None, yd)
-    # 4. the shared expert and the combine
-    shared = None
-    if blk.shared_inter > 0:
-        if "shared_mods" in t:
-            mg, mu, md = t["shared_mods"]
-            sgo, suo = mg(h), mu(h)
-        else:
-            q = t["shared_q"]
-            sgo = _packed_dequant_matmul_eager(h, q["gate"][0], q["gate"][1], q["gate"][2],
-                                               q["gate"][3], 128)
-            suo = _packed_dequant_matmul_eager(h, q["up"][0], q["up"][1], q["up"][2],
-                                               q["up"][3], 128)
-        si = torch.empty_like(sgo)
-        _lib.check(lib.glq_swiglu(sgo.data_ptr(), suo.data_ptr(), si.numel(), si.data_ptr(),
-                                  stream), "glq_swiglu")
-        if "shared_mods" in t:
-            shared = md(si).contiguous()
-        else:
-            q = t["shared_q"]
-            shared = _packed_dequant_matmul_eager(si, q["down"][0], q["down"][1], q["down"][2],
-                                                  q["down"][3], 128)
+    # 4. the combine, after the shared expert's stream has joined
+    if side is not None:
+        cur.wait_stream(side)
+        shared.record_stream(cur)
     out = torch.empty(B, H, dtype=torch.float16, device=dev)
     _lib.check(lib.glq_moe_combine(yd.data_ptr(), wts.data_ptr(), _lib.ptr(shared), sg.data_ptr(),
                                    _lib.ptr(res), B, H, k, out.data_ptr(), stream),
