@@ -93,11 +93,12 @@ __device__ __forceinline__ void t16_elem(int e, int rb, int& n, int& t) {
 
 // Src::bind() gives a view with codes(m), scales(m), zeros(m) (m = 0, or 0
 // and 1 with PAIR), xrow(t) (token t's activation row, t < M), prep(rb, s,
-// ks) (called by every thread of every slice workgroup before its block is
-// published; may hold barriers; what it writes for the finishing workgroup
-// must go out through handoff_put) and store(n, t, y) / PAIR store(n, t, y0,
-// y1), called for every output of the row block by the workgroup that
-// finishes it (reading prep's data through handoff_get).  All 512 threads of the workgroup
+// ks) (called by every thread of every slice workgroup once its loads are
+// issued, before its block is published; may hold barriers and use LDS past
+// t16_lds_bytes; what it writes for the finishing workgroup must go out
+// through handoff_put) and store(n, t, y) / PAIR store(n, t, y0, y1), called
+// for every output of the row block by the workgroup that finishes it
+// (reading prep's data through handoff_get).  All 512 threads of the workgroup
 // call t16_run (barriers inside).
 template <class Src, bool PAIR>
 __device__ void t16_run(const Src& srcs, const T16Geom& tg, int wg, float* lds) {
@@ -131,6 +132,9 @@ __device__ void t16_run(const Src& srcs, const T16Geom& tg, int wg, float* lds) 
 #pragma unroll
   for (int s = 0; s < 4; ++s) xv[s] = *(const f16x8*)(xr + 8 * s);
   __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the decode
+  // the view's own work for the block, while the codes are in flight (its
+  // first wait for its own loads covers theirs too)
+  src.prep(rb, sl, tg.ks);
 
   f16x8 xa[4];
 #pragma unroll
@@ -177,7 +181,6 @@ __device__ void t16_run(const Src& srcs, const T16Geom& tg, int wg, float* lds) 
 #pragma unroll
       for (int q = 0; q < EPT; ++q)
         handoff_put(pb + m * kT16Elems + tid + q * kT16Waves * 64, v[m][q]);
-    src.prep(rb, sl, tg.ks);
     __shared__ int last;
     if (!handoff_arrive(tg.cnt + rb, (unsigned)tg.ks, &last)) return;
     const float* p0 = tg.part + (int64_t)rb * tg.ks * M2 * kT16Elems;
@@ -192,8 +195,7 @@ __device__ void t16_run(const Src& srcs, const T16Geom& tg, int wg, float* lds) 
       }
     if (tid == 0) handoff_reset(tg.cnt + rb);
   } else {
-    src.prep(rb, 0, 1);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // prep's stores, for the store phase
     __syncthreads();
   }
 #pragma unroll
