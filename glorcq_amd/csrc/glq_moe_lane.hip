@@ -1,9 +1,11 @@
 // MoE block decode step for a few tokens (glq_moe_decode with tokens <=
 // kMoeLaneMaxB): GraphCompatibleMoeBlock.forward (inference/moe_block.py:
-// 381-436) on the lane-sliced GEMV of glq_lane.h, one token row per work item,
-// no cross-workgroup handshake inside any launch:
+// 381-436) on the lane-sliced GEMV of glq_lane.h, one token row per work item.
+// The only cross-workgroup handshakes are last-arriver handoffs (glq_handoff.h:
+// coherent stores and loads, no fence): a token's router rows over several
+// workgroups, and the K slices of the token-tile form.
 //
-//  1. moe_lane_route_kernel  one workgroup per token: router logits (fp32 dot
+//  1. moe_lane_route_kernel  workgroups per token: router logits (fp32 dot
 //                            products rounded to fp16 once), softmax, top-k
 //                            (ties to the lower index), optional
 //                            renormalisation (moe_block.py:386-392), the
@@ -27,8 +29,14 @@
 //  5. moe_lane_sdown_kernel  the shared expert's down rows, each row's store
 //                            combining out = fp16(sum_k w_k (y_k + a_down,k
 //                            SV_k^T) + gate * fp16(shared)) (+ the caller's
-//                            residual); without a shared expert
-//                            moe_lane_combine_kernel does the sum alone
+//                            residual); from 8 tokens
+//                            moe_lane_sdown_t16_kernel (token-tile form);
+//                            without a shared expert moe_lane_combine_kernel
+//                            does the sum alone
+//
+// The end of the file holds the pieces of a step whose routed experts are
+// TurboQuant layers (composed by glorcq_amd/moe_block.py): glq_moe_route (the
+// router alone), glq_moe_combine, glq_swiglu.
 //
 // Only the picked experts' weights are read, a pick's U once.  Every sum has
 // a fixed order, so the step gives the same bits on every run; routing and the
