@@ -83,7 +83,10 @@ struct MoeLaneArgs {
   float* agu;       // fp32 partial sums of a over K slices of kXuSlice codes:
                     // [2][P][S][rank] for each pick's gate and up, or (xuall)
                     // [2][C][B][S][rank] for every cluster's gate and up
-  int xuall;        // 1: a for every cluster in the router's launch
+  int xuall;        // a for every cluster in the router's launch: 1 by (matrix,
+                    // cluster, token, slice) jobs, 2 by (matrix, cluster, slice)
+                    // jobs over every token at once (moe_lane_xu_tile); 0: after
+                    // routing, per pick
   int su;           // K slices of gate/up (H), and of down (I)
   int sd;
   int kd, kdp;      // routed down: K parts of a row (one lane piece each), codes per part
@@ -107,6 +110,15 @@ struct MoeLaneArgs {
 };
 
 constexpr int kXuSlice = 512;  // codes per x U job
+constexpr int kXuTileStride = 68;  // halves per staged U row (moe_lane_xu_tile): 34 words,
+                                   // so the 4 row groups of a column read hit 4 bank groups
+constexpr int kXuTileMaxB = 16;    // tokens of a tile job (the MFMA's 16 rows)
+constexpr int kXuTileMaxRank = 64;
+
+// Workgroups of the router launch's x U jobs.
+__host__ __device__ inline int64_t moe_lane_nxu(int xuall, int C, int B, int su) {
+  return xuall == 1 ? 2ll * C * B * su : xuall == 2 ? 2ll * C * su : 0;
+}
 
 // Iterations of row loads in flight per wave: gate/up pairs; single rows of
 // np pieces a lane (fewer for several pieces, whose x slices hold registers).
@@ -482,6 +494,71 @@ __device__ void moe_lane_router(const MoeLaneArgs& a, int t, int q, unsigned cha
   }
 }
 
+// ---- x U of every token for one (matrix, cluster, K slice) by MFMA ----
+// job = (m C + c) su + s.  A = x (token rows, 16-byte loads), B = U: wave w
+// stages its 64 rows of the slice in LDS in two halves of 32 (row stride
+// kXuTileStride halves) and reads each B operand down the columns; the 8
+// waves' 16 x rank partial tiles are summed in LDS in wave order and written
+// as the slice partial of every token, the layout of the (cluster, token)
+// jobs (agu[((m C + c) B + t) su + s][j]).  LDS: 8 x 32 x kXuTileStride
+// halves, then 8 x 4 x 256 floats.  All 512 threads call it.
+__device__ void moe_lane_xu_tile(const MoeLaneArgs& a, int job, unsigned char* smem) {
+  const int s = job % a.su, mc = job / a.su, m = mc / a.C, c = mc - m * a.C;
+  const int row = moe_lane_clamp(a.uslot[m] ? a.uslot[m][c] : c, a.urows[m]);
+  const __half* u = a.U[m] + (int64_t)row * a.H * a.rank;
+  const int r = a.rank, r8 = r / 8, nct = (r + 15) / 16;
+  const int k0 = s * kXuSlice, kn = min(kXuSlice, a.H - k0);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, kb = lane >> 4;
+  __half* ul = (__half*)smem + wave * 32 * kXuTileStride;
+  f32x4 acc[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int h2 = 0; h2 < 2; ++h2) {
+    const int kr = 64 * wave + 32 * h2;  // slice row of the half's first row
+    // U rows [kr, kr + 32) of the slice (rows past H re-read row H - 1: they
+    // meet x = 0), 16-byte global loads, 8-byte LDS stores
+    for (int i = lane; i < 32 * r8; i += 64) {
+      const int rr = i / r8, pc = i - rr * r8;
+      const int k = min(k0 + kr + rr, a.H - 1);
+      const u32x4 v = *(const u32x4*)(u + (int64_t)k * r + 8 * pc);
+      uint2* d = (uint2*)(ul + rr * kXuTileStride + 8 * pc);
+      d[0] = uint2{v.x, v.y};
+      d[1] = uint2{v.z, v.w};
+    }
+    const int kk = kr + 8 * kb;
+    const f16x8 xv = (li < a.B && kk < kn) ? *(const f16x8*)(a.h + (int64_t)li * a.H + k0 + kk)
+                                           : f16x8{};
+    // the wave's LDS stores precede its reads (LDS ops of a wave run in order)
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      if (ct >= nct) break;  // uniform
+      const int col = ct * 16 + li;
+      f16x8 bv;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        bv[j] = col < r ? (_Float16)__half2float(ul[(8 * kb + j) * kXuTileStride + col])
+                        : (_Float16)0.f;
+      acc[ct] = mfma_16x16x32(xv, bv, acc[ct]);
+    }
+  }
+  __syncthreads();  // every wave is past its staging: the LDS becomes the reduction area
+  float* red = (float*)smem;  // [wave][ct][i][lane]
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[((wave * 4 + ct) * 4 + i) * 64 + lane] = acc[ct][i];
+  __syncthreads();
+  for (int e = tid; e < nct * 256; e += kMoeLaneThreads) {
+    const int ct = e >> 8, i = (e >> 6) & 3, l = e & 63;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) v += red[((w * 4 + ct) * 4 + i) * 64 + l];
+    const int t = 4 * (l >> 4) + i, col = ct * 16 + (l & 15);  // D: token row, rank column
+    if (t < a.B && col < r)
+      a.agu[((((int64_t)m * a.C + c) * a.B + t) * a.su + s) * r + col] = v;
+  }
+}
+
 // ---- kernels ----
 __device__ __forceinline__ int moe_lane_wave() {
   return (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -499,7 +576,11 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_route_kernel(MoeLane
     return;
   }
   b -= a.B * a.nrw;
-  const int nxu = a.xuall ? 2 * a.C * a.B * a.su : 0;
+  const int nxu = (int)moe_lane_nxu(a.xuall, a.C, a.B, a.su);
+  if (a.xuall == 2 && b < nxu) {
+    moe_lane_xu_tile(a, b, smem);
+    return;
+  }
   if (b < nxu) {  // job b = ((m C + c) B + t) su + s
     const int s = b % a.su, mct = b / a.su, t = mct % a.B, mc = mct / a.B;
     const int m = mc / a.C, c = mc - m * a.C;
@@ -663,7 +744,7 @@ struct MoeLanePlan {
   bool lora;
   int64_t off_sel, off_wts, off_sg, off_lgw, off_agu, off_inter, off_yb, off_ad, off_sinter,
       off_t16p, off_rtd, ws_need;
-  size_t lds_route, lds_xu, lds_comb, lds_sd16;
+  size_t lds_route, lds_xu, lds_xut, lds_comb, lds_sd16;
 };
 
 }  // namespace
@@ -788,10 +869,14 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   // picks after routing (measured on config 2: every pair wins at B <= 2,
   // the picks from B = 4)
   const int64_t ubytes = 2 * (int64_t)a.C * H * r * 2;
-  a.xuall = lora && ubytes <= kMoeLaneXuAllBytes && (int64_t)a.C * B <= kMoeLaneXuAllPairs &&
-                    !getenv("GLQ_MOE_LANE_XU_GATE")
-                ? 1
-                : 0;
+  const bool uall = lora && ubytes <= kMoeLaneXuAllBytes && !getenv("GLQ_MOE_LANE_XU_GATE");
+  a.xuall = 0;
+  if (uall && (int64_t)a.C * B <= kMoeLaneXuAllPairs) a.xuall = 1;
+  // from 8 tokens, one tile job per (matrix, cluster, slice) takes every token
+  // (measured on config 2: B = 8 65.2 -> 61.2 us, B = 16 82.6 -> 78.3 us; even
+  // at B = 4, where the picks' own jobs stay)
+  if (uall && B >= 8 && B <= kXuTileMaxB && r <= kXuTileMaxRank && !getenv("GLQ_MOE_NO_XU_TILE"))
+    a.xuall = 2;
   P.off_agu = take(4 * 2 * (int64_t)r * a.su * (a.xuall ? (int64_t)a.C * B : P_));
   P.off_inter = take(2 * (int64_t)P_ * I);
   P.off_yb = take(4 * (int64_t)a.kd * P_ * H);
@@ -805,6 +890,7 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   P.ws_need = o;
   P.lds_route = (size_t)(((2 * (a.E + 1) + 15) & ~15) + 4 * a.E + 4 * 16);
   P.lds_xu = lora ? (size_t)LaneXu(r).lds_bytes(r) : 0;
+  P.lds_xut = a.xuall == 2 ? (size_t)std::max(8 * 32 * kXuTileStride * 2, 8 * 4 * 256 * 4) : 0;
   P.lds_comb = (size_t)(4 * ((a.topk * r + 1) / 2) + 4 * a.rows_wg * (a.topk + 1));
   P.lds_sd16 = 0;
   if (a.t16d) {
@@ -819,8 +905,10 @@ template <int SBITS, int SLRP, int RC, bool T16>
 static int launch_route_t(const MoeLanePlan& P, hipStream_t s) {
   const MoeLaneArgs& a = P.a;
   const int64_t shared = T16 ? t16_wgs(a.gS16) : SBITS ? role_blocks(a.gSGU) : 0;
-  const int64_t grid = a.B * a.nrw + (a.xuall ? 2 * a.C * a.B * a.su : 0) + shared;
-  size_t lds = a.xuall ? std::max(P.lds_route, P.lds_xu) : P.lds_route;
+  const int64_t grid = a.B * a.nrw + moe_lane_nxu(a.xuall, a.C, a.B, a.su) + shared;
+  size_t lds = a.xuall == 1 ? std::max(P.lds_route, P.lds_xu)
+               : a.xuall == 2 ? std::max(P.lds_route, P.lds_xut)
+                              : P.lds_route;
   if (T16) lds = std::max(lds, (size_t)t16_lds_bytes(true));
   static size_t attr = 64 * 1024;
   int rc = set_lds_limit(moe_lane_route_kernel<SBITS, SLRP, RC, T16>, lds, attr);
