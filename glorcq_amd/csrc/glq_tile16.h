@@ -8,12 +8,13 @@
 // as columns), so each code is decoded once for every token; the lane form
 // (glq_lane.h) decodes it once per token.
 //
-//  * Workgroup (rb, s) takes rows [64 rb, 64 rb + 64) (four tiles) over K
+//  * Workgroup (rb, s) takes rows [32 rb, 32 rb + 32) (two tiles) over K
 //    slice s: groups [8 s, 8 s + 8), one group a wave.  A wave holds the x of
-//    every token over its group (16 VGPRs) and the codes of its group in all
-//    four tiles; per workgroup that is M x 1024 x 2 bytes of x against
-//    64 x 512 bytes of codes, so x (read from L2 by every row block) costs no
-//    more than the codes.
+//    every token over its group (16 VGPRs) and the codes of its group in both
+//    tiles; per workgroup that is M x 1024 x 2 bytes of x (from L2) against
+//    32 x 512 bytes of codes.  Four tiles a block halve the x reads but leave
+//    the chip fewer workgroups: config 2's shared expert at 16 tokens ran
+//    78.3 us a step with four, 75.5 with two.
 //  * Lane (li, kb) = (row li of a tile, 32-code quarter kb of the group)
 //    loads 16 bytes of codes per tile; the four 8-code dwords are the four
 //    MFMA steps (both operands take the same k order, so the sums are the
@@ -37,9 +38,10 @@
 namespace glq {
 
 constexpr int kT16Waves = 8;              // waves (K groups) a workgroup
-constexpr int kT16Tiles = 4;              // 16-row tiles a row block
+constexpr int kT16Tiles = 2;              // 16-row tiles a row block
 constexpr int kT16Rows = 16 * kT16Tiles;  // rows a row block
 constexpr int kT16Elems = kT16Rows * 16;  // outputs (rows x token rows) a block and matrix
+static_assert(kT16Elems % (kT16Waves * 64) == 0, "every thread takes whole outputs of a block");
 
 // LDS bytes: every wave's partial block of each matrix.
 __host__ __device__ constexpr int t16_lds_bytes(bool pair) {
@@ -71,7 +73,7 @@ __device__ __forceinline__ void t16_decode4(const u32x4& w, float z, const Decod
 }
 
 // Geometry of one token-tile role: N rows of K codes (G groups of 128), M <=
-// 16 token rows; RB row blocks of 64 rows, ks K slices of 8 groups; workgroup
+// 16 token rows; RB row blocks of kT16Rows rows, ks K slices of 8 groups; workgroup
 // wg = rb ks + s.  With ks > 1, part holds [RB][ks][matrices][kT16Elems]
 // partial blocks and cnt[RB] the arrival counters (zero between launches; the
 // last workgroup of a row block leaves its counter at zero).
@@ -84,7 +86,7 @@ struct T16Geom {
 };
 
 // Output element e of a block: tile j = e / 256, D index i, lane l -> token
-// row 4 (l / 16) + i, weight row 64 rb + 16 j + l % 16.
+// row 4 (l / 16) + i, weight row kT16Rows rb + 16 j + l % 16.
 __device__ __forceinline__ void t16_elem(int e, int rb, int& n, int& t) {
   const int l = e & 63;
   t = 4 * (l >> 4) + ((e >> 6) & 3);
