@@ -12,7 +12,7 @@
 //                            shared-expert gate sigmoid(fp16 logit); the other
 //                            workgroups run the shared expert's gate and up
 //                            rows in pairs and write its inter = fp16(fp16(
-//                            silu(g)) * u) (moe_block.py:465-468); from 8
+//                            silu(g)) * u) (moe_block.py:465-468); from 4
 //                            tokens in the token-tile form (glq_tile16.h)
 //  2. moe_lane_xu_kernel     (with LoRA) one workgroup per (pick, gate/up):
 //                            a = fp16(x U_c) of the pick's cluster (the
@@ -29,7 +29,7 @@
 //  5. moe_lane_sdown_kernel  the shared expert's down rows, each row's store
 //                            combining out = fp16(sum_k w_k (y_k + a_down,k
 //                            SV_k^T) + gate * fp16(shared)) (+ the caller's
-//                            residual); from 8 tokens
+//                            residual); from 4 tokens
 //                            moe_lane_sdown_t16_kernel (token-tile form);
 //                            without a shared expert moe_lane_combine_kernel
 //                            does the sum alone
@@ -258,7 +258,7 @@ struct SguTileSrc {
   const MoeLaneArgs& a;
   __device__ SguTileView bind() const { return SguTileView{a}; }
 };
-constexpr int kMoeT16MinB = 8;  // tokens from which the shared expert takes the tile form
+constexpr int kMoeT16MinB = 4;  // tokens from which the shared expert takes the tile form
 
 // Routed part of output rows [n0, n0 + nrows) of token t into LDS routed[]:
 // sum_k w_k (y_k[n] + a_down,k SV_down,k[n]^T), fmaf over the picks in pick
