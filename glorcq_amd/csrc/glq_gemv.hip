@@ -82,6 +82,7 @@ struct DenseSrc {
 }  // namespace glq
 
 #include "glq_lane.h"
+#include "glq_tile16.h"
 
 namespace glq {
 
@@ -115,6 +116,59 @@ struct LaneArgs {
   DenseArgs a;
   LaneGeom g;
 };
+
+// Item `item` of a dense launch in the token-tile form (glq_tile16.h: 4-bit
+// asymmetric codes, each decoded once for all M <= 16 token rows): y = Q(x)
+// + a SV^T + bias, a = fp16 of the x U partials' sum (DenseSrc::load_a),
+// staged in LDS by prep.
+struct DenseTileView {
+  const DenseArgs& a;
+  int item;
+  __half* al;  // LDS [M][rank]
+  __device__ DenseTileView bind() const { return *this; }
+  __device__ const uint32_t* codes(int) const { return a.codes + (int64_t)item * a.codes_es; }
+  __device__ const __half* scales(int) const { return a.scales + (int64_t)item * a.sz_es; }
+  __device__ const __half* zeros(int) const { return a.zeros + (int64_t)item * a.sz_es; }
+  __device__ const __half* xrow(int t) const {
+    return a.x + (int64_t)item * a.x_es + (int64_t)t * a.sh.K;
+  }
+  __device__ void prep(int, int, int) const {
+    const int r = a.sh.rank;
+    if (!a.sv) return;  // uniform over the workgroup
+    const DenseSrc d{a};
+    for (int i = threadIdx.x; i < a.M * r; i += kT16Waves * 64) {
+      const int t = i / r;
+      al[i] = d.load_a(item, t, i - t * r);
+    }
+    __syncthreads();
+  }
+  __device__ void store(int n, int t, float v) const {
+    if (a.sv) {
+      const int r = a.sh.rank;
+      const __half* sv = a.sv + (int64_t)item * a.sv_es + (int64_t)n * r;
+      const __half* at = al + t * r;
+      float l = 0.f;
+      for (int j = 0; j < r; j += 8) {
+        const u32x4 s8 = *(const u32x4*)(sv + j), a8 = *(const u32x4*)(at + j);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) l = dot2(s8[q], a8[q], l);
+      }
+      v += l;
+    }
+    if (a.bias) v += __half2float(a.bias[(int64_t)item * a.bias_es + n]);
+    a.y[(int64_t)item * a.y_es + (int64_t)t * a.sh.N + n] = __float2half(v);
+  }
+};
+
+// Workgroup b = item RB + row block: one K slice (GPW groups a wave cover the row).
+template <int GPW>
+__global__ __launch_bounds__(kT16Waves * 64) void gemv_t16_kernel(DenseArgs a, T16Geom tg) {
+  extern __shared__ __align__(16) float lds[];
+  const int item = blockIdx.x / tg.RB;
+  __half* al = (__half*)(lds + t16_lds_bytes(false) / 4);
+  t16_run<DenseTileView, false, GPW>(DenseTileView{a, item, al}, tg, blockIdx.x - item * tg.RB,
+                                     lds);
+}
 
 template <int BITS, bool SYM, int LRP, int PD, int NSV, bool HASB, bool XU>
 __global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) {
@@ -468,6 +522,42 @@ static int launch_lane(const DenseArgs& a, int bits, bool xu, hipStream_t s) {
   return bits == 2 ? launch_lane_bits<2>(la, xu, s) : launch_lane_bits<4>(la, xu, s);
 }
 
+// Token-tile form (glq_tile16.h) for 4..16 token rows of 4-bit asymmetric
+// group-128 codes whose rows fit one workgroup (K <= 4096: 8 waves of up to 4
+// groups), rank <= 128: each code decoded once for all the rows where the
+// streaming kernel decodes it once and takes a dot2 per row (VALU-bound
+// there).  Returns the groups a wave (1, 2, 4), or 0 when the form does not
+// apply.
+static int t16_gemv_gpw(int64_t M, const TileShape& sh, int bits) {
+  int minm = 4;
+  if (const char* e = getenv("GLQ_GEMV_T16_MINM")) minm = atoi(e);
+  if (getenv("GLQ_GEMV_NO_T16") || M < minm || bits != 4 || sh.sym || sh.zoff != 0.f ||
+      sh.group != 128 || sh.K % 128 != 0 || sh.rank > 128)
+    return 0;
+  const int G = sh.K / 128;
+  return G <= kT16Waves ? 1 : G <= 2 * kT16Waves ? 2 : G <= 4 * kT16Waves ? 4 : 0;
+}
+
+template <int GPW>
+static int launch_t16_gemv(const DenseArgs& a, hipStream_t s) {
+  T16Geom tg{};
+  tg.N = a.sh.N;
+  tg.K = a.sh.K;
+  tg.G = a.sh.G;
+  tg.kw = a.sh.kw;
+  tg.M = a.M;
+  tg.RB = (a.sh.N + kT16Rows - 1) / kT16Rows;
+  tg.ks = 1;
+  const size_t lds = (size_t)t16_lds_bytes(false) + 2 * (size_t)a.M * a.sh.rank;
+  static size_t attr = 64 * 1024;
+  int rc = set_lds_limit(gemv_t16_kernel<GPW>, lds, attr);
+  if (rc) return rc;
+  gemv_t16_kernel<GPW><<<dim3((unsigned)((int64_t)a.items * tg.RB)), dim3(kT16Waves * 64), lds,
+                         s>>>(a, tg);
+  GLQ_LAUNCH_CHECK("gemv_t16_kernel");
+  return GLQ_OK;
+}
+
 static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
                      int64_t K, int64_t N, const int32_t* codes,
                      int64_t codes_stride, int bits, const void* scales,
@@ -557,6 +647,10 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
     GLQ_LAUNCH_CHECK("lowrank_partial_kernel");
   }
   if (lane_shape(M, sh, bits)) return launch_lane(a, bits, false, s);
+  if (const int gpw = t16_gemv_gpw(M, sh, bits)) {
+    return gpw == 1 ? launch_t16_gemv<1>(a, s) : gpw == 2 ? launch_t16_gemv<2>(a, s)
+                                                            : launch_t16_gemv<4>(a, s);
+  }
   DenseStreamArgs sa;
   size_t slds = 0;
   bool sz2 = false;

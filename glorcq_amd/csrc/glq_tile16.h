@@ -1,5 +1,6 @@
 // Token-tile GEMV for a few token rows against the same weight rows (the
-// shared expert of a MoE step at 8..16 tokens): 4-bit group-128 codes,
+// shared expert of a MoE step from 4 tokens, the attention projections of a
+// decode step of 4..16 tokens): 4-bit group-128 codes,
 //
 //   y[t][n] = sum_g s[n,g] * sum_{k in g} fp16(q[n,k] - z[n,g]) x[t][k]
 //
@@ -9,7 +10,9 @@
 // (glq_lane.h) decodes it once per token.
 //
 //  * Workgroup (rb, s) takes rows [32 rb, 32 rb + 32) (two tiles) over K
-//    slice s: groups [8 s, 8 s + 8), one group a wave.  A wave holds the x of
+//    slice s: groups [8 s, 8 s + 8), one group a wave (GPW groups a wave:
+//    [8 GPW s, 8 GPW (s + 1)), whole rows of up to 8 GPW groups in one
+//    workgroup, no slices to sum).  A wave holds the x of
 //    every token over its group (16 VGPRs) and the codes of its group in both
 //    tiles; per workgroup that is M x 1024 x 2 bytes of x (from L2) against
 //    32 x 512 bytes of codes.  Four tiles a block halve the x reads but leave
@@ -73,7 +76,7 @@ __device__ __forceinline__ void t16_decode4(const u32x4& w, float z, const Decod
 }
 
 // Geometry of one token-tile role: N rows of K codes (G groups of 128), M <=
-// 16 token rows; RB row blocks of kT16Rows rows, ks K slices of 8 groups; workgroup
+// 16 token rows; RB row blocks of kT16Rows rows, ks K slices of 8 GPW groups; workgroup
 // wg = rb ks + s.  With ks > 1, part holds [RB][ks][matrices][kT16Elems]
 // partial blocks and cnt[RB] the arrival counters (zero between launches; the
 // last workgroup of a row block leaves its counter at zero).
@@ -102,7 +105,7 @@ __device__ __forceinline__ void t16_elem(int e, int rb, int& n, int& t) {
 // for every output of the row block by the workgroup that finishes it
 // (reading prep's data through handoff_get).  All 512 threads of the workgroup
 // call t16_run (barriers inside).
-template <class Src, bool PAIR>
+template <class Src, bool PAIR, int GPW = 1>
 __device__ void t16_run(const Src& srcs, const T16Geom& tg, int wg, float* lds) {
   constexpr int M2 = PAIR ? 2 : 1;
   const int rb = wg / tg.ks, sl = wg - rb * tg.ks;
@@ -111,55 +114,79 @@ __device__ void t16_run(const Src& srcs, const T16Geom& tg, int wg, float* lds) 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, kb = lane >> 4;
-  const int gw = sl * kT16Waves + wave;  // this wave's group
-  const bool gon = gw < tg.G;            // past G: x = 0, codes of group G - 1 (adds 0)
-  const int g = gon ? gw : tg.G - 1;
+  const int gw0 = (sl * kT16Waves + wave) * GPW;  // this wave's groups gw0 .. + GPW
+  bool gon[GPW];  // past G: x = 0, codes of group G - 1 (adds 0)
+  int g[GPW];
+#pragma unroll
+  for (int i = 0; i < GPW; ++i) {
+    gon[i] = gw0 + i < tg.G;
+    g[i] = gon[i] ? gw0 + i : tg.G - 1;
+  }
 
-  // ---- loads: the codes of the four tiles, then x; all in flight at once ----
-  u32x4 cw[M2][kT16Tiles];
-  __half sv[M2][kT16Tiles], zv[M2][kT16Tiles];
+  // ---- loads: the codes of the tiles, then x; all in flight at once ----
+  u32x4 cw[GPW][M2][kT16Tiles];
+  __half sv[GPW][M2][kT16Tiles], zv[GPW][M2][kT16Tiles];
 #pragma unroll
-  for (int m = 0; m < M2; ++m)
+  for (int i = 0; i < GPW; ++i)
 #pragma unroll
-    for (int j = 0; j < kT16Tiles; ++j) {
-      const int row = min(kT16Rows * rb + 16 * j + li, tg.N - 1);
-      cw[m][j] = *(const u32x4*)((const uint32_t*)src.codes(m) + (int64_t)row * tg.kw + 16 * g +
-                                 4 * kb);
-      sv[m][j] = src.scales(m)[(int64_t)row * tg.G + g];
-      zv[m][j] = src.zeros(m)[(int64_t)row * tg.G + g];
-    }
-  const bool xon = gon && li < tg.M;
-  const __half* xr = src.xrow(li < tg.M ? li : 0) + (int64_t)128 * g + 32 * kb;
-  f16x8 xv[4];
+    for (int m = 0; m < M2; ++m)
 #pragma unroll
-  for (int s = 0; s < 4; ++s) xv[s] = *(const f16x8*)(xr + 8 * s);
+      for (int j = 0; j < kT16Tiles; ++j) {
+        const int row = min(kT16Rows * rb + 16 * j + li, tg.N - 1);
+        cw[i][m][j] = *(const u32x4*)((const uint32_t*)src.codes(m) + (int64_t)row * tg.kw +
+                                      16 * g[i] + 4 * kb);
+        sv[i][m][j] = src.scales(m)[(int64_t)row * tg.G + g[i]];
+        zv[i][m][j] = src.zeros(m)[(int64_t)row * tg.G + g[i]];
+      }
+  const __half* xr0 = src.xrow(li < tg.M ? li : 0) + 32 * kb;
+  f16x8 xv[GPW][4];
+#pragma unroll
+  for (int i = 0; i < GPW; ++i)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xv[i][s] = *(const f16x8*)(xr0 + (int64_t)128 * g[i] + 8 * s);
   __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the decode
   // the view's own work for the block, while the codes are in flight (its
   // first wait for its own loads covers theirs too)
   src.prep(rb, sl, tg.ks);
 
-  f16x8 xa[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    // codes of a dword come decoded as 0,4,1,5,2,6,3,7
-    const f16x8 sh = __builtin_shufflevector(xv[s], xv[s], 0, 4, 1, 5, 2, 6, 3, 7);
-    xa[s] = xon ? sh : f16x8{};
-  }
-  const DecodeConsts dk = DecodeConsts::make();
+  // the wave's groups in order, each scaled, summed in fp32
+  f32x4 yv[M2][kT16Tiles];
 #pragma unroll
   for (int m = 0; m < M2; ++m)
 #pragma unroll
-    for (int j = 0; j < kT16Tiles; ++j) {
-      f16x8 b[4];
-      t16_decode4(cw[m][j], __half2float(zv[m][j]), dk, b);
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < kT16Tiles; ++j) yv[m][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const DecodeConsts dk = DecodeConsts::make();
 #pragma unroll
-      for (int s = 0; s < 4; ++s) acc = mfma_16x16x32(xa[s], b[s], acc);
-      const float sc = __half2float(sv[m][j]);
+  for (int i = 0; i < GPW; ++i) {
+    const bool xon = gon[i] && li < tg.M;
+    f16x8 xa[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      // codes of a dword come decoded as 0,4,1,5,2,6,3,7
+      const f16x8 sh = __builtin_shufflevector(xv[i][s], xv[i][s], 0, 4, 1, 5, 2, 6, 3, 7);
+      xa[s] = xon ? sh : f16x8{};
+    }
+#pragma unroll
+    for (int m = 0; m < M2; ++m)
+#pragma unroll
+      for (int j = 0; j < kT16Tiles; ++j) {
+        f16x8 b[4];
+        t16_decode4(cw[i][m][j], __half2float(zv[i][m][j]), dk, b);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = mfma_16x16x32(xa[s], b[s], acc);
+        const float sc = __half2float(sv[i][m][j]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) yv[m][j][q] = fmaf(sc, acc[q], yv[m][j][q]);
+      }
+  }
+#pragma unroll
+  for (int m = 0; m < M2; ++m)
+#pragma unroll
+    for (int j = 0; j < kT16Tiles; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        lds[((m * kT16Waves + wave) * kT16Tiles + j) * 256 + i * 64 + lane] = sc * acc[i];
-    }
+        lds[((m * kT16Waves + wave) * kT16Tiles + j) * 256 + i * 64 + lane] = yv[m][j][i];
   __syncthreads();
 
   // ---- the block: waves summed in order; thread tid takes elements tid + 512 q ----

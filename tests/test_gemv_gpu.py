@@ -423,3 +423,32 @@ def test_stream_forms(gpu, monkeypatch, ks, K, N, bits, M, items, bias):
     assert torch.equal(y, again)
     for e, p in enumerate(ps):
         assert_parity(y[e], oracle_y(p, bias=bs[e]), f"ks={ks} item {e}")
+
+
+@pytest.mark.parametrize("K,N,M,items", [(2048, 4096, 16, 1), (2048, 512, 8, 3), (4096, 2048, 16, 1),
+                                         (1024, 1408, 4, 2), (2048, 1400, 5, 1), (768, 2048, 6, 1)])
+def test_token_tile_path(gpu, monkeypatch, K, N, M, items):
+    """4-bit asymmetric codes at 4..16 token rows take the token-tile MFMA form
+    (glq_tile16.h via gemv_t16_kernel: each code decoded once for every row;
+    1, 2 or 4 groups a wave for K up to 1024, 2048, 4096; N = 1400 leaves a
+    ragged row block, K = 768 idle waves): against the oracle, with LoRA from
+    U (the partial-sum launch) and bias, with a precomputed xU, and against the
+    streaming kernel forced on the same inputs (GLQ_GEMV_NO_T16)."""
+    ps = [fmt.make_linear(K, N, bits=4, group=128, rank=64, M=M, seed=K + N + M + e)
+          for e in range(items)]
+    bias = (torch.randn(items, N, generator=torch.Generator().manual_seed(3)) * 0.1).half()
+    st = lambda k: torch.stack([getattr(p, k) for p in ps]).to(gpu)  # noqa: E731
+    args = (st("x"), st("codes"), st("scales"), st("zeros"), 4, 128)
+    monkeypatch.delenv("GLQ_GEMV_NO_T16", raising=False)
+    y = K_.packed_dequant_matmul_batched(*args, U=st("U"), SV=st("SV"), bias=bias.to(gpu))
+    y2 = K_.packed_dequant_matmul_batched(*args, U=st("U"), SV=st("SV"), bias=bias.to(gpu))
+    assert torch.equal(y, y2)
+    for e, p in enumerate(ps):
+        assert_parity(y[e], oracle_y(p, bias=bias[e]), f"tile form item {e}")
+    xu = torch.stack([p.x @ p.U for p in ps])
+    yx = K_.packed_dequant_matmul_batched(*args, SV=st("SV"), precomputed_xU=xu.half().to(gpu))
+    for e, p in enumerate(ps):
+        assert_parity(yx[e], oracle_y(p, xu=xu[e].half().float()), f"tile form xU item {e}")
+    monkeypatch.setenv("GLQ_GEMV_NO_T16", "1")
+    ys = K_.packed_dequant_matmul_batched(*args, U=st("U"), SV=st("SV"), bias=bias.to(gpu))
+    _check(y, ys.float(), "tile form vs streaming kernel")
