@@ -184,7 +184,8 @@ __global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) 
 template <int MC>
 __global__ __launch_bounds__(256) void lowrank_partial_kernel(DenseArgs a) {
   __shared__ float red[4 * 4 * 64];
-  __shared__ __half xl[16 * kLowrankRows];
+  __shared__ __align__(16) __half xl[16 * kLowrankRows];
+  __shared__ __align__(16) __half ut[MC == 4 ? 64 * kLowrankUtStride : 8];
   const int item = blockIdx.x / a.P, p = blockIdx.x - item * a.P;
   const __half* X = a.x + (int64_t)item * a.x_es;
   const int K = a.sh.K;
@@ -196,7 +197,7 @@ __global__ __launch_bounds__(256) void lowrank_partial_kernel(DenseArgs a) {
   }
   lowrank_partial<MC>(xrow, a.M, K, a.sh.rank, a.sh.rpad, a.u + ui * a.u_es, p,
                       (float*)a.apart + ((int64_t)item * a.P + p) * a.M * a.sh.rpad, red, xl,
-                      (int)threadIdx.x);
+                      (int)threadIdx.x, ut);
 }
 
 // a = fp16(sum over the P K-slices of the partials): items x M x rank.

@@ -235,6 +235,7 @@ __device__ __forceinline__ void load_batch(u32x4 (&wv)[NB][T], const uint32_t* C
 // columns 8*(tid&7) .. +8 of each 64-column block and rows k0 + (tid>>3) + 32i.
 // ---------------------------------------------------------------------------
 constexpr int kLowrankRows = 256;  // U rows per partial (K-slice)
+constexpr int kLowrankUtStride = kLowrankRows + 8;  // halves per staged U column (MC == 4)
 
 // `tid` is the thread's index in its group of 256 (a workgroup may run several
 // groups side by side, each with its own LDS; every group must make the same
@@ -246,44 +247,57 @@ __device__ void lowrank_partial(const XRow& xrow, int M, int K, int rank, int rp
                                 float* __restrict__ out /* M x rpad */,
                                 float* red /* LDS, 4*4*64 floats */,
                                 __half* xl /* LDS, 16 x kLowrankRows halves */,
-                                int tid) {
+                                int tid, __half* ut = nullptr /* LDS, MC == 4: 64 x
+                                                                  kLowrankUtStride halves */) {
   const int lane = tid & 63, wave = tid >> 6;
   const int j8 = tid & 7, kr = tid >> 3;  // kr in 0..31
   const int k0 = p * kLowrankRows;
   const int kl = min(kLowrankRows, K - k0);
   if constexpr (MC == 4) {
     // 3..16 token rows: one v_mfma_f32_16x16x32_f16 tile per 16 rank columns
-    // (A = the x slice, 16 rows staged in LDS with zeros past M; B = U
-    // straight from memory, lane = column, so the 16 lanes of a k row read
-    // 32 contiguous bytes), waves over the column tiles.
-    for (int idx = tid; idx < 16 * kLowrankRows; idx += 256) {
-      const int m = idx / kLowrankRows, k = idx - m * kLowrankRows;
-      xl[idx] = (m < M && k < kl) ? xrow(m)[k0 + k] : __float2half(0.f);
+    // (A = the x slice, 16 rows staged in LDS with zeros past M; B = a U
+    // column, from U's 64-column block staged transposed in LDS by 16-byte
+    // row loads), a wave per column tile.
+    for (int idx = tid; idx < 16 * (kLowrankRows / 8); idx += 256) {
+      const int m = idx / (kLowrankRows / 8), k = 8 * (idx - m * (kLowrankRows / 8));
+      const __half* xs = xrow(m) + k0 + k;
+      f16x8 v = {};
+      if (m < M && k + 8 <= kl && ((uintptr_t)xs & 15) == 0) {
+        v = *(const f16x8*)xs;
+      } else {  // a row end inside the chunk, or x not 16-byte aligned
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (m < M && k + e < kl) v[e] = (_Float16)__half2float(xs[e]);
+      }
+      *(f16x8*)(xl + m * kLowrankRows + k) = v;
     }
-    __syncthreads();
     const int li = lane & 15, kb = lane >> 4;
-    for (int ct = wave; ct * 16 < rpad; ct += 4) {
-      const int col = ct * 16 + li;
-      const bool cv = col < rank;
+    for (int jb = 0; jb < rpad; jb += 64) {
+      for (int idx = tid; idx < kLowrankRows * 8; idx += 256) {
+        const int k = idx >> 3, c = 8 * (idx & 7);
+        f16x8 v = {};
+        if (k < kl && jb + c < rank) v = *(const f16x8*)(U + (int64_t)(k0 + k) * rank + jb + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ut[(c + e) * kLowrankUtStride + k] = v[e];
+      }
+      __syncthreads();
+      const int cl = wave * 16 + li, col = jb + cl;  // 4 waves x 16 columns
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < kLowrankRows / 32; ++ks) {
         const int kk = 32 * ks + 8 * kb;
-        f16x8 bv;
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          bv[e] = (cv && kk + e < kl) ? (_Float16)__half2float(U[(int64_t)(k0 + kk + e) * rank + col])
-                                      : (_Float16)0.f;
-        acc = mfma_16x16x32(*(const f16x8*)(xl + li * kLowrankRows + kk), bv, acc);
+        acc = mfma_16x16x32(*(const f16x8*)(xl + li * kLowrankRows + kk),
+                            *(const f16x8*)(ut + cl * kLowrankUtStride + kk), acc);
       }
       // acc[i] = sum over the slice for token 4 kb + i, column col
       if (out && col < rpad) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int m = 4 * kb + i;
-          if (m < M) out[m * rpad + col] = cv ? acc[i] : 0.f;
+          if (m < M) out[m * rpad + col] = col < rank ? acc[i] : 0.f;
         }
       }
+      __syncthreads();  // the next block's staging overwrites ut
     }
     return;
   }
