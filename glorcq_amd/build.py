@@ -11,6 +11,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -19,7 +20,10 @@ LIB_DIR = PKG_DIR / "lib"
 LIB_PATH = LIB_DIR / "libglorcq_hip.so"
 ARCH = os.environ.get("GLQ_OFFLOAD_ARCH", "gfx950")
 
-# -packed-fp32-ops: hipcc may not emit packed fp32 VALU ops (v_pk_*_f32).
+# -packed-fp32-ops: the device pass may not emit packed fp32 VALU ops
+# (v_pk_add/mul/fma_f32).  hipcc hands the flag to the host pass too, which
+# warns that x86 has no such feature; the device pass honours it, and
+# check_no_packed_fp32() verifies every built code object after the link.
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -68,7 +72,49 @@ def build_library(verbose: bool = True, jobs: int = 8) -> Path:
     if out.returncode != 0:
         raise RuntimeError(f"link failed:\n{out.stdout}")
     os.replace(tmp, LIB_PATH)
+    check_no_packed_fp32(objs, verbose=verbose)
     return LIB_PATH
+
+
+PACKED_FP32 = ("v_pk_add_f32", "v_pk_mul_f32", "v_pk_fma_f32")
+
+
+def check_no_packed_fp32(objs, verbose: bool = True) -> None:
+    """Disassembles the gfx950 code object of each built object file and
+    fails the build if it holds a packed fp32 VALU instruction."""
+    llvm = Path("/opt/rocm/llvm/bin")
+    tools = [llvm / t for t in ("llvm-objcopy", "clang-offload-bundler", "llvm-objdump")]
+    if not all(t.exists() for t in tools):
+        print("[glorcq_amd.build] LLVM tools missing: packed-fp32 check skipped", flush=True)
+        return
+    objcopy, bundler, objdump = map(str, tools)
+    found = []
+    checked = 0
+    with tempfile.TemporaryDirectory() as tmpd:
+        for obj in objs:
+            fat = Path(tmpd) / (obj.stem + ".fatbin")
+            co = Path(tmpd) / (obj.stem + ".co")
+            dump = subprocess.run([objcopy, f"--dump-section=.hip_fatbin={fat}", str(obj),
+                                   str(Path(tmpd) / "discard.o")], stdout=subprocess.PIPE,
+                                  stderr=subprocess.STDOUT, text=True)
+            if dump.returncode != 0:
+                if "not found" in dump.stdout:
+                    continue  # host code only
+                raise RuntimeError(f"{obj.name}: {dump.stdout}")
+            checked += 1
+            subprocess.run([bundler, "--unbundle", "--type=o", f"--input={fat}",
+                            f"--targets=hipv4-amdgcn-amd-amdhsa--{ARCH}", f"--output={co}"],
+                           check=True)
+            dis = subprocess.run([objdump, "-d", str(co)], check=True, stdout=subprocess.PIPE,
+                                 text=True).stdout
+            n = sum(dis.count(op) for op in PACKED_FP32)
+            if n:
+                found.append(f"{obj.name}: {n}")
+    if found:
+        raise RuntimeError("packed fp32 VALU instructions in the device code: " + ", ".join(found))
+    if verbose:
+        print(f"[glorcq_amd.build] no packed fp32 VALU instructions in {checked} code objects",
+              flush=True)
 
 
 def _drain(procs):

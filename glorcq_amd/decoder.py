@@ -140,6 +140,7 @@ class GLoRCQQwen3Attention(nn.Module):
                                   sin.contiguous(), lay.keys, lay.values, lay.cumulative_length,
                                   self._len)
         if self._ws is None or self._ws_key != (tuple(lay.keys.shape), x.device):
+            kernels.retire_workspace(self._ws)  # a captured graph may still use it
             self._ws = kernels.decode_attention_workspace(qr, lay.keys)
             self._ws_key = (tuple(lay.keys.shape), x.device)
         a = kernels.decode_attention(qr, lay.keys, lay.values, self._len, self.scaling,

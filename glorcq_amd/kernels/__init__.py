@@ -27,6 +27,7 @@ a result always comes from the HIP kernels.
 from __future__ import annotations
 
 import logging
+import weakref
 
 import torch
 
@@ -38,6 +39,18 @@ logger = logging.getLogger(__name__)
 # workspace cache: (device index, stream handle) -> uint8 tensor.  Launches on
 # one stream run in order, so one buffer per stream is enough.
 _workspaces: dict = {}
+
+# Buffers a larger one has replaced.  A graph captured earlier holds the old
+# buffer's address in its kernel arguments, so the memory stays allocated for
+# the life of the process (growth doubles, so these add at most the final
+# size once more).
+_retired_workspaces: list = []
+
+
+def retire_workspace(ws) -> None:
+    """Keeps a replaced workspace buffer alive (see _retired_workspaces)."""
+    if ws is not None:
+        _retired_workspaces.append(ws)
 
 GEMV_MAX_M = 16
 
@@ -85,7 +98,8 @@ def _sym_mode(sym) -> int:
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Scratch for the x*U partial sums, one buffer per (device, current stream),
-    grown on demand (it needs no initialisation)."""
+    grown on demand (it needs no initialisation).  A replaced buffer is kept
+    alive, since a captured graph may still write into it."""
     dev = torch.device(device)
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
     key = (idx, _lib.stream_handle(dev))
@@ -94,6 +108,7 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         size = max(nbytes, 1 << 16)
         if ws is not None:
             size = max(size, 2 * ws.numel())
+        retire_workspace(ws)
         ws = torch.empty(size, dtype=torch.uint8, device=dev)
         _workspaces[key] = ws
     return ws
@@ -227,11 +242,13 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
     The packed-format counterpart of turbo_dequant_grouped_gemv_fused
     (inference/kernels/__init__.py:242-278), with the low-rank term fused.
     """
-    lib = _lib.load()
     _require(x, "x", torch.float16)
     _require(codes, "codes", torch.int32)
     _require(scales, "scales", torch.float16)
-    if _sym_mode(sym) != SYM_SIGNED:
+    asym = _sym_mode(sym) != SYM_SIGNED
+    if asym:
+        if zeros is None:
+            raise RuntimeError("zeros required for codes with zero-points")
         _require(zeros, "zeros", torch.float16)
     if x.dim() == 2:  # one x for every problem
         E, (M, K), x_stride = codes.shape[0], x.shape, 0
@@ -250,7 +267,7 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
     G = K // groupsize
     if tuple(scales.shape) != (E, N, G):
         raise RuntimeError(f"scales must be ({E}, {N}, {G})")
-    if not sym and tuple(zeros.shape) != (E, N, G):
+    if asym and tuple(zeros.shape) != (E, N, G):
         raise RuntimeError(f"zeros must be ({E}, {N}, {G})")
     rank = 0
     if SV is not None:
@@ -281,6 +298,7 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
     if E == 0 or M == 0 or N == 0:
         return out
     xu = precomputed_xU if SV is not None else None
+    lib = _lib.load()
     nbytes = lib.glq_gemv_workspace_bytes(E, M, K, N, rank if xu is None else 0)
     ws = workspace(x.device, nbytes)
     rc = lib.glq_gemv_lora_batched(
@@ -355,27 +373,38 @@ def _lowrank_xu_eager(x: torch.Tensor, U: torch.Tensor,
     return out
 
 
-def gptq_dequant_matmul_fused(x, qweight_int, scales, zeros, groupsize, sym=False,
-                              lora_USV=None, bits: int | None = None):
-    """Reference signature (inference/kernels/__init__.py:284): unpacked (N, K)
-    integer codes, fp16 scales/zeros, optional (U, S, V) low-rank tuple ->
-    fp16 (B, N).  W = q s (sym) or (q - z) s, q the codes as given (the
-    reference's int8 cast, gptq_matmul.cu:15-16, 81-82).
+# Prepared codes of gptq_dequant_matmul_fused: id(qweight_int) -> (weakref to
+# it, its key, code format, container bits, packed codes).  An entry lives as
+# long as its tensor and is valid while the tensor's storage, shape and
+# version counter are unchanged.
+_gptq_prepared: dict = {}
 
-    The reference casts the (N, K) int32 codes to int8 on every call; here they
-    are range-checked (one aminmax, a host sync) and packed on the device into
-    the narrowest container that holds them (2 or 4 bits, or the `bits`
-    given): unsigned asymmetric codes as they are, signed ones (symmetric, or
-    asymmetric like the reference's tests' codes in [-2, 2] with non-integer
-    zero-points) offset by 2^(b-1) with the zero-points applied exactly.
-    Codes that fit no 4-bit form raise.  Keep weights packed (GLoRCQLinear)
-    to avoid the per-call check and pack.
-    """
-    if bits is not None and bits not in (2, 4):
-        raise RuntimeError(f"{bits}-bit codes are not supported (2 or 4)")
-    q = qweight_int
-    if q.dim() != 2:
-        raise RuntimeError("qweight_int must be (N, K)")
+
+def _tensor_version(t: torch.Tensor) -> int:
+    try:
+        return t._version
+    except RuntimeError:  # inference tensors keep no version counter
+        return -1
+
+
+def _gptq_prepare(q: torch.Tensor, sym, groupsize: int, bits: int | None):
+    """(code format, container bits, packed codes) of the reference's (N, K)
+    integer codes, range-checked and packed once per tensor version.
+
+    The check reads min and max back to the host (a sync), so it runs outside
+    graph capture; a repeated call on the same codes reuses the result with
+    no sync and no device work, as the reference's op does under capture
+    (inference/quantized_linear.py:307-311 inside graph_wrapper.py:69-131)."""
+    key = (q.data_ptr(), _tensor_version(q), tuple(q.shape), q.dtype, q.device, bool(sym),
+           bits, groupsize)
+    ent = _gptq_prepared.get(id(q))
+    if ent is not None and ent[0]() is q and ent[1] == key:
+        return ent[2], ent[3], ent[4]
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(
+            "gptq_dequant_matmul_fused: these codes were not prepared before graph capture "
+            "(their range check reads back to the host); call it once on them outside the "
+            "capture, as a warm-up step does")
     lo, hi = (0, 0) if q.numel() == 0 else (int(v) for v in torch.aminmax(q))
     mode = None
     K = q.shape[1]
@@ -401,6 +430,36 @@ def gptq_dequant_matmul_fused(x, qweight_int, scales, zeros, groupsize, sym=Fals
     if mode == SYM_SIGNED_ZEROS:
         qi = qi + (1 << (b - 1))  # stored offset by 2^(b-1); z is applied as given
     codes = pack_codes_device(qi.contiguous(), b)
+    k = id(q)
+    ref = weakref.ref(q, lambda _r, k=k: _gptq_prepared.pop(k, None))
+    _gptq_prepared[k] = (ref, key, mode, b, codes)
+    return mode, b, codes
+
+
+def gptq_dequant_matmul_fused(x, qweight_int, scales, zeros, groupsize, sym=False,
+                              lora_USV=None, bits: int | None = None):
+    """Reference signature (inference/kernels/__init__.py:284): unpacked (N, K)
+    integer codes, fp16 scales/zeros, optional (U, S, V) low-rank tuple ->
+    fp16 (B, N).  W = q s (sym) or (q - z) s, q the codes as given (the
+    reference's int8 cast, gptq_matmul.cu:15-16, 81-82).
+
+    The reference casts the (N, K) int32 codes to int8 on every call; here
+    the first call on a codes tensor range-checks them (one aminmax, a host
+    sync) and packs them on the device into the narrowest container that
+    holds them (2 or 4 bits, or the `bits` given): unsigned asymmetric codes
+    as they are, signed ones (symmetric, or asymmetric like the reference's
+    tests' codes in [-2, 2] with non-integer zero-points) offset by 2^(b-1)
+    with the zero-points applied exactly.  Codes that fit no 4-bit form raise.
+    Later calls on the same, unmodified tensor reuse the packed codes with no
+    sync, so the op can be captured in a CUDA/HIP graph after one warm-up
+    call (a call under capture on codes never seen raises).
+    """
+    if bits is not None and bits not in (2, 4):
+        raise RuntimeError(f"{bits}-bit codes are not supported (2 or 4)")
+    q = qweight_int
+    if q.dim() != 2:
+        raise RuntimeError("qweight_int must be (N, K)")
+    mode, b, codes = _gptq_prepare(q, sym, groupsize, bits)
     xh = x.to(torch.float16).contiguous()
     U = SV = None
     if lora_USV is not None:

@@ -11,12 +11,13 @@ sit on the hot path's data (same names and meaning):
   is_regular_expert, is_shared_expert, extract_expert_info
                                      (utils/moe_utils.py:9-36)
 
-plus `load_glorcq_checkpoint` (the two .pt files, read with the safe loader)
-and `build_glorcq_layers`, the part of `_replace_linear_layers` (:335-433)
-that turns each stored module into a GLoRCQLinear, without building an HF
-model around it (the reference's meta-device HF model construction targets
-transformers 4.45 layouts; here the caller places the layers, e.g. into a
-GraphCompatibleMoeBlock).
+plus `load_glorcq_checkpoint` (the two .pt files, read with the safe loader),
+`build_glorcq_layers`, the part of `_replace_linear_layers` (:335-433) that
+turns each stored module into a GLoRCQLinear, and `load_glorcq_model`
+(:203-312), the one call from a checkpoint directory to a runnable causal LM:
+the HF model built on the meta device from config.json, the stored modules
+swapped in, every MoE block a GraphCompatibleMoeBlock over the stored experts,
+the cross-layer U pool installed.
 
 Differences: LoRA factors are dequantized on the GPU by the library's kernel
 (glq_dequant_factor, bit-identical to the reference's fp32 arithmetic + .half()),
@@ -27,9 +28,12 @@ reference's (K, rows*r) column layout is also returned for callers that use it.
 
 from __future__ import annotations
 
+import glob
 import os
+from types import SimpleNamespace
 
 import torch
+import torch.nn as nn
 
 from . import _lib
 from .hadamard_rotation import generate_rht_signs
@@ -39,7 +43,8 @@ __all__ = [
     "SharedUCache", "RotationCache", "_dequant_intN", "_unpack_int4", "_build_global_u_pool",
     "build_u_pool_stacks", "_install_global_u_pool",
     "_load_lora_for_module", "build_assignment_lookup", "load_glorcq_checkpoint",
-    "build_glorcq_layers", "is_regular_expert", "is_shared_expert", "extract_expert_info",
+    "build_glorcq_layers", "load_glorcq_model", "is_regular_expert", "is_shared_expert",
+    "extract_expert_info",
 ]
 
 
@@ -330,3 +335,212 @@ def build_glorcq_layers(model_data, cross_layer_info, device="cuda", rotation_ca
                                   device, sv_bits=sv_bits)
             out[layer_idx][name] = ql
     return out, u_cache
+
+
+# ---------------------------------------------------------------------------
+# Model loading (model_builder.py:203-312)
+# ---------------------------------------------------------------------------
+def _find_linear_modules(module, prefix=""):
+    """{dotted name: (parent, attribute, nn.Linear)} below `module`."""
+    out = {}
+    for name, child in module.named_children():
+        full = f"{prefix}.{name}" if prefix else name
+        if isinstance(child, nn.Linear):
+            out[full] = (module, name, child)
+        else:
+            out.update(_find_linear_modules(child, full))
+    return out
+
+
+def _dense_state(model_path):
+    """Tensors of any *.safetensors files in the checkpoint directory (the
+    non-quantized weights under their HF names), read with the safetensors
+    loader (no code runs from the file); {} when there are none."""
+    files = sorted(glob.glob(os.path.join(model_path, "*.safetensors")))
+    if not files:
+        return {}
+    from safetensors.torch import load_file
+
+    state = {}
+    for f in files:
+        state.update(load_file(f, device="cpu"))
+    return state
+
+
+_MOE_PROJ = {"gate_proj": "gate_proj", "up_proj": "up_proj", "down_proj": "down_proj",
+             "w1": "gate_proj", "w3": "up_proj", "w2": "down_proj"}
+
+
+def _stored_moe(mods):
+    """{block prefix: ({expert: {proj: GLoRCQLinear}}, {proj: shared GLoRCQLinear})}
+    of one layer's stored modules ('mlp.experts.<e>.gate_proj', Mixtral's
+    'block_sparse_moe.experts.<e>.w1', 'mlp.shared_expert.up_proj', ...)."""
+    blocks = {}
+    for name, ql in mods.items():
+        parts = name.split(".")
+        if "experts" in parts and not is_shared_expert(name):
+            i = parts.index("experts")
+            proj = _MOE_PROJ.get(parts[-1])
+            if proj is None or len(parts) != i + 3:  # <prefix>.experts.<e>.<proj>
+                continue
+            prefix = ".".join(parts[:i])
+            blocks.setdefault(prefix, ({}, {}))[0].setdefault(int(parts[i + 1]), {})[proj] = ql
+        elif is_shared_expert(name) and parts[-1] in _MOE_PROJ:
+            i = parts.index("shared_expert")
+            prefix = ".".join(parts[:i])
+            blocks.setdefault(prefix, ({}, {}))[1][_MOE_PROJ[parts[-1]]] = ql
+    return {k: v for k, v in blocks.items() if v[0]}
+
+
+def _get_submodule(root, dotted):
+    m = root
+    for part in dotted.split("."):
+        m = getattr(m, part, None)
+        if m is None:
+            return None
+    return m
+
+
+def _dense_weight(state, key, shape, device, dtype=torch.float16):
+    """The stored tensor of `key`, or zeros of `shape` when the checkpoint
+    holds none (the reference zero-fills every non-quantized parameter,
+    model_builder.py:416-428)."""
+    t = state.get(key)
+    if t is None:
+        return torch.zeros(shape, dtype=dtype, device=device)
+    if tuple(t.shape) != tuple(shape):
+        raise RuntimeError(f"{key}: stored shape {tuple(t.shape)} != model's {tuple(shape)}")
+    return t.to(device, dtype).contiguous()
+
+
+def _moe_block(config, hf_block, prefix, experts, shared, state, device):
+    """A GraphCompatibleMoeBlock over a layer's stored experts (reference
+    _replace_moe_blocks, model_builder.py:186-197, which wraps the HF block;
+    here the HF block's experts are fused 3-D tensors in transformers 5, so
+    the block is assembled from the stored GLoRCQLinear modules)."""
+    from .moe_block import GraphCompatibleMoeBlock
+
+    E = max(experts) + 1
+    if sorted(experts) != list(range(E)) or any(len(v) != 3 for v in experts.values()):
+        raise RuntimeError(f"{prefix}: the checkpoint must hold gate/up/down of experts 0..{E - 1}")
+    H = experts[0]["gate_proj"].in_features
+    top_k = int(getattr(config, "num_experts_per_tok", 2))
+    norm = getattr(config, "norm_topk_prob", None)
+    if norm is None:  # Mixtral renormalises its top-k weights
+        norm = getattr(config, "model_type", "") == "mixtral"
+    gate_key = f"{prefix}.gate.weight"
+    blk = SimpleNamespace(top_k=top_k, norm_topk_prob=bool(norm), num_experts=E)
+    blk.gate = SimpleNamespace(weight=_dense_weight(state, gate_key, (E, H), device))
+    blk.experts = [SimpleNamespace(**experts[e]) for e in range(E)]
+    if shared:
+        if len(shared) != 3:
+            raise RuntimeError(f"{prefix}: the shared expert needs gate/up/down")
+        blk.shared_expert = SimpleNamespace(**shared)
+        has_gate = _get_submodule(hf_block, "shared_expert_gate") is not None \
+            or f"{prefix}.shared_expert_gate.weight" in state
+        blk.shared_expert_gate = (SimpleNamespace(weight=_dense_weight(
+            state, f"{prefix}.shared_expert_gate.weight", (1, H), device)) if has_gate else None)
+    out = GraphCompatibleMoeBlock(blk)
+    out.return_router_logits = _moe_returns_router_logits()
+    return out
+
+
+def _moe_returns_router_logits() -> bool:
+    """transformers 4.x decoder layers unpack (states, router logits) from
+    their MoE block; 5.x blocks return the states alone."""
+    import transformers
+
+    return int(transformers.__version__.split(".")[0]) < 5
+
+
+def _materialize(model, config, state, device):
+    """Every parameter or buffer still on the meta device gets its stored
+    value from `state` (HF names) or zeros, as the reference does
+    (model_builder.py:316-333, 416-428); rotary embeddings are rebuilt on the
+    device from the config (zero inverse frequencies would switch rotary off)."""
+    for name, mod in list(model.named_modules()):
+        if type(mod).__name__.endswith("RotaryEmbedding") and any(
+                b.is_meta for b in mod.buffers(recurse=False)):
+            new = type(mod)(config=config).to(device)
+            parent = _get_submodule(model, name.rsplit(".", 1)[0]) if "." in name else model
+            setattr(parent, name.rsplit(".", 1)[-1], new)
+    for name, mod in model.named_modules():
+        for pname, p in list(mod.named_parameters(recurse=False)):
+            if p.is_meta:
+                key = f"{name}.{pname}" if name else pname
+                val = _dense_weight(state, key, p.shape, device, p.dtype)
+                setattr(mod, pname, nn.Parameter(val, requires_grad=False))
+        for bname, b in list(mod.named_buffers(recurse=False)):
+            if b.is_meta:
+                key = f"{name}.{bname}" if name else bname
+                mod.register_buffer(bname, _dense_weight(state, key, b.shape, device, b.dtype))
+
+
+def load_glorcq_model(model_path, device="cuda:0", rotation_cache=None):
+    """A GLoRCQ real-quantized checkpoint directory -> a causal LM on `device`
+    whose stored projections are GLoRCQLinear layers on the gfx950 kernels
+    (reference load_glorcq_model, inference/model_builder.py:203-312).
+
+    The directory holds config.json, glorcq_model.pt and cross_layer_info.pt
+    (read with torch's safe loader), and optionally *.safetensors files with
+    the non-quantized weights under their HF names (embeddings, norms, router
+    and shared-expert gates, attention biases, lm_head); what no file holds
+    is zero-filled, as the reference does for every non-quantized parameter.
+    Steps as the reference: the HF model on the meta device from the config
+    (built-in architectures only: no code from the directory runs), each
+    stored nn.Linear module replaced by its GLoRCQLinear with LoRA, each MoE
+    block with stored experts replaced by a GraphCompatibleMoeBlock, the
+    cross-layer U pool installed on every block, the rest materialised on
+    `device`.  TurboQuant modules need `rotation_cache` with their codebook
+    (the reference builds one from the quantizer package, absent here).
+    The result runs eagerly or under GLoRCQGraphWrapper."""
+    from transformers import AutoConfig, AutoModelForCausalLM
+
+    device = torch.device(device)
+    config = AutoConfig.from_pretrained(model_path)
+    config.use_cache = True
+    if not os.path.exists(os.path.join(model_path, "glorcq_model.pt")):
+        raise FileNotFoundError(
+            f"glorcq_model.pt not found in {model_path} (a fake-quant checkpoint loads with "
+            f"the standard HF loader)")
+    model_data, cross = load_glorcq_checkpoint(model_path)
+    mc = model_data.get("model_config", {})
+    if mc.get("use_turboquant", False) and rotation_cache is None:
+        raise RuntimeError("this checkpoint holds TurboQuant modules: pass a RotationCache "
+                           "with their codebook (and rotation)")
+    with torch.device("meta"):
+        model = AutoModelForCausalLM.from_config(config)
+    model = model.to(torch.float16)
+    model.seqlen = 4096
+    layers, u_cache = build_glorcq_layers(model_data, cross, device=device,
+                                          rotation_cache=rotation_cache)
+    state = _dense_state(model_path)
+    base = getattr(model, "model", model)
+    base_prefix = "model." if base is not model else ""
+    for li, layer in enumerate(base.layers):
+        mods = layers.get(li, {})
+        lp = f"{base_prefix}layers.{li}"
+        for prefix, (experts, shared) in _stored_moe(mods).items():
+            hf_block = _get_submodule(layer, prefix)
+            if hf_block is None:
+                raise RuntimeError(f"layer {li}: the model has no module {prefix!r}")
+            blk = _moe_block(config, hf_block, f"{lp}.{prefix}", experts, shared, state, device)
+            parent = _get_submodule(layer, prefix.rsplit(".", 1)[0]) if "." in prefix else layer
+            setattr(parent, prefix.rsplit(".", 1)[-1], blk)
+        for name, (parent, attr, lin) in _find_linear_modules(layer).items():
+            ql = mods.get(name)
+            if ql is None:
+                continue
+            if (ql.in_features, ql.out_features) != (lin.in_features, lin.out_features):
+                raise RuntimeError(f"layer {li} {name}: stored ({ql.out_features}, "
+                                   f"{ql.in_features}) != model's ({lin.out_features}, "
+                                   f"{lin.in_features})")
+            if lin.bias is not None and f"{lp}.{name}.bias" in state:
+                ql.set_bias(state[f"{lp}.{name}.bias"].to(torch.float16), device=device)
+            setattr(parent, attr, ql)
+    _materialize(model, config, state, device)
+    if getattr(config, "tie_word_embeddings", False) and hasattr(model, "lm_head"):
+        model.lm_head.weight = base.embed_tokens.weight
+    _install_global_u_pool(model, u_cache)
+    model.eval()
+    return model

@@ -43,6 +43,7 @@ import torch.nn as nn
 
 from . import _lib
 from .format import PROJS, MoEProblem
+from .kernels import retire_workspace
 
 _PROJ_ATTR = {"gate": "gate_proj", "up": "up_proj", "down": "down_proj"}
 
@@ -79,11 +80,13 @@ class GraphCompatibleMoeBlock(nn.Module):
         # alone, the contract of transformers 5 sparse-MoE blocks
         self.return_router_logits = True
         self.t = stacked  # device tensors (kept alive for the kernels)
-        # the prefill kernels take integer zero-points (GPTQ's are); checked
-        # once here, otherwise a prefill runs as consecutive decode steps
+        # the prefill kernels take integer zero-points (GPTQ's are), routed and
+        # shared alike; checked once here, otherwise a prefill runs as
+        # consecutive decode steps
+        zkeys = [f"zeros_{p}" for p in PROJS]
+        zkeys += [f"szeros_{p}" for p in PROJS if f"szeros_{p}" in stacked]
         self.zeros_integral = self.kind == "gptq" and all(
-            bool(torch.equal(stacked[f"zeros_{p}"], stacked[f"zeros_{p}"].round()))
-            for p in PROJS)
+            bool(torch.equal(stacked[k], stacked[k].round())) for k in zkeys)
 
     # ---- construction ----
     @staticmethod
@@ -518,6 +521,7 @@ def turbo_step(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.Tensor 
     key = (dev.index, stream)
     ws = _route_ws.get(key)
     if ws is None or ws.numel() < n:
+        retire_workspace(ws)  # a captured graph may still use it
         ws = torch.zeros(max(int(n), 256), dtype=torch.uint8, device=dev)  # counters start at zero
         _route_ws[key] = ws
     _lib.check(lib.glq_moe_route(h.data_ptr(), t["router_w"].data_ptr(),
@@ -641,7 +645,9 @@ def moe_decode_launch(h, router_w, shared_gate_w, codes, scales, zeros, U, clust
     ws = _moe_ws.get(key)
     if ws is None or ws.numel() < n:
         # zero-filled once: the router's arrival counter starts at zero and
-        # every step leaves it zero
+        # every step leaves it zero; a replaced buffer stays alive for the
+        # graphs captured with it
+        retire_workspace(ws)
         ws = torch.zeros(max(int(n), 256), dtype=torch.uint8, device=h.device)
         _moe_ws[key] = ws
     _lib.check(lib.glq_moe_decode(ctypes.byref(P), ws.data_ptr(), ws.numel(), stream),

@@ -325,8 +325,9 @@ int glq_moe_decode(const glq_moe_params* p, void* workspace, int64_t workspace_b
  * (inference/moe_block.py:704-740) -- every active expert's SwiGLU
  * projections on its gathered tokens -- with the same params as
  * glq_moe_decode and the decode step's routing and combine arithmetic.
- * tokens up to 2^20; routed codes must use integer zero-points (GPTQ
- * zero-points are integers; run glq_moe_decode steps otherwise).  Launches:
+ * tokens up to 2^20; routed and shared-expert codes must use integer
+ * zero-points (GPTQ zero-points are integers; the kernels use round(z), so
+ * run glq_moe_decode steps otherwise).  Launches:
  * router (+ x in the GEMMs' decode order), dispatch (pairs sorted by expert,
  * token tiles), the low-rank a = x U per pair, the grouped gate/up GEMM with
  * SwiGLU, the low-rank a of the down input, the grouped down GEMM, the

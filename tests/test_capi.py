@@ -234,3 +234,49 @@ def test_gptq_signature_range_checks_codes():
         kernels.gptq_dequant_matmul_fused(x, q, s, s, 128, False)
     with pytest.raises(RuntimeError, match="sym must be"):
         kernels._sym_mode(3)
+
+
+def test_batched_checks_zeros_shape_for_signed_codes_with_zeros(monkeypatch):
+    """Code format sym=2 (signed codes with zero-points) reads the zero-points,
+    so packed_dequant_matmul_batched checks their shape as for unsigned codes,
+    before any library call."""
+    import torch
+
+    from glorcq_amd import kernels
+
+    def dtype_only(t, name, dtype=None):
+        if dtype is not None and t.dtype != dtype:
+            raise RuntimeError(f"{name} must be {dtype}")
+
+    def no_library():
+        raise AssertionError("the library was reached")
+
+    monkeypatch.setattr(kernels, "_require", dtype_only)
+    monkeypatch.setattr(kernels._lib, "load", no_library)
+    E, M, K, N = 2, 1, 256, 16
+    x = torch.zeros(E, M, K, dtype=torch.float16)
+    codes = torch.zeros(E, N, K * 2 // 32, dtype=torch.int32)
+    s = torch.ones(E, N, K // 128, dtype=torch.float16)
+    bad = torch.zeros(E, N, 1, dtype=torch.float16)
+    for sym in (0, 2):
+        with pytest.raises(RuntimeError, match="zeros must be"):
+            kernels.packed_dequant_matmul_batched(x, codes, s, bad, 2, 128, sym=sym)
+        with pytest.raises(RuntimeError, match="zeros required"):
+            kernels.packed_dequant_matmul_batched(x, codes, s, None, 2, 128, sym=sym)
+
+
+def test_gptq_signature_refuses_unprepared_codes_under_capture(monkeypatch):
+    """Under graph capture the reference-signature op cannot range-check codes
+    it has not seen (that reads back to the host): it raises a clear error
+    before any device work instead of failing inside the capture."""
+    import torch
+
+    from glorcq_amd import kernels
+
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    x = torch.zeros(1, 128, dtype=torch.float16)
+    s = torch.ones(16, 1, dtype=torch.float16)
+    q = torch.zeros(16, 128, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="not prepared before graph capture"):
+        kernels.gptq_dequant_matmul_fused(x, q, s, s, 128, False)

@@ -16,7 +16,7 @@ from glorcq_amd import format as fmt
 from glorcq_amd.moe_block import GraphCompatibleMoeBlock
 from oracle import glorcq_oracle as O
 from test_moe_gpu import check_routing, margin
-from test_moe_oracle import bar, lora_heavy
+from test_moe_oracle import bar, lora_heavy, strict_report
 
 pytestmark = pytest.mark.gpu
 
@@ -35,3 +35,4 @@ def test_config3_decode(gpu, B, seed):
     ref = O.moe_forward(p)
     got = out.reshape(B, p.H).cpu()
     assert bar(got, ref), float((got.double() - ref).abs().max())
+    strict_report(p, got, ref, f"config 3 B={B}")

@@ -18,7 +18,7 @@ from glorcq_amd import _lib
 from glorcq_amd import format as fmt
 from glorcq_amd.moe_block import GraphCompatibleMoeBlock
 from oracle import glorcq_oracle as O
-from test_moe_oracle import bar, lora_heavy
+from test_moe_oracle import bar, lora_heavy, strict_report
 
 
 def margin(p):
@@ -110,6 +110,7 @@ def test_config2_parity(gpu, B, seed):
     check_routing(p, logits)
     ref = O.moe_forward(p)
     assert bar(out, ref), float((out.double() - ref).abs().max())
+    strict_report(p, out, ref, f"config 2 B={B}")
 
 
 @pytest.mark.gpu

@@ -43,6 +43,31 @@ def bar(y, ref, atol=1e-3, rtol=1e-2, rowtol=2e-3):
     return bool(ok.all())
 
 
+def strict_fraction(y, ref, atol=1e-3, rtol=1e-2):
+    """Fraction of outputs within the north star's bar alone, |y - ref| <=
+    atol + rtol |ref| (no row term); an output whose reference overflows fp16
+    counts as within when it is that inf."""
+    y = y.double()
+    ref = ref.double()
+    ref16 = ref.half().double()
+    inf = ~torch.isfinite(ref16)
+    ok = (y - ref).abs() <= atol + rtol * ref.abs()
+    ok = torch.where(inf, y == ref16, ok)
+    return float(ok.double().mean())
+
+
+def strict_report(p, out, ref, what):
+    """The strict-bar fraction of a GPU output beside that of the reference's
+    own fp16 CPU arithmetic (oracle.moe_forward(exact=False)) on the same
+    problem; the GPU step (fp32 accumulation) must do at least as well."""
+    mine = strict_fraction(out, ref)
+    fp16 = strict_fraction(O.moe_forward(p, exact=False), ref)
+    print(f"{what}: strict bar (atol 1e-3, rtol 1e-2) GPU {mine:.6f}, reference fp16 "
+          f"arithmetic {fp16:.6f}", flush=True)
+    assert mine >= fp16, (what, mine, fp16)
+    return mine, fp16
+
+
 def test_router_brute_force():
     p = small(B=6)
     logits, w, sel = O.route(p.h, p.router_w, p.top_k, False)

@@ -123,3 +123,21 @@ def test_non_integer_zeros_use_decode_steps(gpu):
     out, logits = blk(p.h.reshape(1, 100, p.H).to(gpu))
     torch.cuda.synchronize()
     check(p, out.reshape(100, p.H).cpu(), logits.cpu(), "non-integer zeros")
+
+
+def test_non_integer_shared_zeros_use_decode_steps(gpu):
+    """Non-integer zero-points on the shared expert only (the routed ones stay
+    integers): the block still takes decode steps, since the prefill GEMMs
+    use round(z) for the shared expert too, and stays within the bar."""
+    p = fmt.make_moe(H=256, E=8, inter=384, top_k=2, n_clusters=3, rank=16, shared_inter=512,
+                     B=100, seed=10)
+    g = torch.Generator().manual_seed(11)
+    for proj in fmt.PROJS:
+        z = p.shared[proj].zeros.float()
+        p.shared[proj].zeros = (z + 0.25 + torch.rand(z.shape, generator=g) * 0.5).half()
+    assert margin(p) >= 2
+    blk = GraphCompatibleMoeBlock.from_problem(p, gpu)
+    assert not blk.zeros_integral
+    out, logits = blk(p.h.reshape(1, 100, p.H).to(gpu))
+    torch.cuda.synchronize()
+    check(p, out.reshape(100, p.H).cpu(), logits.cpu(), "non-integer shared zeros")

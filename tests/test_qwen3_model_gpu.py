@@ -208,3 +208,99 @@ def test_batched_graph_decode_matches_eager(gpu):
     eager = torch.cat(toks, dim=1)
     torch.cuda.synchronize()
     assert torch.equal(out[:, 9:], eager), (out[:, 9:].tolist(), eager.tolist())
+
+
+def _twin_greedy_batch(twin, prompt, n):
+    """Greedy decode of every row of `prompt` (B, T) through the CPU twin:
+    (n lists of B tokens, n lists of B top-2 margins, the prompt's logits)."""
+    from transformers import DynamicCache
+
+    cache = DynamicCache()
+    logits = twin(input_ids=prompt, past_key_values=cache, use_cache=True, return_dict=False)[0]
+    first = logits.clone()
+    toks, margins = [], []
+    for i in range(n):
+        last = logits[:, -1]
+        top2 = torch.topk(last, 2, dim=-1).values
+        margins.append((top2[:, 0] - top2[:, 1]).tolist())
+        t = torch.argmax(last, dim=-1, keepdim=True)
+        toks.append(t[:, 0].tolist())
+        if i + 1 < n:
+            logits = twin(input_ids=t, past_key_values=cache, use_cache=True,
+                          return_dict=False)[0]
+    return toks, margins, first
+
+
+def _check_rows_against_twin(graph, twin_toks, margins, span, what):
+    """Row by row: the graph's tokens equal the twin's up to the first step
+    whose twin margin is below the fp16 pipeline's resolution (2 % of the
+    logit range); later tokens follow another prefix."""
+    matched = 0
+    for b in range(graph.shape[0]):
+        for i in range(graph.shape[1]):
+            if int(graph[b, i]) != twin_toks[i][b]:
+                assert margins[i][b] < 0.02 * span, \
+                    f"{what} row {b} step {i}: {int(graph[b, i])} vs twin {twin_toks[i][b]}, " \
+                    f"margin {margins[i][b]:.4f}"
+                break
+            matched += 1
+    return matched
+
+
+@torch.no_grad()
+def test_b16_graph_decode_matches_twin(gpu):
+    """BASELINE config 4's batch 16: sixteen prompts decoded together under
+    the graph (the MoE step's 16-token path, the token-tile attention
+    projections) against the twin decoding the same batch; the 16 x 12-token
+    prompt (192 tokens) runs the MoE prefill and the prefill GEMM."""
+    from glorcq_amd.graph_wrapper import _static_cache
+
+    model, twin = _build(gpu)
+    B, T, n = 16, 12, 8
+    prompt = torch.randint(0, VOCAB, (B, T), generator=torch.Generator().manual_seed(17))
+    wrapper = GLoRCQGraphWrapper(model, max_batch_size=B, max_seq_len=64)
+    out, _ = wrapper.generate(prompt.to(gpu), max_new_tokens=n)
+    graph = out[:, T:].cpu()
+    cache = _static_cache(model, B, 64, gpu, torch.float16)
+    first = model(input_ids=prompt.to(gpu), cache_position=torch.arange(T, device=gpu),
+                  past_key_values=cache, use_cache=True, return_dict=False)[0].float().cpu()
+    torch.cuda.synchronize()
+    print("B=16 graph decode done; running the twin", flush=True)
+    twin_toks, margins, twin_first = _twin_greedy_batch(twin, prompt, n)
+    span = float(twin_first.abs().max())
+    err = float((first - twin_first.float()).abs().max())
+    assert err <= 0.02 * span, (err, span)
+    matched = _check_rows_against_twin(graph, twin_toks, margins, span, "B=16")
+    print(f"B=16: {matched}/{B * n} tokens matched before any low-margin step; prompt "
+          f"logits max err {err:.4f} of {span:.3f}", flush=True)
+
+
+@torch.no_grad()
+def test_long_prompt_prefill_matches_twin(gpu):
+    """A 128-token prompt (BASELINE config 4's workload is a 512-token prompt):
+    the prefill runs the MoE block's grouped-GEMM path (glq_moe_prefill, more
+    than 64 tokens) and the attention projections' prefill GEMM (glq_gemm_lora,
+    more than 16 rows).  Every prompt position's logits within 2 % of the
+    twin's range, then greedy tokens under the graph equal the eager model's
+    and the twin's where the margin allows."""
+    model, twin = _build(gpu)
+    T, n = 128, 8
+    prompt = torch.randint(0, VOCAB, (1, T), generator=torch.Generator().manual_seed(19))
+    wrapper = GLoRCQGraphWrapper(model, max_batch_size=1, max_seq_len=256)
+    out, _ = wrapper.generate(prompt.to(gpu), max_new_tokens=n)
+    torch.cuda.synchronize()
+    graph_toks = out[0, T:].tolist()
+    eager_toks, eager_first, _ = _eager_greedy(model, prompt, n, gpu, 256)
+    torch.cuda.synchronize()
+    assert graph_toks == eager_toks, (graph_toks, eager_toks)
+    print("T=128 prefill + decode done; running the twin", flush=True)
+    twin_toks, margins, twin_first = _twin_greedy(twin, prompt, n)
+    span = float(twin_first.abs().max())
+    err = (eager_first - twin_first.float()).abs()
+    assert float(err.max()) <= 0.02 * span, (float(err.max()), span)
+    worst = int(err.amax(dim=-1).argmax())
+    matched = _check_rows_against_twin(torch.tensor([graph_toks]),
+                                       [[t] for t in twin_toks], [[m] for m in margins],
+                                       span, "T=128")
+    print(f"T=128: prompt logits max err {float(err.max()):.4f} of {span:.3f} (position "
+          f"{worst}); {matched}/{n} tokens matched", flush=True)

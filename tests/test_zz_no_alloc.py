@@ -1,7 +1,8 @@
 """The allocation-free GEMV entry point (glq_gemv_lora_noalloc, C ABI) gives the
-same bits as glq_gemv_lora with a caller workspace, on two calls in a row (the
-second with a smaller input, so a stale first-call scratch would show), and it
-rejects sizes beyond its static scratch on the host."""
+same bits as glq_gemv_lora with a caller workspace, on calls in a row (the
+second a smaller multi-row input whose x*U partials reuse the scratch, so a
+stale first-call scratch would show), and it rejects sizes beyond its static
+scratch on the host."""
 
 import pytest
 import torch
@@ -33,11 +34,15 @@ def _call_pair(lib, dev, p, stream):
 def test_noalloc_matches_workspace_entry_point(gpu):
     lib = _lib.load()
     stream = _lib.stream_handle(gpu)
-    # first call: config-1 down projection (K=1408) at M=8, rank 128; second:
-    # a smaller problem (M=1, K=512, rank 64) that reuses the same scratch
+    # first call: config-1 down projection (K=1408) at M=8, rank 128, whose
+    # x*U partials fill the static scratch; second: a smaller multi-row
+    # problem (M=4, K=512, rank 64) whose partials reuse the same scratch
+    # (a stale first-call partial would change its bits); third: one token
+    # row, which forms x*U inside its own launch and touches no scratch
     big = fmt.make_linear(1408, 2048, bits=2, rank=128, M=8, seed=71)
-    small = fmt.make_linear(512, 640, bits=4, rank=64, M=1, seed=72)
-    for p in (big, small):
+    small = fmt.make_linear(512, 640, bits=4, rank=64, M=4, seed=72)
+    single = fmt.make_linear(512, 640, bits=4, rank=64, M=1, seed=73)
+    for p in (big, small, single):
         print(f"noalloc case K={p.K} N={p.N} M={p.x.shape[0]} bits={p.bits} r={p.rank}",
               flush=True)
         y_ref, y_new = _call_pair(lib, gpu, p, stream)
