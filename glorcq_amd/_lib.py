@@ -70,6 +70,18 @@ SIGNATURES = {
         _vp, _i64,                      # y, y_stride
         _vp, _i64, _vp,                 # workspace, bytes, stream
     ]),
+    "glq_gemv_lora_clustered": (_c_int, [
+        _i64, _vp, _i64,                # items, x, x_stride
+        _i64, _i64, _i64,               # M, K, N
+        _vp, _i64, _c_int,              # codes, codes_stride, bits
+        _vp, _vp, _i64,                 # scales, zeros, sz_stride
+        _i64, _c_int,                   # group, sym
+        _vp, _i64, _vp, _i64,           # U, u_stride, u_index, n_u
+        _vp, _i64, _i64,                # SV, sv_stride, rank
+        _vp, _i64,                      # bias, bias_stride
+        _vp, _i64,                      # y, y_stride
+        _vp, _i64, _vp,                 # workspace, bytes, stream
+    ]),
     "glq_lowrank_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "glq_lowrank_xu_batched": (_c_int, [
         _i64, _vp, _i64, _i64, _i64,    # items, x, x_stride, M, K

@@ -46,6 +46,12 @@ struct DenseArgs {
   const int32_t* usel = nullptr;
   const int32_t* ucl = nullptr;
   int nsel = 0, nu = 0;
+  // item i's U is U + uidx[i] * u_es (null: U + i * u_es); nuidx U matrices
+  const int32_t* uidx = nullptr;
+  int nuidx = 0;
+  __device__ int64_t u_index(int item) const {
+    return uidx ? (int64_t)min(max(uidx[item], 0), nuidx - 1) : (int64_t)item;
+  }
 };
 
 // Item data of a dense launch: item i is at base + i * stride.
@@ -96,7 +102,7 @@ struct DenseLaneItem {
   __device__ const __half* zeros() const { return a.zeros + (int64_t)item * a.sz_es; }
   __device__ const __half* sv() const { return a.sv + (int64_t)item * a.sv_es; }
   __device__ const __half* bias() const { return a.bias + (int64_t)item * a.bias_es; }
-  __device__ const __half* u() const { return a.u + (int64_t)item * a.u_es; }
+  __device__ const __half* u() const { return a.u + a.u_index(item) * a.u_es; }
   __device__ u32x4 x8(int k) const { return *(const u32x4*)(a.x + (int64_t)item * a.x_es + k); }
   __device__ __half load_a(int j) const {
     if (a.xu) return a.xu[(int64_t)item * a.xu_es + j];
@@ -170,14 +176,14 @@ __global__ __launch_bounds__(kT16Waves * 64) void gemv_t16_kernel(DenseArgs a, T
                                      lds);
 }
 
-template <int BITS, bool SYM, int LRP, int PD, int NSV, bool HASB, bool XU>
+template <int BITS, bool SYM, int LRP, int NP, int PD, int NSV, bool HASB, bool XU>
 __global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) {
   extern __shared__ float xu_lds[];
   constexpr int WPB = XU ? 8 : 4;  // waves per workgroup
   const DenseLaneSrc src{la.a};
   const int wvb = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  lane_run<DenseLaneSrc, BITS, SYM, LRP, 1, PD, NSV, HASB, XU>(src, la.g, blockIdx.x * WPB + wvb,
-                                                               wvb, xu_lds);
+  lane_run<DenseLaneSrc, BITS, SYM, LRP, NP, PD, NSV, HASB, XU>(src, la.g, blockIdx.x * WPB + wvb,
+                                                                wvb, xu_lds);
 }
 
 
@@ -190,7 +196,7 @@ __global__ __launch_bounds__(256) void lowrank_partial_kernel(DenseArgs a) {
   const __half* X = a.x + (int64_t)item * a.x_es;
   const int K = a.sh.K;
   auto xrow = [&](int m) { return X + (int64_t)m * K; };
-  int64_t ui = item;
+  int64_t ui = a.u_index(item);
   if (a.usel) {
     const int e = min(max(a.usel[item], 0), a.nsel - 1);
     ui = min(max(a.ucl[e], 0), a.nu - 1);
@@ -422,13 +428,16 @@ static int launch_stream(const DenseStreamArgs& sa, int64_t items, int bits, boo
 }
 
 // Lane-sliced path (glq_lane.h): one token row, groups of whole 16-byte
-// pieces, a code row of at most 64 pieces, rank <= 128.
+// pieces, a code row of at most 128 pieces (two pieces a lane past 64: the
+// 4096-code rows of a 4-bit o projection), rank <= 128.
 constexpr int kLanePD = 4;              // iterations of loads in flight per wave
 constexpr int64_t kLaneWaves = 4096;    // target waves per launch (4 per SIMD)
+constexpr int kLaneMaxPieces = 128;
 
 static bool lane_row_shape(const TileShape& sh, int bits) {
   if (getenv("GLQ_GEMV_NO_LANE")) return false;
-  return sh.group % (128 / bits) == 0 && sh.rank <= 128 && (int64_t)sh.K * bits / 128 <= 64;
+  return sh.group % (128 / bits) == 0 && sh.rank <= 128 &&
+         (int64_t)sh.K * bits / 128 <= kLaneMaxPieces;
 }
 
 static bool lane_shape(int64_t M, const TileShape& sh, int bits) {
@@ -444,7 +453,7 @@ static size_t lane_xu_lds(const LaneArgs& la) {
   return (size_t)LaneXu(la.g.rank).lds_bytes(la.g.rank);
 }
 
-template <int BITS, bool SYM, int LRP, int NSV, bool HASB>
+template <int BITS, bool SYM, int LRP, int NP, int NSV, bool HASB>
 static int launch_lane_k(const LaneArgs& la, bool xu, hipStream_t s) {
   const int64_t waves = (int64_t)la.g.items * la.g.wpi;
   if (xu) {
@@ -452,14 +461,14 @@ static int launch_lane_k(const LaneArgs& la, bool xu, hipStream_t s) {
     GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
     const size_t lds = lane_xu_lds(la);
     static size_t attr = 64 * 1024;
-    int rc = set_lds_limit(gemv_lane_kernel<BITS, SYM, LRP, kLanePD, NSV, HASB, true>, lds, attr);
+    int rc = set_lds_limit(gemv_lane_kernel<BITS, SYM, LRP, NP, kLanePD, NSV, HASB, true>, lds, attr);
     if (rc) return rc;
-    gemv_lane_kernel<BITS, SYM, LRP, kLanePD, NSV, HASB, true>
+    gemv_lane_kernel<BITS, SYM, LRP, NP, kLanePD, NSV, HASB, true>
         <<<dim3((unsigned)grid), dim3(512), lds, s>>>(la);
   } else {
     const int64_t grid = (waves + 3) / 4;
     GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
-    gemv_lane_kernel<BITS, SYM, LRP, kLanePD, NSV, HASB, false>
+    gemv_lane_kernel<BITS, SYM, LRP, NP, kLanePD, NSV, HASB, false>
         <<<dim3((unsigned)grid), dim3(256), 0, s>>>(la);
   }
   GLQ_LAUNCH_CHECK("gemv_lane_kernel");
@@ -467,22 +476,23 @@ static int launch_lane_k(const LaneArgs& la, bool xu, hipStream_t s) {
 }
 
 // SV dwords per lane: rank / 2 spread over the LRP lanes of a row.
-template <int BITS, bool SYM, int LRP, bool HASB>
+template <int BITS, bool SYM, int LRP, int NP, bool HASB>
 static int launch_lane_sv(const LaneArgs& la, bool xu, hipStream_t s) {
   const int nsv = (la.g.rank / 2 + LRP - 1) / LRP;
-  if (nsv <= 1) return launch_lane_k<BITS, SYM, LRP, 1, HASB>(la, xu, s);
+  if (nsv <= 1) return launch_lane_k<BITS, SYM, LRP, NP, 1, HASB>(la, xu, s);
   if constexpr (LRP <= 32) {
-    if (nsv <= 2) return launch_lane_k<BITS, SYM, LRP, 2, HASB>(la, xu, s);
+    if (nsv <= 2) return launch_lane_k<BITS, SYM, LRP, NP, 2, HASB>(la, xu, s);
   }
-  if constexpr (LRP == 16) return launch_lane_k<BITS, SYM, LRP, 4, HASB>(la, xu, s);
+  if constexpr (LRP == 16) return launch_lane_k<BITS, SYM, LRP, NP, 4, HASB>(la, xu, s);
   GLQ_CHECK(false, "rank %d too large for the lane path", la.a.sh.rank);
 }
 
 template <int BITS, bool SYM, bool HASB>
 static int launch_lane_lrp(const LaneArgs& la, bool xu, hipStream_t s) {
-  if (la.g.lr <= 16) return launch_lane_sv<BITS, SYM, 16, HASB>(la, xu, s);
-  if (la.g.lr <= 32) return launch_lane_sv<BITS, SYM, 32, HASB>(la, xu, s);
-  return launch_lane_sv<BITS, SYM, 64, HASB>(la, xu, s);
+  if (la.g.lr <= 16) return launch_lane_sv<BITS, SYM, 16, 1, HASB>(la, xu, s);
+  if (la.g.lr <= 32) return launch_lane_sv<BITS, SYM, 32, 1, HASB>(la, xu, s);
+  if (la.g.lr <= 64) return launch_lane_sv<BITS, SYM, 64, 1, HASB>(la, xu, s);
+  return launch_lane_sv<BITS, SYM, 64, 2, HASB>(la, xu, s);
 }
 
 template <int BITS>
@@ -567,7 +577,8 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
                      int64_t sv_stride, int64_t rank, const void* xU,
                      int64_t xu_stride, const void* bias, int64_t bias_stride,
                      void* y, int64_t y_stride, void* workspace,
-                     int64_t workspace_bytes_given, void* stream) {
+                     int64_t workspace_bytes_given, void* stream,
+                     const int32_t* u_index = nullptr, int64_t n_u = 0) {
   clear_error();
   GLQ_CHECK(items >= 0 && M >= 0 && K >= 0 && N >= 0, "negative size");
   if (items == 0 || M == 0 || N == 0) return GLQ_OK;
@@ -588,7 +599,7 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
                      bits, scales, zeros, sz_stride, group, sym, U, u_stride, SV, sv_stride,
                      rank, xU ? (const __half*)xU + m * rank : nullptr, xu_stride, bias,
                      bias_stride, (__half*)y + m * N, y_stride, workspace,
-                     workspace_bytes_given, stream);
+                     workspace_bytes_given, stream, u_index, n_u);
       if (rc) return rc;
     }
     return GLQ_OK;
@@ -636,6 +647,8 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   a.P = need_partials && !lane_xu ? (int)lowrank_slices(K) : 0;
   a.tiles = (int)((N + 16 * T - 1) / (16 * T));
   a.sh = sh;
+  a.uidx = u_index;
+  a.nuidx = (int)std::min<int64_t>(n_u, 1 << 30);
 
   GLQ_CHECK(items * a.tiles < (1ll << 31) && items * a.P < (1ll << 31), "too many workgroups");
   hipStream_t s = (hipStream_t)stream;
@@ -773,6 +786,23 @@ int glq_gemv_lora_batched(int64_t items, const void* x, int64_t x_stride,
                    zeros, sz_stride, group, sym, U, u_stride, SV, sv_stride, rank,
                    xU, xu_stride, bias, bias_stride, y, y_stride, workspace,
                    workspace_bytes_given, stream);
+}
+
+int glq_gemv_lora_clustered(int64_t items, const void* x, int64_t x_stride, int64_t M,
+                            int64_t K, int64_t N, const int32_t* codes, int64_t codes_stride,
+                            int bits, const void* scales, const void* zeros, int64_t sz_stride,
+                            int64_t group, int sym, const void* U, int64_t u_stride,
+                            const int32_t* u_index, int64_t n_u, const void* SV,
+                            int64_t sv_stride, int64_t rank, const void* bias,
+                            int64_t bias_stride, void* y, int64_t y_stride, void* workspace,
+                            int64_t workspace_bytes_given, void* stream) {
+  clear_error();
+  GLQ_CHECK(u_index != nullptr && n_u >= 1, "u_index and n_u >= 1 required");
+  GLQ_CHECK(U != nullptr, "U required");
+  return gemv_impl(items, x, x_stride, M, K, N, codes, codes_stride, bits, scales, zeros,
+                   sz_stride, group, sym, U, u_stride, SV, sv_stride, rank, nullptr, 0, bias,
+                   bias_stride, y, y_stride, workspace, workspace_bytes_given, stream, u_index,
+                   n_u);
 }
 
 int64_t glq_lowrank_workspace_bytes(int64_t items, int64_t M, int64_t K, int64_t rank) {

@@ -8,10 +8,10 @@
 // With one token row a 16x16 MFMA tile wastes 15 of its 16 token columns,
 // and the MFMA time then exceeds the decode.  Here the wave's lanes own fixed
 // K slices instead:
-//  * a row of codes is K*bits/8 bytes = LR 16-byte pieces (LR <= 64); lanes
-//    are grouped by LRP = LR rounded up to 16, 32 or 64, so one wave
-//    iteration covers RPI = 64 / LRP rows, lane l holding piece l % LRP of row
-//    l / LRP.  Every load instruction of codes is 64 lanes x 16 bytes of
+//  * a row of codes is K*bits/8 bytes = LR 16-byte pieces (LR <= 64 NP, NP
+//    pieces a lane); lanes are grouped by LRP = LR rounded up to 16, 32 or
+//    64, so one wave iteration covers RPI = 64 / LRP rows, lane l holding
+//    piece l % LRP (+ j LRP) of row l / LRP.  Every load instruction of codes is 64 lanes x 16 bytes of
 //    consecutive rows -- contiguous when LR = LRP.
 //  * lane l's x slice (the 64 or 32 codes of its piece) lives in registers
 //    for the whole run of rows, already in the decode's operand order, with

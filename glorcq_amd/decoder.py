@@ -81,11 +81,12 @@ class GLoRCQQwen3Attention(nn.Module):
             for i, m in enumerate(lins):
                 m.U = self._U_qkv[i]  # the same values, now views of the stack
         # Decode tokens (up to 16): q, k and v as ONE batched GEMV launch
-        # (plus its x U partials) over items of kv_out rows -- q's rows as
-        # q_out/kv_out items, then k, then v -- with the three layers' codes,
-        # scales, zero-points and SV laid end to end (the layers keep views of
-        # them) and each item's U (q's repeated per q item); q comes out
-        # item-major, which the norm/rotary kernel reads as it is.
+        # (plus, from 2 tokens, its x U partials) over items of kv_out rows --
+        # q's rows as q_out/kv_out items, then k, then v -- with the three
+        # layers' codes, scales, zero-points and SV laid end to end (the layers
+        # keep views of them) and each item naming its U in the (3, K, r)
+        # stack (q's items share one, so one token forms x U_q once); q comes
+        # out item-major, which the norm/rotary kernel reads as it is.
         self._qkv = None
         q, k, v = lins
         nkv = k.out_features
@@ -101,7 +102,9 @@ class GLoRCQQwen3Attention(nn.Module):
                 setattr(q, name, full[:q.out_features])
                 setattr(k, name, full[q.out_features:q.out_features + nkv])
                 setattr(v, name, full[q.out_features + nkv:])
-            cat["U"] = torch.stack([q.U] * nq + [k.U, v.U]).contiguous()
+            cat["U"] = self._U_qkv
+            cat["u_index"] = torch.tensor([0] * nq + [1, 2], dtype=torch.int32,
+                                          device=self._U_qkv.device)
             self._qkv = cat
         self._len = None  # device int32: positions the step attends to
         self._ws = None   # decode attention workspace (counters stay zero between calls)
@@ -120,7 +123,8 @@ class GLoRCQQwen3Attention(nn.Module):
             c = self._qkv
             y = kernels.packed_dequant_matmul_batched(
                 x.contiguous(), c["codes"], c["scales"], c["zeros"], inner.q_proj.pack_bits,
-                inner.q_proj.gptq_groupsize, U=c["U"], SV=c["SV"])  # (items, B, kv rows)
+                inner.q_proj.gptq_groupsize, U=c["U"], SV=c["SV"],
+                u_index=c["u_index"])  # (items, B, kv rows)
             n = y.shape[0] - 2
             q, k, v = y[:n], y[n], y[n + 1]  # q item-major: the norm/rotary kernel reads it so
         elif self._U_qkv is not None and B <= kernels.GEMV_MAX_M:

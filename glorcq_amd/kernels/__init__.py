@@ -234,10 +234,14 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
                                   SV: torch.Tensor | None = None,
                                   bias: torch.Tensor | None = None,
                                   out: torch.Tensor | None = None,
-                                  precomputed_xU: torch.Tensor | None = None) -> torch.Tensor:
+                                  precomputed_xU: torch.Tensor | None = None,
+                                  u_index: torch.Tensor | None = None) -> torch.Tensor:
     """E independent problems in one launch: x (E, M, K), codes (E, N, Kw),
     scales/zeros (E, N, G), U (E, K, r), SV (E, N, r), bias (E, N) -> (E, M, N).
     A 2-D x (M, K) is the one input of every problem (x stride 0).
+
+    u_index (E,) int32 on the device: problem i uses U[u_index[i]] of U
+    (C, K, r) (cluster-shared U, glq_gemv_lora_clustered).
 
     The packed-format counterpart of turbo_dequant_grouped_gemv_fused
     (inference/kernels/__init__.py:242-278), with the low-rank term fused.
@@ -283,7 +287,12 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
             if U is None:
                 raise RuntimeError("LoRA needs U or precomputed_xU")
             _require(U, "U", torch.float16)
-            if tuple(U.shape) != (E, K, rank):
+            if u_index is not None:
+                _require(u_index, "u_index", torch.int32)
+                if tuple(u_index.shape) != (E,) or U.dim() != 3 or U.shape[0] < 1 \
+                        or tuple(U.shape[1:]) != (K, rank):
+                    raise RuntimeError(f"u_index must be ({E},) with U (C, {K}, {rank})")
+            elif tuple(U.shape) != (E, K, rank):
                 raise RuntimeError(f"U must be ({E}, {K}, {rank})")
     if bias is not None:
         _require(bias, "bias", torch.float16)
@@ -301,6 +310,15 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
     lib = _lib.load()
     nbytes = lib.glq_gemv_workspace_bytes(E, M, K, N, rank if xu is None else 0)
     ws = workspace(x.device, nbytes)
+    if u_index is not None and SV is not None and xu is None:
+        rc = lib.glq_gemv_lora_clustered(
+            E, x.data_ptr(), x_stride, M, K, N, codes.data_ptr(),
+            codes.shape[1] * codes.shape[2], bits, scales.data_ptr(), _lib.ptr(zeros),
+            scales.shape[1] * scales.shape[2], groupsize, _sym_mode(sym), U.data_ptr(), K * rank,
+            u_index.data_ptr(), U.shape[0], SV.data_ptr(), N * rank, rank, _lib.ptr(bias), N,
+            out.data_ptr(), M * N, ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device))
+        _lib.check(rc, "glq_gemv_lora_clustered")
+        return out
     rc = lib.glq_gemv_lora_batched(
         E, x.data_ptr(), x_stride, M, K, N, codes.data_ptr(), codes.shape[1] * codes.shape[2],
         bits, scales.data_ptr(), _lib.ptr(zeros), scales.shape[1] * scales.shape[2],

@@ -72,7 +72,7 @@ int64_t glq_gemv_workspace_bytes(int64_t items, int64_t M, int64_t K,
  * the LoRA tail of GLoRCQLinear.forward (inference/quantized_linear.py:338-349).
  *   bits      2 or 4;  K % group == 0;  group % 128 == 0, or any group of
  *             whole 16-byte pieces (a multiple of 128/bits codes) when a
- *             code row has at most 64 pieces and rank <= 128 (one lane-
+ *             code row has at most 128 pieces and rank <= 128 (one lane-
  *             kernel launch per token row: the reference's 64 x 64, group
  *             64 case, test_gptq_kernel.py:193)
  *   sym       0, 1 or 2 (code formats above)
@@ -133,6 +133,29 @@ int glq_gemv_lora_batched(int64_t items, const void* x, int64_t x_stride,
                           int64_t bias_stride, void* y, int64_t y_stride,
                           void* workspace, int64_t workspace_bytes,
                           void* stream);
+
+/*
+ * Batched form with cluster-shared U: item i reads U + u_index[i]*u_stride
+ * (u_index: `items` int32 on the device, each clamped to [0, n_u)), so one
+ * copy of a cluster's U serves every item of the cluster.  This is the
+ * reference's per-cluster U shared by the cluster's experts
+ * (_precompute_xU_for_experts, inference/moe_block.py:290-322; the same
+ * cluster fusion in _batched_proj_forward, moe_block.py:545-565), and it
+ * serves projections that share an input and a U (q, k and v of one layer
+ * cut into equal items).  Other arguments as glq_gemv_lora_batched; U and
+ * u_index are required, xU is not taken.
+ */
+int glq_gemv_lora_clustered(int64_t items, const void* x, int64_t x_stride,
+                            int64_t M, int64_t K, int64_t N,
+                            const int32_t* codes, int64_t codes_stride, int bits,
+                            const void* scales, const void* zeros,
+                            int64_t sz_stride, int64_t group, int sym,
+                            const void* U, int64_t u_stride,
+                            const int32_t* u_index, int64_t n_u, const void* SV,
+                            int64_t sv_stride, int64_t rank, const void* bias,
+                            int64_t bias_stride, void* y, int64_t y_stride,
+                            void* workspace, int64_t workspace_bytes,
+                            void* stream);
 
 /*
  * Low-rank factor a = fp16(x U) for `items` problems: x (M, K) fp16 at

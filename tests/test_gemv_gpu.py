@@ -15,6 +15,8 @@ outputs |y - y_ref| <= 1e-3 + 1e-2 |y_ref| (fp16 out, fp32 accumulate) against
 Every call goes through the C ABI (libglorcq_hip.so) via glorcq_amd.kernels.
 """
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -344,6 +346,51 @@ def test_lane_path_batched_items(gpu, monkeypatch):
                                          128, U=st("U"), SV=st("SV"))
     for e, p in enumerate(ps):
         assert_parity(y[e], oracle_y(p), f"item {e}")
+
+
+@pytest.mark.parametrize("bits,K,N,rank,sym", [
+    (4, 4096, 2048, 64, False),   # config-4 o projection: 128 pieces, two a lane
+    (2, 8192, 512, 128, True),    # 2-bit rows of 128 pieces, rank 128, symmetric codes
+    (4, 2560, 320, 64, False),    # 80 pieces: the second piece live on 16 of 64 lanes
+])
+def test_lane_two_pieces_a_lane(gpu, monkeypatch, bits, K, N, rank, sym):
+    """Code rows of 65..128 16-byte pieces on the one-token-row kernel, two
+    pieces a lane (NP = 2), with a = x U formed in the launch; against the
+    oracle and the streaming kernel forced on the same inputs."""
+    p = fmt.make_linear(K, N, bits=bits, rank=rank, M=1, seed=K + 7 * N + bits, sym=sym)
+    d = to(p, gpu)
+    zeros = None if sym else d["zeros"]
+    y = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], zeros, bits, 128,
+                                       sym=sym, U=d["U"], SV=d["SV"])
+    assert_parity(y, oracle_y(p), f"two pieces a lane K={K} N={N}")
+    monkeypatch.setenv("GLQ_GEMV_NO_LANE", "1")
+    ys = K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], zeros, bits, 128,
+                                        sym=sym, U=d["U"], SV=d["SV"])
+    assert_parity(ys, oracle_y(p), "stream kernel, same inputs")
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_clustered_u_index(gpu, M):
+    """q, k and v of one layer as ten items sharing x (glq_gemv_lora_clustered):
+    items 0..7 name U 0, items 8 and 9 name U 1 and 2.  The same bits as the
+    batched call with each item's U copied out, and parity per item."""
+    K, N, r, bits = 2048, 512, 64, 4
+    ps = [fmt.make_linear(K, N, bits=bits, rank=r, M=M, seed=900 + i) for i in range(10)]
+    x = ps[0].x
+    Us = torch.stack([ps[0].U, ps[8].U, ps[9].U])
+    uidx = [0] * 8 + [1, 2]
+    st = lambda k: torch.stack([getattr(p, k) for p in ps]).to(gpu)  # noqa: E731
+    args = (x.to(gpu), st("codes"), st("scales"), st("zeros"), bits, 128)
+    y = K_.packed_dequant_matmul_batched(*args, U=Us.to(gpu), SV=st("SV"),
+                                         u_index=torch.tensor(uidx, dtype=torch.int32,
+                                                              device=gpu))
+    ycopy = K_.packed_dequant_matmul_batched(*args, U=Us[uidx].contiguous().to(gpu),
+                                             SV=st("SV"))
+    torch.cuda.synchronize()
+    assert torch.equal(y, ycopy)
+    for i, p in enumerate(ps):
+        q = dataclasses.replace(p, x=x, U=Us[uidx[i]])
+        assert_parity(y[i], oracle_y(q), f"item {i}")
 
 
 @pytest.mark.parametrize("bits", [2, 4])
