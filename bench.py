@@ -406,6 +406,43 @@ def bench_moe(dev, seed=6, reps=20, trials=15):
     return res
 
 
+def bench_moe_cold(dev, seed=6, copies=8, rounds=3, trials=9):
+    """Config 2's decode step with cold caches: `copies` distinct copies of the
+    block (each about 200 MB, 1.6 GB in all: more than twice the L2s and the
+    256 MB Infinity Cache together) stepped in turn inside one hipGraph, so
+    no step finds its weights left in a cache by the step before; the same
+    routing and bytes as bench_moe's warm figure, which replays one block."""
+    import torch
+
+    from glorcq_amd import format as fmt
+    from glorcq_amd.moe_block import GraphCompatibleMoeBlock
+
+    res = {}
+    for B in MOE_BATCHES:
+        p = fmt.make_moe(B=B, seed=seed)
+        blks = [GraphCompatibleMoeBlock.from_problem(p, dev) for _ in range(copies)]
+        h = p.h.reshape(1, B, p.H).to(dev)
+        _, logits = blks[0](h)
+
+        def rotate():
+            for b in blks:
+                b(h)
+
+        us = _graph_step_us(rotate, rounds, trials) / copies
+        sel = torch.topk(logits.float().cpu(), p.top_k, dim=-1).indices
+        act = sorted(set(sel.flatten().tolist()))
+        clusters = {proj: len({int(p.cluster_of[proj][e]) for e in act}) for proj in fmt.PROJS}
+        nbytes = fmt.moe_step_bytes(p, len(act), clusters)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[str(B)] = {"us_per_step": round(us, 2), "us_per_token": round(us / B, 3),
+                       "algorithmic_bytes": nbytes, "achieved_GBps": round(gbs, 1),
+                       "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"moe cold B={B}: {us:.2f} us/step, {us / B:.3f} us/token, {gbs:.0f} GB/s")
+        del blks
+        torch.cuda.empty_cache()
+    return res
+
+
 def bench_moe_turbo(dev, seed=6, reps=10, trials=9):
     """Config 2's block with TurboQuant routed experts (the reference's 2-bit
     expert format; format.make_turbo_moe: gate/up rotated by an RHT, down by a
@@ -644,6 +681,16 @@ def main():
         kernels.packed_dequant_matmul_batched(x, codes, scales, zeros, BITS, GROUP, U=U, SV=SV,
                                               out=out)
 
+    # The step's one kernel, HIP events on the launch stream (the roofline
+    # figure).  It runs first: the device's first passes over a fresh 2.6 GB
+    # pool are slower than its steady state (about 450 against 417 us a step
+    # for the first 25 steps on an MI355X), so the timed step loop below does
+    # not start on a device that has only just allocated the pool.
+    log("timing the fused kernel with HIP events")
+    k_ms = time_events(step, args.steps, max(args.warmup, 25))
+    k_bytes = layer_bytes() * args.pool
+    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
+
     log("timing steps (one fused launch over the pool)")
     for _ in range(args.warmup):
         step()
@@ -654,12 +701,6 @@ def main():
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     gbs = layer_bytes() * args.pool / (ms * 1e-3) / 1e9
-
-    # the step's one kernel, HIP events on the launch stream
-    log("timing the fused kernel with HIP events")
-    k_ms = time_events(step, args.steps, args.warmup)
-    k_bytes = layer_bytes() * args.pool
-    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
 
     # the GEMV fed a precomputed a = x*U (the separate-launch form)
     xu = kernels.lowrank_xu(x, U)
@@ -736,8 +777,18 @@ def main():
             "workload": ("config 2: Qwen1.5-MoE-A2.7B block (H 2048, 60 experts, inter 1408, "
                          "top-4, 2-bit g128 routed experts with rank-64 LoRA, U shared over 16 "
                          "clusters, 4-bit shared expert inter 5632), seed 6, one hipGraph of 20 "
-                         "steps per replay"),
+                         "steps per replay of ONE block: warm caches (its weights stay in the "
+                         "256 MB Infinity Cache between steps)"),
             "by_batch": moe}
+        log("MoE block decode step (config 2), cold caches: 8 block copies in turn")
+        cold = bench_moe_cold(dev)
+        result["moe_block_decode_cold_us_per_token"] = {b: v["us_per_token"]
+                                                        for b, v in cold.items()}
+        result["moe_block_decode_cold"] = {
+            "workload": ("config 2 as moe_block_decode, 8 distinct copies of the block "
+                         "(1.6 GB) stepped in turn inside one hipGraph: cold L2 and "
+                         "Infinity Cache"),
+            "by_batch": cold}
         log("Mixtral-shaped MoE layer (config 3): decode steps and a prefill")
         result["mixtral_layer"] = bench_mixtral(dev)
         log("config 2 block with TurboQuant routed experts")

@@ -58,8 +58,10 @@ constexpr int kMoeLaneMaxB = 16;
 // The header holds arrival counters, zero between steps: word 0 (the
 // many-token router), bytes 64 .. 255 (the lane path's per-token router
 // counters), bytes 1024 .. 2559 and 2560 .. 4095 (the lane path's token-tile
-// row-block counters of the shared gate/up and the shared down).
-constexpr int64_t kMoeWsHeader = 4096;
+// row-block counters of the shared gate/up and the shared down), bytes 4096
+// .. 8191 (the lane path's (token, row block) combine counters).
+constexpr int64_t kMoeWsHeader = 8192;
+constexpr int kMoeCombineCnt = 1024;
 constexpr int kMoeT16MaxRB = 384;  // row blocks a token-tile role may count
 int64_t moe_lane_workspace_bytes(const glq_moe_params* p);
 int moe_lane_decode(const glq_moe_params* p, void* workspace, int64_t workspace_bytes,

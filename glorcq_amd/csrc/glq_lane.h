@@ -29,6 +29,8 @@
 // fp32 summation order.
 #pragma once
 
+#include <type_traits>
+
 #include "glq_gemv_core.h"
 
 namespace glq {
@@ -194,6 +196,35 @@ __device__ __half* lane_xu_phase(const View& src, int K, int rank, bool lora, fl
   return ah;
 }
 
+// Item types may issue the loads of a before the x slice's wait
+// (a_issue(j, v) / a_issue(m, j, v) with PAIR: up to kLaneEarlyA fp32 partials
+// of a[j] into v, zeros past them, and a_count() of them); lane_run then sums
+// them after that wait, in sum_strided's order, so one memory round trip
+// covers the rows' first loads, x and a.
+constexpr int kLaneEarlyA = 4;
+template <class T, class = void>
+struct lane_early_a : std::false_type {};
+template <class T>
+struct lane_early_a<T, std::void_t<decltype(&T::a_count)>> : std::true_type {};
+// Item types may also have after_issue(): work of the whole workgroup (it may
+// hold barriers) run by every wave right after its rows' first loads are
+// issued, so its own loads share their round trip.  Waves without rows of
+// their own take part too.
+template <class T, class = void>
+struct lane_hook : std::false_type {};
+template <class T>
+struct lane_hook<T, std::void_t<decltype(&T::after_issue)>> : std::true_type {};
+
+// sum_strided's sum of n <= kLaneEarlyA loaded partials (its zeros included)
+__device__ __forceinline__ float lane_early_sum(const float (&v)[kLaneEarlyA]) {
+  float s = 0.f;
+#pragma unroll
+  for (int u = 0; u < kLaneEarlyA; ++u) s += v[u];
+#pragma unroll
+  for (int u = kLaneEarlyA; u < 8; ++u) s += 0.f;
+  return s;
+}
+
 // Geometry of one lane launch (or one role of a launch): every item has N
 // rows of K codes; rows are cut into 64-row units of NIT = LRP iterations,
 // taken in rounds of PD iterations; wave w of an item runs rounds
@@ -248,7 +279,8 @@ __device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, in
   // rounds rb .. rb + nr - 1 of PD iterations each, [PD R, PD R + PD)
   const int rb = (wv - item * lg.wpi) * lg.rpw;
   const int nr = min(lg.rpw, lg.rounds - rb);
-  if (!XU && nr <= 0) return;  // (XU: every wave takes part in forming a)
+  constexpr bool HOOK = lane_hook<decltype(srcs.bind(0))>::value;
+  if (!XU && !HOOK && nr <= 0) return;  // (XU, HOOK: every wave takes part)
   const auto src = srcs.bind(item);
   const int rlast = min(rb + max(nr, 1), lg.rounds) - 1;  // idle waves re-read a valid round
   const int N = lg.N, G = lg.G, kw = lg.kw, rank = lg.rank;
@@ -379,8 +411,31 @@ __device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, in
     }
   };
   // the rows' loads go out first; x and a (below) arrive under them
+  using Item = std::decay_t<decltype(src)>;
+  constexpr bool EARLY = !XU && lane_early_a<Item>::value;
+  float araw[EARLY ? M2 : 1][EARLY ? NSV : 1][2][kLaneEarlyA];
+  bool early = false;
   if constexpr (!XU) {
-    prologue();
+    if (!HOOK || nr > 0) prologue();
+    if constexpr (HOOK) {
+      src.after_issue();
+      if (nr <= 0) return;
+    }
+    if constexpr (EARLY) {
+      early = src.lora() && src.a_count() <= kLaneEarlyA;
+      if (early) {
+#pragma unroll
+        for (int m = 0; m < M2; ++m)
+#pragma unroll
+          for (int k = 0; k < NSV; ++k)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const int j = min(2 * (p + k * LRP) + e, rank - 1);  // past the rank: unused
+              if constexpr (PAIR) src.a_issue(m, j, araw[m][k][e]);
+              else src.a_issue(j, araw[m][k][e]);
+            }
+      }
+    }
     load_x();
   }
 
@@ -408,6 +463,14 @@ __device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, in
       for (int k = 0; k < NSV; ++k) {
         const int j = p + k * LRP;
         f16x2 pr = {(_Float16)0.f, (_Float16)0.f};
+        if constexpr (EARLY) {
+          if (early && 2 * j < rank) {
+            pr[0] = (_Float16)lane_early_sum(araw[m][k][0]);
+            pr[1] = (_Float16)lane_early_sum(araw[m][k][1]);
+            ap[m][k] = __builtin_bit_cast(uint32_t, pr);
+            continue;
+          }
+        }
         if (lora && 2 * j < rank) {
           if constexpr (PAIR) {
             pr[0] = (_Float16)__half2float(src.load_a(m, 2 * j));

@@ -107,6 +107,18 @@ struct MoeLaneArgs {
   float* rtd;           // [B][H] routed part of the outputs (t16d)
   int nrd;          // workgroups of the routed down rows
   int rows_wg;      // output rows per shared-down workgroup (its combine)
+  // Combine in the routed down launch (fuse): the shared down runs in the
+  // gate/up launch (sy = fp16 of its rows), and the last of a (token, row
+  // block)'s down workgroups and a_down jobs to arrive on ccnt combines the
+  // block's rows.
+  int fuse;
+  __half* sy;       // [B][H] shared expert outputs
+  unsigned* ccnt;   // [B][nrb] arrival counters (zero between steps)
+  unsigned* adcnt;  // [B] the token's a_down jobs done (low half) and their readers (high)
+  uint64_t spin;    // bound of the combine's wait, ticks of the 100 MHz real-time counter
+  int nrb;          // row blocks of an output row (routed down workgroups per item)
+  int rows_blk;     // output rows per row block
+  int ngu;          // workgroups of the routed gate/up role (fuse: the shared down's follow)
 };
 
 constexpr int kXuSlice = 512;  // codes per x U job
@@ -159,11 +171,21 @@ struct RguItem {
   __device__ const __half* sv(int m) const { return a.SV[m] + (int64_t)e * a.sv_es[m]; }
   __device__ u32x4 x8(int k) const { return *(const u32x4*)(x + k); }
   // a = fp16(sum of the slices' partials, in slice order)
-  __device__ __half load_a(int m, int j) const {
+  __device__ const float* a_parts(int m, int j) const {
     const int64_t job = a.xuall ? ((int64_t)m * a.C + moe_lane_clamp(a.clus[m][e], a.C)) * a.B +
                                       p / a.topk
                                 : (int64_t)m * a.B * a.topk + p;
-    return __float2half(sum_strided(a.agu + job * a.su * a.rank + j, a.rank, a.su));
+    return a.agu + job * a.su * a.rank + j;
+  }
+  __device__ __half load_a(int m, int j) const {
+    return __float2half(sum_strided(a_parts(m, j), a.rank, a.su));
+  }
+  // the slices' partials, issued before the x slice's wait (glq_lane.h)
+  __device__ int a_count() const { return a.su; }
+  __device__ void a_issue(int m, int j, float (&v)[kLaneEarlyA]) const {
+    const float* pp = a_parts(m, j);
+#pragma unroll
+    for (int q = 0; q < kLaneEarlyA; ++q) v[q] = q < a.su ? pp[(int64_t)q * a.rank] : 0.f;
   }
   __device__ void store(int n, float g, float u) const {
     a.inter[(int64_t)p * a.I + n] = swiglu_fp16(g, u);
@@ -200,7 +222,9 @@ struct RdItem {
   }
   __device__ __half load_a(int) const { return __float2half(0.f); }
   __device__ void store(int n, float v) const {
-    a.yb[((int64_t)q * a.B * a.topk + p) * a.H + n] = v;
+    float* d = a.yb + ((int64_t)q * a.B * a.topk + p) * a.H + n;
+    if (a.fuse) handoff_put(d, v);  // read by this launch's combine
+    else *d = v;
   }
 };
 template <int BITS>
@@ -260,25 +284,47 @@ struct SguTileSrc {
 };
 constexpr int kMoeT16MinB = 4;  // tokens from which the shared expert takes the tile form
 
+// sum_strided of data handed over inside the launch (agent-scope loads)
+__device__ __forceinline__ float sum_strided_coh(const float* p, int64_t stride, int n) {
+  float s = 0.f;
+  for (int q0 = 0; q0 < n; q0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = q0 + u < n ? handoff_get(p + (int64_t)(q0 + u) * stride) : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  return s;
+}
+
 // Routed part of output rows [n0, n0 + nrows) of token t into LDS routed[]:
 // sum_k w_k (y_k[n] + a_down,k SV_down,k[n]^T), fmaf over the picks in pick
 // order (the many-token combine's order), a_down = fp16(sum of its slices'
 // partials).  All `nth` threads of the workgroup call it (barriers inside).
 // LDS: adl (topk x rank halves), contrib (nrows x topk floats), routed.
+// COH: y and the a_down partials were written in this launch (agent-scope
+// loads).
+// adl_ready: adl already holds the token's a_down values.
+template <bool COH = false>
 __device__ void moe_lane_routed_rows(const MoeLaneArgs& a, int t, int n0, int nrows, int nth,
-                                     __half* adl, float* contrib, float* routed) {
+                                     __half* adl, float* contrib, float* routed,
+                                     bool adl_ready = false) {
   const int tid = threadIdx.x, K = a.topk, r = a.rank;
   const bool lora = r > 0 && a.SV[2] != nullptr;
-  if (lora)
+  if (lora && !adl_ready)
     for (int i = tid; i < K * r; i += nth) {
       const int k = i / r, j = i - k * r;
-      adl[i] = __float2half(sum_strided(a.ad + (int64_t)(t * K + k) * a.sd * r + j, r, a.sd));
+      const float* pp = a.ad + (int64_t)(t * K + k) * a.sd * r + j;
+      adl[i] = __float2half(COH ? sum_strided_coh(pp, r, a.sd) : sum_strided(pp, r, a.sd));
     }
   __syncthreads();
   for (int i = tid; i < nrows * K; i += nth) {
     const int rr = i / K, k = i - rr * K, n = min(n0 + rr, a.H - 1), pk = t * K + k;
     float y = 0.f;
-    for (int q = 0; q < a.kd; ++q) y += a.yb[((int64_t)q * a.B * K + pk) * a.H + n];
+    for (int q = 0; q < a.kd; ++q) {
+      const float* yp = a.yb + ((int64_t)q * a.B * K + pk) * a.H + n;
+      y += COH ? handoff_get(yp) : *yp;
+    }
     if (lora) {
       const __half* sv = a.SV[2] + (int64_t)a.sel[pk] * a.sv_es[2] + (int64_t)n * r;
       const __half* ak = adl + k * r;
@@ -301,12 +347,18 @@ __device__ void moe_lane_routed_rows(const MoeLaneArgs& a, int t, int n0, int nr
   __syncthreads();
 }
 
-// Shared down rows of token t, the combine in each row's store (the rows'
-// routed parts precomputed in LDS from row n0).
+// Shared down rows of token t, the combine in each row's store; the rows'
+// routed parts (from row n0) are formed in LDS while the rows' first loads
+// are in flight (after_issue).
 struct SdItem {
   const MoeLaneArgs& a;
-  int t, n0;
-  const float* routed;
+  int t, n0, nrows;
+  __half* adl;
+  float* contrib;
+  float* routed;
+  __device__ void after_issue() const {
+    moe_lane_routed_rows(a, t, n0, nrows, kMoeLaneThreads, adl, contrib, routed);
+  }
   __device__ bool lora() const { return false; }
   __device__ const uint32_t* codes() const { return a.scodes[2]; }
   __device__ const __half* scales() const { return a.sscales[2]; }
@@ -327,11 +379,36 @@ struct SdItem {
     a.out[(int64_t)t * a.H + n] = __float2half(o);
   }
 };
+// Shared down rows of token t storing sy = fp16 of each row (the combine
+// follows in the routed down launch).
+struct SdyItem {
+  const MoeLaneArgs& a;
+  int t;
+  __device__ bool lora() const { return false; }
+  __device__ const uint32_t* codes() const { return a.scodes[2]; }
+  __device__ const __half* scales() const { return a.sscales[2]; }
+  __device__ const __half* zeros() const { return a.szeros[2]; }
+  __device__ const __half* sv() const { return nullptr; }
+  __device__ const __half* bias() const { return nullptr; }
+  __device__ const __half* u() const { return nullptr; }
+  __device__ u32x4 x8(int k) const {
+    return *(const u32x4*)(a.sinter + (int64_t)t * a.SI + k);
+  }
+  __device__ __half load_a(int) const { return __float2half(0.f); }
+  __device__ void store(int n, float v) const { a.sy[(int64_t)t * a.H + n] = __float2half(v); }
+};
+struct SdySrc {
+  const MoeLaneArgs& a;
+  __device__ SdyItem bind(int t) const { return SdyItem{a, t}; }
+};
+
 struct SdSrc {
   const MoeLaneArgs& a;
-  int n0;
-  const float* routed;
-  __device__ SdItem bind(int t) const { return SdItem{a, t, n0, routed}; }
+  int n0, nrows;
+  __half* adl;
+  float* contrib;
+  float* routed;
+  __device__ SdItem bind(int t) const { return SdItem{a, t, n0, nrows, adl, contrib, routed}; }
 };
 
 // Shared down rows of every token in the token-tile form.  Before it
@@ -621,20 +698,144 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_gu_kernel(MoeLaneArg
 }
 
 
+// The routed gate/up role, then (fuse, with a shared expert) the shared
+// down's rows storing sy.
+template <int BITS, int LRP, int NSV, int SBITS, int SLRP, int SNP>
+__global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_gu_sd_kernel(MoeLaneArgs a) {
+  const int wvb = moe_lane_wave();
+  if ((int)blockIdx.x < a.ngu) {
+    lane_run<RguSrc, BITS, false, LRP, 1, kMoePairPD, NSV, false, false, true>(
+        RguSrc{a}, a.gRGU, blockIdx.x * 8 + wvb, wvb, nullptr);
+    return;
+  }
+  const int b = blockIdx.x - a.ngu;
+  lane_run<SdySrc, SBITS, false, SLRP, SNP, moe_lane_pd(SNP), 1, false, false>(
+      SdySrc{a}, a.gSD, b * 8 + wvb, wvb, nullptr);
+}
+
+// a_down of token t's picks formed here, slice by slice in the a_down jobs'
+// order (the same bits as their handed-over partials), into adl.  Every
+// thread calls it.
+__device__ void moe_lane_local_adown(const MoeLaneArgs& a, int t, __half* adl, float* xu) {
+  for (int k = 0; k < a.topk; ++k) {
+    const int pk = t * a.topk + k;
+    const XuJob job{a.inter + (int64_t)pk * a.I, moe_lane_u(a, 2, a.sel[pk])};
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // sum_strided's batches of 8
+    float tot = 0.f;
+    for (int q = 0; q < a.sd; ++q) {
+      const int k0 = q * kXuSlice;
+      const float* sums = lane_xu_sum(job, k0, min(kXuSlice, a.I - k0), a.rank, xu);
+      if ((int)threadIdx.x < a.rank) acc[q & 7] = sums[threadIdx.x];
+      __syncthreads();  // the next slice's partials overwrite the sums
+      if ((q & 7) == 7 || q == a.sd - 1) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          tot += (u <= (q & 7)) ? acc[u] : 0.f;
+          acc[u] = 0.f;
+        }
+      }
+    }
+    if ((int)threadIdx.x < a.rank) adl[k * a.rank + threadIdx.x] = __float2half(tot);
+  }
+  __syncthreads();
+}
+
+// Rows of row block rb of token t: out = fp16(routed + gate * sy) (+ the
+// residual), or fp16(routed) without a shared expert -- the arithmetic of
+// SdItem::store and moe_lane_combine_kernel.  Every thread calls it.  With
+// LoRA it first waits (bounded) for the token's a_down jobs; a wait that
+// outlasts kMoeSpinTicks forms a_down itself (the same bits).
+constexpr uint64_t kMoeSpinTicks = 100000;  // 1 ms of the 100 MHz real-time counter
+__device__ void moe_lane_block_combine(const MoeLaneArgs& a, int t, int rb, float* lds,
+                                       int* flag) {
+  const int n0 = rb * a.rows_blk, nrows = min(a.rows_blk, a.H - n0);
+  const bool lora = a.rank > 0 && a.SV[2] != nullptr;
+  __half* adl = (__half*)lds;
+  float* contrib = lds + (a.topk * a.rank + 1) / 2;
+  float* routed = contrib + a.rows_blk * a.topk;
+  bool ready = false;
+  if (lora) {
+    const unsigned need = (unsigned)(a.topk * a.sd);
+    if (threadIdx.x == 0) {
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      int ok = 0;
+      while (true) {
+        if ((handoff_get(a.adcnt + t) & 0xffffu) >= need) {
+          ok = 1;
+          break;
+        }
+        if (__builtin_amdgcn_s_memrealtime() - t0 > a.spin) break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+      *flag = ok;
+    }
+    __syncthreads();
+    if (!*flag) {  // (uniform)
+      moe_lane_local_adown(a, t, adl, routed + a.rows_blk);
+      ready = true;
+    }
+  }
+  moe_lane_routed_rows<true>(a, t, n0, nrows, kMoeLaneThreads, adl, contrib, routed, ready);
+  if (lora && threadIdx.x == 0) {  // this block's reader is done with the a_down partials
+    const unsigned fin = ((unsigned)a.nrb << 16) | (unsigned)(a.topk * a.sd);
+    const unsigned old = __hip_atomic_fetch_add(a.adcnt + t, 1u << 16, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    if (old + (1u << 16) == fin) handoff_reset(a.adcnt + t);
+  }
+  for (int r = threadIdx.x; r < nrows; r += kMoeLaneThreads) {
+    const int n = n0 + r;
+    float acc = routed[r];
+    if (a.SI > 0)
+      acc = fmaf(__half2float(a.sg[t]), __half2float(a.sy[(int64_t)t * a.H + n]), acc);
+    float o = __half2float(__float2half(acc));
+    if (a.res) o += __half2float(a.res[(int64_t)t * a.H + n]);
+    a.out[(int64_t)t * a.H + n] = __float2half(o);
+  }
+}
+
+// Workgroups [0, nad): the a_down jobs (LoRA), job b = p sd + s; then the
+// routed down rows.  fuse: a job hands its partial over and counts itself
+// on its token; a down workgroup counts itself on its (token, row block), and
+// the last of the block's down workgroups combines the block.  The jobs come
+// first in the grid, so a combine waits only on workgroups dispatched before
+// its own.
 template <int BITS, int LRP, int NP>
 __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_down_kernel(MoeLaneArgs a) {
   extern __shared__ float lds[];
-  if ((int)blockIdx.x >= a.nrd) {  // partial a_down of (pick, K slice) job b = p sd + s
-    const int b = blockIdx.x - a.nrd, s = b % a.sd, p = b / a.sd;
+  __shared__ int flag;
+  const int nad = a.rank > 0 && a.SV[2] != nullptr ? a.B * a.topk * a.sd : 0;
+  if ((int)blockIdx.x < nad) {  // partial a_down of (pick, K slice)
+    const int b = blockIdx.x, s = b % a.sd, p = b / a.sd;
     const XuJob job{a.inter + (int64_t)p * a.I, moe_lane_u(a, 2, a.sel[p])};
     const int k0 = s * kXuSlice;
     const float* sums = lane_xu_sum(job, k0, min(kXuSlice, a.I - k0), a.rank, lds);
-    if ((int)threadIdx.x < a.rank) a.ad[(int64_t)b * a.rank + threadIdx.x] = sums[threadIdx.x];
+    if ((int)threadIdx.x < a.rank) {
+      float* d = a.ad + (int64_t)b * a.rank + threadIdx.x;
+      if (a.fuse) handoff_put(d, sums[threadIdx.x]);
+      else *d = sums[threadIdx.x];
+    }
+    if (a.fuse) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(a.adcnt + p / a.topk, 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
     return;
   }
+  const int db = blockIdx.x - nad;
   const int wvb = moe_lane_wave();
   lane_run<RdSrc<BITS>, BITS, false, LRP, NP, moe_lane_pd(NP), 1, false, false>(
-      RdSrc<BITS>{a}, a.gRD, blockIdx.x * 8 + wvb, wvb, nullptr);
+      RdSrc<BITS>{a}, a.gRD, db * 8 + wvb, wvb, nullptr);
+  if (!a.fuse) return;
+  // the workgroup's rows: row block rb of item i = p kd + q (whole workgroups
+  // per item); the block's last down workgroup combines it
+  const int wgi = a.gRD.wpi / 8, i = db / wgi, rb = db - i * wgi;
+  const int t = i / a.kd / a.topk;
+  if (handoff_arrive(a.ccnt + t * a.nrb + rb, (unsigned)(a.topk * a.kd), &flag)) {
+    moe_lane_block_combine(a, t, rb, lds, &flag);
+    if (threadIdx.x == 0) handoff_reset(a.ccnt + t * a.nrb + rb);
+  }
 }
 
 // Each workgroup holds one token's rows (wpi a multiple of 8): first the
@@ -653,10 +854,9 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_sdown_kernel(MoeLane
   __half* adl = (__half*)lds;                          // topk x rank
   float* contrib = lds + (a.topk * a.rank + 1) / 2;    // rows_wg x topk
   float* routed = contrib + a.rows_wg * a.topk;        // rows_wg
-  moe_lane_routed_rows(a, t, n0, nrows, kMoeLaneThreads, adl, contrib, routed);
   const int wvb = moe_lane_wave();
-  lane_run<SdSrc, SBITS, false, SLRP, SNP, PD, 1, false, false>(SdSrc{a, n0, routed}, g,
-                                                                wv0 + wvb, wvb, nullptr);
+  lane_run<SdSrc, SBITS, false, SLRP, SNP, PD, 1, false, false>(
+      SdSrc{a, n0, nrows, adl, contrib, routed}, g, wv0 + wvb, wvb, nullptr);
 }
 
 // The shared down and combine in the token-tile form (4-bit shared codes).
@@ -743,8 +943,8 @@ struct MoeLanePlan {
   int bits, sbits, rc;
   bool lora;
   int64_t off_sel, off_wts, off_sg, off_lgw, off_agu, off_inter, off_yb, off_ad, off_sinter,
-      off_t16p, off_rtd, ws_need;
-  size_t lds_route, lds_xu, lds_xut, lds_comb, lds_sd16;
+      off_t16p, off_rtd, off_sy, ws_need;
+  size_t lds_route, lds_xu, lds_xut, lds_comb, lds_sd16, lds_down;
 };
 
 }  // namespace
@@ -849,6 +1049,33 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   } else {
     a.rows_wg = std::max(1, 256 / a.topk);
   }
+  a.ngu = (int)role_blocks(a.gRGU);
+  // The combine in the routed down launch (3 launches instead of 4): the
+  // down role in whole workgroups per item, each its row block; with a
+  // shared expert, its down (lane form, rows of 64-lane groups) in the
+  // gate/up launch.  2-bit experts, a 4-bit shared expert or none.
+  a.fuse = 0;
+  if (!getenv("GLQ_MOE_NO_FUSE") && bits == 2 &&
+      (SI == 0 || (sbits == 4 && !a.t16d && lane_lrp(a.gSD.lr) == 64 &&
+                   (a.gSD.lr + 63) / 64 <= 4))) {
+    LaneGeom g = role_geom((int)H, a.kdp, bits, 0, P_ * a.kd, false, true);
+    g.G = a.gRD.G;
+    g.kw = a.gRD.kw;
+    const int np = (g.lr + 63) / 64, rpi = 64 / lane_lrp(g.lr);
+    const int nrb = g.wpi / 8, rows_blk = 8 * g.rpw * moe_lane_pd(np) * rpi;
+    if (nrb <= kMoeCombineCnt / 4 && (int64_t)B * nrb <= kMoeCombineCnt &&
+        (int64_t)nrb * rows_blk >= H) {
+      a.fuse = 1;
+      // GLQ_MOE_SPIN_TICKS: the combine's wait bound (tests set 0 to take the
+      // local a_down path)
+      const char* e = getenv("GLQ_MOE_SPIN_TICKS");
+      a.spin = e ? (uint64_t)strtoull(e, nullptr, 10) : kMoeSpinTicks;
+      a.gRD = g;
+      a.nrd = (int)role_blocks(g);
+      a.nrb = nrb;
+      a.rows_blk = rows_blk;
+    }
+  }
   // The header (kMoeWsHeader bytes) holds the many-token path's router
   // arrival counter (word 0), this path's per-token router counters (bytes
   // 64 ..) and its token-tile row-block counters (bytes 1024 ..), all of
@@ -887,11 +1114,16 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   const int64_t t16p = std::max(a.t16s ? t16_wgs(a.gS16) * 2 : 0, a.t16d ? t16_wgs(a.gSD16) : 0);
   P.off_t16p = take(4 * t16p * kT16Elems);
   P.off_rtd = take(a.t16d ? 4 * B * H : 0);
+  P.off_sy = take(a.fuse && SI > 0 ? 2 * B * H : 0);
   P.ws_need = o;
   P.lds_route = (size_t)(((2 * (a.E + 1) + 15) & ~15) + 4 * a.E + 4 * 16);
   P.lds_xu = lora ? (size_t)LaneXu(r).lds_bytes(r) : 0;
   P.lds_xut = a.xuall == 2 ? (size_t)std::max(8 * 32 * kXuTileStride * 2, 8 * 4 * 256 * 4) : 0;
   P.lds_comb = (size_t)(4 * ((a.topk * r + 1) / 2) + 4 * a.rows_wg * (a.topk + 1));
+  P.lds_down = P.lds_xu;
+  if (a.fuse)  // the combine's adl, contrib and routed; after them a local a_down's scratch
+    P.lds_down = std::max(P.lds_down, (size_t)(4 * ((a.topk * r + 1) / 2) +
+                                               4 * a.rows_blk * (a.topk + 1)) + P.lds_xu);
   P.lds_sd16 = 0;
   if (a.t16d) {
     const int64_t nt = (B + a.gSD16.ks - 1) / a.gSD16.ks;  // tokens of a K slice's routed part
@@ -941,13 +1173,34 @@ static int launch_gu(const MoeLanePlan& P, hipStream_t s) {
   return GLQ_OK;
 }
 
+template <int BITS, int LRP, int NSV, int SNP>
+static int launch_gu_sd(const MoeLanePlan& P, hipStream_t s) {
+  const int64_t grid = P.a.ngu + role_blocks(P.a.gSD);
+  moe_lane_gu_sd_kernel<BITS, LRP, NSV, 4, 64, SNP>
+      <<<dim3((unsigned)grid), dim3(kMoeLaneThreads), 0, s>>>(P.a);
+  GLQ_LAUNCH_CHECK("moe_lane_gu_sd_kernel");
+  return GLQ_OK;
+}
+template <int BITS, int LRP, int NSV>
+static int launch_gu_or_sd(const MoeLanePlan& P, hipStream_t s) {
+  if (!P.a.fuse || P.a.SI == 0) return launch_gu<BITS, LRP, NSV>(P, s);
+  if constexpr (BITS == 2) {
+    const int snp = (P.a.gSD.lr + 63) / 64;
+    if (snp == 1) return launch_gu_sd<BITS, LRP, NSV, 1>(P, s);
+    if (snp == 2) return launch_gu_sd<BITS, LRP, NSV, 2>(P, s);
+    if (snp == 3) return launch_gu_sd<BITS, LRP, NSV, 3>(P, s);
+    return launch_gu_sd<BITS, LRP, NSV, 4>(P, s);
+  }
+  GLQ_CHECK(false, "fused combine needs 2-bit experts");
+}
+
 template <int BITS, int LRP, int NP>
 static int launch_down(const MoeLanePlan& P, hipStream_t s) {
   const int64_t grid = P.a.nrd + (P.lora ? (int64_t)P.a.B * P.a.topk * P.a.sd : 0);
   static size_t attr = 64 * 1024;
-  int rc = set_lds_limit(moe_lane_down_kernel<BITS, LRP, NP>, P.lds_xu, attr);
+  int rc = set_lds_limit(moe_lane_down_kernel<BITS, LRP, NP>, P.lds_down, attr);
   if (rc) return rc;
-  moe_lane_down_kernel<BITS, LRP, NP><<<dim3((unsigned)grid), dim3(kMoeLaneThreads), P.lds_xu,
+  moe_lane_down_kernel<BITS, LRP, NP><<<dim3((unsigned)grid), dim3(kMoeLaneThreads), P.lds_down,
                                         s>>>(P.a);
   GLQ_LAUNCH_CHECK("moe_lane_down_kernel");
   return GLQ_OK;
@@ -980,10 +1233,11 @@ static int launch_sdown(const MoeLanePlan& P, hipStream_t s) {
 template <int BITS>
 static int dispatch_gu(const MoeLanePlan& P, hipStream_t s) {
   const int lrp = lane_lrp(P.a.gRGU.lr), r = P.a.rank;
-  if (lrp == 64) return launch_gu<BITS, 64, 1>(P, s);
-  if (lrp == 32) return r <= 64 ? launch_gu<BITS, 32, 1>(P, s) : launch_gu<BITS, 32, 2>(P, s);
-  if (r <= 32) return launch_gu<BITS, 16, 1>(P, s);
-  return r <= 64 ? launch_gu<BITS, 16, 2>(P, s) : launch_gu<BITS, 16, 4>(P, s);
+  if (lrp == 64) return launch_gu_or_sd<BITS, 64, 1>(P, s);
+  if (lrp == 32)
+    return r <= 64 ? launch_gu_or_sd<BITS, 32, 1>(P, s) : launch_gu_or_sd<BITS, 32, 2>(P, s);
+  if (r <= 32) return launch_gu_or_sd<BITS, 16, 1>(P, s);
+  return r <= 64 ? launch_gu_or_sd<BITS, 16, 2>(P, s) : launch_gu_or_sd<BITS, 16, 4>(P, s);
 }
 
 template <int BITS>
@@ -1039,9 +1293,10 @@ static int moe_lane_launch(const MoeLanePlan& P, hipStream_t s) {
   // 3. routed gate/up
   rc = P.bits == 2 ? dispatch_gu<2>(P, s) : dispatch_gu<4>(P, s);
   if (rc) return rc;
-  // 4. routed down (+ a_down)
+  // 4. routed down (+ a_down; fuse: + the combine)
   rc = P.bits == 2 ? dispatch_down<2>(P, s) : dispatch_down<4>(P, s);
   if (rc) return rc;
+  if (a.fuse) return GLQ_OK;
   // 5. shared down + combine, or the combine alone
   if (P.sbits == 2) return dispatch_shared<2>(P, s, false);
   if (P.sbits == 4) return dispatch_shared<4>(P, s, false);
@@ -1089,6 +1344,9 @@ int moe_lane_decode(const glq_moe_params* p, void* workspace, int64_t workspace_
   a.gS16.cnt = (unsigned*)(w + 1024);
   a.gSD16.cnt = (unsigned*)(w + 1024 + 4 * kMoeT16MaxRB);
   a.rtd = (float*)(w + P.off_rtd);
+  a.sy = (__half*)(w + P.off_sy);
+  a.ccnt = (unsigned*)(w + 4096);  // header bytes 4096 .. 8191, zero between steps
+  a.adcnt = (unsigned*)(w + 512);  // header bytes 512 .. 575 (16 tokens)
   return moe_lane_launch(P, s);
 }
 

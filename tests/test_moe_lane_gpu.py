@@ -137,3 +137,56 @@ def test_xu_forms_agree(gpu, monkeypatch, B):
     o2, _ = blk(h)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
+
+
+@pytest.mark.parametrize("cfg,B", [("config2", 1), ("config2", 2), ("config3", 1),
+                                   ("config3", 8), ("config4", 1), ("config4", 16)])
+def test_fused_combine_same_bits(gpu, monkeypatch, cfg, B):
+    """The combine in the routed down launch (the last of a (token, row
+    block)'s down workgroups and a_down jobs to arrive forms the block's rows;
+    the shared down in the gate/up launch) against the separate combine
+    launch (GLQ_MOE_NO_FUSE): the same sums in the same order, so the same
+    bits, with a residual; repeated steps and graph replays too (the arrival
+    counters are left at zero), and combines whose wait for the a_down jobs
+    is bounded at zero ticks (GLQ_MOE_SPIN_TICKS=0: a_down formed in the
+    combining workgroup)."""
+    monkeypatch.delenv("GLQ_MOE_NO_LANE", raising=False)
+    if cfg == "config2":
+        p = lora_heavy(fmt.make_moe(B=B, seed=1))
+    elif cfg == "config3":
+        p = lora_heavy(fmt.make_mixtral_layer(B=B, seed=3), f=3.0)
+    else:
+        p = lora_heavy(fmt.make_moe(H=2048, E=128, inter=768, top_k=8, n_clusters=100, rank=64,
+                                    shared_inter=0, B=B, seed=5))
+    print(f"fused combine {cfg} B={B}", flush=True)
+    blk = GraphCompatibleMoeBlock.from_problem(p, gpu)
+    res = (torch.randn(1, B, p.H, generator=torch.Generator().manual_seed(9)) * 0.5).half().to(gpu)
+    h = p.h.reshape(1, B, p.H).to(gpu)
+    fused = [blk(h, residual=res)[0].clone() for _ in range(3)]
+    # a combine whose wait is bounded at zero ticks forms a_down itself
+    monkeypatch.setenv("GLQ_MOE_SPIN_TICKS", "0")
+    fused += [blk(h, residual=res)[0].clone() for _ in range(2)]
+    monkeypatch.delenv("GLQ_MOE_SPIN_TICKS")
+    monkeypatch.setenv("GLQ_MOE_NO_FUSE", "1")
+    sep, _ = blk(h, residual=res)
+    monkeypatch.delenv("GLQ_MOE_NO_FUSE")
+    torch.cuda.synchronize()
+    for i, o in enumerate(fused):
+        assert torch.equal(o, sep), f"{cfg} B={B} step {i}: fused != separate combine"
+    out = torch.empty_like(sep)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        blk(h, residual=res)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        o, _ = blk(h, residual=res)
+        out.copy_(o)
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, sep), f"{cfg} B={B} replay {i}"
+        _ = (h.float() * 2).sum().item()  # eager work between replays
