@@ -682,12 +682,13 @@ def main():
                                               out=out)
 
     # The step's one kernel, HIP events on the launch stream (the roofline
-    # figure).  It runs first: the device's first passes over a fresh 2.6 GB
-    # pool are slower than its steady state (about 450 against 417 us a step
-    # for the first 25 steps on an MI355X), so the timed step loop below does
-    # not start on a device that has only just allocated the pool.
+    # figure).  It runs first, after 60 untimed calls: the device's first
+    # passes over a fresh 2.6 GB pool are slower than its steady state (about
+    # 450 against 417 us a step for the first 25 steps on an MI355X), so
+    # neither this figure nor the timed step loop below measures a device that
+    # has only just allocated the pool.
     log("timing the fused kernel with HIP events")
-    k_ms = time_events(step, args.steps, max(args.warmup, 25))
+    k_ms = time_events(step, args.steps, max(args.warmup, 60))
     k_bytes = layer_bytes() * args.pool
     k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
 

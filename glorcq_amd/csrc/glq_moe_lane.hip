@@ -746,6 +746,7 @@ __device__ void moe_lane_local_adown(const MoeLaneArgs& a, int t, __half* adl, f
 // LoRA it first waits (bounded) for the token's a_down jobs; a wait that
 // outlasts kMoeSpinTicks forms a_down itself (the same bits).
 constexpr uint64_t kMoeSpinTicks = 100000;  // 1 ms of the 100 MHz real-time counter
+constexpr int kMoeFuseWork = 256;  // output rows x picks of one fused combine, at most
 __device__ void moe_lane_block_combine(const MoeLaneArgs& a, int t, int rb, float* lds,
                                        int* flag) {
   const int n0 = rb * a.rows_blk, nrows = min(a.rows_blk, a.H - n0);
@@ -1051,20 +1052,23 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   }
   a.ngu = (int)role_blocks(a.gRGU);
   // The combine in the routed down launch (3 launches instead of 4): the
-  // down role in whole workgroups per item, each its row block; with a
-  // shared expert, its down (lane form, rows of 64-lane groups) in the
-  // gate/up launch.  2-bit experts, a 4-bit shared expert or none.
+  // down role in whole workgroups per item, each its row block, whose last
+  // arriving workgroup combines the block; the shared expert's down (lane
+  // form, rows of 64-lane groups) moves to the gate/up launch.  Taken with a
+  // 4-bit shared expert (its down then leaves the last launch) when a block's
+  // combine is light (rows x picks <= kMoeFuseWork): config 2 at 1-2 tokens.
+  // Without a shared expert, or with larger blocks, the separate combine
+  // launch spreads the combine wider and measured faster.
   a.fuse = 0;
-  if (!getenv("GLQ_MOE_NO_FUSE") && bits == 2 &&
-      (SI == 0 || (sbits == 4 && !a.t16d && lane_lrp(a.gSD.lr) == 64 &&
-                   (a.gSD.lr + 63) / 64 <= 4))) {
+  if (!getenv("GLQ_MOE_NO_FUSE") && bits == 2 && SI > 0 && sbits == 4 && !a.t16d &&
+      lane_lrp(a.gSD.lr) == 64 && (a.gSD.lr + 63) / 64 <= 4) {
     LaneGeom g = role_geom((int)H, a.kdp, bits, 0, P_ * a.kd, false, true);
     g.G = a.gRD.G;
     g.kw = a.gRD.kw;
     const int np = (g.lr + 63) / 64, rpi = 64 / lane_lrp(g.lr);
     const int nrb = g.wpi / 8, rows_blk = 8 * g.rpw * moe_lane_pd(np) * rpi;
     if (nrb <= kMoeCombineCnt / 4 && (int64_t)B * nrb <= kMoeCombineCnt &&
-        (int64_t)nrb * rows_blk >= H) {
+        (int64_t)nrb * rows_blk >= H && rows_blk * a.topk <= kMoeFuseWork) {
       a.fuse = 1;
       // GLQ_MOE_SPIN_TICKS: the combine's wait bound (tests set 0 to take the
       // local a_down path)
