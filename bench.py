@@ -754,12 +754,12 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
-            "kernel": "glq::gemv_lane_kernel<2,false,32,4,1,false,true>",
+            "kernel": "glq::gemv_lane_kernel<2,false,32,1,4,1,false,true>",
             "kernel_avg_us": round(k_ms * 1e3, 2),
             "algorithmic_bytes_per_launch": k_bytes,
         },
         "gemv_with_precomputed_a": {
-            "kernel": "glq::gemv_lane_kernel<2,false,32,4,1,false,false>",
+            "kernel": "glq::gemv_lane_kernel<2,false,32,1,4,1,false,false>",
             "kernel_avg_us": round(g_ms * 1e3, 2),
             "achieved_gbs": round(g_bytes / (g_ms * 1e-3) / 1e9, 1),
             "algorithmic_bytes_per_launch": g_bytes,
