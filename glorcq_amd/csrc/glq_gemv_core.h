@@ -50,6 +50,7 @@
 
 #include <hip/hip_fp16.h>
 
+#include "glq_handoff.h"
 #include "glq_internal.h"
 
 namespace glq {
@@ -241,7 +242,8 @@ constexpr int kLowrankUtStride = kLowrankRows + 8;  // halves per staged U colum
 // groups side by side, each with its own LDS; every group must make the same
 // calls, since the barriers are workgroup-wide).  out == nullptr: compute, but
 // write nothing (a group without a job of its own).
-template <int MC, class XRow>
+// COH: the partials are read inside the same launch (agent-scope stores).
+template <int MC, class XRow, bool COH = false>
 __device__ void lowrank_partial(const XRow& xrow, int M, int K, int rank, int rpad,
                                 const __half* __restrict__ U, int p,
                                 float* __restrict__ out /* M x rpad */,
@@ -294,7 +296,11 @@ __device__ void lowrank_partial(const XRow& xrow, int M, int K, int rank, int rp
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int m = 4 * kb + i;
-          if (m < M) out[m * rpad + col] = col < rank ? acc[i] : 0.f;
+          if (m < M) {
+            const float v = col < rank ? acc[i] : 0.f;
+            if constexpr (COH) handoff_put(out + m * rpad + col, v);
+            else out[m * rpad + col] = v;
+          }
         }
       }
       __syncthreads();  // the next block's staging overwrites ut
@@ -355,7 +361,8 @@ __device__ void lowrank_partial(const XRow& xrow, int M, int K, int rank, int rp
         if (out && mm < MC && mb + mm < M && jb + jj < rpad) {
           const float s = red[(0 * 4 + mm) * 64 + jj] + red[(1 * 4 + mm) * 64 + jj] +
                           red[(2 * 4 + mm) * 64 + jj] + red[(3 * 4 + mm) * 64 + jj];
-          out[(mb + mm) * rpad + jb + jj] = s;
+          if constexpr (COH) handoff_put(out + (mb + mm) * rpad + jb + jj, s);
+          else out[(mb + mm) * rpad + jb + jj] = s;
         }
       }
       __syncthreads();

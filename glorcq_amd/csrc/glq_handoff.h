@@ -46,4 +46,19 @@ __device__ __forceinline__ void handoff_reset(unsigned* cnt) {
   __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// p[0] + p[stride] + ... + p[(n-1) stride] of data handed over inside the
+// launch (agent-scope loads), in that order, loads in batches of 8 (the
+// order and the zeros of sum_strided, glq_gemv_core.h).
+__device__ __forceinline__ float sum_strided_coh(const float* p, int64_t stride, int n) {
+  float s = 0.f;
+  for (int q0 = 0; q0 < n; q0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = q0 + u < n ? handoff_get(p + (int64_t)(q0 + u) * stride) : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  return s;
+}
+
 }  // namespace glq

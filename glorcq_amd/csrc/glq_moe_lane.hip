@@ -284,19 +284,6 @@ struct SguTileSrc {
 };
 constexpr int kMoeT16MinB = 4;  // tokens from which the shared expert takes the tile form
 
-// sum_strided of data handed over inside the launch (agent-scope loads)
-__device__ __forceinline__ float sum_strided_coh(const float* p, int64_t stride, int n) {
-  float s = 0.f;
-  for (int q0 = 0; q0 < n; q0 += 8) {
-    float v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = q0 + u < n ? handoff_get(p + (int64_t)(q0 + u) * stride) : 0.f;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) s += v[u];
-  }
-  return s;
-}
-
 // Routed part of output rows [n0, n0 + nrows) of token t into LDS routed[]:
 // sum_k w_k (y_k[n] + a_down,k SV_down,k[n]^T), fmaf over the picks in pick
 // order (the many-token combine's order), a_down = fp16(sum of its slices'

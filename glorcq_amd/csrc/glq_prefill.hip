@@ -85,7 +85,122 @@ struct PfArgs {
   int out_bits;              // GATE/UP: decode order of inter's consumer (2 or 4)
   int max_tiles;             // token tiles in the grid (y dimension)
   float zoff;                // added to every zero-point (signed codes stored offset by 2^(b-1))
+  // a = x U formed in the same launch (dense form, no K split; pf_xu_job):
+  // row-block jobs fill the first xu_rows rows of the grid, and the epilogue
+  // waits for its token rows' blocks (a read coherently).  xu_rows == 0: a
+  // is given (or absent).
+  int xu_rows, xu_nrb, xu_ns, xu_rpad;
+  const __half* xu_u;        // U (K, rank)
+  float* xu_part;            // (nrb, ns, 16, rpad) fp32 slice partials
+  unsigned* xu_cnt;          // (nrb) words: arrivals | ready bit | readers << 16; zero between launches
+  uint64_t xu_spin;          // the epilogue's wait bound (100 MHz real-time counter ticks)
 };
+
+// The x U jobs of the fused dense launch (see PfArgs).  A row block's word:
+// low bits the slices that arrived, kXuReady once its last slice has
+// written a, then 1 << 16 per GEMM workgroup that has read it; whichever
+// event completes the final word sets it back to zero.
+constexpr unsigned kXuReady = 0x8000u;
+constexpr size_t kXuJobLds = (4 * 4 * 64) * 4 + 16 * kLowrankRows * 2 +
+                             64 * kLowrankUtStride * 2 + 16 * 128 * 4;
+
+__device__ __forceinline__ unsigned pf_xu_final(const PfArgs& g) {
+  return ((unsigned)g.ntn << 16) | kXuReady | (unsigned)g.xu_ns;
+}
+
+// Job (row block rb, K slice sp): lowrank_partial<4> over the slice, handed
+// over; the block's last slice sums the slices in slice order and writes
+// a = fp16 (agent-scope stores), then marks the block ready.
+__device__ void pf_xu_job(const PfArgs& g, int job, unsigned char* smem, int* flag) {
+  const int rb = job / g.xu_ns, sp = job - rb * g.xu_ns, tid = threadIdx.x;
+  const int r0 = 16 * rb, rows = min(16, g.M - r0), rank = g.rank, rpad = g.xu_rpad;
+  float* red = (float*)smem;
+  __half* xl = (__half*)(red + 4 * 4 * 64);
+  __half* ut = xl + 16 * kLowrankRows;
+  const __half* xb = g.xp + (int64_t)r0 * g.K;
+  auto xrow = [&](int m) { return xb + (int64_t)m * g.K; };
+  float* slices = g.xu_part + (int64_t)rb * g.xu_ns * 16 * rpad;
+  lowrank_partial<4, decltype(xrow), true>(xrow, rows, g.K, rank, rpad, g.xu_u, sp,
+                                           slices + (int64_t)sp * 16 * rpad, red, xl, tid, ut);
+  if (!handoff_arrive(g.xu_cnt + rb, (unsigned)g.xu_ns, flag)) return;
+  for (int i = tid; i < rows * rank; i += kPfThreads) {
+    const int m = i / rank, j = i - m * rank;
+    const __half v = __float2half(sum_strided_coh(slices + m * rpad + j, 16 * rpad, g.xu_ns));
+    handoff_put((uint16_t*)g.a + (int64_t)(r0 + m) * g.a_ld + j, __half_as_ushort(v));
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned old = __hip_atomic_fetch_add(g.xu_cnt + rb, kXuReady, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    if (old + kXuReady == pf_xu_final(g)) handoff_reset(g.xu_cnt + rb);
+  }
+}
+
+// The epilogue's wait for the row blocks of token rows [p0, p0 + rows): a
+// block not ready within xu_spin is formed here, slice by slice in the
+// jobs' order (the same bits), and written as the jobs write it.  Every
+// thread calls it; smem is free (the ring has drained).
+__device__ void pf_xu_wait(const PfArgs& g, int p0, int rows, unsigned char* smem, int* flag) {
+  const int rb0 = p0 / 16, rb1 = (p0 + rows - 1) / 16, tid = threadIdx.x;
+  if (tid == 0) {
+    int missing = 0;
+    for (int rb = rb0; rb <= rb1; ++rb) {
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      while (!(handoff_get(g.xu_cnt + rb) & kXuReady)) {
+        if (__builtin_amdgcn_s_memrealtime() - t0 > g.xu_spin) {
+          missing |= 1 << (rb - rb0);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    *flag = missing;
+  }
+  __syncthreads();
+  const int missing = *flag;
+  __syncthreads();
+  for (int rb = rb0; rb <= rb1; ++rb) {
+    if (!(missing & (1 << (rb - rb0)))) continue;  // uniform
+    const int r0 = 16 * rb, brows = min(16, g.M - r0), rank = g.rank, rpad = g.xu_rpad;
+    float* red = (float*)smem;
+    __half* xl = (__half*)(red + 4 * 4 * 64);
+    __half* ut = xl + 16 * kLowrankRows;
+    float* out = (float*)(ut + 64 * kLowrankUtStride);  // 16 x rpad
+    const __half* xb = g.xp + (int64_t)r0 * g.K;
+    auto xrow = [&](int m) { return xb + (int64_t)m * g.K; };
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // elements tid + 256 q of the block
+    for (int sp = 0; sp < g.xu_ns; ++sp) {
+      lowrank_partial<4>(xrow, brows, g.K, rank, rpad, g.xu_u, sp, out, red, xl, tid, ut);
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i = tid + kPfThreads * q, m = i / rpad, j = i - m * rpad;
+        if (m < brows && j < rank) acc[q] += out[m * rpad + j];
+      }
+      __syncthreads();
+    }
+    const int pad = (8 - g.xu_ns % 8) % 8;  // sum_strided's zeros after the last batch
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      for (int z = 0; z < pad; ++z) acc[q] += 0.f;
+      const int i = tid + kPfThreads * q, m = i / rpad, j = i - m * rpad;
+      if (m < brows && j < rank)
+        handoff_put((uint16_t*)g.a + (int64_t)(r0 + m) * g.a_ld + j,
+                    __half_as_ushort(__float2half(acc[q])));
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+}
+
+// 8 halves of a written inside this launch (agent-scope loads).
+__device__ __forceinline__ f16x8 pf_load8_coh(const __half* p) {
+  const unsigned long long lo = handoff_get((const unsigned long long*)p);
+  const unsigned long long hi = handoff_get((const unsigned long long*)p + 1);
+  return __builtin_bit_cast(f16x8, u32x4{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi,
+                                         (uint32_t)(hi >> 32)});
+}
 
 // Position of natural column c inside its 16-code block in decode order
 // (inverse of perm_src).
@@ -239,7 +354,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, kb = lane >> 4;
-  const int ty = blockIdx.y;
+  __shared__ int xflag;
+  if (g.xu_rows && (int)blockIdx.y < g.xu_rows) {  // an x U job (uniform)
+    const int job = blockIdx.y * gridDim.x + blockIdx.x;
+    if (job < g.xu_nrb * g.xu_ns) pf_xu_job(g, job, smem, &xflag);
+    return;
+  }
+  const int ty = blockIdx.y - g.xu_rows;
   int e = 0, p0, rows;
   if (g.tiles) {
     if (ty >= *g.ntiles) return;  // uniform over the workgroup
@@ -464,6 +585,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
   }
 
   // ---- low-rank term: y += a SV^T (a: token rows, SV: weight rows) ----
+  if (g.xu_rows && g.rank > 0) pf_xu_wait(g, p0, rows, smem, &xflag);
   if (g.a != nullptr && g.rank > 0) {
     constexpr int RM = RT / NMAT;  // row tiles per matrix
     for (int j0 = 0; j0 < g.rank; j0 += 32) {
@@ -483,7 +605,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
         for (int i = 0; i < TT; ++i) {
           const int p = p0 + min(16 * i + li, rows - 1);
           f16x8 av = f16x8{};
-          if (jv) av = *(const f16x8*)(g.a + (int64_t)p * g.a_ld + m * g.rank + jk);
+          if (jv) {
+            const __half* ap = g.a + (int64_t)p * g.a_ld + m * g.rank + jk;
+            av = g.xu_rows ? pf_load8_coh(ap) : *(const f16x8*)ap;
+          }
 #pragma unroll
           for (int q = 0; q < RM; ++q) y[i][m * RM + q] = mfma_16x16x32(av, bv[q], y[i][m * RM + q]);
         }
@@ -526,6 +651,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(PfArgs g) {
             g.yf[(int64_t)(p0 + r) * g.yf_ld + n] = y[i][rt][j];
         }
     }
+  }
+  if (g.xu_rows && g.rank > 0) {  // the workgroup has read a of its rows' blocks
+    __syncthreads();
+    if (tid == 0)
+      for (int rb = p0 / 16; rb <= (p0 + rows - 1) / 16; ++rb) {
+        const unsigned old = __hip_atomic_fetch_add(g.xu_cnt + rb, 1u << 16, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        if (old + (1u << 16) == pf_xu_final(g)) handoff_reset(g.xu_cnt + rb);
+      }
   }
 }
 
@@ -674,6 +808,36 @@ __device__ void pf_lowrank_job(const PfLowrank& L, int job, int sp, unsigned cha
   }
 }
 
+// a = fp16(x U) of the dense prefill in one launch: workgroup (row block
+// rb, K slice sp) forms the fp32 partial of 16 token rows over a slice of
+// kLowrankRows codes (lowrank_partial<4>: v_mfma_f32_16x16x32_f16 tiles
+// with U staged transposed in LDS), hands it over and counts itself in on
+// the row block's counter (glq_handoff.h); the last of the block's slices
+// sums them in slice order, rounds once and leaves the counter at zero.
+__global__ __launch_bounds__(256) void pf_xu_kernel(const __half* __restrict__ x, int M, int K,
+                                                    const __half* __restrict__ U, int rank,
+                                                    int rpad, int ns, float* part,
+                                                    unsigned* cnt, __half* __restrict__ a_out) {
+  __shared__ float red[4 * 4 * 64];
+  __shared__ __align__(16) __half xl[16 * kLowrankRows];
+  __shared__ __align__(16) __half ut[64 * kLowrankUtStride];
+  __shared__ int last;
+  const int rb = blockIdx.x / ns, sp = blockIdx.x - rb * ns, tid = threadIdx.x;
+  const int r0 = rb * 16, rows = min(16, M - r0);
+  const __half* xb = x + (int64_t)r0 * K;
+  auto xrow = [&](int m) { return xb + (int64_t)m * K; };
+  float* slices = part + (int64_t)rb * ns * 16 * rpad;  // [slice][row][rpad]
+  lowrank_partial<4, decltype(xrow), true>(xrow, rows, K, rank, rpad, U, sp,
+                                           slices + (int64_t)sp * 16 * rpad, red, xl, tid, ut);
+  if (!handoff_arrive(cnt + rb, (unsigned)ns, &last)) return;
+  for (int i = tid; i < rows * rank; i += 256) {
+    const int m = i / rank, j = i - m * rank;
+    a_out[(int64_t)(r0 + m) * rank + j] =
+        __float2half(sum_strided_coh(slices + m * rpad + j, 16 * rpad, ns));
+  }
+  if (tid == 0) handoff_reset(cnt + rb);
+}
+
 // Grid: n_jobs * ks lowrank jobs.
 __global__ __launch_bounds__(kPfThreads) void pf_lowrank_kernel(PfLowrank L) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -692,10 +856,11 @@ template <int BITS, int TM, int RT, int MODE, bool SYM, bool ZF, bool DEEP = fal
 static int pf_launch_k(const PfArgs& g, hipStream_t s) {
   static size_t attr = 64 * 1024;
   using SL = PfSlot<BITS, TM, RT, DEEP>;
-  const size_t lds = (size_t)SL::D * SL::BYTES;
+  size_t lds = (size_t)SL::D * SL::BYTES;
+  if (g.xu_rows) lds = std::max(lds, kXuJobLds);  // the x U jobs and the epilogue's local form
   int rc = set_lds_limit(pf_gemm_kernel<BITS, TM, RT, MODE, SYM, ZF, DEEP>, lds, attr);
   if (rc) return rc;
-  const dim3 grid((unsigned)(g.ntn * g.ks), (unsigned)g.max_tiles);
+  const dim3 grid((unsigned)(g.ntn * g.ks), (unsigned)(g.max_tiles + g.xu_rows));
   pf_gemm_kernel<BITS, TM, RT, MODE, SYM, ZF, DEEP><<<grid, dim3(kPfThreads), lds, s>>>(g);
   GLQ_LAUNCH_CHECK("pf_gemm_kernel");
   return GLQ_OK;
@@ -814,19 +979,28 @@ static void pf_lowrank_split(int64_t K, int& ks, int& kps) {
 struct PfDensePlan {
   int tm, rt, ntn, ntm, ks, gps, lr_ks, lr_kps;
   bool deep;
+  bool xu1;          // a = x U by pf_xu_kernel (one launch)
+  int xu_ns;         // its K slices
   int64_t a_bytes, lp_bytes, part_bytes, cnt_bytes, total;
 };
 
+// The dense prefill workspace starts with kPfSyncBytes of counter words (the
+// x U row blocks' arrivals), zero before the first call and after every
+// call, so the one-launch x U takes at most kPfSyncBytes / 4 row blocks.
+constexpr int64_t kPfSyncBytes = 4096;
+
 static PfDensePlan pf_dense_plan(int64_t M, int64_t K, int64_t N, int64_t rank, int bits) {
   PfDensePlan P;
-  // Big launches (a 64 x 128 tile per CU or more): 64- or 128-token tiles,
-  // shallow rings, two workgroups per CU.  Smaller ones: 32-token tiles of
+  // Big launches (a 64 x 128 tile per CU or more): 64-token tiles, shallow
+  // rings, two workgroups per CU.  Smaller ones: 32-token tiles of
   // 128 rows from 256 tokens, else 16-token tiles of 64 rows, with deep rings
   // (the whole K range of a small tile nearly in flight).  No K split: the
   // tiles are sized to give the chip enough workgroups without one.
   const int64_t t64 = ((M + 63) / 64) * ((N + 127) / 128);
   if (t64 >= 256) {
-    P.tm = (M >= 128 && (M / 128) * ((N + 127) / 128) >= 256) ? 128 : 64;
+    // (64-token tiles: the 128-token tile of asymmetric codes needs more
+    // than 256 VGPRs and spills)
+    P.tm = 64;
     P.rt = 2;
     P.deep = false;
   } else if (M >= 256) {
@@ -860,16 +1034,33 @@ static PfDensePlan pf_dense_plan(int64_t M, int64_t K, int64_t N, int64_t rank, 
   P.ks = (G + P.gps - 1) / P.gps;
   pf_lowrank_split(K, P.lr_ks, P.lr_kps);
   P.a_bytes = rank > 0 ? align_up(M * rank * 2, 256) : 0;
-  P.lp_bytes = rank > 0 && P.lr_ks > 1 ? align_up((int64_t)P.lr_ks * M * rank * 4, 256) : 0;
+  // a = x U in one launch (16-row blocks x K slices, last arrivers sum) when
+  // the GEMM needs no split-K counters (those are cleared by the two-launch
+  // form's first launch)
+  const int64_t nrb = (M + 15) / 16;
+  P.xu_ns = (int)((K + kLowrankRows - 1) / kLowrankRows);
+  P.xu1 = rank > 0 && rank <= 128 && P.ks == 1 && nrb <= kPfSyncBytes / 4 &&
+          !getenv("GLQ_PF_XU2");
+  if (P.xu1) {
+    const int64_t rpad = align_up(rank, 32);
+    P.lp_bytes = align_up(nrb * P.xu_ns * 16 * rpad * 4, 256);
+  } else {
+    P.lp_bytes = rank > 0 && P.lr_ks > 1 ? align_up((int64_t)P.lr_ks * M * rank * 4, 256) : 0;
+  }
   P.part_bytes = P.ks > 1 ? align_up((int64_t)P.ks * P.ntm * P.tm * P.ntn * 64 * P.rt * 4, 256)
                           : 0;
   P.cnt_bytes = P.ks > 1 ? align_up((int64_t)P.ntm * P.ntn * 4, 256) : 0;
-  P.total = P.a_bytes + P.lp_bytes + P.part_bytes + P.cnt_bytes;
+  // the counter words come first in every workspace this path uses, so no
+  // call's tables overwrite another's counters
+  const int64_t body = P.a_bytes + P.lp_bytes + P.part_bytes + P.cnt_bytes;
+  P.total = body ? kPfSyncBytes + body : 0;
   return P;
 }
 
-// Workspace of the prefill path of glq_gemm_lora (the split-K arrival
-// counters in it are zeroed by the first launch of every call).
+// Workspace of the prefill path of glq_gemm_lora: kPfSyncBytes of counter
+// words (zero before the first call, left zero by every call), then a, its
+// partials, the split-K tiles (whose arrival counters the two-launch form's
+// first launch clears); none at all when the call needs no tables.
 int64_t pf_gemm_prefill_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t rank,
                                         int bits) {
   if (M <= 0 || K <= 0 || N <= 0) return 0;
@@ -889,15 +1080,27 @@ int pf_dense_gemm(const void* x, int64_t M, int64_t K, int64_t N, const int32_t*
             "workspace of %lld bytes needed (got %lld)", (long long)P.total,
             (long long)workspace_bytes);
   GLQ_CHECK(M * K < (1ll << 31), "M*K too large for the prefill path");
-  char* w = (char*)workspace;
+  unsigned* xcnt = (unsigned*)workspace;  // zero between calls
+  char* w = (char*)workspace + (P.total ? kPfSyncBytes : 0);
   __half* abuf = P.a_bytes ? (__half*)w : nullptr;
   float* lpart = P.lp_bytes ? (float*)(w + P.a_bytes) : nullptr;
   char* w3 = w + P.a_bytes + P.lp_bytes;
   float* part = P.ks > 1 ? (float*)w3 : nullptr;
   unsigned* cnt = P.ks > 1 ? (unsigned*)(w3 + P.part_bytes) : nullptr;
-  // launch 1 (when U is given, or split-K counters need clearing): the split
-  // partials of a = x U, summed by a finalize launch
-  if (P.a_bytes || cnt) {
+  const bool fused = P.xu1 && xU == nullptr && !getenv("GLQ_PF_XU1");
+  if (fused) {
+    // a = x U in the GEMM's launch (its first grid rows)
+  } else if (P.xu1 && xU == nullptr) {
+    // launch 1: a = x U in one launch (its row blocks count on the
+    // workspace's first words)
+    const int nrb = (int)((M + 15) / 16);
+    pf_xu_kernel<<<dim3((unsigned)(nrb * P.xu_ns)), dim3(256), 0, s>>>(
+        (const __half*)x, (int)M, (int)K, (const __half*)U, (int)rank,
+        (int)align_up(rank, 32), P.xu_ns, lpart, xcnt, abuf);
+    GLQ_LAUNCH_CHECK("pf_xu_kernel");
+  } else if (P.a_bytes || cnt) {
+    // launch 1 (when U is given, or split-K counters need clearing): the split
+    // partials of a = x U, summed by a finalize launch
     PfLowrank L = {};
     L.x = (const __half*)x;
     L.aperm = 0;
@@ -942,6 +1145,19 @@ int pf_dense_gemm(const void* x, int64_t M, int64_t K, int64_t N, const int32_t*
   g.gps = P.gps;
   g.max_tiles = P.ntm;
   g.zoff = sym == 2 ? (float)(1 << (bits - 1)) : 0.f;
+  if (fused) {
+    g.xu_nrb = (int)((M + 15) / 16);
+    g.xu_ns = P.xu_ns;
+    g.xu_rows = (int)((g.xu_nrb * g.xu_ns + g.ntn * g.ks - 1) / (g.ntn * g.ks));
+    g.xu_rpad = (int)align_up(rank, 32);
+    g.xu_u = (const __half*)U;
+    g.xu_part = lpart;
+    g.xu_cnt = xcnt;
+    // GLQ_PF_SPIN_TICKS: the epilogue's wait bound (tests set 0 to take the
+    // local form)
+    const char* e = getenv("GLQ_PF_SPIN_TICKS");
+    g.xu_spin = e ? (uint64_t)strtoull(e, nullptr, 10) : 100000;  // 1 ms
+  }
   return pf_launch_dense(g, bits, PfTile{P.tm, P.rt, P.deep}, sym == 1, s);
 }
 }  // namespace glq

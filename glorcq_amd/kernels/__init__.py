@@ -114,6 +114,29 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+# GEMM workspaces: (device index, stream handle) -> zero-filled uint8 tensor
+_gemm_workspaces: dict = {}
+
+
+def gemm_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Workspace of glq_gemm_lora, one per (device, current stream): its first
+    4096 bytes are the x U row blocks' arrival counters, zero between calls,
+    so it is allocated zero-filled and serves no other entry point.  A
+    replaced buffer is kept alive (a captured graph may still use it)."""
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (idx, _lib.stream_handle(dev))
+    ws = _gemm_workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, 1 << 16)
+        if ws is not None:
+            size = max(size, 2 * ws.numel())
+        retire_workspace(ws)
+        ws = torch.zeros(size, dtype=torch.uint8, device=dev)
+        _gemm_workspaces[key] = ws
+    return ws
+
+
 def packed_dequant_matmul_fused(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
                                 zeros: torch.Tensor | None, bits: int, groupsize: int,
                                 sym: bool = False, U: torch.Tensor | None = None,
@@ -204,7 +227,7 @@ def _packed_dequant_matmul_eager(x: torch.Tensor, codes: torch.Tensor, scales: t
     if M > GEMV_MAX_M and groupsize == 128:
         # prefill: one MFMA GEMM over all M rows (glq_gemm_lora)
         nbytes = lib.glq_gemm_workspace_bytes(M, K, N, rank if precomputed_xU is None else 0)
-        ws = workspace(x.device, nbytes)
+        ws = gemm_workspace(x.device, nbytes)
         rc = lib.glq_gemm_lora(
             x.data_ptr(), M, K, N, codes.data_ptr(), bits, scales.data_ptr(), _lib.ptr(zeros),
             groupsize, _sym_mode(sym), _lib.ptr(U if precomputed_xU is None else None),

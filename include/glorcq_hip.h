@@ -194,9 +194,14 @@ int glq_lowrank_xu_routed(int64_t picks, const void* x, int64_t K, const void* U
  * (inference/quantized_linear.py:338-349).  Group 128.  Codes decode into
  * exact fp16 operands (q - zero-point's integer part) of
  * v_mfma_f32_16x16x32_f16, each group's fp32 sum scaled once (any zero-point,
- * symmetric or not); a = fp16(x U) comes from xU or from a low-rank launch.
- * The workspace (glq_gemm_workspace_bytes, 256-byte aligned) is required; it
- * needs no initialisation.
+ * symmetric or not); a = fp16(x U) comes from xU or from a low-rank launch
+ * before the GEMM (rank <= 128: one launch whose 16-row blocks' K slices
+ * hand their partial sums to the block's last arriving slice).
+ * The workspace (glq_gemm_workspace_bytes, 256-byte aligned) is required.
+ * When U is given (no xU) its first 4096 bytes are arrival counters: they
+ * must be zero before the workspace's first use with glq_gemm_lora (allocate
+ * it zero-filled) and every call leaves them zero; do not share the buffer
+ * with other entry points.  The rest needs no initialisation.
  */
 int64_t glq_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t rank);
 int glq_gemm_lora(const void* x, int64_t M, int64_t K, int64_t N,

@@ -208,3 +208,58 @@ def test_tile_configs(gpu, monkeypatch, cfg, bits):
     ys = K_.packed_dequant_matmul_fused(ds["x"], ds["codes"], ds["scales"], None, bits, 128,
                                         sym=True, U=ds["U"], SV=ds["SV"])
     assert_parity(ys, oracle_y(ps), f"cfg {cfg} bits {bits} sym")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N,bits", [(128, 2048, 1408, 2), (77, 2048, 512, 4),
+                                        (512, 1408, 2048, 2), (4100, 1024, 256, 4)])
+def test_one_launch_xu(gpu, monkeypatch, M, K, N, bits):
+    """a = x U of the prefill formed in the GEMM's own launch (16-row blocks
+    over K slices in the first grid rows, the block's last arriving slice sums
+    them; the GEMM's epilogue waits for its rows' blocks): parity, the same
+    bits on repeated calls and graph replays (the arrival counters are left at
+    zero), with every epilogue wait bounded at zero ticks (GLQ_PF_SPIN_TICKS=0:
+    a block not yet ready is formed in the waiting workgroup, in the same
+    order) and from the separate one-launch x U (GLQ_PF_XU1); the two-launch
+    form (GLQ_PF_XU2) within the parity bar."""
+    p = fmt.make_linear(K, N, bits=bits, rank=64, M=M, seed=M + K)
+    d = to(p, gpu)
+    print(f"one-launch x U M={M} K={K} N={N} bits={bits}", flush=True)
+
+    def call(out=None):
+        return K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], bits,
+                                              128, U=d["U"], SV=d["SV"], out=out)
+
+    y = call()
+    torch.cuda.synchronize()
+    assert_parity(y, oracle_y(p), f"M={M}")
+    for i in range(2):
+        assert torch.equal(call(), y), f"repeat {i}"
+    out = torch.empty_like(y)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call(out)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call(out)
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y), f"replay {i}"
+        _ = (d["x"].float() * 2).sum().item()  # eager work between replays
+    monkeypatch.setenv("GLQ_PF_SPIN_TICKS", "0")
+    for i in range(2):
+        assert torch.equal(call(), y), f"zero-tick wait {i}"
+    monkeypatch.delenv("GLQ_PF_SPIN_TICKS")
+    monkeypatch.setenv("GLQ_PF_XU1", "1")
+    assert torch.equal(call(), y), "separate one-launch x U"
+    monkeypatch.delenv("GLQ_PF_XU1")
+    assert torch.equal(call(), y), "fused again"
+    monkeypatch.setenv("GLQ_PF_XU2", "1")
+    y2 = call()
+    torch.cuda.synchronize()
+    assert_parity(y2, oracle_y(p), f"two-launch x U M={M}")
