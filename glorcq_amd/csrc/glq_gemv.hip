@@ -49,6 +49,16 @@ struct DenseArgs {
   // item i's U is U + uidx[i] * u_es (null: U + i * u_es); nuidx U matrices
   const int32_t* uidx = nullptr;
   int nuidx = 0;
+  // a = x U formed in the token-tile launch (t16_xu_job): xt_jobs workgroups
+  // of (item, pair of K slices) come first; item i's word xt_cnt[i] holds
+  // its slices' arrivals, kXtReady once a is written, then 1 << 16 per
+  // row-block workgroup that has read it; zero between launches
+  int xt_jobs = 0;
+  int xt_rb = 0;             // row blocks an item (its readers)
+  unsigned* xt_cnt = nullptr;
+  float* xt_part = nullptr;  // (items, P, M, rpad) slice partials
+  __half* xt_a = nullptr;    // (items, M, rank)
+  uint64_t xt_spin = 0;
   __device__ int64_t u_index(int item) const {
     return uidx ? (int64_t)min(max(uidx[item], 0), nuidx - 1) : (int64_t)item;
   }
@@ -127,10 +137,13 @@ struct LaneArgs {
 // asymmetric codes, each decoded once for all M <= 16 token rows): y = Q(x)
 // + a SV^T + bias, a = fp16 of the x U partials' sum (DenseSrc::load_a),
 // staged in LDS by prep.
+__device__ void t16_xu_wait(const DenseArgs& a, int item, __half* al, float* lds);
+
 struct DenseTileView {
   const DenseArgs& a;
   int item;
   __half* al;  // LDS [M][rank]
+  float* lds;  // the launch's LDS (the fused form's local x U)
   __device__ DenseTileView bind() const { return *this; }
   __device__ const uint32_t* codes(int) const { return a.codes + (int64_t)item * a.codes_es; }
   __device__ const __half* scales(int) const { return a.scales + (int64_t)item * a.sz_es; }
@@ -138,9 +151,12 @@ struct DenseTileView {
   __device__ const __half* xrow(int t) const {
     return a.x + (int64_t)item * a.x_es + (int64_t)t * a.sh.K;
   }
+  __device__ void before_store() const {
+    if (a.sv && a.xt_jobs) t16_xu_wait(a, item, al, lds);  // (uniform)
+  }
   __device__ void prep(int, int, int) const {
     const int r = a.sh.rank;
-    if (!a.sv) return;  // uniform over the workgroup
+    if (!a.sv || a.xt_jobs) return;  // uniform over the workgroup
     const DenseSrc d{a};
     for (int i = threadIdx.x; i < a.M * r; i += kT16Waves * 64) {
       const int t = i / r;
@@ -166,13 +182,133 @@ struct DenseTileView {
   }
 };
 
-// Workgroup b = item RB + row block: one K slice (GPW groups a wave cover the row).
+// LDS (floats) of one 256-thread group of lowrank_partial<4>: red, the x
+// slice, U transposed, and a 16 x 128 output block.
+constexpr int kXtGroupLds = 4 * 4 * 64 + 16 * kLowrankRows / 2 + 64 * kLowrankUtStride / 2;
+constexpr int kXtLds = (2 * kXtGroupLds + 2 * 16 * 128) * 4;  // bytes: two groups, two blocks
+constexpr unsigned kXtReady = 0x8000u;
+
+__device__ __forceinline__ unsigned t16_xu_final(const DenseArgs& a) {
+  return ((unsigned)a.xt_rb << 16) | kXtReady | (unsigned)a.P;
+}
+
+// Slices 2 jp and 2 jp + 1 of item i's x U partials, one per 256-thread half
+// of the workgroup (lowrank_partial<4>: MFMA tiles, U transposed in LDS);
+// COH: into global memory for other workgroups, else into LDS.  Every thread
+// calls it.
+template <bool COH>
+__device__ void t16_xu_pair(const DenseArgs& a, int item, int jp, float* lds, float* out0,
+                            float* out1) {
+  const int half = threadIdx.x >> 8, tid = threadIdx.x & 255, sp = 2 * jp + half;
+  float* g = lds + half * kXtGroupLds;
+  __half* xl = (__half*)(g + 4 * 4 * 64);
+  __half* ut = xl + 16 * kLowrankRows;
+  const __half* X = a.x + (int64_t)item * a.x_es;
+  auto xrow = [&](int m) { return X + (int64_t)m * a.sh.K; };
+  float* out = half ? out1 : out0;
+  if (sp >= a.P) out = nullptr;
+  lowrank_partial<4, decltype(xrow), COH>(xrow, a.M, a.sh.K, a.sh.rank, a.sh.rpad,
+                                           a.u + a.u_index(item) * a.u_es, min(sp, a.P - 1),
+                                           out, g, xl, tid, ut);
+}
+
+// Job (item, slice pair): its partials handed over; the item's last slice to
+// arrive sums the slices in slice order into a = fp16 (agent-scope stores)
+// and marks the item ready.
+__device__ void t16_xu_job(const DenseArgs& a, int job, float* lds) {
+  __shared__ int last;
+  const int npair = (a.P + 1) / 2, item = job / npair, jp = job - item * npair;
+  const int rp = a.sh.rpad, M = a.M, rank = a.sh.rank;
+  float* parts = a.xt_part + (int64_t)item * a.P * M * rp;
+  t16_xu_pair<true>(a, item, jp, lds, parts + (int64_t)(2 * jp) * M * rp,
+              parts + (int64_t)(2 * jp + 1) * M * rp);
+  const unsigned mine = (unsigned)min(2, a.P - 2 * jp);  // slices this job formed
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(a.xt_cnt + item, mine, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT) + mine == (unsigned)a.P;
+  __syncthreads();
+  if (!last) return;
+  for (int i = threadIdx.x; i < M * rank; i += kT16Waves * 64) {
+    const int m = i / rank, j = i - m * rank;
+    const __half v = __float2half(sum_strided_coh(parts + m * rp + j, (int64_t)M * rp, a.P));
+    handoff_put((uint16_t*)a.xt_a + (int64_t)item * M * rank + i, __half_as_ushort(v));
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned old = __hip_atomic_fetch_add(a.xt_cnt + item, kXtReady, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    if (old + kXtReady == t16_xu_final(a)) handoff_reset(a.xt_cnt + item);
+  }
+}
+
+// Before a row block's stores: item's a into LDS al.  A wait that outlasts
+// xt_spin forms it here, slice by slice in the jobs' order (the same bits).
+// Every thread calls it.
+__device__ void t16_xu_wait(const DenseArgs& a, int item, __half* al, float* lds) {
+  __shared__ int ok;
+  const int M = a.M, rank = a.sh.rank, rp = a.sh.rpad, tid = threadIdx.x;
+  __syncthreads();  // every thread is past the block sums: the LDS is free
+  if (tid == 0) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    int r = 1;
+    while (!(handoff_get(a.xt_cnt + item) & kXtReady)) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > a.xt_spin) {
+        r = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    ok = r;
+  }
+  __syncthreads();
+  if (ok) {
+    for (int i = tid; i < M * rank; i += kT16Waves * 64)
+      al[i] = __ushort_as_half(handoff_get((const uint16_t*)a.xt_a + (int64_t)item * M * rank + i));
+  } else {
+    float* outs = lds + 2 * kXtGroupLds;  // two 16 x rpad partial blocks
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // elements tid + 512 q
+    for (int jp = 0; jp < (a.P + 1) / 2; ++jp) {
+      t16_xu_pair<false>(a, item, jp, lds, outs, outs + 16 * 128);
+      __syncthreads();
+      for (int h = 0; h < 2 && 2 * jp + h < a.P; ++h)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int i = tid + kT16Waves * 64 * q, m = i / rank, j = i - m * rank;
+          if (m < M) acc[q] += outs[h * 16 * 128 + m * rp + j];
+        }
+      __syncthreads();
+    }
+    const int pad = (8 - a.P % 8) % 8;  // sum_strided's zeros after the last batch
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      for (int z = 0; z < pad; ++z) acc[q] += 0.f;
+      const int i = tid + kT16Waves * 64 * q, m = i / rank;
+      if (m < M) al[i] = __float2half(acc[q]);
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {  // this row block has read item's a
+    const unsigned old = __hip_atomic_fetch_add(a.xt_cnt + item, 1u << 16, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    if (old + (1u << 16) == t16_xu_final(a)) handoff_reset(a.xt_cnt + item);
+  }
+}
+
+// Workgroup b = item RB + row block: one K slice (GPW groups a wave cover the
+// row); with the in-launch x U, its jobs come first.
 template <int GPW>
 __global__ __launch_bounds__(kT16Waves * 64) void gemv_t16_kernel(DenseArgs a, T16Geom tg) {
   extern __shared__ __align__(16) float lds[];
-  const int item = blockIdx.x / tg.RB;
+  if ((int)blockIdx.x < a.xt_jobs) {  // (uniform)
+    t16_xu_job(a, blockIdx.x, lds);
+    return;
+  }
+  const int b = blockIdx.x - a.xt_jobs, item = b / tg.RB;
   __half* al = (__half*)(lds + t16_lds_bytes(false) / 4);
-  t16_run<DenseTileView, false, GPW>(DenseTileView{a, item, al}, tg, blockIdx.x - item * tg.RB,
+  t16_run<DenseTileView, false, GPW>(DenseTileView{a, item, al, lds}, tg, b - item * tg.RB,
                                      lds);
 }
 
@@ -261,6 +397,15 @@ static int64_t workspace_need(int64_t items, int64_t M, int64_t K, int64_t rank)
   if (rank <= 0) return 0;
   const int64_t rpad = align_up(rank, 32);
   return align_up(items * lowrank_slices(K) * M * rpad * 4, 256);
+}
+
+// The GEMV entry points' workspace: kGemvSyncBytes of counter words (zero
+// before the first call, left zero by every call), the x U partials, and
+// the token-tile form's a (items x M x rank fp16).
+constexpr int64_t kGemvSyncBytes = 4096;
+static int64_t gemv_workspace_need(int64_t items, int64_t M, int64_t K, int64_t rank) {
+  if (rank <= 0) return 0;
+  return kGemvSyncBytes + workspace_need(items, M, K, rank) + align_up(items * M * rank * 2, 256);
 }
 
 // Codes per K-phase: the whole K when x fits the staging budget, else the
@@ -559,12 +704,13 @@ static int launch_t16_gemv(const DenseArgs& a, hipStream_t s) {
   tg.M = a.M;
   tg.RB = (a.sh.N + kT16Rows - 1) / kT16Rows;
   tg.ks = 1;
-  const size_t lds = (size_t)t16_lds_bytes(false) + 2 * (size_t)a.M * a.sh.rank;
+  size_t lds = (size_t)t16_lds_bytes(false) + 2 * (size_t)a.M * a.sh.rank;
+  if (a.xt_jobs) lds = std::max(lds, (size_t)kXtLds);
   static size_t attr = 64 * 1024;
   int rc = set_lds_limit(gemv_t16_kernel<GPW>, lds, attr);
   if (rc) return rc;
-  gemv_t16_kernel<GPW><<<dim3((unsigned)((int64_t)a.items * tg.RB)), dim3(kT16Waves * 64), lds,
-                         s>>>(a, tg);
+  gemv_t16_kernel<GPW><<<dim3((unsigned)(a.xt_jobs + (int64_t)a.items * tg.RB)),
+                         dim3(kT16Waves * 64), lds, s>>>(a, tg);
   GLQ_LAUNCH_CHECK("gemv_t16_kernel");
   return GLQ_OK;
 }
@@ -614,7 +760,11 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   // one token row with U given: the lane kernel forms a = x U itself (one
   // launch, no workspace); GLQ_LANE_NO_XU=1 keeps the separate partial-sum launch
   const bool lane_xu = need_partials && lane_shape(M, sh, bits) && !getenv("GLQ_LANE_NO_XU");
-  const int64_t need = need_partials && !lane_xu ? workspace_need(items, M, K, rank) : 0;
+  // the token-tile form with x U formed in its own launch (GLQ_T16_XU2=1: the
+  // separate partial-sum launch)
+  const bool t16_xu = need_partials && !lane_shape(M, sh, bits) && t16_gemv_gpw(M, sh, bits) &&
+                      M <= 16 && items <= kGemvSyncBytes / 4 && !getenv("GLQ_T16_XU2");
+  const int64_t need = need_partials && !lane_xu ? gemv_workspace_need(items, M, K, rank) : 0;
   if (need > 0) {
     GLQ_CHECK(workspace != nullptr && workspace_bytes_given >= need,
               "workspace of %lld bytes needed (got %lld)", (long long)need,
@@ -641,7 +791,10 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   a.y_es = y_stride;
   a.xu = lora ? (const __half*)xU : nullptr;
   a.xu_es = xu_stride;
-  a.apart = need_partials && !lane_xu ? (const float*)workspace : nullptr;
+  // workspace: kGemvSyncBytes of counter words (zero between calls), then
+  // the x U partials (and the token-tile form's a)
+  a.apart = need_partials && !lane_xu ? (const float*)((char*)workspace + kGemvSyncBytes)
+                                      : nullptr;
   a.items = (int)items;
   a.M = (int)M;
   a.P = need_partials && !lane_xu ? (int)lowrank_slices(K) : 0;
@@ -653,7 +806,17 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   GLQ_CHECK(items * a.tiles < (1ll << 31) && items * a.P < (1ll << 31), "too many workgroups");
   hipStream_t s = (hipStream_t)stream;
   if (lane_xu) return launch_lane(a, bits, true, s);
-  if (need_partials) {
+  if (t16_xu) {
+    a.xt_jobs = (int)(items * ((a.P + 1) / 2));
+    a.xt_rb = (int)((N + kT16Rows - 1) / kT16Rows);
+    a.xt_cnt = (unsigned*)workspace;
+    a.xt_part = (float*)a.apart;
+    a.xt_a = (__half*)((char*)workspace + kGemvSyncBytes + workspace_need(items, M, K, rank));
+    // GLQ_T16_SPIN_TICKS: the stores' wait bound (tests set 0 to take the
+    // local x U)
+    const char* e = getenv("GLQ_T16_SPIN_TICKS");
+    a.xt_spin = e ? (uint64_t)strtoull(e, nullptr, 10) : 100000;  // 1 ms
+  } else if (need_partials) {
     const dim3 grid((unsigned)(items * a.P));
     if (M == 1) lowrank_partial_kernel<1><<<grid, dim3(256), 0, s>>>(a);
     else if (M == 2) lowrank_partial_kernel<2><<<grid, dim3(256), 0, s>>>(a);
@@ -740,7 +903,7 @@ int glq_gemv_lora_noalloc(const void* x, int64_t M, int64_t K, int64_t N,
   clear_error();
   GLQ_CHECK(M >= 0 && K >= 0 && N >= 0 && rank >= 0, "negative size");
   const bool partials = SV != nullptr && rank > 0 && xU == nullptr && M > 0 && N > 0;
-  const int64_t need = partials ? workspace_need(1, M, K, rank) : 0;
+  const int64_t need = partials ? gemv_workspace_need(1, M, K, rank) : 0;
   GLQ_CHECK(need <= kScratchBytes,
             "x*U partials need %lld bytes, above the %lld-byte static scratch of the "
             "allocation-free entry point (use glq_gemv_lora with a workspace)",
@@ -758,7 +921,7 @@ int64_t glq_gemv_workspace_bytes(int64_t items, int64_t M, int64_t K, int64_t N,
                                  int64_t rank) {
   (void)N;
   if (items < 0 || M < 0 || K < 0 || rank < 0) return -1;
-  return workspace_need(items, M, K, rank);
+  return gemv_workspace_need(items, M, K, rank);
 }
 
 int glq_gemv_lora(const void* x, int64_t M, int64_t K, int64_t N,

@@ -274,6 +274,7 @@ struct SguTileView {
   __device__ const __half* zeros(int m) const { return a.szeros[m]; }
   __device__ const __half* xrow(int t) const { return a.h + (int64_t)t * a.H; }
   __device__ void prep(int, int, int) const {}
+  __device__ void before_store() const {}
   __device__ void store(int n, int t, float g, float u) const {
     a.sinter[(int64_t)t * a.SI + n] = swiglu_fp16(g, u);
   }
@@ -449,6 +450,7 @@ struct SdTileView {
       if (n < a.H) handoff_put(a.rtd + (int64_t)t * a.H + n, acc);
     }
   }
+  __device__ void before_store() const {}
   // out = fp16(routed + gate * fp16(shared)) (+ residual)
   __device__ void store(int n, int t, float v) const {
     float acc = handoff_get(a.rtd + (int64_t)t * a.H + n);

@@ -103,8 +103,10 @@ __device__ __forceinline__ void t16_elem(int e, int rb, int& n, int& t) {
 // t16_lds_bytes; what it writes for the finishing workgroup must go out
 // through handoff_put) and store(n, t, y) / PAIR store(n, t, y0, y1), called
 // for every output of the row block by the workgroup that finishes it
-// (reading prep's data through handoff_get).  All 512 threads of the workgroup
-// call t16_run (barriers inside).
+// (reading prep's data through handoff_get); before_store() is called by
+// every thread of that workgroup right before its stores (it may hold
+// barriers and use all of the LDS: the block is in registers by then).  All
+// 512 threads of the workgroup call t16_run (barriers inside).
 template <class Src, bool PAIR, int GPW = 1>
 __device__ void t16_run(const Src& srcs, const T16Geom& tg, int wg, float* lds) {
   constexpr int M2 = PAIR ? 2 : 1;
@@ -227,6 +229,7 @@ __device__ void t16_run(const Src& srcs, const T16Geom& tg, int wg, float* lds) 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // prep's stores, for the store phase
     __syncthreads();
   }
+  src.before_store();
 #pragma unroll
   for (int q = 0; q < EPT; ++q) {
     int n, t;

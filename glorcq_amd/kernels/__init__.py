@@ -114,8 +114,24 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
-# GEMM workspaces: (device index, stream handle) -> zero-filled uint8 tensor
+def _zeroed_buffer(table: dict, device: torch.device, nbytes: int) -> torch.Tensor:
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (idx, _lib.stream_handle(dev))
+    ws = table.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, 1 << 16)
+        if ws is not None:
+            size = max(size, 2 * ws.numel())
+        retire_workspace(ws)
+        ws = torch.zeros(size, dtype=torch.uint8, device=dev)
+        table[key] = ws
+    return ws
+
+
+# GEMM and GEMV workspaces: (device index, stream handle) -> zero-filled uint8 tensor
 _gemm_workspaces: dict = {}
+_gemv_workspaces: dict = {}
 
 
 def gemm_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
@@ -123,18 +139,14 @@ def gemm_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     4096 bytes are the x U row blocks' arrival counters, zero between calls,
     so it is allocated zero-filled and serves no other entry point.  A
     replaced buffer is kept alive (a captured graph may still use it)."""
-    dev = torch.device(device)
-    idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    key = (idx, _lib.stream_handle(dev))
-    ws = _gemm_workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        size = max(nbytes, 1 << 16)
-        if ws is not None:
-            size = max(size, 2 * ws.numel())
-        retire_workspace(ws)
-        ws = torch.zeros(size, dtype=torch.uint8, device=dev)
-        _gemm_workspaces[key] = ws
-    return ws
+    return _zeroed_buffer(_gemm_workspaces, device, nbytes)
+
+
+def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Workspace of the glq_gemv_lora* entry points, one per (device, current
+    stream), zero-filled and for them alone: its first 4096 bytes are the
+    token-tile launch's x U arrival counters, zero between calls."""
+    return _zeroed_buffer(_gemv_workspaces, device, nbytes)
 
 
 def packed_dequant_matmul_fused(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
@@ -239,7 +251,7 @@ def _packed_dequant_matmul_eager(x: torch.Tensor, codes: torch.Tensor, scales: t
         m1 = min(M, m0 + GEMV_MAX_M)
         mb = m1 - m0
         nbytes = lib.glq_gemv_workspace_bytes(1, mb, K, N, rank if precomputed_xU is None else 0)
-        ws = workspace(x.device, nbytes)
+        ws = gemv_workspace(x.device, nbytes)
         xu = None if precomputed_xU is None else precomputed_xU[m0:m1]
         rc = lib.glq_gemv_lora(
             x[m0:m1].data_ptr(), mb, K, N, codes.data_ptr(), bits, scales.data_ptr(),
@@ -332,7 +344,7 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
     xu = precomputed_xU if SV is not None else None
     lib = _lib.load()
     nbytes = lib.glq_gemv_workspace_bytes(E, M, K, N, rank if xu is None else 0)
-    ws = workspace(x.device, nbytes)
+    ws = gemv_workspace(x.device, nbytes)
     if u_index is not None and SV is not None and xu is None:
         rc = lib.glq_gemv_lora_clustered(
             E, x.data_ptr(), x_stride, M, K, N, codes.data_ptr(),

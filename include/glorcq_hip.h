@@ -58,10 +58,14 @@ const char* glq_last_error(void);
 /*
  * Bytes of workspace glq_gemv_lora / glq_gemv_lora_batched need for `items`
  * independent problems of shape (M, K, N, rank) when they compute a = x U
- * themselves (0 when rank == 0).  The workspace holds fp32 partial sums of a
- * over K-slices of U, written by a first launch and read by the second on the
- * same stream; it needs no initialisation.  Calls that may run concurrently
- * (different streams) need different workspaces.
+ * themselves (0 when rank == 0).  Its first 4096 bytes are arrival counters
+ * (the 4..16-row token-tile launch forms a = x U in its own first
+ * workgroups and hands it to the rest): they must be zero before the
+ * workspace's first use with these entry points (allocate it zero-filled),
+ * every call leaves them zero, and the buffer must serve no other entry
+ * point.  The rest holds fp32 partial sums of a over K-slices of U and needs
+ * no initialisation.  Calls that may run concurrently (different streams)
+ * need different workspaces.
  */
 int64_t glq_gemv_workspace_bytes(int64_t items, int64_t M, int64_t K,
                                  int64_t N, int64_t rank);
@@ -83,8 +87,12 @@ int64_t glq_gemv_workspace_bytes(int64_t items, int64_t M, int64_t K,
  *   bias      optional (N) fp16
  *   workspace device buffer of glq_gemv_workspace_bytes(1, M, K, N, rank),
  *             256-byte aligned (may be NULL when xU is given or rank == 0)
- * Launches: a K-sliced x*U partial-sum kernel (only when U is used), then the
- * GEMV kernel, whose epilogue adds a*SV^T with MFMA and rounds once to fp16.
+ * Launches: M == 1 (code rows of at most 128 16-byte pieces): one, whose
+ * workgroups form a = x*U, the GEMV and a*SV^T; 4..16 rows of 4-bit codes
+ * (the token-tile form): one, whose first workgroups form a = x*U and hand it
+ * to the row blocks' stores; otherwise a K-sliced x*U partial-sum kernel
+ * (only when U is used), then the GEMV kernel, whose epilogue adds a*SV^T
+ * and rounds once to fp16.
  */
 int glq_gemv_lora(const void* x, int64_t M, int64_t K, int64_t N,
                   const int32_t* codes, int bits, const void* scales,
@@ -104,7 +112,8 @@ int glq_gemv_lora(const void* x, int64_t M, int64_t K, int64_t N,
  * when U is used) fail with GLQ_ERR_INVALID.  Every call on one GPU shares
  * that GPU's scratch: calls that may overlap on one GPU (different streams,
  * or different host threads) race and must be ordered by the caller.  The
- * partials are fully rewritten by each call, so nothing needs clearing.
+ * scratch's counter words start at zero (static device memory) and every
+ * call leaves them zero; the partials are fully rewritten by each call.
  */
 int64_t glq_gemv_noalloc_max_scratch_bytes(void);
 int glq_gemv_lora_noalloc(const void* x, int64_t M, int64_t K, int64_t N,

@@ -69,7 +69,7 @@ def test_replaced_workspace_survives_for_captured_graph(gpu):
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         eager = K_.packed_dequant_matmul_fused(*args, **kw).clone()
-        ws0 = K_.workspace(gpu, 1)
+        ws0 = K_.gemv_workspace(gpu, 1)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
@@ -78,7 +78,7 @@ def test_replaced_workspace_survives_for_captured_graph(gpu):
     with torch.cuda.stream(stream):
         K_.packed_dequant_matmul_fused(d(big.x), d(big.codes), d(big.scales), d(big.zeros), 4,
                                        128, U=d(big.U), SV=d(big.SV))
-        ws1 = K_.workspace(gpu, 1)
+        ws1 = K_.gemv_workspace(gpu, 1)
     torch.cuda.synchronize()
     assert ws1.data_ptr() != ws0.data_ptr(), "the large call should have grown the workspace"
     del ws0

@@ -479,8 +479,8 @@ def test_token_tile_path(gpu, monkeypatch, K, N, M, items):
     (glq_tile16.h via gemv_t16_kernel: each code decoded once for every row;
     1, 2 or 4 groups a wave for K up to 1024, 2048, 4096; N = 1400 leaves a
     ragged row block, K = 768 idle waves): against the oracle, with LoRA from
-    U (the partial-sum launch) and bias, with a precomputed xU, and against the
-    streaming kernel forced on the same inputs (GLQ_GEMV_NO_T16)."""
+    U (x U formed in the same launch) and bias, with a precomputed xU, and
+    against the streaming kernel forced on the same inputs (GLQ_GEMV_NO_T16)."""
     ps = [fmt.make_linear(K, N, bits=4, group=128, rank=64, M=M, seed=K + N + M + e)
           for e in range(items)]
     bias = (torch.randn(items, N, generator=torch.Generator().manual_seed(3)) * 0.1).half()
@@ -496,6 +496,21 @@ def test_token_tile_path(gpu, monkeypatch, K, N, M, items):
     yx = K_.packed_dequant_matmul_batched(*args, SV=st("SV"), precomputed_xU=xu.half().to(gpu))
     for e, p in enumerate(ps):
         assert_parity(yx[e], oracle_y(p, xu=xu[e].half().float()), f"tile form xU item {e}")
+    # x U formed in the tile form's own launch (its first workgroups, handed
+    # over) against the separate partial-sum launch (GLQ_T16_XU2) and against
+    # row blocks whose wait is bounded at zero ticks (GLQ_T16_SPIN_TICKS=0:
+    # a formed in the waiting workgroup): the same sums in the same order
+    monkeypatch.setenv("GLQ_T16_XU2", "1")
+    y3 = K_.packed_dequant_matmul_batched(*args, U=st("U"), SV=st("SV"), bias=bias.to(gpu))
+    monkeypatch.delenv("GLQ_T16_XU2")
+    monkeypatch.setenv("GLQ_T16_SPIN_TICKS", "0")
+    y4 = K_.packed_dequant_matmul_batched(*args, U=st("U"), SV=st("SV"), bias=bias.to(gpu))
+    monkeypatch.delenv("GLQ_T16_SPIN_TICKS")
+    y5 = K_.packed_dequant_matmul_batched(*args, U=st("U"), SV=st("SV"), bias=bias.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(y, y3), "in-launch x U vs the separate launch"
+    assert torch.equal(y, y4), "zero-tick wait"
+    assert torch.equal(y, y5), "in-launch x U after the local runs"
     monkeypatch.setenv("GLQ_GEMV_NO_T16", "1")
     ys = K_.packed_dequant_matmul_batched(*args, U=st("U"), SV=st("SV"), bias=bias.to(gpu))
     _check(y, ys.float(), "tile form vs streaming kernel")

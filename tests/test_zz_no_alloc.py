@@ -19,7 +19,7 @@ def _call_pair(lib, dev, p, stream):
     y_ref = torch.empty(M, N, dtype=torch.float16, device=dev)
     y_new = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
     nbytes = lib.glq_gemv_workspace_bytes(1, M, K, N, r)
-    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=dev)  # counter words at zero
     args = (d["x"].data_ptr(), M, K, N, d["codes"].data_ptr(), p.bits, d["scales"].data_ptr(),
             d["zeros"].data_ptr(), p.group, 0, d["U"].data_ptr(), d["SV"].data_ptr(), r, None,
             None)
