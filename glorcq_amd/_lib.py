@@ -77,10 +77,22 @@ SIGNATURES = {
         _vp, _vp, _i64,                 # scales, zeros, sz_stride
         _i64, _c_int,                   # group, sym
         _vp, _i64, _vp, _i64,           # U, u_stride, u_index, n_u
+        _vp, _i64,                      # xU (per U), xu_stride
         _vp, _i64, _i64,                # SV, sv_stride, rank
         _vp, _i64,                      # bias, bias_stride
         _vp, _i64,                      # y, y_stride
         _vp, _i64, _vp,                 # workspace, bytes, stream
+    ]),
+    "glq_gemv_lora_parts": (_c_int, [
+        _i64, _vp, _i64,                # items, x, x_stride
+        _i64, _i64, _i64,               # M, K, N
+        _vp, _i64, _c_int,              # codes, codes_stride, bits
+        _vp, _vp, _i64,                 # scales, zeros, sz_stride
+        _i64, _c_int,                   # group, sym
+        _vp, _i64, _i64,                # SV, sv_stride, rank
+        _vp, _i64, _vp, _i64,           # parts, P, u_index, n_u
+        _vp, _i64,                      # bias, bias_stride
+        _vp, _i64, _vp,                 # y, y_stride, stream
     ]),
     "glq_lowrank_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "glq_lowrank_xu_batched": (_c_int, [
@@ -137,6 +149,12 @@ SIGNATURES = {
     "glq_dequant_weight": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp, _i64, _c_int, _vp, _vp]),
     "glq_pack_codes": (_c_int, [_vp, _i64, _i64, _c_int, _vp, _vp]),
     "glq_rmsnorm": (_c_int, [_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp, _vp, _vp]),
+    "glq_rmsnorm_xu": (_c_int, [
+        _vp, _vp, _vp, _i64, _i64,      # x, residual, weight, rows, dim
+        ctypes.c_float, _vp, _vp,       # eps, out, residual_out
+        _vp, _i64, _i64, _i64, _vp,     # U, u_stride, n_u, rank, parts
+        _vp,                            # stream
+    ]),
     "glq_qk_norm_rope": (_c_int, [
         _vp, _vp, _vp, _i64,            # q, k, v, tokens
         _i64, _i64, _i64,               # q_heads, kv_heads, head_dim
@@ -152,6 +170,13 @@ SIGNATURES = {
         _i64, _i64, _i64, _i64,         # q_heads, kv_heads, head_dim, max_len
         _vp, ctypes.c_float, _vp,       # len, scale, advance
         _vp, _vp, _i64, _vp,            # out, workspace, bytes, stream
+    ]),
+    "glq_decode_attention_xu": (_c_int, [
+        _vp, _vp, _vp, _i64,            # q, k_cache, v_cache, tokens
+        _i64, _i64, _i64, _i64,         # q_heads, kv_heads, head_dim, max_len
+        _vp, ctypes.c_float, _vp,       # len, scale, advance
+        _vp, _vp, _i64, _vp,            # out, U, rank, parts
+        _vp, _i64, _vp,                 # workspace, bytes, stream
     ]),
 }
 

@@ -8,6 +8,7 @@
 
 #include <hip/hip_fp16.h>
 
+#include "glq_gemv_core.h"
 #include "glq_handoff.h"
 #include "glq_internal.h"
 
@@ -17,7 +18,6 @@ namespace {
 constexpr int kDecThreads = 256;
 constexpr int kHeadDim = 128;
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 __device__ inline float wave_sum(float v) {
@@ -49,6 +49,59 @@ __device__ inline float block_reduce(float v, float* red) {
 __device__ inline _Float16 hmul(_Float16 a, _Float16 b) { return (_Float16)((float)a * (float)b); }
 
 // ---------------------------------------------------------------------------
+// One token row's partial of a = x U over R <= 32 NI rows of U, with the U
+// loads issued before x exists (a launch that normalizes or merges the row
+// first): thread t holds columns jb + 8 (t & 7) .. + 8 of rows (t >> 3) +
+// 32 i; rows past R and columns past rank read as zero.  Then dot() sums
+// x[k] U[k][jb + j] over the rows (fp32; per thread over its rows, then the
+// 32 row groups in order through LDS) and returns the sum of column jb + j
+// to thread j < 64.  Every thread of the 256 calls both.
+// ---------------------------------------------------------------------------
+constexpr int kURowsRed = 32 * 64;  // LDS floats of URows::dot
+
+template <int NI>
+struct URows {
+  f16x8 u[NI];
+  __device__ void issue(const __half* U, int rank, int R, int jb) {
+    const int c = jb + 8 * (threadIdx.x & 7), r0 = threadIdx.x >> 3;
+    asm volatile("" ::: "memory");  // after the memory operations issued before
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = r0 + 32 * i;
+      u[i] = (row < R && c < rank) ? *(const f16x8*)(U + (int64_t)row * rank + c) : f16x8{};
+    }
+    // compiler memory barriers on both sides keep the loads where they are
+    // issued (the compiler would otherwise move them next to their first use,
+    // or ahead of loads the caller needs first); they wait for nothing
+    asm volatile("" ::: "memory");
+  }
+  // x must be complete in LDS (a barrier after its writes) before the call.
+  __device__ float dot(const __half* x /* LDS, R values */, int R,
+                       float* red /* LDS, kURowsRed floats */) const {
+    const int r0 = threadIdx.x >> 3;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = r0 + 32 * i;
+      const float xv = row < R ? __half2float(x[row]) : 0.f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[c] = fmaf(xv, (float)u[i][c], acc[c]);
+    }
+    __syncthreads();  // red may still be read from a previous call
+    float* mine = red + r0 * 64 + 8 * (threadIdx.x & 7);
+    *(float4*)mine = float4{acc[0], acc[1], acc[2], acc[3]};
+    *(float4*)(mine + 4) = float4{acc[4], acc[5], acc[6], acc[7]};
+    __syncthreads();
+    float v = 0.f;
+    if (threadIdx.x < 64) {
+#pragma unroll 8
+      for (int q = 0; q < 32; ++q) v += red[q * 64 + threadIdx.x];
+    }
+    return v;
+  }
+};
+
+// ---------------------------------------------------------------------------
 // RMSNorm over rows of D fp16 values (Qwen3MoeRMSNorm.forward):
 //   y   = x (+ residual, fp16 add)            -> residual_out when fused
 //   out = fp16(w * fp16(y * rsqrt(mean(y^2) + eps)))
@@ -56,14 +109,14 @@ __device__ inline _Float16 hmul(_Float16 a, _Float16 b) { return (_Float16)((flo
 // ---------------------------------------------------------------------------
 constexpr int kNormIters = 4;  // D <= 256 * 8 * 4 = 8192
 
-__global__ __launch_bounds__(kDecThreads) void rmsnorm_kernel(
-    const __half* __restrict__ x, const __half* __restrict__ res, const __half* __restrict__ w,
-    __half* __restrict__ out, __half* __restrict__ res_out, int D, float eps) {
-  __shared__ float red[4];
-  const int64_t row = blockIdx.x;
+// The row pass of the RMSNorm, shared by every kernel that normalizes a row
+// (256 threads, the same order of sums everywhere, so the same bits): thread
+// tid takes 8-wide pieces tid + 256 it of the row into y (x, or fp16(x +
+// residual)) and every thread gets r = rsqrt(mean(y^2) + eps).
+__device__ inline float rms_row(const __half* x, const __half* res, int64_t row, int D, float eps,
+                                f16x8 (&y)[kNormIters], float* red) {
   const f16x8* xr = (const f16x8*)(x + row * D);
   const f16x8* rr = res ? (const f16x8*)(res + row * D) : nullptr;
-  f16x8 y[kNormIters];
   float ss = 0.f;
 #pragma unroll
   for (int it = 0; it < kNormIters; ++it) {
@@ -74,7 +127,6 @@ __global__ __launch_bounds__(kDecThreads) void rmsnorm_kernel(
         const f16x8 r = rr[i];
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = (_Float16)((float)v[e] + (float)r[e]);
-        ((f16x8*)(res_out + row * D))[i] = v;
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += (float)v[e] * (float)v[e];
@@ -82,18 +134,111 @@ __global__ __launch_bounds__(kDecThreads) void rmsnorm_kernel(
     }
   }
   const float total = block_reduce<false>(ss, red);
-  const float r = rsqrtf(total / (float)D + eps);
-  const f16x8* wr = (const f16x8*)w;
+  return rsqrtf(total / (float)D + eps);
+}
+
+// out = fp16(w * fp16(y * r)) of one 8-wide piece.
+__device__ inline f16x8 rms_piece(const f16x8& y, const __half* w, int i, float r) {
+  const f16x8 wv = ((const f16x8*)w)[i];
+  f16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = hmul(wv[e], (_Float16)((float)y[e] * r));
+  return o;
+}
+
+__global__ __launch_bounds__(kDecThreads) void rmsnorm_kernel(
+    const __half* __restrict__ x, const __half* __restrict__ res, const __half* __restrict__ w,
+    __half* __restrict__ out, __half* __restrict__ res_out, int D, float eps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  f16x8 y[kNormIters];
+  const float r = rms_row(x, res, row, D, eps, y, red);
 #pragma unroll
   for (int it = 0; it < kNormIters; ++it) {
     const int i = threadIdx.x + it * kDecThreads;
     if (i * 8 < D) {
-      const f16x8 wv = wr[i];
-      f16x8 o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = hmul(wv[e], (_Float16)((float)y[it][e] * r));
-      ((f16x8*)(out + row * D))[i] = o;
+      if (res) ((f16x8*)(res_out + row * D))[i] = y[it];
+      ((f16x8*)(out + row * D))[i] = rms_piece(y[it], w, i, r);
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm of M <= 16 rows and, in the same launch, the fp32 partials of
+// out U_u for n_u matrices U_u (D x rank): the x U of the projections that
+// read the normalized rows (q, k and v of a decoder layer), which sum the
+// partials in slice order as they load a (glq_gemv_lora_parts).  Workgroup
+// (u, s) normalizes every row (rms_row: the bits of rmsnorm_kernel), keeps
+// its K slice s (kLowrankRows values of each row) in LDS -- and, for u = 0,
+// writes that slice of out (and of the fused residual sum) -- then writes the
+// slice's partial of out U_u to parts[u][s].
+// ---------------------------------------------------------------------------
+struct RxArgs {
+  const __half *x, *res, *w;
+  __half *out, *res_out;
+  const __half* U;
+  int64_t u_stride;  // halves between U matrices
+  float* part;       // (n_u, S, M, rpad)
+  int M, D, S, rank, rpad;
+  float eps;
+};
+
+constexpr int kRxMaxRows = 16;
+constexpr size_t kRxLds = (size_t)kRxMaxRows * kLowrankRows * 2   // the rows' slices (fp16)
+                          + kURowsRed * 4                         // partial sums
+                          + (size_t)16 * kLowrankRows * 2         // lowrank_partial's x slice
+                          + (size_t)64 * kLowrankUtStride * 2;    // U block, transposed
+
+// MC = 0: up to kRxPfRows rows, the slice's U loads issued before the
+// norms (URows); MC = 4: 3..16 rows by MFMA tiles (lowrank_partial).
+constexpr int kRxPfRows = 3;
+
+template <int MC>
+__global__ __launch_bounds__(kDecThreads) void rmsnorm_xu_kernel(RxArgs g) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __half* xn = (__half*)smem;                               // [M][kLowrankRows]
+  float* red = (float*)(xn + kRxMaxRows * kLowrankRows);    // kURowsRed (>= 4*4*64)
+  __half* xl = (__half*)(red + kURowsRed);                  // 16 x kLowrankRows
+  __half* ut = xl + 16 * kLowrankRows;                      // 64 x kLowrankUtStride
+  __shared__ float red4[4];
+  const int u = blockIdx.x / g.S, s = blockIdx.x - u * g.S;
+  const int k0 = s * kLowrankRows, kl = min(kLowrankRows, g.D - k0);
+  const int p0 = k0 / 8, p1 = p0 + kl / 8;  // the slice's 8-wide pieces
+  const __half* Us = g.U + u * g.u_stride + (int64_t)k0 * g.rank;  // the slice's rows
+  URows<kLowrankRows / 32> ur;
+  if constexpr (MC == 0) ur.issue(Us, g.rank, kl, 0);
+  for (int m = 0; m < g.M; ++m) {
+    f16x8 y[kNormIters];
+    const float r = rms_row(g.x, g.res, m, g.D, g.eps, y, red4);
+#pragma unroll
+    for (int it = 0; it < kNormIters; ++it) {
+      const int i = threadIdx.x + it * kDecThreads;
+      if (i >= p0 && i < p1) {
+        const f16x8 o = rms_piece(y[it], g.w, i, r);
+        *(f16x8*)(xn + m * kLowrankRows + 8 * (i - p0)) = o;
+        if (u == 0) {
+          ((f16x8*)(g.out + (int64_t)m * g.D))[i] = o;
+          if (g.res) ((f16x8*)(g.res_out + (int64_t)m * g.D))[i] = y[it];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  float* mine = g.part + ((int64_t)u * g.S + s) * g.M * g.rpad;
+  if constexpr (MC == 0) {
+    for (int jb = 0; jb < g.rpad; jb += 64) {
+      if (jb > 0) ur.issue(Us, g.rank, kl, jb);
+      for (int m = 0; m < g.M; ++m) {
+        const float v = ur.dot(xn + m * kLowrankRows, kl, red);
+        if (threadIdx.x < 64 && jb + threadIdx.x < g.rpad) mine[m * g.rpad + jb + threadIdx.x] = v;
+      }
+    }
+  } else {
+    // rows of the slice from LDS, indexed as lowrank_partial reads them
+    // (xrow(m) + k for k in [k0, k0 + kl))
+    auto xrow = [&](int m) { return xn + m * kLowrankRows - k0; };
+    lowrank_partial<MC>(xrow, g.M, g.D, g.rank, g.rpad, g.U + u * g.u_stride, s, mine, red, xl,
+                        (int)threadIdx.x, ut);
   }
 }
 
@@ -197,6 +342,11 @@ struct AttnArgs {
   unsigned* count; // [B][Hk], zero between calls
   int B, Hq, Hk, max_len, nsplit;
   float scale;
+  // XU form: the fp32 partials of out U of each token (the o projection's
+  // x U), one per KV group, summed in group order by the projection
+  const __half* U;  // (Hq * 128, rank)
+  float* xpart;     // [Hk][B][rpad]
+  int rank, rpad;
 };
 
 constexpr size_t kAttnLds = 2 * kAttnMaxRep * kHeadDim          // q rows
@@ -204,6 +354,7 @@ constexpr size_t kAttnLds = 2 * kAttnMaxRep * kHeadDim          // q rows
                             + 2 * kAttnChunk * kHeadDim          // V rows
                             + 4 * kAttnMaxRep * kAttnChunk + 16;  // weights, flag
 
+template <bool XU>
 __global__ __launch_bounds__(kDecThreads) void decode_attention_kernel(AttnArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __half* qs = (__half*)smem;
@@ -312,43 +463,67 @@ __global__ __launch_bounds__(kDecThreads) void decode_attention_kernel(AttnArgs 
   }
   // arrival (glq_handoff.h); the last block of (b, g) merges the splits
   if (!handoff_arrive(a.count + b * a.Hk + g, (unsigned)a.nsplit, flag)) return;
-  if (h < rep) {
-    // the other blocks' partials through coherent loads, up to 8 splits'
-    // worth in flight at once,
-    // merged online (running max M, sums rescaled when M grows)
-    const float* ph = a.part + ((int64_t)b * a.Hq + g * rep + h) * a.nsplit * kPartStride;
-    float M = -__builtin_inff(), den = 0.f, r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
-    for (int s0 = 0; s0 < a.nsplit; s0 += 8) {
-      float ms[8], ls[8];
-      float4 os[8];
+  // The other blocks' partials through coherent loads, up to 8 splits' worth
+  // in flight at once, merged online (running max M, sums rescaled when M
+  // grows).  Every thread loads (threads past rep read head rep - 1's and
+  // drop them), so that in the XU form the group's rows of U -- rows
+  // [g R, g R + R) -- go out right after the first 8 splits' loads: the merge
+  // waits for its own loads only and the U rows arrive behind it.
+  const int R = rep * kHeadDim;
+  URows<kAttnMaxRep * kHeadDim / 32> ur;
+  const float* ph =
+      a.part + ((int64_t)b * a.Hq + g * rep + min(h, rep - 1)) * a.nsplit * kPartStride;
+  float M = -__builtin_inff(), den = 0.f, r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
+  auto merge8 = [&](int s0, bool first) {
+    float ms[8], ls[8];
+    float4 os[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int s2 = min(s0 + j, a.nsplit - 1);
-        const float* pp = ph + s2 * kPartStride;
-        ms[j] = handoff_get(pp);
-        ls[j] = handoff_get(pp + 1);
-        os[j] = float4{handoff_get(pp + 4 + 4 * l32), handoff_get(pp + 5 + 4 * l32),
-                       handoff_get(pp + 6 + 4 * l32), handoff_get(pp + 7 + 4 * l32)};
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (s0 + j >= a.nsplit || ms[j] == -__builtin_inff()) continue;  // none / empty split
-        const float Mn = fmaxf(M, ms[j]);
-        const float fo = expf(M - Mn), fn = expf(ms[j] - Mn);  // M = -inf: fo = 0
-        den = den * fo + ls[j] * fn;
-        r0 = r0 * fo + os[j].x * fn;
-        r1 = r1 * fo + os[j].y * fn;
-        r2 = r2 * fo + os[j].z * fn;
-        r3 = r3 * fo + os[j].w * fn;
-        M = Mn;
-      }
+    for (int j = 0; j < 8; ++j) {
+      const int s2 = min(s0 + j, a.nsplit - 1);
+      const float* pp = ph + s2 * kPartStride;
+      ms[j] = handoff_get(pp);
+      ls[j] = handoff_get(pp + 1);
+      os[j] = float4{handoff_get(pp + 4 + 4 * l32), handoff_get(pp + 5 + 4 * l32),
+                     handoff_get(pp + 6 + 4 * l32), handoff_get(pp + 7 + 4 * l32)};
     }
+    if constexpr (XU) {
+      if (first) ur.issue(a.U + (int64_t)g * R * a.rank, a.rank, R, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (s0 + j >= a.nsplit || ms[j] == -__builtin_inff()) continue;  // none / empty split
+      const float Mn = fmaxf(M, ms[j]);
+      const float fo = expf(M - Mn), fn = expf(ms[j] - Mn);  // M = -inf: fo = 0
+      den = den * fo + ls[j] * fn;
+      r0 = r0 * fo + os[j].x * fn;
+      r1 = r1 * fo + os[j].y * fn;
+      r2 = r2 * fo + os[j].z * fn;
+      r3 = r3 * fo + os[j].w * fn;
+      M = Mn;
+    }
+  };
+  merge8(0, true);
+  for (int s0 = 8; s0 < a.nsplit; s0 += 8) merge8(s0, false);
+  if (h < rep) {
     const float inv = 1.f / den;
     f16x2 oa = {(_Float16)(r0 * inv), (_Float16)(r1 * inv)};
     f16x2 ob = {(_Float16)(r2 * inv), (_Float16)(r3 * inv)};
     __half* dst = a.out + (int64_t)b * a.Hq * kHeadDim + (int64_t)(g * rep + h) * kHeadDim;
-    *(uint2*)(dst + 4 * l32) =
-        uint2{__builtin_bit_cast(uint32_t, oa), __builtin_bit_cast(uint32_t, ob)};
+    const uint2 o4 = uint2{__builtin_bit_cast(uint32_t, oa), __builtin_bit_cast(uint32_t, ob)};
+    *(uint2*)(dst + 4 * l32) = o4;
+    if constexpr (XU) *(uint2*)((__half*)ks + h * kHeadDim + 4 * l32) = o4;  // K rows are dead
+  }
+  if constexpr (XU) {
+    // the group's partial of out U (fp32), read by the next launch
+    const __half* xo = (const __half*)ks;
+    float* red = (float*)((__half*)ks + kAttnMaxRep * kHeadDim);  // kURowsRed floats
+    float* mine = a.xpart + ((int64_t)g * a.B + b) * a.rpad;
+    __syncthreads();  // the merged rows are in xo
+    for (int jb = 0; jb < a.rpad; jb += 64) {
+      if (jb > 0) ur.issue(a.U + (int64_t)g * R * a.rank, a.rank, R, jb);
+      const float v = ur.dot(xo, R, red);
+      if (tid < 64 && jb + tid < a.rpad) mine[jb + tid] = v;
+    }
   }
   if (tid == 0) {
     handoff_reset(a.count + b * a.Hk + g);
@@ -380,6 +555,50 @@ extern "C" int glq_rmsnorm(const void* x, const void* residual, const void* weig
       (const __half*)x, (const __half*)residual, (const __half*)weight, (__half*)out,
       (__half*)residual_out, (int)dim, eps);
   GLQ_LAUNCH_CHECK("rmsnorm_kernel");
+  return GLQ_OK;
+}
+
+extern "C" int glq_rmsnorm_xu(const void* x, const void* residual, const void* weight,
+                              int64_t rows, int64_t dim, float eps, void* out,
+                              void* residual_out, const void* U, int64_t u_stride, int64_t n_u,
+                              int64_t rank, float* parts, void* stream) {
+  using namespace glq;
+  clear_error();
+  GLQ_CHECK(rows >= 0 && dim > 0, "rows must be >= 0 and dim > 0");
+  GLQ_CHECK(rows <= kRxMaxRows, "rows must be <= %d (got %lld)", kRxMaxRows, (long long)rows);
+  GLQ_CHECK(dim % 8 == 0 && dim <= kDecThreads * 8 * kNormIters,
+            "dim must be a multiple of 8 and <= %d (got %lld)", kDecThreads * 8 * kNormIters,
+            (long long)dim);
+  GLQ_CHECK(n_u >= 1 && n_u <= 65535, "n_u must be in [1, 65535]");
+  GLQ_CHECK(rank > 0 && rank <= 1024 && rank % 8 == 0,
+            "rank must be a multiple of 8 in [8, 1024]");
+  GLQ_CHECK(u_stride >= dim * rank || n_u == 1, "u_stride must cover a (dim, rank) matrix");
+  if (rows == 0) return GLQ_OK;
+  GLQ_CHECK(x && weight && out && U && parts && al16(x) && al16(weight) && al16(out) &&
+                al16(U) && (n_u == 1 || u_stride % 8 == 0) && ((uintptr_t)parts & 3) == 0,
+            "x, weight, out, U must be non-null and 16-byte aligned, parts non-null");
+  GLQ_CHECK(!residual || (residual_out && al16(residual) && al16(residual_out)),
+            "a residual needs a 16-byte aligned residual_out");
+  RxArgs g;
+  g.x = (const __half*)x; g.res = (const __half*)residual; g.w = (const __half*)weight;
+  g.out = (__half*)out; g.res_out = (__half*)residual_out;
+  g.U = (const __half*)U; g.u_stride = u_stride;
+  g.part = parts;
+  g.M = (int)rows; g.D = (int)dim; g.S = (int)((dim + kLowrankRows - 1) / kLowrankRows);
+  g.rank = (int)rank; g.rpad = (int)align_up(rank, 32); g.eps = eps;
+  const dim3 grid((unsigned)(n_u * g.S));
+  if (rows > kRxPfRows) {
+    static size_t attr = 64 * 1024;
+    int rc = set_lds_limit(rmsnorm_xu_kernel<4>, kRxLds, attr);
+    if (rc) return rc;
+    rmsnorm_xu_kernel<4><<<grid, dim3(kDecThreads), kRxLds, (hipStream_t)stream>>>(g);
+  } else {
+    static size_t attr = 64 * 1024;
+    int rc = set_lds_limit(rmsnorm_xu_kernel<0>, kRxLds, attr);
+    if (rc) return rc;
+    rmsnorm_xu_kernel<0><<<grid, dim3(kDecThreads), kRxLds, (hipStream_t)stream>>>(g);
+  }
+  GLQ_LAUNCH_CHECK("rmsnorm_xu_kernel");
   return GLQ_OK;
 }
 
@@ -438,14 +657,46 @@ extern "C" int64_t glq_decode_attention_workspace_bytes(int64_t tokens, int64_t 
   return part + align_up(4 * tokens * kv_heads, 256);
 }
 
+static int attention_launch(const void* q, const void* k_cache, const void* v_cache,
+                            int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                            int64_t max_len, const int32_t* len, float scale, int64_t* advance,
+                            void* out, const void* U, int64_t rank, float* parts,
+                            void* workspace, int64_t workspace_bytes, void* stream);
+
 extern "C" int glq_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                                     int64_t tokens, int64_t q_heads, int64_t kv_heads,
                                     int64_t head_dim, int64_t max_len, const int32_t* len,
                                     float scale, int64_t* advance, void* out, void* workspace,
                                     int64_t workspace_bytes, void* stream) {
+  glq::clear_error();
+  return attention_launch(q, k_cache, v_cache, tokens, q_heads, kv_heads, head_dim, max_len, len,
+                          scale, advance, out, nullptr, 0, nullptr, workspace, workspace_bytes,
+                          stream);
+}
+
+extern "C" int glq_decode_attention_xu(const void* q, const void* k_cache, const void* v_cache,
+                                       int64_t tokens, int64_t q_heads, int64_t kv_heads,
+                                       int64_t head_dim, int64_t max_len, const int32_t* len,
+                                       float scale, int64_t* advance, void* out, const void* U,
+                                       int64_t rank, float* parts, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
   using namespace glq;
   clear_error();
-  static size_t attr = 64 * 1024;
+  GLQ_CHECK(U && parts && rank > 0 && rank <= 1024, "U, parts and 0 < rank <= 1024 required");
+  GLQ_CHECK(al16(U) && al4(parts) && rank % 8 == 0,
+            "U must be 16-byte aligned, parts 4-byte, rank a multiple of 8");
+  return attention_launch(q, k_cache, v_cache, tokens, q_heads, kv_heads, head_dim, max_len, len,
+                          scale, advance, out, U, rank, parts, workspace, workspace_bytes,
+                          stream);
+}
+
+static int attention_launch(const void* q, const void* k_cache, const void* v_cache,
+                            int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                            int64_t max_len, const int32_t* len, float scale, int64_t* advance,
+                            void* out, const void* U, int64_t rank, float* parts,
+                            void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace glq;
+  static size_t attr = 64 * 1024, attr_xu = 64 * 1024;
   GLQ_CHECK(head_dim == kHeadDim, "head_dim must be %d (got %lld)", kHeadDim,
             (long long)head_dim);
   GLQ_CHECK(tokens >= 0 && tokens <= 65535, "tokens must be in [0, 65535]");
@@ -473,10 +724,20 @@ extern "C" int glq_decode_attention(const void* q, const void* k_cache, const vo
   a.part = (float*)workspace;
   a.count = (unsigned*)((char*)workspace +
                         align_up(4 * tokens * q_heads * (int64_t)a.nsplit * kPartStride, 256));
-  int rc = set_lds_limit(decode_attention_kernel, kAttnLds, attr);
-  if (rc) return rc;
-  decode_attention_kernel<<<dim3((unsigned)a.nsplit, (unsigned)kv_heads, (unsigned)tokens),
-                            dim3(kDecThreads), kAttnLds, (hipStream_t)stream>>>(a);
+  a.U = (const __half*)U;
+  a.xpart = parts;
+  a.rank = (int)rank;
+  a.rpad = (int)align_up(rank, 32);
+  const dim3 grid((unsigned)a.nsplit, (unsigned)kv_heads, (unsigned)tokens);
+  if (U) {
+    int rc = set_lds_limit(decode_attention_kernel<true>, kAttnLds, attr_xu);
+    if (rc) return rc;
+    decode_attention_kernel<true><<<grid, dim3(kDecThreads), kAttnLds, (hipStream_t)stream>>>(a);
+  } else {
+    int rc = set_lds_limit(decode_attention_kernel<false>, kAttnLds, attr);
+    if (rc) return rc;
+    decode_attention_kernel<false><<<grid, dim3(kDecThreads), kAttnLds, (hipStream_t)stream>>>(a);
+  }
   GLQ_LAUNCH_CHECK("decode_attention_kernel");
   return GLQ_OK;
 }

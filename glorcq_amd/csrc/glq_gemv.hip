@@ -46,9 +46,15 @@ struct DenseArgs {
   const int32_t* usel = nullptr;
   const int32_t* ucl = nullptr;
   int nsel = 0, nu = 0;
-  // item i's U is U + uidx[i] * u_es (null: U + i * u_es); nuidx U matrices
+  // item i's U is U + uidx[i] * u_es (null: U + i * u_es); nuidx U matrices;
+  // xu_u: the caller's a is one row block per U (item i reads xu + uidx[i] *
+  // xu_es), not one per item
   const int32_t* uidx = nullptr;
   int nuidx = 0;
+  bool xu_u = false;
+  // apart_u: the caller's partials are one block per U (item i reads block
+  // uidx[i]), not one per item
+  bool apart_u = false;
   // a = x U formed in the token-tile launch (t16_xu_job): xt_jobs workgroups
   // of (item, pair of K slices) come first; item i's word xt_cnt[i] holds
   // its slices' arrivals, kXtReady once a is written, then 1 << 16 per
@@ -61,6 +67,12 @@ struct DenseArgs {
   uint64_t xt_spin = 0;
   __device__ int64_t u_index(int item) const {
     return uidx ? (int64_t)min(max(uidx[item], 0), nuidx - 1) : (int64_t)item;
+  }
+  __device__ const __half* xu_rows(int item) const {
+    return xu + (xu_u ? u_index(item) : (int64_t)item) * xu_es;
+  }
+  __device__ int64_t apart_block(int item) const {
+    return apart_u ? u_index(item) : (int64_t)item;
   }
 };
 
@@ -86,8 +98,8 @@ struct DenseSrc {
   }
   __device__ __half load_a(int item, int, int m, int j) const { return load_a(item, m, j); }
   __device__ __half load_a(int item, int m, int j) const {
-    if (a.xu) return a.xu[(int64_t)item * a.xu_es + (int64_t)m * a.sh.rank + j];
-    const float* p = a.apart + ((int64_t)item * a.P * a.M + m) * a.sh.rpad + j;
+    if (a.xu) return a.xu_rows(item)[(int64_t)m * a.sh.rank + j];
+    const float* p = a.apart + (a.apart_block(item) * a.P * a.M + m) * a.sh.rpad + j;
     return __float2half(sum_strided(p, (int64_t)a.M * a.sh.rpad, a.P));
   }
   __device__ void store(int item, int m, int n, float v) const {
@@ -115,8 +127,8 @@ struct DenseLaneItem {
   __device__ const __half* u() const { return a.u + a.u_index(item) * a.u_es; }
   __device__ u32x4 x8(int k) const { return *(const u32x4*)(a.x + (int64_t)item * a.x_es + k); }
   __device__ __half load_a(int j) const {
-    if (a.xu) return a.xu[(int64_t)item * a.xu_es + j];
-    const float* pp = a.apart + (int64_t)item * a.P * a.M * a.sh.rpad + j;
+    if (a.xu) return a.xu_rows(item)[j];
+    const float* pp = a.apart + a.apart_block(item) * a.P * a.M * a.sh.rpad + j;
     return __float2half(sum_strided(pp, (int64_t)a.M * a.sh.rpad, a.P));
   }
   __device__ void store(int n, float v) const {
@@ -724,21 +736,29 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
                      int64_t xu_stride, const void* bias, int64_t bias_stride,
                      void* y, int64_t y_stride, void* workspace,
                      int64_t workspace_bytes_given, void* stream,
-                     const int32_t* u_index = nullptr, int64_t n_u = 0) {
+                     const int32_t* u_index = nullptr, int64_t n_u = 0,
+                     const float* parts = nullptr, int64_t n_parts = 0) {
   clear_error();
   GLQ_CHECK(items >= 0 && M >= 0 && K >= 0 && N >= 0, "negative size");
   if (items == 0 || M == 0 || N == 0) return GLQ_OK;
   const bool lora = SV != nullptr && rank > 0;
+  if (parts) {  // a given as fp32 partials: no U, no xU
+    GLQ_CHECK(lora && n_parts >= 1 && n_parts < (1 << 20), "partials need SV, rank and P >= 1");
+    U = nullptr;
+    xU = nullptr;
+  }
   TileShape sh;
   int rc = gemv_check_shape(M, K, N, bits, group, sym, lora ? rank : 0, sh);
   if (rc) return rc;
   GLQ_CHECK(x && codes && scales && y && (sym == 1 || zeros), "null data pointer");
-  if (lora) GLQ_CHECK(U != nullptr || xU != nullptr, "LoRA needs U or a precomputed xU");
+  if (lora) GLQ_CHECK(U != nullptr || xU != nullptr || parts != nullptr,
+                      "LoRA needs U or a precomputed xU");
   GLQ_CHECK(tile_shape(sh) || lane_row_shape(sh, bits),
             "K=%lld, group=%lld at %d bits: rows or groups that are not whole 128-code "
             "chunks take the lane kernel only (at most %d codes a row, rank <= 128)",
             (long long)K, (long long)group, bits, 64 * 128 / bits);
   if (!tile_shape(sh) && M > 1) {
+    GLQ_CHECK(parts == nullptr, "given partials take whole 128-code groups when M > 1");
     // one lane launch per token row (x, a and y rows of the items advance together)
     for (int64_t m = 0; m < M; ++m) {
       rc = gemv_impl(items, (const __half*)x + m * K, x_stride, 1, K, N, codes, codes_stride,
@@ -756,7 +776,7 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   GLQ_CHECK(items == 1 || (x_stride % 8 == 0 && codes_stride % 4 == 0 &&
                            (!lora || sv_stride % 8 == 0) && (!lora || !U || u_stride % 8 == 0)),
             "item strides must keep 16-byte alignment");
-  const bool need_partials = lora && xU == nullptr;
+  const bool need_partials = lora && xU == nullptr && parts == nullptr;
   // one token row with U given: the lane kernel forms a = x U itself (one
   // launch, no workspace); GLQ_LANE_NO_XU=1 keeps the separate partial-sum launch
   const bool lane_xu = need_partials && lane_shape(M, sh, bits) && !getenv("GLQ_LANE_NO_XU");
@@ -794,14 +814,16 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   // workspace: kGemvSyncBytes of counter words (zero between calls), then
   // the x U partials (and the token-tile form's a)
   a.apart = need_partials && !lane_xu ? (const float*)((char*)workspace + kGemvSyncBytes)
-                                      : nullptr;
+                                      : parts;
   a.items = (int)items;
   a.M = (int)M;
-  a.P = need_partials && !lane_xu ? (int)lowrank_slices(K) : 0;
+  a.P = need_partials && !lane_xu ? (int)lowrank_slices(K) : (int)n_parts;
   a.tiles = (int)((N + 16 * T - 1) / (16 * T));
   a.sh = sh;
   a.uidx = u_index;
   a.nuidx = (int)std::min<int64_t>(n_u, 1 << 30);
+  a.xu_u = u_index != nullptr && a.xu != nullptr;
+  a.apart_u = u_index != nullptr && parts != nullptr;
 
   GLQ_CHECK(items * a.tiles < (1ll << 31) && items * a.P < (1ll << 31), "too many workgroups");
   hipStream_t s = (hipStream_t)stream;
@@ -955,17 +977,35 @@ int glq_gemv_lora_clustered(int64_t items, const void* x, int64_t x_stride, int6
                             int64_t K, int64_t N, const int32_t* codes, int64_t codes_stride,
                             int bits, const void* scales, const void* zeros, int64_t sz_stride,
                             int64_t group, int sym, const void* U, int64_t u_stride,
-                            const int32_t* u_index, int64_t n_u, const void* SV,
-                            int64_t sv_stride, int64_t rank, const void* bias,
-                            int64_t bias_stride, void* y, int64_t y_stride, void* workspace,
-                            int64_t workspace_bytes_given, void* stream) {
+                            const int32_t* u_index, int64_t n_u, const void* xU,
+                            int64_t xu_stride, const void* SV, int64_t sv_stride, int64_t rank,
+                            const void* bias, int64_t bias_stride, void* y, int64_t y_stride,
+                            void* workspace, int64_t workspace_bytes_given, void* stream) {
   clear_error();
   GLQ_CHECK(u_index != nullptr && n_u >= 1, "u_index and n_u >= 1 required");
-  GLQ_CHECK(U != nullptr, "U required");
+  GLQ_CHECK(U != nullptr || xU != nullptr, "U or xU required");
+  GLQ_CHECK(xU == nullptr || xu_stride >= M * rank, "xu_stride must cover M x rank");
   return gemv_impl(items, x, x_stride, M, K, N, codes, codes_stride, bits, scales, zeros,
-                   sz_stride, group, sym, U, u_stride, SV, sv_stride, rank, nullptr, 0, bias,
-                   bias_stride, y, y_stride, workspace, workspace_bytes_given, stream, u_index,
-                   n_u);
+                   sz_stride, group, sym, xU ? nullptr : U, u_stride, SV, sv_stride, rank, xU,
+                   xu_stride, bias, bias_stride, y, y_stride, workspace, workspace_bytes_given,
+                   stream, u_index, n_u);
+}
+
+int glq_gemv_lora_parts(int64_t items, const void* x, int64_t x_stride, int64_t M, int64_t K,
+                        int64_t N, const int32_t* codes, int64_t codes_stride, int bits,
+                        const void* scales, const void* zeros, int64_t sz_stride, int64_t group,
+                        int sym, const void* SV, int64_t sv_stride, int64_t rank,
+                        const float* parts, int64_t P, const int32_t* u_index, int64_t n_u,
+                        const void* bias, int64_t bias_stride, void* y, int64_t y_stride,
+                        void* stream) {
+  clear_error();
+  GLQ_CHECK(SV != nullptr && rank > 0 && parts != nullptr && P >= 1,
+            "SV, rank > 0, parts and P >= 1 required");
+  GLQ_CHECK(((uintptr_t)parts & 3) == 0, "parts must be 4-byte aligned");
+  GLQ_CHECK(u_index == nullptr || n_u >= 1, "u_index needs n_u >= 1");
+  return gemv_impl(items, x, x_stride, M, K, N, codes, codes_stride, bits, scales, zeros,
+                   sz_stride, group, sym, nullptr, 0, SV, sv_stride, rank, nullptr, 0, bias,
+                   bias_stride, y, y_stride, nullptr, 0, stream, u_index, n_u, parts, P);
 }
 
 int64_t glq_lowrank_workspace_bytes(int64_t items, int64_t M, int64_t K, int64_t rank) {

@@ -106,12 +106,37 @@ class GLoRCQQwen3Attention(nn.Module):
             cat["u_index"] = torch.tensor([0] * nq + [1, 2], dtype=torch.int32,
                                           device=self._U_qkv.device)
             self._qkv = cat
+        # The o projection's x U formed by the attention launch itself (its
+        # merging blocks, glq_decode_attention_xu) at up to XU_PRODUCER_MAX_M
+        # tokens, as partials that the projection sums as its a
+        # (glq_gemv_lora_parts).
+        o = attn.o_proj
+        self._o_xu = (getattr(o, "quant_type", None) == "gptq" and getattr(o, "U", None) is not None
+                      and getattr(o, "SV", None) is not None and o.U.is_cuda
+                      and o.U.shape[1] % 8 == 0 and o.bias_param is None)
         self._len = None  # device int32: positions the step attends to
         self._ws = None   # decode attention workspace (counters stay zero between calls)
         self._ws_key = None
 
+    # Up to this many tokens the decode step forms the projections' x U in the
+    # launches that produce their inputs (the input RMSNorm for q/k/v, the
+    # attention for o); from 4 tokens the token-tile GEMV forms it in its own
+    # launch.
+    XU_PRODUCER_MAX_M = 3
+
+    def qkv_u(self, B):
+        """The (3, K, r) stack of the q/k/v U factors when a decode step of B
+        tokens takes its x U partials from the input RMSNorm's launch
+        (rmsnorm_xu), else None."""
+        if self._qkv is not None and B <= self.XU_PRODUCER_MAX_M and self._U_qkv.shape[2] % 8 == 0:
+            return self._U_qkv
+        return None
+
     def forward(self, hidden_states, position_embeddings, attention_mask, past_key_values=None,
-                **kwargs):
+                qkv_xu=None, **kwargs):
+        """qkv_xu: x U partials of the q/k/v stack (3, S, B, rpad) for this
+        step's normalized hidden states, formed by their RMSNorm launch
+        (qkv_u, rmsnorm_xu)."""
         B, S, H = hidden_states.shape
         lay = _static_layer(past_key_values, self.layer_idx, B) if S == 1 else None
         if lay is None or self.head_dim != 128:
@@ -121,10 +146,15 @@ class GLoRCQQwen3Attention(nn.Module):
         x = hidden_states.reshape(B, H)
         if self._qkv is not None and B <= kernels.GEMV_MAX_M:
             c = self._qkv
-            y = kernels.packed_dequant_matmul_batched(
-                x.contiguous(), c["codes"], c["scales"], c["zeros"], inner.q_proj.pack_bits,
-                inner.q_proj.gptq_groupsize, U=c["U"], SV=c["SV"],
-                u_index=c["u_index"])  # (items, B, kv rows)
+            if qkv_xu is not None:  # partials per U, item i summing qkv_xu[u_index[i]]
+                y = kernels.packed_dequant_matmul_parts(
+                    x.contiguous(), c["codes"], c["scales"], c["zeros"], inner.q_proj.pack_bits,
+                    inner.q_proj.gptq_groupsize, c["SV"], qkv_xu, u_index=c["u_index"])
+            else:
+                y = kernels.packed_dequant_matmul_batched(
+                    x.contiguous(), c["codes"], c["scales"], c["zeros"], inner.q_proj.pack_bits,
+                    inner.q_proj.gptq_groupsize, U=c["U"], SV=c["SV"],
+                    u_index=c["u_index"])  # (items, B, kv rows)
             n = y.shape[0] - 2
             q, k, v = y[:n], y[n], y[n + 1]  # q item-major: the norm/rotary kernel reads it so
         elif self._U_qkv is not None and B <= kernels.GEMV_MAX_M:
@@ -147,6 +177,16 @@ class GLoRCQQwen3Attention(nn.Module):
             kernels.retire_workspace(self._ws)  # a captured graph may still use it
             self._ws = kernels.decode_attention_workspace(qr, lay.keys)
             self._ws_key = (tuple(lay.keys.shape), x.device)
+        if self._o_xu and B <= self.XU_PRODUCER_MAX_M:
+            o = inner.o_proj
+            a, parts = kernels.decode_attention(qr, lay.keys, lay.values, self._len, self.scaling,
+                                                advance=lay.cumulative_length, workspace=self._ws,
+                                                U=o.U)
+            y = kernels.packed_dequant_matmul_parts(
+                a, o.codes.unsqueeze(0), o.scales.unsqueeze(0),
+                None if o.gptq_sym else o.zeros.unsqueeze(0), o.pack_bits, o.gptq_groupsize,
+                o.SV.unsqueeze(0), parts.unsqueeze(0), sym=o.gptq_sym)
+            return y.reshape(B, 1, -1), None
         a = kernels.decode_attention(qr, lay.keys, lay.values, self._len, self.scaling,
                                      advance=lay.cumulative_length, workspace=self._ws)
         return inner.o_proj(a).reshape(B, 1, -1), None
@@ -168,7 +208,13 @@ class GLoRCQQwen3DecoderLayer(nn.Module):
                 past_key_values=None, use_cache=False, position_embeddings=None, **kwargs):
         ln1, ln2 = self.input_layernorm, self.post_attention_layernorm
         x = hidden_states.contiguous()
-        h = kernels.rmsnorm(x, ln1.weight, ln1.variance_epsilon)
+        B, S = x.shape[0], x.shape[1]
+        Uq = self.self_attn.qkv_u(B) if S == 1 else None
+        if Uq is not None:  # the q/k/v x U in the norm's launch
+            h, xu = kernels.rmsnorm_xu(x, ln1.weight, ln1.variance_epsilon, Uq)
+            kwargs["qkv_xu"] = xu
+        else:
+            h = kernels.rmsnorm(x, ln1.weight, ln1.variance_epsilon)
         a, _ = self.self_attn(hidden_states=h, position_embeddings=position_embeddings,
                               attention_mask=attention_mask, past_key_values=past_key_values,
                               position_ids=position_ids, use_cache=use_cache, **kwargs)

@@ -276,7 +276,9 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
     A 2-D x (M, K) is the one input of every problem (x stride 0).
 
     u_index (E,) int32 on the device: problem i uses U[u_index[i]] of U
-    (C, K, r) (cluster-shared U, glq_gemv_lora_clustered).
+    (C, K, r) (cluster-shared U, glq_gemv_lora_clustered); with u_index a
+    precomputed_xU is given per U as well, (C, M, r), problem i reading
+    precomputed_xU[u_index[i]].
 
     The packed-format counterpart of turbo_dequant_grouped_gemv_fused
     (inference/kernels/__init__.py:242-278), with the low-rank term fused.
@@ -316,7 +318,13 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
         rank = SV.shape[2]
         if precomputed_xU is not None:
             _require(precomputed_xU, "precomputed_xU", torch.float16)
-            if tuple(precomputed_xU.shape) != (E, M, rank):
+            if u_index is not None:
+                _require(u_index, "u_index", torch.int32)
+                if (precomputed_xU.dim() != 3 or precomputed_xU.shape[0] < 1
+                        or tuple(precomputed_xU.shape[1:]) != (M, rank)
+                        or tuple(u_index.shape) != (E,)):
+                    raise RuntimeError(f"u_index must be ({E},) with precomputed_xU (C, {M}, {rank})")
+            elif tuple(precomputed_xU.shape) != (E, M, rank):
                 raise RuntimeError("precomputed_xU must be (E, M, r)")
         else:
             if U is None:
@@ -345,12 +353,14 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
     lib = _lib.load()
     nbytes = lib.glq_gemv_workspace_bytes(E, M, K, N, rank if xu is None else 0)
     ws = gemv_workspace(x.device, nbytes)
-    if u_index is not None and SV is not None and xu is None:
+    if u_index is not None and SV is not None:
+        n_u = U.shape[0] if xu is None else xu.shape[0]
         rc = lib.glq_gemv_lora_clustered(
             E, x.data_ptr(), x_stride, M, K, N, codes.data_ptr(),
             codes.shape[1] * codes.shape[2], bits, scales.data_ptr(), _lib.ptr(zeros),
-            scales.shape[1] * scales.shape[2], groupsize, _sym_mode(sym), U.data_ptr(), K * rank,
-            u_index.data_ptr(), U.shape[0], SV.data_ptr(), N * rank, rank, _lib.ptr(bias), N,
+            scales.shape[1] * scales.shape[2], groupsize, _sym_mode(sym),
+            _lib.ptr(U if xu is None else None), K * rank, u_index.data_ptr(), n_u,
+            _lib.ptr(xu), M * rank, SV.data_ptr(), N * rank, rank, _lib.ptr(bias), N,
             out.data_ptr(), M * N, ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device))
         _lib.check(rc, "glq_gemv_lora_clustered")
         return out
@@ -361,6 +371,73 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
         N * rank, rank, _lib.ptr(xu), M * rank, _lib.ptr(bias), N, out.data_ptr(), M * N,
         ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device))
     _lib.check(rc, "glq_gemv_lora_batched")
+    return out
+
+
+def packed_dequant_matmul_parts(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
+                                zeros: torch.Tensor | None, bits: int, groupsize: int,
+                                SV: torch.Tensor, parts: torch.Tensor,
+                                u_index: torch.Tensor | None = None, sym: bool = False,
+                                bias: torch.Tensor | None = None,
+                                out: torch.Tensor | None = None) -> torch.Tensor:
+    """packed_dequant_matmul_batched with a = x U given as fp32 partials
+    (glq_gemv_lora_parts): parts (blocks, P, M, rpad), item i taking
+    a = fp16(sum over p in order of parts[b][p]) with b = u_index[i], or i
+    when u_index is None -- what rmsnorm_xu and decode_attention(U=...)
+    write.  x (M, K) is every item's input; codes (E, N, K*bits/32)."""
+    _require(x, "x", torch.float16)
+    _require(codes, "codes", torch.int32)
+    _require(scales, "scales", torch.float16)
+    _require(SV, "SV", torch.float16)
+    _require(parts, "parts", torch.float32)
+    asym = _sym_mode(sym) != SYM_SIGNED
+    if asym:
+        if zeros is None:
+            raise RuntimeError("zeros required for codes with zero-points")
+        _require(zeros, "zeros", torch.float16)
+    if x.dim() != 2 or codes.dim() != 3:
+        raise RuntimeError("x must be (M, K) and codes (E, N, K*bits/32)")
+    (M, K), (E, N) = x.shape, codes.shape[:2]
+    if codes.shape[2] * (32 // bits) != K:
+        raise RuntimeError("codes must be (E, N, K*bits/32)")
+    if M > GEMV_MAX_M:
+        raise RuntimeError(f"takes M <= {GEMV_MAX_M}")
+    if groupsize <= 0 or K % groupsize:
+        raise RuntimeError(f"groupsize {groupsize} must divide K={K}")
+    G = K // groupsize
+    if tuple(scales.shape) != (E, N, G) or (asym and tuple(zeros.shape) != (E, N, G)):
+        raise RuntimeError(f"scales/zeros must be ({E}, {N}, {G})")
+    if SV.dim() != 3 or tuple(SV.shape[:2]) != (E, N):
+        raise RuntimeError(f"SV must be ({E}, {N}, r)")
+    rank = SV.shape[2]
+    rpad = (rank + 31) // 32 * 32
+    if parts.dim() != 4 or tuple(parts.shape[2:]) != (M, rpad):
+        raise RuntimeError(f"parts must be (blocks, P, {M}, {rpad})")
+    nb = parts.shape[0]
+    if u_index is not None:
+        _require(u_index, "u_index", torch.int32)
+        if tuple(u_index.shape) != (E,):
+            raise RuntimeError(f"u_index must be ({E},)")
+    elif nb != E:
+        raise RuntimeError(f"parts must hold one block per item ({E}) without u_index")
+    if bias is not None:
+        _require(bias, "bias", torch.float16)
+        if tuple(bias.shape) != (E, N):
+            raise RuntimeError(f"bias must be ({E}, {N})")
+    if out is None:
+        out = torch.empty(E, M, N, dtype=torch.float16, device=x.device)
+    elif tuple(out.shape) != (E, M, N) or out.dtype != torch.float16 or not out.is_contiguous():
+        raise RuntimeError(f"out must be contiguous fp16 ({E}, {M}, {N})")
+    if E == 0 or M == 0 or N == 0:
+        return out
+    lib = _lib.load()
+    rc = lib.glq_gemv_lora_parts(
+        E, x.data_ptr(), 0, M, K, N, codes.data_ptr(), codes.shape[1] * codes.shape[2], bits,
+        scales.data_ptr(), _lib.ptr(zeros), scales.shape[1] * scales.shape[2], groupsize,
+        _sym_mode(sym), SV.data_ptr(), N * rank, rank, parts.data_ptr(), parts.shape[1],
+        _lib.ptr(u_index), nb, _lib.ptr(bias), N, out.data_ptr(), M * N,
+        _lib.stream_handle(x.device))
+    _lib.check(rc, "glq_gemv_lora_parts")
     return out
 
 
@@ -778,6 +855,49 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     return out if residual is None else (out, res_out)
 
 
+def rmsnorm_xu(x: torch.Tensor, weight: torch.Tensor, eps: float, U: torch.Tensor,
+               residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
+               parts: torch.Tensor | None = None):
+    """rmsnorm of x (M <= 16 rows of dim D) and, in the same launch, the fp32
+    partials of out U[u] over 256-row slices for U (n_u, D, r):
+    parts (n_u, S, M, rpad), S = ceil(D / 256), rpad = r rounded up to 32
+    -- the a of packed_dequant_matmul_parts (glq_rmsnorm_xu).  Returns
+    (out, parts), or (out, y, parts) when a residual is given (y = fp16(x +
+    residual), as rmsnorm)."""
+    lib = _lib.load()
+    _require(x, "x", torch.float16)
+    _require(weight, "weight", torch.float16)
+    _require(U, "U", torch.float16)
+    D = x.shape[-1]
+    if weight.shape != (D,):
+        raise RuntimeError(f"weight must be ({D},)")
+    if U.dim() == 2:
+        U = U.unsqueeze(0)
+    if U.dim() != 3 or U.shape[1] != D:
+        raise RuntimeError(f"U must be (n_u, {D}, r)")
+    n_u, _, r = U.shape
+    rows = x.numel() // D if D else 0
+    if out is None:
+        out = torch.empty_like(x)
+    res_out = None
+    if residual is not None:
+        _require(residual, "residual", torch.float16)
+        if residual.shape != x.shape:
+            raise RuntimeError("residual must match x")
+        res_out = torch.empty_like(x)
+    S, rpad = (D + 255) // 256, (r + 31) // 32 * 32
+    if parts is None:
+        parts = torch.empty(n_u, S, rows, rpad, dtype=torch.float32, device=x.device)
+    elif tuple(parts.shape) != (n_u, S, rows, rpad) or parts.dtype != torch.float32 \
+            or not parts.is_contiguous():
+        raise RuntimeError(f"parts must be contiguous fp32 ({n_u}, {S}, {rows}, {rpad})")
+    _lib.check(lib.glq_rmsnorm_xu(
+        x.data_ptr(), _lib.ptr(residual), weight.data_ptr(), rows, D, float(eps), out.data_ptr(),
+        _lib.ptr(res_out), U.data_ptr(), D * r, n_u, r, parts.data_ptr(),
+        _lib.stream_handle(x.device)), "glq_rmsnorm_xu")
+    return (out, parts) if residual is None else (out, res_out, parts)
+
+
 def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_w: torch.Tensor,
                  k_norm_w: torch.Tensor, eps: float, cos: torch.Tensor, sin: torch.Tensor,
                  k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor,
@@ -838,11 +958,16 @@ def decode_attention_workspace(q: torch.Tensor, k_cache: torch.Tensor) -> torch.
 def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                      length: torch.Tensor, scale: float, advance: torch.Tensor | None = None,
                      out: torch.Tensor | None = None,
-                     workspace: torch.Tensor | None = None) -> torch.Tensor:
+                     workspace: torch.Tensor | None = None, U: torch.Tensor | None = None,
+                     parts: torch.Tensor | None = None):
     """Single-query GQA attention over cache positions [0, length): q (T, Hq,
     128), caches (T, Hk, max_len, 128) -> (T, Hq*128) fp16.  `advance`
     (device int64) is incremented by one after the launch's reads.
-    `workspace` from decode_attention_workspace (a fresh one when None)."""
+    `workspace` from decode_attention_workspace (a fresh one when None).
+    With U (Hq*128, r) the same launch also forms the fp32 partials of out U,
+    one per KV group, parts (Hk, T, rpad) -- the a of
+    packed_dequant_matmul_parts (glq_decode_attention_xu) -- and (out, parts)
+    is returned."""
     lib = _lib.load()
     for t, n in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache")):
         _require(t, n, torch.float16)
@@ -855,6 +980,25 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     Hq = q.shape[1]
     if out is None:
         out = torch.empty(T, Hq * hd, dtype=torch.float16, device=q.device)
+    if U is not None:
+        _require(U, "U", torch.float16)
+        if U.dim() != 2 or U.shape[0] != Hq * hd:
+            raise RuntimeError(f"U must be ({Hq * hd}, r)")
+        r = U.shape[1]
+        rpad = (r + 31) // 32 * 32
+        if parts is None:
+            parts = torch.empty(Hk, T, rpad, dtype=torch.float32, device=q.device)
+        elif tuple(parts.shape) != (Hk, T, rpad) or parts.dtype != torch.float32 \
+                or not parts.is_contiguous():
+            raise RuntimeError(f"parts must be contiguous fp32 ({Hk}, {T}, {rpad})")
+        if workspace is None:
+            workspace = decode_attention_workspace(q, k_cache)
+        _lib.check(lib.glq_decode_attention_xu(
+            q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), T, Hq, Hk, hd, max_len,
+            length.data_ptr(), float(scale), _lib.ptr(advance), out.data_ptr(), U.data_ptr(), r,
+            parts.data_ptr(), workspace.data_ptr(), workspace.numel(),
+            _lib.stream_handle(q.device)), "glq_decode_attention_xu")
+        return out, parts
     if workspace is None:
         workspace = decode_attention_workspace(q, k_cache)
     _lib.check(lib.glq_decode_attention(

@@ -151,8 +151,10 @@ int glq_gemv_lora_batched(int64_t items, const void* x, int64_t x_stride,
  * (_precompute_xU_for_experts, inference/moe_block.py:290-322; the same
  * cluster fusion in _batched_proj_forward, moe_block.py:545-565), and it
  * serves projections that share an input and a U (q, k and v of one layer
- * cut into equal items).  Other arguments as glq_gemv_lora_batched; U and
- * u_index are required, xU is not taken.
+ * cut into equal items).  Other arguments as glq_gemv_lora_batched;
+ * u_index is required.  xU, when not NULL, is a = x U given per U matrix
+ * ((n_u, M, rank) fp16 at xu_stride halves apart, item i reading row block
+ * u_index[i]) and U is then not read.
  */
 int glq_gemv_lora_clustered(int64_t items, const void* x, int64_t x_stride,
                             int64_t M, int64_t K, int64_t N,
@@ -160,11 +162,33 @@ int glq_gemv_lora_clustered(int64_t items, const void* x, int64_t x_stride,
                             const void* scales, const void* zeros,
                             int64_t sz_stride, int64_t group, int sym,
                             const void* U, int64_t u_stride,
-                            const int32_t* u_index, int64_t n_u, const void* SV,
+                            const int32_t* u_index, int64_t n_u, const void* xU,
+                            int64_t xu_stride, const void* SV,
                             int64_t sv_stride, int64_t rank, const void* bias,
                             int64_t bias_stride, void* y, int64_t y_stride,
                             void* workspace, int64_t workspace_bytes,
                             void* stream);
+
+/*
+ * Batched GEMV whose a = x U arrives as fp32 partials: item i takes
+ *   a[m][j] = fp16(parts[b][0][m][j] + parts[b][1][m][j] + ... + parts[b][P-1][m][j])
+ * (summed in that order), b = u_index[i] (clamped to [0, n_u)) or b = i
+ * when u_index is NULL; parts is (blocks, P, M, rpad) fp32 with rpad = rank
+ * rounded up to 32 -- what glq_rmsnorm_xu and glq_decode_attention_xu write,
+ * so the projection after a norm or an attention launch streams its codes
+ * with no x U launch or x U work of its own.  The reference's fused forward
+ * with a precomputed a (GLoRCQLinear.forward with precomputed_xU,
+ * inference/quantized_linear.py:338-345).  Other arguments as
+ * glq_gemv_lora_batched (no U, no workspace); M > 1 takes whole 128-code
+ * groups.
+ */
+int glq_gemv_lora_parts(int64_t items, const void* x, int64_t x_stride, int64_t M, int64_t K,
+                        int64_t N, const int32_t* codes, int64_t codes_stride, int bits,
+                        const void* scales, const void* zeros, int64_t sz_stride, int64_t group,
+                        int sym, const void* SV, int64_t sv_stride, int64_t rank,
+                        const float* parts, int64_t P, const int32_t* u_index, int64_t n_u,
+                        const void* bias, int64_t bias_stride, void* y, int64_t y_stride,
+                        void* stream);
 
 /*
  * Low-rank factor a = fp16(x U) for `items` problems: x (M, K) fp16 at
@@ -482,6 +506,25 @@ int glq_rmsnorm(const void* x, const void* residual, const void* weight, int64_t
                 int64_t dim, float eps, void* out, void* residual_out, void* stream);
 
 /*
+ * glq_rmsnorm of rows <= 16 rows and, in the same launch, the low-rank
+ * factors of the projections that read its output, as fp32 partials: for
+ * each of the n_u matrices U_u (dim, rank) fp16 at U + u*u_stride and each
+ * 256-row slice s of dim (S = ceil(dim / 256) slices),
+ *   parts[u][s][m][j] = sum over k in slice s of out[m][k] U_u[k][j]
+ * (fp32, (n_u, S, rows, rpad) with rpad = rank rounded up to 32; columns
+ * past rank are zero).  glq_gemv_lora_parts sums them in slice order as its
+ * a, so the projections of a decoder layer's attention (q, k, v after the
+ * input RMSNorm) stream their codes with no x U of their own.  No reference
+ * kernel: the reference forms x U inside each GLoRCQLinear.forward
+ * (inference/quantized_linear.py:338-345) after the framework's RMSNorm.
+ * out and residual_out carry the same bits as glq_rmsnorm's.  rank a
+ * multiple of 8 (<= 1024), n_u <= 65535; no workspace.
+ */
+int glq_rmsnorm_xu(const void* x, const void* residual, const void* weight, int64_t rows,
+                   int64_t dim, float eps, void* out, void* residual_out, const void* U,
+                   int64_t u_stride, int64_t n_u, int64_t rank, float* parts, void* stream);
+
+/*
  * One decode token per row (tokens rows): per-head RMSNorm of q (q_heads
  * heads) and k (kv_heads heads) over head_dim = 128 with weights q_norm_w /
  * k_norm_w, then the rotary embedding x' = fp16(fp16(x cos) +
@@ -528,6 +571,25 @@ int glq_decode_attention(const void* q, const void* k_cache, const void* v_cache
                          int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                          int64_t max_len, const int32_t* len, float scale, int64_t* advance,
                          void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * glq_decode_attention, and in the same launch the low-rank factor of the
+ * projection that reads its output (the o projection) as fp32 partials, one
+ * per KV group g (the rows of its q heads):
+ *   parts[g][t][j] = sum over k in group g's rows of out[t][k] U[k][j]
+ * ((kv_heads, tokens, rpad), rpad = rank rounded up to 32), which
+ * glq_gemv_lora_parts sums in group order as its a.  U (q_heads * 128,
+ * rank) fp16, 16-byte aligned, rank a multiple of 8 (<= 1024).  Each
+ * (token, KV group) block that merges the splits forms its group's partial
+ * (its U rows' loads issued behind the merge's).  No reference kernel: the
+ * reference forms x U inside GLoRCQLinear.forward
+ * (inference/quantized_linear.py:338-345).  workspace as glq_decode_attention.
+ */
+int glq_decode_attention_xu(const void* q, const void* k_cache, const void* v_cache,
+                            int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                            int64_t max_len, const int32_t* len, float scale, int64_t* advance,
+                            void* out, const void* U, int64_t rank, float* parts,
+                            void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -61,6 +61,50 @@ def test_rmsnorm_matches_framework(gpu, rows, dim):
     assert float((out2.double() - ref64).abs().max()) <= 4e-3 * float(ref64.abs().max())
 
 
+def _xu_bar(xu, ref):
+    """x U as fp32 partials summed, against the fp32 product of the fp16 rows:
+    the sum orders differ (relative 2^-16 of the row's terms) -- within
+    2^-12 |ref| + 1e-4 of the row's largest magnitude."""
+    err = (xu.float() - ref).abs()
+    tol = 2.0 ** -12 * ref.abs() + 1e-4 * ref.abs().amax(-1, keepdim=True) + 1e-5
+    return bool((err <= tol).all()), float(err.max())
+
+
+@pytest.mark.parametrize("rows,dim,n_u,rank", [(1, 2048, 3, 64), (2, 2048, 3, 64),
+                                               (3, 2048, 1, 96), (16, 2048, 2, 32),
+                                               (1, 4096, 1, 128), (5, 136, 2, 64)])
+def test_rmsnorm_xu(gpu, rows, dim, n_u, rank):
+    """glq_rmsnorm_xu: the normalized rows (and the fused residual sum) carry
+    the bits of glq_rmsnorm; the slice partials summed give out U[u] within
+    fp32 rounding of the fp32 product (columns past rank zero); a second call
+    gives the same bits; a planted wrong U (the stack's order reversed) fails
+    the bar."""
+    m = _hf_norm(dim, 1e-6, gpu, rows + 7)
+    g = torch.Generator(device=gpu).manual_seed(dim + rows)
+    x = (torch.randn(rows, dim, generator=g, device=gpu) * 3).half()
+    r = torch.randn(rows, dim, generator=g, device=gpu).half()
+    U = (torch.randn(n_u, dim, rank, generator=g, device=gpu) * 0.05).half()
+    S, rpad = (dim + 255) // 256, (rank + 31) // 32 * 32
+    with torch.no_grad():
+        out, parts = kernels.rmsnorm_xu(x, m.weight, 1e-6, U)
+        assert torch.equal(out, kernels.rmsnorm(x, m.weight, 1e-6))
+        out2, y, parts2 = kernels.rmsnorm_xu(x, m.weight, 1e-6, U, residual=r)
+        ref_out, ref_y = kernels.rmsnorm(x, m.weight, 1e-6, residual=r)
+        assert torch.equal(out2, ref_out) and torch.equal(y, ref_y)
+        again = kernels.rmsnorm_xu(x, m.weight, 1e-6, U, residual=r)[2]
+    torch.cuda.synchronize()
+    assert tuple(parts.shape) == (n_u, S, rows, rpad)
+    assert torch.equal(parts2, again)
+    assert not bool(parts[..., rank:].any())
+    for o, pt in ((out, parts), (out2, parts2)):
+        ref = torch.matmul(o.float().unsqueeze(0), U.float())  # (n_u, rows, rank)
+        ok, worst = _xu_bar(pt.sum(1)[..., :rank], ref)
+        assert ok, worst
+    if n_u > 1:
+        wrong = torch.matmul(out.float().unsqueeze(0), U.flip(0).float())
+        assert not _xu_bar(parts.sum(1)[..., :rank], wrong)[0]
+
+
 def _rope(dev, positions):
     from glorcq_amd.synthetic_model import qwen3_moe_config
     from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeRotaryEmbedding
@@ -168,6 +212,40 @@ def test_decode_attention_matches_fp32(gpu, B, Hq, Hk, L, maxlen):
     assert bool((err <= 2e-3 + 1e-2 * ref.abs()).all()), float(err.max())
 
 
+@pytest.mark.parametrize("B,Hq,Hk,L,maxlen,rank", [(1, 32, 4, 600, 640, 64),
+                                                    (2, 32, 4, 1, 640, 64),
+                                                    (3, 16, 4, 300, 512, 32),
+                                                    (1, 8, 8, 129, 256, 128)])
+def test_decode_attention_xu(gpu, B, Hq, Hk, L, maxlen, rank):
+    """glq_decode_attention_xu: out carries the bits of glq_decode_attention
+    and the KV groups' partials summed give out U within fp32 rounding of the
+    fp32 product; repeated calls give the same bits and advance the fill
+    counter once each; a planted wrong row order of U fails the bar."""
+    hd = 128
+    g = torch.Generator(device=gpu).manual_seed(L + 3 * B)
+    q = torch.randn(B, Hq, hd, generator=g, device=gpu).half()
+    kc = torch.randn(B, Hk, maxlen, hd, generator=g, device=gpu).half()
+    vc = torch.randn(B, Hk, maxlen, hd, generator=g, device=gpu).half()
+    U = (torch.randn(Hq * hd, rank, generator=g, device=gpu) * 0.05).half()
+    ln = torch.tensor([L], dtype=torch.int32, device=gpu)
+    adv = torch.tensor(0, dtype=torch.int64, device=gpu)
+    scale = hd ** -0.5
+    ref_out = kernels.decode_attention(q, kc, vc, ln, scale)
+    ws = kernels.decode_attention_workspace(q, kc)
+    out, parts = kernels.decode_attention(q, kc, vc, ln, scale, advance=adv, workspace=ws, U=U)
+    out2, parts2 = kernels.decode_attention(q, kc, vc, ln, scale, advance=adv, workspace=ws,
+                                            U=U)
+    torch.cuda.synchronize()
+    assert int(adv) == 2
+    assert torch.equal(out, ref_out) and torch.equal(out2, out) and torch.equal(parts2, parts)
+    assert tuple(parts.shape) == (Hk, B, (rank + 31) // 32 * 32)
+    xu = parts.sum(0)[:, :rank]
+    ok, worst = _xu_bar(xu, out.float() @ U.float())
+    assert ok, worst
+    wrong = out.float() @ U.roll(Hq // Hk * hd, dims=0).float()
+    assert not _xu_bar(xu, wrong)[0]
+
+
 def _models(dev, layers=2):
     from glorcq_amd.synthetic_model import build_qwen3_moe, qwen3_moe_config
 
@@ -179,14 +257,15 @@ def _models(dev, layers=2):
 
 
 @torch.no_grad()
-@pytest.mark.parametrize("B", [2, 12])
+@pytest.mark.parametrize("B", [1, 2, 12])
 def test_fused_layers_match_framework_layers(gpu, B):
     """The same weights (same seed) with the fused decoder layers and with
     transformers' layer code: a 20-token prefill and 8 decode steps through
     static caches give logits within 1 % of the range and the same greedy
     tokens where the margin allows; the caches agree within fp16 rounding.
-    B = 12 takes the 2 < M <= 16 GEMV forms (K-split stream, and the
-    one-shot kernel for the 4096-wide o projection)."""
+    B = 1 and 2 take x U from the launches that produce the projections'
+    inputs (glq_rmsnorm_xu for q/k/v, glq_decode_attention_xu for o); B = 12
+    the token-tile forms with x U in their own launches."""
     from glorcq_amd.graph_wrapper import _static_cache
 
     cfg, fused, plain = _models(gpu)
@@ -208,7 +287,7 @@ def test_fused_layers_match_framework_layers(gpu, B):
         t = b.argmax(-1, keepdim=True)
         outs = [m(input_ids=t, past_key_values=c, use_cache=True, return_dict=False)[0]
                 for m, c in zip((fused, plain), caches)]
-    assert checked >= 8
+    assert checked >= min(8, 4 * B)  # (8 steps: B = 1 offers 8 comparisons in all)
     for la, lb in zip(caches[0].layers, caches[1].layers):
         assert int(la.cumulative_length) == int(lb.cumulative_length) == 28
         n = 28

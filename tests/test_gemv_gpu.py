@@ -391,6 +391,52 @@ def test_clustered_u_index(gpu, M):
     for i, p in enumerate(ps):
         q = dataclasses.replace(p, x=x, U=Us[uidx[i]])
         assert_parity(y[i], oracle_y(q), f"item {i}")
+    # a given per U (C, M, r), item i reading row block u_index[i]: the same
+    # bits as the batched call with each item's a copied out
+    a = K_.lowrank_xu(x.to(gpu), Us.to(gpu))  # (3, M, r)
+    ya = K_.packed_dequant_matmul_batched(*args, SV=st("SV"), precomputed_xU=a,
+                                          u_index=torch.tensor(uidx, dtype=torch.int32,
+                                                               device=gpu))
+    yacopy = K_.packed_dequant_matmul_batched(*args, SV=st("SV"),
+                                              precomputed_xU=a[uidx].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(ya, yacopy)
+    for i, p in enumerate(ps):
+        q = dataclasses.replace(p, x=x, U=Us[uidx[i]])
+        assert_parity(ya[i], oracle_y(q), f"item {i}, a per U")
+
+
+@pytest.mark.parametrize("M,bits,nb,uidx", [(1, 4, 3, [0] * 8 + [1, 2]), (3, 4, 2, [1, 0, 1]),
+                                             (5, 4, 1, [0, 0]), (16, 4, 2, None),
+                                             (1, 2, 2, None), (2, 2, 4, [3, 1])])
+def test_parts_entry_point(gpu, M, bits, nb, uidx):
+    """glq_gemv_lora_parts: a given as fp32 partials (blocks, P, M, rpad),
+    item i summing block u_index[i] in order -- the same bits as the batched
+    GEMV given a = fp16 of that sum (sequential fp32 adds, the kernels'
+    order) for each item, and parity with the oracle.  M = 1 takes the lane
+    kernel, 3 the streaming kernel, 5 and 16 the token-tile form."""
+    K, N, r, P = 2048, 512, 64, 8
+    E = len(uidx) if uidx is not None else nb
+    ps = [fmt.make_linear(K, N, bits=bits, rank=r, M=M, seed=700 + i) for i in range(E)]
+    x = ps[0].x.to(gpu)
+    gen = torch.Generator().manual_seed(M + 10 * bits)
+    parts = (torch.randn(nb, P, M, r, generator=gen) * 0.3).float().to(gpu)
+    st = lambda k: torch.stack([getattr(p, k) for p in ps]).to(gpu)  # noqa: E731
+    ui = torch.tensor(uidx, dtype=torch.int32, device=gpu) if uidx is not None else None
+    y = K_.packed_dequant_matmul_parts(x, st("codes"), st("scales"), st("zeros"), bits, 128,
+                                       st("SV"), parts, u_index=ui)
+    acc = torch.zeros(nb, M, r, dtype=torch.float32, device=gpu)
+    for p in range(P):  # the kernels' order
+        acc = acc + parts[:, p]
+    a = acc.half()
+    blocks = uidx if uidx is not None else list(range(nb))
+    ya = K_.packed_dequant_matmul_batched(x, st("codes"), st("scales"), st("zeros"), bits, 128,
+                                          SV=st("SV"), precomputed_xU=a[blocks].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(y, ya)
+    for i, p in enumerate(ps):
+        assert_parity(y[i], oracle_y(dataclasses.replace(p, x=ps[0].x), xu=a[blocks[i]].cpu()),
+                      f"item {i}")
 
 
 @pytest.mark.parametrize("bits", [2, 4])
