@@ -37,6 +37,14 @@ class MoeParams(ctypes.Structure):
     ]
 
 
+class TurboMat(ctypes.Structure):
+    """glq_turbo_mat (include/glorcq_hip.h), field for field."""
+    _fields_ = [
+        ("x_rot", _vp), ("codes", _vp), ("norms", _vp), ("centroids", _vp), ("SV", _vp),
+        ("parts", _vp), ("cluster", _vp), ("blocks", _i64),
+    ]
+
+
 # name -> (restype, argtypes); must match include/glorcq_hip.h exactly.
 SIGNATURES = {
     "glq_version": (_c_int, []),
@@ -135,6 +143,21 @@ SIGNATURES = {
         _i64, _i64, _i64, _i64, _c_int,  # tokens, hidden, experts, top_k, norm
         _vp, _vp, _vp, _vp,             # sel, weights, shared_gate, logits
         _vp, _i64, _vp,                 # workspace, bytes, stream
+    ]),
+    "glq_turbo_moe_prep": (_c_int, [
+        _vp, _vp, _vp, _i64, _i64, _i64, _i64,  # h, router_w, shared_gate_w, tokens, hidden, E, k
+        _c_int, _vp, _vp, _vp, _vp,             # norm, sel, weights, shared_gate, logits
+        _vp, _i64, _vp, _vp,                    # workspace, bytes, rht_signs, x_rot
+        _vp, _i64, _i64, _vp, _vp,              # U, n_u, rank, parts, stream
+    ]),
+    "glq_turbo_moe_down_prep": (_c_int, [
+        _i64, _i64, _vp, _vp, _vp, _vp,         # picks, inter_dim, inter, Pi, rht_signs, xd
+        _vp, _i64, _vp, _vp, _i64, _i64,        # U, n_clusters, cluster, sel, experts, rank
+        _vp, _vp,                               # parts, stream
+    ]),
+    "glq_turbo_moe_gemv2": (_c_int, [
+        _i64, _i64, _i64, _i64, _i64, _vp,      # picks, x_div, K, N, experts, sel
+        _vp, _vp, _i64, _i64, _vp, _vp,         # m, up, rank, P, y, stream
     ]),
     "glq_turbo_moe_gemv": (_c_int, [
         _i64, _i64, _vp, _i64, _i64, _i64,  # picks, x_div, x_rot, K, N, experts

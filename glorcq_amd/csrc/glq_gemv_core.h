@@ -646,6 +646,28 @@ __device__ void gemv_tile(const Src& src, const TileShape& sh, int item, int til
 }
 
 // inter = fp16(fp16(silu(fp16(g))) * fp16(u)): the rounding points of
+// y = fp16((1/sqrt(d)) H diag(signs) x) of one row of d = 2^logd fp16 values
+// (rht_forward(x.float(), signs).half(), inference/moe_block.py:351): the
+// row in LDS as fp32 (v, d floats), log2(d) butterfly passes with a barrier
+// each, the whole workgroup (nth threads) calling; the order of every sum is
+// rht_kernel's (glq_turbo.hip).
+__device__ inline void rht_row_f16(const __half* x, const float* signs, __half* y, int d, int logd,
+                                   float scale, float* v, int nth) {
+  for (int i = threadIdx.x; i < d; i += nth) v[i] = __half2float(x[i]) * signs[i];
+  __syncthreads();
+  for (int s = 0; s < logd; ++s) {
+    const int h = 1 << s;
+    for (int p = threadIdx.x; p < d / 2; p += nth) {
+      const int i = ((p >> s) << (s + 1)) | (p & (h - 1)), j = i + h;
+      const float u = v[i], w = v[j];
+      v[i] = u + w;
+      v[j] = u - w;
+    }
+    __syncthreads();
+  }
+  for (int i = threadIdx.x; i < d; i += nth) y[i] = __float2half(v[i] * scale);
+}
+
 // act_fn(gate(x)) * up(x) on fp16 tensors; the product of two fp16 values is
 // exact in fp32, so one rounding gives the correctly rounded fp16 product.
 __device__ __forceinline__ __half swiglu_fp16(float g, float u) {

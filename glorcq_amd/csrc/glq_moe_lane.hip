@@ -1355,6 +1355,60 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_route_only_kernel(MoeLane
   moe_lane_router<RC>(a, blockIdx.x / a.nrw, blockIdx.x % a.nrw, smem);
 }
 
+// The first launch of a TurboQuant block's decode step: routing, the
+// randomized Hadamard transform of the tokens' rows for gate and up, and the
+// fp32 partials of h U for every gate and up cluster -- three jobs that need
+// only h, in one launch.  Workgroups [0, B nrw): the router
+// (moe_lane_router); then, with signs, B workgroups of one row's transform
+// (rht_kernel's arithmetic: fp32 butterflies in LDS, one rounding); then
+// pairs of (U, 256-row slice) jobs, two per workgroup (lowrank_partial over
+// the B token rows) into parts[u][s] (n_u, S, B, rpad).
+struct TurboPrepArgs {
+  MoeLaneArgs a;
+  const float* signs;  // (H,) or null: no transform
+  __half* xrot;        // (B, H)
+  int logd;
+  float scale;
+  const __half* U;     // (n_u, H, rank)
+  int n_u, S, rank, rpad;
+  float* parts;        // (n_u, S, B, rpad)
+};
+
+constexpr int kPrepJobLds = (4 * 4 * 64) * 4 + 16 * kLowrankRows * 2 + 64 * kLowrankUtStride * 2;
+
+template <int RC, int MC>
+__global__ __launch_bounds__(kMoeLaneThreads) void turbo_prep_kernel(TurboPrepArgs g) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const MoeLaneArgs& a = g.a;
+  int b = blockIdx.x;
+  if (b < a.B * a.nrw) {
+    moe_lane_router<RC>(a, b / a.nrw, b % a.nrw, smem);
+    return;
+  }
+  b -= a.B * a.nrw;
+  if (g.signs) {
+    if (b < a.B) {  // the transform of token b's row
+      rht_row_f16(a.h + (int64_t)b * a.H, g.signs, g.xrot + (int64_t)b * a.H, a.H, g.logd,
+                  g.scale, (float*)smem, kMoeLaneThreads);
+      return;
+    }
+    b -= a.B;
+  }
+  // two (U, slice) jobs: 256-thread groups side by side, each with its LDS
+  const int grp = threadIdx.x >> 8, tid = threadIdx.x & 255;
+  const int job = 2 * b + grp, njobs = g.n_u * g.S;
+  const int jc = min(job, njobs - 1);  // a group past the list computes job njobs-1 and writes nothing
+  const int u = jc / g.S, sl = jc - u * g.S;
+  unsigned char* gl = smem + grp * kPrepJobLds;
+  float* red = (float*)gl;
+  __half* xl = (__half*)(red + 4 * 4 * 64);
+  __half* ut = xl + 16 * kLowrankRows;
+  auto xrow = [&](int m) { return a.h + (int64_t)m * a.H; };
+  lowrank_partial<MC>(xrow, a.B, a.H, g.rank, g.rpad, g.U + (int64_t)u * a.H * g.rank, sl,
+                      job < njobs ? g.parts + ((int64_t)u * g.S + sl) * a.B * g.rpad : nullptr,
+                      red, xl, tid, ut);
+}
+
 // out[t][n] = fp16(sum_k w[t][k] y[t k + k][n] + sg[t] shared[t][n])
 // (+ residual): the lane path's combine (fmaf over the picks in pick order,
 // then the gated shared term), one thread per output.
@@ -1444,6 +1498,84 @@ extern "C" int glq_moe_route(const void* h, const void* router_w, const void* sh
   else if (rc == 4) moe_route_only_kernel<4><<<grid, block, lds, s>>>(a);
   else moe_route_only_kernel<8><<<grid, block, lds, s>>>(a);
   GLQ_LAUNCH_CHECK("moe_route_only_kernel");
+  return GLQ_OK;
+}
+
+extern "C" int glq_turbo_moe_prep(const void* h, const void* router_w, const void* shared_gate_w,
+                                  int64_t tokens, int64_t hidden, int64_t experts, int64_t top_k,
+                                  int norm_topk_prob, int32_t* sel, void* weights,
+                                  void* shared_gate, void* logits, void* workspace,
+                                  int64_t workspace_bytes, const float* rht_signs, void* x_rot,
+                                  const void* U, int64_t n_u, int64_t rank, float* parts,
+                                  void* stream) {
+  using namespace glq;
+  clear_error();
+  if (int rc = moe_route_shape(tokens, hidden, experts, top_k)) return rc;
+  GLQ_CHECK(tokens <= 16, "tokens must be <= 16 (got %lld)", (long long)tokens);
+  GLQ_CHECK(h && router_w && sel && weights && shared_gate, "null h, router_w or outputs");
+  GLQ_CHECK(((uintptr_t)h & 15) == 0 && ((uintptr_t)router_w & 15) == 0 &&
+                (!shared_gate_w || ((uintptr_t)shared_gate_w & 15) == 0),
+            "h, router_w and shared_gate_w must be 16-byte aligned");
+  GLQ_CHECK(!rht_signs || (x_rot && (hidden & (hidden - 1)) == 0),
+            "the transform needs x_rot and a power-of-two hidden size");
+  GLQ_CHECK(n_u >= 0 && (n_u == 0 || (U && parts && rank > 0 && rank <= 1024 && rank % 8 == 0 &&
+                                      ((uintptr_t)U & 15) == 0)),
+            "x U needs U (16-byte aligned), parts and a rank that is a multiple of 8");
+  const int64_t need = glq_moe_route_workspace_bytes(tokens, experts);
+  GLQ_CHECK(workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15) == 0,
+            "workspace of %lld bytes needed, 16-byte aligned", (long long)need);
+  TurboPrepArgs g;
+  memset(&g, 0, sizeof(g));
+  MoeLaneArgs& a = g.a;
+  a.B = (int)tokens;
+  a.H = (int)hidden;
+  a.E = (int)experts;
+  a.topk = (int)top_k;
+  a.norm = norm_topk_prob ? 1 : 0;
+  a.h = (const __half*)h;
+  a.rw = (const __half*)router_w;
+  a.sgw = (const __half*)shared_gate_w;
+  a.sel = sel;
+  a.wts = (__half*)weights;
+  a.sg = (__half*)shared_gate;
+  a.logits = (__half*)logits;
+  a.rcnt = (unsigned*)workspace;
+  a.lgw = (__half*)((char*)workspace + 4 * align_up(tokens, 64));
+  const int rc = hidden <= 512 ? 1 : hidden <= 1024 ? 2 : hidden <= 2048 ? 4 : 8;
+  const int rb = rc >= 8 ? 2 : 16 / rc, nrow = (int)experts + (shared_gate_w ? 1 : 0);
+  a.nrw = (nrow + 8 * rb - 1) / (8 * rb);
+  g.signs = rht_signs;
+  g.xrot = (__half*)x_rot;
+  int logd = 0;
+  while ((1ll << logd) < hidden) ++logd;
+  g.logd = logd;
+  g.scale = 1.f / sqrtf((float)hidden);
+  g.U = (const __half*)U;
+  g.n_u = (int)n_u;
+  g.S = (int)((hidden + kLowrankRows - 1) / kLowrankRows);
+  g.rank = (int)rank;
+  g.rpad = (int)align_up(rank, 32);
+  g.parts = parts;
+  const size_t lds_route = (size_t)(((2 * (experts + 1) + 15) & ~15) + 4 * experts + 4 * 16);
+  const size_t lds = std::max({lds_route, rht_signs ? (size_t)4 * hidden : (size_t)0,
+                               n_u > 0 ? (size_t)2 * kPrepJobLds : (size_t)0});
+  const int64_t grid = tokens * a.nrw + (rht_signs ? tokens : 0) + (n_u * g.S + 1) / 2;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 gd((unsigned)grid), block(kMoeLaneThreads);
+#define GLQ_PREP_LAUNCH(RC_, MC_)                                           \
+  do {                                                                      \
+    static size_t attr = 64 * 1024;                                         \
+    int rc2 = set_lds_limit(turbo_prep_kernel<RC_, MC_>, lds, attr);        \
+    if (rc2) return rc2;                                                    \
+    turbo_prep_kernel<RC_, MC_><<<gd, block, lds, s>>>(g);                  \
+  } while (0)
+  const bool mc4 = tokens >= 3;
+  if (rc == 1) { if (mc4) GLQ_PREP_LAUNCH(1, 4); else GLQ_PREP_LAUNCH(1, 1); }
+  else if (rc == 2) { if (mc4) GLQ_PREP_LAUNCH(2, 4); else GLQ_PREP_LAUNCH(2, 1); }
+  else if (rc == 4) { if (mc4) GLQ_PREP_LAUNCH(4, 4); else GLQ_PREP_LAUNCH(4, 1); }
+  else { if (mc4) GLQ_PREP_LAUNCH(8, 4); else GLQ_PREP_LAUNCH(8, 1); }
+#undef GLQ_PREP_LAUNCH
+  GLQ_LAUNCH_CHECK("turbo_prep_kernel");
   return GLQ_OK;
 }
 

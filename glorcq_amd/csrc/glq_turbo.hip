@@ -26,6 +26,7 @@
 // accuracy like the reference's fp32 FMA loop; y = fp16(acc * norm) as in the
 // reference.
 #include <algorithm>
+#include <cstring>
 
 #include "glq_gemv_core.h"
 
@@ -67,6 +68,12 @@ struct TurboArgs {
   const int32_t* xclus = nullptr;  // a row of item i: xclus[wsel[i]] * xu_tok + i / x_div (< xu_rows)
   int xu_tok = 0, xu_rows = 0;
   const __half* gate = nullptr;   // (items, M, N): y = fp16(fp16(silu(gate)) * y)
+  // a given as fp32 partials instead of xu (M = 1 items): a of item i is
+  // fp16(sum over s in order of parts[((blk * pP + s) * pM + t) * rpad + j]),
+  // blk = xclus[wsel[i]] and t = i / x_div with xclus (a per (cluster,
+  // token)), else blk = i and t = 0
+  const float* parts = nullptr;
+  int pP = 0, pM = 1, pB = 1;  // slices, token rows and blocks of parts
 };
 
 // Weight set, x row and low-rank row of an item.
@@ -122,12 +129,11 @@ __device__ __forceinline__ void turbo_decode(uint32_t w, const TurboLut& H, cons
   s1l = __builtin_bit_cast(f16x8, bl);
 }
 
-// Writes one 16-row tile: y = norm * acc + a SV^T + bias, rounded once to fp16.
+// norm * acc + a SV^T + bias of one 16-row tile (fp32), in acc's layout:
 // acc[i] of lane (li, kb) holds token 4kb + i, row r0 + li; a_l holds the
 // block's low-rank factor a (rows < mr, zero-padded to rpad columns).
-__device__ __forceinline__ void turbo_epilogue(const TurboArgs& a, f32x4 acc, int item, int m0,
-                                               int mr, int r0, const __half* a_l, int li,
-                                               int kb) {
+__device__ __forceinline__ f32x4 turbo_values(const TurboArgs& a, f32x4 acc, int item, int mr,
+                                              int r0, const __half* a_l, int li, int kb) {
   const int r = r0 + li, row = min(r, a.N - 1), w = turbo_w(a, item);
   const float nr = a.norms[(int64_t)w * a.n_es + row];
 #pragma unroll
@@ -144,15 +150,45 @@ __device__ __forceinline__ void turbo_epilogue(const TurboArgs& a, f32x4 acc, in
     }
   }
   const float bb = a.bias ? __half2float(a.bias[(int64_t)w * a.bias_es + row]) : 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] += bb;
+  return acc;
+}
+
+// Writes one 16-row tile: y = fp16(norm * acc + a SV^T + bias), or with gate
+// the SwiGLU of the gate's stored value and it.
+__device__ __forceinline__ void turbo_epilogue(const TurboArgs& a, f32x4 acc, int item, int m0,
+                                               int mr, int r0, const __half* a_l, int li,
+                                               int kb) {
+  const f32x4 v = turbo_values(a, acc, item, mr, r0, a_l, li, kb);
+  const int r = r0 + li;
   if (r < a.N) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = 4 * kb + i;
       if (m < mr) {
         const int64_t o = (int64_t)item * a.y_es + (int64_t)(m0 + m) * a.N + r;
-        a.y[o] = a.gate ? swiglu_fp16(__half2float(a.gate[o]), acc[i] + bb)
-                        : __float2half(acc[i] + bb);
+        a.y[o] = a.gate ? swiglu_fp16(__half2float(a.gate[o]), v[i]) : __float2half(v[i]);
       }
+    }
+  }
+}
+
+// The pair form's tile: y = fp16(fp16(silu(fp16(gate values))) * fp16(up
+// values)) -- the bits of the gate launch's store followed by the up
+// launch's SwiGLU store.
+__device__ __forceinline__ void turbo_pair_epilogue(const TurboArgs& g, const TurboArgs& u,
+                                                    f32x4 accg, f32x4 accu, int item, int m0,
+                                                    int mr, int r0, const __half* a_lg,
+                                                    const __half* a_lu, int li, int kb) {
+  const f32x4 vg = turbo_values(g, accg, item, mr, r0, a_lg, li, kb);
+  const f32x4 vu = turbo_values(u, accu, item, mr, r0, a_lu, li, kb);
+  const int r = r0 + li;
+  if (r < u.N) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 4 * kb + i;
+      if (m < mr) u.y[(int64_t)item * u.y_es + (int64_t)(m0 + m) * u.N + r] = swiglu_fp16(vg[i], vu[i]);
     }
   }
 }
@@ -163,7 +199,15 @@ __device__ __forceinline__ void turbo_epilogue(const TurboArgs& a, f32x4 acc, in
 __device__ __forceinline__ void turbo_stage(const TurboArgs& a, const __half* X, int item, int m0,
                                             int mr, int sb, int se, __half* xs, __half* a_l,
                                             bool with_a, int tid) {
-  if (with_a && a.sv) {
+  if (with_a && a.sv && a.parts) {  // (M = 1 items) a from the partials, in slice order
+    const int64_t blk = min(max(a.xclus ? (int64_t)a.xclus[turbo_w(a, item)] : (int64_t)item,
+                                (int64_t)0), (int64_t)a.pB - 1);
+    const int t = a.xclus ? item / a.x_div : 0;
+    const float* pp = a.parts + ((blk * a.pP) * a.pM + t) * a.rpad;
+    for (int j = tid; j < a.rpad; j += 256)
+      a_l[j] = j < a.rank ? __float2half(sum_strided(pp + j, (int64_t)a.pM * a.rpad, a.pP))
+                          : __float2half(0.f);
+  } else if (with_a && a.sv) {
     for (int idx = tid; idx < mr * a.rpad; idx += 256) {
       const int m = idx / a.rpad, j = idx - m * a.rpad;
       a_l[m * a.apad + j] = j < a.rank ? a.xu[turbo_arow(a, item) * a.xu_es +
@@ -256,11 +300,19 @@ __global__ __launch_bounds__(256) void turbo_stream_kernel(TurboArgs a) {
   }
 }
 
-__global__ __launch_bounds__(256) void turbo_gemv_kernel(TurboArgs a) {
+// PAIR: a second matrix u of the same shape (the up projection of a gate/up
+// pair, its own codes, norms, codebook, low-rank term and input) is walked
+// beside a, each with its own accumulator and the same order of sums as a
+// launch of its own, and the tile's store is the SwiGLU of the two
+// (turbo_pair_epilogue) -- one launch where gate and up took two.
+template <bool PAIR>
+__global__ __launch_bounds__(256) void turbo_gemv_kernel(TurboArgs a, TurboArgs u) {
   extern __shared__ __align__(16) unsigned char smem[];
-  float* red = (float*)smem;                  // [4 waves][4][64] partial sums
-  __half* a_l = (__half*)(smem + 4096);       // [16][apad] low-rank factor a
-  __half* xs = a_l + 16 * a.apad;             // [mr][xstride], one K segment
+  constexpr int NM = PAIR ? 2 : 1;
+  float* red = (float*)smem;                       // [NM][4 waves][4][64] partial sums
+  __half* a_l = (__half*)(smem + 4096 * NM);       // [16][apad] low-rank factor a (u's after)
+  __half* a_lu = a_l + 16 * a.apad;
+  __half* xs = a_l + NM * 16 * a.apad;             // [mr][xstride], one K segment (u's after)
   const int per_item = a.rwgs * a.twgs;
   const int item = blockIdx.x / per_item;
   const int rem = blockIdx.x - item * per_item;
@@ -271,16 +323,27 @@ __global__ __launch_bounds__(256) void turbo_gemv_kernel(TurboArgs a) {
   const int part = wave % wpt, r0 = (rg * tpw + wave / wpt) * 16;
   const int m0 = 16 * tb, mr = min(16, a.M - m0);  // token rows of this block
   const __half* X = a.x + turbo_xrow(a, item) * a.x_es + (int64_t)m0 * a.K;
+  const __half* Xu = PAIR ? u.x + turbo_xrow(u, item) * u.x_es + (int64_t)m0 * u.K : X;
+  const bool own_xu = PAIR && Xu != X;  // (uniform) u's input staged apart
+  __half* xsu = own_xu ? xs + mr * a.xstride : xs;
 
   const TurboLut H = turbo_lut(a.cent, false), L = turbo_lut(a.cent, true);
+  TurboLut Hu = H, Lu = L;
+  if constexpr (PAIR) {
+    Hu = turbo_lut(u.cent, false);
+    Lu = turbo_lut(u.cent, true);
+  }
   const int row = min(r0 + li, a.N - 1);
   const uint32_t* crow =
       a.codes + (int64_t)turbo_w(a, item) * a.c_es + (int64_t)row * a.kw;
+  const uint32_t* crowu =
+      PAIR ? u.codes + (int64_t)turbo_w(u, item) * u.c_es + (int64_t)row * u.kw : crow;
   const int wlast = a.kw - 4;  // last whole 16-byte piece (kw is a multiple of 4)
   const __half* xr = xs + min(li, mr - 1) * a.xstride;
+  const __half* xru = xsu + min(li, mr - 1) * a.xstride;
   const int nsteps = (a.K + 255) >> 8;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  constexpr int PF = kTurboPF;  // 256-code steps of codes in flight per wave
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+  constexpr int PF = kTurboPF;  // 256-code steps of codes in flight per wave (per matrix)
 
   for (int sb = 0; sb < nsteps; sb += a.segsteps) {
     const int se = min(nsteps, sb + a.segsteps);
@@ -289,35 +352,48 @@ __global__ __launch_bounds__(256) void turbo_gemv_kernel(TurboArgs a) {
     const int jn = max(0, min(se, j0 + q) - j0);  // and its step count
     // a step of a row is 16 words; lane kb holds words 4kb..4kb+3 (clamped:
     // words past the row end meet zero x and add nothing)
-    u32x4 buf[PF];
+    u32x4 buf[PF], bufu[PF];
 #pragma unroll
-    for (int p = 0; p < PF; ++p)
-      buf[p] = p < jn ? *(const u32x4*)(crow + min(16 * (j0 + p) + 4 * kb, wlast))
-                      : u32x4{0, 0, 0, 0};
+    for (int p = 0; p < PF; ++p) {
+      const int wo = min(16 * (j0 + p) + 4 * kb, wlast);
+      buf[p] = p < jn ? *(const u32x4*)(crow + wo) : u32x4{0, 0, 0, 0};
+      if constexpr (PAIR) bufu[p] = p < jn ? *(const u32x4*)(crowu + wo) : u32x4{0, 0, 0, 0};
+    }
     if (sb > 0) __syncthreads();  // every wave is done with the previous segment
     turbo_stage(a, X, item, m0, mr, sb, se, xs, a_l, sb == 0, tid);
+    if constexpr (PAIR) {
+      if (own_xu) turbo_stage(u, Xu, item, m0, mr, sb, se, xsu, a_lu, sb == 0, tid);
+      else turbo_stage(u, Xu, item, m0, mr, sb, sb, xsu, a_lu, sb == 0, tid);  // a alone
+    }
     __syncthreads();
-    auto consume = [&](const u32x4& w, int j) {
+    auto consume = [&](const u32x4& w, const u32x4& wu, int j) {
       turbo_step(w, xr + (j0 + j - sb) * 256 + 64 * kb, H, L, acc);
+      if constexpr (PAIR) turbo_step(wu, xru + (j0 + j - sb) * 256 + 64 * kb, Hu, Lu, accu);
     };
     int jj = 0;
     for (; jj + PF <= jn; jj += PF) {  // whole rounds: refill each slot after use
 #pragma unroll
       for (int p = 0; p < PF; ++p) {
-        const u32x4 w = buf[p];
-        if (jj + p + PF < jn)
-          buf[p] = *(const u32x4*)(crow + min(16 * (j0 + jj + p + PF) + 4 * kb, wlast));
-        consume(w, jj + p);
+        const u32x4 w = buf[p], wu = PAIR ? bufu[p] : w;
+        if (jj + p + PF < jn) {
+          const int wo = min(16 * (j0 + jj + p + PF) + 4 * kb, wlast);
+          buf[p] = *(const u32x4*)(crow + wo);
+          if constexpr (PAIR) bufu[p] = *(const u32x4*)(crowu + wo);
+        }
+        consume(w, wu, jj + p);
       }
     }
 #pragma unroll
     for (int p = 0; p < PF; ++p)  // the last jn % PF steps
-      if (jj + p < jn) consume(buf[p], jj + p);
+      if (jj + p < jn) consume(buf[p], PAIR ? bufu[p] : buf[p], jj + p);
   }
   // acc[i] of lane (li, kb): token 4kb + i, row li of the tile
   if (wpt > 1) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
+    for (int i = 0; i < 4; ++i) {
+      red[(wave * 4 + i) * 64 + lane] = acc[i];
+      if constexpr (PAIR) red[1024 + (wave * 4 + i) * 64 + lane] = accu[i];
+    }
     __syncthreads();
     if (part != 0) return;
 #pragma unroll
@@ -325,9 +401,97 @@ __global__ __launch_bounds__(256) void turbo_gemv_kernel(TurboArgs a) {
       float v = red[(wave * 4 + i) * 64 + lane];
       for (int w2 = 1; w2 < wpt; ++w2) v += red[((wave + w2) * 4 + i) * 64 + lane];
       acc[i] = v;
+      if constexpr (PAIR) {
+        float vu = red[1024 + (wave * 4 + i) * 64 + lane];
+        for (int w2 = 1; w2 < wpt; ++w2) vu += red[1024 + ((wave + w2) * 4 + i) * 64 + lane];
+        accu[i] = vu;
+      }
     }
   }
-  turbo_epilogue(a, acc, item, m0, mr, r0, a_l, li, kb);
+  if constexpr (PAIR)
+    turbo_pair_epilogue(a, u, acc, accu, item, m0, mr, r0, a_l, a_lu, li, kb);
+  else
+    turbo_epilogue(a, acc, item, m0, mr, r0, a_l, li, kb);
+}
+
+// ---------------------------------------------------------------------------
+// The down projection's inputs of a TurboQuant block's decode step, for
+// every pick p, in one launch: xd[p] = fp16(inter[p] Pi^T) (the QR rotation:
+// the reference's fp16(x.float() @ Pi.float().T), moe_block.py:352-356) or,
+// with signs, the transform of inter[p] (rht_row_f16); and the fp32 partials
+// of inter[p] U_down[cluster(sel[p])] over 256-row slices (the down GEMV's a:
+// each pick's own x U, moe_block.py:661-676).
+// Rotation workgroup (16-row block of xd, 16-pick block): its 4 waves split
+// K; A = the picks' inter rows, B = Pi's rows (row n weighs output n,
+// contiguous in k), one v_mfma_f32_16x16x32_f16 per 32 k; the waves' tiles
+// summed in LDS in wave order.
+// ---------------------------------------------------------------------------
+struct TurboDownPrepArgs {
+  const __half* inter;    // (P, I)
+  const __half* Pi;       // (I, I), or null with signs
+  const float* signs;     // (I,), or null
+  __half* xd;             // (P, I)
+  int P, I, logd;
+  float scale;
+  int nrot;               // workgroups of the rotation, first in the grid
+  const __half* U;        // (C, I, rank), or null: no x U
+  const int32_t* cluster;  // (E,) expert -> U
+  const int32_t* sel;     // (P,) pick -> expert
+  int E, C, S, rank, rpad;
+  float* parts;           // (P, S, 1, rpad)
+};
+
+constexpr int kDownPrepLds = 4 * 4 * 64 * 4 + 16 * kLowrankRows * 2;
+
+__global__ __launch_bounds__(256) void turbo_down_prep_kernel(TurboDownPrepArgs g) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x;
+  int b = blockIdx.x;
+  if (b < g.nrot) {
+    if (g.signs) {
+      rht_row_f16(g.inter + (int64_t)b * g.I, g.signs, g.xd + (int64_t)b * g.I, g.I, g.logd,
+                  g.scale, (float*)smem, 256);
+      return;
+    }
+    const int nrb = (g.I + 15) / 16, rb = b % nrb, pb = b / nrb;
+    const int wave = tid >> 6, lane = tid & 63, li = lane & 15, kb = lane >> 4;
+    const __half* brow = g.Pi + (int64_t)min(rb * 16 + li, g.I - 1) * g.I;
+    const int pa = pb * 16 + li;  // this lane's A row (pick)
+    const __half* arow = g.inter + (int64_t)min(pa, g.P - 1) * g.I;
+    const int nsteps = g.I / 32, q = (nsteps + 3) / 4;
+    const int s0 = wave * q, s1 = min(nsteps, s0 + q);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int st = s0; st < s1; ++st) {
+      const int k = 32 * st + 8 * kb;
+      const f16x8 av = pa < g.P ? *(const f16x8*)(arow + k) : f16x8{};
+      acc = mfma_16x16x32(av, *(const f16x8*)(brow + k), acc);
+    }
+    // acc[i] of lane (li, kb): pick 4kb + i, output row li of the block
+    float* red = (float*)smem;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
+    __syncthreads();
+    if (wave == 0) {
+      const int n = rb * 16 + li;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = ((red[i * 64 + lane] + red[(4 + i) * 64 + lane]) +
+                         red[(8 + i) * 64 + lane]) + red[(12 + i) * 64 + lane];
+        const int p = pb * 16 + 4 * kb + i;
+        if (p < g.P && n < g.I) g.xd[(int64_t)p * g.I + n] = __float2half(v);
+      }
+    }
+    return;
+  }
+  b -= g.nrot;  // x U job (pick, slice)
+  const int p = b / g.S, sl = b - p * g.S;
+  const int e = min(max(g.sel[p], 0), g.E - 1);
+  const int c = min(max(g.cluster[e], 0), g.C - 1);
+  float* red = (float*)smem;
+  __half* xl = (__half*)(red + 4 * 4 * 64);
+  auto xrow = [&](int) { return g.inter + (int64_t)p * g.I; };
+  lowrank_partial<1>(xrow, 1, g.I, g.rank, g.rpad, g.U + (int64_t)c * g.I * g.rank, sl,
+                     g.parts + ((int64_t)p * g.S + sl) * g.rpad, red, xl, tid);
 }
 
 // ---------------------------------------------------------------------------
@@ -375,7 +539,10 @@ __global__ __launch_bounds__(256) void rht_kernel(const TI* __restrict__ x,
 namespace glq {
 namespace {
 // Picks the form and launches; a holds every pointer, size and item field.
-int turbo_run(TurboArgs& a, int64_t items, int64_t M, int64_t K, int64_t N, hipStream_t s) {
+// With u (the pair form: a second matrix of the same shape, same items) the
+// one-shot kernel runs both, with the plan a launch of a alone would take.
+int turbo_run(TurboArgs& a, int64_t items, int64_t M, int64_t K, int64_t N, hipStream_t s,
+              TurboArgs* u = nullptr) {
   const int mr = (int)std::min<int64_t>(16, M);
   const int nsteps = (int)((K + 255) / 256);
   const int fit = (kTurboXBudget / (2 * mr) - 8) / 256;  // steps of a segment that fit
@@ -385,7 +552,7 @@ int turbo_run(TurboArgs& a, int64_t items, int64_t M, int64_t K, int64_t N, hipS
   const int64_t T = (N + 15) / 16, tiles = items * a.twgs * T;
   const int64_t kpad = (int64_t)nsteps * 256;
   const size_t stream_lds = (size_t)16 * a.apad * 2 + (size_t)mr * (kpad + 8) * 2;
-  if (tiles >= kTurboStreamTiles && stream_lds <= (size_t)kTurboStreamLds) {
+  if (!u && tiles >= kTurboStreamTiles && stream_lds <= (size_t)kTurboStreamLds) {
     // streaming form: the whole K staged once per workgroup, waves walk tiles
     a.segsteps = nsteps;
     a.xstride = (int)kpad + 8;
@@ -407,13 +574,31 @@ int turbo_run(TurboArgs& a, int64_t items, int64_t M, int64_t K, int64_t N, hipS
   a.wpt = tiles >= 2048 ? 1 : tiles >= 1024 ? 2 : 4;
   const int tpw = 4 / a.wpt;
   a.rwgs = (int)((T + tpw - 1) / tpw);
-  const size_t lds = 4096 + (size_t)16 * a.apad * 2 + (size_t)mr * a.xstride * 2;
-  static size_t attr = 64 * 1024;
-  int rc = set_lds_limit(turbo_gemv_kernel, lds, attr);
-  if (rc) return rc;
   const int64_t grid = items * a.rwgs * a.twgs;
   GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
-  turbo_gemv_kernel<<<dim3((unsigned)grid), dim3(256), lds, s>>>(a);
+  if (u) {
+    // the same plan for u (its staging and order of sums are a's)
+    u->segsteps = a.segsteps;
+    u->xstride = a.xstride;
+    u->twgs = a.twgs;
+    u->wpt = a.wpt;
+    u->rwgs = a.rwgs;
+    GLQ_CHECK(u->apad == a.apad && u->K == a.K && u->N == a.N && u->M == a.M &&
+                  u->kw == a.kw && a.segsteps * 256 >= a.K,
+              "the pair's matrices must share their shape, rank and one K segment");
+    const size_t lds = 2 * 4096 + (size_t)2 * 16 * a.apad * 2 + (size_t)2 * mr * a.xstride * 2;
+    static size_t attr = 64 * 1024;
+    int rc = set_lds_limit(turbo_gemv_kernel<true>, lds, attr);
+    if (rc) return rc;
+    turbo_gemv_kernel<true><<<dim3((unsigned)grid), dim3(256), lds, s>>>(a, *u);
+    GLQ_LAUNCH_CHECK("turbo_gemv_kernel");
+    return GLQ_OK;
+  }
+  const size_t lds = 4096 + (size_t)16 * a.apad * 2 + (size_t)mr * a.xstride * 2;
+  static size_t attr = 64 * 1024;
+  int rc = set_lds_limit(turbo_gemv_kernel<false>, lds, attr);
+  if (rc) return rc;
+  turbo_gemv_kernel<false><<<dim3((unsigned)grid), dim3(256), lds, s>>>(a, a);
   GLQ_LAUNCH_CHECK("turbo_gemv_kernel");
   return GLQ_OK;
 }
@@ -534,6 +719,134 @@ extern "C" int glq_turbo_moe_gemv(int64_t picks, int64_t x_div, const void* x_ro
   a.xu_rows = (int)std::min<int64_t>(xu_rows, 1 << 30);
   a.gate = (const __half*)gate;
   return turbo_run(a, picks, 1, K, N, (hipStream_t)stream);
+}
+
+namespace glq {
+namespace {
+// TurboArgs of one projection of glq_turbo_moe_gemv2.
+int turbo_mat_args(const glq_turbo_mat& m, int64_t picks, int64_t x_div, int64_t K, int64_t N,
+                   int64_t experts, const int32_t* sel, int64_t rank, int64_t P, void* y,
+                   TurboArgs& a) {
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  GLQ_CHECK(m.x_rot && m.codes && m.norms && m.centroids, "null projection pointer");
+  GLQ_CHECK(al16(m.x_rot) && al16(m.codes), "x_rot and codes must be 16-byte aligned");
+  const bool lora = m.SV != nullptr && rank > 0;
+  GLQ_CHECK(!lora || (m.parts && P >= 1 && m.blocks >= 1 && al16(m.SV) &&
+                      ((uintptr_t)m.parts & 3) == 0),
+            "SV needs parts, P >= 1, blocks >= 1 and 16-byte alignment");
+  a.x = (const __half*)m.x_rot;
+  a.x_es = K;
+  a.codes = (const uint32_t*)m.codes;
+  a.c_es = N * (K / 16);
+  a.norms = m.norms;
+  a.n_es = N;
+  a.cent = m.centroids;
+  a.xu = nullptr;
+  a.xu_es = 0;
+  a.sv = lora ? (const __half*)m.SV : nullptr;
+  a.sv_es = N * rank;
+  a.bias = nullptr;
+  a.bias_es = 0;
+  a.rank = lora ? (int)rank : 0;
+  a.rpad = (int)align_up(a.rank, 32);
+  a.apad = a.rpad + 8;
+  a.y = (__half*)y;
+  a.y_es = N;
+  a.M = 1;
+  a.K = (int)K;
+  a.N = (int)N;
+  a.kw = (int)(K / 16);
+  a.wsel = sel;
+  a.nw = (int)experts;
+  a.x_div = (int)x_div;
+  a.xclus = lora ? m.cluster : nullptr;
+  a.xu_tok = 0;
+  a.xu_rows = 0;
+  a.gate = nullptr;
+  a.parts = lora ? m.parts : nullptr;
+  a.pP = (int)P;
+  a.pM = m.cluster ? (int)((picks + x_div - 1) / x_div) : 1;
+  a.pB = (int)std::min<int64_t>(m.blocks, 1 << 30);
+  return GLQ_OK;
+}
+}  // namespace
+}  // namespace glq
+
+extern "C" int glq_turbo_moe_gemv2(int64_t picks, int64_t x_div, int64_t K, int64_t N,
+                                   int64_t experts, const int32_t* sel, const glq_turbo_mat* m,
+                                   const glq_turbo_mat* up, int64_t rank, int64_t P, void* y,
+                                   void* stream) {
+  using namespace glq;
+  clear_error();
+  GLQ_CHECK(picks >= 0 && K >= 0 && N >= 0 && experts >= 1 && x_div >= 1, "bad size");
+  if (picks == 0 || N == 0) return GLQ_OK;
+  GLQ_CHECK(K > 0 && K % 64 == 0 && K < (1 << 24),
+            "K=%lld must be a positive multiple of 64 (whole 16-byte code pieces per row)",
+            (long long)K);
+  GLQ_CHECK(picks < (1 << 20) && N < (1ll << 26) && experts < (1 << 20), "sizes too large");
+  GLQ_CHECK(m && sel && y, "null m, sel or y");
+  GLQ_CHECK(rank >= 0 && rank <= 256 && rank % 8 == 0, "rank=%lld must be a multiple of 8 up to 256",
+            (long long)rank);
+  TurboArgs a, u;
+  if (int rc = turbo_mat_args(*m, picks, x_div, K, N, experts, sel, rank, P, y, a)) return rc;
+  if (!up) return turbo_run(a, picks, 1, K, N, (hipStream_t)stream);
+  if (int rc = turbo_mat_args(*up, picks, x_div, K, N, experts, sel, rank, P, y, u)) return rc;
+  GLQ_CHECK((a.sv == nullptr) == (u.sv == nullptr), "gate and up must both have SV or neither");
+  return turbo_run(a, picks, 1, K, N, (hipStream_t)stream, &u);
+}
+
+extern "C" int glq_turbo_moe_down_prep(int64_t picks, int64_t inter_dim, const void* inter,
+                                       const void* Pi, const float* rht_signs, void* xd,
+                                       const void* U, int64_t n_clusters,
+                                       const int32_t* cluster, const int32_t* sel,
+                                       int64_t experts, int64_t rank, float* parts,
+                                       void* stream) {
+  using namespace glq;
+  clear_error();
+  GLQ_CHECK(picks >= 0 && inter_dim > 0 && experts >= 1, "bad size");
+  if (picks == 0) return GLQ_OK;
+  GLQ_CHECK(picks < (1 << 20) && inter_dim < (1 << 16), "sizes too large");
+  GLQ_CHECK(inter && xd && sel && (Pi != nullptr) != (rht_signs != nullptr),
+            "inter, xd, sel and exactly one of Pi and rht_signs required");
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  GLQ_CHECK(al16(inter) && (!Pi || al16(Pi)), "inter and Pi must be 16-byte aligned");
+  GLQ_CHECK(Pi ? inter_dim % 32 == 0 : (inter_dim & (inter_dim - 1)) == 0,
+            "inter_dim must be a multiple of 32 (Pi) or a power of two (transform)");
+  const bool lora = U != nullptr && rank > 0;
+  GLQ_CHECK(!lora || (parts && cluster && n_clusters >= 1 && rank % 8 == 0 && rank <= 1024 &&
+                      al16(U)),
+            "x U needs parts, cluster, n_clusters and a rank that is a multiple of 8");
+  TurboDownPrepArgs g;
+  memset(&g, 0, sizeof(g));
+  g.inter = (const __half*)inter;
+  g.Pi = (const __half*)Pi;
+  g.signs = rht_signs;
+  g.xd = (__half*)xd;
+  g.P = (int)picks;
+  g.I = (int)inter_dim;
+  int logd = 0;
+  while ((1ll << logd) < inter_dim) ++logd;
+  g.logd = logd;
+  g.scale = 1.f / sqrtf((float)inter_dim);
+  g.nrot = Pi ? (int)(((inter_dim + 15) / 16) * ((picks + 15) / 16)) : (int)picks;
+  g.U = lora ? (const __half*)U : nullptr;
+  g.cluster = cluster;
+  g.sel = sel;
+  g.E = (int)experts;
+  g.C = (int)n_clusters;
+  g.S = (int)((inter_dim + kLowrankRows - 1) / kLowrankRows);
+  g.rank = lora ? (int)rank : 0;
+  g.rpad = (int)align_up(g.rank, 32);
+  g.parts = parts;
+  const int64_t grid = g.nrot + (lora ? picks * g.S : 0);
+  GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
+  const size_t lds = std::max<size_t>(kDownPrepLds, rht_signs ? 4 * (size_t)inter_dim : 0);
+  static size_t attr = 64 * 1024;
+  int rc = set_lds_limit(turbo_down_prep_kernel, lds, attr);
+  if (rc) return rc;
+  turbo_down_prep_kernel<<<dim3((unsigned)grid), dim3(256), lds, (hipStream_t)stream>>>(g);
+  GLQ_LAUNCH_CHECK("turbo_down_prep_kernel");
+  return GLQ_OK;
 }
 
 extern "C" int glq_rht(const void* x, int x_fp32, int64_t rows, int64_t d, const float* signs,

@@ -37,6 +37,7 @@ Differences:
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 import torch.nn as nn
@@ -420,11 +421,16 @@ def _turbo_from_problem(p: MoEProblem, d) -> dict:
 
 def _turbo_derived(t: dict) -> None:
     """Tensors the turbo step reads that follow from the block's own: Pi^T per
-    QR-rotated projection (x Pi^T as one fp16 GEMM with fp32 accumulation), and
-    the gate and up U stacked (one x U launch for both)."""
+    QR-rotated projection (x Pi^T as one fp16 GEMM with fp32 accumulation),
+    down's Pi as fp16 rows, and the gate and up U stacked (one x U launch for
+    both)."""
     for proj in PROJS:
         Pi = t[f"Pi_{proj}"]
         t[f"PiT_{proj}"] = None if Pi is None else Pi.t().contiguous()
+    # Pi of down as fp16 rows (output n's weights contiguous), for
+    # glq_turbo_moe_down_prep
+    Pd = t["Pi_down"]
+    t["Pi_down_c"] = None if Pd is None else Pd.to(torch.float16).contiguous()
     if t["rank"] > 0:
         t["U_gu"] = torch.cat([t["U_gate"], t["U_up"]]).contiguous()
 
@@ -491,9 +497,122 @@ def _turbo_shared_expert(t: dict, h: torch.Tensor, lib) -> torch.Tensor:
                                         q["down"][3], 128)
 
 
+def _turbo_fused_ok(blk: GraphCompatibleMoeBlock, B: int) -> bool:
+    """The four-launch form of the turbo step (turbo_step_fused) takes this
+    block: gate and up rotated alike (by one transform, or by one Pi), the
+    down by a transform or a Pi of a 32-multiple width, a rank that is a
+    multiple of 8 (or none), at most 16 tokens."""
+    t = blk.t
+    if os.environ.get("GLQ_TURBO_SEQ") or B > 16 or not t["same_rot_gu"]:
+        return False
+    if blk.rank and blk.rank % 8:
+        return False
+    if t["signs_down"] is None and (t["Pi_down"] is None or blk.inter % 32):
+        return False
+    return True
+
+
+def _route_workspace(dev, stream, B, E, lib) -> torch.Tensor:
+    n = lib.glq_moe_route_workspace_bytes(B, E)
+    key = (dev.index, stream)
+    ws = _route_ws.get(key)
+    if ws is None or ws.numel() < n:
+        retire_workspace(ws)  # a captured graph may still use it
+        ws = torch.zeros(max(int(n), 256), dtype=torch.uint8, device=dev)  # counters start at zero
+        _route_ws[key] = ws
+    return ws
+
+
+def _turbo_mat(x_rot, t, proj, parts, cluster, blocks) -> _lib.TurboMat:
+    m = _lib.TurboMat()
+    m.x_rot, m.codes = x_rot.data_ptr(), t[f"words_{proj}"].data_ptr()
+    m.norms, m.centroids = t[f"norms_{proj}"].data_ptr(), t[f"cent_{proj}"].data_ptr()
+    m.SV = _lib.ptr(t.get(f"SV_{proj}"))
+    m.parts, m.cluster, m.blocks = parts, _lib.ptr(cluster), blocks
+    return m
+
+
+def turbo_step_fused(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.Tensor | None):
+    """turbo_step in four launches on the main stream (and the shared expert
+    beside them): glq_turbo_moe_prep (routing, gate/up's transform of h and
+    every gate/up cluster's x U partials), glq_turbo_moe_gemv2 as the
+    gate/up pair (SwiGLU inter), glq_turbo_moe_down_prep (the down's input
+    rotation and each pick's x U partials), glq_turbo_moe_gemv2 for down;
+    then the combine.  The same arithmetic as turbo_step's launches except
+    for the order of the Pi rotation's fp32 sums."""
+    lib = _lib.load()
+    t = blk.t
+    dev = h.device
+    B, H = h.shape
+    E, k, I, r = blk.num_experts, blk.top_k, blk.inter, blk.rank
+    P = B * k
+    stream = _lib.stream_handle(dev)
+    shared = side = None
+    if blk.shared_inter > 0:
+        cur = torch.cuda.current_stream(dev)
+        side = _side_stream(dev)
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            shared = _turbo_shared_expert(t, h, lib)
+    sel = torch.empty(P, dtype=torch.int32, device=dev)
+    wts = torch.empty(P, dtype=torch.float16, device=dev)
+    sg = torch.empty(B, dtype=torch.float16, device=dev)
+    logits = torch.empty(B, E, dtype=torch.float16, device=dev)
+    ws = _route_workspace(dev, stream, B, E, lib)
+    signs = t["signs_gate"]
+    xg = torch.empty(B, H, dtype=torch.float16, device=dev) if signs is not None \
+        else _rotate(h, None, t["PiT_gate"])
+    rpad = (r + 31) // 32 * 32
+    S_h = (H + 255) // 256
+    parts = None
+    n_u = 0
+    if r:
+        n_u = t["U_gu"].shape[0]
+        parts = torch.empty(n_u, S_h, B, rpad, dtype=torch.float32, device=dev)
+    _lib.check(lib.glq_turbo_moe_prep(
+        h.data_ptr(), t["router_w"].data_ptr(), _lib.ptr(t["shared_gate_w"]), B, H, E, k,
+        int(blk.norm_topk_prob), sel.data_ptr(), wts.data_ptr(), sg.data_ptr(), logits.data_ptr(),
+        ws.data_ptr(), ws.numel(), _lib.ptr(signs), xg.data_ptr(),
+        _lib.ptr(t["U_gu"] if r else None), n_u, r, _lib.ptr(parts), stream),
+        "glq_turbo_moe_prep")
+    cg = t["U_gate"].shape[0] if r else 0
+    pp = parts.data_ptr() if r else None
+    gm = _turbo_mat(xg, t, "gate", pp, t.get("cluster_gate"), max(cg, 1))
+    um = _turbo_mat(xg, t, "up", pp + cg * S_h * B * rpad * 4 if r else None,
+                    t.get("cluster_up"), max(n_u - cg, 1))
+    inter = torch.empty(P, I, dtype=torch.float16, device=dev)
+    _lib.check(lib.glq_turbo_moe_gemv2(P, k, H, I, E, sel.data_ptr(), ctypes.byref(gm),
+                                       ctypes.byref(um), r, S_h, inter.data_ptr(), stream),
+               "glq_turbo_moe_gemv2")
+    xd = torch.empty(P, I, dtype=torch.float16, device=dev)
+    S_i = (I + 255) // 256
+    parts_d = torch.empty(P, S_i, 1, rpad, dtype=torch.float32, device=dev) if r else None
+    Ud = t.get("U_down") if r else None
+    _lib.check(lib.glq_turbo_moe_down_prep(
+        P, I, inter.data_ptr(), _lib.ptr(t.get("Pi_down_c") if t["signs_down"] is None else None),
+        _lib.ptr(t["signs_down"]), xd.data_ptr(), _lib.ptr(Ud), Ud.shape[0] if r else 0,
+        _lib.ptr(t.get("cluster_down") if r else None), sel.data_ptr(), E, r,
+        _lib.ptr(parts_d), stream), "glq_turbo_moe_down_prep")
+    dm = _turbo_mat(xd, t, "down", _lib.ptr(parts_d), None, P)
+    yd = torch.empty(P, H, dtype=torch.float16, device=dev)
+    _lib.check(lib.glq_turbo_moe_gemv2(P, 1, I, H, E, sel.data_ptr(), ctypes.byref(dm), None, r,
+                                       S_i, yd.data_ptr(), stream), "glq_turbo_moe_gemv2")
+    if side is not None:
+        cur.wait_stream(side)
+        shared.record_stream(cur)
+    out = torch.empty(B, H, dtype=torch.float16, device=dev)
+    _lib.check(lib.glq_moe_combine(yd.data_ptr(), wts.data_ptr(), _lib.ptr(shared), sg.data_ptr(),
+                                   _lib.ptr(res), B, H, k, out.data_ptr(), stream),
+               "glq_moe_combine")
+    return out, logits
+
+
 def turbo_step(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.Tensor | None):
     """One decode step of a TurboQuant block (<= TURBO_MAX_TOKENS tokens):
-    (out (B, H) fp16, router logits (B, E) fp16)."""
+    (out (B, H) fp16, router logits (B, E) fp16).  turbo_step_fused when it
+    takes the block, else this launch sequence."""
+    if _turbo_fused_ok(blk, h.shape[0]):
+        return turbo_step_fused(blk, h, res)
     from .kernels import _lowrank_xu_eager, workspace
     lib = _lib.load()
     t = blk.t
@@ -517,13 +636,7 @@ def turbo_step(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.Tensor 
     wts = torch.empty(P, dtype=torch.float16, device=dev)
     sg = torch.empty(B, dtype=torch.float16, device=dev)
     logits = torch.empty(B, E, dtype=torch.float16, device=dev)
-    n = lib.glq_moe_route_workspace_bytes(B, E)
-    key = (dev.index, stream)
-    ws = _route_ws.get(key)
-    if ws is None or ws.numel() < n:
-        retire_workspace(ws)  # a captured graph may still use it
-        ws = torch.zeros(max(int(n), 256), dtype=torch.uint8, device=dev)  # counters start at zero
-        _route_ws[key] = ws
+    ws = _route_workspace(dev, stream, B, E, lib)
     _lib.check(lib.glq_moe_route(h.data_ptr(), t["router_w"].data_ptr(),
                                  _lib.ptr(t["shared_gate_w"]), B, H, E, k,
                                  int(blk.norm_topk_prob), sel.data_ptr(), wts.data_ptr(),

@@ -421,6 +421,69 @@ int glq_moe_route(const void* h, const void* router_w, const void* shared_gate_w
                   void* logits, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * The first launch of a TurboQuant block's decode step (the composition in
+ * glorcq_amd/moe_block.py): glq_moe_route's routing (same arguments,
+ * outputs and workspace contract), and in the same launch, from the same h:
+ * with rht_signs, x_rot = fp16((1/sqrt(hidden)) H diag(rht_signs) h) for
+ * gate and up (rht_forward(h.float(), signs).half(),
+ * inference/moe_block.py:351; hidden a power of two); with n_u > 0, the
+ * fp32 partials of h U_u over 256-row slices for the n_u matrices U
+ * (n_u, hidden, rank) -- every gate and up cluster's x U,
+ * _precompute_xU_for_experts (moe_block.py:290-322) -- into parts
+ * (n_u, S, tokens, rpad), S = ceil(hidden / 256), rpad = rank rounded up
+ * to 32, which glq_turbo_moe_gemv2 sums in slice order.  tokens <= 16.
+ */
+int glq_turbo_moe_prep(const void* h, const void* router_w, const void* shared_gate_w,
+                       int64_t tokens, int64_t hidden, int64_t experts, int64_t top_k,
+                       int norm_topk_prob, int32_t* sel, void* weights, void* shared_gate,
+                       void* logits, void* workspace, int64_t workspace_bytes,
+                       const float* rht_signs, void* x_rot, const void* U, int64_t n_u,
+                       int64_t rank, float* parts, void* stream);
+
+/* One projection of the TurboQuant experts for glq_turbo_moe_gemv2. */
+typedef struct glq_turbo_mat {
+  const void* x_rot;      /* the rotated input: row p / x_div for pick p, K fp16 each */
+  const int32_t* codes;   /* (experts, N, K/16) */
+  const float* norms;     /* (experts, N) */
+  const float* centroids; /* (4,) */
+  const void* SV;         /* (experts, N, rank) fp16, or NULL: no low-rank term */
+  const float* parts;     /* a as fp32 partials (blocks, P, rows, rpad) */
+  const int32_t* cluster; /* expert -> block, row = p / x_div (rows = tokens); NULL:
+                             block = pick p, rows = 1 */
+  int64_t blocks;
+} glq_turbo_mat;
+
+/*
+ * glq_turbo_moe_gemv with a given as partials (what glq_turbo_moe_prep
+ * writes for gate and up, glq_turbo_moe_down_prep for down): pick p's a =
+ * fp16(sum over s in order of parts[b][s][row]), b = cluster[sel[p]] (or
+ * p), then y = fp16(norm * C[q] . x_rot + a SV^T).  With up != NULL the
+ * launch walks both matrices (the same shape; gate = m) and stores the
+ * SwiGLU inter fp16(fp16(silu(fp16(gate))) * fp16(up)) -- the bits of the
+ * gate launch followed by the up launch's SwiGLU store, in one launch
+ * (the reference's act_fn(gate) * up, moe_block.py:465-468).  y (picks, N).
+ */
+int glq_turbo_moe_gemv2(int64_t picks, int64_t x_div, int64_t K, int64_t N, int64_t experts,
+                        const int32_t* sel, const glq_turbo_mat* m, const glq_turbo_mat* up,
+                        int64_t rank, int64_t P, void* y, void* stream);
+
+/*
+ * The down projection's inputs of a TurboQuant block's decode step, in one
+ * launch, for every pick p (inter (picks, inter_dim) fp16, the SwiGLU of
+ * glq_turbo_moe_gemv2): xd[p] = fp16(inter[p] Pi^T) with Pi (inter_dim,
+ * inter_dim) fp16 row-major (the QR rotation, moe_block.py:352-356;
+ * inter_dim a multiple of 32), or with rht_signs instead the transform
+ * fp16((1/sqrt(d)) H diag(signs) inter[p]) (d a power of two); and with U
+ * (n_clusters, inter_dim, rank) the fp32 partials of inter[p]
+ * U[cluster[sel[p]]] over 256-row slices into parts (picks, S, 1, rpad),
+ * the down GEMV's a (glq_turbo_moe_gemv2 with cluster = NULL).
+ */
+int glq_turbo_moe_down_prep(int64_t picks, int64_t inter_dim, const void* inter, const void* Pi,
+                            const float* rht_signs, void* xd, const void* U, int64_t n_clusters,
+                            const int32_t* cluster, const int32_t* sel, int64_t experts,
+                            int64_t rank, float* parts, void* stream);
+
+/*
  * Turbo GEMV of every pick (turbo_dequant_matmul_fused per expert,
  * inference/kernels/__init__.py:184-239, as _batched_proj_forward and
  * _batched_down_forward call it, moe_block.py:480-702): pick p multiplies x

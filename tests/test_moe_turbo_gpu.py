@@ -219,3 +219,35 @@ def test_turbo_block_from_checkpoint(gpu, tmp_path):
     out, logits = run(mine, p, gpu)
     check_routing(p, logits)
     assert bar(out, O.moe_forward(p))
+
+
+@pytest.mark.parametrize("B,seed,inter,rot_gu,rot_down", [(1, 11, 1408, "rht", "qr"),
+                                                          (4, 12, 1408, "rht", "qr"),
+                                                          (3, 13, 1024, "rht", "rht"),
+                                                          (2, 15, 1408, "qr", "qr"),
+                                                          (16, 14, 1408, "rht", "qr")])
+def test_turbo_fused_step_matches_launch_sequence(gpu, B, seed, inter, rot_gu, rot_down,
+                                                  monkeypatch):
+    """The four-launch turbo step (glq_turbo_moe_prep, the gate/up pair,
+    glq_turbo_moe_down_prep, down) against the launch-by-launch step
+    (GLQ_TURBO_SEQ=1): the same routing; with the down rotated by the
+    transform the same bits end to end (with a Pi only the rotation's fp32
+    sums run in another order); both within the oracle's bar."""
+    p = fmt.make_turbo_moe(H=2048, E=16, inter=inter, top_k=4, n_clusters=4, rank=64,
+                           shared_inter=0, B=B, seed=seed, rot_gate_up=rot_gu,
+                           rot_down=rot_down)
+    p = lora_heavy(p, 10.0)
+    blk = GraphCompatibleMoeBlock.from_problem(p, gpu)
+    h = p.h.reshape(1, p.B, p.H).to(gpu)
+    print(f"turbo fused B={B} inter={inter} {rot_gu}/{rot_down}", flush=True)
+    out_f, lg_f = blk(h)
+    out_f, lg_f = out_f.clone(), lg_f.clone()
+    monkeypatch.setenv("GLQ_TURBO_SEQ", "1")
+    out_s, lg_s = blk(h)
+    torch.cuda.synchronize()
+    assert torch.equal(lg_f, lg_s)
+    if rot_down == "rht":
+        assert torch.equal(out_f, out_s)
+    ref = O.moe_forward(p)
+    for out in (out_f, out_s):
+        assert bar(out.reshape(p.B, p.H).cpu(), ref)
