@@ -37,6 +37,14 @@ class MoeParams(ctypes.Structure):
     ]
 
 
+class MoeShared(ctypes.Structure):
+    """glq_moe_shared (include/glorcq_hip.h), field for field."""
+    _fields_ = [
+        ("codes", _vp * 3), ("scales", _vp * 3), ("zeros", _vp * 3), ("inter", _i64),
+        ("bits", ctypes.c_int32), ("reserved", ctypes.c_int32), ("sinter", _vp), ("sy", _vp),
+    ]
+
+
 class TurboMat(ctypes.Structure):
     """glq_turbo_mat (include/glorcq_hip.h), field for field."""
     _fields_ = [
@@ -148,12 +156,12 @@ SIGNATURES = {
         _vp, _vp, _vp, _i64, _i64, _i64, _i64,  # h, router_w, shared_gate_w, tokens, hidden, E, k
         _c_int, _vp, _vp, _vp, _vp,             # norm, sel, weights, shared_gate, logits
         _vp, _i64, _vp, _vp,                    # workspace, bytes, rht_signs, x_rot
-        _vp, _i64, _i64, _vp, _vp,              # U, n_u, rank, parts, stream
+        _vp, _i64, _i64, _vp, _vp, _vp,         # U, n_u, rank, parts, shared, stream
     ]),
     "glq_turbo_moe_down_prep": (_c_int, [
         _i64, _i64, _vp, _vp, _vp, _vp,         # picks, inter_dim, inter, Pi, rht_signs, xd
         _vp, _i64, _vp, _vp, _i64, _i64,        # U, n_clusters, cluster, sel, experts, rank
-        _vp, _vp,                               # parts, stream
+        _vp, _i64, _i64, _vp, _vp,              # parts, tokens, hidden, shared, stream
     ]),
     "glq_turbo_moe_gemv2": (_c_int, [
         _i64, _i64, _i64, _i64, _i64, _vp,      # picks, x_div, K, N, experts, sel

@@ -1362,9 +1362,11 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_route_only_kernel(MoeLane
 // (moe_lane_router); then, with signs, B workgroups of one row's transform
 // (rht_kernel's arithmetic: fp32 butterflies in LDS, one rounding); then
 // pairs of (U, 256-row slice) jobs, two per workgroup (lowrank_partial over
-// the B token rows) into parts[u][s] (n_u, S, B, rpad).
+// the B token rows) into parts[u][s] (n_u, S, B, rpad); then (SBITS > 0) the
+// shared expert's gate/up rows in pairs (the lane router launch's role,
+// SguSrc: sinter).
 struct TurboPrepArgs {
-  MoeLaneArgs a;
+  MoeLaneArgs a;  // the router's fields; with a shared expert, its gate/up role (gSGU)
   const float* signs;  // (H,) or null: no transform
   __half* xrot;        // (B, H)
   int logd;
@@ -1376,7 +1378,7 @@ struct TurboPrepArgs {
 
 constexpr int kPrepJobLds = (4 * 4 * 64) * 4 + 16 * kLowrankRows * 2 + 64 * kLowrankUtStride * 2;
 
-template <int RC, int MC>
+template <int RC, int MC, int SBITS, int SLRP>
 __global__ __launch_bounds__(kMoeLaneThreads) void turbo_prep_kernel(TurboPrepArgs g) {
   extern __shared__ __align__(16) unsigned char smem[];
   const MoeLaneArgs& a = g.a;
@@ -1394,9 +1396,18 @@ __global__ __launch_bounds__(kMoeLaneThreads) void turbo_prep_kernel(TurboPrepAr
     }
     b -= a.B;
   }
+  const int njobs = g.n_u * g.S, nxw = (njobs + 1) / 2;
+  if (b >= nxw) {
+    if constexpr (SBITS != 0) {
+      const int wvb = moe_lane_wave();
+      lane_run<SguSrc, SBITS, false, SLRP, 1, kMoePairPD, 1, false, false, true>(
+          SguSrc{a}, a.gSGU, (b - nxw) * 8 + wvb, wvb, nullptr);
+    }
+    return;
+  }
   // two (U, slice) jobs: 256-thread groups side by side, each with its LDS
   const int grp = threadIdx.x >> 8, tid = threadIdx.x & 255;
-  const int job = 2 * b + grp, njobs = g.n_u * g.S;
+  const int job = 2 * b + grp;
   const int jc = min(job, njobs - 1);  // a group past the list computes job njobs-1 and writes nothing
   const int u = jc / g.S, sl = jc - u * g.S;
   unsigned char* gl = smem + grp * kPrepJobLds;
@@ -1407,6 +1418,99 @@ __global__ __launch_bounds__(kMoeLaneThreads) void turbo_prep_kernel(TurboPrepAr
   lowrank_partial<MC>(xrow, a.B, a.H, g.rank, g.rpad, g.U + (int64_t)u * a.H * g.rank, sl,
                       job < njobs ? g.parts + ((int64_t)u * g.S + sl) * a.B * g.rpad : nullptr,
                       red, xl, tid, ut);
+}
+
+// ---------------------------------------------------------------------------
+// The down projection's inputs of a TurboQuant block's decode step, for
+// every pick p, in one launch: xd[p] = fp16(inter[p] Pi^T) (the QR rotation:
+// the reference's fp16(x.float() @ Pi.float().T), moe_block.py:352-356) or,
+// with signs, the transform of inter[p] (rht_row_f16); and the fp32 partials
+// of inter[p] U_down[cluster(sel[p])] over 256-row slices (the down GEMV's a:
+// each pick's own x U, moe_block.py:661-676).
+// Rotation workgroup (16-row block of xd, 16-pick block): its 4 waves split
+// K; A = the picks' inter rows, B = Pi's rows (row n weighs output n,
+// contiguous in k), one v_mfma_f32_16x16x32_f16 per 32 k; the waves' tiles
+// summed in LDS in wave order.  Then (SNP > 0) the shared expert's down rows
+// over its sinter, 4 waves a workgroup (SdySrc: sy).
+// ---------------------------------------------------------------------------
+struct TurboDownPrepArgs {
+  const __half* inter;    // (P, I)
+  const __half* Pi;       // (I, I), or null with signs
+  const float* signs;     // (I,), or null
+  __half* xd;             // (P, I)
+  int P, I, logd;
+  float scale;
+  int nrot;               // workgroups of the rotation, first in the grid
+  const __half* U;        // (C, I, rank), or null: no x U
+  const int32_t* cluster;  // (E,) expert -> U
+  const int32_t* sel;     // (P,) pick -> expert
+  int E, C, S, rank, rpad;
+  float* parts;           // (P, S, 1, rpad)
+  int nxu;                // x U jobs, after the rotation
+  MoeLaneArgs sa;         // the shared down role (scodes[2], sinter, sy, gSD)
+};
+
+constexpr int kDownPrepLds = 4 * 4 * 64 * 4 + 16 * kLowrankRows * 2;
+
+template <int SLRP, int SNP>
+__global__ __launch_bounds__(256) void turbo_down_prep_kernel(TurboDownPrepArgs g) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x;
+  int b = blockIdx.x;
+  if (b < g.nrot) {
+    if (g.signs) {
+      rht_row_f16(g.inter + (int64_t)b * g.I, g.signs, g.xd + (int64_t)b * g.I, g.I, g.logd,
+                  g.scale, (float*)smem, 256);
+      return;
+    }
+    const int nrb = (g.I + 15) / 16, rb = b % nrb, pb = b / nrb;
+    const int wave = tid >> 6, lane = tid & 63, li = lane & 15, kb = lane >> 4;
+    const __half* brow = g.Pi + (int64_t)min(rb * 16 + li, g.I - 1) * g.I;
+    const int pa = pb * 16 + li;  // this lane's A row (pick)
+    const __half* arow = g.inter + (int64_t)min(pa, g.P - 1) * g.I;
+    const int nsteps = g.I / 32, q = (nsteps + 3) / 4;
+    const int s0 = wave * q, s1 = min(nsteps, s0 + q);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int st = s0; st < s1; ++st) {
+      const int k = 32 * st + 8 * kb;
+      const f16x8 av = pa < g.P ? *(const f16x8*)(arow + k) : f16x8{};
+      acc = mfma_16x16x32(av, *(const f16x8*)(brow + k), acc);
+    }
+    // acc[i] of lane (li, kb): pick 4kb + i, output row li of the block
+    float* red = (float*)smem;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
+    __syncthreads();
+    if (wave == 0) {
+      const int n = rb * 16 + li;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = ((red[i * 64 + lane] + red[(4 + i) * 64 + lane]) +
+                         red[(8 + i) * 64 + lane]) + red[(12 + i) * 64 + lane];
+        const int p = pb * 16 + 4 * kb + i;
+        if (p < g.P && n < g.I) g.xd[(int64_t)p * g.I + n] = __float2half(v);
+      }
+    }
+    return;
+  }
+  b -= g.nrot;
+  if (b >= g.nxu) {
+    if constexpr (SNP > 0) {
+      const int wvb = (int)__builtin_amdgcn_readfirstlane(tid >> 6);
+      lane_run<SdySrc, 4, false, SLRP, SNP, moe_lane_pd(SNP), 1, false, false>(
+          SdySrc{g.sa}, g.sa.gSD, (b - g.nxu) * 4 + wvb, wvb, nullptr);
+    }
+    return;
+  }
+  // x U job (pick, slice)
+  const int p = b / g.S, sl = b - p * g.S;
+  const int e = min(max(g.sel[p], 0), g.E - 1);
+  const int c = min(max(g.cluster[e], 0), g.C - 1);
+  float* red = (float*)smem;
+  __half* xl = (__half*)(red + 4 * 4 * 64);
+  auto xrow = [&](int) { return g.inter + (int64_t)p * g.I; };
+  lowrank_partial<1>(xrow, 1, g.I, g.rank, g.rpad, g.U + (int64_t)c * g.I * g.rank, sl,
+                     g.parts + ((int64_t)p * g.S + sl) * g.rpad, red, xl, tid);
 }
 
 // out[t][n] = fp16(sum_k w[t][k] y[t k + k][n] + sg[t] shared[t][n])
@@ -1507,7 +1611,7 @@ extern "C" int glq_turbo_moe_prep(const void* h, const void* router_w, const voi
                                   void* shared_gate, void* logits, void* workspace,
                                   int64_t workspace_bytes, const float* rht_signs, void* x_rot,
                                   const void* U, int64_t n_u, int64_t rank, float* parts,
-                                  void* stream) {
+                                  const glq_moe_shared* shared, void* stream) {
   using namespace glq;
   clear_error();
   if (int rc = moe_route_shape(tokens, hidden, experts, top_k)) return rc;
@@ -1556,26 +1660,145 @@ extern "C" int glq_turbo_moe_prep(const void* h, const void* router_w, const voi
   g.rank = (int)rank;
   g.rpad = (int)align_up(rank, 32);
   g.parts = parts;
+  int64_t nsgu = 0;
+  int slrp = 0;
+  if (shared) {
+    GLQ_CHECK(shared->bits == 4 && shared->inter > 0 && shared->codes[0] && shared->codes[1] &&
+                  shared->scales[0] && shared->scales[1] && shared->zeros[0] &&
+                  shared->zeros[1] && shared->sinter && hidden % 128 == 0,
+              "the shared gate/up take 4-bit codes with zero-points and hidden a multiple of "
+              "128");
+    for (int m = 0; m < 2; ++m) {
+      a.scodes[m] = (const uint32_t*)shared->codes[m];
+      a.sscales[m] = (const __half*)shared->scales[m];
+      a.szeros[m] = (const __half*)shared->zeros[m];
+    }
+    a.SI = (int)shared->inter;
+    a.sinter = (__half*)shared->sinter;
+    a.gSGU = role_geom((int)shared->inter, (int)hidden, 4, 0, (int)tokens, true);
+    slrp = lane_lrp(a.gSGU.lr);
+    GLQ_CHECK(slrp >= 32 && a.gSGU.lr <= 64, "the shared gate/up take 33..256-row pieces");
+    nsgu = role_blocks(a.gSGU);
+  }
   const size_t lds_route = (size_t)(((2 * (experts + 1) + 15) & ~15) + 4 * experts + 4 * 16);
   const size_t lds = std::max({lds_route, rht_signs ? (size_t)4 * hidden : (size_t)0,
                                n_u > 0 ? (size_t)2 * kPrepJobLds : (size_t)0});
-  const int64_t grid = tokens * a.nrw + (rht_signs ? tokens : 0) + (n_u * g.S + 1) / 2;
+  const int64_t grid = tokens * a.nrw + (rht_signs ? tokens : 0) + (n_u * g.S + 1) / 2 + nsgu;
   hipStream_t s = (hipStream_t)stream;
   const dim3 gd((unsigned)grid), block(kMoeLaneThreads);
-#define GLQ_PREP_LAUNCH(RC_, MC_)                                           \
+#define GLQ_PREP_LAUNCH(RC_, MC_, SB_, SL_)                                 \
   do {                                                                      \
     static size_t attr = 64 * 1024;                                         \
-    int rc2 = set_lds_limit(turbo_prep_kernel<RC_, MC_>, lds, attr);        \
+    int rc2 = set_lds_limit(turbo_prep_kernel<RC_, MC_, SB_, SL_>, lds, attr); \
     if (rc2) return rc2;                                                    \
-    turbo_prep_kernel<RC_, MC_><<<gd, block, lds, s>>>(g);                  \
+    turbo_prep_kernel<RC_, MC_, SB_, SL_><<<gd, block, lds, s>>>(g);        \
+  } while (0)
+#define GLQ_PREP_SHARED(RC_, MC_)                                           \
+  do {                                                                      \
+    if (slrp == 0) GLQ_PREP_LAUNCH(RC_, MC_, 0, 64);                        \
+    else if (slrp == 32) GLQ_PREP_LAUNCH(RC_, MC_, 4, 32);                  \
+    else GLQ_PREP_LAUNCH(RC_, MC_, 4, 64);                                  \
   } while (0)
   const bool mc4 = tokens >= 3;
-  if (rc == 1) { if (mc4) GLQ_PREP_LAUNCH(1, 4); else GLQ_PREP_LAUNCH(1, 1); }
-  else if (rc == 2) { if (mc4) GLQ_PREP_LAUNCH(2, 4); else GLQ_PREP_LAUNCH(2, 1); }
-  else if (rc == 4) { if (mc4) GLQ_PREP_LAUNCH(4, 4); else GLQ_PREP_LAUNCH(4, 1); }
-  else { if (mc4) GLQ_PREP_LAUNCH(8, 4); else GLQ_PREP_LAUNCH(8, 1); }
+  if (rc == 1) { if (mc4) GLQ_PREP_SHARED(1, 4); else GLQ_PREP_SHARED(1, 1); }
+  else if (rc == 2) { if (mc4) GLQ_PREP_SHARED(2, 4); else GLQ_PREP_SHARED(2, 1); }
+  else if (rc == 4) { if (mc4) GLQ_PREP_SHARED(4, 4); else GLQ_PREP_SHARED(4, 1); }
+  else { if (mc4) GLQ_PREP_SHARED(8, 4); else GLQ_PREP_SHARED(8, 1); }
+#undef GLQ_PREP_SHARED
 #undef GLQ_PREP_LAUNCH
   GLQ_LAUNCH_CHECK("turbo_prep_kernel");
+  return GLQ_OK;
+}
+
+extern "C" int glq_turbo_moe_down_prep(int64_t picks, int64_t inter_dim, const void* inter,
+                                       const void* Pi, const float* rht_signs, void* xd,
+                                       const void* U, int64_t n_clusters,
+                                       const int32_t* cluster, const int32_t* sel,
+                                       int64_t experts, int64_t rank, float* parts,
+                                       int64_t tokens, int64_t hidden,
+                                       const glq_moe_shared* shared, void* stream) {
+  using namespace glq;
+  clear_error();
+  GLQ_CHECK(picks >= 0 && inter_dim > 0 && experts >= 1, "bad size");
+  if (picks == 0) return GLQ_OK;
+  GLQ_CHECK(picks < (1 << 20) && inter_dim < (1 << 16), "sizes too large");
+  GLQ_CHECK(inter && xd && sel && (Pi != nullptr) != (rht_signs != nullptr),
+            "inter, xd, sel and exactly one of Pi and rht_signs required");
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  GLQ_CHECK(al16(inter) && (!Pi || al16(Pi)), "inter and Pi must be 16-byte aligned");
+  GLQ_CHECK(Pi ? inter_dim % 32 == 0 : (inter_dim & (inter_dim - 1)) == 0,
+            "inter_dim must be a multiple of 32 (Pi) or a power of two (transform)");
+  const bool lora = U != nullptr && rank > 0;
+  GLQ_CHECK(!lora || (parts && cluster && n_clusters >= 1 && rank % 8 == 0 && rank <= 1024 &&
+                      al16(U)),
+            "x U needs parts, cluster, n_clusters and a rank that is a multiple of 8");
+  TurboDownPrepArgs g;
+  memset(&g, 0, sizeof(g));
+  g.inter = (const __half*)inter;
+  g.Pi = (const __half*)Pi;
+  g.signs = rht_signs;
+  g.xd = (__half*)xd;
+  g.P = (int)picks;
+  g.I = (int)inter_dim;
+  int logd = 0;
+  while ((1ll << logd) < inter_dim) ++logd;
+  g.logd = logd;
+  g.scale = 1.f / sqrtf((float)inter_dim);
+  g.nrot = Pi ? (int)(((inter_dim + 15) / 16) * ((picks + 15) / 16)) : (int)picks;
+  g.U = lora ? (const __half*)U : nullptr;
+  g.cluster = cluster;
+  g.sel = sel;
+  g.E = (int)experts;
+  g.C = (int)n_clusters;
+  g.S = (int)((inter_dim + kLowrankRows - 1) / kLowrankRows);
+  g.rank = lora ? (int)rank : 0;
+  g.rpad = (int)align_up(g.rank, 32);
+  g.parts = parts;
+  g.nxu = lora ? (int)(picks * g.S) : 0;
+  int snp = 0, slrp = 64;
+  int64_t nsd = 0;
+  if (shared) {
+    GLQ_CHECK(shared->bits == 4 && shared->inter > 0 && shared->inter % 128 == 0 &&
+                  hidden > 0 && tokens >= 1 && tokens <= 16 && shared->codes[2] &&
+                  shared->scales[2] && shared->zeros[2] && shared->sinter && shared->sy,
+              "the shared down takes 4-bit codes, inter a multiple of 128, 1..16 tokens");
+    MoeLaneArgs& sa = g.sa;
+    sa.B = (int)tokens;
+    sa.H = (int)hidden;
+    sa.SI = (int)shared->inter;
+    sa.scodes[2] = (const uint32_t*)shared->codes[2];
+    sa.sscales[2] = (const __half*)shared->scales[2];
+    sa.szeros[2] = (const __half*)shared->zeros[2];
+    sa.sinter = (__half*)shared->sinter;
+    sa.sy = (__half*)shared->sy;
+    sa.gSD = role_geom((int)hidden, (int)shared->inter, 4, 0, (int)tokens, false);
+    const int lr = sa.gSD.lr;
+    slrp = lane_lrp(lr);
+    snp = (lr + 63) / 64;
+    GLQ_CHECK(snp <= 4 && (snp == 1 || slrp == 64), "shared inter too wide for the lane form");
+    nsd = ((int64_t)sa.gSD.items * sa.gSD.wpi + 3) / 4;
+  }
+  const int64_t grid = g.nrot + g.nxu + nsd;
+  GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
+  const size_t lds = std::max<size_t>(kDownPrepLds, rht_signs ? 4 * (size_t)inter_dim : 0);
+  hipStream_t s = (hipStream_t)stream;
+  int rc = GLQ_OK;
+#define GLQ_DPREP(L, N)                                                                     \
+  do {                                                                                      \
+    static size_t attr = 64 * 1024;                                                         \
+    rc = set_lds_limit(turbo_down_prep_kernel<L, N>, lds, attr);                            \
+    if (rc) return rc;                                                                      \
+    turbo_down_prep_kernel<L, N><<<dim3((unsigned)grid), dim3(256), lds, s>>>(g);          \
+  } while (0)
+  if (snp == 0) GLQ_DPREP(64, 0);
+  else if (slrp == 16) GLQ_DPREP(16, 1);
+  else if (slrp == 32) GLQ_DPREP(32, 1);
+  else if (snp == 1) GLQ_DPREP(64, 1);
+  else if (snp == 2) GLQ_DPREP(64, 2);
+  else if (snp == 3) GLQ_DPREP(64, 3);
+  else GLQ_DPREP(64, 4);
+#undef GLQ_DPREP
+  GLQ_LAUNCH_CHECK("turbo_down_prep_kernel");
   return GLQ_OK;
 }
 

@@ -26,7 +26,6 @@
 // accuracy like the reference's fp32 FMA loop; y = fp16(acc * norm) as in the
 // reference.
 #include <algorithm>
-#include <cstring>
 
 #include "glq_gemv_core.h"
 
@@ -415,86 +414,6 @@ __global__ __launch_bounds__(256) void turbo_gemv_kernel(TurboArgs a, TurboArgs 
 }
 
 // ---------------------------------------------------------------------------
-// The down projection's inputs of a TurboQuant block's decode step, for
-// every pick p, in one launch: xd[p] = fp16(inter[p] Pi^T) (the QR rotation:
-// the reference's fp16(x.float() @ Pi.float().T), moe_block.py:352-356) or,
-// with signs, the transform of inter[p] (rht_row_f16); and the fp32 partials
-// of inter[p] U_down[cluster(sel[p])] over 256-row slices (the down GEMV's a:
-// each pick's own x U, moe_block.py:661-676).
-// Rotation workgroup (16-row block of xd, 16-pick block): its 4 waves split
-// K; A = the picks' inter rows, B = Pi's rows (row n weighs output n,
-// contiguous in k), one v_mfma_f32_16x16x32_f16 per 32 k; the waves' tiles
-// summed in LDS in wave order.
-// ---------------------------------------------------------------------------
-struct TurboDownPrepArgs {
-  const __half* inter;    // (P, I)
-  const __half* Pi;       // (I, I), or null with signs
-  const float* signs;     // (I,), or null
-  __half* xd;             // (P, I)
-  int P, I, logd;
-  float scale;
-  int nrot;               // workgroups of the rotation, first in the grid
-  const __half* U;        // (C, I, rank), or null: no x U
-  const int32_t* cluster;  // (E,) expert -> U
-  const int32_t* sel;     // (P,) pick -> expert
-  int E, C, S, rank, rpad;
-  float* parts;           // (P, S, 1, rpad)
-};
-
-constexpr int kDownPrepLds = 4 * 4 * 64 * 4 + 16 * kLowrankRows * 2;
-
-__global__ __launch_bounds__(256) void turbo_down_prep_kernel(TurboDownPrepArgs g) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int tid = threadIdx.x;
-  int b = blockIdx.x;
-  if (b < g.nrot) {
-    if (g.signs) {
-      rht_row_f16(g.inter + (int64_t)b * g.I, g.signs, g.xd + (int64_t)b * g.I, g.I, g.logd,
-                  g.scale, (float*)smem, 256);
-      return;
-    }
-    const int nrb = (g.I + 15) / 16, rb = b % nrb, pb = b / nrb;
-    const int wave = tid >> 6, lane = tid & 63, li = lane & 15, kb = lane >> 4;
-    const __half* brow = g.Pi + (int64_t)min(rb * 16 + li, g.I - 1) * g.I;
-    const int pa = pb * 16 + li;  // this lane's A row (pick)
-    const __half* arow = g.inter + (int64_t)min(pa, g.P - 1) * g.I;
-    const int nsteps = g.I / 32, q = (nsteps + 3) / 4;
-    const int s0 = wave * q, s1 = min(nsteps, s0 + q);
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int st = s0; st < s1; ++st) {
-      const int k = 32 * st + 8 * kb;
-      const f16x8 av = pa < g.P ? *(const f16x8*)(arow + k) : f16x8{};
-      acc = mfma_16x16x32(av, *(const f16x8*)(brow + k), acc);
-    }
-    // acc[i] of lane (li, kb): pick 4kb + i, output row li of the block
-    float* red = (float*)smem;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
-    __syncthreads();
-    if (wave == 0) {
-      const int n = rb * 16 + li;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float v = ((red[i * 64 + lane] + red[(4 + i) * 64 + lane]) +
-                         red[(8 + i) * 64 + lane]) + red[(12 + i) * 64 + lane];
-        const int p = pb * 16 + 4 * kb + i;
-        if (p < g.P && n < g.I) g.xd[(int64_t)p * g.I + n] = __float2half(v);
-      }
-    }
-    return;
-  }
-  b -= g.nrot;  // x U job (pick, slice)
-  const int p = b / g.S, sl = b - p * g.S;
-  const int e = min(max(g.sel[p], 0), g.E - 1);
-  const int c = min(max(g.cluster[e], 0), g.C - 1);
-  float* red = (float*)smem;
-  __half* xl = (__half*)(red + 4 * 4 * 64);
-  auto xrow = [&](int) { return g.inter + (int64_t)p * g.I; };
-  lowrank_partial<1>(xrow, 1, g.I, g.rank, g.rpad, g.U + (int64_t)c * g.I * g.rank, sl,
-                     g.parts + ((int64_t)p * g.S + sl) * g.rpad, red, xl, tid);
-}
-
-// ---------------------------------------------------------------------------
 // Randomized Hadamard transform of rows of length d (a power of two):
 //   forward: y = (1/sqrt(d)) H diag(signs) x
 //   inverse: y = diag(signs) (1/sqrt(d)) H x
@@ -793,60 +712,6 @@ extern "C" int glq_turbo_moe_gemv2(int64_t picks, int64_t x_div, int64_t K, int6
   if (int rc = turbo_mat_args(*up, picks, x_div, K, N, experts, sel, rank, P, y, u)) return rc;
   GLQ_CHECK((a.sv == nullptr) == (u.sv == nullptr), "gate and up must both have SV or neither");
   return turbo_run(a, picks, 1, K, N, (hipStream_t)stream, &u);
-}
-
-extern "C" int glq_turbo_moe_down_prep(int64_t picks, int64_t inter_dim, const void* inter,
-                                       const void* Pi, const float* rht_signs, void* xd,
-                                       const void* U, int64_t n_clusters,
-                                       const int32_t* cluster, const int32_t* sel,
-                                       int64_t experts, int64_t rank, float* parts,
-                                       void* stream) {
-  using namespace glq;
-  clear_error();
-  GLQ_CHECK(picks >= 0 && inter_dim > 0 && experts >= 1, "bad size");
-  if (picks == 0) return GLQ_OK;
-  GLQ_CHECK(picks < (1 << 20) && inter_dim < (1 << 16), "sizes too large");
-  GLQ_CHECK(inter && xd && sel && (Pi != nullptr) != (rht_signs != nullptr),
-            "inter, xd, sel and exactly one of Pi and rht_signs required");
-  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-  GLQ_CHECK(al16(inter) && (!Pi || al16(Pi)), "inter and Pi must be 16-byte aligned");
-  GLQ_CHECK(Pi ? inter_dim % 32 == 0 : (inter_dim & (inter_dim - 1)) == 0,
-            "inter_dim must be a multiple of 32 (Pi) or a power of two (transform)");
-  const bool lora = U != nullptr && rank > 0;
-  GLQ_CHECK(!lora || (parts && cluster && n_clusters >= 1 && rank % 8 == 0 && rank <= 1024 &&
-                      al16(U)),
-            "x U needs parts, cluster, n_clusters and a rank that is a multiple of 8");
-  TurboDownPrepArgs g;
-  memset(&g, 0, sizeof(g));
-  g.inter = (const __half*)inter;
-  g.Pi = (const __half*)Pi;
-  g.signs = rht_signs;
-  g.xd = (__half*)xd;
-  g.P = (int)picks;
-  g.I = (int)inter_dim;
-  int logd = 0;
-  while ((1ll << logd) < inter_dim) ++logd;
-  g.logd = logd;
-  g.scale = 1.f / sqrtf((float)inter_dim);
-  g.nrot = Pi ? (int)(((inter_dim + 15) / 16) * ((picks + 15) / 16)) : (int)picks;
-  g.U = lora ? (const __half*)U : nullptr;
-  g.cluster = cluster;
-  g.sel = sel;
-  g.E = (int)experts;
-  g.C = (int)n_clusters;
-  g.S = (int)((inter_dim + kLowrankRows - 1) / kLowrankRows);
-  g.rank = lora ? (int)rank : 0;
-  g.rpad = (int)align_up(g.rank, 32);
-  g.parts = parts;
-  const int64_t grid = g.nrot + (lora ? picks * g.S : 0);
-  GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
-  const size_t lds = std::max<size_t>(kDownPrepLds, rht_signs ? 4 * (size_t)inter_dim : 0);
-  static size_t attr = 64 * 1024;
-  int rc = set_lds_limit(turbo_down_prep_kernel, lds, attr);
-  if (rc) return rc;
-  turbo_down_prep_kernel<<<dim3((unsigned)grid), dim3(256), lds, (hipStream_t)stream>>>(g);
-  GLQ_LAUNCH_CHECK("turbo_down_prep_kernel");
-  return GLQ_OK;
 }
 
 extern "C" int glq_rht(const void* x, int x_fp32, int64_t rows, int64_t d, const float* signs,

@@ -314,6 +314,10 @@ class GraphCompatibleMoeBlock(nn.Module):
 # TurboQuant routed experts
 # ---------------------------------------------------------------------------
 TURBO_MAX_TOKENS = 16  # tokens per turbo step (the cluster-shared x U takes <= 16 rows)
+# Tokens up to which the fused turbo step runs the shared expert inside its
+# launches (measured, config 2 with turbo experts: B = 1 59.3 -> 42.7 us,
+# B = 4 77.6 -> 69.5 us, B = 16 128.3 -> 147.4 us)
+TURBO_SHARED_LANE_MAX_B = 4
 
 
 def _turbo_rotation(lins, proj):
@@ -532,14 +536,37 @@ def _turbo_mat(x_rot, t, proj, parts, cluster, blocks) -> _lib.TurboMat:
     return m
 
 
+def _turbo_shared_weights(t: dict):
+    """(codes, scales, zeros) of the shared expert's gate, up, down when they
+    can ride in the fused step's launches (4-bit unsigned codes with
+    zero-points, group 128, no low-rank term or bias), else None."""
+    if "shared_q" in t:
+        q = t["shared_q"]
+        if any(q[p][3] != 4 for p in PROJS):
+            return None
+        return [tuple(q[p][i] for p in PROJS) for i in range(3)]
+    if "shared_mods" in t:
+        ms = t["shared_mods"]
+        for m in ms:
+            if (getattr(m, "quant_type", None) != "gptq" or m.pack_bits != 4 or m.gptq_sym
+                    or m.gptq_groupsize != 128 or m.SV is not None or m.bias_param is not None
+                    or m.zeros is None):
+                return None
+        return [tuple(m.codes for m in ms), tuple(m.scales for m in ms),
+                tuple(m.zeros for m in ms)]
+    return None
+
+
 def turbo_step_fused(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.Tensor | None):
-    """turbo_step in four launches on the main stream (and the shared expert
-    beside them): glq_turbo_moe_prep (routing, gate/up's transform of h and
-    every gate/up cluster's x U partials), glq_turbo_moe_gemv2 as the
-    gate/up pair (SwiGLU inter), glq_turbo_moe_down_prep (the down's input
-    rotation and each pick's x U partials), glq_turbo_moe_gemv2 for down;
-    then the combine.  The same arithmetic as turbo_step's launches except
-    for the order of the Pi rotation's fp32 sums."""
+    """turbo_step in four launches: glq_turbo_moe_prep (routing, gate/up's
+    transform of h, every gate/up cluster's x U partials, the shared expert's
+    gate/up rows), glq_turbo_moe_gemv2 as the gate/up pair (SwiGLU inter),
+    glq_turbo_moe_down_prep (the down's input rotation, each pick's x U
+    partials, the shared expert's down rows), glq_turbo_moe_gemv2 for down;
+    then the combine.  The same arithmetic as turbo_step's launches except for
+    the order of the Pi rotation's fp32 sums and the shared down's sums (the
+    lane form's instead of the streaming kernel's).  A shared expert that
+    cannot ride in the launches runs on a side stream as in turbo_step."""
     lib = _lib.load()
     t = blk.t
     dev = h.device
@@ -547,13 +574,28 @@ def turbo_step_fused(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.T
     E, k, I, r = blk.num_experts, blk.top_k, blk.inter, blk.rank
     P = B * k
     stream = _lib.stream_handle(dev)
-    shared = side = None
-    if blk.shared_inter > 0:
+    shared = side = sh = None
+    # the shared expert in the launches' lane form up to TURBO_SHARED_LANE_MAX_B
+    # tokens (each token decodes its codes again), on the side stream above
+    sw = (_turbo_shared_weights(t) if 0 < blk.shared_inter and B <= TURBO_SHARED_LANE_MAX_B
+          else None)
+    if sw is not None:
+        SI = blk.shared_inter
+        sh = _lib.MoeShared()
+        for i in range(3):
+            sh.codes[i], sh.scales[i], sh.zeros[i] = (sw[0][i].data_ptr(), sw[1][i].data_ptr(),
+                                                      sw[2][i].data_ptr())
+        sh.inter, sh.bits = SI, 4
+        sinter = torch.empty(B, SI, dtype=torch.float16, device=dev)
+        shared = torch.empty(B, H, dtype=torch.float16, device=dev)
+        sh.sinter, sh.sy = sinter.data_ptr(), shared.data_ptr()
+    elif blk.shared_inter > 0:
         cur = torch.cuda.current_stream(dev)
         side = _side_stream(dev)
         side.wait_stream(cur)
         with torch.cuda.stream(side):
             shared = _turbo_shared_expert(t, h, lib)
+    shp = ctypes.byref(sh) if sh is not None else None
     sel = torch.empty(P, dtype=torch.int32, device=dev)
     wts = torch.empty(P, dtype=torch.float16, device=dev)
     sg = torch.empty(B, dtype=torch.float16, device=dev)
@@ -573,7 +615,7 @@ def turbo_step_fused(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.T
         h.data_ptr(), t["router_w"].data_ptr(), _lib.ptr(t["shared_gate_w"]), B, H, E, k,
         int(blk.norm_topk_prob), sel.data_ptr(), wts.data_ptr(), sg.data_ptr(), logits.data_ptr(),
         ws.data_ptr(), ws.numel(), _lib.ptr(signs), xg.data_ptr(),
-        _lib.ptr(t["U_gu"] if r else None), n_u, r, _lib.ptr(parts), stream),
+        _lib.ptr(t["U_gu"] if r else None), n_u, r, _lib.ptr(parts), shp, stream),
         "glq_turbo_moe_prep")
     cg = t["U_gate"].shape[0] if r else 0
     pp = parts.data_ptr() if r else None
@@ -592,7 +634,7 @@ def turbo_step_fused(blk: GraphCompatibleMoeBlock, h: torch.Tensor, res: torch.T
         P, I, inter.data_ptr(), _lib.ptr(t.get("Pi_down_c") if t["signs_down"] is None else None),
         _lib.ptr(t["signs_down"]), xd.data_ptr(), _lib.ptr(Ud), Ud.shape[0] if r else 0,
         _lib.ptr(t.get("cluster_down") if r else None), sel.data_ptr(), E, r,
-        _lib.ptr(parts_d), stream), "glq_turbo_moe_down_prep")
+        _lib.ptr(parts_d), B, H, shp, stream), "glq_turbo_moe_down_prep")
     dm = _turbo_mat(xd, t, "down", _lib.ptr(parts_d), None, P)
     yd = torch.empty(P, H, dtype=torch.float16, device=dev)
     _lib.check(lib.glq_turbo_moe_gemv2(P, 1, I, H, E, sel.data_ptr(), ctypes.byref(dm), None, r,

@@ -421,6 +421,26 @@ int glq_moe_route(const void* h, const void* router_w, const void* shared_gate_w
                   void* logits, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * A GPTQ shared expert riding in the launches of a TurboQuant block's decode
+ * step (glq_turbo_moe_prep: gate and up, glq_turbo_moe_down_prep: down):
+ * codes/scales/zeros of gate, up, down as in glq_moe_params (unsigned codes
+ * with zero-points, group 128), inter its width, bits 2 or 4.
+ *   sinter (tokens, inter) fp16 = fp16(fp16(silu(fp16(h gate^T))) * fp16(h up^T))
+ *   sy (tokens, hidden) fp16 = fp16(sinter down^T), the shared expert's
+ *   output for glq_moe_combine (moe_block.py:429-435).
+ */
+typedef struct glq_moe_shared {
+  const int32_t* codes[3];
+  const void* scales[3];
+  const void* zeros[3];
+  int64_t inter;
+  int32_t bits;
+  int32_t reserved;
+  void* sinter;
+  void* sy;
+} glq_moe_shared;
+
+/*
  * The first launch of a TurboQuant block's decode step (the composition in
  * glorcq_amd/moe_block.py): glq_moe_route's routing (same arguments,
  * outputs and workspace contract), and in the same launch, from the same h:
@@ -431,14 +451,16 @@ int glq_moe_route(const void* h, const void* router_w, const void* shared_gate_w
  * (n_u, hidden, rank) -- every gate and up cluster's x U,
  * _precompute_xU_for_experts (moe_block.py:290-322) -- into parts
  * (n_u, S, tokens, rpad), S = ceil(hidden / 256), rpad = rank rounded up
- * to 32, which glq_turbo_moe_gemv2 sums in slice order.  tokens <= 16.
+ * to 32, which glq_turbo_moe_gemv2 sums in slice order; with shared, the
+ * shared expert's gate and up rows (sinter).  tokens <= 16.
  */
 int glq_turbo_moe_prep(const void* h, const void* router_w, const void* shared_gate_w,
                        int64_t tokens, int64_t hidden, int64_t experts, int64_t top_k,
                        int norm_topk_prob, int32_t* sel, void* weights, void* shared_gate,
                        void* logits, void* workspace, int64_t workspace_bytes,
                        const float* rht_signs, void* x_rot, const void* U, int64_t n_u,
-                       int64_t rank, float* parts, void* stream);
+                       int64_t rank, float* parts, const glq_moe_shared* shared,
+                       void* stream);
 
 /* One projection of the TurboQuant experts for glq_turbo_moe_gemv2. */
 typedef struct glq_turbo_mat {
@@ -476,12 +498,15 @@ int glq_turbo_moe_gemv2(int64_t picks, int64_t x_div, int64_t K, int64_t N, int6
  * fp16((1/sqrt(d)) H diag(signs) inter[p]) (d a power of two); and with U
  * (n_clusters, inter_dim, rank) the fp32 partials of inter[p]
  * U[cluster[sel[p]]] over 256-row slices into parts (picks, S, 1, rpad),
- * the down GEMV's a (glq_turbo_moe_gemv2 with cluster = NULL).
+ * the down GEMV's a (glq_turbo_moe_gemv2 with cluster = NULL); with shared,
+ * the shared expert's down rows over its sinter (tokens of hidden values,
+ * sy).
  */
 int glq_turbo_moe_down_prep(int64_t picks, int64_t inter_dim, const void* inter, const void* Pi,
                             const float* rht_signs, void* xd, const void* U, int64_t n_clusters,
                             const int32_t* cluster, const int32_t* sel, int64_t experts,
-                            int64_t rank, float* parts, void* stream);
+                            int64_t rank, float* parts, int64_t tokens, int64_t hidden,
+                            const glq_moe_shared* shared, void* stream);
 
 /*
  * Turbo GEMV of every pick (turbo_dequant_matmul_fused per expert,

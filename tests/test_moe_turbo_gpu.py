@@ -52,10 +52,12 @@ def test_turbo_routed_parity(gpu, B, seed):
     assert not bar(out, O.moe_forward(q))
 
 
-@pytest.mark.parametrize("B,seed", [(1, 7), (8, 8)])
+@pytest.mark.parametrize("B,seed", [(1, 7), (3, 9), (8, 8)])
 def test_turbo_with_shared_expert(gpu, B, seed):
     """Config-2 semantics: turbo routed experts plus the 4-bit GPTQ shared
-    expert behind its sigmoid gate, and the caller's residual folded in."""
+    expert behind its sigmoid gate, and the caller's residual folded in (1 and
+    3 tokens: the shared expert inside the fused step's launches; 8: on the
+    side stream)."""
     p = problem(B, seed, shared_inter=1024, E=60)
     assert margin(p) >= 2
     blk = GraphCompatibleMoeBlock.from_problem(p, gpu)
