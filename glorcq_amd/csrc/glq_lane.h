@@ -442,6 +442,8 @@ __device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, in
   // ---- a pairs of this lane's SV dwords (zero past the rank) ----
   uint32_t ap[M2][NSV];
   if constexpr (XU) {
+    // the rows' first loads go out before the x U phase and arrive under it
+    if (nr > 0) prologue();
     __half* ah = lane_xu_phase(src, lg.K, rank, lora, xu_lds);
 #pragma unroll
     for (int k = 0; k < NSV; ++k) {
@@ -455,7 +457,6 @@ __device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, in
     }
     if (nr <= 0) return;  // a wave with no rows of its own
     load_x();
-    prologue();
   } else {
 #pragma unroll
     for (int m = 0; m < M2; ++m)
