@@ -131,10 +131,38 @@ __device__ __forceinline__ void turbo_decode(uint32_t w, const TurboLut& H, cons
 // norm * acc + a SV^T + bias of one 16-row tile (fp32), in acc's layout:
 // acc[i] of lane (li, kb) holds token 4kb + i, row r0 + li; a_l holds the
 // block's low-rank factor a (rows < mr, zero-padded to rpad columns).
+// The epilogue's own loads for a lane's row -- its norm, bias and the SV
+// fragments of the first kTurboPreBlocks 32-column blocks -- which need
+// nothing the tile computes, so the one-shot kernel issues them at its start
+// and they arrive under the K loop.
+constexpr int kTurboPreBlocks = 2;
+struct TurboPre {
+  float nr, bb;
+  f16x8 sv[kTurboPreBlocks];
+};
+__device__ __forceinline__ TurboPre turbo_pre(const TurboArgs& a, int item, int r0, int li,
+                                              int kb) {
+  TurboPre q;
+  const int row = min(r0 + li, a.N - 1), w = turbo_w(a, item);
+  q.nr = a.norms[(int64_t)w * a.n_es + row];
+  q.bb = a.bias ? __half2float(a.bias[(int64_t)w * a.bias_es + row]) : 0.f;
+  const __half* svr = a.sv ? a.sv + (int64_t)w * a.sv_es + (int64_t)row * a.rank : nullptr;
+#pragma unroll
+  for (int b = 0; b < kTurboPreBlocks; ++b) {
+    const int j = 32 * b + 8 * kb;
+    q.sv[b] = svr && j < a.rank ? *(const f16x8*)(svr + j) : f16x8{};
+  }
+  // a compiler memory barrier keeps the loads here instead of next to their
+  // use after the K loop; it waits for nothing
+  asm volatile("" ::: "memory");
+  return q;
+}
+
 __device__ __forceinline__ f32x4 turbo_values(const TurboArgs& a, f32x4 acc, int item, int mr,
-                                              int r0, const __half* a_l, int li, int kb) {
+                                              int r0, const __half* a_l, int li, int kb,
+                                              const TurboPre* pre = nullptr) {
   const int r = r0 + li, row = min(r, a.N - 1), w = turbo_w(a, item);
-  const float nr = a.norms[(int64_t)w * a.n_es + row];
+  const float nr = pre ? pre->nr : a.norms[(int64_t)w * a.n_es + row];
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i] *= nr;
   if (a.sv) {
@@ -144,11 +172,19 @@ __device__ __forceinline__ f32x4 turbo_values(const TurboArgs& a, f32x4 acc, int
     for (int s0 = 0; s0 < a.rpad; s0 += 32) {
       const int j = s0 + 8 * kb;
       const f16x8 av = *(const f16x8*)(ar + j);
-      const f16x8 bv = j < a.rank ? *(const f16x8*)(svr + j) : f16x8{};
+      f16x8 bv = {};
+      if (pre && s0 < 32 * kTurboPreBlocks) {
+#pragma unroll
+        for (int b = 0; b < kTurboPreBlocks; ++b)
+          if (s0 == 32 * b) bv = pre->sv[b];
+      } else {
+        bv = j < a.rank ? *(const f16x8*)(svr + j) : f16x8{};
+      }
       acc = mfma_16x16x32(av, bv, acc);
     }
   }
-  const float bb = a.bias ? __half2float(a.bias[(int64_t)w * a.bias_es + row]) : 0.f;
+  const float bb = pre ? pre->bb
+                       : (a.bias ? __half2float(a.bias[(int64_t)w * a.bias_es + row]) : 0.f);
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i] += bb;
   return acc;
@@ -158,8 +194,8 @@ __device__ __forceinline__ f32x4 turbo_values(const TurboArgs& a, f32x4 acc, int
 // the SwiGLU of the gate's stored value and it.
 __device__ __forceinline__ void turbo_epilogue(const TurboArgs& a, f32x4 acc, int item, int m0,
                                                int mr, int r0, const __half* a_l, int li,
-                                               int kb) {
-  const f32x4 v = turbo_values(a, acc, item, mr, r0, a_l, li, kb);
+                                               int kb, const TurboPre* pre = nullptr) {
+  const f32x4 v = turbo_values(a, acc, item, mr, r0, a_l, li, kb, pre);
   const int r = r0 + li;
   if (r < a.N) {
 #pragma unroll
@@ -179,9 +215,10 @@ __device__ __forceinline__ void turbo_epilogue(const TurboArgs& a, f32x4 acc, in
 __device__ __forceinline__ void turbo_pair_epilogue(const TurboArgs& g, const TurboArgs& u,
                                                     f32x4 accg, f32x4 accu, int item, int m0,
                                                     int mr, int r0, const __half* a_lg,
-                                                    const __half* a_lu, int li, int kb) {
-  const f32x4 vg = turbo_values(g, accg, item, mr, r0, a_lg, li, kb);
-  const f32x4 vu = turbo_values(u, accu, item, mr, r0, a_lu, li, kb);
+                                                    const __half* a_lu, int li, int kb,
+                                                    const TurboPre* preg, const TurboPre* preu) {
+  const f32x4 vg = turbo_values(g, accg, item, mr, r0, a_lg, li, kb, preg);
+  const f32x4 vu = turbo_values(u, accu, item, mr, r0, a_lu, li, kb, preu);
   const int r = r0 + li;
   if (r < u.N) {
 #pragma unroll
@@ -340,6 +377,10 @@ __global__ __launch_bounds__(256) void turbo_gemv_kernel(TurboArgs a, TurboArgs 
   const int wlast = a.kw - 4;  // last whole 16-byte piece (kw is a multiple of 4)
   const __half* xr = xs + min(li, mr - 1) * a.xstride;
   const __half* xru = xsu + min(li, mr - 1) * a.xstride;
+  // the epilogue's loads (the tile's first wave of each K split writes it)
+  const TurboPre pre = turbo_pre(a, item, r0, li, kb);
+  TurboPre preu = pre;
+  if constexpr (PAIR) preu = turbo_pre(u, item, r0, li, kb);
   const int nsteps = (a.K + 255) >> 8;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
   constexpr int PF = kTurboPF;  // 256-code steps of codes in flight per wave (per matrix)
@@ -408,9 +449,9 @@ __global__ __launch_bounds__(256) void turbo_gemv_kernel(TurboArgs a, TurboArgs 
     }
   }
   if constexpr (PAIR)
-    turbo_pair_epilogue(a, u, acc, accu, item, m0, mr, r0, a_l, a_lu, li, kb);
+    turbo_pair_epilogue(a, u, acc, accu, item, m0, mr, r0, a_l, a_lu, li, kb, &pre, &preu);
   else
-    turbo_epilogue(a, acc, item, m0, mr, r0, a_l, li, kb);
+    turbo_epilogue(a, acc, item, m0, mr, r0, a_l, li, kb, &pre);
 }
 
 // ---------------------------------------------------------------------------
