@@ -51,6 +51,7 @@
 #include "glq_moe_route.h"
 #include "glq_stream.h"
 #include "glq_tile16.h"
+#include "glq_xstream.h"
 
 namespace glq {
 
@@ -119,6 +120,12 @@ struct MoeLaneArgs {
   int nrb;          // row blocks of an output row (routed down workgroups per item)
   int rows_blk;     // output rows per row block
   int ngu;          // workgroups of the routed gate/up role (fuse: the shared down's follow)
+  // Routed experts in the streamed token-tile form (xt, glq_xstream.h): one
+  // workgroup set per expert whose token rows are the expert's picks, each
+  // code decoded once for all of them; gate/up (pairs, whole K, the low-rank
+  // term by MFMA) and down (K slices stored apart in yb, kd = the slices).
+  int xt;
+  XsGeom gXgu, gXd;
 };
 
 constexpr int kXuSlice = 512;  // codes per x U job
@@ -284,6 +291,107 @@ struct SguTileSrc {
   __device__ SguTileView bind() const { return SguTileView{a}; }
 };
 constexpr int kMoeT16MinB = 4;  // tokens from which the shared expert takes the tile form
+
+// ---- routed experts in the streamed token-tile form (glq_xstream.h) ----
+// The picks of expert e in pick order, which is token order (a token picks an
+// expert once), as the token rows of the tile: lane l loads sel[l] and
+// sel[64 + l] (P <= 128) before the expert's codes go out; after them the
+// two ballots give every wave the same list.
+struct XtPicks {
+  int s0, s1;
+  int mine;  // pick of the token row this thread stages (row 0's past M)
+  int M;
+  __device__ void issue(const MoeLaneArgs& a) {
+    const int l = threadIdx.x & 63, P = a.B * a.topk;
+    s0 = l < P ? a.sel[l] : -1;
+    s1 = l + 64 < P ? a.sel[l + 64] : -1;
+  }
+  // xl[t] = the pick of token row t (LDS; read after a barrier)
+  __device__ int resolve(int e, int ts, int* xl) {
+    const uint64_t m0 = __builtin_amdgcn_ballot_w64(s0 == e);
+    const uint64_t m1 = __builtin_amdgcn_ballot_w64(s1 == e);
+    int slot = 0, first = 0, own = -1;
+    for (uint64_t m = m0; m; m &= m - 1, ++slot) {
+      const int p = __builtin_ctzll(m);
+      if (slot == 0) first = p;
+      if (slot == ts) own = p;
+    }
+    for (uint64_t m = m1; m; m &= m - 1, ++slot) {
+      const int p = 64 + __builtin_ctzll(m);
+      if (slot == 0) first = p;
+      if (slot == ts) own = p;
+    }
+    M = min(slot, 16);
+    mine = own >= 0 ? own : first;
+    if ((threadIdx.x & 7) == 0 && threadIdx.x < 128 && ts < M) xl[ts] = mine;
+    return M;
+  }
+};
+
+// Gate and up rows of expert e for its picks, in pairs, each pick's low-rank
+// term a SV^T by MFMA (a = fp16 of the sum of its slices' partials, the lane
+// form's load_a), storing the picks' inter.  kXguWaves waves, whole rows.
+constexpr int kXguWaves = 4;
+struct XguView {
+  const MoeLaneArgs& a;
+  int e;
+  __half* al;  // LDS [2][16][rank]: a of each token row
+  int* xl;     // LDS [16]
+  XtPicks pk;
+  __device__ const uint32_t* codes(int m) const { return a.codes[m] + (int64_t)e * a.c_es[m]; }
+  __device__ const __half* scales(int m) const { return a.scales[m] + (int64_t)e * a.s_es[m]; }
+  __device__ const __half* zeros(int m) const { return a.zeros[m] + (int64_t)e * a.s_es[m]; }
+  __device__ void issue_meta() { pk.issue(a); }
+  __device__ int resolve(int ts) { return pk.resolve(e, ts, xl); }
+  __device__ const __half* xrow_slot() const { return a.h + (int64_t)(pk.mine / a.topk) * a.H; }
+  __device__ bool lora() const { return a.rank > 0 && a.SV[0] != nullptr; }
+  __device__ int rank() const { return a.rank; }
+  __device__ const __half* sv(int m, int n) const {
+    return a.SV[m] + (int64_t)e * a.sv_es[m] + (int64_t)n * a.rank;
+  }
+  __device__ f16x8 a_frag(int m, int li, int s, int kb) const {
+    const int c = 32 * s + 8 * kb;
+    return li < pk.M && c < a.rank ? *(const f16x8*)(al + (m * 16 + li) * a.rank + c) : f16x8{};
+  }
+  // a of every (matrix, token row) into al: thread (m, t, j0) = (tid / 128,
+  // (tid / 8) % 16, tid % 8) sums columns j0, j0 + 8, ...
+  __device__ void prep(int, int) const {
+    if (!lora()) return;  // uniform
+    const int tid = threadIdx.x, m = tid >> 7, t = (tid >> 3) & 15, r = a.rank;
+    if (t < pk.M) {
+      const int p = pk.mine;
+      const int64_t job = a.xuall ? ((int64_t)m * a.C + moe_lane_clamp(a.clus[m][e], a.C)) * a.B +
+                                        p / a.topk
+                                  : (int64_t)m * a.B * a.topk + p;
+      for (int j = tid & 7; j < r; j += 8)
+        al[(m * 16 + t) * r + j] = __float2half(sum_strided(a.agu + job * a.su * r + j, r, a.su));
+    }
+    __syncthreads();
+  }
+  __device__ void store(int n, int t, float g, float u) const {
+    a.inter[(int64_t)xl[t] * a.I + n] = swiglu_fp16(g, u);
+  }
+};
+
+// Down rows of expert e for its picks over K slice s, stored apart (yb[s]):
+// the combine sums the slices in order, then adds a_down SV^T.  All
+// kMoeLaneThreads threads (the same launch's a_down jobs need all of them).
+struct XdView {
+  const MoeLaneArgs& a;
+  int e;
+  int* xl;
+  XtPicks pk;
+  __device__ const uint32_t* codes(int) const { return a.codes[2] + (int64_t)e * a.c_es[2]; }
+  __device__ const __half* scales(int) const { return a.scales[2] + (int64_t)e * a.s_es[2]; }
+  __device__ const __half* zeros(int) const { return a.zeros[2] + (int64_t)e * a.s_es[2]; }
+  __device__ void issue_meta() { pk.issue(a); }
+  __device__ int resolve(int ts) { return pk.resolve(e, ts, xl); }
+  __device__ const __half* xrow_slot() const { return a.inter + (int64_t)pk.mine * a.I; }
+  __device__ void prep(int, int) const {}
+  __device__ void store(int s, int n, int t, float v) const {
+    a.yb[((int64_t)s * a.B * a.topk + xl[t]) * a.H + n] = v;
+  }
+};
 
 // Routed part of output rows [n0, n0 + nrows) of token t into LDS routed[]:
 // sum_k w_k (y_k[n] + a_down,k SV_down,k[n]^T), fmaf over the picks in pick
@@ -783,6 +891,15 @@ __device__ void moe_lane_block_combine(const MoeLaneArgs& a, int t, int rb, floa
   }
 }
 
+// Partial a_down of job b = p sd + s: the sums of pick p's inter slice s
+// against its down U rows (LDS; thread j < rank holds column j).
+__device__ const float* moe_lane_adown_part(const MoeLaneArgs& a, int b, float* lds) {
+  const int s = b % a.sd, p = b / a.sd;
+  const XuJob job{a.inter + (int64_t)p * a.I, moe_lane_u(a, 2, a.sel[p])};
+  const int k0 = s * kXuSlice;
+  return lane_xu_sum(job, k0, min(kXuSlice, a.I - k0), a.rank, lds);
+}
+
 // Workgroups [0, nad): the a_down jobs (LoRA), job b = p sd + s; then the
 // routed down rows.  fuse: a job hands its partial over and counts itself
 // on its token; a down workgroup counts itself on its (token, row block), and
@@ -795,10 +912,8 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_down_kernel(MoeLaneA
   __shared__ int flag;
   const int nad = a.rank > 0 && a.SV[2] != nullptr ? a.B * a.topk * a.sd : 0;
   if ((int)blockIdx.x < nad) {  // partial a_down of (pick, K slice)
-    const int b = blockIdx.x, s = b % a.sd, p = b / a.sd;
-    const XuJob job{a.inter + (int64_t)p * a.I, moe_lane_u(a, 2, a.sel[p])};
-    const int k0 = s * kXuSlice;
-    const float* sums = lane_xu_sum(job, k0, min(kXuSlice, a.I - k0), a.rank, lds);
+    const int b = blockIdx.x, p = b / a.sd;
+    const float* sums = moe_lane_adown_part(a, b, lds);
     if ((int)threadIdx.x < a.rank) {
       float* d = a.ad + (int64_t)b * a.rank + threadIdx.x;
       if (a.fuse) handoff_put(d, sums[threadIdx.x]);
@@ -826,6 +941,37 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_down_kernel(MoeLaneA
     moe_lane_block_combine(a, t, rb, lds, &flag);
     if (threadIdx.x == 0) handoff_reset(a.ccnt + t * a.nrb + rb);
   }
+}
+
+// Routed gate/up in the streamed token-tile form: workgroup (e, row block) of
+// every expert (an expert no token picked leaves at once), whole rows.
+constexpr int kXsChunk = 4;  // groups of an x chunk and of a code ring slot
+constexpr int kXdWaves = kMoeLaneThreads / 64;
+__global__ __launch_bounds__(kXguWaves * 64) void moe_lane_gu_xt_kernel(MoeLaneArgs a) {
+  extern __shared__ __align__(16) float lds[];
+  __shared__ int xl[16];
+  const int e = blockIdx.x / a.gXgu.RB, rb = blockIdx.x - e * a.gXgu.RB;
+  XguView v{a, e, (__half*)lds + xs_lds_bytes(kXsChunk) / 2, xl, {}};
+  xs_run<XguView, true, true, false, kXguWaves, kXsChunk>(v, a.gXgu, rb, 0, (__half*)lds);
+}
+
+// Routed down in the streamed token-tile form: the a_down jobs first (as
+// moe_lane_down_kernel's), then workgroup (e, row block, K slice) of every
+// expert, each slice stored apart.
+__global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_down_xt_kernel(MoeLaneArgs a) {
+  extern __shared__ __align__(16) float lds[];
+  __shared__ int xl[16];
+  const int nad = a.rank > 0 && a.SV[2] != nullptr ? a.B * a.topk * a.sd : 0;
+  if ((int)blockIdx.x < nad) {
+    const float* sums = moe_lane_adown_part(a, blockIdx.x, lds);
+    if ((int)threadIdx.x < a.rank)
+      a.ad[(int64_t)blockIdx.x * a.rank + threadIdx.x] = sums[threadIdx.x];
+    return;
+  }
+  const int b = blockIdx.x - nad, per = a.gXd.RB * a.gXd.ks, e = b / per;
+  const int rb = (b - e * per) / a.gXd.ks, sl = (b - e * per) - rb * a.gXd.ks;
+  XdView v{a, e, xl, {}};
+  xs_run<XdView, false, false, true, kXdWaves, kXsChunk>(v, a.gXd, rb, sl, (__half*)lds);
 }
 
 // Each workgroup holds one token's rows (wpi a multiple of 8): first the
@@ -928,13 +1074,27 @@ T16Geom t16_geom(int N, int K, int M) {
 }
 int64_t t16_wgs(const T16Geom& t) { return (int64_t)t.RB * t.ks; }
 
+// Streamed token-tile role of one expert's N rows of K 2-bit codes, row
+// blocks of `rows`, ks K slices.
+XsGeom xs_geom(int N, int K, int rows, int ks) {
+  XsGeom t{};
+  t.N = N;
+  t.K = K;
+  t.G = K / 128;
+  t.kw = K / 16;
+  t.RB = (N + rows - 1) / rows;
+  t.ks = ks;
+  t.kg = (t.G + ks - 1) / ks;
+  return t;
+}
+
 struct MoeLanePlan {
   MoeLaneArgs a;
   int bits, sbits, rc;
   bool lora;
   int64_t off_sel, off_wts, off_sg, off_lgw, off_agu, off_inter, off_yb, off_ad, off_sinter,
       off_t16p, off_rtd, off_sy, ws_need;
-  size_t lds_route, lds_xu, lds_xut, lds_comb, lds_sd16, lds_down;
+  size_t lds_route, lds_xu, lds_xut, lds_comb, lds_sd16, lds_down, lds_xgu, lds_xd;
 };
 
 }  // namespace
@@ -1022,6 +1182,26 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   a.nrd = (int)role_blocks(a.gRD);
   a.su = (int)((H + kXuSlice - 1) / kXuSlice);
   a.sd = (int)((I + kXuSlice - 1) / kXuSlice);
+  // Routed experts in the streamed token-tile form when the picks are at
+  // least four times the experts (four token rows a tile on average; config
+  // 3 at 16 tokens: 326 -> 215 us a step, at 8 tokens the lane form's 179 us
+  // still beat its 209): each code decoded once for all of an expert's tokens
+  // instead of once per pick.  GLQ_MOE_XT16=0/1 overrides the choice.
+  a.xt = 0;
+  {
+    const char* f = getenv("GLQ_MOE_XT16");
+    const bool want = f ? atoi(f) != 0 : P_ >= 4 * a.E;
+    if (want && bits == 2 && P_ <= 128 && H % 128 == 0 && I % 128 == 0 &&
+        (!lora || (r <= 64 && r % 8 == 0))) {
+      // the down's rows in K slices of at most 16 groups: config 3's 14336
+      // in seven
+      const int gd = (int)(I / 128);
+      a.xt = 1;
+      a.gXgu = xs_geom((int)I, (int)H, 16 * kXguWaves, 1);
+      a.gXd = xs_geom((int)H, (int)I, 16 * kXdWaves, (gd + 15) / 16);
+      a.kd = a.gXd.ks;  // summed at the combine
+    }
+  }
   if (SI > 0) {
     a.gSGU = role_geom((int)SI, (int)H, sbits, 0, (int)B, true);
     // from kMoeT16MinB tokens the shared gate/up runs in the tile form: each
@@ -1049,7 +1229,7 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   // Without a shared expert, or with larger blocks, the separate combine
   // launch spreads the combine wider and measured faster.
   a.fuse = 0;
-  if (!getenv("GLQ_MOE_NO_FUSE") && bits == 2 && SI > 0 && sbits == 4 && !a.t16d &&
+  if (!getenv("GLQ_MOE_NO_FUSE") && !a.xt && bits == 2 && SI > 0 && sbits == 4 && !a.t16d &&
       lane_lrp(a.gSD.lr) == 64 && (a.gSD.lr + 63) / 64 <= 4) {
     LaneGeom g = role_geom((int)H, a.kdp, bits, 0, P_ * a.kd, false, true);
     g.G = a.gRD.G;
@@ -1117,6 +1297,8 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   if (a.fuse)  // the combine's adl, contrib and routed; after them a local a_down's scratch
     P.lds_down = std::max(P.lds_down, (size_t)(4 * ((a.topk * r + 1) / 2) +
                                                4 * a.rows_blk * (a.topk + 1)) + P.lds_xu);
+  P.lds_xgu = (size_t)xs_lds_bytes(kXsChunk) + 2 * 16 * 2 * (size_t)r;
+  P.lds_xd = std::max((size_t)xs_lds_bytes(kXsChunk), P.lds_xu);
   P.lds_sd16 = 0;
   if (a.t16d) {
     const int64_t nt = (B + a.gSD16.ks - 1) / a.gSD16.ks;  // tokens of a K slice's routed part
@@ -1196,6 +1378,23 @@ static int launch_down(const MoeLanePlan& P, hipStream_t s) {
   moe_lane_down_kernel<BITS, LRP, NP><<<dim3((unsigned)grid), dim3(kMoeLaneThreads), P.lds_down,
                                         s>>>(P.a);
   GLQ_LAUNCH_CHECK("moe_lane_down_kernel");
+  return GLQ_OK;
+}
+
+// Routed gate/up and down in the token-tile form.
+static int launch_xt(const MoeLanePlan& P, hipStream_t s) {
+  static size_t attr_gu = 64 * 1024, attr_d = 64 * 1024;
+  int rc = set_lds_limit(moe_lane_gu_xt_kernel, P.lds_xgu, attr_gu);
+  if (rc) return rc;
+  int64_t grid = (int64_t)P.a.E * P.a.gXgu.RB;
+  moe_lane_gu_xt_kernel<<<dim3((unsigned)grid), dim3(kXguWaves * 64), P.lds_xgu, s>>>(P.a);
+  GLQ_LAUNCH_CHECK("moe_lane_gu_xt_kernel");
+  rc = set_lds_limit(moe_lane_down_xt_kernel, P.lds_xd, attr_d);
+  if (rc) return rc;
+  grid = (P.lora ? (int64_t)P.a.B * P.a.topk * P.a.sd : 0) +
+         (int64_t)P.a.E * P.a.gXd.RB * P.a.gXd.ks;
+  moe_lane_down_xt_kernel<<<dim3((unsigned)grid), dim3(kMoeLaneThreads), P.lds_xd, s>>>(P.a);
+  GLQ_LAUNCH_CHECK("moe_lane_down_xt_kernel");
   return GLQ_OK;
 }
 
@@ -1283,12 +1482,18 @@ static int moe_lane_launch(const MoeLanePlan& P, hipStream_t s) {
                          P.lds_xu, s>>>(a);
     GLQ_LAUNCH_CHECK("moe_lane_xu_kernel");
   }
-  // 3. routed gate/up
-  rc = P.bits == 2 ? dispatch_gu<2>(P, s) : dispatch_gu<4>(P, s);
-  if (rc) return rc;
-  // 4. routed down (+ a_down; fuse: + the combine)
-  rc = P.bits == 2 ? dispatch_down<2>(P, s) : dispatch_down<4>(P, s);
-  if (rc) return rc;
+  if (a.xt) {
+    // 3-4. routed gate/up and down (+ a_down) in the token-tile form
+    rc = launch_xt(P, s);
+    if (rc) return rc;
+  } else {
+    // 3. routed gate/up
+    rc = P.bits == 2 ? dispatch_gu<2>(P, s) : dispatch_gu<4>(P, s);
+    if (rc) return rc;
+    // 4. routed down (+ a_down; fuse: + the combine)
+    rc = P.bits == 2 ? dispatch_down<2>(P, s) : dispatch_down<4>(P, s);
+    if (rc) return rc;
+  }
   if (a.fuse) return GLQ_OK;
   // 5. shared down + combine, or the combine alone
   if (P.sbits == 2) return dispatch_shared<2>(P, s, false);
