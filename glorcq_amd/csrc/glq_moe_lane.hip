@@ -951,8 +951,10 @@ __global__ __launch_bounds__(kXguWaves * 64) void moe_lane_gu_xt_kernel(MoeLaneA
   extern __shared__ __align__(16) float lds[];
   __shared__ int xl[16];
   const int e = blockIdx.x / a.gXgu.RB, rb = blockIdx.x - e * a.gXgu.RB;
-  XguView v{a, e, (__half*)lds + xs_lds_bytes(kXsChunk) / 2, xl, {}};
-  xs_run<XguView, true, true, false, kXguWaves, kXsChunk>(v, a.gXgu, rb, 0, (__half*)lds);
+  unsigned char* sm = (unsigned char*)lds;  // x chunks, transposition areas, a
+  XguView v{a, e, (__half*)(sm + xs_lds_bytes(kXsChunk) + xs_tr_bytes(kXguWaves)), xl, {}};
+  xs_run<XguView, true, true, false, kXguWaves, kXsChunk, 2>(
+      v, a.gXgu, rb, 0, (__half*)sm, (uint32_t*)(sm + xs_lds_bytes(kXsChunk)));
 }
 
 // Routed down in the streamed token-tile form: the a_down jobs first (as
@@ -971,7 +973,9 @@ __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_down_xt_kernel(MoeLa
   const int b = blockIdx.x - nad, per = a.gXd.RB * a.gXd.ks, e = b / per;
   const int rb = (b - e * per) / a.gXd.ks, sl = (b - e * per) - rb * a.gXd.ks;
   XdView v{a, e, xl, {}};
-  xs_run<XdView, false, false, true, kXdWaves, kXsChunk>(v, a.gXd, rb, sl, (__half*)lds);
+  unsigned char* sm = (unsigned char*)lds;  // x chunks, transposition areas
+  xs_run<XdView, false, false, true, kXdWaves, kXsChunk, 3>(
+      v, a.gXd, rb, sl, (__half*)sm, (uint32_t*)(sm + xs_lds_bytes(kXsChunk)));
 }
 
 // Each workgroup holds one token's rows (wpi a multiple of 8): first the
@@ -1297,8 +1301,8 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   if (a.fuse)  // the combine's adl, contrib and routed; after them a local a_down's scratch
     P.lds_down = std::max(P.lds_down, (size_t)(4 * ((a.topk * r + 1) / 2) +
                                                4 * a.rows_blk * (a.topk + 1)) + P.lds_xu);
-  P.lds_xgu = (size_t)xs_lds_bytes(kXsChunk) + 2 * 16 * 2 * (size_t)r;
-  P.lds_xd = std::max((size_t)xs_lds_bytes(kXsChunk), P.lds_xu);
+  P.lds_xgu = (size_t)(xs_lds_bytes(kXsChunk) + xs_tr_bytes(kXguWaves)) + 2 * 16 * 2 * (size_t)r;
+  P.lds_xd = std::max((size_t)(xs_lds_bytes(kXsChunk) + xs_tr_bytes(kXdWaves)), P.lds_xu);
   P.lds_sd16 = 0;
   if (a.t16d) {
     const int64_t nt = (B + a.gSD16.ks - 1) / a.gSD16.ks;  // tokens of a K slice's routed part

@@ -14,10 +14,11 @@
 //
 //  * Workgroup (row block rb, K slice s) of W waves: wave w takes the 16 rows
 //    [16 (W rb + w), + 16) of each of M2 matrices over the slice's groups, in
-//    order, through a ring of two chunks of C groups of codes (8 bytes a lane
-//    a group and matrix) with their rows' scales and zeros (one 8-byte load
-//    each for 4 groups) -- the whole row slice in one wave, so no partial sums
-//    meet.
+//    order, through a ring of R chunks of 4 groups of codes (two 16-byte
+//    loads a lane, each covering 8 rows' whole 128-byte lines; the wave's LDS
+//    area turns them to 8 bytes of each group for the MFMA) with their
+//    rows' scales and zeros (one 8-byte load each) -- the whole row slice in
+//    one wave, so no partial sums meet.
 //  * x is shared by the waves through LDS: chunks of C groups of the token
 //    rows, double-buffered, each staged once by the workgroup (32 bytes a
 //    thread) already in the decode order below, rows padded to 272 bytes
@@ -45,8 +46,12 @@ namespace glq {
 
 constexpr int kXsRowHalves = 136;  // halves a staged token row of a group (128 + pad)
 
+constexpr int kXsTrRow = 36;        // dwords a row of the code transposition area (32 + pad)
+
 // LDS bytes of the double-buffered x chunks of C groups.
 __host__ __device__ constexpr int xs_lds_bytes(int C) { return 2 * C * 16 * kXsRowHalves * 2; }
+// LDS bytes of the W waves' code transposition areas (16 rows of a chunk).
+__host__ __device__ constexpr int xs_tr_bytes(int W) { return W * 16 * kXsTrRow * 4; }
 
 // Row blocks of 16 W rows, K slices of kg groups (of the G groups of a row).
 struct XsGeom {
@@ -92,12 +97,13 @@ __device__ __forceinline__ void xs_decode2(const u32x2& w, const DecodeConsts& d
 // kb, + 8), zero past the rank; staged by prep), rank(), and the stores.
 // Every thread of the W-wave workgroup calls xs_run; each stages 2 C / W
 // pieces of 32 bytes of a chunk, of its token row ts = (thread / 8) % 16.
-template <class View, bool PAIR, bool LORA, bool SPLIT, int W, int C>
-__device__ void xs_run(View& v, const XsGeom& g, int rb, int sl, __half* xlds) {
+template <class View, bool PAIR, bool LORA, bool SPLIT, int W, int C, int R>
+__device__ void xs_run(View& v, const XsGeom& g, int rb, int sl, __half* xlds, uint32_t* tlds) {
   constexpr int M2 = PAIR ? 2 : 1;
   constexpr int NP = 2 * C / W;  // 32-byte x pieces a thread stages a chunk
   static_assert(NP >= 1 && NP * W == 2 * C, "whole x pieces per thread");
-  static_assert(C <= 4, "a chunk's scales in one 8-byte load");
+  static_assert(C == 4, "a lane's 32 bytes of a chunk row are one group");
+  static_assert(R == 2 || R == 3, "a ring of two or three chunks");
   constexpr int BUFH = C * 16 * kXsRowHalves;
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   const int tid = threadIdx.x, lane = tid & 63;
@@ -108,23 +114,30 @@ __device__ void xs_run(View& v, const XsGeom& g, int rb, int sl, __half* xlds) {
   v.issue_meta();
 
   const int row = min(16 * (W * rb + wave) + li, g.N - 1);
-  const int coff = row * g.kw + 2 * kb, soff = row * g.G;
+  const int soff = row * g.G;
+  int rowq[2];  // code word offsets of the rows this lane loads
+#pragma unroll
+  for (int h = 0; h < 2; ++h) rowq[h] = min(16 * (W * rb + wave) + 8 * h + (lane >> 3), g.N - 1) * g.kw;
   const int nch = (ng + C - 1) / C;
-  // a chunk's codes (8 bytes a lane a group and matrix) and its rows' scales
-  // and zeros: with G and the slice in whole quads of groups, one 8-byte load
-  // of each for C = 4 groups
-  const bool quads = C == 4 && g.G % 4 == 0 && g.kg % 4 == 0;  // uniform
+  // a chunk's codes: two 16-byte loads a lane over the tile's 16 rows x 128
+  // bytes (whole lines), passed through LDS to the MFMA order (8 bytes of
+  // every group for lane (li, kb)); and the
+  // rows' scales and zeros: with G and the slice in whole quads of groups,
+  // one 8-byte load of each
+  const bool quads = g.G % 4 == 0 && g.kg % 4 == 0;  // uniform
   struct Buf {
-    u32x2 c[C][M2];
+    u32x4 c[M2][2];
     u32x2 s[M2], z[M2];  // C fp16 scales, zeros
   };
   auto load_chunk = [&](Buf& b, int c) {  // groups past the slice: its last (unused)
+    // load h takes rows 8 h + lane / 8 of the tile, 16 bytes (lane % 8) of
+    // each row's 128 bytes: eight whole lines a load
+    const int gq = gb + min(c * C + (lane & 7) / 2, ng - 1);
 #pragma unroll
-    for (int gc = 0; gc < C; ++gc) {
-      const int gi = gb + min(c * C + gc, ng - 1);
+    for (int m = 0; m < M2; ++m)
 #pragma unroll
-      for (int m = 0; m < M2; ++m) b.c[gc][m] = *(const u32x2*)(v.codes(m) + coff + 8 * gi);
-    }
+      for (int h = 0; h < 2; ++h)
+        b.c[m][h] = *(const u32x4*)(v.codes(m) + rowq[h] + 8 * gq + 4 * (lane & 1));
 #pragma unroll
     for (int m = 0; m < M2; ++m) {
       if (quads) {
@@ -134,7 +147,7 @@ __device__ void xs_run(View& v, const XsGeom& g, int rb, int sl, __half* xlds) {
       } else {
         uint16_t sh[4] = {0, 0, 0, 0}, zh[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int gc = 0; gc < C && gc < 4; ++gc) {
+        for (int gc = 0; gc < C; ++gc) {
           const int gi = gb + min(c * C + gc, ng - 1);
           sh[gc] = ((const uint16_t*)v.scales(m))[soff + gi];
           zh[gc] = ((const uint16_t*)v.zeros(m))[soff + gi];
@@ -144,7 +157,7 @@ __device__ void xs_run(View& v, const XsGeom& g, int rb, int sl, __half* xlds) {
       }
     }
   };
-  Buf ring[2];
+  Buf ring[R];
   load_chunk(ring[0], 0);
   if (nch > 1) load_chunk(ring[1], 1);
   __builtin_amdgcn_sched_barrier(0);  // the codes go out before the routing is read
@@ -188,7 +201,24 @@ __device__ void xs_run(View& v, const XsGeom& g, int rb, int sl, __half* xlds) {
 #pragma unroll
   for (int m = 0; m < M2; ++m) yv[m] = f32x4{0.f, 0.f, 0.f, 0.f};
   const DecodeConsts dk = DecodeConsts::make();
-  auto compute = [&](const Buf& b, int gc, const __half* xg) {
+  // the chunk's codes in MFMA order: each matrix's 16 rows x 128 bytes through
+  // the wave's LDS area (its LDS operations run in order; the asm statements
+  // keep the compiler from moving the reads above the writes)
+  uint32_t* tl = tlds + wave * 16 * kXsTrRow;
+  auto transpose = [&](const Buf& b, u32x2 (&cw)[C][M2]) {
+#pragma unroll
+    for (int m = 0; m < M2; ++m) {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        *(u32x4*)(tl + (8 * h + (lane >> 3)) * kXsTrRow + 4 * (lane & 7)) = b.c[m][h];
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int gc = 0; gc < C; ++gc) cw[gc][m] = *(const u32x2*)(tl + li * kXsTrRow + 8 * gc + 2 * kb);
+    }
+    asm volatile("" ::: "memory");
+  };
+  auto compute = [&](const Buf& b, const u32x2 (&cw)[C][M2], int gc, const __half* xg) {
     f16x8 xa[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) xa[s] = *(const f16x8*)(xg + li * kXsRowHalves + 32 * kb + 8 * s);
@@ -199,7 +229,7 @@ __device__ void xs_run(View& v, const XsGeom& g, int rb, int sl, __half* xlds) {
 #pragma unroll
     for (int m = 0; m < M2; ++m) {
       f16x8 bb[4];
-      xs_decode2(b.c[gc][m], dk, bb);
+      xs_decode2(cw[gc][m], dk, bb);
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) acc = mfma_16x16x32(xa[s], bb[s], acc);
@@ -210,20 +240,26 @@ __device__ void xs_run(View& v, const XsGeom& g, int rb, int sl, __half* xlds) {
       for (int q = 0; q < 4; ++q) yv[m][q] = fmaf(sc, fmaf(-z, xs[q], acc[q]), yv[m][q]);
     }
   };
-  // chunk c decodes from x buffer c & 1 and ring slot c & 1, which then loads
-  // chunk c + 2; the next chunk's x is loaded before and stored after the
-  // chunk's groups, then one barrier
-  for (int c0 = 0; c0 < nch; c0 += 2) {
+  // chunk c decodes from x buffer c & 1 and ring slot c % R; before its
+  // groups it issues the next chunk's x and (R = 3) chunk c + 2's codes into
+  // the slot chunk c - 1 freed (so the x store after the groups waits for the
+  // x alone), or (R = 2) after its groups into its own slot; then one barrier
+  for (int c0 = 0; c0 < nch; c0 += R) {
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
+    for (int cc = 0; cc < R; ++cc) {
       const int c = c0 + cc;
       if (c < nch) {  // uniform
         if (c + 1 < nch) load_x(c + 1);
-        const __half* xb = xlds + cc * BUFH;
+        if constexpr (R == 3)
+          if (c + 2 < nch) load_chunk(ring[(cc + 2) % 3], c + 2);
+        const __half* xb = xlds + (c & 1) * BUFH;
+        u32x2 cw[C][M2];
+        transpose(ring[cc], cw);
 #pragma unroll
         for (int gc = 0; gc < C; ++gc)
-          if (c * C + gc < ng) compute(ring[cc], gc, xb + gc * 16 * kXsRowHalves);
-        if (c + 2 < nch) load_chunk(ring[cc], c + 2);
+          if (c * C + gc < ng) compute(ring[cc], cw, gc, xb + gc * 16 * kXsRowHalves);
+        if constexpr (R == 2)
+          if (c + 2 < nch) load_chunk(ring[cc], c + 2);
         if (c + 1 < nch) store_x(c + 1);
         __syncthreads();
       }
