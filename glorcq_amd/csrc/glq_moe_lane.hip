@@ -1188,21 +1188,21 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   a.sd = (int)((I + kXuSlice - 1) / kXuSlice);
   // Routed experts in the streamed token-tile form when the picks are at
   // least four times the experts (four token rows a tile on average; config
-  // 3 at 16 tokens: 326 -> 215 us a step, at 8 tokens the lane form's 179 us
-  // still beat its 209): each code decoded once for all of an expert's tokens
-  // instead of once per pick.  GLQ_MOE_XT16=0/1 overrides the choice.
+  // 3 at 16 tokens: 316 -> 179 us a step; at 8 tokens the two forms tie, 179
+  // and 175 us): each code decoded once for all of an expert's tokens instead
+  // of once per pick.  GLQ_MOE_XT16=0/1 overrides the choice.
   a.xt = 0;
   {
     const char* f = getenv("GLQ_MOE_XT16");
     const bool want = f ? atoi(f) != 0 : P_ >= 4 * a.E;
     if (want && bits == 2 && P_ <= 128 && H % 128 == 0 && I % 128 == 0 &&
         (!lora || (r <= 64 && r % 8 == 0))) {
-      // the down's rows in K slices of at most 16 groups: config 3's 14336
-      // in seven
+      // the down's rows in K slices of at most 28 groups: config 3's 14336
+      // in four
       const int gd = (int)(I / 128);
       a.xt = 1;
       a.gXgu = xs_geom((int)I, (int)H, 16 * kXguWaves, 1);
-      a.gXd = xs_geom((int)H, (int)I, 16 * kXdWaves, (gd + 15) / 16);
+      a.gXd = xs_geom((int)H, (int)I, 16 * kXdWaves, (gd + 27) / 28);
       a.kd = a.gXd.ks;  // summed at the combine
     }
   }
