@@ -1187,14 +1187,14 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   a.su = (int)((H + kXuSlice - 1) / kXuSlice);
   a.sd = (int)((I + kXuSlice - 1) / kXuSlice);
   // Routed experts in the streamed token-tile form when the picks are at
-  // least four times the experts (four token rows a tile on average; config
-  // 3 at 16 tokens: 316 -> 179 us a step; at 8 tokens the two forms tie, 179
-  // and 175 us): each code decoded once for all of an expert's tokens instead
-  // of once per pick.  GLQ_MOE_XT16=0/1 overrides the choice.
+  // least twice the experts (two token rows a tile on average; config 3 at
+  // 16 tokens: 316 -> 179 us a step, at 8 tokens 179 -> 175 us): each code
+  // decoded once for all of an expert's tokens instead of once per pick.
+  // GLQ_MOE_XT16=0/1 overrides the choice.
   a.xt = 0;
   {
     const char* f = getenv("GLQ_MOE_XT16");
-    const bool want = f ? atoi(f) != 0 : P_ >= 4 * a.E;
+    const bool want = f ? atoi(f) != 0 : P_ >= 2 * a.E;
     if (want && bits == 2 && P_ <= 128 && H % 128 == 0 && I % 128 == 0 &&
         (!lora || (r <= 64 && r % 8 == 0))) {
       // the down's rows in K slices of at most 28 groups: config 3's 14336

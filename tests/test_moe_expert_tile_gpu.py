@@ -3,7 +3,7 @@
 moe_lane_down_xt_kernel over glq_tile16.h's 2-bit form): one workgroup set per
 expert whose token rows are the expert's picks, so each code is decoded once
 for all of them (the lane form decodes it once per pick).  The lane path takes
-it when the picks are at least four times the experts (BASELINE config 3 at 16
+it when the picks are at least twice the experts (BASELINE config 3 from 8
 tokens); GLQ_MOE_XT16=1 / 0 forces it on / off.
 
 Bars as tests/test_moe_gpu.py against the MoE oracle (routing ids identical,
