@@ -33,6 +33,9 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
                                          of known size, for rocprofv3 --pmc)
        python bench.py --pmc-workload-kernels   (MoE decode steps and prefill
                                                  GEMMs, for rocprofv3 --pmc)
+       python bench.py --model-only [--model-layers L] [--model-batches 1,16]
+       python bench.py --turbo-step-only [--turbo-batches 1]   (the TurboQuant-
+                                         expert MoE step, then 5 eager steps)
 """
 
 from __future__ import annotations
@@ -443,16 +446,19 @@ def bench_moe_cold(dev, seed=6, copies=8, rounds=3, trials=9):
     return res
 
 
-def bench_moe_turbo(dev, seed=6, reps=10, trials=9):
+def bench_moe_turbo(dev, seed=6, reps=10, trials=9, batches=(1, 4, 16), eager=0):
     """Config 2's block with TurboQuant routed experts (the reference's 2-bit
     expert format; format.make_turbo_moe: gate/up rotated by an RHT, down by a
     QR Pi, the 4-bit GPTQ shared expert): one decode step per call through
-    GraphCompatibleMoeBlock's turbo step, hipGraph replays as bench_moe."""
+    GraphCompatibleMoeBlock's turbo step, hipGraph replays as bench_moe; then
+    `eager` eager steps (for a kernel trace)."""
+    import torch
+
     from glorcq_amd import format as fmt
     from glorcq_amd.moe_block import GraphCompatibleMoeBlock
 
     res = {}
-    for B in (1, 4, 16):
+    for B in batches:
         p = fmt.make_turbo_moe(B=B, seed=seed)
         blk = GraphCompatibleMoeBlock.from_problem(p, dev)
         h = p.h.reshape(1, B, p.H).to(dev)
@@ -460,6 +466,9 @@ def bench_moe_turbo(dev, seed=6, reps=10, trials=9):
         us = _graph_step_us(lambda: blk(h), reps, trials)
         res[str(B)] = {"us_per_step": round(us, 2), "us_per_token": round(us / B, 3)}
         log(f"moe turbo experts B={B}: {us:.2f} us/step")
+        for _ in range(eager):
+            blk(h)
+        torch.cuda.synchronize()
         del blk
     return res
 
@@ -644,6 +653,10 @@ def main():
                     help="run only the model-level decode leg and print its JSON (profiling)")
     ap.add_argument("--model-layers", type=int, default=48)
     ap.add_argument("--model-batches", default="1,16")
+    ap.add_argument("--turbo-step-only", action="store_true",
+                    help="run only the TurboQuant-expert MoE step leg, then 5 eager steps, "
+                         "and print its JSON (profiling)")
+    ap.add_argument("--turbo-batches", default="1")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (every box here has one); "
@@ -655,6 +668,14 @@ def main():
         return 0
     if args.pmc_workload:
         pmc_workload()
+        return 0
+    if args.turbo_step_only:
+        import torch
+
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        batches = tuple(int(b) for b in args.turbo_batches.split(","))
+        print(json.dumps(bench_moe_turbo(dev, batches=batches, eager=5)), flush=True)
         return 0
     if args.model_only:
         import torch
