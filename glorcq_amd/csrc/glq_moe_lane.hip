@@ -126,6 +126,11 @@ struct MoeLaneArgs {
   // term by MFMA) and down (K slices stored apart in yb, kd = the slices).
   int xt;
   XsGeom gXgu, gXd;
+  // (xuall = 2 with xt) a = fp16 of the slices' sums of every (matrix,
+  // cluster, token), [2][C][B][rank], formed by the last of a (matrix,
+  // cluster)'s tile jobs to arrive on xucnt[m C + c] (zero between steps)
+  __half* a16;
+  unsigned* xucnt;
 };
 
 constexpr int kXuSlice = 512;  // codes per x U job
@@ -300,6 +305,7 @@ constexpr int kMoeT16MinB = 4;  // tokens from which the shared expert takes the
 struct XtPicks {
   int s0, s1;
   int mine;  // pick of the token row this thread stages (row 0's past M)
+  int mli;   // pick of token row li (the lane's MFMA A row; row 0's past M)
   int M;
   __device__ void issue(const MoeLaneArgs& a) {
     const int l = threadIdx.x & 63, P = a.B * a.topk;
@@ -307,22 +313,25 @@ struct XtPicks {
     s1 = l + 64 < P ? a.sel[l + 64] : -1;
   }
   // xl[t] = the pick of token row t (LDS; read after a barrier)
-  __device__ int resolve(int e, int ts, int* xl) {
+  __device__ int resolve(int e, int ts, int li, int* xl) {
     const uint64_t m0 = __builtin_amdgcn_ballot_w64(s0 == e);
     const uint64_t m1 = __builtin_amdgcn_ballot_w64(s1 == e);
-    int slot = 0, first = 0, own = -1;
+    int slot = 0, first = 0, own = -1, ownl = -1;
     for (uint64_t m = m0; m; m &= m - 1, ++slot) {
       const int p = __builtin_ctzll(m);
       if (slot == 0) first = p;
       if (slot == ts) own = p;
+      if (slot == li) ownl = p;
     }
     for (uint64_t m = m1; m; m &= m - 1, ++slot) {
       const int p = 64 + __builtin_ctzll(m);
       if (slot == 0) first = p;
       if (slot == ts) own = p;
+      if (slot == li) ownl = p;
     }
     M = min(slot, 16);
     mine = own >= 0 ? own : first;
+    mli = ownl >= 0 ? ownl : first;
     if ((threadIdx.x & 7) == 0 && threadIdx.x < 128 && ts < M) xl[ts] = mine;
     return M;
   }
@@ -341,22 +350,39 @@ struct XguView {
   __device__ const uint32_t* codes(int m) const { return a.codes[m] + (int64_t)e * a.c_es[m]; }
   __device__ const __half* scales(int m) const { return a.scales[m] + (int64_t)e * a.s_es[m]; }
   __device__ const __half* zeros(int m) const { return a.zeros[m] + (int64_t)e * a.s_es[m]; }
+  u32x4 svf[2][2], af[2][2];  // the lane's SV and (a16) a fragments, matrix x MFMA step
   __device__ void issue_meta() { pk.issue(a); }
-  __device__ int resolve(int ts) { return pk.resolve(e, ts, xl); }
+  __device__ int resolve(int ts, int li) { return pk.resolve(e, ts, li, xl); }
   __device__ const __half* xrow_slot() const { return a.h + (int64_t)(pk.mine / a.topk) * a.H; }
   __device__ bool lora() const { return a.rank > 0 && a.SV[0] != nullptr; }
-  __device__ int rank() const { return a.rank; }
-  __device__ const __half* sv(int m, int n) const {
-    return a.SV[m] + (int64_t)e * a.sv_es[m] + (int64_t)n * a.rank;
+  // the low-rank term's loads, issued with the first codes: SV of the lane's
+  // row (B) and, with a16, a of its token row li (A)
+  __device__ void lora_issue(int row, int li, int kb) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int c = 32 * s + 8 * kb;
+        svf[m][s] = c < a.rank ? *(const u32x4*)(a.SV[m] + (int64_t)e * a.sv_es[m] +
+                                                 (int64_t)row * a.rank + c)
+                               : u32x4{0u, 0u, 0u, 0u};
+        af[m][s] = u32x4{0u, 0u, 0u, 0u};
+        if (a.a16 && li < pk.M && c < a.rank) {
+          const int cl = moe_lane_clamp(a.clus[m][e], a.C), t = pk.mli / a.topk;
+          af[m][s] = *(const u32x4*)(a.a16 + (((int64_t)m * a.C + cl) * a.B + t) * a.rank + c);
+        }
+      }
   }
+  __device__ f16x8 sv_frag(int m, int s) const { return __builtin_bit_cast(f16x8, svf[m][s]); }
   __device__ f16x8 a_frag(int m, int li, int s, int kb) const {
+    if (a.a16) return __builtin_bit_cast(f16x8, af[m][s]);
     const int c = 32 * s + 8 * kb;
     return li < pk.M && c < a.rank ? *(const f16x8*)(al + (m * 16 + li) * a.rank + c) : f16x8{};
   }
-  // a of every (matrix, token row) into al: thread (m, t, j0) = (tid / 128,
-  // (tid / 8) % 16, tid % 8) sums columns j0, j0 + 8, ...
+  // without a16: a of every (matrix, token row) into al: thread (m, t, j0) =
+  // (tid / 128, (tid / 8) % 16, tid % 8) sums columns j0, j0 + 8, ...
   __device__ void prep(int, int) const {
-    if (!lora()) return;  // uniform
+    if (!lora() || a.a16) return;  // uniform
     const int tid = threadIdx.x, m = tid >> 7, t = (tid >> 3) & 15, r = a.rank;
     if (t < pk.M) {
       const int p = pk.mine;
@@ -385,7 +411,7 @@ struct XdView {
   __device__ const __half* scales(int) const { return a.scales[2] + (int64_t)e * a.s_es[2]; }
   __device__ const __half* zeros(int) const { return a.zeros[2] + (int64_t)e * a.s_es[2]; }
   __device__ void issue_meta() { pk.issue(a); }
-  __device__ int resolve(int ts) { return pk.resolve(e, ts, xl); }
+  __device__ int resolve(int ts, int li) { return pk.resolve(e, ts, li, xl); }
   __device__ const __half* xrow_slot() const { return a.inter + (int64_t)pk.mine * a.I; }
   __device__ void prep(int, int) const {}
   __device__ void store(int s, int n, int t, float v) const {
@@ -728,9 +754,23 @@ __device__ void moe_lane_xu_tile(const MoeLaneArgs& a, int job, unsigned char* s
 #pragma unroll
     for (int w = 0; w < 8; ++w) v += red[((w * 4 + ct) * 4 + i) * 64 + l];
     const int t = 4 * (l >> 4) + i, col = ct * 16 + (l & 15);  // D: token row, rank column
-    if (t < a.B && col < r)
-      a.agu[((((int64_t)m * a.C + c) * a.B + t) * a.su + s) * r + col] = v;
+    if (t < a.B && col < r) {
+      float* d = a.agu + ((((int64_t)m * a.C + c) * a.B + t) * a.su + s) * r + col;
+      if (a.a16) handoff_put(d, v);
+      else *d = v;
+    }
   }
+  if (!a.a16) return;
+  // the last slice job of (matrix, cluster) to arrive: a = fp16 of the slices'
+  // sums in slice order (the lane form's load_a), for every token
+  __shared__ int last;
+  if (!handoff_arrive(a.xucnt + mc, (unsigned)a.su, &last)) return;
+  for (int e = tid; e < a.B * r; e += kMoeLaneThreads) {
+    const int t = e / r, j = e - t * r;
+    const float* pp = a.agu + (((int64_t)mc * a.B + t) * a.su) * r + j;
+    a.a16[((int64_t)mc * a.B + t) * r + j] = __float2half(sum_strided_coh(pp, r, a.su));
+  }
+  if (tid == 0) handoff_reset(a.xucnt + mc);
 }
 
 // ---- kernels ----
@@ -1097,7 +1137,7 @@ struct MoeLanePlan {
   int bits, sbits, rc;
   bool lora;
   int64_t off_sel, off_wts, off_sg, off_lgw, off_agu, off_inter, off_yb, off_ad, off_sinter,
-      off_t16p, off_rtd, off_sy, ws_need;
+      off_t16p, off_rtd, off_sy, off_a16, ws_need;
   size_t lds_route, lds_xu, lds_xut, lds_comb, lds_sd16, lds_down, lds_xgu, lds_xd;
 };
 
@@ -1282,6 +1322,8 @@ static bool moe_lane_plan(const glq_moe_params* p, MoeLanePlan& P) {
   if (uall && B >= 8 && B <= kXuTileMaxB && r <= kXuTileMaxRank && !getenv("GLQ_MOE_NO_XU_TILE"))
     a.xuall = 2;
   P.off_agu = take(4 * 2 * (int64_t)r * a.su * (a.xuall ? (int64_t)a.C * B : P_));
+  // the streamed expert tiles read a as fp16, finished by the tile jobs
+  P.off_a16 = take(a.xt && a.xuall == 2 && lora ? 2 * 2 * (int64_t)a.C * B * r : 0);
   P.off_inter = take(2 * (int64_t)P_ * I);
   P.off_yb = take(4 * (int64_t)a.kd * P_ * H);
   P.off_ad = take(4 * (int64_t)P_ * a.sd * r);
@@ -1548,6 +1590,10 @@ int moe_lane_decode(const glq_moe_params* p, void* workspace, int64_t workspace_
   a.rtd = (float*)(w + P.off_rtd);
   a.sy = (__half*)(w + P.off_sy);
   a.ccnt = (unsigned*)(w + 4096);  // header bytes 4096 .. 8191, zero between steps
+  if (a.xt && a.xuall == 2 && P.lora) {
+    a.a16 = (__half*)(w + P.off_a16);
+    a.xucnt = (unsigned*)(w + 256);  // header bytes 256 .. 511 (2 C <= 64 counters)
+  }
   a.adcnt = (unsigned*)(w + 512);  // header bytes 512 .. 575 (16 tokens)
   return moe_lane_launch(P, s);
 }

@@ -31,9 +31,10 @@
 //  * Token rows past the expert's M only fill MFMA rows that are never stored
 //    (a D row depends on its A row alone), so they are neither loaded nor
 //    masked.
-//  * LORA: slice 0 adds a SV^T (rank <= 64) as two more MFMA steps per
-//    matrix (A = the view's fp16 a of each token row, from LDS; B = the
-//    wave's rows of SV).
+//  * LORA: slice 0 adds a SV^T (rank <= 64) after its K loop, two MFMA steps
+//    per matrix (A = the view's fp16 a of each token row; B = the wave's rows
+//    of SV), both loaded in one round trip (loaded with the first codes they
+//    would hold 32 VGPRs through the loop: a wave fewer a SIMD).
 //  * Each lane stores its outputs (token rows 4 kb .. 4 kb + 3 of row li):
 //    SPLIT the slice's partial, store(s, n, t, y); PAIR store(n, t, y0, y1)
 //    over the whole K (one slice).  Every sum has a fixed order: the same bits
@@ -89,12 +90,13 @@ __device__ __forceinline__ void xs_decode2(const u32x2& w, const DecodeConsts& d
 // View: codes(m), scales(m), zeros(m) (matrix m's rows; uniform pointers),
 // issue_meta() (its loads, issued before the codes), resolve(ts) (the token
 // rows M <= 16, the same in every thread, read after the first codes are
-// issued; it also finds token row ts's input), xrow_slot() (the input row of
-// token row ts, ts = (thread / 8) % 16, valid when ts < M), prep(rb, s)
-// (every thread, after the first x chunk is in LDS; may hold barriers and use
-// LDS past xs_lds_bytes), with LORA lora() (uniform), sv(m, n) (row n of
-// matrix m's SV) and a_frag(m, li, s, kb) (token row li's a, columns [32 s + 8
-// kb, + 8), zero past the rank; staged by prep), rank(), and the stores.
+// issued; it also finds token rows ts's and li's inputs), xrow_slot() (the
+// input row of token row ts, ts = (thread / 8) % 16, valid when ts < M),
+// prep(rb, s) (every thread, after the first x chunk is in LDS; may hold
+// barriers and use LDS past xs_lds_bytes), with LORA lora() (uniform),
+// lora_issue(row, li, kb) (the term's loads, after the K loop), and
+// sv_frag(m, s) and a_frag(m, li, s, kb) (the lane's row's SV and token row
+// li's a, columns [32 s + 8 kb, + 8), zero past the rank), and the stores.
 // Every thread of the W-wave workgroup calls xs_run; each stages 2 C / W
 // pieces of 32 bytes of a chunk, of its token row ts = (thread / 8) % 16.
 template <class View, bool PAIR, bool LORA, bool SPLIT, int W, int C, int R>
@@ -162,8 +164,10 @@ __device__ void xs_run(View& v, const XsGeom& g, int rb, int sl, __half* xlds, u
   if (nch > 1) load_chunk(ring[1], 1);
   __builtin_amdgcn_sched_barrier(0);  // the codes go out before the routing is read
   const int ts = (tid >> 3) & 15;     // the token row this thread stages
-  const int M = v.resolve(ts);
+  const int M = v.resolve(ts, li);
   if (M == 0) return;  // uniform: no token picked this expert
+  bool lw = false;  // the low-rank term (slice 0)
+  if constexpr (LORA) lw = sl == 0 && v.lora();  // uniform
 
   // x staging: piece j of a chunk = (group q / 128, token row (q / 8) % 16,
   // 16-code pair q % 8), q = tid + 64 W j (token row ts for every j)
@@ -200,6 +204,7 @@ __device__ void xs_run(View& v, const XsGeom& g, int rb, int sl, __half* xlds, u
   f32x4 yv[M2];
 #pragma unroll
   for (int m = 0; m < M2; ++m) yv[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
   const DecodeConsts dk = DecodeConsts::make();
   // the chunk's codes in MFMA order: each matrix's 16 rows x 128 bytes through
   // the wave's LDS area (its LDS operations run in order; the asm statements
@@ -266,19 +271,16 @@ __device__ void xs_run(View& v, const XsGeom& g, int rb, int sl, __half* xlds, u
     }
   }
   if constexpr (LORA) {
-    if (sl == 0 && v.lora()) {  // a SV^T (uniform)
+    if (lw) {  // a SV^T (uniform): its loads in one round trip after the K loop
+      v.lora_issue(row, li, kb);
+      f32x4 acc[M2];
 #pragma unroll
       for (int m = 0; m < M2; ++m) {
-        const __half* svr = v.sv(m, row);
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const int c = 32 * s + 8 * kb;
-          const f16x8 b = c < v.rank() ? *(const f16x8*)(svr + c) : f16x8{};
-          acc = mfma_16x16x32(v.a_frag(m, li, s, kb), b, acc);
-        }
+        for (int s = 0; s < 2; ++s) acc[m] = mfma_16x16x32(v.a_frag(m, li, s, kb), v.sv_frag(m, s), acc[m]);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) yv[m][q] += acc[q];
+        for (int q = 0; q < 4; ++q) yv[m][q] += acc[m][q];
       }
     }
   }
