@@ -997,20 +997,20 @@ __global__ __launch_bounds__(kXguWaves * 64) void moe_lane_gu_xt_kernel(MoeLaneA
       v, a.gXgu, rb, 0, (__half*)sm, (uint32_t*)(sm + xs_lds_bytes(kXsChunk)));
 }
 
-// Routed down in the streamed token-tile form: the a_down jobs first (as
-// moe_lane_down_kernel's), then workgroup (e, row block, K slice) of every
-// expert, each slice stored apart.
+// Routed down in the streamed token-tile form: workgroup (e, row block, K
+// slice) of every expert, each slice stored apart, then the a_down jobs (as
+// moe_lane_down_kernel's).
 __global__ __launch_bounds__(kMoeLaneThreads) void moe_lane_down_xt_kernel(MoeLaneArgs a) {
   extern __shared__ __align__(16) float lds[];
   __shared__ int xl[16];
-  const int nad = a.rank > 0 && a.SV[2] != nullptr ? a.B * a.topk * a.sd : 0;
-  if ((int)blockIdx.x < nad) {
-    const float* sums = moe_lane_adown_part(a, blockIdx.x, lds);
-    if ((int)threadIdx.x < a.rank)
-      a.ad[(int64_t)blockIdx.x * a.rank + threadIdx.x] = sums[threadIdx.x];
+  const int per = a.gXd.RB * a.gXd.ks, ntile = a.E * per;
+  if ((int)blockIdx.x >= ntile) {  // the a_down jobs last: they fill the tiles' last round
+    const int j = blockIdx.x - ntile;
+    const float* sums = moe_lane_adown_part(a, j, lds);
+    if ((int)threadIdx.x < a.rank) a.ad[(int64_t)j * a.rank + threadIdx.x] = sums[threadIdx.x];
     return;
   }
-  const int b = blockIdx.x - nad, per = a.gXd.RB * a.gXd.ks, e = b / per;
+  const int b = blockIdx.x, e = b / per;
   const int rb = (b - e * per) / a.gXd.ks, sl = (b - e * per) - rb * a.gXd.ks;
   XdView v{a, e, xl, {}};
   unsigned char* sm = (unsigned char*)lds;  // x chunks, transposition areas
