@@ -23,7 +23,7 @@ step's to the fp32 summation order of a.
 Also reported: the MoE block decode step of config 2 at B = 1, 4, 16, 32
 (microseconds per step and per token under hipGraph replay, achieved GB/s on
 the step's algorithmic bytes), single-call latency of config 0 (one layer,
-both launches), and
+one launch; eager and per call in a hipGraph), and
 the CPU baseline = the reference's CPU fallback restated in oracle/ (fp16
 dequant loop + fp16 x@W.T + fp16 LoRA) on config 0, timed on the host cores;
 its output doubles as the parity check of the GPU result for the same input.
@@ -36,6 +36,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --model-only [--model-layers L] [--model-batches 1,16]
        python bench.py --turbo-step-only [--turbo-batches 1]   (the TurboQuant-
                                          expert MoE step, then 5 eager steps)
+       python bench.py --single-only   (config-0 single calls, eager and in a
+                                        hipGraph)
 """
 
 from __future__ import annotations
@@ -105,6 +107,49 @@ def time_events(fn, steps, warmup):
     end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
+
+
+def bench_single(dev, calls=200):
+    """Config 0 (one layer, one token row, x U from U in the launch): mean µs
+    per call over `calls` back-to-back eager calls (HIP events, host launch
+    cost included), and per call of 100 calls captured in one hipGraph (the
+    best of 5 replays)."""
+    import torch
+
+    from glorcq_amd import format as fmt
+    from glorcq_amd import kernels
+
+    p0 = fmt.make_linear(K_, N_, bits=BITS, group=GROUP, rank=RANK, M=M_, seed=0)
+    d0 = [t.to(dev) for t in (p0.x, p0.codes, p0.scales, p0.zeros, p0.U, p0.SV)]
+    y0 = torch.empty(M_, N_, dtype=torch.float16, device=dev)
+
+    def single():
+        kernels.packed_dequant_matmul_fused(d0[0], d0[1], d0[2], d0[3], BITS, GROUP, U=d0[4],
+                                            SV=d0[5], out=y0)
+
+    eager_ms = time_events(single, calls, 20)
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            single()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(100):
+            single()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(5):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / 100)
+    return {"single_call_config0_us": round(eager_ms * 1e3, 2),
+            "single_call_config0_graph_us": round(best, 2)}
 
 
 def cpu_model_name():
@@ -657,6 +702,8 @@ def main():
                     help="run only the TurboQuant-expert MoE step leg, then 5 eager steps, "
                          "and print its JSON (profiling)")
     ap.add_argument("--turbo-batches", default="1")
+    ap.add_argument("--single-only", action="store_true",
+                    help="run only the config-0 single-call leg and print its JSON (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (every box here has one); "
@@ -668,6 +715,13 @@ def main():
         return 0
     if args.pmc_workload:
         pmc_workload()
+        return 0
+    if args.single_only:
+        import torch
+
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        print(json.dumps(bench_single(dev)), flush=True)
         return 0
     if args.turbo_step_only:
         import torch
@@ -738,18 +792,8 @@ def main():
     diff = (out.float() - out2.float()).abs()
     agree = bool((diff <= 1e-4 + 2e-3 * out2.float().abs()).all())
 
-    # single-call latency, config 0 (one layer: both launches)
-    p0 = fmt.make_linear(K_, N_, bits=BITS, group=GROUP, rank=RANK, M=M_, seed=0)
-    d0 = [t.to(dev) for t in (p0.x, p0.codes, p0.scales, p0.zeros, p0.U, p0.SV)]
-    y0 = torch.empty(M_, N_, dtype=torch.float16, device=dev)
-
-    def single():
-        kernels.packed_dequant_matmul_fused(d0[0], d0[1], d0[2], d0[3], BITS, GROUP, U=d0[4],
-                                            SV=d0[5], out=y0)
-
     log("timing single calls")
-    single_ms = time_events(single, 200, 20)
-    torch.cuda.synchronize()
+    single = bench_single(dev)
 
     result = {
         "metric": METRIC,
@@ -787,7 +831,8 @@ def main():
             "matches_step_output": agree,
             "max_abs_diff": float(diff.max()),
         },
-        "single_call_config0_us": round(single_ms * 1e3, 2),
+        "single_call_config0_us": single["single_call_config0_us"],
+        "single_call_config0_graph_us": single["single_call_config0_graph_us"],
     }
     log("prefill GEMM (config 1, M = 128 and 512)")
     result["prefill_gemm"] = bench_prefill(dev)

@@ -65,6 +65,15 @@ struct DenseArgs {
   float* xt_part = nullptr;  // (items, P, M, rpad) slice partials
   __half* xt_a = nullptr;    // (items, M, rank)
   uint64_t xt_spin = 0;
+  // a = x U of the one-token lane launch handed over by xj jobs an item
+  // (lane_xj_job: K slices of kLowrankRows rows) in front of the grid, into
+  // xt_part (items, xj, rank) as bit-inverted words (0: not yet written);
+  // xt_cnt[i] counts the jobs (1 each) and the row workgroups (xt_rb an
+  // item, 1 << 16 each) done with item i's words, and the last of them
+  // clears the words: both zero between launches.  xj = 0: every row
+  // workgroup forms a itself.
+  int xj = 0;
+  int xj_jobs = 0;
   __device__ int64_t u_index(int item) const {
     return uidx ? (int64_t)min(max(uidx[item], 0), nuidx - 1) : (int64_t)item;
   }
@@ -134,6 +143,10 @@ struct DenseLaneItem {
   __device__ void store(int n, float v) const {
     a.y[(int64_t)item * a.y_es + n] = __float2half(v);
   }
+  // with x U jobs in the XU launch: a = fp16(x U) in LDS from their sums
+  // (lane_run calls it after the first round's quantized sums)
+  __device__ bool xu_defer() const { return a.xj > 0 && lora(); }
+  __device__ __half* xu_wait(int K, int rank, float* xu_lds) const;
 };
 struct DenseLaneSrc {
   const DenseArgs& a;
@@ -324,14 +337,127 @@ __global__ __launch_bounds__(kT16Waves * 64) void gemv_t16_kernel(DenseArgs a, T
                                      lds);
 }
 
-template <int BITS, bool SYM, int LRP, int NP, int PD, int NSV, bool HASB, bool XU>
+constexpr int kLaneXjMax = 16;  // x U jobs an item (K up to 16 kLowrankRows)
+
+// Item's counter: jobs add 1 once their words are stored, row workgroups
+// 1 << 16 once they have read them; the last of all clears the item's words
+// and the counter (threads t, t + n, ... of the caller).
+__device__ __forceinline__ unsigned lane_xj_final(const DenseArgs& a) {
+  return ((unsigned)a.xt_rb << 16) | (unsigned)a.xj;
+}
+__device__ void lane_xj_clear(const DenseArgs& a, int item, int t, int n) {
+  uint32_t* w = (uint32_t*)a.xt_part + (int64_t)item * a.xj * a.sh.rank;
+  for (int i = t; i < a.xj * a.sh.rank; i += n) handoff_put(w + i, 0u);
+  if (t == 0) handoff_reset(a.xt_cnt + item);
+}
+
+// x U job `job` of the lane launch (512 threads): item job / xj, K rows
+// [kLowrankRows j, kLowrankRows (j + 1)) of j = job % xj summed by
+// lane_xu_sum; the rank fp32 sums handed over bit-inverted (a word of the
+// partials is 0 until its job writes it: no sum has the bits 0xffffffff,
+// a NaN payload that fp16 inputs cannot give), then the arrival that counts
+// the workgroups done with the words.
+__device__ void lane_xj_job(const DenseArgs& a, int job, float* xu_lds) {
+  const int item = job / a.xj, j = job - item * a.xj, rank = a.sh.rank;
+  const int k0 = j * kLowrankRows;
+  const float* s = lane_xu_sum(DenseLaneItem{a, item}, k0, min(kLowrankRows, a.sh.K - k0), rank,
+                               xu_lds);
+  uint32_t* part = (uint32_t*)a.xt_part + ((int64_t)item * a.xj + j) * rank;
+  if ((int)threadIdx.x < rank) handoff_put(part + threadIdx.x, ~__float_as_uint(s[threadIdx.x]));
+  __shared__ int last;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(a.xt_cnt + item, 1u, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT) + 1u == lane_xj_final(a);
+  __syncthreads();
+  if (last) lane_xj_clear(a, item, threadIdx.x, blockDim.x);
+}
+
+// a from the x U jobs: the workgroup polls the item's xj x rank words
+// (thread t words t + 512 q) until none is 0 and stages the sums in LDS, and
+// each of the first rank threads sums its column in slice order
+// (sum_strided's order and zeros); a wait that outlasts xt_spin has the
+// workgroup form the slices with the jobs' code and sum them in the same
+// order (the same bits).
+__device__ __half* DenseLaneItem::xu_wait(int K, int rank, float* xu_lds) const {
+  __shared__ int fail;
+  const LaneXu L(rank);
+  __half* ah = (__half*)(xu_lds + L.ks * rank + L.nseg * rank);
+  const int t = threadIdx.x, n = a.xj, nw = n * rank;  // nw <= ks rank (4096 floats)
+  if (t == 0) fail = 0;
+  __syncthreads();
+  {
+    const uint32_t* w = (const uint32_t*)a.xt_part + (int64_t)item * nw;
+    constexpr int Q = kLaneXjMax * 128 / 512;  // words a thread (rank <= 128)
+    uint32_t b[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) b[q] = t + 512 * q < nw ? handoff_get(w + t + 512 * q) : 1u;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+      bool all = a.xt_spin > 0;  // a bound of 0: no wait (the slices formed here)
+#pragma unroll
+      for (int q = 0; q < Q; ++q) all = all && b[q] != 0u;
+      if (all) break;
+      if (__builtin_amdgcn_s_memrealtime() - t0 >= a.xt_spin) {
+        fail = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int q = 0; q < Q; ++q)
+        if (b[q] == 0u) b[q] = handoff_get(w + t + 512 * q);
+    }
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+      if (t + 512 * q < nw) xu_lds[t + 512 * q] = __uint_as_float(~b[q]);
+  }
+  __syncthreads();
+  float acc = 0.f;
+  if (t < rank)
+    for (int q = 0; q < n; ++q) acc += xu_lds[q * rank + t];
+  __syncthreads();
+  if (fail) {
+    acc = 0.f;
+    for (int j = 0; j < n; ++j) {
+      const int k0 = j * kLowrankRows;
+      const float* s = lane_xu_sum<DenseLaneItem, 0>(*this, k0, min(kLowrankRows, K - k0), rank,
+                                                      xu_lds);
+      if (t < rank) acc += s[t];
+      __syncthreads();  // the next slice rewrites s
+    }
+  }
+  for (int z = n; z % 8; ++z) acc += 0.f;  // sum_strided's zeros after the last batch
+  if (t < rank) ah[t] = __float2half(acc);
+  __syncthreads();
+  if (t < 64) {  // wave 0: this workgroup is done with the item's words (the others go on)
+    unsigned old = 0;
+    if (t == 0)
+      old = __hip_atomic_fetch_add(a.xt_cnt + item, 1u << 16, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    old = __shfl(old, 0);
+    if (old + (1u << 16) == lane_xj_final(a)) lane_xj_clear(a, item, t, 64);
+  }
+  return ah;
+}
+
+// XJ (with XU): the x U jobs come first, then the row workgroups.
+template <int BITS, bool SYM, int LRP, int NP, int PD, int NSV, bool HASB, bool XU, bool XJ>
 __global__ __launch_bounds__(XU ? 512 : 256) void gemv_lane_kernel(LaneArgs la) {
   extern __shared__ float xu_lds[];
   constexpr int WPB = XU ? 8 : 4;  // waves per workgroup
+  int b = blockIdx.x;
+  if constexpr (XJ) {
+    if (b < la.a.xj_jobs) {  // (uniform)
+      lane_xj_job(la.a, b, xu_lds);
+      return;
+    }
+    b -= la.a.xj_jobs;
+  }
   const DenseLaneSrc src{la.a};
   const int wvb = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  lane_run<DenseLaneSrc, BITS, SYM, LRP, NP, PD, NSV, HASB, XU>(src, la.g, blockIdx.x * WPB + wvb,
-                                                                wvb, xu_lds);
+  lane_run<DenseLaneSrc, BITS, SYM, LRP, NP, PD, NSV, HASB, XU, false, XJ>(
+      src, la.g, b * WPB + wvb, wvb, xu_lds);
 }
 
 
@@ -411,13 +537,16 @@ static int64_t workspace_need(int64_t items, int64_t M, int64_t K, int64_t rank)
   return align_up(items * lowrank_slices(K) * M * rpad * 4, 256);
 }
 
-// The GEMV entry points' workspace: kGemvSyncBytes of counter words (zero
-// before the first call, left zero by every call), the x U partials, and
-// the token-tile form's a (items x M x rank fp16).
+// The GEMV entry points' workspace: kGemvSyncBytes of counter words and
+// kLaneXjBytes of the lane launch's x U words (both zero before the first
+// call and left zero by every call; no other form writes them), the x U
+// partials, and the token-tile form's a (items x M x rank fp16).
 constexpr int64_t kGemvSyncBytes = 4096;
+constexpr int64_t kLaneXjBytes = 64 << 10;
+constexpr int64_t kGemvHeadBytes = kGemvSyncBytes + kLaneXjBytes;
 static int64_t gemv_workspace_need(int64_t items, int64_t M, int64_t K, int64_t rank) {
   if (rank <= 0) return 0;
-  return kGemvSyncBytes + workspace_need(items, M, K, rank) + align_up(items * M * rank * 2, 256);
+  return kGemvHeadBytes + workspace_need(items, M, K, rank) + align_up(items * M * rank * 2, 256);
 }
 
 // Codes per K-phase: the whole K when x fits the staging budget, else the
@@ -614,18 +743,28 @@ template <int BITS, bool SYM, int LRP, int NP, int NSV, bool HASB>
 static int launch_lane_k(const LaneArgs& la, bool xu, hipStream_t s) {
   const int64_t waves = (int64_t)la.g.items * la.g.wpi;
   if (xu) {
-    const int64_t grid = waves / 8;  // wpi is a multiple of 8
+    const int64_t grid = waves / 8 + la.a.xj_jobs;  // wpi is a multiple of 8
     GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
     const size_t lds = lane_xu_lds(la);
-    static size_t attr = 64 * 1024;
-    int rc = set_lds_limit(gemv_lane_kernel<BITS, SYM, LRP, NP, kLanePD, NSV, HASB, true>, lds, attr);
-    if (rc) return rc;
-    gemv_lane_kernel<BITS, SYM, LRP, NP, kLanePD, NSV, HASB, true>
-        <<<dim3((unsigned)grid), dim3(512), lds, s>>>(la);
+    if (la.a.xj > 0) {
+      static size_t attr_j = 64 * 1024;
+      int rc = set_lds_limit(gemv_lane_kernel<BITS, SYM, LRP, NP, kLanePD, NSV, HASB, true, true>,
+                             lds, attr_j);
+      if (rc) return rc;
+      gemv_lane_kernel<BITS, SYM, LRP, NP, kLanePD, NSV, HASB, true, true>
+          <<<dim3((unsigned)grid), dim3(512), lds, s>>>(la);
+    } else {
+      static size_t attr = 64 * 1024;
+      int rc = set_lds_limit(gemv_lane_kernel<BITS, SYM, LRP, NP, kLanePD, NSV, HASB, true, false>,
+                             lds, attr);
+      if (rc) return rc;
+      gemv_lane_kernel<BITS, SYM, LRP, NP, kLanePD, NSV, HASB, true, false>
+          <<<dim3((unsigned)grid), dim3(512), lds, s>>>(la);
+    }
   } else {
     const int64_t grid = (waves + 3) / 4;
     GLQ_CHECK(grid < (1ll << 31), "too many workgroups");
-    gemv_lane_kernel<BITS, SYM, LRP, NP, kLanePD, NSV, HASB, false>
+    gemv_lane_kernel<BITS, SYM, LRP, NP, kLanePD, NSV, HASB, false, false>
         <<<dim3((unsigned)grid), dim3(256), 0, s>>>(la);
   }
   GLQ_LAUNCH_CHECK("gemv_lane_kernel");
@@ -686,6 +825,8 @@ static int launch_lane(const DenseArgs& a, int bits, bool xu, hipStream_t s) {
   if (xu) {  // whole 8-wave workgroups per item, the rounds spread over all of them
     g.wpi = (g.wpi + 7) / 8 * 8;
     g.rpw = (g.rounds + g.wpi - 1) / g.wpi;
+    la.a.xt_rb = g.wpi / 8;
+    la.a.xj_jobs = la.a.xj * a.items;
   }
   return bits == 2 ? launch_lane_bits<2>(la, xu, s) : launch_lane_bits<4>(la, xu, s);
 }
@@ -811,9 +952,9 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
   a.y_es = y_stride;
   a.xu = lora ? (const __half*)xU : nullptr;
   a.xu_es = xu_stride;
-  // workspace: kGemvSyncBytes of counter words (zero between calls), then
-  // the x U partials (and the token-tile form's a)
-  a.apart = need_partials && !lane_xu ? (const float*)((char*)workspace + kGemvSyncBytes)
+  // workspace: the counter words and the lane launch's x U words (zero
+  // between calls), then the x U partials (and the token-tile form's a)
+  a.apart = need_partials && !lane_xu ? (const float*)((char*)workspace + kGemvHeadBytes)
                                       : parts;
   a.items = (int)items;
   a.M = (int)M;
@@ -827,13 +968,32 @@ static int gemv_impl(int64_t items, const void* x, int64_t x_stride, int64_t M,
 
   GLQ_CHECK(items * a.tiles < (1ll << 31) && items * a.P < (1ll << 31), "too many workgroups");
   hipStream_t s = (hipStream_t)stream;
-  if (lane_xu) return launch_lane(a, bits, true, s);
+  if (lane_xu) {
+    // x U in K slices by jobs in front of the launch when the workspace
+    // holds their counters and sums (GLQ_LANE_XJ=0: each row workgroup
+    // forms a over the whole row)
+    const char* xj = getenv("GLQ_LANE_XJ");
+    if (workspace != nullptr && ((uintptr_t)workspace & 255) == 0 &&
+        workspace_bytes_given >= gemv_workspace_need(items, M, K, rank) &&
+        items <= kGemvSyncBytes / 4 && lowrank_slices(K) <= kLaneXjMax &&
+        items * lowrank_slices(K) * rank * 4 <= kLaneXjBytes &&
+        !(xj && atoi(xj) == 0)) {
+      a.xj = (int)lowrank_slices(K);
+      a.xt_cnt = (unsigned*)workspace;
+      a.xt_part = (float*)((char*)workspace + kGemvSyncBytes);
+      // GLQ_LANE_SPIN_TICKS: the row workgroups' wait bound (tests set 0 to
+      // take the local x U)
+      const char* e = getenv("GLQ_LANE_SPIN_TICKS");
+      a.xt_spin = e ? (uint64_t)strtoull(e, nullptr, 10) : 100000;  // 1 ms
+    }
+    return launch_lane(a, bits, true, s);
+  }
   if (t16_xu) {
     a.xt_jobs = (int)(items * ((a.P + 1) / 2));
     a.xt_rb = (int)((N + kT16Rows - 1) / kT16Rows);
     a.xt_cnt = (unsigned*)workspace;
     a.xt_part = (float*)a.apart;
-    a.xt_a = (__half*)((char*)workspace + kGemvSyncBytes + workspace_need(items, M, K, rank));
+    a.xt_a = (__half*)((char*)workspace + kGemvHeadBytes + workspace_need(items, M, K, rank));
     // GLQ_T16_SPIN_TICKS: the stores' wait bound (tests set 0 to take the
     // local x U)
     const char* e = getenv("GLQ_T16_SPIN_TICKS");

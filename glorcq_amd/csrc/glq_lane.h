@@ -124,7 +124,10 @@ struct LaneXu {
 // row pairs into fp32, the partials summed in LDS in a fixed order.  Returns
 // the sums' LDS copy (rank floats); every thread of the workgroup must call
 // it (it holds barriers).
-template <class View>
+// DEPTH: 8-row chunks in flight per thread (0: one row pair at a time, for
+// callers short of registers; every DEPTH gives the same sums in the same
+// order).
+template <class View, int DEPTH = 2>
 __device__ float* lane_xu_sum(const View& src, int k0, int kn, int rank, float* xu_lds) {
   const LaneXu L(rank);
   const int t = threadIdx.x;
@@ -154,15 +157,38 @@ __device__ float* lane_xu_sum(const View& src, int k0, int kn, int rank, float* 
         }
       }
     };
-    // two chunks in flight: slot, slot + ks, ...; a slot at or past the last
-    // chunk adds nothing
-    load(slot, u0, x0);
-    for (int c = slot; c < nch; c += 2 * L.ks) {
-      load(c + L.ks, u1, x1);
-      fma_chunk(u0, x0);
-      if (c + L.ks >= nch) break;
-      load(c + 2 * L.ks, u0, x0);
-      fma_chunk(u1, x1);
+    // chunks slot, slot + ks, ... (two in flight); a slot at or past the
+    // last chunk adds nothing
+    if constexpr (DEPTH == 0) {
+      for (int c = slot; c < nch; c += L.ks) {
+        const u32x4 xv = src.x8(k0 + 8 * c);
+#pragma unroll 1
+        for (int i = 0; i < 4; ++i) {  // rows 2i, 2i + 1: fma_chunk's steps for i
+          const u32x4 ua = *(const u32x4*)(ub + (int64_t)(8 * c + 2 * i) * rank);
+          const u32x4 uc = *(const u32x4*)(ub + (int64_t)(8 * c + 2 * i + 1) * rank);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t lo = __builtin_amdgcn_perm(uc[j], ua[j], 0x05040100u);
+            const uint32_t hi = __builtin_amdgcn_perm(uc[j], ua[j], 0x07060302u);
+            acc[2 * j] = dot2(lo, xv[i], acc[2 * j]);
+            acc[2 * j + 1] = dot2(hi, xv[i], acc[2 * j + 1]);
+          }
+        }
+      }
+    } else if constexpr (DEPTH == 1) {
+      for (int c = slot; c < nch; c += L.ks) {
+        load(c, u0, x0);
+        fma_chunk(u0, x0);
+      }
+    } else {
+      load(slot, u0, x0);
+      for (int c = slot; c < nch; c += 2 * L.ks) {
+        load(c + L.ks, u1, x1);
+        fma_chunk(u0, x0);
+        if (c + L.ks >= nch) break;
+        load(c + 2 * L.ks, u0, x0);
+        fma_chunk(u1, x1);
+      }
     }
 #pragma unroll
     for (int c = 0; c < 8; ++c) part[slot * rank + 8 * b + c] = acc[c];
@@ -215,6 +241,7 @@ struct lane_hook : std::false_type {};
 template <class T>
 struct lane_hook<T, std::void_t<decltype(&T::after_issue)>> : std::true_type {};
 
+
 // sum_strided's sum of n <= kLaneEarlyA loaded partials (its zeros included)
 __device__ __forceinline__ float lane_early_sum(const float (&v)[kLaneEarlyA]) {
   float s = 0.f;
@@ -262,8 +289,14 @@ struct LaneGeom {
 // partials are summed in LDS in a fixed order and rounded to fp16 once.
 // Then the waves take their x slices and stream their rows.  An item whose
 // rows are spread over several workgroups has each of them form a.
+//
+// DEFER (with XU): a is formed elsewhere in the launch.  When the item's
+// xu_defer() is true, each wave sums its first round without the low-rank
+// term, then the workgroup calls the item's xu_wait(K, rank, xu_lds) (every
+// thread; it returns a's fp16 LDS copy at lane_xu_phase's place in xu_lds),
+// and the round is finished with the same operations in the same order.
 template <class Src, int BITS, bool SYM, int LRP, int NP, int PD, int NSV, bool HASB, bool XU,
-          bool PAIR = false>
+          bool PAIR = false, bool DEFER = false>
 __device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, int wv, int wvb,
                                          float* xu_lds) {
   constexpr int C = lane_piece_codes<BITS>();  // codes per piece
@@ -441,10 +474,7 @@ __device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, in
 
   // ---- a pairs of this lane's SV dwords (zero past the rank) ----
   uint32_t ap[M2][NSV];
-  if constexpr (XU) {
-    // the rows' first loads go out before the x U phase and arrive under it
-    if (nr > 0) prologue();
-    __half* ah = lane_xu_phase(src, lg.K, rank, lora, xu_lds);
+  auto set_ap = [&](const __half* ah) {
 #pragma unroll
     for (int k = 0; k < NSV; ++k) {
       const int j = p + k * LRP;
@@ -455,8 +485,19 @@ __device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, in
       }
       ap[0][k] = __builtin_bit_cast(uint32_t, pr);
     }
-    if (nr <= 0) return;  // a wave with no rows of its own
-    load_x();
+  };
+  // DEFER: a handed over by other workgroups (the item's xu_defer()); the
+  // wave's first round is summed before a is waited for (below)
+  bool defer = false;
+  if constexpr (XU) {
+    // the rows' first loads go out before the x U phase and arrive under it
+    if (nr > 0) prologue();
+    if constexpr (DEFER) defer = src.xu_defer();
+    if (!defer) {
+      set_ap(lane_xu_phase(src, lg.K, rank, lora, xu_lds));
+      if (nr <= 0) return;  // a wave with no rows of its own
+    }
+    if (nr > 0) load_x();
   } else {
 #pragma unroll
     for (int m = 0; m < M2; ++m)
@@ -487,7 +528,90 @@ __device__ __forceinline__ void lane_run(const Src& srcs, const LaneGeom& lg, in
 
   const DecodeConsts dk = DecodeConsts::make();
   constexpr uint32_t xor_mask = SYM ? (BITS == 2 ? 0xAAAAAAAAu : 0x88888888u) : 0u;
-  for (int r = 0; r < nr; ++r) {
+  int r0 = 0;
+  if constexpr (XU && DEFER) {
+    if (defer) {
+      // the quantized sum (and bias) of this lane's pieces of iteration d
+      // (the loop's steps below)
+      auto qpart = [&](int d) {
+        float part = 0.f;
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+          u32x4 w = cw[d][j];
+          if constexpr (SYM) w ^= xor_mask;
+          float acc0 = -c1[j], acc1 = 0.f;  // the operand bias leaves with c1
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            if constexpr (BITS == 2) {
+              u32x4 da, db;
+              decode2_words(w[k], da, db, dk);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                acc0 = dot2(da[q], xw[j][8 * k + q], acc0);
+                acc1 = dot2(db[q], xw[j][8 * k + 4 + q], acc1);
+              }
+            } else {
+              u32x4 da;
+              decode4_words(w[k], da, dk);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                if (q & 1) acc1 = dot2(da[q], xw[j][4 * k + q], acc1);
+                else acc0 = dot2(da[q], xw[j][4 * k + q], acc0);
+              }
+            }
+          }
+          const float s = __half2float(__ushort_as_half((uint16_t)sw[d][j]));
+          float z = (float)(1 << (BITS - 1));
+          if constexpr (!SYM) z = __half2float(__ushort_as_half((uint16_t)zw[d][j]));
+          part = fmaf(s, (acc0 + acc1) - z * c2[j], part);
+        }
+        if constexpr (HASB) part = fmaf(bsel, __half2float(__ushort_as_half((uint16_t)bw[d])), part);
+        return part;
+      };
+      // lane l holds row (l % LRP) * RPI + l / LRP of the unit; the lanes of
+      // round r's row groups store
+      auto store_round = [&](int r, float yv, float yu) {
+        constexpr int RG = PAIR ? PD / 2 : PD;  // row groups per round
+        const int i0 = (rb + r) * PD;
+        const int g0 = PAIR ? i0 >> 1 : i0;
+        const int u = g0 / NIT, it0 = g0 & (NIT - 1);
+        const int n = u * 64 + p * RPI + ri;
+        if (p >= it0 && p < it0 + RG && n < N) {
+          if constexpr (PAIR) src.store(n, yv, yu);
+          else src.store(n, yv);
+        }
+      };
+      // round 0 without the low-rank term; then a (the whole workgroup),
+      // the term, the next round's loads, the sums and the stores -- the
+      // same operations in the same order as the loop below
+      float pt[PD];
+      if (nr > 0) {
+#pragma unroll
+        for (int d = 0; d < PD; ++d) pt[d] = qpart(d);
+      }
+      set_ap(src.xu_wait(lg.K, rank, xu_lds));
+      if (nr <= 0) return;  // a wave with no rows of its own
+      float yv = 0.f;
+#pragma unroll
+      for (int d = 0; d < PD; ++d) {
+        float part = pt[d];
+#pragma unroll
+        for (int k = 0; k < NSV; ++k) part = dot2(vw[d][k], ap[0][k], part);
+        if (nr > 1) {  // (a single round reads nothing more)
+          __builtin_amdgcn_sched_barrier(0);
+          issue(d, 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        const float tot = lane_group_sum<LRP>(part);
+        yv = p == ((rb * PD + d) & (NIT - 1)) ? tot : yv;
+      }
+      store_round(0, yv, 0.f);
+      // x again for later rounds (its registers were free over the wait)
+      if (nr > 1) load_x();
+      r0 = 1;
+    }
+  }
+  for (int r = r0; r < nr; ++r) {
     const int i0 = (rb + r) * PD;  // first iteration of the round
     float yv = 0.f, yu = 0.f;      // (PAIR: matrix 0 and matrix 1 of a row)
 #pragma unroll

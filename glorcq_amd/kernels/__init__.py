@@ -144,8 +144,9 @@ def gemm_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 
 def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Workspace of the glq_gemv_lora* entry points, one per (device, current
-    stream), zero-filled and for them alone: its first 4096 bytes are the
-    token-tile launch's x U arrival counters, zero between calls."""
+    stream), zero-filled and for them alone: its first 69632 bytes (the
+    token-tile launch's x U arrival counters, the one-row launch's x U job
+    counters and K-slice sums) are zero between calls."""
     return _zeroed_buffer(_gemv_workspaces, device, nbytes)
 
 

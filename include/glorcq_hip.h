@@ -58,12 +58,14 @@ const char* glq_last_error(void);
 /*
  * Bytes of workspace glq_gemv_lora / glq_gemv_lora_batched need for `items`
  * independent problems of shape (M, K, N, rank) when they compute a = x U
- * themselves (0 when rank == 0).  Its first 4096 bytes are arrival counters
- * (the 4..16-row token-tile launch forms a = x U in its own first
- * workgroups and hands it to the rest): they must be zero before the
- * workspace's first use with these entry points (allocate it zero-filled),
- * every call leaves them zero, and the buffer must serve no other entry
- * point.  The rest holds fp32 partial sums of a over K-slices of U and needs
+ * themselves (0 when rank == 0).  Its first 69632 bytes are arrival
+ * counters (4096 bytes) and the one-token-row launch's x U words (64 KiB):
+ * the 4..16-row token-tile launch forms a = x U in its own first workgroups
+ * and hands it to the rest, and the one-row launch has jobs in front of its
+ * grid form K-slice sums of a that its row workgroups read.  They must be
+ * zero before the workspace's first use with these entry points (allocate
+ * it zero-filled), every call leaves them zero, and the buffer must serve no
+ * other entry point.  The rest holds fp32 partial sums of a over K-slices of U and needs
  * no initialisation.  Calls that may run concurrently (different streams)
  * need different workspaces.
  */

@@ -348,6 +348,84 @@ def test_lane_path_batched_items(gpu, monkeypatch):
         assert_parity(y[e], oracle_y(p), f"item {e}")
 
 
+@pytest.mark.parametrize("bits,K,N,rank,items", [
+    (2, 2048, 1408, 64, 1),   # config 0: 8 K slices
+    (2, 1408, 1462, 40, 1),   # a last slice of 128 rows, rank 40
+    (4, 4096, 448, 128, 1),   # 16 slices, rank 128
+    (2, 512, 130, 8, 1),      # 2 slices, rank 8
+    (2, 2048, 1408, 64, 9),   # 9 items: 72 jobs, one counter an item
+])
+def test_lane_xu_jobs(gpu, monkeypatch, bits, K, N, rank, items):
+    """a = x U of the one-token-row launch formed by job workgroups in front
+    of the grid (one 256-row K slice each, handed over) and summed in slice
+    order by every row workgroup: against the oracle; against the launch
+    whose row workgroups each form a over the whole row (GLQ_LANE_XJ=0,
+    another fp32 order); bit-equal to row workgroups whose wait is bounded
+    at zero ticks (GLQ_LANE_SPIN_TICKS=0: the slices formed locally in the
+    same order) and to calls after those (the counters left zero)."""
+    ps = [fmt.make_linear(K, N, bits=bits, rank=rank, M=1, seed=K + N + rank + e)
+          for e in range(items)]
+    st = lambda k: torch.stack([getattr(p, k) for p in ps]).to(gpu)  # noqa: E731
+    args = (st("x"), st("codes"), st("scales"), st("zeros"), bits, 128)
+
+    def call():
+        y = K_.packed_dequant_matmul_batched(*args, U=st("U"), SV=st("SV"))
+        torch.cuda.synchronize()
+        return y
+
+    for v in ("GLQ_LANE_XJ", "GLQ_LANE_SPIN_TICKS", "GLQ_LANE_NO_XU"):
+        monkeypatch.delenv(v, raising=False)
+    y = call()
+    for e, p in enumerate(ps):
+        assert_parity(y[e], oracle_y(p), f"x U jobs item {e}")
+    monkeypatch.setenv("GLQ_LANE_SPIN_TICKS", "0")
+    y0 = call()
+    monkeypatch.delenv("GLQ_LANE_SPIN_TICKS")
+    assert torch.equal(y, y0), "zero-tick wait"
+    monkeypatch.setenv("GLQ_LANE_XJ", "0")
+    yw = call()
+    monkeypatch.delenv("GLQ_LANE_XJ")
+    assert torch.equal(y, call()), "x U jobs after the local runs"
+    # the two differ only in the fp32 summation order of a = x U
+    assert bool(((y.float() - yw.float()).abs() <= 1e-4 + 2e-3 * yw.float().abs()).all())
+
+
+def test_lane_xu_jobs_graph_replays(gpu):
+    """The one-token-row call with x U jobs captured in a HIP graph on a side
+    stream (its own zero-filled workspace): replays with eager calls on the
+    capture stream between them all match the eager result."""
+    p = fmt.make_linear(2048, 1408, bits=2, rank=64, M=1, seed=5)
+    d = to(p, gpu)
+    out = torch.empty(1, 1408, dtype=torch.float16, device=gpu)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+
+    def call(o):
+        K_.packed_dequant_matmul_fused(d["x"], d["codes"], d["scales"], d["zeros"], 2, 128,
+                                       U=d["U"], SV=d["SV"], out=o)
+
+    with torch.cuda.stream(s):
+        call(out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for _ in range(3):
+            call(out)
+    for i in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        with torch.cuda.stream(s):
+            other = torch.empty_like(out)
+            call(other)
+        s.synchronize()
+        assert torch.equal(other, eager), f"eager call after replay {i}"
+
+
 @pytest.mark.parametrize("bits,K,N,rank,sym", [
     (4, 4096, 2048, 64, False),   # config-4 o projection: 128 pieces, two a lane
     (2, 8192, 512, 128, True),    # 2-bit rows of 128 pieces, rank 128, symmetric codes
