@@ -113,7 +113,7 @@ def bench_single(dev, calls=200):
     """Config 0 (one layer, one token row, x U from U in the launch): mean µs
     per call over `calls` back-to-back eager calls (HIP events, host launch
     cost included), and per call of 100 calls captured in one hipGraph (the
-    best of 5 replays)."""
+    best of 5 replays).  Returns the figures and the call's output."""
     import torch
 
     from glorcq_amd import format as fmt
@@ -149,7 +149,7 @@ def bench_single(dev, calls=200):
         torch.cuda.synchronize()
         best = min(best, e0.elapsed_time(e1) * 1e3 / 100)
     return {"single_call_config0_us": round(eager_ms * 1e3, 2),
-            "single_call_config0_graph_us": round(best, 2)}
+            "single_call_config0_graph_us": round(best, 2)}, y0
 
 
 def cpu_model_name():
@@ -721,7 +721,7 @@ def main():
 
         dev = torch.device("cuda:0")
         torch.cuda.set_device(dev)
-        print(json.dumps(bench_single(dev)), flush=True)
+        print(json.dumps(bench_single(dev)[0]), flush=True)
         return 0
     if args.turbo_step_only:
         import torch
@@ -793,7 +793,7 @@ def main():
     agree = bool((diff <= 1e-4 + 2e-3 * out2.float().abs()).all())
 
     log("timing single calls")
-    single = bench_single(dev)
+    single, y0 = bench_single(dev)
 
     result = {
         "metric": METRIC,
