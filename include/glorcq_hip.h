@@ -114,8 +114,9 @@ int glq_gemv_lora(const void* x, int64_t M, int64_t K, int64_t N,
  * when U is used) fail with GLQ_ERR_INVALID.  Every call on one GPU shares
  * that GPU's scratch: calls that may overlap on one GPU (different streams,
  * or different host threads) race and must be ordered by the caller.  The
- * scratch's counter words start at zero (static device memory) and every
- * call leaves them zero; the partials are fully rewritten by each call.
+ * scratch's header (counter words and the one-row launch's x*U words) starts
+ * at zero (static device memory) and every call leaves it zero; the partials
+ * are fully rewritten by each call.
  */
 int64_t glq_gemv_noalloc_max_scratch_bytes(void);
 int glq_gemv_lora_noalloc(const void* x, int64_t M, int64_t K, int64_t N,

@@ -39,12 +39,15 @@ def test_noalloc_matches_workspace_entry_point(gpu):
     # problem (M=4, K=512, rank 64) whose partials reuse the same scratch
     # (a stale first-call partial would change its bits), in the token-tile
     # form whose in-launch x*U counters sit in the scratch's header, twice
-    # (the first call must leave them zero); last: one token row, which forms
-    # x*U inside its own launch and touches no scratch
+    # (the first call must leave them zero); last: one token row twice and a
+    # config-0 row, whose x*U jobs keep their counters and K-slice words in
+    # the scratch's header (each call must leave them zero, or the next one
+    # reads stale words)
     big = fmt.make_linear(1408, 2048, bits=2, rank=128, M=8, seed=71)
     small = fmt.make_linear(512, 640, bits=4, rank=64, M=4, seed=72)
     single = fmt.make_linear(512, 640, bits=4, rank=64, M=1, seed=73)
-    for p in (big, small, small, single):
+    config0 = fmt.make_linear(2048, 1408, bits=2, rank=64, M=1, seed=74)
+    for p in (big, small, small, single, single, config0):
         print(f"noalloc case K={p.K} N={p.N} M={p.x.shape[0]} bits={p.bits} r={p.rank}",
               flush=True)
         y_ref, y_new = _call_pair(lib, gpu, p, stream)
