@@ -107,7 +107,6 @@ __device__ void xs_run(View& v, const XsGeom& g, int rb, int sl, __half* xlds, u
   static_assert(C == 4, "a lane's 32 bytes of a chunk row are one group");
   static_assert(R == 2 || R == 3, "a ring of two or three chunks");
   constexpr int BUFH = C * 16 * kXsRowHalves;
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, kb = lane >> 4;
