@@ -107,9 +107,9 @@ class GLoRCQQwen3Attention(nn.Module):
                                           device=self._U_qkv.device)
             self._qkv = cat
         # The o projection's x U formed by the attention launch itself (its
-        # merging blocks, glq_decode_attention_xu) at up to XU_PRODUCER_MAX_M
-        # tokens, as partials that the projection sums as its a
-        # (glq_gemv_lora_parts).
+        # merging blocks, glq_decode_attention_xu) at XU_PRODUCER_MIN_M ..
+        # XU_PRODUCER_MAX_M tokens, as partials that the projection sums as
+        # its a (glq_gemv_lora_parts).
         o = attn.o_proj
         self._o_xu = (getattr(o, "quant_type", None) == "gptq" and getattr(o, "U", None) is not None
                       and getattr(o, "SV", None) is not None and o.U.is_cuda
@@ -118,17 +118,24 @@ class GLoRCQQwen3Attention(nn.Module):
         self._ws = None   # decode attention workspace (counters stay zero between calls)
         self._ws_key = None
 
-    # Up to this many tokens the decode step forms the projections' x U in the
+    # At this many tokens the decode step forms the projections' x U in the
     # launches that produce their inputs (the input RMSNorm for q/k/v, the
-    # attention for o); from 4 tokens the token-tile GEMV forms it in its own
-    # launch.
+    # attention for o).  At one token the projections' own one-row launches
+    # form it (x U jobs in front of the row workgroups: about 2.8 us a layer
+    # less than the producers' partials); from 4 tokens the token-tile GEMV
+    # forms it in its own launch.
+    XU_PRODUCER_MIN_M = 2
     XU_PRODUCER_MAX_M = 3
+
+    @classmethod
+    def xu_by_producer(cls, B):
+        return cls.XU_PRODUCER_MIN_M <= B <= cls.XU_PRODUCER_MAX_M
 
     def qkv_u(self, B):
         """The (3, K, r) stack of the q/k/v U factors when a decode step of B
         tokens takes its x U partials from the input RMSNorm's launch
         (rmsnorm_xu), else None."""
-        if self._qkv is not None and B <= self.XU_PRODUCER_MAX_M and self._U_qkv.shape[2] % 8 == 0:
+        if self._qkv is not None and self.xu_by_producer(B) and self._U_qkv.shape[2] % 8 == 0:
             return self._U_qkv
         return None
 
@@ -177,7 +184,7 @@ class GLoRCQQwen3Attention(nn.Module):
             kernels.retire_workspace(self._ws)  # a captured graph may still use it
             self._ws = kernels.decode_attention_workspace(qr, lay.keys)
             self._ws_key = (tuple(lay.keys.shape), x.device)
-        if self._o_xu and B <= self.XU_PRODUCER_MAX_M:
+        if self._o_xu and self.xu_by_producer(B):
             o = inner.o_proj
             a, parts = kernels.decode_attention(qr, lay.keys, lay.values, self._len, self.scaling,
                                                 advance=lay.cumulative_length, workspace=self._ws,

@@ -257,16 +257,23 @@ def _models(dev, layers=2):
 
 
 @torch.no_grad()
-@pytest.mark.parametrize("B", [1, 2, 12])
-def test_fused_layers_match_framework_layers(gpu, B):
+@pytest.mark.parametrize("B,producer", [(1, False), (1, True), (2, True), (12, False)])
+def test_fused_layers_match_framework_layers(gpu, monkeypatch, B, producer):
     """The same weights (same seed) with the fused decoder layers and with
     transformers' layer code: a 20-token prefill and 8 decode steps through
     static caches give logits within 1 % of the range and the same greedy
     tokens where the margin allows; the caches agree within fp16 rounding.
-    B = 1 and 2 take x U from the launches that produce the projections'
-    inputs (glq_rmsnorm_xu for q/k/v, glq_decode_attention_xu for o); B = 12
-    the token-tile forms with x U in their own launches."""
+    B = 1 takes x U in the projections' own one-row launches (x U jobs in
+    front of the row workgroups) and, forced, from the launches that produce
+    the projections' inputs (glq_rmsnorm_xu for q/k/v,
+    glq_decode_attention_xu for o), as B = 2 does; B = 12 the token-tile
+    forms with x U in their own launches."""
+    from glorcq_amd import decoder
     from glorcq_amd.graph_wrapper import _static_cache
+
+    if producer:
+        monkeypatch.setattr(decoder.GLoRCQQwen3Attention, "XU_PRODUCER_MIN_M", 1)
+    assert decoder.GLoRCQQwen3Attention.xu_by_producer(B) == producer
 
     cfg, fused, plain = _models(gpu)
     assert type(fused.model.layers[0]).__name__ == "GLoRCQQwen3DecoderLayer"
