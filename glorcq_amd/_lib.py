@@ -253,6 +253,11 @@ def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device=None) -> int:
     """hipStream_t of torch's current stream on `device`."""
+    if _raw_stream is not None and isinstance(device, torch.device) and device.index is not None:
+        return _raw_stream(device.index)  # (the per-call cost of the public form is ~2 us)
     return torch.cuda.current_stream(device).cuda_stream

@@ -114,10 +114,11 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
-def _zeroed_buffer(table: dict, device: torch.device, nbytes: int) -> torch.Tensor:
+def _zeroed_buffer(table: dict, device: torch.device, nbytes: int,
+                   stream: int | None = None) -> torch.Tensor:
     dev = torch.device(device)
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    key = (idx, _lib.stream_handle(dev))
+    key = (idx, _lib.stream_handle(dev) if stream is None else stream)
     ws = table.get(key)
     if ws is None or ws.numel() < nbytes:
         size = max(nbytes, 1 << 16)
@@ -142,12 +143,25 @@ def gemm_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return _zeroed_buffer(_gemm_workspaces, device, nbytes)
 
 
-def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+def gemv_workspace(device: torch.device, nbytes: int, stream: int | None = None) -> torch.Tensor:
     """Workspace of the glq_gemv_lora* entry points, one per (device, current
     stream), zero-filled and for them alone: its first 69632 bytes (the
     token-tile launch's x U arrival counters, the one-row launch's x U job
-    counters and K-slice sums) are zero between calls."""
-    return _zeroed_buffer(_gemv_workspaces, device, nbytes)
+    counters and K-slice sums) are zero between calls.  `stream`: the
+    current stream's handle when the caller has it."""
+    return _zeroed_buffer(_gemv_workspaces, device, nbytes, stream)
+
+
+_gemv_ws_bytes: dict = {}
+
+
+def _gemv_workspace_bytes(lib, items: int, M: int, K: int, N: int, rank: int) -> int:
+    """glq_gemv_workspace_bytes, memoized (a pure function of its sizes)."""
+    key = (items, M, K, N, rank)
+    n = _gemv_ws_bytes.get(key)
+    if n is None:
+        n = _gemv_ws_bytes[key] = lib.glq_gemv_workspace_bytes(items, M, K, N, rank)
+    return n
 
 
 def packed_dequant_matmul_fused(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
@@ -251,8 +265,8 @@ def _packed_dequant_matmul_eager(x: torch.Tensor, codes: torch.Tensor, scales: t
     for m0 in range(0, M, GEMV_MAX_M):
         m1 = min(M, m0 + GEMV_MAX_M)
         mb = m1 - m0
-        nbytes = lib.glq_gemv_workspace_bytes(1, mb, K, N, rank if precomputed_xU is None else 0)
-        ws = gemv_workspace(x.device, nbytes)
+        nbytes = _gemv_workspace_bytes(lib, 1, mb, K, N, rank if precomputed_xU is None else 0)
+        ws = gemv_workspace(x.device, nbytes, stream)
         xu = None if precomputed_xU is None else precomputed_xU[m0:m1]
         rc = lib.glq_gemv_lora(
             x[m0:m1].data_ptr(), mb, K, N, codes.data_ptr(), bits, scales.data_ptr(),
@@ -352,8 +366,9 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
         return out
     xu = precomputed_xU if SV is not None else None
     lib = _lib.load()
-    nbytes = lib.glq_gemv_workspace_bytes(E, M, K, N, rank if xu is None else 0)
-    ws = gemv_workspace(x.device, nbytes)
+    stream = _lib.stream_handle(x.device)
+    nbytes = _gemv_workspace_bytes(lib, E, M, K, N, rank if xu is None else 0)
+    ws = gemv_workspace(x.device, nbytes, stream)
     if u_index is not None and SV is not None:
         n_u = U.shape[0] if xu is None else xu.shape[0]
         rc = lib.glq_gemv_lora_clustered(
@@ -362,7 +377,7 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
             scales.shape[1] * scales.shape[2], groupsize, _sym_mode(sym),
             _lib.ptr(U if xu is None else None), K * rank, u_index.data_ptr(), n_u,
             _lib.ptr(xu), M * rank, SV.data_ptr(), N * rank, rank, _lib.ptr(bias), N,
-            out.data_ptr(), M * N, ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device))
+            out.data_ptr(), M * N, ws.data_ptr(), ws.numel(), stream)
         _lib.check(rc, "glq_gemv_lora_clustered")
         return out
     rc = lib.glq_gemv_lora_batched(
@@ -370,7 +385,7 @@ def packed_dequant_matmul_batched(x: torch.Tensor, codes: torch.Tensor, scales: 
         bits, scales.data_ptr(), _lib.ptr(zeros), scales.shape[1] * scales.shape[2],
         groupsize, _sym_mode(sym), _lib.ptr(U if xu is None else None), K * rank, _lib.ptr(SV),
         N * rank, rank, _lib.ptr(xu), M * rank, _lib.ptr(bias), N, out.data_ptr(), M * N,
-        ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device))
+        ws.data_ptr(), ws.numel(), stream)
     _lib.check(rc, "glq_gemv_lora_batched")
     return out
 
