@@ -262,9 +262,12 @@ def pmc_workload():
 
 
 def pmc_workload_kernels():
-    """What the MoE and prefill counter profiles run: 4 eager decode steps of
-    the config-2 block (B = 1, 16) and of the config-3 layer (B = 1, 16), then
-    4 prefill GEMMs with a precomputed a per config-1 shape at M = 512."""
+    """What the MoE and prefill counter profiles run: 4 calls each of the
+    config-4 attention projections at one token (q/k/v as one launch of 10
+    items of 512 x 2048 with q's 8 sharing a U, then o, 2048 x 4096; 4-bit,
+    rank 64, x U from U), 4 eager decode steps of the config-2 block (B = 1,
+    16) and of the config-3 layer (B = 1, 16), then 4 prefill GEMMs with a
+    precomputed a per config-1 shape at M = 512."""
     import torch
 
     from glorcq_amd import format as fmt
@@ -272,6 +275,22 @@ def pmc_workload_kernels():
     from glorcq_amd.moe_block import GraphCompatibleMoeBlock
 
     dev = torch.device("cuda:0")
+    ps = [fmt.make_linear(2048, 512, bits=4, group=GROUP, rank=RANK, M=1, seed=s)
+          for s in range(10)]
+    st = lambda k: torch.stack([getattr(p, k) for p in ps]).to(dev)  # noqa: E731
+    U = torch.stack([ps[0].U, ps[8].U, ps[9].U]).to(dev)
+    uidx = torch.tensor([0] * 8 + [1, 2], dtype=torch.int32, device=dev)
+    po = fmt.make_linear(4096, 2048, bits=4, group=GROUP, rank=RANK, M=1, seed=11)
+    do = {k: getattr(po, k).to(dev) for k in ("codes", "scales", "zeros", "U", "SV", "x")}
+    for _ in range(4):
+        kernels.packed_dequant_matmul_batched(ps[0].x.to(dev), st("codes"), st("scales"),
+                                              st("zeros"), 4, GROUP, U=U, SV=st("SV"),
+                                              u_index=uidx)
+    for _ in range(4):
+        kernels.packed_dequant_matmul_fused(do["x"], do["codes"], do["scales"], do["zeros"], 4,
+                                            GROUP, U=do["U"], SV=do["SV"])
+    torch.cuda.synchronize()
+    print("config 4 q/k/v and o at one token", flush=True)
     for tag, p in (("config 2 B=1", fmt.make_moe(B=1, seed=6)),
                    ("config 2 B=16", fmt.make_moe(B=16, seed=6)),
                    ("config 3 B=1", fmt.make_mixtral_layer(B=1, seed=3)),
