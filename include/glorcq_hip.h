@@ -377,9 +377,10 @@ int64_t glq_moe_workspace_bytes(const glq_moe_params* p);
  * a step of 17-32 tokens with at most 4 per expert on average runs as
  * consecutive steps of at most 16 tokens.
  * The workspace (256-byte aligned) must be zero-filled before its first use:
- * its first 4096 bytes hold arrival counters (router workgroups, token-tile
- * row blocks), and every step leaves them zero again.  Steps that share a
- * workspace must not overlap.
+ * its first 8192 bytes hold arrival counters (router workgroups, the
+ * combine's and the token-tile form's row blocks, the a_down word), and
+ * every step leaves them zero again.  Steps that share a workspace must not
+ * overlap.
  */
 int glq_moe_decode(const glq_moe_params* p, void* workspace, int64_t workspace_bytes,
                    void* stream);
